@@ -1,0 +1,336 @@
+"""Benchmark of the amd_tuned_torch hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-details] [--no-cpu]
+
+Headline workload (config 2): causal depthwise conv1d
+(Mamba-style) through the patched torch.nn.functional API,
+    y = F.conv1d(x, w, b, padding=3, groups=2048)[..., :8192],
+    x [16, 2048, 8192] bf16 ~ N(0,1), w [2048, 1, 4] ~ N(0, 1/4), b ~ N(0, 0.1), seeded.
+A step is one such call with x already resident in HBM; `value` is algorithmic HBM bytes
+(read x + write y, 2 B each: 1,073,741,824 B) per second over K timed steps.
+
+`roofline` is the dominant kernel alone: the same per-launch bytes divided by its average
+duration from HIP events around back-to-back launches on the launching stream, against
+MI355X's 8 TB/s.  `cpu_baseline` is the reference's CPU path (stock torch.nn.functional,
+fp32, on the host cores) on a bounded sample of the same workload.  `details` carries the
+other BASELINE configs (GroupNorm GB/s, conv3d TFLOP/s, each with its parity error against
+stock fp32 on the GPU).  Exactly one JSON line goes to stdout; progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "rocm-kernel-select_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "conv3d TFLOPS; dwconv1d & GroupNorm HBM GB/s; % of MI355X roofline"
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "fp16": 2500.0, "fp32": 157.3}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def _gen(seed):
+    import torch
+    return torch.Generator().manual_seed(seed)
+
+
+def event_time_ms(fn, iters: int, warmup: int = 3) -> float:
+    """Average ms per call of `fn` from HIP events around `iters` back-to-back calls on
+    the current stream (where the native kernels are launched)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    s = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record(s)
+    for _ in range(iters):
+        fn()
+    b.record(s)
+    b.synchronize()
+    return a.elapsed_time(b) / iters
+
+
+def max_rel_err(y, ref) -> float:
+    y, ref = y.float(), ref.float()
+    den = ref.abs().max().item()
+    return (y - ref).abs().max().item() / den if den > 0 else (y - ref).abs().max().item()
+
+
+# ---------------------------------------------------------------------------
+# config 2: depthwise conv1d
+# ---------------------------------------------------------------------------
+def c2_inputs(dtype, K, dev):
+    import torch
+    g = _gen(1002)
+    N, C, L = 16, 2048, 8192
+    x = torch.randn(N, C, L, generator=g).to(dtype).to(dev)
+    w = (torch.randn(C, 1, K, generator=g) * (1.0 / K) ** 0.5).to(dtype).to(dev)
+    b = (torch.randn(C, generator=g) * 0.1 ** 0.5).to(dtype).to(dev)
+    return x, w, b
+
+
+def dw_kernel_ms(x, w, b, pad, l_out, variant_name, iters=20):
+    import torch
+    from amd_tuned_torch import _native as nat
+    names = nat.variants(nat.OP_DWCONV1D)
+    vi = names.index(variant_name) if variant_name in names else -1
+    out = torch.empty(x.shape[0], x.shape[1], l_out, dtype=x.dtype, device=x.device)
+    w2 = w.squeeze(1).contiguous()
+    return event_time_ms(lambda: nat.dwconv1d(x, w2, b, pad, l_out, variant=vi, out=out), iters)
+
+
+def bench_dw_detail(dtype, mode, dev):
+    import torch
+    import torch.nn.functional as F
+    import amd_tuned_torch  # noqa: F401
+    K, pad = (4, 3) if mode == "causal" else (3, 1)
+    x, w, b = c2_inputs(dtype, K, dev)
+    L = x.shape[-1]
+    y = F.conv1d(x, w, b, padding=pad, groups=x.shape[1])[..., :L]
+    ref = amd_tuned_torch.miopen_fallback._original_conv1d(
+        x.float(), w.float(), b.float(), 1, pad, 1, x.shape[1])[..., :L]
+    err = max_rel_err(y, ref)
+    del ref
+    from amd_tuned_torch import kernel_select
+    won = kernel_select.cached("conv1d", x, w, 1, pad, 1) or "?"
+    l_out = L + 2 * pad - K + 1
+    if won.startswith("native."):
+        ms = dw_kernel_ms(x, w, b, pad, l_out, won[7:])
+    else:
+        ms = event_time_ms(lambda: F.conv1d(x, w, b, padding=pad, groups=x.shape[1]), 10)
+    nbytes = 2 * x.numel() * x.element_size()
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"ms": round(ms, 4), "GB/s": round(gbs, 1), "roofline_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "variant": won, "max_rel_err_vs_stock_fp32": float(f"{err:.3g}")}
+
+
+# ---------------------------------------------------------------------------
+# configs 3 / 5: GroupNorm
+# ---------------------------------------------------------------------------
+def bench_gn_detail(shape, G, eps, dtype, silu, dev):
+    import torch
+    import torch.nn.functional as F
+    import amd_tuned_torch
+    from amd_tuned_torch import _native as nat
+    g = _gen(1003)
+    C = shape[1]
+    mu = torch.rand(C, generator=g) * 4 - 2
+    x = (torch.randn(*shape, generator=g) + mu.view(1, C, *([1] * (len(shape) - 2)))).to(dtype).to(dev)
+    gm = (1 + 0.1 * torch.randn(C, generator=g)).to(dtype).to(dev)
+    bt = (0.1 * torch.randn(C, generator=g)).to(dtype).to(dev)
+    if silu:
+        y = amd_tuned_torch.group_norm_silu(x, G, gm, bt, eps)
+        ref = F.silu(torch.group_norm(x.float(), G, gm.float(), bt.float(), eps))
+        kind = "group_norm_silu"
+    else:
+        y = F.group_norm(x, G, gm, bt, eps)
+        ref = torch.group_norm(x.float(), G, gm.float(), bt.float(), eps)
+        kind = "group_norm"
+    err = max_rel_err(y, ref)
+    del ref
+    from amd_tuned_torch import kernel_select
+    won = None
+    for k, v in kernel_select.debug_winners().items():
+        if k[0] == kind and (tuple(x.shape) in k):
+            won = v
+    won = won or "?"
+    if won.startswith("native."):
+        vi = nat.variants(nat.OP_GROUP_NORM).index(won[7:])
+        out = torch.empty_like(x)
+        ms = event_time_ms(lambda: nat.group_norm(x, G, gm, bt, eps, silu=silu, variant=vi, out=out), 50)
+    else:
+        ms = event_time_ms(lambda: torch.group_norm(x, G, gm, bt, eps), 50)
+    nbytes = 2 * x.numel() * x.element_size()
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"ms": round(ms, 4), "GB/s": round(gbs, 1), "roofline_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "variant": won, "max_rel_err_vs_stock_fp32": float(f"{err:.3g}")}
+
+
+# ---------------------------------------------------------------------------
+# configs 4 / 5: conv3d
+# ---------------------------------------------------------------------------
+def bench_conv_detail(xs, ws, pad, dtype, dev, iters=10):
+    import torch
+    import torch.nn.functional as F
+    import amd_tuned_torch  # noqa: F401
+    from amd_tuned_torch import _native as nat
+    from amd_tuned_torch import kernel_select
+    g = _gen(1004)
+    fan_in = math.prod(ws[1:])
+    x = torch.randn(*xs, generator=g).to(dtype).to(dev)
+    w = (torch.randn(*ws, generator=g) * math.sqrt(2.0 / fan_in)).to(dtype).to(dev)
+    b = (0.1 * torch.randn(ws[0], generator=g)).to(dtype).to(dev)
+    y = F.conv3d(x, w, b, 1, pad)
+    ref = amd_tuned_torch._ORIGINALS[(F, "conv3d")](x.float(), w.float(), b.float(), 1, pad)
+    err = max_rel_err(y, ref)
+    del ref
+    won = kernel_select.cached("conv3d", x, w, 1, pad, 1) or "?"
+    if won.startswith("native."):
+        vi = nat.variants(nat.OP_CONV).index(won[7:])
+        out = torch.empty_like(y)
+        ms = event_time_ms(lambda: nat.conv3d(x, w, b, 1, pad, 1, variant=vi, out=out), iters)
+    else:
+        orig = amd_tuned_torch._ORIGINALS[(F, "conv3d")]
+        ms = event_time_ms(lambda: orig(x, w, b, 1, pad), iters)
+    osp = math.prod(y.shape[2:])
+    flops = 2.0 * xs[0] * ws[0] * osp * ws[1] * math.prod(ws[2:])
+    tf = flops / (ms * 1e-3) / 1e12
+    key = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[dtype]
+    return {"ms": round(ms, 4), "TFLOP/s": round(tf, 2),
+            "roofline_frac": round(tf / MFMA_PEAK_TFLOPS[key], 4), "variant": won,
+            "max_rel_err_vs_stock_fp32": float(f"{err:.3g}")}
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline: stock torch.nn.functional on the host (the reference's CPU path)
+# ---------------------------------------------------------------------------
+def cpu_baseline(rows_sample: int = 1):
+    import torch
+    import amd_tuned_torch
+    conv1d = amd_tuned_torch.miopen_fallback._original_conv1d or torch.nn.functional.conv1d
+    threads = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    g = _gen(1002)
+    C, L, K = 2048, 8192, 4
+    x = torch.randn(rows_sample, C, L, generator=g).to(torch.bfloat16).float()
+    w = (torch.randn(C, 1, K, generator=g) * 0.5).to(torch.bfloat16).float()
+    b = (torch.randn(C, generator=g) * 0.1 ** 0.5).to(torch.bfloat16).float()
+    conv1d(x, w, b, 1, 3, 1, C)  # warm-up
+    best = float("inf")
+    t_end = time.time() + 20.0
+    rounds = 0
+    while rounds < 3 or (time.time() < t_end and rounds < 10):
+        t0 = time.perf_counter()
+        conv1d(x, w, b, 1, 3, 1, C)[..., :L]
+        best = min(best, time.perf_counter() - t0)
+        rounds += 1
+    nbytes = 2 * x.numel() * 2  # the bf16 workload's algorithmic bytes for this sample
+    return {"value": round(nbytes / best / 1e9, 2), "unit": "GB/s", "cores": threads,
+            "kind": "reference",
+            "sample": (f"stock torch.nn.functional.conv1d (fp32 upcast of the bf16 inputs) on "
+                       f"{rows_sample} of the 16 batch rows ([{rows_sample},2048,8192], k=4, pad=3, "
+                       f"[..., :L]), min of {rounds} runs; GB/s counts the bf16 workload's "
+                       f"2 B read + 2 B write per element")}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-details", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one MI355X; the hot path has no multi-GPU "
+              "component (see DESIGN.md for how it would shard). Run with --gpus 1.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import torch.nn.functional as F
+    import amd_tuned_torch
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    assert amd_tuned_torch.native_available(), "native library missing"
+    dev = torch.device("cuda", 0)
+
+    # ---- headline: causal depthwise conv1d bf16 (config 2) --------------------------
+    x, w, b = c2_inputs(torch.bfloat16, 4, dev)
+    L = x.shape[-1]
+
+    def step():
+        return F.conv1d(x, w, b, padding=3, groups=x.shape[1])[..., :L]
+
+    log("warmup (first call runs the per-shape contest)")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    ms_per_step = dt * 1e3 / args.steps
+    nbytes = 2 * x.numel() * x.element_size()
+    value = nbytes / (dt / args.steps) / 1e9
+    won = amd_tuned_torch.kernel_select.cached("conv1d", x, w, 1, 3, 1) or "?"
+    log(f"headline: {ms_per_step:.4f} ms/step, {value:.1f} GB/s, winner {won}")
+
+    if won.startswith("native."):
+        kms = dw_kernel_ms(x, w, b, 3, L + 3, won[7:], iters=max(20, args.steps))
+        kernel_name = "dwconv1d_lds_kernel" if won[7:].startswith("lds") else "dwconv1d_direct_kernel"
+    else:
+        kms = event_time_ms(lambda: step(), 20)
+        kernel_name = "stock"
+    achieved = nbytes / (kms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": kernel_name, "variant": won, "kernel_ms": round(kms, 4),
+                "bytes_per_launch": nbytes}
+    y = step()
+    ref = amd_tuned_torch.miopen_fallback._original_conv1d(
+        x.float(), w.float(), b.float(), 1, 3, 1, x.shape[1])[..., :L]
+    parity = max_rel_err(y, ref)
+    del ref, y
+
+    details = {}
+    if not args.no_details:
+        plan = [
+            ("c2_causal_fp16", lambda: bench_dw_detail(torch.float16, "causal", dev)),
+            ("c2_sym_k3_bf16", lambda: bench_dw_detail(torch.bfloat16, "sym", dev)),
+            ("c2_sym_k3_fp16", lambda: bench_dw_detail(torch.float16, "sym", dev)),
+        ]
+        for dt_name, dtype in (("fp16", torch.float16), ("bf16", torch.bfloat16)):
+            for silu in (False, True):
+                sfx = "_silu" if silu else ""
+                plan.append((f"c3_nchw_{dt_name}{sfx}", lambda dtype=dtype, silu=silu:
+                             bench_gn_detail((8, 512, 64, 64), 32, 1e-5, dtype, silu, dev)))
+                plan.append((f"c3_ncdhw_{dt_name}{sfx}", lambda dtype=dtype, silu=silu:
+                             bench_gn_detail((1, 512, 16, 64, 64), 32, 1e-5, dtype, silu, dev)))
+        plan.append(("c5_gn_silu_bf16", lambda: bench_gn_detail((1, 256, 8, 64, 64), 32, 1e-6,
+                                                                torch.bfloat16, True, dev)))
+        plan += [
+            ("c4_conv3d_small_fp16", lambda: bench_conv_detail((1, 64, 16, 32, 32), (64, 64, 3, 3, 3), 1, torch.float16, dev)),
+            ("c4_conv3d_small_fp32", lambda: bench_conv_detail((1, 64, 16, 32, 32), (64, 64, 3, 3, 3), 1, torch.float32, dev)),
+            ("c4_conv3d_scaled_bf16", lambda: bench_conv_detail((2, 128, 16, 64, 64), (128, 128, 3, 3, 3), 1, torch.bfloat16, dev, 3)),
+            ("c5_conv3d_bf16", lambda: bench_conv_detail((1, 256, 8, 64, 64), (256, 256, 3, 3, 3), 1, torch.bfloat16, dev, 3)),
+            ("c5_conv3d_k7_fp16", lambda: bench_conv_detail((1, 64, 16, 32, 32), (64, 64, 7, 7, 7), 3, torch.float16, dev, 3)),
+        ]
+        for name, fn in plan:
+            log(f"detail {name} ...")
+            try:
+                details[name] = fn()
+                log(f"  {details[name]}")
+            except Exception as exc:  # a detail failing must not hide the headline
+                details[name] = {"error": repr(exc)[:300]}
+                log(f"  error: {exc!r}")
+            torch.cuda.empty_cache()
+
+    cpu = None if args.no_cpu else cpu_baseline()
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "causal depthwise conv1d (BASELINE config 2): F.conv1d(x, w, b, "
+                               "padding=3, groups=2048)[..., :8192], x [16,2048,8192] bf16, k=4, "
+                               "fp32 accumulation", "parallelism": "single GPU"},
+        "parity_max_rel_err_vs_stock_fp32": float(f"{parity:.3g}"),
+        "roofline": roofline, "cpu_baseline": cpu, "details": details,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,148 @@
+/*
+ * amd_tuned_torch_hip.h -- C ABI of libamd_tuned_torch_hip.so, the gfx950 (MI355X)
+ * kernel library behind the `amd_tuned_torch` Python package.
+ *
+ * The reference (WifiLast/rocm-kernel-select) reaches its kernels through pybind11
+ * functions that take torch::Tensor and allocate their own outputs.  This library
+ * replaces those entry points with plain C functions: raw device pointers, sizes,
+ * a dtype code and an explicit hipStream_t.  The caller (the Python host, or any
+ * other FFI) owns every buffer: inputs, outputs and the optional workspace.  The
+ * library never allocates or frees device memory and keeps no per-shape state,
+ * so every entry point is reentrant; calls that share one workspace buffer must
+ * not run concurrently (they are ordered when issued on one stream).
+ *
+ * Return codes (every compute entry point):
+ *   ATK_OK           (0) kernels were enqueued on `stream`;
+ *   ATK_UNSUPPORTED  (1) this build has no kernel for the shape / dtype / variant:
+ *                        nothing was enqueued and the output is untouched.  The
+ *                        Python host turns this into a declining candidate, the
+ *                        same contract as the reference's `launch_conv3d_fp32_winograd`
+ *                        returning false (src/main_rocm.cpp:165-177);
+ *   ATK_EINVAL       (2) inconsistent arguments (the reference's TORCH_CHECK
+ *                        failures, src/main_rocm.cpp:556-599,669-715,798-854);
+ *   ATK_ELAUNCH      (3) the HIP runtime rejected a launch.
+ * atk_last_error() returns a thread-local, human-readable reason for the last
+ * non-zero code.
+ *
+ * Layout: every tensor argument is dense and row-major ("contiguous" in torch
+ * terms), 16-byte alignment of base pointers is not required (kernels take a
+ * slower element-wise path when it is missing).
+ */
+#ifndef AMD_TUNED_TORCH_HIP_H
+#define AMD_TUNED_TORCH_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* atk_stream_t; /* == hipStream_t; NULL = the null stream */
+
+enum {
+  ATK_OK = 0,
+  ATK_UNSUPPORTED = 1,
+  ATK_EINVAL = 2,
+  ATK_ELAUNCH = 3
+};
+
+/* Element type codes. */
+enum { ATK_F32 = 0, ATK_F16 = 1, ATK_BF16 = 2 };
+
+/* Operation codes for the variant-table queries. */
+enum { ATK_OP_DWCONV1D = 0, ATK_OP_GROUP_NORM = 1, ATK_OP_CONV = 2 };
+
+/* Library ABI version (bumped on any signature change). */
+int atk_abi_version(void);
+
+/* Thread-local message for the last failing call on this thread ("" if none). */
+const char* atk_last_error(void);
+
+/* Variant tables: the tile / wave-count instances of each op this build carries.
+ * Variant indices are stable within one ABI version.  The per-shape selector in
+ * the Python host times these against stock PyTorch and caches the winner by
+ * name.  Returns the count / a static string (NULL when out of range). */
+int atk_num_variants(int op);
+const char* atk_variant_name(int op, int variant);
+
+/* ---------------------------------------------------------------------------
+ * Depthwise conv1d forward (groups == channels, one input channel per group,
+ * stride 1, dilation 1), BCL layout:
+ *
+ *   y[n,c,t] = bias[c] + sum_{j<K} w[c,j] * x[n,c,t - pad_left + j],   t in [0, L_out)
+ *
+ * with x taken as zero outside [0, L).  Covers both callers of the reference:
+ *   - symmetric padding p (odd K): pad_left = p, L_out = L + 2p - K + 1
+ *     (replaces `conv1d_forward(u, weight, bias, padding, is_bhl=True)`,
+ *      amd_tuned_torch/_vendor/flashfftconv_depthwise_conv1d/host.cpp:10,
+ *      conv1d.h:56-83, conv1d_bhl.hip:102-142);
+ *   - causal (Mamba) padding: pad_left = K - 1 with L_out = L + K - 1 (stock
+ *     F.conv1d shape) or L_out = L (the truncated shape
+ *     `causal_conv1d_fwd(x, w, bias, ..., silu)` returns,
+ *     src/causal-conv1d-amd/csrc/causal_conv1d.cpp:131-238).
+ * x: [N, C, L], w: [C, K], bias: [C] or NULL, y: [N, C, L_out]; all of `dtype`.
+ * Accumulation is fp32 for every dtype.  fuse_silu != 0 applies y*sigmoid(y)
+ * before the store (the causal kernel's `silu_activation` flag).
+ * K in [1, 64]; pad_left in [0, 64].  variant < 0 picks the default.
+ * ------------------------------------------------------------------------- */
+int atk_dwconv1d_fwd(const void* x, const void* w, const void* bias, void* y,
+                     int64_t N, int64_t C, int64_t L, int K, int pad_left, int64_t L_out,
+                     int dtype, int fuse_silu, int variant, atk_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * GroupNorm forward, NC[spatial] layout (replaces `group_norm(input, num_groups,
+ * weight?, bias?, eps)`, src/main_rocm.cpp:556-599 -> src/cuda/group_norm.cu:41-136,
+ * and the fused GroupNorm+SiLU of amd_tuned_torch/conv_fusion_ops.py:192-275):
+ *
+ *   y[n,c,s] = act( (x[n,c,s] - mean[n,g]) * rsqrt(var[n,g] + eps) * gamma[c] + beta[c] )
+ *
+ * g = c / (C/G); mean/var are the population statistics of the C/G * S elements
+ * of group (n, g), computed in fp32 from data held on chip (exact two-pass
+ * statistics, no E[x^2]-E[x]^2 cancellation).  act = SiLU when fuse_silu != 0,
+ * identity otherwise.  gamma/beta may be NULL (non-affine) and have their own
+ * element type `param_dtype` (torch allows fp32 affine parameters under 16-bit
+ * activations).  S = product of the spatial extents (1 for a [N, C] input).
+ * Needs a workspace of atk_group_norm_workspace_bytes(...) bytes whose first
+ * atk_group_norm_workspace_zero_bytes(...) bytes are zero before the FIRST call
+ * that uses it (the kernels leave them zero again on exit).
+ * ------------------------------------------------------------------------- */
+size_t atk_group_norm_workspace_bytes(int64_t N, int64_t C, int64_t S, int G, int dtype,
+                                      int variant);
+size_t atk_group_norm_workspace_zero_bytes(int64_t N, int64_t C, int64_t S, int G,
+                                           int dtype, int variant);
+int atk_group_norm_fwd(const void* x, const void* gamma, const void* beta, void* y,
+                       int64_t N, int64_t C, int64_t S, int G, float eps, int fuse_silu,
+                       int dtype, int param_dtype, int variant, void* workspace,
+                       size_t workspace_bytes, atk_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Dense convolution forward, groups = 1, NCDHW layout, as an implicit GEMM on
+ * MFMA (replaces `conv3d(input, weight, bias?, stride, padding, dilation)`,
+ * src/main_rocm.cpp:798-854, and `conv2d(...)`, src/main_rocm.cpp:669-715):
+ *
+ *   y[n,o,z,y,x] = bias[o] + sum_{i,a,b,c} w[o,i,a,b,c] *
+ *                  x[n, i, z*sd - pd + a*dd, y*sh - ph + b*dh, x*sw - pw + c*dw]
+ *
+ * x: [N, Ci, D, H, W], w: [Co, Ci, KD, KH, KW], bias: [Co] or NULL,
+ * y: [N, Co, Do, Ho, Wo] with Do = (D + 2pd - dd(KD-1) - 1)/sd + 1 (likewise H, W),
+ * the output-size formula of src/main_rocm.cpp:204-206.  conv2d is the D = KD = 1
+ * case.  16-bit inputs use bf16/fp16 MFMA with fp32 accumulation; fp32 inputs use
+ * fp32 MFMA.  Needs a workspace of atk_conv_workspace_bytes(...) bytes (repacked
+ * weights and split-K partial sums).
+ * ------------------------------------------------------------------------- */
+size_t atk_conv_workspace_bytes(int64_t N, int64_t Ci, int64_t D, int64_t H, int64_t W,
+                                int64_t Co, int KD, int KH, int KW, int sd, int sh, int sw,
+                                int pd, int ph, int pw, int dd, int dh, int dw, int dtype,
+                                int variant);
+int atk_conv_fwd(const void* x, const void* w, const void* bias, void* y, int64_t N,
+                 int64_t Ci, int64_t D, int64_t H, int64_t W, int64_t Co, int KD, int KH,
+                 int KW, int sd, int sh, int sw, int pd, int ph, int pw, int dd, int dh,
+                 int dw, int dtype, int variant, void* workspace, size_t workspace_bytes,
+                 atk_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AMD_TUNED_TORCH_HIP_H */

@@ -1,0 +1,124 @@
+/*
+ * atk_oracle.c -- CPU restatement (float64) of the hot-path operators, used ONLY as the
+ * checker by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg.  Nothing in
+ * the product links or calls it.
+ *
+ * The parity target of the reference is stock torch.nn.functional (its selector verifies
+ * every candidate against stock, amd_tuned_torch/kernel_select.py:68-82,615-651); these are
+ * the textbook definitions of those stock operators, written as loops with float64
+ * accumulation, in the form each reference kernel states them.
+ */
+#include <math.h>
+#include <stddef.h>
+#include <stdint.h>
+
+/* Depthwise conv1d, BCL (amd_tuned_torch/_vendor/flashfftconv_depthwise_conv1d/
+ * conv1d_bhl.hip:55-100; causal variant src/causal-conv1d-amd/csrc/causal_conv1d_fwd.cu:
+ * 39-130 == pad_left = K-1 and the first L outputs):
+ *   y[n,c,t] = b[c] + sum_j w[c,j] * x[n,c,t-pad_left+j],  t in [0, L_out), x = 0 outside [0, L).
+ * silu != 0 applies y / (1 + exp(-y)) (causal_conv1d_fwd.cu silu_activation). */
+void oracle_dwconv1d(const double* x, const double* w, const double* b, double* y, int64_t N,
+                     int64_t C, int64_t L, int64_t K, int64_t pad_left, int64_t L_out, int silu) {
+  for (int64_t n = 0; n < N; ++n)
+    for (int64_t c = 0; c < C; ++c) {
+      const double* xr = x + (n * C + c) * L;
+      double* yr = y + (n * C + c) * L_out;
+      for (int64_t t = 0; t < L_out; ++t) {
+        double acc = b ? b[c] : 0.0;
+        for (int64_t j = 0; j < K; ++j) {
+          const int64_t p = t - pad_left + j;
+          if (p >= 0 && p < L) acc += w[c * K + j] * xr[p];
+        }
+        yr[t] = silu ? acc / (1.0 + exp(-acc)) : acc;
+      }
+    }
+}
+
+/* GroupNorm over NC[S] (src/cuda/group_norm.cu:41-104; fused SiLU of
+ * amd_tuned_torch/conv_fusion_ops.py:192-242): group (n, g) = channels [g*C/G, (g+1)*C/G)
+ * x all S positions; population variance (divide by the group size), eps inside the
+ * square root, optional per-channel affine.  Statistics by two passes in float64.
+ * mean_out / rstd_out ([N*G], may be NULL) receive the group statistics. */
+void oracle_group_norm(const double* x, const double* gamma, const double* beta, double* y,
+                       int64_t N, int64_t C, int64_t S, int64_t G, double eps, int silu,
+                       double* mean_out, double* rstd_out) {
+  const int64_t cpg = C / G, E = cpg * S;
+  for (int64_t gi = 0; gi < N * G; ++gi) {
+    const double* xg = x + gi * E;
+    double* yg = y + gi * E;
+    double s = 0.0;
+    for (int64_t e = 0; e < E; ++e) s += xg[e];
+    const double mean = s / (double)E;
+    double m2 = 0.0;
+    for (int64_t e = 0; e < E; ++e) {
+      const double d = xg[e] - mean;
+      m2 += d * d;
+    }
+    const double rstd = 1.0 / sqrt(m2 / (double)E + eps);
+    if (mean_out) mean_out[gi] = mean;
+    if (rstd_out) rstd_out[gi] = rstd;
+    const int64_t g = gi % G;
+    for (int64_t cl = 0; cl < cpg; ++cl) {
+      const int64_t c = g * cpg + cl;
+      const double gm = gamma ? gamma[c] : 1.0, bt = beta ? beta[c] : 0.0;
+      for (int64_t sp = 0; sp < S; ++sp) {
+        const int64_t e = cl * S + sp;
+        double v = (xg[e] - mean) * rstd * gm + bt;
+        if (silu) v = v / (1.0 + exp(-v));
+        yg[e] = v;
+      }
+    }
+  }
+}
+
+/* Dense conv3d, groups = 1, NCDHW (the implicit GEMM of src/cuda/generated/
+ * conv3d_fp16_bm256_bn128_bk32_s2.cu:84-324 and the direct kernel of src/cuda/conv3d_fp32.cu:
+ * 33-149 both compute this):
+ *   y[n,o,z,h,v] = b[o] + sum_{i,a,bb,c} w[o,i,a,bb,c] * x[n,i,z*sd-pd+a*dd, h*sh-ph+bb*dh, v*sw-pw+c*dw]
+ * Output extents follow src/main_rocm.cpp:204-206.  Computes only the `npts` output
+ * elements whose flat NCDHW indices are listed in `pts` (all of them when pts == NULL, in
+ * which case npts must equal the output size), so large problems can be spot-checked. */
+static int64_t out_extent(int64_t in, int64_t k, int64_t s, int64_t p, int64_t d) {
+  return (in + 2 * p - d * (k - 1) - 1) / s + 1;
+}
+
+void oracle_conv3d(const double* x, const double* w, const double* b, double* y, int64_t N,
+                   int64_t Ci, int64_t D, int64_t H, int64_t W, int64_t Co, int64_t KD,
+                   int64_t KH, int64_t KW, int64_t sd, int64_t sh, int64_t sw, int64_t pd,
+                   int64_t ph, int64_t pw, int64_t dd, int64_t dh, int64_t dw, const int64_t* pts,
+                   int64_t npts) {
+  (void)N; /* batch index comes from the flat output index */
+  const int64_t Do = out_extent(D, KD, sd, pd, dd), Ho = out_extent(H, KH, sh, ph, dh),
+                Wo = out_extent(W, KW, sw, pw, dw);
+  const int64_t osp = Do * Ho * Wo, isp = D * H * W, taps = KD * KH * KW;
+  for (int64_t q = 0; q < npts; ++q) {
+    const int64_t f = pts ? pts[q] : q;
+    const int64_t n = f / (Co * osp);
+    int64_t r = f - n * Co * osp;
+    const int64_t o = r / osp;
+    r -= o * osp;
+    const int64_t z = r / (Ho * Wo);
+    r -= z * Ho * Wo;
+    const int64_t h = r / Wo;
+    const int64_t v = r - h * Wo;
+    double acc = b ? b[o] : 0.0;
+    for (int64_t i = 0; i < Ci; ++i) {
+      const double* xc = x + (n * Ci + i) * isp;
+      const double* wc = w + (o * Ci + i) * taps;
+      for (int64_t a = 0; a < KD; ++a) {
+        const int64_t iz = z * sd - pd + a * dd;
+        if (iz < 0 || iz >= D) continue;
+        for (int64_t bb = 0; bb < KH; ++bb) {
+          const int64_t iy = h * sh - ph + bb * dh;
+          if (iy < 0 || iy >= H) continue;
+          for (int64_t c = 0; c < KW; ++c) {
+            const int64_t ix = v * sw - pw + c * dw;
+            if (ix < 0 || ix >= W) continue;
+            acc += wc[(a * KH + bb) * KW + c] * xc[(iz * H + iy) * W + ix];
+          }
+        }
+      }
+    }
+    y[q] = acc;
+  }
+}

@@ -1,0 +1,417 @@
+"""Per-shape benchmark-once selection among candidate implementations, stock included.
+
+Behavioural restatement of the reference's selector (amd_tuned_torch/kernel_select.py:
+132-733).  On the first call for a shape key every candidate is timed (2 warm-up calls, then
+3 individually event-timed calls, minimum kept -- kernel_select.py:430-431,454-492), the
+fastest NON-reference candidate is checked numerically against the reference candidate
+(always the LAST entry, stock by convention -- kernel_select.py:554-693), and the verified
+winner's NAME is cached in memory and in a JSON file keyed by GPU + torch + Python version
+(kernel_select.py:310-423).  Later calls with the same key dispatch straight to the winner.
+
+Candidates here are this package's own gfx950 kernel variants (named "native.<variant>")
+plus "stock".  Policies kept from the reference because callers and tests depend on them:
+
+* a thunk returning None declines; a cached winner that declines is evicted (memory and
+  disk) and the shape re-contested (kernel_select.py:562-571);
+* a candidate that measures fastest but fails verification is excluded for that exact key,
+  persisted, with a warning; the next-fastest is verified in turn, down to the reference
+  (kernel_select.py:670-680);
+* the verification bar is max(atol, rtol * RMS(reference)), compared in 8M-element chunks
+  (kernel_select.py:164-295); an OOM while comparing is INDETERMINATE: the reference output
+  is served and nothing is recorded (kernel_select.py:652-669);
+* an OOM inside a candidate or the reference is a decline, any other exception propagates
+  (kernel_select.py:597-629);
+* blacklists written under another verification-bar version are dropped together with the
+  winners of those keys (kernel_select.py:297-309,378-395);
+* AMD_TUNED_TORCH_MEASURE_KERNELS=0 (legacy AMD_TUNED_TORCH_CONV_MEASURE) disables the
+  contest, AMD_TUNED_TORCH_KERNEL_SELECT_VERIFY=0 skips verification,
+  AMD_TUNED_TORCH_KERNEL_SELECT_CACHE=0 disables the disk file and
+  AMD_TUNED_TORCH_KERNEL_SELECT_CACHE_DIR relocates it (all read once at import).
+"""
+from __future__ import annotations
+
+import json
+import math
+import os
+import re
+import sys
+import threading
+import warnings
+from typing import Callable, Optional
+
+import torch
+
+_ENABLED = (os.environ.get("AMD_TUNED_TORCH_MEASURE_KERNELS",
+                           os.environ.get("AMD_TUNED_TORCH_CONV_MEASURE", "1")) != "0")
+_VERIFY_ENABLED = os.environ.get("AMD_TUNED_TORCH_KERNEL_SELECT_VERIFY", "1") != "0"
+
+_winners: dict = {}          # key -> winning candidate name
+_bad_candidates: dict = {}   # key -> {names that failed verification}
+_lock = threading.Lock()
+
+# (rtol, atol) per output dtype (kernel_select.py:150-155)
+_TOLERANCES = {
+    torch.float16: (1e-2, 1e-2),
+    torch.bfloat16: (2e-2, 2e-2),
+    torch.float32: (1e-4, 1e-5),
+}
+_DEFAULT_TOLERANCE = (2e-2, 2e-2)
+
+_VERIFY_SCALE_SAMPLE = 1 << 20     # elements sampled (strided) for the RMS scale
+_VERIFY_CHUNK_ELEMENTS = 1 << 23   # elements upcast per comparison slice
+
+_VERIFY_BAR_VERSION = 3
+_DISK_CACHE_ENABLED = os.environ.get("AMD_TUNED_TORCH_KERNEL_SELECT_CACHE", "1") != "0"
+_CACHE_DIR = os.environ.get(
+    "AMD_TUNED_TORCH_KERNEL_SELECT_CACHE_DIR",
+    os.path.join(os.path.dirname(os.path.abspath(__file__)), "_kernel_select_cache"))
+
+_WARMUP = 2
+_ITERS = 3
+
+# The disk cache is read on first use rather than at import, so importing the package does
+# not initialise the GPU runtime (the cache file name embeds the GPU model).
+_disk_loaded = False
+
+
+def _ensure_disk_cache() -> None:
+    global _disk_loaded
+    if not _disk_loaded:
+        _disk_loaded = True
+        _load_disk_cache()
+
+
+def enabled() -> bool:
+    return _ENABLED
+
+
+# ---------------------------------------------------------------------------
+# verification
+# ---------------------------------------------------------------------------
+def _is_oom(exc: BaseException) -> bool:
+    for cls in (getattr(torch, "OutOfMemoryError", None),
+                getattr(getattr(torch, "cuda", None), "OutOfMemoryError", None)):
+        if isinstance(cls, type) and isinstance(exc, cls):
+            return True
+    return "out of memory" in str(exc).lower()
+
+
+def _reference_scale(reference_out) -> Optional[float]:
+    """RMS of a strided sample of the reference output (None if not measurable)."""
+    try:
+        flat = reference_out.flatten()
+        step = max(1, flat.numel() // _VERIFY_SCALE_SAMPLE)
+        rms = float(flat[::step].float().pow(2).mean().sqrt())
+    except (RuntimeError, TypeError, ValueError, AttributeError, ZeroDivisionError):
+        return None
+    return rms if (math.isfinite(rms) and rms > 0.0) else None
+
+
+def _verify(candidate_out, reference_out, tolerance=None) -> Optional[bool]:
+    """True = agrees, False = disagrees, None = indeterminate (the comparison ran out of
+    memory).  A comparison that cannot run for a reason about the candidate (shape, type)
+    is a failure, never a pass."""
+    try:
+        rtol, atol = tolerance if tolerance is not None else _TOLERANCES.get(
+            candidate_out.dtype, _DEFAULT_TOLERANCE)
+        scale = _reference_scale(reference_out)
+        if scale is not None:
+            atol = max(atol, rtol * scale)
+        if candidate_out.shape != reference_out.shape:
+            return False
+        if candidate_out.dim() == 0:
+            return bool(torch.allclose(candidate_out.float(), reference_out.float(),
+                                       rtol=rtol, atol=atol, equal_nan=True))
+        rows = candidate_out.shape[0]
+        per_row = max(1, candidate_out.numel() // max(1, rows))
+        step = max(1, _VERIFY_CHUNK_ELEMENTS // per_row)
+        for lo in range(0, rows, step):
+            hi = min(rows, lo + step)
+            if not torch.allclose(candidate_out[lo:hi].float(), reference_out[lo:hi].float(),
+                                  rtol=rtol, atol=atol, equal_nan=True):
+                return False
+        return True
+    except (RuntimeError, TypeError, ValueError, AttributeError) as exc:
+        return None if _is_oom(exc) else False
+
+
+# ---------------------------------------------------------------------------
+# disk cache
+# ---------------------------------------------------------------------------
+def _device_key() -> str:
+    try:
+        name = torch.cuda.get_device_name(0) if torch.cuda.is_available() else "cpu"
+    except Exception:
+        name = "unknown"
+    name = re.sub(r"[^A-Za-z0-9_.-]+", "_", name)
+    tv = torch.__version__.replace("+", "_").replace("/", "_")
+    return f"{name}-torch-{tv}-cp{sys.version_info.major}{sys.version_info.minor}"
+
+
+def _cache_path() -> str:
+    return os.path.join(_CACHE_DIR, f"{_device_key()}.json")
+
+
+def _encode(v):
+    if isinstance(v, torch.dtype):
+        return {"__dtype__": str(v)}
+    if isinstance(v, tuple):
+        return {"__tuple__": [_encode(e) for e in v]}
+    return v
+
+
+def _decode(v):
+    if isinstance(v, dict):
+        if "__dtype__" in v:
+            return getattr(torch, v["__dtype__"].rsplit(".", 1)[-1])
+        if "__tuple__" in v:
+            return tuple(_decode(e) for e in v["__tuple__"])
+    return v
+
+
+def _key_str(key) -> str:
+    return json.dumps([_encode(e) for e in key])
+
+
+def _decode_key(s: str):
+    return tuple(_decode(e) for e in json.loads(s))
+
+
+def _load_disk_cache() -> None:
+    """Best effort; accepts the sectioned format and the older flat {key: winner} one."""
+    if not _DISK_CACHE_ENABLED:
+        return
+    try:
+        with open(_cache_path(), "r") as f:
+            raw = json.load(f)
+    except (OSError, ValueError):
+        return
+    if not isinstance(raw, dict):
+        return
+    if "winners" in raw or "bad" in raw:
+        winners, bad = raw.get("winners", {}), raw.get("bad", {})
+    else:
+        winners, bad = raw, {}
+    stale = raw.get("verify_bar") != _VERIFY_BAR_VERSION
+    with _lock:
+        for ks, name in winners.items():
+            if stale and ks in bad:
+                continue
+            try:
+                _winners.setdefault(_decode_key(ks), name)
+            except (ValueError, TypeError, AttributeError):
+                continue
+        if not stale:
+            for ks, names in bad.items():
+                try:
+                    _bad_candidates.setdefault(_decode_key(ks), set()).update(names)
+                except (ValueError, TypeError, AttributeError):
+                    continue
+
+
+def _save_disk_cache() -> None:
+    """Rewrite the whole file atomically (temp file + os.replace)."""
+    if not _DISK_CACHE_ENABLED:
+        return
+    path = _cache_path()
+    try:
+        os.makedirs(os.path.dirname(path), exist_ok=True)
+        with _lock:
+            raw = {
+                "verify_bar": _VERIFY_BAR_VERSION,
+                "winners": {_key_str(k): v for k, v in _winners.items()},
+                "bad": {_key_str(k): sorted(v) for k, v in _bad_candidates.items() if v},
+            }
+        tmp = f"{path}.tmp{os.getpid()}"
+        with open(tmp, "w") as f:
+            json.dump(raw, f)
+        os.replace(tmp, path)
+    except OSError:
+        pass
+
+
+# ---------------------------------------------------------------------------
+# keys, timing, lookup
+# ---------------------------------------------------------------------------
+def _norm(v):
+    return (v,) if isinstance(v, int) else tuple(v)
+
+
+def _key(kind, input, weight, stride, padding, dilation):
+    # memory format is part of the identity (kernel_select.py:438-445)
+    channels_last = (input.is_contiguous(memory_format=torch.channels_last)
+                     or input.is_contiguous(memory_format=torch.channels_last_3d))
+    return (kind, input.dtype, tuple(input.shape), tuple(weight.shape), _norm(stride),
+            _norm(padding), _norm(dilation), channels_last)
+
+
+def _time(fn) -> Optional[float]:
+    """Minimum over _ITERS individually event-timed runs, after _WARMUP runs; None if the
+    candidate declines or raises a Runtime/Type/AssertionError."""
+    try:
+        for _ in range(_WARMUP):
+            if fn() is None:
+                return None
+        torch.cuda.synchronize()
+        pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                 for _ in range(_ITERS)]
+        for a, b in pairs:
+            a.record()
+            fn()
+            b.record()
+        torch.cuda.synchronize()
+        return min(a.elapsed_time(b) for a, b in pairs)
+    except (RuntimeError, TypeError, AssertionError):
+        return None
+
+
+def cached(kind: str, input, weight, stride, padding, dilation) -> Optional[str]:
+    """Winner already decided for this conv shape, or None."""
+    if not _ENABLED:
+        return None
+    _ensure_disk_cache()
+    key = _key(kind, input, weight, stride, padding, dilation)
+    with _lock:
+        return _winners.get(key)
+
+
+def cached_key(kind: str, key) -> Optional[str]:
+    if not _ENABLED:
+        return None
+    _ensure_disk_cache()
+    with _lock:
+        return _winners.get((kind,) + tuple(key))
+
+
+def pick(kind: str, input, weight, stride, padding, dilation,
+         candidates: "list[tuple[str, Callable]]", tolerance=None):
+    """Output of the fastest verified candidate for this conv shape (None when disabled).
+    The last candidate is the reference (stock) and is assumed to always work."""
+    if not _ENABLED:
+        return None
+    return _contest(_key(kind, input, weight, stride, padding, dilation), candidates, tolerance)
+
+
+def pick_key(kind: str, key, candidates: "list[tuple[str, Callable]]", tolerance=None):
+    """Same as pick() over a caller-built key (group_norm keys on the group count)."""
+    if not _ENABLED:
+        return None
+    return _contest((kind,) + tuple(key), candidates, tolerance)
+
+
+def _record(key, name: str) -> None:
+    with _lock:
+        _winners[key] = name
+    _save_disk_cache()
+
+
+def _call_guarded(thunk):
+    """Run a thunk; an OOM becomes (None, True), other Runtime/Type/AssertionErrors raise."""
+    try:
+        return thunk(), False
+    except (RuntimeError, TypeError, AssertionError) as exc:
+        if not _is_oom(exc):
+            raise
+        return None, True
+
+
+def _contest(key, candidates, tolerance=None):
+    if not candidates:
+        return None
+    _ensure_disk_cache()
+    ref_name, ref_thunk = candidates[-1]
+    with _lock:
+        winner = _winners.get(key)
+        bad = set(_bad_candidates.get(key, ()))
+
+    if winner is not None and winner not in bad:
+        for name, thunk in candidates:
+            if name == winner:
+                out = thunk()
+                if out is not None:
+                    return out
+                break
+        with _lock:  # cached winner declined (or is no longer offered): evict, re-contest
+            _winners.pop(key, None)
+        _save_disk_cache()
+
+    timed = []
+    for name, thunk in candidates:
+        if name in bad:
+            continue
+        ms = _time(thunk)
+        if ms is not None:
+            timed.append((ms, name, thunk))
+    timed.sort(key=lambda r: r[0])
+
+    ref_out = None
+    ref_done = False
+    ref_oom = False
+    for _, name, thunk in timed:
+        out, _oom = _call_guarded(thunk)
+        if out is None:
+            continue
+        if name == ref_name or not _VERIFY_ENABLED:
+            _record(key, name)
+            return out
+        if not ref_done:
+            ref_done = True
+            ref_out, ref_oom = _call_guarded(ref_thunk)
+            if ref_out is None:
+                if ref_oom:
+                    return out          # nothing learned: serve, record nothing
+                _record(key, name)      # reference declined: nothing to verify against
+                return out
+        verdict = _verify(out, ref_out, tolerance)
+        if verdict:
+            _record(key, name)
+            return out
+        if verdict is None:
+            warnings.warn(
+                f"amd_tuned_torch.kernel_select: ran out of memory verifying candidate "
+                f"'{name}' for {key} against '{ref_name}'; serving the reference for this "
+                "call and recording nothing (not evidence that the candidate is wrong).",
+                UserWarning)
+            return ref_out
+        warnings.warn(
+            f"amd_tuned_torch.kernel_select: candidate '{name}' for {key} measured fastest but "
+            f"did not match '{ref_name}' within tolerance; excluding it for this exact shape.",
+            UserWarning)
+        with _lock:
+            _bad_candidates.setdefault(key, set()).add(name)
+        _save_disk_cache()
+
+    if ref_oom:
+        return ref_out
+    if ref_done and ref_out is not None:
+        _record(key, ref_name)
+        return ref_out
+    return None
+
+
+def debug_winners() -> dict:
+    """{key: winning candidate name}."""
+    _ensure_disk_cache()
+    with _lock:
+        return dict(_winners)
+
+
+def debug_bad_candidates() -> dict:
+    """{key: {names excluded for failing verification}}."""
+    with _lock:
+        return {k: set(v) for k, v in _bad_candidates.items()}
+
+
+def reset() -> None:
+    """Forget every winner and exclusion, in memory and this GPU's cache file."""
+    global _disk_loaded
+    _disk_loaded = True
+    with _lock:
+        _winners.clear()
+        _bad_candidates.clear()
+    if _DISK_CACHE_ENABLED:
+        try:
+            os.remove(_cache_path())
+        except OSError:
+            pass
+

@@ -1,0 +1,104 @@
+// Shared device/host helpers for the gfx950 kernels of libamd_tuned_torch_hip.so.
+//
+// Element types: float, _Float16 and __bf16 (clang's native types; on gfx950 the
+// f32->bf16 conversion lowers to the hardware round-to-nearest-even convert, which
+// is the rounding PyTorch applies when it narrows an fp32 result).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include "../../include/amd_tuned_torch_hip.h"
+
+namespace atk {
+
+// ---------------------------------------------------------------------------
+// Host-side error reporting (thread-local message behind atk_last_error()).
+// ---------------------------------------------------------------------------
+void set_error(const char* fmt, ...);
+int fail(int code, const char* fmt, ...);
+int check_launch(const char* what);
+int device_cu_count();
+
+inline size_t dtype_size(int dtype) { return dtype == ATK_F32 ? 4 : 2; }
+inline bool dtype_ok(int dtype) { return dtype == ATK_F32 || dtype == ATK_F16 || dtype == ATK_BF16; }
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// ---------------------------------------------------------------------------
+// Element conversions.
+// ---------------------------------------------------------------------------
+template <typename T> __device__ __forceinline__ float to_f32(T v) { return static_cast<float>(v); }
+template <typename T> __device__ __forceinline__ T from_f32(float v) { return static_cast<T>(v); }
+
+// Runtime-typed scalar load (affine parameters, per-channel bias): cheap, used
+// off the streaming path only.
+__device__ __forceinline__ float load_param(const void* p, int dtype, int64_t i) {
+  if (dtype == ATK_F32) return reinterpret_cast<const float*>(p)[i];
+  if (dtype == ATK_F16) return static_cast<float>(reinterpret_cast<const _Float16*>(p)[i]);
+  return static_cast<float>(reinterpret_cast<const __bf16*>(p)[i]);
+}
+
+// 16-byte vector of elements, reinterpretable as raw dwords.
+template <typename T> struct Vec16 {
+  static constexpr int N = 16 / sizeof(T);
+  union {
+    uint4 raw;
+    T e[N];
+  };
+};
+
+__device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + __expf(-v)); }
+
+// ---------------------------------------------------------------------------
+// Wave64 / block reductions (fp32 sums).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Sum over the block; every thread receives the total.  `red` must hold
+// blockDim/64 floats of shared memory.  Contains two __syncthreads().
+template <int NT>
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  constexpr int NW = NT / 64;
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  if (NW == 1) return v;
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  float t = 0.f;
+#pragma unroll
+  for (int i = 0; i < NW; ++i) t += red[i];  // identical order in every thread
+  __syncthreads();
+  return t;
+}
+
+// ---------------------------------------------------------------------------
+// Division by a runtime-invariant divisor d (1 <= d < 2^31) for numerators
+// n < 2^31:  q = (umulhi(n, m) + n) >> s   (round-up multiplier method,
+// Granlund & Montgomery 1994, "Division by invariant integers using
+// multiplication").
+// ---------------------------------------------------------------------------
+struct FastDiv {
+  uint32_t d, m, s;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f;
+  f.d = d;
+  uint32_t s = 0;
+  while ((1ull << s) < d) ++s;  // s = ceil(log2 d)
+  f.s = s;
+  f.m = (uint32_t)((((1ull << s) - d) << 32) / d + 1);
+  if (d == 1) { f.m = 0; f.s = 0; }
+  return f;
+}
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, FastDiv f) {
+  return (__umulhi(n, f.m) + n) >> f.s;
+}
+
+}  // namespace atk

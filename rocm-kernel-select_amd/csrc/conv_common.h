@@ -1,0 +1,23 @@
+// Shape descriptor shared by the conv entry points and kernels.
+#pragma once
+#include "atk_common.h"
+
+namespace atk {
+
+struct ConvShape {
+  int N, Ci, D, H, W, Co;
+  int KD, KH, KW;
+  int sd, sh, sw, pd, ph, pw, dd, dh, dw;
+  int Do, Ho, Wo;
+  int dtype;
+};
+
+// MFMA implicit-GEMM kernels (conv_igemm.hip).  Variant indices here are local to the
+// implicit-GEMM table; the C ABI offsets them by one (ABI variant 0 = direct kernel).
+int conv_igemm_num_variants();
+const char* conv_igemm_variant_name(int v);
+size_t conv_igemm_workspace_bytes(const ConvShape& p, int v);
+int conv_igemm_launch(const ConvShape& p, const void* x, const void* w, const void* bias, void* y,
+                      int v, void* ws, size_t ws_bytes, hipStream_t s);
+
+}  // namespace atk

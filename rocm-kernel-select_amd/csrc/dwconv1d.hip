@@ -1,0 +1,367 @@
+// Depthwise conv1d forward for gfx950 (BCL layout, stride 1, dilation 1).
+//
+//   y[n,c,t] = bias[c] + sum_{j<K} w[c,j] * x[n,c,t - pad + j],  t in [0, L_out),
+//   x == 0 outside [0, L).
+//
+// Math follows the reference's two kernels for this op
+// (amd_tuned_torch/_vendor/flashfftconv_depthwise_conv1d/conv1d_bhl.hip:25-100 for the
+// symmetric case, src/causal-conv1d-amd/csrc/causal_conv1d_fwd.cu:39-130 for the causal
+// one, whose output is the first L columns of the pad = K-1 result); unlike the first of
+// those it accumulates in fp32 for 16-bit inputs.
+//
+// Design (HBM-bound streaming, 2 bytes in + 2 bytes out per element for 16-bit):
+//   * The output tensor is treated as ONE flat array of N*C*L_out elements and cut into
+//     tiles of 256 threads x OPT outputs.  Tile origins are chosen so that every thread's
+//     outputs are a naturally aligned 16-byte vector in memory, whatever L_out is: the
+//     stock-shaped causal output (L_out = L + K - 1, rows not 16-byte aligned) is stored
+//     with full-width coalesced stores just like the symmetric case.
+//   * The flat input range a tile depends on (its rows' windows, including the K-1 halo)
+//     is staged once into LDS with aligned 16-byte loads; each thread then reads its
+//     VEC + K - 1 window from LDS.  Zero padding is a mask on the row position, applied
+//     only on the few windows that touch a row edge.
+//   * Per-row weights and bias of the (few) rows a tile touches are staged to LDS as
+//     fp32 and read as broadcasts.
+// A "direct" variant (one output per thread, global loads, no LDS) covers shapes whose
+// LDS window would not fit.
+#include "atk_common.h"
+
+namespace atk {
+
+namespace {
+
+constexpr int DW_NT = 256;        // threads per block
+constexpr int DW_MAXR = 16;       // rows whose weights are staged in LDS
+constexpr int DW_KMAX = 64;       // largest supported kernel width
+constexpr int DW_PADMAX = 64;     // largest supported left padding
+
+struct DwArgs {
+  const void* x;
+  const void* w;
+  const void* b;
+  void* y;
+  int64_t total_in, total_out;
+  uint32_t C, L, Lout;
+  int K, pad;
+  int x_off, y_off;        // misalignment of the x / y base pointers, in elements
+  int silu;
+  FastDiv div_lout, div_c;
+  int win_cap;             // LDS window capacity, elements
+};
+
+template <typename T, int KT, int OPT>
+__global__ __launch_bounds__(DW_NT) void dwconv1d_lds_kernel(DwArgs a) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int U = OPT / VEC;
+  constexpr int TO = DW_NT * OPT;
+  const int K = KT > 0 ? KT : a.K;
+  const int pad = a.pad;
+  const T* __restrict__ x = static_cast<const T*>(a.x);
+  const T* __restrict__ w = static_cast<const T*>(a.w);
+  const T* __restrict__ bias = static_cast<const T*>(a.b);
+  T* __restrict__ y = static_cast<T*>(a.y);
+
+  extern __shared__ uint4 lds_raw[];
+  T* win = reinterpret_cast<T*>(lds_raw);
+  float* wl = reinterpret_cast<float*>(win + a.win_cap);  // [DW_MAXR][K + 1]
+
+  const int tid = threadIdx.x;
+  const int64_t F0 = (int64_t)blockIdx.x * TO - a.y_off;  // tile origin, 16B aligned in memory
+  const int64_t Fs = F0 > 0 ? F0 : 0;
+  const int64_t Fe = (F0 + TO) < a.total_out ? (F0 + TO) : a.total_out;
+  if (Fs >= Fe) return;
+
+  const uint32_t L = a.L, Lout = a.Lout;
+  const int64_t ra = Fs / Lout;
+  const uint32_t ta = (uint32_t)(Fs - ra * Lout);
+  const int64_t rb = (Fe - 1) / Lout;
+  const uint32_t tb = (uint32_t)((Fe - 1) - rb * Lout);
+
+  // ---- stage the flat input window [I_lo, I_hi) -------------------------------------
+  int64_t I_lo = ra * (int64_t)L + (((int)ta - pad) > 0 ? ((int)ta - pad) : 0);
+  int64_t hi_t = (int64_t)tb - pad + K;
+  if (hi_t > (int64_t)L) hi_t = L;
+  const int64_t I_hi = rb * (int64_t)L + hi_t;
+  // aligned-down start so that global vectors land on 16B boundaries
+  int64_t t0 = I_lo + a.x_off;
+  t0 = (t0 >= 0 ? t0 / VEC : -((-t0 + VEC - 1) / VEC)) * VEC;
+  const int64_t I_base = t0 - a.x_off;
+  const int nvec = I_hi > I_lo ? (int)((I_hi - I_base + VEC - 1) / VEC) : 0;
+  for (int v = tid; v < nvec; v += DW_NT) {
+    const int64_t gi = I_base + (int64_t)v * VEC;
+    Vec16<T> val;
+    if (gi >= 0 && gi + VEC <= a.total_in) {
+      val.raw = *reinterpret_cast<const uint4*>(x + gi);
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const int64_t idx = gi + e;
+        val.e[e] = (idx >= 0 && idx < a.total_in) ? x[idx] : static_cast<T>(0.0f);
+      }
+    }
+    reinterpret_cast<uint4*>(win)[v] = val.raw;
+  }
+  // ---- stage per-row weights + bias (fp32) --------------------------------------------
+  const int nrows = (int)(rb - ra + 1);
+  const bool rows_in_lds = nrows <= DW_MAXR;
+  if (rows_in_lds) {
+    const int per = K + 1;
+    for (int i = tid; i < nrows * per; i += DW_NT) {
+      const int rr = i / per, j = i - rr * per;
+      const uint32_t c = fdiv((uint32_t)(ra + rr), a.div_c);
+      const uint32_t ch = (uint32_t)(ra + rr) - c * a.C;
+      float v;
+      if (j < K) v = to_f32(w[(int64_t)ch * K + j]);
+      else v = bias ? to_f32(bias[ch]) : 0.f;
+      wl[i] = v;
+    }
+  }
+  __syncthreads();
+
+  const int per = K + 1;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int vi = u * DW_NT + tid;
+    const int64_t f = F0 + (int64_t)vi * VEC;
+    if (f + VEC <= Fs || f >= Fe) continue;
+    bool fast = (f >= Fs) && (f + VEC <= Fe);
+    uint32_t r_rel = 0, t = 0;
+    if (fast) {
+      const uint32_t q = ta + (uint32_t)(f - Fs);
+      r_rel = fdiv(q, a.div_lout);
+      t = q - r_rel * Lout;
+      fast = (t + VEC <= Lout);
+    }
+    if (fast) {
+      const int64_t r = ra + r_rel;
+      float wk[KT > 0 ? KT : 1];
+      float bv;
+      const float* wrow = nullptr;
+      const T* wg = nullptr;
+      uint32_t ch = 0;
+      if (rows_in_lds) {
+        wrow = wl + r_rel * per;
+        bv = wrow[K];
+      } else {
+        const uint32_t c = fdiv((uint32_t)r, a.div_c);
+        ch = (uint32_t)r - c * a.C;
+        wg = w + (int64_t)ch * K;
+        bv = bias ? to_f32(bias[ch]) : 0.f;
+      }
+      if (KT > 0) {
+        if (rows_in_lds) {
+#pragma unroll
+          for (int j = 0; j < (KT > 0 ? KT : 1); ++j) wk[j] = wrow[j];
+        } else {
+#pragma unroll
+          for (int j = 0; j < (KT > 0 ? KT : 1); ++j) wk[j] = to_f32(wg[j]);
+        }
+      }
+      const int s = (int)t - pad;  // input position of window element 0
+      const int p0 = (int)(r * (int64_t)L + s - I_base);
+      const bool interior = (s >= 0) && (s + VEC + K - 1 <= (int)L);
+      float acc[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) acc[e] = bv;
+      if (KT > 0) {
+        constexpr int WN = VEC + (KT > 0 ? KT : 1) - 1;
+        float wv[WN];
+        if (interior) {
+#pragma unroll
+          for (int q = 0; q < WN; ++q) wv[q] = to_f32(win[p0 + q]);
+        } else {
+#pragma unroll
+          for (int q = 0; q < WN; ++q) {
+            const int pos = s + q;
+            wv[q] = ((unsigned)pos < L) ? to_f32(win[p0 + q]) : 0.f;
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < VEC; ++e)
+#pragma unroll
+          for (int j = 0; j < (KT > 0 ? KT : 1); ++j) acc[e] = fmaf(wk[j], wv[e + j], acc[e]);
+      } else {
+        for (int j = 0; j < K; ++j) {
+          float wj;
+          if (rows_in_lds) wj = wrow[j];
+          else wj = to_f32(wg[j]);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            const int pos = s + e + j;
+            const float xv = (interior || (unsigned)pos < L) ? to_f32(win[p0 + e + j]) : 0.f;
+            acc[e] = fmaf(wj, xv, acc[e]);
+          }
+        }
+      }
+      Vec16<T> o;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        float v = acc[e];
+        if (a.silu) v = silu_f32(v);
+        o.e[e] = from_f32<T>(v);
+      }
+      *reinterpret_cast<uint4*>(y + f) = o.raw;
+    } else {
+      // row boundary inside the vector, or a partial vector at the tensor ends
+#pragma unroll 1
+      for (int e = 0; e < VEC; ++e) {
+        const int64_t fe = f + e;
+        if (fe < Fs || fe >= Fe) continue;
+        const uint32_t q = ta + (uint32_t)(fe - Fs);
+        const uint32_t rr = fdiv(q, a.div_lout);
+        const uint32_t te = q - rr * Lout;
+        const int64_t r = ra + rr;
+        float acc, wj;
+        const uint32_t c = fdiv((uint32_t)r, a.div_c);
+        const uint32_t ch = (uint32_t)r - c * a.C;
+        if (rows_in_lds) acc = wl[rr * per + K];
+        else acc = bias ? to_f32(bias[ch]) : 0.f;
+        const int s = (int)te - pad;
+        const int p0 = (int)(r * (int64_t)L + s - I_base);
+        for (int j = 0; j < K; ++j) {
+          const int pos = s + j;
+          if ((unsigned)pos >= L) continue;
+          wj = rows_in_lds ? wl[rr * per + j] : to_f32(w[(int64_t)ch * K + j]);
+          acc = fmaf(wj, to_f32(win[p0 + j]), acc);
+        }
+        if (a.silu) acc = silu_f32(acc);
+        y[fe] = from_f32<T>(acc);
+      }
+    }
+  }
+}
+
+// One output per thread, straight from global memory.  Generic fallback.
+template <typename T>
+__global__ __launch_bounds__(DW_NT) void dwconv1d_direct_kernel(DwArgs a) {
+  const T* __restrict__ x = static_cast<const T*>(a.x);
+  const T* __restrict__ w = static_cast<const T*>(a.w);
+  const T* __restrict__ bias = static_cast<const T*>(a.b);
+  T* __restrict__ y = static_cast<T*>(a.y);
+  const int64_t f = (int64_t)blockIdx.x * DW_NT + threadIdx.x;
+  if (f >= a.total_out) return;
+  const int64_t r = f / a.Lout;
+  const int64_t t = f - r * a.Lout;
+  const int64_t ch = r % a.C;
+  float acc = bias ? to_f32(bias[ch]) : 0.f;
+  const int64_t s = t - a.pad;
+  for (int j = 0; j < a.K; ++j) {
+    const int64_t pos = s + j;
+    if (pos < 0 || pos >= (int64_t)a.L) continue;
+    acc = fmaf(to_f32(w[ch * a.K + j]), to_f32(x[r * (int64_t)a.L + pos]), acc);
+  }
+  if (a.silu) acc = silu_f32(acc);
+  y[f] = from_f32<T>(acc);
+}
+
+struct DwVariant {
+  const char* name;
+  int opt;  // outputs per thread; 0 = direct kernel
+};
+
+const DwVariant kDwVariants[] = {
+    {"lds_opt16", 16},
+    {"lds_opt8", 8},
+    {"lds_opt32", 32},
+    {"direct", 0},
+};
+constexpr int kNumDw = sizeof(kDwVariants) / sizeof(kDwVariants[0]);
+
+template <typename T, int KT, int OPT>
+int launch_lds_t(const DwArgs& a, size_t shmem, hipStream_t s) {
+  constexpr int TO = DW_NT * OPT;
+  const int64_t nblk = (a.total_out + a.y_off + TO - 1) / TO;
+  if (nblk > 0x7fffffff) return fail(ATK_UNSUPPORTED, "dwconv1d: grid too large");
+  hipLaunchKernelGGL((dwconv1d_lds_kernel<T, KT, OPT>), dim3((unsigned)nblk), dim3(DW_NT),
+                     shmem, s, a);
+  return check_launch("dwconv1d_lds_kernel");
+}
+
+template <typename T, int OPT>
+int launch_lds_k(const DwArgs& a, size_t shmem, hipStream_t s) {
+  switch (a.K) {
+    case 2: return launch_lds_t<T, 2, OPT>(a, shmem, s);
+    case 3: return launch_lds_t<T, 3, OPT>(a, shmem, s);
+    case 4: return launch_lds_t<T, 4, OPT>(a, shmem, s);
+    case 5: return launch_lds_t<T, 5, OPT>(a, shmem, s);
+    default: return launch_lds_t<T, 0, OPT>(a, shmem, s);
+  }
+}
+
+template <typename T>
+int launch_dw(DwArgs a, int variant, hipStream_t s) {
+  constexpr int VEC = 16 / sizeof(T);
+  const int opt = kDwVariants[variant].opt;
+  if (opt == 0 || opt < VEC) {
+    const int64_t nblk = (a.total_out + DW_NT - 1) / DW_NT;
+    if (nblk > 0x7fffffff) return fail(ATK_UNSUPPORTED, "dwconv1d: grid too large");
+    hipLaunchKernelGGL((dwconv1d_direct_kernel<T>), dim3((unsigned)nblk), dim3(DW_NT), 0, s, a);
+    return check_launch("dwconv1d_direct_kernel");
+  }
+  // LDS window bound for one tile (see the kernel): TO outputs span at most
+  // floor((TO-1)/Lout)+1 row boundaries, each adding (L - Lout) inputs when L > Lout.
+  const int64_t TO = (int64_t)DW_NT * opt;
+  const int64_t extra_rows = (TO - 1) / a.Lout + 1;
+  int64_t need = TO + a.K + a.pad + 2 * VEC;
+  if ((int64_t)a.L > (int64_t)a.Lout) need += extra_rows * ((int64_t)a.L - a.Lout);
+  need = (need + VEC - 1) / VEC * VEC;
+  const size_t shmem = (size_t)need * sizeof(T) + (size_t)DW_MAXR * (a.K + 1) * sizeof(float);
+  if (shmem > 64 * 1024) return fail(ATK_UNSUPPORTED, "dwconv1d: LDS window too large for variant");
+  a.win_cap = (int)need;
+  switch (opt) {
+    case 8: return launch_lds_k<T, 8>(a, shmem, s);
+    case 16: return launch_lds_k<T, 16>(a, shmem, s);
+    case 32: return launch_lds_k<T, 32>(a, shmem, s);
+    default: return fail(ATK_UNSUPPORTED, "dwconv1d: bad variant");
+  }
+}
+
+}  // namespace
+
+int dwconv1d_num_variants() { return kNumDw; }
+const char* dwconv1d_variant_name(int v) {
+  return (v >= 0 && v < kNumDw) ? kDwVariants[v].name : nullptr;
+}
+
+}  // namespace atk
+
+extern "C" int atk_dwconv1d_fwd(const void* x, const void* w, const void* bias, void* y,
+                                int64_t N, int64_t C, int64_t L, int K, int pad_left,
+                                int64_t L_out, int dtype, int fuse_silu, int variant,
+                                atk_stream_t stream) {
+  using namespace atk;
+  if (!dtype_ok(dtype)) return fail(ATK_EINVAL, "dwconv1d: unknown dtype code %d", dtype);
+  if (N < 0 || C <= 0 || L < 0 || L_out < 0) return fail(ATK_EINVAL, "dwconv1d: bad sizes");
+  if (K < 1 || K > DW_KMAX) return fail(ATK_UNSUPPORTED, "dwconv1d: kernel width %d outside [1, %d]", K, DW_KMAX);
+  if (pad_left < 0 || pad_left > DW_PADMAX) return fail(ATK_UNSUPPORTED, "dwconv1d: padding %d outside [0, %d]", pad_left, DW_PADMAX);
+  if (variant < 0) variant = 0;
+  if (variant >= kNumDw) return fail(ATK_EINVAL, "dwconv1d: variant %d out of range", variant);
+  const int64_t total_out = N * C * L_out;
+  if (total_out == 0) return ATK_OK;
+  if (!x || !w || !y) return fail(ATK_EINVAL, "dwconv1d: null pointer");
+  const int64_t rows = N * C;
+  if (rows >= (1ll << 31) || L >= (1ll << 30) || L_out >= (1ll << 30))
+    return fail(ATK_UNSUPPORTED, "dwconv1d: sizes exceed 32-bit row/column indexing");
+  const size_t es = dtype_size(dtype);
+  const uintptr_t xa = reinterpret_cast<uintptr_t>(x), ya = reinterpret_cast<uintptr_t>(y);
+  if ((xa % es) || (ya % es)) return fail(ATK_EINVAL, "dwconv1d: misaligned element pointer");
+  DwArgs a;
+  a.x = x; a.w = w; a.b = bias; a.y = y;
+  a.total_in = rows * L;
+  a.total_out = total_out;
+  a.C = (uint32_t)C; a.L = (uint32_t)L; a.Lout = (uint32_t)L_out;
+  a.K = K; a.pad = pad_left;
+  a.x_off = (int)((xa & 15u) / es);
+  a.y_off = (int)((ya & 15u) / es);
+  a.silu = fuse_silu ? 1 : 0;
+  a.div_lout = make_fastdiv((uint32_t)L_out);
+  a.div_c = make_fastdiv((uint32_t)C);
+  a.win_cap = 0;
+  // fdiv() needs numerators below 2^31: row-relative offsets stay below L_out + tile.
+  if ((uint64_t)L_out + 65536 >= (1ull << 31)) return fail(ATK_UNSUPPORTED, "dwconv1d: L_out too large");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case ATK_F32: return launch_dw<float>(a, variant, s);
+    case ATK_F16: return launch_dw<_Float16>(a, variant, s);
+    default: return launch_dw<__bf16>(a, variant, s);
+  }
+}

@@ -1,0 +1,109 @@
+"""GPU parity of the dense conv2d/conv3d kernels (C ABI atk_conv_fwd), every variant,
+against the float64 oracle.  Bars: fp32 <= 1e-5 max-abs-rel, fp16/bf16 <= 1e-2."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+BAR = {torch.float32: 1e-5, torch.float16: 1e-2, torch.bfloat16: 1e-2}
+
+
+def _native():
+    from amd_tuned_torch import _native
+    return _native
+
+
+def _inputs(xshape, wshape, dtype, seed=0, bias=True):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(*xshape, generator=g)
+    fan_in = math.prod(wshape[1:])
+    w = torch.randn(*wshape, generator=g) * math.sqrt(2.0 / fan_in)  # kaiming-normal
+    b = torch.randn(wshape[0], generator=g) * 0.1 if bias else None
+    return x.to(dtype), w.to(dtype), (b.to(dtype) if bias else None)
+
+
+def _variants_for(dtype):
+    nat = _native()
+    names = nat.variants(nat.OP_CONV)
+    out = []
+    for i, n in enumerate(names):
+        if n.startswith("f32_") and dtype != torch.float32:
+            continue
+        if n.startswith("h_") and dtype == torch.float32:
+            continue
+        out.append((i, n))
+    return out
+
+
+CONV3D = [
+    # xshape, wshape, stride, padding, dilation
+    ((1, 8, 6, 7, 9), (16, 8, 3, 3, 3), 1, 1, 1),
+    ((2, 5, 5, 6, 7), (3, 5, 3, 3, 3), 1, 1, 1),           # channel counts off the tiles
+    ((1, 16, 4, 9, 10), (8, 16, 1, 3, 3), (1, 2, 2), (0, 1, 1), 1),
+    ((1, 4, 7, 8, 9), (6, 4, 3, 2, 3), (2, 1, 1), (1, 0, 2), (1, 2, 1)),
+    ((1, 32, 8, 16, 16), (64, 32, 3, 3, 3), 1, 1, 1),
+    ((1, 8, 9, 9, 9), (8, 8, 5, 5, 5), 1, 2, 1),
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("case", CONV3D, ids=lambda c: "x".join(map(str, c[0])) + "_w" + "x".join(map(str, c[1])))
+def test_conv3d_all_variants(dev, case, dtype):
+    xs, ws, s, p, d = case
+    nat = _native()
+    x, w, b = _inputs(xs, ws, dtype, seed=sum(xs))
+    ref = O.conv3d(x, w, b, s, p, d)
+    for vi, name in _variants_for(dtype):
+        try:
+            y = nat.conv3d(x.to(dev), w.to(dev), b.to(dev), s, p, d, variant=vi)
+        except nat.Unsupported:
+            continue
+        torch.cuda.synchronize()
+        assert tuple(y.shape) == ref.shape
+        err = O.max_rel_err(y.cpu(), ref)
+        assert err <= BAR[dtype], f"{name}: max_rel_err {err:.3g}"
+
+
+CONV2D = [
+    ((2, 8, 13, 17), (16, 8, 3, 3), 1, 1, 1),
+    ((1, 16, 20, 20), (8, 16, 3, 3), 2, 1, 1),
+    ((1, 3, 11, 12), (5, 3, 5, 3), 1, (2, 1), (1, 2)),
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("case", CONV2D, ids=lambda c: "x".join(map(str, c[0])))
+def test_conv2d_all_variants(dev, case, dtype):
+    xs, ws, s, p, d = case
+    nat = _native()
+    x, w, b = _inputs(xs, ws, dtype, seed=sum(xs))
+    ref = O.conv2d(x, w, b, s, p, d)
+    for vi, name in _variants_for(dtype):
+        try:
+            y = nat.conv2d(x.to(dev), w.to(dev), b.to(dev), s, p, d, variant=vi)
+        except nat.Unsupported:
+            continue
+        torch.cuda.synchronize()
+        err = O.max_rel_err(y.cpu(), ref)
+        assert err <= BAR[dtype], f"{name}: max_rel_err {err:.3g}"
+
+
+def test_conv_no_bias(dev):
+    nat = _native()
+    x, w, _ = _inputs((1, 8, 4, 6, 6), (8, 8, 3, 3, 3), torch.float32, seed=4, bias=False)
+    ref = O.conv3d(x, w, None, 1, 1, 1)
+    for vi, name in _variants_for(torch.float32):
+        try:
+            y = nat.conv3d(x.to(dev), w.to(dev), None, 1, 1, 1, variant=vi)
+        except nat.Unsupported:
+            continue
+        torch.cuda.synchronize()
+        assert O.max_rel_err(y.cpu(), ref) <= 1e-5, name

@@ -1,0 +1,130 @@
+"""GPU parity of the depthwise conv1d kernel (C ABI atk_dwconv1d_fwd through the ctypes
+binding) against the float64 oracle.  Bars: fp32 max-abs-rel <= 1e-5, fp16/bf16 <= 1e-2
+(fp32 accumulation)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+BAR = {torch.float32: 1e-5, torch.float16: 1e-2, torch.bfloat16: 1e-2}
+
+
+def _native():
+    from amd_tuned_torch import _native
+    return _native
+
+
+def _inputs(N, C, L, K, dtype, seed=0, bias=True):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(N, C, L, generator=g)
+    w = torch.randn(C, K, generator=g) * (1.0 / K) ** 0.5
+    b = torch.randn(C, generator=g) * 0.1 ** 0.5 if bias else None
+    return x.to(dtype), w.to(dtype), (b.to(dtype) if b is not None else None)
+
+
+def _check(y, x, w, b, pad, l_out, silu=False):
+    ref = O.dwconv1d(x, w, b, pad, l_out, silu=silu)
+    assert tuple(y.shape) == ref.shape
+    err = O.max_rel_err(y, ref)
+    assert err <= BAR[y.dtype], f"max_rel_err {err:.3g} > {BAR[y.dtype]}"
+    return err
+
+
+CASES = [
+    # (N, C, L, K, pad_left, l_out)
+    (2, 3, 37, 3, 1, 37),        # symmetric
+    (2, 3, 37, 4, 3, 40),        # causal, stock output shape (rows not 16B aligned)
+    (2, 3, 37, 4, 3, 37),        # causal, truncated to L
+    (2, 5, 64, 2, 1, 65),        # causal K=2
+    (1, 4, 100, 5, 2, 100),
+    (2, 2, 50, 7, 3, 50),        # generic-K path
+    (1, 3, 40, 31, 15, 40),      # wide kernel
+    (1, 2, 30, 3, 0, 28),        # 'valid' (L_out < L)
+    (1, 2, 10, 3, 5, 18),        # padding wider than the kernel
+    (3, 7, 1, 3, 1, 1),          # L = 1
+    (2, 16, 8, 1, 0, 8),         # K = 1
+    (1, 8, 4096, 4, 3, 4099),    # long rows, stock causal
+    (4, 64, 333, 3, 1, 333),     # many short rows per tile
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(map(str, c)))
+def test_dwconv1d_all_variants(dev, case, dtype):
+    N, C, L, K, pad, l_out = case
+    nat = _native()
+    x, w, b = _inputs(N, C, L, K, dtype, seed=sum(case))
+    xd, wd, bd = x.to(dev), w.to(dev), b.to(dev)
+    for vi, name in enumerate(nat.variants(nat.OP_DWCONV1D)):
+        y = nat.dwconv1d(xd, wd, bd, pad, l_out, variant=vi)
+        torch.cuda.synchronize()
+        _check(y.cpu(), x, w, b, pad, l_out)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_dwconv1d_no_bias_and_silu(dev, dtype):
+    nat = _native()
+    x, w, _ = _inputs(2, 6, 123, 4, dtype, seed=7, bias=False)
+    y = nat.dwconv1d(x.to(dev), w.to(dev), None, 3, 126)
+    _check(y.cpu(), x, w, None, 3, 126)
+    x, w, b = _inputs(2, 6, 123, 4, dtype, seed=8)
+    y = nat.dwconv1d(x.to(dev), w.to(dev), b.to(dev), 3, 123, silu=True)
+    _check(y.cpu(), x, w, b, 3, 123, silu=True)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_dwconv1d_misaligned_pointers(dev, dtype):
+    """x and y views whose data pointers are not 16-byte aligned."""
+    nat = _native()
+    N, C, L, K = 2, 5, 77, 3
+    x, w, b = _inputs(N, C, L, K, dtype, seed=3)
+    xb = torch.zeros(N * C * L + 3, dtype=dtype)
+    xb[1:1 + N * C * L] = x.flatten()
+    xv = xb.to(dev)[1:1 + N * C * L].view(N, C, L)
+    for l_out, pad in ((L, 1), (L + 2, 2)):
+        ob = torch.full((N * C * l_out + 5,), float("nan"), dtype=dtype, device=dev)
+        yv = ob[3:3 + N * C * l_out].view(N, C, l_out)
+        for vi in range(len(nat.variants(nat.OP_DWCONV1D))):
+            nat.dwconv1d(xv, w.to(dev), b.to(dev), pad, l_out, variant=vi, out=yv)
+            torch.cuda.synchronize()
+            _check(yv.cpu(), x, w, b, pad, l_out)
+            # the guard elements around the output view are untouched
+            assert torch.isnan(ob[:3].float()).all() and torch.isnan(ob[3 + N * C * l_out:].float()).all()
+
+
+def test_dwconv1d_empty_batch(dev):
+    nat = _native()
+    x = torch.zeros(0, 4, 16, device=dev)
+    y = nat.dwconv1d(x, torch.zeros(4, 3, device=dev), None, 1, 16)
+    assert y.shape == (0, 4, 16)
+
+
+def test_dwconv1d_rejects_bad_args(dev):
+    nat = _native()
+    x = torch.zeros(1, 4, 16, device=dev)
+    with pytest.raises(RuntimeError):
+        nat.dwconv1d(x, torch.zeros(5, 3, device=dev), None, 1, 16)       # channel mismatch
+    with pytest.raises(nat.Unsupported):
+        nat.dwconv1d(x, torch.zeros(4, 65, device=dev), None, 1, 16)      # K > 64
+    with pytest.raises(RuntimeError):
+        nat.dwconv1d(x, torch.zeros(4, 3, device=dev, dtype=torch.float16), None, 1, 16)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("mode", ["causal_stock", "causal_trunc", "symmetric"])
+def test_dwconv1d_config2_full_size(dev, dtype, mode):
+    """BASELINE config 2 at its full size: N=16, C=2048, L=8192; causal K=4 (stock shape
+    and truncated) and symmetric K=3 -- every output checked against the oracle."""
+    N, C, L = 16, 2048, 8192
+    K, pad, l_out = {"causal_stock": (4, 3, L + 3), "causal_trunc": (4, 3, L),
+                     "symmetric": (3, 1, L)}[mode]
+    x, w, b = _inputs(N, C, L, K, dtype, seed=1002)
+    nat = _native()
+    y = nat.dwconv1d(x.to(dev), w.to(dev), b.to(dev), pad, l_out)
+    torch.cuda.synchronize()
+    _check(y.cpu(), x, w, b, pad, l_out)

@@ -1,0 +1,151 @@
+"""GPU parity of the GroupNorm (+ fused SiLU) kernels (C ABI atk_group_norm_fwd) against
+the float64 oracle, every variant.  Bars: fp32 <= 1e-5 max-abs-rel, fp16/bf16 <= 1e-2."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+BAR = {torch.float32: 1e-5, torch.float16: 1e-2, torch.bfloat16: 1e-2}
+
+
+def _native():
+    from amd_tuned_torch import _native
+    return _native
+
+
+def _inputs(shape, dtype, seed=0, affine=True, pdtype=None):
+    g = torch.Generator().manual_seed(seed)
+    C = shape[1]
+    mu = torch.rand(C, generator=g) * 4 - 2          # per-channel means in U(-2, 2)
+    x = torch.randn(*shape, generator=g) + mu.view(1, C, *([1] * (len(shape) - 2)))
+    gamma = 1 + 0.1 * torch.randn(C, generator=g)
+    beta = 0.1 * torch.randn(C, generator=g)
+    pdtype = pdtype or dtype
+    if not affine:
+        return x.to(dtype), None, None
+    return x.to(dtype), gamma.to(pdtype), beta.to(pdtype)
+
+
+def _check(y, x, G, gamma, beta, eps, silu=False):
+    ref = O.group_norm(x, G, gamma, beta, eps, silu=silu)
+    err = O.max_rel_err(y, ref)
+    assert err <= BAR[y.dtype], f"max_rel_err {err:.3g} > {BAR[y.dtype]}"
+    return err
+
+
+SHAPES = [
+    ((2, 64, 8, 8), 8),           # one small slice per group
+    ((1, 32, 128, 128), 2),       # groups of 262144 elements: several slices, cooperative
+    ((2, 12, 5, 7, 8), 3),        # 3-D spatial
+    ((3, 10, 24), 5),             # 1-D spatial
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("shape_g", SHAPES, ids=lambda s: "x".join(map(str, s[0])) + f"_g{s[1]}")
+def test_group_norm_all_variants(dev, shape_g, dtype):
+    shape, G = shape_g
+    nat = _native()
+    x, gm, bt = _inputs(shape, dtype, seed=len(shape) + G)
+    xd, gd, bd = x.to(dev), gm.to(dev), bt.to(dev)
+    ran = 0
+    for vi, name in enumerate(nat.variants(nat.OP_GROUP_NORM)):
+        for silu in (False, True):
+            try:
+                y = nat.group_norm(xd, G, gd, bd, 1e-5, silu=silu, variant=vi)
+            except nat.Unsupported:
+                assert name != "twopass", "the two-pass variant must accept every shape"
+                continue
+            torch.cuda.synchronize()
+            _check(y.cpu(), x, G, gm, bt, 1e-5, silu=silu)
+            ran += 1
+    assert ran >= 2
+    assert not nat.group_norm_barrier_error(dev)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_group_norm_odd_spatial_and_2d(dev, dtype):
+    """S not a multiple of the vector width, and [N, C] input (S = 1): only the two-pass
+    kernel takes them; the register-resident variants decline."""
+    nat = _native()
+    names = nat.variants(nat.OP_GROUP_NORM)
+    for shape, G in (((2, 6, 7, 7), 3), ((4, 16), 4)):
+        x, gm, bt = _inputs(shape, dtype, seed=5)
+        for vi, name in enumerate(names):
+            if name == "twopass":
+                y = nat.group_norm(x.to(dev), G, gm.to(dev), bt.to(dev), 1e-5, variant=vi)
+                torch.cuda.synchronize()
+                _check(y.cpu(), x, G, gm, bt, 1e-5)
+            else:
+                with pytest.raises(nat.Unsupported):
+                    nat.group_norm(x.to(dev), G, gm.to(dev), bt.to(dev), 1e-5, variant=vi)
+
+
+def test_group_norm_non_affine_and_mixed_param_dtype(dev):
+    nat = _native()
+    x, _, _ = _inputs((2, 32, 16, 16), torch.float16, seed=9, affine=False)
+    y = nat.group_norm(x.to(dev), 8, None, None, 1e-6)
+    _check(y.cpu(), x, 8, None, None, 1e-6)
+    x, gm, bt = _inputs((2, 32, 16, 16), torch.bfloat16, seed=10, pdtype=torch.float32)
+    y = nat.group_norm(x.to(dev), 8, gm.to(dev), bt.to(dev), 1e-5, silu=True)
+    _check(y.cpu(), x, 8, gm, bt, 1e-5, silu=True)
+
+
+def test_group_norm_misaligned_pointer(dev):
+    nat = _native()
+    x, gm, bt = _inputs((2, 16, 8, 8), torch.float16, seed=11)
+    buf = torch.zeros(x.numel() + 1, dtype=x.dtype)
+    buf[1:] = x.flatten()
+    xv = buf.to(dev)[1:].view(x.shape)
+    names = nat.variants(nat.OP_GROUP_NORM)
+    y = nat.group_norm(xv, 4, gm.to(dev), bt.to(dev), 1e-5, variant=names.index("twopass"))
+    _check(y.cpu(), x, 4, gm, bt, 1e-5)
+    with pytest.raises(nat.Unsupported):
+        nat.group_norm(xv, 4, gm.to(dev), bt.to(dev), 1e-5, variant=names.index("res_nt1024_v8"))
+
+
+def test_group_norm_repeated_calls_keep_barrier_consistent(dev):
+    """Cooperative variants reuse the workspace barrier: many calls in a row, different
+    slice counts, all correct and no spin-bound hits."""
+    nat = _native()
+    names = nat.variants(nat.OP_GROUP_NORM)
+    x, gm, bt = _inputs((1, 32, 128, 128), torch.bfloat16, seed=12)
+    xd, gd, bd = x.to(dev), gm.to(dev), bt.to(dev)
+    ref = O.group_norm(x, 2, gm, bt, 1e-5)
+    for _ in range(5):
+        for name in ("res_nt256_v8", "res_nt1024_v8", "res_nt512_v8"):
+            y = nat.group_norm(xd, 2, gd, bd, 1e-5, variant=names.index(name))
+            torch.cuda.synchronize()
+            assert O.max_rel_err(y.cpu(), ref) <= 1e-2
+    assert not nat.group_norm_barrier_error(dev)
+
+
+CONFIG3 = [((8, 512, 64, 64), 32, 1e-5), ((1, 512, 16, 64, 64), 32, 1e-5),
+           ((1, 256, 8, 64, 64), 32, 1e-6)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("cfg", CONFIG3, ids=["c3_nchw", "c3_ncdhw", "c5_gn"])
+def test_group_norm_config_full_size(dev, cfg, dtype):
+    """BASELINE configs 3 and 5 (GroupNorm part) at full size, plain and fused SiLU, every
+    variant that accepts the shape."""
+    shape, G, eps = cfg
+    nat = _native()
+    x, gm, bt = _inputs(shape, dtype, seed=1003)
+    xd, gd, bd = x.to(dev), gm.to(dev), bt.to(dev)
+    for silu in (False, True):
+        ref = O.group_norm(x, G, gm, bt, eps, silu=silu)
+        for vi, name in enumerate(nat.variants(nat.OP_GROUP_NORM)):
+            try:
+                y = nat.group_norm(xd, G, gd, bd, eps, silu=silu, variant=vi)
+            except nat.Unsupported:
+                continue
+            torch.cuda.synchronize()
+            err = O.max_rel_err(y.cpu(), ref)
+            assert err <= 1e-2, f"{name} silu={silu}: {err:.3g}"
+    assert not nat.group_norm_barrier_error(dev)
