@@ -30,9 +30,13 @@ int check_launch(const char* what) {
 }
 
 int device_cu_count() {
+  // per device, queried once (the host code runs on one device at a time)
+  static int cached[64] = {0};
   int dev = 0, n = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < 64 && cached[dev] > 0) return cached[dev];
   if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < 64) cached[dev] = n;
   return n;
 }
 

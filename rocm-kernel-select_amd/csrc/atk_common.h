@@ -48,7 +48,35 @@ template <typename T> struct Vec16 {
   };
 };
 
-__device__ __forceinline__ float silu_f32(float v) { return v / (1.0f + __expf(-v)); }
+// SiLU v * sigmoid(v) with the hardware exp2 and reciprocal (about 1 ulp each); exp(-v)
+// overflowing to +inf gives v * 0 = -0 for very negative v, as the exact formula does.
+__device__ __forceinline__ float silu_f32(float v) {
+  return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v));
+}
+
+// 16-byte global accesses with an optional nontemporal (streaming) hint: data read or
+// written exactly once should not displace reusable lines in L2 / MALL.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+template <bool NT>
+__device__ __forceinline__ uint4 ld16(const void* p) {
+  uint4 r;
+  if (NT) {
+    u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    r.x = v.x; r.y = v.y; r.z = v.z; r.w = v.w;
+  } else {
+    r = *reinterpret_cast<const uint4*>(p);
+  }
+  return r;
+}
+template <bool NT>
+__device__ __forceinline__ void st16(void* p, uint4 r) {
+  if (NT) {
+    u32x4 v = {r.x, r.y, r.z, r.w};
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+  } else {
+    *reinterpret_cast<uint4*>(p) = r;
+  }
+}
 
 // ---------------------------------------------------------------------------
 // Wave64 / block reductions (fp32 sums).

@@ -1,14 +1,375 @@
-// MFMA implicit-GEMM conv kernels (placeholder table until the kernels land).
+// Dense conv2d/conv3d forward as an implicit GEMM on gfx950 MFMA.
+//
+//   Y[co, m] = bias[co] + sum_k Wt[co, k] * X_im2col[k, m]
+//   m = output position (n, z, y, x), k = (tap, ci), tap = (kd, kh, kw)
+//
+// The reference's kernel for this op (src/cuda/generated/conv3d_fp16_bm256_bn128_bk32_s2.cu:
+// 84-324) is a rocWMMA implicit GEMM with M = positions, N = Co, K = Ci*taps, gathering im2col
+// rows from global memory per K step.  This kernel is organised around CDNA4 instead:
+//
+//  * MFMA v_mfma_f32_32x32x16_{bf16,f16} (fp32 inputs: v_mfma_f32_32x32x2_f32 with four
+//    steps per 8-channel block), fp32 accumulation.  Weights are the MFMA A operand (32
+//    output channels per fragment) and im2col the B operand (32 positions per fragment), so
+//    accumulator lanes hold 32 consecutive positions of one channel: stores are coalesced
+//    along x in NCDHW.
+//  * The K loop runs over "stages" = (input-channel chunk of CB, kd).  A stage stages the
+//    input PATCH its tile needs -- (TY-1)*sh+(KH-1)*dh+1 rows x (TX-1)*sw+(KW-1)*dw+1 columns
+//    of one input plane -- into LDS once, channels-last with a 16-byte pad per position
+//    (conflict-free ds_read_b128), and every tap (kh, kw) of the stage reads its im2col
+//    fragments from that patch: each input element is fetched from memory once per stage
+//    instead of once per tap.
+//  * Weights are pre-packed (a small kernel, into the workspace) into fragment order
+//    [tap][ci-block][co-block32][32 co][KB ci]: a wave's A fragment is one contiguous 1 KB
+//    global load, L2-resident across the workgroups that share the output-channel tile.
+//  * Split-K over stages for shapes with too few output tiles to fill 256 CUs, with
+//    per-split fp32 partials summed in a deterministic finalize kernel.
 #include "conv_common.h"
 
 namespace atk {
 
-int conv_igemm_num_variants() { return 0; }
-const char* conv_igemm_variant_name(int) { return nullptr; }
-size_t conv_igemm_workspace_bytes(const ConvShape&, int) { return 0; }
-int conv_igemm_launch(const ConvShape&, const void*, const void*, const void*, void*, int, void*,
-                      size_t, hipStream_t) {
-  return fail(ATK_UNSUPPORTED, "conv: no implicit-GEMM variants in this build");
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+struct IgArgs {
+  const void* x;
+  const void* wp;     // packed weights
+  const void* bias;
+  void* y;
+  float* part;        // split-K partials [splits][N*Co*SPo], or null
+  int N, Ci, D, H, W, Co, KD, KH, KW, sd, sh, sw, pd, ph, pw, dd, dh, dw, Do, Ho, Wo;
+  int TX, TY, tiles_x, tiles_y;
+  int PX, PY;
+  int n_stages;       // n_cc * KD
+  int stages_per_split;
+  int n_kb;           // ci k-blocks in the packed weights = n_cc * CB / KB
+  int co_blocks;      // 32-row co blocks in the packed weights (multiple of BN / 32)
+};
+
+template <typename T> struct MfmaTraits;
+template <> struct MfmaTraits<__bf16> { static constexpr int KB = 16, VEC = 8; };
+template <> struct MfmaTraits<_Float16> { static constexpr int KB = 16, VEC = 8; };
+template <> struct MfmaTraits<float> { static constexpr int KB = 8, VEC = 4; };
+
+__device__ __forceinline__ void mfma_block(f32x16& acc, const uint4& a, const uint4& b, __bf16*) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8*>(&a),
+                                                *reinterpret_cast<const bf16x8*>(&b), acc, 0, 0, 0);
+}
+__device__ __forceinline__ void mfma_block(f32x16& acc, const uint4& a, const uint4& b, _Float16*) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const f16x8*>(&a),
+                                               *reinterpret_cast<const f16x8*>(&b), acc, 0, 0, 0);
+}
+// fp32: the lane's 4 consecutive channels feed 4 MFMA steps; step e pairs channels (e, 4+e)
+// of the 8-channel block across the two lane halves, identically for A and B.
+__device__ __forceinline__ void mfma_block(f32x16& acc, const uint4& a, const uint4& b, float*) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.x), __uint_as_float(b.x), acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.y), __uint_as_float(b.y), acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.z), __uint_as_float(b.z), acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.w), __uint_as_float(b.w), acc, 0, 0, 0);
+}
+
+template <typename T, int WCO, int WSP, int FCO, int FSP, int CB>
+__global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm_kernel(IgArgs a) {
+  constexpr int NT = 64 * WCO * WSP;
+  constexpr int KB = MfmaTraits<T>::KB, VEC = MfmaTraits<T>::VEC;
+  constexpr int CBS = CB + VEC;           // padded channel stride of a patch position
+  constexpr int BN = WCO * FCO * 32;      // output channels per workgroup
+  static_assert(CB % KB == 0, "chunk must hold whole k-blocks");
+  extern __shared__ uint4 lds_raw[];
+  T* patch = reinterpret_cast<T*>(lds_raw);
+
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int wco = wv % WCO, wsp = wv / WCO;
+  const int half = lane >> 5, col = lane & 31;
+
+  // ---- tile coordinates ---------------------------------------------------------------
+  int t = blockIdx.x;
+  const int tx_t = t % a.tiles_x; t /= a.tiles_x;
+  const int ty_t = t % a.tiles_y; t /= a.tiles_y;
+  const int oz = t % a.Do;
+  const int n = t / a.Do;
+  const int co_tile = blockIdx.y;
+  const int split = blockIdx.z;
+  const int s_begin = split * a.stages_per_split;
+  const int s_end = min(a.n_stages, s_begin + a.stages_per_split);
+  const int oy0 = ty_t * a.TY, ox0 = tx_t * a.TX;
+  const int iy0 = oy0 * a.sh - a.ph, ix0 = ox0 * a.sw - a.pw;
+
+  // per-lane patch base position of each im2col column this lane feeds
+  int pos0[FSP];
+#pragma unroll
+  for (int j = 0; j < FSP; ++j) {
+    const int m = (wsp * FSP + j) * 32 + col;
+    const int ty = m / a.TX, tx = m - (m / a.TX) * a.TX;
+    pos0[j] = (ty * a.sh) * a.PX + tx * a.sw;
+  }
+
+  f32x16 acc[FCO][FSP];
+#pragma unroll
+  for (int i = 0; i < FCO; ++i)
+#pragma unroll
+    for (int j = 0; j < FSP; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  const T* __restrict__ x = static_cast<const T*>(a.x);
+  const T* __restrict__ wp = static_cast<const T*>(a.wp);
+  const int64_t plane = (int64_t)a.H * a.W;
+  const int npatch = a.PY * a.PX;
+  const int taps = a.KD * a.KH * a.KW;
+  const int co_blk0 = co_tile * (BN / 32) + wco * FCO;
+  // element offset of this lane inside a 32 x KB weight fragment
+  const int wlane = col * KB + half * VEC;
+
+  for (int s = s_begin; s < s_end; ++s) {
+    const int cc = s / a.KD, kd = s - (s / a.KD) * a.KD;
+    const int iz = oz * a.sd - a.pd + kd * a.dd;
+    const bool zin = (unsigned)iz < (unsigned)a.D;
+    // ---- stage the input patch (channels-last) -----------------------------------------
+    __syncthreads();  // previous stage's readers are done with the patch
+    for (int idx = tid; idx < CB * npatch; idx += NT) {
+      const int cl = idx / npatch;
+      const int rem = idx - cl * npatch;
+      const int py = rem / a.PX, px = rem - (rem / a.PX) * a.PX;
+      const int ci = cc * CB + cl;
+      const int iy = iy0 + py, ix = ix0 + px;
+      T v = static_cast<T>(0.0f);
+      if (zin && ci < a.Ci && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W)
+        v = x[((int64_t)n * a.Ci + ci) * a.D * plane + (int64_t)iz * plane + (int64_t)iy * a.W + ix];
+      patch[rem * CBS + cl] = v;
+    }
+    __syncthreads();
+    if (!zin) continue;  // a padding plane contributes nothing
+    // ---- taps of this stage ---------------------------------------------------------------
+    for (int kh = 0; kh < a.KH; ++kh) {
+      for (int kw = 0; kw < a.KW; ++kw) {
+        const int tap = (kd * a.KH + kh) * a.KW + kw;
+        const int toff = (kh * a.dh) * a.PX + kw * a.dw;
+#pragma unroll
+        for (int kb = 0; kb < CB / KB; ++kb) {
+          const int kbg = cc * (CB / KB) + kb;
+          uint4 wf[FCO], pf[FSP];
+#pragma unroll
+          for (int i = 0; i < FCO; ++i) {
+            const int64_t frag = ((int64_t)tap * a.n_kb + kbg) * a.co_blocks + co_blk0 + i;
+            wf[i] = *reinterpret_cast<const uint4*>(wp + frag * (32 * KB) + wlane);
+          }
+#pragma unroll
+          for (int j = 0; j < FSP; ++j)
+            pf[j] = *reinterpret_cast<const uint4*>(patch + (pos0[j] + toff) * CBS + kb * KB + half * VEC);
+#pragma unroll
+          for (int i = 0; i < FCO; ++i)
+#pragma unroll
+            for (int j = 0; j < FSP; ++j) mfma_block(acc[i][j], wf[i], pf[j], static_cast<T*>(nullptr));
+        }
+      }
+    }
+    (void)taps;
+  }
+
+  // ---- epilogue: rows = output channels, columns = positions -----------------------------
+  const int64_t spo = (int64_t)a.Do * a.Ho * a.Wo;
+  const T* __restrict__ bias = static_cast<const T*>(a.bias);
+#pragma unroll
+  for (int j = 0; j < FSP; ++j) {
+    const int m = (wsp * FSP + j) * 32 + col;
+    const int ty = m / a.TX, tx = m - (m / a.TX) * a.TX;
+    const int oy = oy0 + ty, ox = ox0 + tx;
+    if (oy >= a.Ho || ox >= a.Wo) continue;
+    const int64_t sp = ((int64_t)oz * a.Ho + oy) * a.Wo + ox;
+#pragma unroll
+    for (int i = 0; i < FCO; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int co = co_tile * BN + (wco * FCO + i) * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+        if (co >= a.Co) continue;
+        const int64_t o = ((int64_t)n * a.Co + co) * spo + sp;
+        if (a.part) {
+          a.part[(int64_t)split * a.N * a.Co * spo + o] = acc[i][j][r];
+        } else {
+          float v = acc[i][j][r];
+          if (bias) v += to_f32(bias[co]);
+          static_cast<T*>(a.y)[o] = from_f32<T>(v);
+        }
+      }
+    }
+  }
+}
+
+// Packed weights Wp[tap][kb][co_block][32][KB] from w[Co][Ci][taps]; zero beyond Co / Ci.
+template <typename T>
+__global__ __launch_bounds__(256) void pack_weights_kernel(const T* __restrict__ w, T* __restrict__ wp,
+                                                           int Co, int Ci, int taps, int n_kb,
+                                                           int co_blocks, int64_t total) {
+  constexpr int KB = MfmaTraits<T>::KB;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int k = (int)(i % KB);
+  int64_t r = i / KB;
+  const int row = (int)(r % 32); r /= 32;
+  const int cb = (int)(r % co_blocks); r /= co_blocks;
+  const int kb = (int)(r % n_kb);
+  const int tap = (int)(r / n_kb);
+  const int co = cb * 32 + row, ci = kb * KB + k;
+  wp[i] = (co < Co && ci < Ci) ? w[((int64_t)co * Ci + ci) * taps + tap] : static_cast<T>(0.0f);
+}
+
+// y = sum over splits of the fp32 partials + bias
+template <typename T>
+__global__ __launch_bounds__(256) void splitk_finalize_kernel(const float* __restrict__ part, const T* __restrict__ bias,
+                                                              T* __restrict__ y, int splits, int Co, int64_t spo,
+                                                              int64_t total) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  float v = 0.f;
+  for (int s = 0; s < splits; ++s) v += part[(int64_t)s * total + i];
+  if (bias) v += to_f32(bias[(i / spo) % Co]);
+  y[i] = from_f32<T>(v);
+}
+
+struct IgVariant {
+  const char* name;
+  int dtype_class;  // 0 = 16-bit, 1 = fp32
+  int wco, wsp, fco, fsp, cb;
+};
+
+const IgVariant kIg[] = {
+    {"h_w22_f22_cb32", 0, 2, 2, 2, 2, 32},
+    {"h_w22_f42_cb32", 0, 2, 2, 4, 2, 32},
+    {"h_w22_f24_cb32", 0, 2, 2, 2, 4, 32},
+    {"h_w14_f22_cb32", 0, 1, 4, 2, 2, 32},
+    {"h_w22_f22_cb16", 0, 2, 2, 2, 2, 16},
+    {"f32_w22_f22_cb16", 1, 2, 2, 2, 2, 16},
+    {"f32_w14_f22_cb16", 1, 1, 4, 2, 2, 16},
+    {"f32_w22_f12_cb16", 1, 2, 2, 1, 2, 16},
+};
+constexpr int kNumIg = sizeof(kIg) / sizeof(kIg[0]);
+
+struct IgPlan {
+  IgArgs a;
+  int bn, bm, splits, nthreads;
+  size_t lds, wp_bytes, part_bytes;
+  int64_t tiles;
+};
+
+int plan_ig(const ConvShape& p, int v, IgPlan& pl) {
+  const IgVariant& vr = kIg[v];
+  const bool f32 = p.dtype == ATK_F32;
+  if ((vr.dtype_class == 1) != f32) return fail(ATK_UNSUPPORTED, "conv %s: dtype not served", vr.name);
+  const int es = f32 ? 4 : 2;
+  const int KB = f32 ? 8 : 16, VEC = f32 ? 4 : 8;
+  pl.bn = vr.wco * vr.fco * 32;
+  pl.bm = vr.wsp * vr.fsp * 32;
+  pl.nthreads = 64 * vr.wco * vr.wsp;
+  IgArgs& a = pl.a;
+  a.N = p.N; a.Ci = p.Ci; a.D = p.D; a.H = p.H; a.W = p.W; a.Co = p.Co;
+  a.KD = p.KD; a.KH = p.KH; a.KW = p.KW; a.sd = p.sd; a.sh = p.sh; a.sw = p.sw;
+  a.pd = p.pd; a.ph = p.ph; a.pw = p.pw; a.dd = p.dd; a.dh = p.dh; a.dw = p.dw;
+  a.Do = p.Do; a.Ho = p.Ho; a.Wo = p.Wo;
+  int tx = 1;
+  while (tx < p.Wo && tx < 64) tx <<= 1;
+  if (tx > pl.bm) tx = pl.bm;
+  a.TX = tx;
+  a.TY = pl.bm / tx;
+  a.tiles_x = (p.Wo + a.TX - 1) / a.TX;
+  a.tiles_y = (p.Ho + a.TY - 1) / a.TY;
+  a.PX = (a.TX - 1) * p.sw + (p.KW - 1) * p.dw + 1;
+  a.PY = (a.TY - 1) * p.sh + (p.KH - 1) * p.dh + 1;
+  const int n_cc = (p.Ci + vr.cb - 1) / vr.cb;
+  a.n_stages = n_cc * p.KD;
+  a.n_kb = n_cc * (vr.cb / KB);
+  a.co_blocks = (p.Co + pl.bn - 1) / pl.bn * (pl.bn / 32);
+  pl.lds = (size_t)a.PY * a.PX * (vr.cb + VEC) * es;
+  if (pl.lds > 64 * 1024) return fail(ATK_UNSUPPORTED, "conv %s: input patch of %zu bytes exceeds LDS", vr.name, pl.lds);
+  pl.tiles = (int64_t)p.N * p.Do * a.tiles_y * a.tiles_x;
+  const int co_tiles = (p.Co + pl.bn - 1) / pl.bn;
+  if (pl.tiles > 0x7fffffff || co_tiles > 65535) return fail(ATK_UNSUPPORTED, "conv %s: grid too large", vr.name);
+  // split K (stages) until the grid covers the chip about twice
+  const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+  const int64_t wgs = pl.tiles * co_tiles;
+  int splits = 1;
+  while (wgs * splits < 2 * cus && splits * 2 <= a.n_stages && splits < 16) splits *= 2;
+  a.stages_per_split = (a.n_stages + splits - 1) / splits;
+  splits = (a.n_stages + a.stages_per_split - 1) / a.stages_per_split;
+  pl.splits = splits;
+  const int taps = p.KD * p.KH * p.KW;
+  pl.wp_bytes = (size_t)taps * a.n_kb * a.co_blocks * 32 * KB * es;
+  const int64_t ysz = (int64_t)p.N * p.Co * p.Do * p.Ho * p.Wo;
+  pl.part_bytes = splits > 1 ? (size_t)splits * ysz * 4 : 0;
+  return ATK_OK;
+}
+
+inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+template <typename T, int WCO, int WSP, int FCO, int FSP, int CB>
+int launch_ig_t(const IgPlan& pl, hipStream_t s) {
+  dim3 grid((unsigned)pl.tiles, (unsigned)((pl.a.Co + pl.bn - 1) / pl.bn), (unsigned)pl.splits);
+  hipLaunchKernelGGL((conv_igemm_kernel<T, WCO, WSP, FCO, FSP, CB>), grid, dim3(64 * WCO * WSP), pl.lds, s, pl.a);
+  return check_launch("conv_igemm_kernel");
+}
+
+template <typename T>
+int launch_ig(const ConvShape& p, const void* x, const void* w, const void* bias, void* y, int v,
+              void* ws, size_t ws_bytes, hipStream_t s) {
+  IgPlan pl;
+  int rc = plan_ig(p, v, pl);
+  if (rc) return rc;
+  const size_t need = align256(pl.wp_bytes) + pl.part_bytes;
+  if (!ws || ws_bytes < need) return fail(ATK_EINVAL, "conv: workspace of %zu bytes needed", need);
+  IgArgs& a = pl.a;
+  a.x = x; a.bias = bias; a.y = y;
+  a.wp = ws;
+  a.part = pl.splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + align256(pl.wp_bytes)) : nullptr;
+  // pack the weights
+  const int taps = p.KD * p.KH * p.KW;
+  const int64_t wtotal = (int64_t)pl.wp_bytes / sizeof(T);
+  hipLaunchKernelGGL((pack_weights_kernel<T>), dim3((unsigned)((wtotal + 255) / 256)), dim3(256), 0, s,
+                     static_cast<const T*>(w), static_cast<T*>(ws), p.Co, p.Ci, taps, a.n_kb, a.co_blocks, wtotal);
+  rc = check_launch("pack_weights_kernel");
+  if (rc) return rc;
+  switch (v) {
+    case 0: rc = launch_ig_t<T, 2, 2, 2, 2, 32>(pl, s); break;
+    case 1: rc = launch_ig_t<T, 2, 2, 4, 2, 32>(pl, s); break;
+    case 2: rc = launch_ig_t<T, 2, 2, 2, 4, 32>(pl, s); break;
+    case 3: rc = launch_ig_t<T, 1, 4, 2, 2, 32>(pl, s); break;
+    case 4: rc = launch_ig_t<T, 2, 2, 2, 2, 16>(pl, s); break;
+    case 5: rc = launch_ig_t<T, 2, 2, 2, 2, 16>(pl, s); break;
+    case 6: rc = launch_ig_t<T, 1, 4, 2, 2, 16>(pl, s); break;
+    case 7: rc = launch_ig_t<T, 2, 2, 1, 2, 16>(pl, s); break;
+    default: return fail(ATK_EINVAL, "conv: bad variant");
+  }
+  if (rc || pl.splits == 1) return rc;
+  const int64_t ysz = (int64_t)p.N * p.Co * p.Do * p.Ho * p.Wo;
+  const int64_t spo = (int64_t)p.Do * p.Ho * p.Wo;
+  hipLaunchKernelGGL((splitk_finalize_kernel<T>), dim3((unsigned)((ysz + 255) / 256)), dim3(256), 0, s,
+                     a.part, static_cast<const T*>(bias), static_cast<T*>(y), pl.splits, p.Co, spo, ysz);
+  return check_launch("splitk_finalize_kernel");
+}
+
+}  // namespace
+
+int conv_igemm_num_variants() { return kNumIg; }
+const char* conv_igemm_variant_name(int v) { return (v >= 0 && v < kNumIg) ? kIg[v].name : nullptr; }
+
+size_t conv_igemm_workspace_bytes(const ConvShape& p, int v) {
+  if (v < 0 || v >= kNumIg) return 0;
+  IgPlan pl;
+  if (plan_ig(p, v, pl)) return 0;
+  return align256(pl.wp_bytes) + pl.part_bytes;
+}
+
+int conv_igemm_launch(const ConvShape& p, const void* x, const void* w, const void* bias, void* y, int v,
+                      void* ws, size_t ws_bytes, hipStream_t s) {
+  if (v < 0 || v >= kNumIg) return fail(ATK_EINVAL, "conv: variant out of range");
+  const int64_t ysz = (int64_t)p.N * p.Co * p.Do * p.Ho * p.Wo;
+  if (ysz >= (1ll << 31)) return fail(ATK_UNSUPPORTED, "conv: output too large for the split-K finalize");
+  switch (p.dtype) {
+    case ATK_F32: return launch_ig<float>(p, x, w, bias, y, v, ws, ws_bytes, s);
+    case ATK_F16: return launch_ig<_Float16>(p, x, w, bias, y, v, ws, ws_bytes, s);
+    default: return launch_ig<__bf16>(p, x, w, bias, y, v, ws, ws_bytes, s);
+  }
 }
 
 }  // namespace atk

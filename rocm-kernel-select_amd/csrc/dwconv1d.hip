@@ -48,7 +48,7 @@ struct DwArgs {
   int win_cap;             // LDS window capacity, elements
 };
 
-template <typename T, int KT, int OPT>
+template <typename T, int KT, int OPT, bool NTH>
 __global__ __launch_bounds__(DW_NT) void dwconv1d_lds_kernel(DwArgs a) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int U = OPT / VEC;
@@ -90,7 +90,7 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_lds_kernel(DwArgs a) {
     const int64_t gi = I_base + (int64_t)v * VEC;
     Vec16<T> val;
     if (gi >= 0 && gi + VEC <= a.total_in) {
-      val.raw = *reinterpret_cast<const uint4*>(x + gi);
+      val.raw = ld16<NTH>(x + gi);
     } else {
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
@@ -199,7 +199,7 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_lds_kernel(DwArgs a) {
         if (a.silu) v = silu_f32(v);
         o.e[e] = from_f32<T>(v);
       }
-      *reinterpret_cast<uint4*>(y + f) = o.raw;
+      st16<NTH>(y + f, o.raw);
     } else {
       // row boundary inside the vector, or a partial vector at the tensor ends
 #pragma unroll 1
@@ -256,34 +256,38 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_direct_kernel(DwArgs a) {
 struct DwVariant {
   const char* name;
   int opt;  // outputs per thread; 0 = direct kernel
+  bool nt;  // nontemporal loads/stores
 };
 
 const DwVariant kDwVariants[] = {
-    {"lds_opt16", 16},
-    {"lds_opt8", 8},
-    {"lds_opt32", 32},
-    {"direct", 0},
+    {"lds_opt16", 16, false},
+    {"lds_opt8", 8, false},
+    {"lds_opt32", 32, false},
+    {"direct", 0, false},
+    {"lds_opt16_nt", 16, true},
+    {"lds_opt32_nt", 32, true},
+    {"lds_opt64_nt", 64, true},
 };
 constexpr int kNumDw = sizeof(kDwVariants) / sizeof(kDwVariants[0]);
 
-template <typename T, int KT, int OPT>
+template <typename T, int KT, int OPT, bool NTH>
 int launch_lds_t(const DwArgs& a, size_t shmem, hipStream_t s) {
   constexpr int TO = DW_NT * OPT;
   const int64_t nblk = (a.total_out + a.y_off + TO - 1) / TO;
   if (nblk > 0x7fffffff) return fail(ATK_UNSUPPORTED, "dwconv1d: grid too large");
-  hipLaunchKernelGGL((dwconv1d_lds_kernel<T, KT, OPT>), dim3((unsigned)nblk), dim3(DW_NT),
+  hipLaunchKernelGGL((dwconv1d_lds_kernel<T, KT, OPT, NTH>), dim3((unsigned)nblk), dim3(DW_NT),
                      shmem, s, a);
   return check_launch("dwconv1d_lds_kernel");
 }
 
-template <typename T, int OPT>
+template <typename T, int OPT, bool NTH>
 int launch_lds_k(const DwArgs& a, size_t shmem, hipStream_t s) {
   switch (a.K) {
-    case 2: return launch_lds_t<T, 2, OPT>(a, shmem, s);
-    case 3: return launch_lds_t<T, 3, OPT>(a, shmem, s);
-    case 4: return launch_lds_t<T, 4, OPT>(a, shmem, s);
-    case 5: return launch_lds_t<T, 5, OPT>(a, shmem, s);
-    default: return launch_lds_t<T, 0, OPT>(a, shmem, s);
+    case 2: return launch_lds_t<T, 2, OPT, NTH>(a, shmem, s);
+    case 3: return launch_lds_t<T, 3, OPT, NTH>(a, shmem, s);
+    case 4: return launch_lds_t<T, 4, OPT, NTH>(a, shmem, s);
+    case 5: return launch_lds_t<T, 5, OPT, NTH>(a, shmem, s);
+    default: return launch_lds_t<T, 0, OPT, NTH>(a, shmem, s);
   }
 }
 
@@ -307,10 +311,18 @@ int launch_dw(DwArgs a, int variant, hipStream_t s) {
   const size_t shmem = (size_t)need * sizeof(T) + (size_t)DW_MAXR * (a.K + 1) * sizeof(float);
   if (shmem > 64 * 1024) return fail(ATK_UNSUPPORTED, "dwconv1d: LDS window too large for variant");
   a.win_cap = (int)need;
+  if (kDwVariants[variant].nt) {
+    switch (opt) {
+      case 16: return launch_lds_k<T, 16, true>(a, shmem, s);
+      case 32: return launch_lds_k<T, 32, true>(a, shmem, s);
+      case 64: return launch_lds_k<T, 64, true>(a, shmem, s);
+      default: return fail(ATK_UNSUPPORTED, "dwconv1d: bad variant");
+    }
+  }
   switch (opt) {
-    case 8: return launch_lds_k<T, 8>(a, shmem, s);
-    case 16: return launch_lds_k<T, 16>(a, shmem, s);
-    case 32: return launch_lds_k<T, 32>(a, shmem, s);
+    case 8: return launch_lds_k<T, 8, false>(a, shmem, s);
+    case 16: return launch_lds_k<T, 16, false>(a, shmem, s);
+    case 32: return launch_lds_k<T, 32, false>(a, shmem, s);
     default: return fail(ATK_UNSUPPORTED, "dwconv1d: bad variant");
   }
 }

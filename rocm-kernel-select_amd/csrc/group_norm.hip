@@ -27,8 +27,16 @@ namespace atk {
 
 namespace {
 
-constexpr uint32_t GN_SPIN_LIMIT = 1u << 24;  // ~0.5 s of s_sleep(1): never reached when co-resident
+constexpr uint32_t GN_SPIN_LIMIT = 1u << 20;  // polls (s_sleep(2) apart): never reached when co-resident
 constexpr int GN_MAX_NS = 4096;
+// Workspace layout is FIXED so that calls of different shapes sharing one workspace can
+// never write partials over another shape's barrier counters:
+//   [0, 256)                      error flag
+//   [256, 256 + 8*GN_MAX_COOP)    (arrivals, generation) per group, cooperative variants
+//   [GN_PARTIALS_OFF, ...)        per-slice (mean, M2) partials
+constexpr int GN_MAX_COOP = 4096;             // groups a cooperative launch may span
+constexpr size_t GN_ZERO_BYTES = 256 + 8 * (size_t)GN_MAX_COOP;
+constexpr size_t GN_PARTIALS_OFF = GN_ZERO_BYTES;
 constexpr int GN_TP_NT = 256;                 // two-pass kernels
 constexpr int GN_MAX_AFF = 512;               // channels per slice whose affine is staged in LDS
 
@@ -65,13 +73,14 @@ __device__ void group_barrier(uint32_t* cnt, uint32_t* gen, int NS, uint32_t* er
     __hip_atomic_fetch_add(gen, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
   } else {
     uint32_t it = 0;
-    while (__hip_atomic_load(gen, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == g0) {
-      __builtin_amdgcn_s_sleep(1);
+    while (__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == g0) {
+      __builtin_amdgcn_s_sleep(2);
       if (++it > GN_SPIN_LIMIT) {
         __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
       }
     }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
 }
 
@@ -139,7 +148,7 @@ __global__ __launch_bounds__(NT) void gn_resident_kernel(GnArgs a) {
 #pragma unroll
   for (int i = 0; i < EPV; ++i) {
     const int64_t e = s0 + ((int64_t)i * NT + tid) * VEC;
-    if (e < E) buf[i].raw = *reinterpret_cast<const uint4*>(xg + e);
+    if (e < E) buf[i].raw = ld16<true>(xg + e);
     else buf[i].raw = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
     for (int k = 0; k < VEC; ++k) sum += to_f32(buf[i].e[k]);  // padding lanes hold +0
@@ -210,7 +219,7 @@ __global__ __launch_bounds__(NT) void gn_resident_kernel(GnArgs a) {
       } else {
         channel_affine(a, cabs0 + cl, mean, rstd, sc, sh);
       }
-      *reinterpret_cast<uint4*>(yg + e) = normalize_vec<T>(buf[i], sc, sh, a.silu);
+      st16<true>(yg + e, normalize_vec<T>(buf[i], sc, sh, a.silu));
     }
   }
 }
@@ -303,7 +312,7 @@ __global__ __launch_bounds__(GN_TP_NT) void gn_apply_kernel(GnArgs a) {
     if (VECOK) {
       Vec16<T> b;
       b.raw = *reinterpret_cast<const uint4*>(xg + e);
-      *reinterpret_cast<uint4*>(yg + e) = normalize_vec<T>(b, sc, sh, a.silu);
+      st16<true>(yg + e, normalize_vec<T>(b, sc, sh, a.silu));
     } else {
       float v = fmaf(to_f32(xg[e]), sc, sh);
       if (a.silu) v = silu_f32(v);
@@ -337,7 +346,7 @@ struct GnPlan {
 
 inline size_t round256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// Slicing and workspace layout: [err (256 B)][counters 8 B/group][partials 8 B/slice]
+// Slicing and workspace size (layout: see GN_ZERO_BYTES / GN_PARTIALS_OFF)
 bool plan_gn(int64_t N, int64_t C, int64_t S, int G, int dtype, int variant, GnPlan& p) {
   const int64_t cpg = C / G;
   const int64_t E = cpg * S;
@@ -360,8 +369,8 @@ bool plan_gn(int64_t N, int64_t C, int64_t S, int G, int dtype, int variant, GnP
     p.NS = (int)((E + sl - 1) / sl);
   }
   if (p.NS > GN_MAX_NS) return false;
-  p.zero_bytes = 256 + round256((size_t)ngroups * 8);
-  p.ws_bytes = p.zero_bytes + round256((size_t)ngroups * p.NS * 8);
+  p.zero_bytes = GN_ZERO_BYTES;
+  p.ws_bytes = GN_PARTIALS_OFF + round256((size_t)ngroups * p.NS * 8);
   return true;
 }
 
@@ -374,6 +383,9 @@ int launch_resident(GnArgs a, int64_t ngroups, hipStream_t s) {
     hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(NT), 0, s, a);
     return check_launch("gn_resident_kernel");
   }
+  if (ngroups > GN_MAX_COOP)
+    return fail(ATK_UNSUPPORTED, "group_norm: %lld groups exceed the cooperative barrier table",
+                (long long)ngroups);
   int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kern), NT, 0) != hipSuccess)
     return fail(ATK_ELAUNCH, "group_norm: occupancy query failed");
@@ -498,7 +510,7 @@ extern "C" int atk_group_norm_fwd(const void* x, const void* gamma, const void* 
   char* ws = static_cast<char*>(workspace);
   a.err = reinterpret_cast<uint32_t*>(ws);
   a.counters = reinterpret_cast<uint32_t*>(ws + 256);
-  a.partials = reinterpret_cast<float*>(ws + p.zero_bytes);
+  a.partials = reinterpret_cast<float*>(ws + GN_PARTIALS_OFF);
   const int64_t ngroups = N * G;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (dtype) {

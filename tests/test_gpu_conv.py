@@ -107,3 +107,48 @@ def test_conv_no_bias(dev):
             continue
         torch.cuda.synchronize()
         assert O.max_rel_err(y.cpu(), ref) <= 1e-5, name
+
+
+CONFIGS = [
+    # BASELINE configs 4 and 5: (xshape, wshape, padding, dtype)
+    ((1, 64, 16, 32, 32), (64, 64, 3, 3, 3), 1, torch.float16),
+    ((1, 64, 16, 32, 32), (64, 64, 3, 3, 3), 1, torch.float32),
+    ((2, 128, 16, 64, 64), (128, 128, 3, 3, 3), 1, torch.bfloat16),
+    ((1, 256, 8, 64, 64), (256, 256, 3, 3, 3), 1, torch.bfloat16),
+    ((1, 64, 16, 32, 32), (64, 64, 7, 7, 7), 3, torch.float16),
+]
+
+
+@pytest.mark.parametrize("cfg", CONFIGS, ids=["c4_small_fp16", "c4_small_fp32", "c4_scaled_bf16",
+                                               "c5_bf16", "c5_k7_fp16"])
+def test_conv3d_config_full_size(dev, cfg):
+    """Every MFMA variant at the BASELINE shapes: 4096 sampled outputs against the float64
+    oracle, and every output against stock F.conv3d in fp32 on the same inputs."""
+    xs, ws, pad, dtype = cfg
+    nat = _native()
+    x, w, b = _inputs(xs, ws, dtype, seed=1004)
+    g = torch.Generator().manual_seed(7)
+    oshape = O.conv_out_shape(xs, ws, 1, pad, 1)
+    pts = torch.randint(0, math.prod(oshape), (4096,), generator=g).numpy()
+    ref_pts = O.conv3d(x, w, b, 1, pad, 1, points=pts)
+    xd, wd, bd = x.to(dev), w.to(dev), b.to(dev)
+    stock = torch.nn.functional.conv3d  # the package may be imported: use aten directly
+    ref_full = torch.ops.aten.convolution(xd.float(), wd.float(), bd.float(), [1, 1, 1], [pad] * 3,
+                                          [1, 1, 1], False, [0, 0, 0], 1)
+    ran = 0
+    for vi, name in _variants_for(dtype):
+        if name == "direct":
+            continue
+        try:
+            y = nat.conv3d(xd, wd, bd, 1, pad, 1, variant=vi)
+        except nat.Unsupported:
+            continue
+        torch.cuda.synchronize()
+        yp = y.flatten()[torch.from_numpy(pts).to(dev)].cpu()
+        e1 = float(np.max(np.abs(O.f64(yp) - ref_pts)) / np.max(np.abs(ref_pts)))
+        e2 = O.max_rel_err(y.float(), ref_full)
+        assert e1 <= BAR[dtype], f"{name}: sampled max_rel_err {e1:.3g}"
+        assert e2 <= max(BAR[dtype], 2e-5 if dtype == torch.float32 else 0), f"{name}: vs stock {e2:.3g}"
+        ran += 1
+    del stock
+    assert ran >= 1

@@ -149,3 +149,25 @@ def test_group_norm_config_full_size(dev, cfg, dtype):
             err = O.max_rel_err(y.cpu(), ref)
             assert err <= 1e-2, f"{name} silu={silu}: {err:.3g}"
     assert not nat.group_norm_barrier_error(dev)
+
+
+def test_group_norm_workspace_shared_across_shapes(dev):
+    """Regression: a shape with few groups and many slices writes many partials into the
+    shared workspace; a following cooperative call on a shape with many groups must still
+    find its barrier counters at zero (they live in a fixed region the partials never
+    reach)."""
+    nat = _native()
+    names = nat.variants(nat.OP_GROUP_NORM)
+    xa, ga, ba = _inputs((8, 256, 64, 64), torch.float16, seed=21)    # 256 groups of 32768
+    xb, gb, bb = _inputs((1, 64, 64, 64, 16), torch.float16, seed=22)  # 32 groups of 131072
+    ref_a = O.group_norm(xa, 32, ga, ba, 1e-5)
+    ref_b = O.group_norm(xb, 32, gb, bb, 1e-5)
+    xa, ga, ba, xb, gb, bb = (t.to(dev) for t in (xa, ga, ba, xb, gb, bb))
+    for _ in range(2):
+        for name in ("res_nt256_v8", "twopass", "res_nt256_v16"):
+            yb = nat.group_norm(xb, 32, gb, bb, 1e-5, variant=names.index(name))
+            ya = nat.group_norm(xa, 32, ga, ba, 1e-5, variant=names.index("res_nt256_v8"))
+            torch.cuda.synchronize()
+            assert O.max_rel_err(yb.cpu(), ref_b) <= 1e-2
+            assert O.max_rel_err(ya.cpu(), ref_a) <= 1e-2
+    assert not nat.group_norm_barrier_error(dev)
