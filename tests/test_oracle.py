@@ -1,0 +1,219 @@
+"""Pins the float64 CPU oracle (oracle/atk_oracle.c) before it is trusted as the GPU
+parity checker: the committed golden fixtures (stock torch float64), the reference's
+depthwise output-length known answers, stock torch on random shapes, brute-force Python
+loops, and identities a plausible mistake (dropped term, wrong sign, off-by-one index,
+transposed operand) would break."""
+from __future__ import annotations
+
+import itertools
+import math
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "golden.npz")
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return np.load(GOLDEN, allow_pickle=False)
+
+
+# ---------------------------------------------------------------------------
+# golden fixtures
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("name", ["dw_sym", "dw_causal", "dw_valid", "dw_widepad"])
+def test_dwconv1d_matches_golden(golden, name):
+    N, C, L, K, p = golden[f"{name}_meta"].tolist()
+    y = O.dwconv1d(golden[f"{name}_x"], golden[f"{name}_w"], golden[f"{name}_b"], p,
+                   L + 2 * p - K + 1)
+    np.testing.assert_allclose(y, golden[f"{name}_y"], rtol=0, atol=1e-12)
+
+
+def test_group_norm_matches_golden(golden):
+    y = O.group_norm(golden["gn_x"], 3, golden["gn_g"], golden["gn_b"], 1e-5)
+    np.testing.assert_allclose(y, golden["gn_y"], rtol=0, atol=1e-12)
+    y = O.group_norm(golden["gn_x"], 3, golden["gn_g"], golden["gn_b"], 1e-5, silu=True)
+    np.testing.assert_allclose(y, golden["gn_silu_y"], rtol=0, atol=1e-12)
+    y = O.group_norm(golden["gn3_x"], 2, None, None, 1e-6)
+    np.testing.assert_allclose(y, golden["gn3_y"], rtol=0, atol=1e-12)
+
+
+def test_conv_matches_golden(golden):
+    y = O.conv2d(golden["c2_x"], golden["c2_w"], golden["c2_b"], (2, 1), (1, 2), (1, 2))
+    np.testing.assert_allclose(y, golden["c2_y"], rtol=0, atol=1e-12)
+    y = O.conv3d(golden["c3_x"], golden["c3_w"], golden["c3_b"], (1, 2, 1), 1, 1)
+    np.testing.assert_allclose(y, golden["c3_y"], rtol=0, atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# known answers of the reference's own tests
+# ---------------------------------------------------------------------------
+def test_out_len_known_answers():
+    """tests/test_depthwise_conv1d_ops.py:64-71 of the reference."""
+    assert O.conv1d_out_len(10, 1, 3) == 10
+    assert O.conv1d_out_len(10, 0, 3) == 8
+    assert O.conv1d_out_len(100, 5, 11) == 100
+    x = np.zeros((1, 1, 100))
+    assert O.dwconv1d(x, np.ones((1, 11)), None, 5, O.conv1d_out_len(100, 5, 11)).shape == (1, 1, 100)
+
+
+# ---------------------------------------------------------------------------
+# brute force (pure Python loops) on tiny shapes
+# ---------------------------------------------------------------------------
+def _bf_dw(x, w, b, pad, l_out):
+    N, C, L = x.shape
+    K = w.shape[-1]
+    y = np.zeros((N, C, l_out))
+    for n, c, t in itertools.product(range(N), range(C), range(l_out)):
+        s = b[c] if b is not None else 0.0
+        for j in range(K):
+            p = t - pad + j
+            if 0 <= p < L:
+                s += w[c, j] * x[n, c, p]
+        y[n, c, t] = s
+    return y
+
+
+def test_dwconv1d_brute_force():
+    rng = np.random.default_rng(0)
+    for (N, C, L, K, pad, l_out) in [(1, 2, 7, 3, 1, 7), (2, 1, 5, 4, 3, 8), (1, 2, 6, 4, 3, 6),
+                                     (1, 1, 4, 2, 5, 10)]:
+        x, w, b = rng.normal(size=(N, C, L)), rng.normal(size=(C, K)), rng.normal(size=C)
+        np.testing.assert_allclose(O.dwconv1d(x, w, b, pad, l_out), _bf_dw(x, w, b, pad, l_out),
+                                   rtol=0, atol=1e-12)
+
+
+def _bf_conv3d(x, w, b, s, p, d):
+    N, Ci, D, H, W = x.shape
+    Co, _, KD, KH, KW = w.shape
+    Do, Ho, Wo = ((D + 2 * p[0] - d[0] * (KD - 1) - 1) // s[0] + 1,
+                  (H + 2 * p[1] - d[1] * (KH - 1) - 1) // s[1] + 1,
+                  (W + 2 * p[2] - d[2] * (KW - 1) - 1) // s[2] + 1)
+    y = np.zeros((N, Co, Do, Ho, Wo))
+    for n, o, z, h, v in itertools.product(range(N), range(Co), range(Do), range(Ho), range(Wo)):
+        acc = b[o]
+        for i, a, bb, c in itertools.product(range(Ci), range(KD), range(KH), range(KW)):
+            iz, iy, ix = z * s[0] - p[0] + a * d[0], h * s[1] - p[1] + bb * d[1], v * s[2] - p[2] + c * d[2]
+            if 0 <= iz < D and 0 <= iy < H and 0 <= ix < W:
+                acc += w[o, i, a, bb, c] * x[n, i, iz, iy, ix]
+        y[n, o, z, h, v] = acc
+    return y
+
+
+def test_conv3d_brute_force():
+    rng = np.random.default_rng(1)
+    x, w, b = rng.normal(size=(1, 2, 3, 4, 5)), rng.normal(size=(2, 2, 2, 3, 2)), rng.normal(size=2)
+    for s, p, d in [((1, 1, 1), (1, 1, 1), (1, 1, 1)), ((2, 1, 2), (0, 2, 1), (1, 1, 2))]:
+        np.testing.assert_allclose(O.conv3d(x, w, b, s, p, d), _bf_conv3d(x, w, b, s, p, d),
+                                   rtol=0, atol=1e-12)
+
+
+def test_conv3d_points_subset_matches_full():
+    rng = np.random.default_rng(2)
+    x, w, b = rng.normal(size=(2, 3, 4, 5, 6)), rng.normal(size=(4, 3, 3, 3, 3)), rng.normal(size=4)
+    full = O.conv3d(x, w, b, 1, 1, 1)
+    pts = rng.integers(0, full.size, size=50)
+    np.testing.assert_allclose(O.conv3d(x, w, b, 1, 1, 1, points=pts), full.ravel()[pts], atol=1e-12)
+
+
+def _bf_gn(x, G, gm, bt, eps):
+    N, C = x.shape[:2]
+    y = np.empty_like(x)
+    cpg = C // G
+    for n in range(N):
+        for g in range(G):
+            blk = x[n, g * cpg:(g + 1) * cpg]
+            mu = sum(blk.ravel()) / blk.size
+            var = sum((v - mu) ** 2 for v in blk.ravel()) / blk.size
+            for c in range(g * cpg, (g + 1) * cpg):
+                y[n, c] = (x[n, c] - mu) / math.sqrt(var + eps) * gm[c] + bt[c]
+    return y
+
+
+def test_group_norm_brute_force():
+    rng = np.random.default_rng(3)
+    x, gm, bt = rng.normal(size=(2, 4, 3)), rng.normal(size=4), rng.normal(size=4)
+    np.testing.assert_allclose(O.group_norm(x, 2, gm, bt, 1e-5), _bf_gn(x, 2, gm, bt, 1e-5),
+                               rtol=0, atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# stock torch (float64) on random shapes
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("seed", range(4))
+def test_oracle_vs_stock_random(seed):
+    g = torch.Generator().manual_seed(seed)
+    d = torch.float64
+    N, C, L = 2, 5, 23 + seed
+    K = 1 + seed * 2
+    x, w, b = torch.randn(N, C, L, generator=g, dtype=d), torch.randn(C, 1, K, generator=g, dtype=d), torch.randn(C, generator=g, dtype=d)
+    for p in (0, (K - 1) // 2, K - 1):
+        ref = F.conv1d(x, w, b, padding=p, groups=C).numpy()
+        np.testing.assert_allclose(O.dwconv1d(x, w, b, p, ref.shape[-1]), ref, atol=1e-12)
+    xs = torch.randn(3, 8, 5, 3, generator=g, dtype=d) * 3 + 7
+    gm, bt = torch.randn(8, generator=g, dtype=d), torch.randn(8, generator=g, dtype=d)
+    for G in (1, 2, 8):
+        np.testing.assert_allclose(O.group_norm(xs, G, gm, bt, 1e-5),
+                                   F.group_norm(xs, G, gm, bt, 1e-5).numpy(), atol=1e-11)
+    xc, wc, bc = torch.randn(1, 3, 5, 6, 7, generator=g, dtype=d), torch.randn(4, 3, 3, 3, 3, generator=g, dtype=d), torch.randn(4, generator=g, dtype=d)
+    np.testing.assert_allclose(O.conv3d(xc, wc, bc, (1, 1, 2), (1, 0, 1), (1, 2, 1)),
+                               F.conv3d(xc, wc, bc, (1, 1, 2), (1, 0, 1), (1, 2, 1)).numpy(), atol=1e-11)
+
+
+# ---------------------------------------------------------------------------
+# identities
+# ---------------------------------------------------------------------------
+def test_delta_kernels_shift_the_input():
+    """A one-hot depthwise kernel at tap j shifts every row by j - pad (zero filled);
+    a one-hot conv3d kernel at the centre tap with pad 1 is the identity on its channel."""
+    rng = np.random.default_rng(4)
+    x = rng.normal(size=(1, 2, 9))
+    for j in range(4):
+        w = np.zeros((2, 4))
+        w[:, j] = 1.0
+        y = O.dwconv1d(x, w, None, 3, 12)
+        for t in range(12):
+            p = t - 3 + j
+            np.testing.assert_allclose(y[..., t], x[..., p] if 0 <= p < 9 else 0.0, atol=0)
+    xc = rng.normal(size=(1, 3, 4, 5, 6))
+    w = np.zeros((3, 3, 3, 3, 3))
+    for c in range(3):
+        w[c, c, 1, 1, 1] = 1.0
+    np.testing.assert_allclose(O.conv3d(xc, w, None, 1, 1, 1), xc, atol=0)
+
+
+def test_linearity():
+    rng = np.random.default_rng(5)
+    x1, x2 = rng.normal(size=(1, 2, 3, 4, 5)), rng.normal(size=(1, 2, 3, 4, 5))
+    w = rng.normal(size=(3, 2, 3, 3, 3))
+    np.testing.assert_allclose(O.conv3d(2 * x1 - 3 * x2, w, None, 1, 1, 1),
+                               2 * O.conv3d(x1, w, None, 1, 1, 1) - 3 * O.conv3d(x2, w, None, 1, 1, 1),
+                               atol=1e-10)
+
+
+def test_group_norm_invariants():
+    """Without affine: each group has mean 0 and variance var/(var+eps); the output is
+    invariant to a per-group shift and positive scale (up to the eps term)."""
+    rng = np.random.default_rng(6)
+    x = rng.normal(size=(2, 6, 7)) * 5 + 3
+    y, mean, rstd = O.group_norm(x, 3, None, None, 0.0, return_stats=True)
+    grp = y.reshape(2, 3, -1)
+    np.testing.assert_allclose(grp.mean(-1), 0, atol=1e-12)
+    np.testing.assert_allclose(grp.var(-1), 1, atol=1e-12)
+    x2 = x.reshape(2, 3, -1) * np.array([1.5, 0.25, 4.0])[None, :, None] + 11.0
+    np.testing.assert_allclose(O.group_norm(x2.reshape(x.shape), 3, None, None, 0.0), y, atol=1e-10)
+    silu = O.group_norm(x, 3, None, None, 1e-5, silu=True)
+    plain = O.group_norm(x, 3, None, None, 1e-5)
+    np.testing.assert_allclose(silu, plain / (1 + np.exp(-plain)), atol=1e-14)
+
+
+def test_max_rel_err_metric():
+    """max|y - ref| / max|ref| (tools/bench_fast.py:147-162 of the reference)."""
+    assert O.max_rel_err(np.array([1.0, 2.0, 4.5]), np.array([1.0, 2.0, 4.0])) == pytest.approx(0.125)
+    assert O.max_rel_err(np.zeros(3), np.zeros(3)) == 0.0
