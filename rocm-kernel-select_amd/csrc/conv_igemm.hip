@@ -42,6 +42,12 @@ struct IgArgs {
   int N, Ci, D, H, W, Co, KD, KH, KW, sd, sh, sw, pd, ph, pw, dd, dh, dw, Do, Ho, Wo;
   int TX, TY, tiles_x, tiles_y;
   int PX, PY;
+  int NCX;            // 16-byte chunks per patch row (aligned-down start)
+  int PXS;            // patch row stride in positions = NCX * VEC
+  int vec_rows;       // input rows are 16-byte aligned (W % VEC == 0, aligned base)
+  int patch_elems;    // elements of one patch buffer (two are allocated)
+  uint32_t x_sample_bytes;  // bytes of one input sample (buffer range of the patch loads)
+  uint32_t wp_bytes;        // bytes of the packed weights
   int n_stages;       // n_cc * KD
   int stages_per_split;
   int n_kb;           // ci k-blocks in the packed weights = n_cc * CB / KB
@@ -70,15 +76,99 @@ __device__ __forceinline__ void mfma_block(f32x16& acc, const uint4& a, const ui
   acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.w), __uint_as_float(b.w), acc, 0, 0, 0);
 }
 
-template <typename T, int WCO, int WSP, int FCO, int FSP, int CB>
+// Raw buffer access (gfx9 buffer resource, stride 0): a 32-bit lane offset plus a uniform
+// SGPR offset, and offsets at or beyond `bytes` read as zero -- used both to keep address
+// arithmetic off the VALU and to zero-fill masked loads without branches.
+constexpr uint32_t kOOB = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+template <typename T>
+__device__ __forceinline__ T bload_elem(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  if constexpr (sizeof(T) == 2) {
+    const unsigned short u = __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, 0, 0);
+    return __builtin_bit_cast(T, u);
+  } else {
+    const unsigned int u = __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, 0, 0);
+    return __builtin_bit_cast(T, u);
+  }
+}
+
+// Patch staging.  The patch of a stage is CB channels x PY input rows x NCX 16-byte chunks,
+// stored channels-last as patch[(py * PXS + px') * CBS + cl] with PXS = NCX * VEC: position
+// px' = chunk * VEC + e holds input column gx0 + px', gx0 being the tile's first needed
+// column (ix0) rounded down to a 16-byte boundary, so every chunk is written whole with no
+// per-element bounds test; readers add mis = ix0 - gx0.  Chunk c maps to (row-chunk
+// rc = c / CB, channel cl = c % CB): consecutive lanes write consecutive channels of one
+// patch position.
+template <typename T, int CB, bool VR>
+struct PatchLoader {
+  static constexpr int VEC = 16 / sizeof(T);
+  static constexpr int MAXC = 8;  // chunks per thread held for the next stage
+  uint4 buf[MAXC];
+
+  // rsrc covers sample n of the input; iz may be out of range (a padding plane)
+  __device__ __forceinline__ void load(const IgArgs& a, __amdgpu_buffer_rsrc_t rx, int cc, int iz, int iy0,
+                                       int gx0, int total, int tid, int nt) {
+    const bool zin = (unsigned)iz < (unsigned)a.D;
+#pragma unroll
+    for (int u = 0; u < MAXC; ++u) {
+      const int c = tid + u * nt;
+      const int cl = c % CB, rc = c / CB;
+      const int py = rc / a.NCX, cx = rc - (rc / a.NCX) * a.NCX;
+      const int ci = cc * CB + cl, iy = iy0 + py, gx = gx0 + cx * VEC;
+      const bool rowok = c < total && zin && ci < a.Ci && (unsigned)iy < (unsigned)a.H;
+      const uint32_t row = (uint32_t)((((uint32_t)ci * a.D + iz) * a.H + iy) * a.W);
+      if (VR) {
+        const bool ok = rowok && gx >= 0 && gx + VEC <= a.W;  // chunks are all-in or all-out
+        buf[u] = bload16(rx, ok ? (row + gx) * (uint32_t)sizeof(T) : kOOB, 0);
+      } else {
+        Vec16<T> v;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const int ix = gx + e;
+          const bool ok = rowok && (unsigned)ix < (unsigned)a.W;
+          v.e[e] = bload_elem<T>(rx, ok ? (row + ix) * (uint32_t)sizeof(T) : kOOB);
+        }
+        buf[u] = v.raw;
+      }
+    }
+  }
+
+  __device__ __forceinline__ void store(const IgArgs& a, T* patch, int total, int tid, int nt) const {
+    constexpr int CBS = CB + VEC;
+#pragma unroll
+    for (int u = 0; u < MAXC; ++u) {
+      const int c = tid + u * nt;
+      if (c >= total) break;
+      const int cl = c % CB, rc = c / CB;
+      const int py = rc / a.NCX, cx = rc - (rc / a.NCX) * a.NCX;
+      Vec16<T> v;
+      v.raw = buf[u];
+      T* dst = patch + (py * a.PXS + cx * VEC) * CBS + cl;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) dst[e * CBS] = v.e[e];
+    }
+  }
+};
+
+template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, bool VR>
 __global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm_kernel(IgArgs a) {
   constexpr int NT = 64 * WCO * WSP;
   constexpr int KB = MfmaTraits<T>::KB, VEC = MfmaTraits<T>::VEC;
+  constexpr int ES = sizeof(T);
   constexpr int CBS = CB + VEC;           // padded channel stride of a patch position
   constexpr int BN = WCO * FCO * 32;      // output channels per workgroup
+  constexpr int NKB = CB / KB;            // k-blocks per tap
+  constexpr uint32_t FRAG = 32 * KB * ES; // bytes of one packed weight fragment
   static_assert(CB % KB == 0, "chunk must hold whole k-blocks");
   extern __shared__ uint4 lds_raw[];
-  T* patch = reinterpret_cast<T*>(lds_raw);
+  char* lds_bytes = reinterpret_cast<char*>(lds_raw);
 
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int wco = wv % WCO, wsp = wv / WCO;
@@ -96,15 +186,26 @@ __global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm_kernel(IgArgs a) {
   const int s_end = min(a.n_stages, s_begin + a.stages_per_split);
   const int oy0 = ty_t * a.TY, ox0 = tx_t * a.TX;
   const int iy0 = oy0 * a.sh - a.ph, ix0 = ox0 * a.sw - a.pw;
+  const int gx0 = (ix0 >= 0 ? ix0 / VEC : -((-ix0 + VEC - 1) / VEC)) * VEC;  // aligned-down start
+  const int mis = ix0 - gx0;
+  const int total_chunks = CB * a.PY * a.NCX;
 
-  // per-lane patch base position of each im2col column this lane feeds
-  int pos0[FSP];
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(
+      static_cast<const T*>(a.x) + (int64_t)n * a.Ci * a.D * a.H * a.W, a.x_sample_bytes);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.wp, a.wp_bytes);
+
+  // byte offset of this lane's first im2col element of column block j in a patch buffer
+  uint32_t pb[FSP];
 #pragma unroll
   for (int j = 0; j < FSP; ++j) {
     const int m = (wsp * FSP + j) * 32 + col;
     const int ty = m / a.TX, tx = m - (m / a.TX) * a.TX;
-    pos0[j] = (ty * a.sh) * a.PX + tx * a.sw;
+    pb[j] = (uint32_t)(((ty * a.sh) * a.PXS + tx * a.sw + mis) * CBS + half * VEC) * ES;
   }
+  const uint32_t wlane = (uint32_t)(col * KB + half * VEC) * ES;
+  const uint32_t patch_bytes = (uint32_t)a.patch_elems * ES;
+  const uint32_t kh_step = (uint32_t)(a.dh * a.PXS * CBS) * ES;  // patch bytes per kernel row
+  const uint32_t kw_step = (uint32_t)(a.dw * CBS) * ES;          // patch bytes per kernel column
 
   f32x16 acc[FCO][FSP];
 #pragma unroll
@@ -114,59 +215,78 @@ __global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm_kernel(IgArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  const T* __restrict__ x = static_cast<const T*>(a.x);
-  const T* __restrict__ wp = static_cast<const T*>(a.wp);
-  const int64_t plane = (int64_t)a.H * a.W;
-  const int npatch = a.PY * a.PX;
-  const int taps = a.KD * a.KH * a.KW;
+  const int ntaps2d = a.KH * a.KW;
   const int co_blk0 = co_tile * (BN / 32) + wco * FCO;
-  // element offset of this lane inside a 32 x KB weight fragment
-  const int wlane = col * KB + half * VEC;
+
+  PatchLoader<T, CB, VR> ld;
+  if (s_begin < s_end) {
+    const int cc = s_begin / a.KD, kd = s_begin - (s_begin / a.KD) * a.KD;
+    ld.load(a, rx, cc, oz * a.sd - a.pd + kd * a.dd, iy0, gx0, total_chunks, tid, NT);
+    ld.store(a, reinterpret_cast<T*>(lds_bytes), total_chunks, tid, NT);
+  }
+  __syncthreads();
 
   for (int s = s_begin; s < s_end; ++s) {
     const int cc = s / a.KD, kd = s - (s / a.KD) * a.KD;
     const int iz = oz * a.sd - a.pd + kd * a.dd;
-    const bool zin = (unsigned)iz < (unsigned)a.D;
-    // ---- stage the input patch (channels-last) -----------------------------------------
-    __syncthreads();  // previous stage's readers are done with the patch
-    for (int idx = tid; idx < CB * npatch; idx += NT) {
-      const int cl = idx / npatch;
-      const int rem = idx - cl * npatch;
-      const int py = rem / a.PX, px = rem - (rem / a.PX) * a.PX;
-      const int ci = cc * CB + cl;
-      const int iy = iy0 + py, ix = ix0 + px;
-      T v = static_cast<T>(0.0f);
-      if (zin && ci < a.Ci && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W)
-        v = x[((int64_t)n * a.Ci + ci) * a.D * plane + (int64_t)iz * plane + (int64_t)iy * a.W + ix];
-      patch[rem * CBS + cl] = v;
+    const uint32_t pbuf = ((s - s_begin) & 1) ? patch_bytes : 0u;
+    // prefetch the next stage's patch into registers while this stage computes
+    const bool has_next = s + 1 < s_end;
+    if (has_next) {
+      const int cc1 = (s + 1) / a.KD, kd1 = (s + 1) - ((s + 1) / a.KD) * a.KD;
+      ld.load(a, rx, cc1, oz * a.sd - a.pd + kd1 * a.dd, iy0, gx0, total_chunks, tid, NT);
     }
-    __syncthreads();
-    if (!zin) continue;  // a padding plane contributes nothing
-    // ---- taps of this stage ---------------------------------------------------------------
-    for (int kh = 0; kh < a.KH; ++kh) {
-      for (int kw = 0; kw < a.KW; ++kw) {
-        const int tap = (kd * a.KH + kh) * a.KW + kw;
-        const int toff = (kh * a.dh) * a.PX + kw * a.dw;
+    if ((unsigned)iz < (unsigned)a.D) {
+      // uniform byte offset of fragment (tap, kb of this chunk, co_blk0) in the packed weights
+      const uint32_t tap_bytes = (uint32_t)a.n_kb * a.co_blocks * FRAG;
+      const uint32_t kb_bytes = (uint32_t)a.co_blocks * FRAG;
+      uint32_t wsoff = (uint32_t)(kd * ntaps2d) * tap_bytes + (uint32_t)(cc * NKB) * kb_bytes + co_blk0 * FRAG;
+      uint4 wA[NKB][FCO], wB[NKB][FCO];
+      auto load_w = [&](uint4 (&w)[NKB][FCO], uint32_t so) {
 #pragma unroll
-        for (int kb = 0; kb < CB / KB; ++kb) {
-          const int kbg = cc * (CB / KB) + kb;
-          uint4 wf[FCO], pf[FSP];
+        for (int kb = 0; kb < NKB; ++kb)
 #pragma unroll
-          for (int i = 0; i < FCO; ++i) {
-            const int64_t frag = ((int64_t)tap * a.n_kb + kbg) * a.co_blocks + co_blk0 + i;
-            wf[i] = *reinterpret_cast<const uint4*>(wp + frag * (32 * KB) + wlane);
-          }
+          for (int i = 0; i < FCO; ++i) w[kb][i] = bload16(rw, wlane, so + kb * kb_bytes + i * FRAG);
+      };
+      auto compute = [&](const uint4 (&w)[NKB][FCO], uint32_t toffb) {
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+          uint4 pf[FSP];
 #pragma unroll
           for (int j = 0; j < FSP; ++j)
-            pf[j] = *reinterpret_cast<const uint4*>(patch + (pos0[j] + toff) * CBS + kb * KB + half * VEC);
+            pf[j] = *reinterpret_cast<const uint4*>(lds_bytes + pbuf + pb[j] + toffb + kb * KB * ES);
 #pragma unroll
           for (int i = 0; i < FCO; ++i)
 #pragma unroll
-            for (int j = 0; j < FSP; ++j) mfma_block(acc[i][j], wf[i], pf[j], static_cast<T*>(nullptr));
+            for (int j = 0; j < FSP; ++j) mfma_block(acc[i][j], w[kb][i], pf[j], static_cast<T*>(nullptr));
+        }
+      };
+      load_w(wA, wsoff);
+      int kh = 0, kw = 0;
+      uint32_t toffb = 0;
+      auto next_tap = [&]() {
+        if (++kw == a.KW) {
+          kw = 0;
+          ++kh;
+          toffb = kh * kh_step;
+        } else {
+          toffb += kw_step;
+        }
+      };
+      for (int t2 = 0; t2 < ntaps2d; t2 += 2) {
+        const bool two = t2 + 1 < ntaps2d;
+        if (two) load_w(wB, wsoff + (t2 + 1) * tap_bytes);
+        compute(wA, toffb);
+        next_tap();
+        if (t2 + 2 < ntaps2d) load_w(wA, wsoff + (t2 + 2) * tap_bytes);
+        if (two) {
+          compute(wB, toffb);
+          next_tap();
         }
       }
     }
-    (void)taps;
+    if (has_next) ld.store(a, reinterpret_cast<T*>(lds_bytes + (pbuf ^ patch_bytes)), total_chunks, tid, NT);
+    __syncthreads();
   }
 
   // ---- epilogue: rows = output channels, columns = positions -----------------------------
@@ -241,9 +361,15 @@ const IgVariant kIg[] = {
     {"h_w22_f24_cb32", 0, 2, 2, 2, 4, 32},
     {"h_w14_f22_cb32", 0, 1, 4, 2, 2, 32},
     {"h_w22_f22_cb16", 0, 2, 2, 2, 2, 16},
+    {"h_w41_f24_cb32", 0, 4, 1, 2, 4, 32},
+    {"h_w41_f22_cb32", 0, 4, 1, 2, 2, 32},
+    {"h_w21_f24_cb32", 0, 2, 1, 2, 4, 32},
+    {"h_w22_f12_cb32", 0, 2, 2, 1, 2, 32},
+    {"h_w21_f14_cb32", 0, 2, 1, 1, 4, 32},
     {"f32_w22_f22_cb16", 1, 2, 2, 2, 2, 16},
     {"f32_w14_f22_cb16", 1, 1, 4, 2, 2, 16},
     {"f32_w22_f12_cb16", 1, 2, 2, 1, 2, 16},
+    {"f32_w21_f14_cb16", 1, 2, 1, 1, 4, 16},
 };
 constexpr int kNumIg = sizeof(kIg) / sizeof(kIg[0]);
 
@@ -281,8 +407,13 @@ int plan_ig(const ConvShape& p, int v, IgPlan& pl) {
   a.n_stages = n_cc * p.KD;
   a.n_kb = n_cc * (vr.cb / KB);
   a.co_blocks = (p.Co + pl.bn - 1) / pl.bn * (pl.bn / 32);
-  pl.lds = (size_t)a.PY * a.PX * (vr.cb + VEC) * es;
-  if (pl.lds > 64 * 1024) return fail(ATK_UNSUPPORTED, "conv %s: input patch of %zu bytes exceeds LDS", vr.name, pl.lds);
+  a.NCX = (a.PX + VEC - 1) / VEC + 1;
+  a.PXS = a.NCX * VEC;
+  a.patch_elems = a.PY * a.PXS * (vr.cb + VEC);
+  pl.lds = (size_t)2 * a.patch_elems * es;
+  if (pl.lds > 150 * 1024) return fail(ATK_UNSUPPORTED, "conv %s: input patch of %zu bytes exceeds LDS", vr.name, pl.lds);
+  if (vr.cb * a.PY * a.NCX > 8 * pl.nthreads)
+    return fail(ATK_UNSUPPORTED, "conv %s: input patch needs more than 8 chunks per thread", vr.name);
   pl.tiles = (int64_t)p.N * p.Do * a.tiles_y * a.tiles_x;
   const int co_tiles = (p.Co + pl.bn - 1) / pl.bn;
   if (pl.tiles > 0x7fffffff || co_tiles > 65535) return fail(ATK_UNSUPPORTED, "conv %s: grid too large", vr.name);
@@ -296,6 +427,9 @@ int plan_ig(const ConvShape& p, int v, IgPlan& pl) {
   pl.splits = splits;
   const int taps = p.KD * p.KH * p.KW;
   pl.wp_bytes = (size_t)taps * a.n_kb * a.co_blocks * 32 * KB * es;
+  // buffer loads address one input sample / the packed weights with 31-bit byte offsets
+  if ((int64_t)p.Ci * p.D * p.H * p.W * es >= (1ll << 31) || pl.wp_bytes >= (1ull << 31))
+    return fail(ATK_UNSUPPORTED, "conv %s: sample or weights exceed 2 GiB", vr.name);
   const int64_t ysz = (int64_t)p.N * p.Co * p.Do * p.Ho * p.Wo;
   pl.part_bytes = splits > 1 ? (size_t)splits * ysz * 4 : 0;
   return ATK_OK;
@@ -303,11 +437,28 @@ int plan_ig(const ConvShape& p, int v, IgPlan& pl) {
 
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, bool VR>
+int launch_ig_vr(const IgPlan& pl, hipStream_t s) {
+  auto kern = conv_igemm_kernel<T, WCO, WSP, FCO, FSP, CB, VR>;
+  if (pl.lds > 64 * 1024) {
+    // opt in to more than 64 KB of dynamic LDS (gfx950 has 160 KB per CU); once per kernel
+    static bool raised = false;
+    if (!raised) {
+      if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              150 * 1024) != hipSuccess)
+        return fail(ATK_UNSUPPORTED, "conv: cannot raise the LDS limit");
+      raised = true;
+    }
+  }
+  dim3 grid((unsigned)pl.tiles, (unsigned)((pl.a.Co + pl.bn - 1) / pl.bn), (unsigned)pl.splits);
+  hipLaunchKernelGGL(kern, grid, dim3(64 * WCO * WSP), pl.lds, s, pl.a);
+  return check_launch("conv_igemm_kernel");
+}
+
 template <typename T, int WCO, int WSP, int FCO, int FSP, int CB>
 int launch_ig_t(const IgPlan& pl, hipStream_t s) {
-  dim3 grid((unsigned)pl.tiles, (unsigned)((pl.a.Co + pl.bn - 1) / pl.bn), (unsigned)pl.splits);
-  hipLaunchKernelGGL((conv_igemm_kernel<T, WCO, WSP, FCO, FSP, CB>), grid, dim3(64 * WCO * WSP), pl.lds, s, pl.a);
-  return check_launch("conv_igemm_kernel");
+  return pl.a.vec_rows ? launch_ig_vr<T, WCO, WSP, FCO, FSP, CB, true>(pl, s)
+                       : launch_ig_vr<T, WCO, WSP, FCO, FSP, CB, false>(pl, s);
 }
 
 template <typename T>
@@ -320,6 +471,9 @@ int launch_ig(const ConvShape& p, const void* x, const void* w, const void* bias
   if (!ws || ws_bytes < need) return fail(ATK_EINVAL, "conv: workspace of %zu bytes needed", need);
   IgArgs& a = pl.a;
   a.x = x; a.bias = bias; a.y = y;
+  a.vec_rows = (p.W % (16 / (int)sizeof(T)) == 0) && aligned16(x);
+  a.x_sample_bytes = (uint32_t)((int64_t)p.Ci * p.D * p.H * p.W * sizeof(T));
+  a.wp_bytes = (uint32_t)pl.wp_bytes;
   a.wp = ws;
   a.part = pl.splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + align256(pl.wp_bytes)) : nullptr;
   // pack the weights
@@ -329,16 +483,29 @@ int launch_ig(const ConvShape& p, const void* x, const void* w, const void* bias
                      static_cast<const T*>(w), static_cast<T*>(ws), p.Co, p.Ci, taps, a.n_kb, a.co_blocks, wtotal);
   rc = check_launch("pack_weights_kernel");
   if (rc) return rc;
-  switch (v) {
-    case 0: rc = launch_ig_t<T, 2, 2, 2, 2, 32>(pl, s); break;
-    case 1: rc = launch_ig_t<T, 2, 2, 4, 2, 32>(pl, s); break;
-    case 2: rc = launch_ig_t<T, 2, 2, 2, 4, 32>(pl, s); break;
-    case 3: rc = launch_ig_t<T, 1, 4, 2, 2, 32>(pl, s); break;
-    case 4: rc = launch_ig_t<T, 2, 2, 2, 2, 16>(pl, s); break;
-    case 5: rc = launch_ig_t<T, 2, 2, 2, 2, 16>(pl, s); break;
-    case 6: rc = launch_ig_t<T, 1, 4, 2, 2, 16>(pl, s); break;
-    case 7: rc = launch_ig_t<T, 2, 2, 1, 2, 16>(pl, s); break;
-    default: return fail(ATK_EINVAL, "conv: bad variant");
+  // instantiate only the variants of this element type's class
+  if constexpr (sizeof(T) == 2) {
+    switch (v) {
+      case 0: rc = launch_ig_t<T, 2, 2, 2, 2, 32>(pl, s); break;
+      case 1: rc = launch_ig_t<T, 2, 2, 4, 2, 32>(pl, s); break;
+      case 2: rc = launch_ig_t<T, 2, 2, 2, 4, 32>(pl, s); break;
+      case 3: rc = launch_ig_t<T, 1, 4, 2, 2, 32>(pl, s); break;
+      case 4: rc = launch_ig_t<T, 2, 2, 2, 2, 16>(pl, s); break;
+      case 5: rc = launch_ig_t<T, 4, 1, 2, 4, 32>(pl, s); break;
+      case 6: rc = launch_ig_t<T, 4, 1, 2, 2, 32>(pl, s); break;
+      case 7: rc = launch_ig_t<T, 2, 1, 2, 4, 32>(pl, s); break;
+      case 8: rc = launch_ig_t<T, 2, 2, 1, 2, 32>(pl, s); break;
+      case 9: rc = launch_ig_t<T, 2, 1, 1, 4, 32>(pl, s); break;
+      default: return fail(ATK_EINVAL, "conv: bad variant");
+    }
+  } else {
+    switch (v) {
+      case 10: rc = launch_ig_t<T, 2, 2, 2, 2, 16>(pl, s); break;
+      case 11: rc = launch_ig_t<T, 1, 4, 2, 2, 16>(pl, s); break;
+      case 12: rc = launch_ig_t<T, 2, 2, 1, 2, 16>(pl, s); break;
+      case 13: rc = launch_ig_t<T, 2, 1, 1, 4, 16>(pl, s); break;
+      default: return fail(ATK_EINVAL, "conv: bad variant");
+    }
   }
   if (rc || pl.splits == 1) return rc;
   const int64_t ysz = (int64_t)p.N * p.Co * p.Do * p.Ho * p.Wo;
