@@ -1,6 +1,9 @@
 """Benchmark of the amd_tuned_torch hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-details] [--no-cpu]
+    python bench.py --traffic-probe [--variant V]          # workload of the counter passes
+    python bench.py --summarize-traffic FETCH_DIR WRITE_DIR [--variant V] [--command C]
+    python bench.py --summarize-stats STATS_DIR OUT.txt [--command C]
 
 Headline workload (config 2): causal depthwise conv1d
 (Mamba-style) through the patched torch.nn.functional API,
@@ -224,14 +227,135 @@ def cpu_baseline(rows_sample: int = 1):
                        f"2 B read + 2 B write per element")}
 
 
+# ---------------------------------------------------------------------------
+# HBM traffic of the headline kernel, from rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+# ---------------------------------------------------------------------------
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "dwconv1d_lds_kernel_c2_traffic.txt")
+CALIB_ELEMS = 16 * 2048 * 8192  # bf16 elements read and written by the calibration kernel
+
+
+def traffic_probe(variant: str, iters: int = 10):
+    """Workload for the counter passes: `iters` launches of the headline dwconv1d variant,
+    then `iters` launches of torch.neg over a bf16 tensor of CALIB_ELEMS elements — an
+    elementwise kernel that reads and writes exactly CALIB_ELEMS*2 bytes each, so its
+    FETCH_SIZE / WRITE_SIZE readings calibrate the counters' units and overheads."""
+    import torch
+    dev = torch.device("cuda", 0)
+    x, w, b = c2_inputs(torch.bfloat16, 4, dev)
+    L = x.shape[-1]
+    dw_kernel_ms(x, w, b, 3, L + 3, variant, iters=iters)
+    src = torch.randn(CALIB_ELEMS, device=dev, dtype=torch.bfloat16)
+    dst = torch.empty_like(src)
+    for _ in range(iters):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    log("traffic probe done")
+
+
+def _counter_means(run_dir: str, counter: str) -> "dict[str, float]":
+    """Mean per-dispatch value of `counter` for each kernel name in a rocprofv3 --pmc run."""
+    import csv
+    import glob
+    acc: "dict[str, list]" = {}
+    for f in glob.glob(os.path.join(run_dir, "**", "*counter_collection.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            if r["Counter_Name"] == counter:
+                acc.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+    return {k: sum(v) / len(v) for k, v in acc.items()}
+
+
+def _pick(means: "dict[str, float]", *needles: str) -> "tuple[str, float]":
+    hits = [(k, v) for k, v in means.items() if all(n in k for n in needles)]
+    if len(hits) != 1:
+        raise SystemExit(f"expected one kernel matching {needles}, found {[k[:80] for k, _ in hits]}")
+    return hits[0]
+
+
+def summarize_traffic(fetch_dir: str, write_dir: str, variant: str, command: str):
+    """Turn the two counter passes into the committed traffic summary (TRAFFIC_FILE)."""
+    fetch, write = _counter_means(fetch_dir, "FETCH_SIZE"), _counter_means(write_dir, "WRITE_SIZE")
+    kname, k_fetch = _pick(fetch, "dwconv1d_lds_kernel")
+    _, k_write = _pick(write, "dwconv1d_lds_kernel")
+    cname, c_fetch = _pick(fetch, "neg")
+    _, c_write = _pick(write, "neg")
+    calib_bytes = CALIB_ELEMS * 2
+    f_scale = c_fetch * 1024.0 / calib_bytes   # counter bytes per true byte read
+    w_scale = c_write * 1024.0 / calib_bytes
+    rd = k_fetch * 1024.0 / f_scale
+    wr = k_write * 1024.0 / w_scale
+    algo = 2 * CALIB_ELEMS * 2
+    rec = {"variant": variant, "kernel": kname[:120], "read_bytes": round(rd), "write_bytes": round(wr),
+           "traffic_bytes": round(rd + wr), "algorithmic_bytes": algo,
+           "fetch_kib_kernel": k_fetch, "write_kib_kernel": k_write,
+           "fetch_kib_calib": c_fetch, "write_kib_calib": c_write,
+           "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4)}
+    lines = [
+        "# HBM traffic per launch of the headline dwconv1d kernel (config 2, bf16, causal k=4)",
+        f"# commands: {command}",
+        f"# kernel: {kname[:160]}",
+        f"# calibration kernel (torch.neg over {CALIB_ELEMS} bf16 = {calib_bytes} B read + written): {cname[:120]}",
+        f"# FETCH_SIZE KiB/dispatch: kernel {k_fetch:.1f}, calibration {c_fetch:.1f} -> scale {f_scale:.4f}",
+        f"# WRITE_SIZE KiB/dispatch: kernel {k_write:.1f}, calibration {c_write:.1f} -> scale {w_scale:.4f}",
+        f"# traffic = {rd:.4g} B read + {wr:.4g} B written = {(rd + wr) / algo:.4f} x algorithmic {algo} B",
+        "TRAFFIC_JSON " + json.dumps(rec),
+    ]
+    with open(TRAFFIC_FILE, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
+def summarize_stats(stats_dir: str, out_path: str, command: str, top: int = 25):
+    """Write a rocprofv3 --kernel-trace --stats summary (per-kernel calls, average, min,
+    max duration, share of GPU time) as a short text file."""
+    import csv
+    import glob
+    rows = []
+    for f in glob.glob(os.path.join(stats_dir, "**", "*kernel_stats.csv"), recursive=True):
+        rows += list(csv.DictReader(open(f)))
+    rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    lines = [f"# rocprofv3 --kernel-trace --stats summary", f"# command: {command}",
+             f"# {'calls':>6} {'avg_us':>10} {'min_us':>10} {'max_us':>10} {'pct':>6}  kernel"]
+    for r in rows[:top]:
+        lines.append(f"  {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:10.2f} "
+                     f"{float(r['MinNs']) / 1e3:10.2f} {float(r['MaxNs']) / 1e3:10.2f} "
+                     f"{float(r['Percentage']):6.2f}  {r['Name'][:150]}")
+    with open(out_path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
+def load_traffic() -> "dict | None":
+    try:
+        for line in open(TRAFFIC_FILE):
+            if line.startswith("TRAFFIC_JSON "):
+                return json.loads(line[len("TRAFFIC_JSON "):])
+    except OSError:
+        return None
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-details", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="run only the workload of the FETCH_SIZE/WRITE_SIZE counter passes")
+    ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="write the traffic summary from two rocprofv3 --pmc output folders")
+    ap.add_argument("--summarize-stats", nargs=2, metavar=("STATS_DIR", "OUT"),
+                    help="write a text summary of a rocprofv3 --kernel-trace --stats folder")
+    ap.add_argument("--variant", default="lds_opt32_nt", help="dwconv1d variant for --traffic-probe")
+    ap.add_argument("--command", default="", help="command line recorded by --summarize-traffic")
     args = ap.parse_args()
+    if args.summarize_stats:
+        summarize_stats(*args.summarize_stats, args.command)
+        return
+    if args.summarize_traffic:
+        summarize_traffic(*args.summarize_traffic, args.variant, args.command)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; the hot path has no multi-GPU "
               "component (see DESIGN.md for how it would shard). Run with --gpus 1.",
@@ -244,6 +368,9 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a GPU"
     assert amd_tuned_torch.native_available(), "native library missing"
     dev = torch.device("cuda", 0)
+    if args.traffic_probe:
+        traffic_probe(args.variant)
+        return
 
     # ---- headline: causal depthwise conv1d bf16 (config 2) --------------------------
     x, w, b = c2_inputs(torch.bfloat16, 4, dev)
@@ -274,10 +401,19 @@ def main():
         kms = event_time_ms(lambda: step(), 20)
         kernel_name = "stock"
     achieved = nbytes / (kms * 1e-3) / 1e9
+    tr = load_traffic()
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": tr["traffic_bytes"] if tr else None,
                 "kernel": kernel_name, "variant": won, "kernel_ms": round(kms, 4),
                 "bytes_per_launch": nbytes}
+    if tr:
+        roofline["traffic_detail"] = {
+            "read_bytes": tr["read_bytes"], "write_bytes": tr["write_bytes"],
+            "measured_variant": tr["variant"],
+            "source": "profiles/" + os.path.basename(TRAFFIC_FILE) +
+                      " (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, scaled by a torch.neg copy "
+                      "of known size)"}
     y = step()
     ref = amd_tuned_torch.miopen_fallback._original_conv1d(
         x.float(), w.float(), b.float(), 1, 3, 1, x.shape[1])[..., :L]

@@ -51,6 +51,35 @@ def test_conv_matches_golden(golden):
     np.testing.assert_allclose(y, golden["c3_y"], rtol=0, atol=1e-12)
 
 
+def _far(a, b) -> bool:
+    return a.shape != b.shape or not np.allclose(a, b, rtol=0, atol=1e-9)
+
+
+def test_golden_pins_catch_planted_mistakes(golden):
+    """Each plausible mistake, planted in a call of the oracle, misses the golden fixture:
+    off-by-one padding, a flipped (correlation vs convolution) kernel, a dropped bias, a
+    wrong group count, a dropped eps, SiLU applied before the affine, and swapped
+    stride/dilation or a transposed weight in conv."""
+    m = golden["dw_causal_meta"].tolist()
+    N, C, L, K, p = m
+    x, w, b, y = (golden[f"dw_causal_{k}"] for k in "xwby")
+    lo = L + 2 * p - K + 1
+    assert _far(O.dwconv1d(x, w, b, p - 1, lo), y)
+    assert _far(O.dwconv1d(x, w[..., ::-1].copy(), b, p, lo), y)
+    assert _far(O.dwconv1d(x, w, None, p, lo), y)
+    gx, gg, gb = golden["gn_x"], golden["gn_g"], golden["gn_b"]
+    assert _far(O.group_norm(gx, 1, gg, gb, 1e-5), golden["gn_y"])
+    assert _far(O.group_norm(gx, 3, gg, gb, 0.0), golden["gn_y"])
+    assert _far(O.group_norm(gx, 3, gg, gb, 1e-5, silu=True), golden["gn_y"])
+    silu_first = O.group_norm(gx, 3, None, None, 1e-5, silu=True) * gg.reshape(1, -1, *([1] * (gx.ndim - 2))) \
+        + gb.reshape(1, -1, *([1] * (gx.ndim - 2)))
+    assert _far(silu_first, golden["gn_silu_y"])
+    assert _far(O.conv2d(golden["c2_x"], golden["c2_w"], golden["c2_b"], (1, 2), (1, 2), (2, 1)), golden["c2_y"])
+    c3w = golden["c3_w"]
+    assert _far(O.conv3d(golden["c3_x"], np.swapaxes(c3w, 3, 4).copy(), golden["c3_b"], (1, 2, 1), 1, 1),
+                golden["c3_y"])
+
+
 # ---------------------------------------------------------------------------
 # known answers of the reference's own tests
 # ---------------------------------------------------------------------------
