@@ -105,7 +105,11 @@ int atk_dwconv1d_fwd(const void* x, const void* w, const void* bias, void* y,
  * activations).  S = product of the spatial extents (1 for a [N, C] input).
  * Needs a workspace of atk_group_norm_workspace_bytes(...) bytes whose first
  * atk_group_norm_workspace_zero_bytes(...) bytes are zero before the FIRST call
- * that uses it (the kernels leave them zero again on exit).
+ * that uses it (the kernels leave them zero again on exit, apart from the first
+ * 4 bytes: a diagnostics word set to 1 when a workgroup stopped waiting for another's
+ * partial statistics and computed them itself -- results are exact either way).
+ * The zeroed region has a fixed size and layout for every shape, so one workspace
+ * serves calls of any shape (ordered on one stream), including HIP graph replays.
  * ------------------------------------------------------------------------- */
 size_t atk_group_norm_workspace_bytes(int64_t N, int64_t C, int64_t S, int G, int dtype,
                                       int variant);

@@ -175,9 +175,19 @@ def workspace(device: torch.device, purpose: str, nbytes: int) -> torch.Tensor:
         return buf
 
 
+def group_norm_clear_diag(device: Optional[torch.device] = None) -> None:
+    """Reset the diagnostics word that group_norm_barrier_error() reads."""
+    dev = device or torch.device("cuda", torch.cuda.current_device())
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), "group_norm")
+    buf = _workspaces.get(key)
+    if buf is not None:
+        buf[:4].zero_()
+
+
 def group_norm_barrier_error(device: Optional[torch.device] = None) -> bool:
-    """True if a cooperative GroupNorm launch ever exhausted its barrier spin bound on
-    `device` (it never should: cooperative launches guarantee co-residency)."""
+    """True if a register-resident GroupNorm launch on `device` ever gave up waiting for
+    another workgroup's slice statistics and computed them itself (results stay exact;
+    it only means the grid was not fully resident, e.g. under concurrent kernels)."""
     dev = device or torch.device("cuda", torch.cuda.current_device())
     key = (dev.index if dev.index is not None else torch.cuda.current_device(), "group_norm")
     buf = _workspaces.get(key)

@@ -40,6 +40,16 @@ int device_cu_count() {
   return n;
 }
 
+int device_wall_clock_khz() {
+  static int cached[64] = {0};
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < 64 && cached[dev] > 0) return cached[dev];
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeWallClockRate, dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < 64) cached[dev] = n;
+  return n;
+}
+
 // Variant tables are defined next to their kernels.
 int dwconv1d_num_variants();
 const char* dwconv1d_variant_name(int v);

@@ -20,6 +20,8 @@ void set_error(const char* fmt, ...);
 int fail(int code, const char* fmt, ...);
 int check_launch(const char* what);
 int device_cu_count();
+// Frequency of the device's constant wall clock (wall_clock64()) in kHz, 0 on error.
+int device_wall_clock_khz();
 
 inline size_t dtype_size(int dtype) { return dtype == ATK_F32 ? 4 : 2; }
 inline bool dtype_ok(int dtype) { return dtype == ATK_F32 || dtype == ATK_F16 || dtype == ATK_BF16; }
@@ -75,6 +77,36 @@ __device__ __forceinline__ void st16(void* p, uint4 r) {
     __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
   } else {
     *reinterpret_cast<uint4*>(p) = r;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Raw buffer access (gfx9 buffer resource, stride 0): a 32-bit lane offset plus a uniform
+// SGPR offset, and offsets at or beyond `bytes` read as zero -- used both to keep address
+// arithmetic off the VALU and to zero-fill masked loads without branches (a branch per
+// masked load makes the compiler wait for each load inside its branch).
+// ---------------------------------------------------------------------------
+constexpr uint32_t kOOB = 0x80000000u;  // >= every num_records used: reads zero
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+// AUX: cache-policy bits of the instruction (0 = default, 2 = nontemporal)
+template <int AUX = 0>
+__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, AUX);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+// (No buffer stores: 16-byte buffer stores with an SGPR offset produced sporadically wrong
+// output values on gfx950 in workgroups of >= 512 threads; stores use global_store.)
+template <typename T>
+__device__ __forceinline__ T bload_elem(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
+  if constexpr (sizeof(T) == 2) {
+    const unsigned short u = __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, 0, 0);
+    return __builtin_bit_cast(T, u);
+  } else {
+    const unsigned int u = __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, 0, 0);
+    return __builtin_bit_cast(T, u);
   }
 }
 

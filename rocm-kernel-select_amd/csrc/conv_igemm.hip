@@ -79,29 +79,6 @@ __device__ __forceinline__ void mfma_block(f32x16& acc, const uint4& a, const ui
   acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.w), __uint_as_float(b.w), acc, 0, 0, 0);
 }
 
-// Raw buffer access (gfx9 buffer resource, stride 0): a 32-bit lane offset plus a uniform
-// SGPR offset, and offsets at or beyond `bytes` read as zero -- used both to keep address
-// arithmetic off the VALU and to zero-fill masked loads without branches.
-constexpr uint32_t kOOB = 0x80000000u;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
-}
-__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0);
-  return make_uint4(v[0], v[1], v[2], v[3]);
-}
-template <typename T>
-__device__ __forceinline__ T bload_elem(__amdgpu_buffer_rsrc_t r, uint32_t voff) {
-  if constexpr (sizeof(T) == 2) {
-    const unsigned short u = __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, 0, 0);
-    return __builtin_bit_cast(T, u);
-  } else {
-    const unsigned int u = __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff, 0, 0);
-    return __builtin_bit_cast(T, u);
-  }
-}
-
 // Patch staging.  The patch of a stage is CB channels x PY input rows x NCX 16-byte chunks,
 // stored channels-last as patch[(py * PXS + px') * CBS + cl] with PXS = NCX * VEC: position
 // px' = chunk * VEC + e holds input column gx0 + px', gx0 being the tile's first needed
@@ -116,9 +93,12 @@ struct PatchLoader {
   uint4 buf[MAXC];
 
   // rsrc covers sample n of the input; iz may be out of range (a padding plane)
+  // valid == false issues the same loads with out-of-range offsets (they read zero): callers
+  // prefetch unconditionally, because a load inside a branch makes the compiler wait for it
+  // (and unpack it) inside that branch instead of where the data is used.
   __device__ __forceinline__ void load(const IgArgs& a, __amdgpu_buffer_rsrc_t rx, int cc, int iz, int iy0,
-                                       int gx0, int total, int tid, int nt) {
-    const bool zin = (unsigned)iz < (unsigned)a.D;
+                                       int gx0, int total, int tid, int nt, bool valid = true) {
+    const bool zin = valid && (unsigned)iz < (unsigned)a.D;
 #pragma unroll
     for (int u = 0; u < MAXC; ++u) {
       const int c = tid + u * nt;
@@ -145,8 +125,8 @@ struct PatchLoader {
 
   // Issue the load of chunk u only (same addressing as load()).
   __device__ __forceinline__ void load_one(const IgArgs& a, __amdgpu_buffer_rsrc_t rx, int u, int cc, int iz,
-                                           int iy0, int gx0, int total, int tid, int nt) {
-    const bool zin = (unsigned)iz < (unsigned)a.D;
+                                           int iy0, int gx0, int total, int tid, int nt, bool valid = true) {
+    const bool zin = valid && (unsigned)iz < (unsigned)a.D;
     const int c = tid + u * nt;
     const int cl = c % CB, rc = c / CB;
     const int py = rc / a.NCX, cx = rc - (rc / a.NCX) * a.NCX;
@@ -185,6 +165,50 @@ struct PatchLoader {
   }
 };
 
+// Bias of the workgroup's BN output channels as fp32 in LDS (zero without bias or when
+// writing split-K partials), staged before the main loop: read per element in the epilogue
+// from global memory, every element would wait for its own load.
+template <typename T, int BN, int NT>
+__device__ __forceinline__ void stage_bias(const IgArgs& a, int co_tile, float* s_bias) {
+  const T* __restrict__ bias = static_cast<const T*>(a.bias);
+  for (int i = threadIdx.x; i < BN; i += NT) {
+    const int co = co_tile * BN + i;
+    s_bias[i] = (bias && !a.part && co < a.Co) ? to_f32(bias[co]) : 0.f;
+  }
+}
+
+// Epilogue: accumulator rows = output channels, columns = positions.  Writes y (bias added,
+// converted) or, under split-K, this split's fp32 partial sums.
+template <typename T, int FCO, int FSP, int BN>
+__device__ __forceinline__ void store_tile(const IgArgs& a, const f32x16 (&acc)[FCO][FSP], const float* s_bias,
+                                           int n, int co_tile, int split, int oz, int oy0, int ox0, int wco,
+                                           int wsp, int half, int col) {
+  const int64_t spo = (int64_t)a.Do * a.Ho * a.Wo;
+#pragma unroll
+  for (int j = 0; j < FSP; ++j) {
+    const int m = (wsp * FSP + j) * 32 + col;
+    const int ty = m / a.TX, tx = m - (m / a.TX) * a.TX;
+    const int oy = oy0 + ty, ox = ox0 + tx;
+    if (oy >= a.Ho || ox >= a.Wo) continue;
+    const int64_t sp = ((int64_t)oz * a.Ho + oy) * a.Wo + ox;
+#pragma unroll
+    for (int i = 0; i < FCO; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int cl = (wco * FCO + i) * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+        const int co = co_tile * BN + cl;
+        if (co >= a.Co) continue;
+        const int64_t o = ((int64_t)n * a.Co + co) * spo + sp;
+        if (a.part) {
+          a.part[(int64_t)split * a.N * a.Co * spo + o] = acc[i][j][r];
+        } else {
+          static_cast<T*>(a.y)[o] = from_f32<T>(acc[i][j][r] + s_bias[cl]);
+        }
+      }
+    }
+  }
+}
+
 template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, bool VR, int KHT, int KWT>
 __global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm_kernel(IgArgs a) {
   constexpr int NT = 64 * WCO * WSP;
@@ -210,6 +234,8 @@ __global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm_kernel(IgArgs a) {
   const int n = t / a.Do;
   const int co_tile = blockIdx.y;
   const int split = blockIdx.z;
+  __shared__ float s_bias[BN];
+  stage_bias<T, BN, NT>(a, co_tile, s_bias);  // visible after the prologue's barrier
   const int s_begin = split * a.stages_per_split;
   const int s_end = min(a.n_stages, s_begin + a.stages_per_split);
   const int oy0 = ty_t * a.TY, ox0 = tx_t * a.TX;
@@ -283,7 +309,7 @@ __global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm_kernel(IgArgs a) {
       for (int p = 0; p < PF; ++p) load_w(wb[p], w_soff(s_begin, p));
     }
     for (int s = s_begin; s < s_end; ++s) {
-      const int cc = s / a.KD, kd = s - (s / a.KD) * a.KD;
+      const int kd = s - (s / a.KD) * a.KD;
       const int iz = oz * a.sd - a.pd + kd * a.dd;
       const bool zin = (unsigned)iz < (unsigned)a.D;
       const uint32_t pbuf = ((s - s_begin) & 1) ? patch_bytes : 0u;
@@ -293,8 +319,8 @@ __global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm_kernel(IgArgs a) {
 #pragma unroll
       for (int t2 = 0; t2 < NT2; ++t2) {
         load_w(wb[(t2 + PF) % NB], w_soff(s, t2 + PF));
-        if (t2 < PatchLoader<T, CB, VR>::MAXC && has_next)
-          ld.load_one(a, rx, t2, cc1, iz1, iy0, gx0, total_chunks, tid, NT);
+        if (t2 < PatchLoader<T, CB, VR>::MAXC)
+          ld.load_one(a, rx, t2, cc1, iz1, iy0, gx0, total_chunks, tid, NT, has_next);
         if (zin) {
           const uint32_t toffb = (uint32_t)(t2 / KWT) * kh_step + (uint32_t)(t2 % KWT) * kw_step;
 #pragma unroll
@@ -311,12 +337,10 @@ __global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm_kernel(IgArgs a) {
           }
         }
       }
-      if (has_next) {
 #pragma unroll
-        for (int u = NT2; u < PatchLoader<T, CB, VR>::MAXC; ++u)
-          ld.load_one(a, rx, u, cc1, iz1, iy0, gx0, total_chunks, tid, NT);
-        ld.store(a, reinterpret_cast<T*>(lds_bytes + (pbuf ^ patch_bytes)), total_chunks, tid, NT);
-      }
+      for (int u = NT2; u < PatchLoader<T, CB, VR>::MAXC; ++u)
+        ld.load_one(a, rx, u, cc1, iz1, iy0, gx0, total_chunks, tid, NT, has_next);
+      if (has_next) ld.store(a, reinterpret_cast<T*>(lds_bytes + (pbuf ^ patch_bytes)), total_chunks, tid, NT);
       __syncthreads();
     }
   } else
@@ -326,9 +350,9 @@ __global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm_kernel(IgArgs a) {
     const uint32_t pbuf = ((s - s_begin) & 1) ? patch_bytes : 0u;
     // prefetch the next stage's patch into registers while this stage computes
     const bool has_next = s + 1 < s_end;
-    if (has_next) {
+    {
       const int cc1 = (s + 1) / a.KD, kd1 = (s + 1) - ((s + 1) / a.KD) * a.KD;
-      ld.load(a, rx, cc1, oz * a.sd - a.pd + kd1 * a.dd, iy0, gx0, total_chunks, tid, NT);
+      ld.load(a, rx, cc1, oz * a.sd - a.pd + kd1 * a.dd, iy0, gx0, total_chunks, tid, NT, has_next);
     }
     if ((unsigned)iz < (unsigned)a.D) {
       // uniform byte offset of fragment (tap, kb of this chunk, co_blk0) in the packed weights
@@ -383,33 +407,7 @@ __global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm_kernel(IgArgs a) {
     __syncthreads();
   }
 
-  // ---- epilogue: rows = output channels, columns = positions -----------------------------
-  const int64_t spo = (int64_t)a.Do * a.Ho * a.Wo;
-  const T* __restrict__ bias = static_cast<const T*>(a.bias);
-#pragma unroll
-  for (int j = 0; j < FSP; ++j) {
-    const int m = (wsp * FSP + j) * 32 + col;
-    const int ty = m / a.TX, tx = m - (m / a.TX) * a.TX;
-    const int oy = oy0 + ty, ox = ox0 + tx;
-    if (oy >= a.Ho || ox >= a.Wo) continue;
-    const int64_t sp = ((int64_t)oz * a.Ho + oy) * a.Wo + ox;
-#pragma unroll
-    for (int i = 0; i < FCO; ++i) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int co = co_tile * BN + (wco * FCO + i) * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-        if (co >= a.Co) continue;
-        const int64_t o = ((int64_t)n * a.Co + co) * spo + sp;
-        if (a.part) {
-          a.part[(int64_t)split * a.N * a.Co * spo + o] = acc[i][j][r];
-        } else {
-          float v = acc[i][j][r];
-          if (bias) v += to_f32(bias[co]);
-          static_cast<T*>(a.y)[o] = from_f32<T>(v);
-        }
-      }
-    }
-  }
+  store_tile<T, FCO, FSP, BN>(a, acc, s_bias, n, co_tile, split, oz, oy0, ox0, wco, wsp, half, col);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -444,6 +442,8 @@ __global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm2_kernel(IgArgs a) {
   const int n = t / a.Do;
   const int co_tile = blockIdx.y;
   const int split = blockIdx.z;
+  __shared__ float s_bias[BN];
+  stage_bias<T, BN, NT>(a, co_tile, s_bias);  // visible after the prologue's barrier
   const int s_begin = split * a.stages_per_split;
   const int s_end = min(a.n_stages, s_begin + a.stages_per_split);
   const int oy0 = ty_t * a.TY, ox0 = tx_t * a.TX;
@@ -486,11 +486,12 @@ __global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm2_kernel(IgArgs a) {
   PatchLoader<T, CB, VR> ld;
   uint4 wbuf[WMAX];
   // global byte offset of weight chunk w of stage (cc, kd, rg)
-  auto load_stage = [&](int s) {
+  auto load_stage = [&](int s, bool valid) {
     const int rg = s % a.n_rg;
     const int ckd = s / a.n_rg;
     const int cc = ckd / a.KD, kd = ckd - (ckd / a.KD) * a.KD;
-    ld.load(a, rx, cc, oz * a.sd - a.pd + kd * a.dd, iy0 + rg * a.rps * a.dh, gx0, total_chunks, tid, NT);
+    ld.load(a, rx, cc, oz * a.sd - a.pd + kd * a.dd, iy0 + rg * a.rps * a.dh, gx0, total_chunks, tid, NT,
+            valid);
 #pragma unroll
     for (int u = 0; u < WMAX; ++u) {
       const int w = tid + u * NT;
@@ -502,7 +503,7 @@ __global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm2_kernel(IgArgs a) {
       const int tap = (kd * a.KH + rg * a.rps + r) * a.KW + kw;
       const uint32_t src = ((uint32_t)(tap * a.n_kb + cc * NKB + kb) * a.co_blocks + co_tile * NF + f) * FRAG
                            + (uint32_t)l16 * 16;
-      wbuf[u] = bload16(rw, w < wchunks ? src : kOOB, 0);
+      wbuf[u] = bload16(rw, valid && w < wchunks ? src : kOOB, 0);
     }
   };
   auto store_stage = [&](int buf) {
@@ -516,7 +517,7 @@ __global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm2_kernel(IgArgs a) {
   };
 
   if (s_begin < s_end) {
-    load_stage(s_begin);
+    load_stage(s_begin, true);
     store_stage(0);
   }
   __syncthreads();
@@ -524,7 +525,7 @@ __global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm2_kernel(IgArgs a) {
   for (int s = s_begin; s < s_end; ++s) {
     const int buf = (s - s_begin) & 1;
     const bool has_next = s + 1 < s_end;
-    if (has_next) load_stage(s + 1);
+    load_stage(s + 1, has_next);
     const int ckd = s / a.n_rg;
     const int kd = ckd - (ckd / a.KD) * a.KD;
     const int iz = oz * a.sd - a.pd + kd * a.dd;
@@ -561,33 +562,7 @@ __global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm2_kernel(IgArgs a) {
     __syncthreads();
   }
 
-  // ---- epilogue ------------------------------------------------------------------------
-  const int64_t spo = (int64_t)a.Do * a.Ho * a.Wo;
-  const T* __restrict__ bias = static_cast<const T*>(a.bias);
-#pragma unroll
-  for (int j = 0; j < FSP; ++j) {
-    const int m = (wsp * FSP + j) * 32 + col;
-    const int ty = m / a.TX, tx = m - (m / a.TX) * a.TX;
-    const int oy = oy0 + ty, ox = ox0 + tx;
-    if (oy >= a.Ho || ox >= a.Wo) continue;
-    const int64_t sp = ((int64_t)oz * a.Ho + oy) * a.Wo + ox;
-#pragma unroll
-    for (int i = 0; i < FCO; ++i) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int co = co_tile * BN + (wco * FCO + i) * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
-        if (co >= a.Co) continue;
-        const int64_t o = ((int64_t)n * a.Co + co) * spo + sp;
-        if (a.part) {
-          a.part[(int64_t)split * a.N * a.Co * spo + o] = acc[i][j][r];
-        } else {
-          float v = acc[i][j][r];
-          if (bias) v += to_f32(bias[co]);
-          static_cast<T*>(a.y)[o] = from_f32<T>(v);
-        }
-      }
-    }
-  }
+  store_tile<T, FCO, FSP, BN>(a, acc, s_bias, n, co_tile, split, oz, oy0, ox0, wco, wsp, half, col);
 }
 
 // Packed weights Wp[tap][kb][co_block][32][KB] from w[Co][Ci][taps]; zero beyond Co / Ci.

@@ -14,31 +14,52 @@
 //   res_*    Register-resident single pass.  A group is cut into NS slices of
 //            NT threads x EPV 16-byte vectors; each workgroup loads its slice ONCE into
 //            registers, reduces it twice (sum, then squared deviations about the slice
-//            mean), and, when NS > 1, exchanges (mean, M2) with the other slices of its
-//            group through a per-group generation barrier in the workspace.  All
-//            workgroups must be co-resident, so NS > 1 launches cooperatively (the
-//            runtime refuses the launch rather than oversubscribe) and the barrier spin
-//            is bounded.  HBM traffic: one read + one write of the tensor.
+//            mean) and, when NS > 1, publishes its (mean, M2) in a workspace slot.  One
+//            wave then collects the group's slots, lanes polling different slots.  A slot
+//            that has not appeared within a wall-clock bound is computed by the waiting
+//            workgroup itself, from x, with arithmetic identical to the owner's, so no
+//            workgroup ever depends on another being scheduled (no cooperative launch, no
+//            deadlock when the grid exceeds what is resident) and every workgroup of a
+//            group derives bit-identical statistics.  The last workgroup of a group to
+//            finish reading (a per-group counter) clears the group's slots, so every
+//            launch starts from empty slots -- also when replayed from a HIP graph.
+//            HBM traffic: one read + one write of the tensor.
 //   twopass  Streaming fallback for any size / alignment: a statistics kernel writes
 //            per-slice (mean, M2) partials, an apply kernel merges them and normalises.
+#include <cstdlib>
+
 #include "atk_common.h"
 
 namespace atk {
 
 namespace {
 
-constexpr uint32_t GN_SPIN_LIMIT = 1u << 20;  // polls (s_sleep(2) apart): never reached when co-resident
-constexpr int GN_MAX_NS = 4096;
-// Workspace layout is FIXED so that calls of different shapes sharing one workspace can
-// never write partials over another shape's barrier counters:
-//   [0, 256)                      error flag
-//   [256, 256 + 8*GN_MAX_COOP)    (arrivals, generation) per group, cooperative variants
-//   [GN_PARTIALS_OFF, ...)        per-slice (mean, M2) partials
-constexpr int GN_MAX_COOP = 4096;             // groups a cooperative launch may span
-constexpr size_t GN_ZERO_BYTES = 256 + 8 * (size_t)GN_MAX_COOP;
+constexpr int GN_MAX_NS = 4096;      // slices per group, two-pass
+constexpr int GN_RES_MAX_NS = 1024;  // slices per group, register-resident (LDS slot table)
+constexpr uint32_t GN_WAIT_US = 200; // wait for a slot before computing it locally
+// Workspace layout is FIXED (independent of the shape) so that calls of different shapes
+// sharing one workspace never see each other's state:
+//   [0, 256)                    diagnostics word (set when a wait timed out)
+//   [256, GN_SLOTS_OFF)         per-group "done reading" counters (register-resident)
+//   [GN_SLOTS_OFF, GN_ZERO_BYTES) register-resident slots, 16 B each
+//   [GN_PARTIALS_OFF, ...)      two-pass (mean, M2) partials
+// Everything below GN_ZERO_BYTES is zeroed once, at allocation, and every launch leaves
+// it zero again (apart from the diagnostics word).
+constexpr int GN_MAX_SLOTTED = 4096;   // groups a multi-slice register-resident launch may have
+constexpr int GN_MAX_SLOTS = 65536;    // groups x slices of such a launch
+constexpr size_t GN_SLOTS_OFF = 256 + 8 * (size_t)GN_MAX_SLOTTED;
+constexpr size_t GN_ZERO_BYTES = GN_SLOTS_OFF + 16 * (size_t)GN_MAX_SLOTS;
 constexpr size_t GN_PARTIALS_OFF = GN_ZERO_BYTES;
 constexpr int GN_TP_NT = 256;                 // two-pass kernels
 constexpr int GN_MAX_AFF = 512;               // channels per slice whose affine is staged in LDS
+
+// One slot = two 64-bit words (1 << 32 | bits(mean)), (1 << 32 | bits(M2)), each stored
+// and read with single-copy-atomic relaxed agent-scope accesses: a reader that sees the
+// marker in both words has both values, with no fence on either side (agent-scope
+// acquire/release would write back / invalidate the XCD's L2 on every poll).  Empty = 0.
+struct GnSlot {
+  unsigned long long w[2];
+};
 
 struct GnArgs {
   const void* x;
@@ -53,54 +74,34 @@ struct GnArgs {
   int silu;
   int pdt;            // dtype of gamma/beta
   FastDiv div_s;
-  uint32_t* err;      // workspace: error flag
-  uint32_t* counters; // workspace: [ngroups][2] (arrivals, generation)
-  float* partials;    // workspace: [ngroups][NS][2] (mean, M2)
+  uint64_t wait_ticks;// wall-clock ticks to wait for a slot
+  uint32_t* diag;     // workspace: diagnostics word
+  uint32_t* done;     // workspace: [ngroups] workgroups that finished reading the slots
+  GnSlot* slots;      // workspace: [ngroups][NS] (register-resident)
+  float* partials;    // workspace: [ngroups][NS][2] (mean, M2) (two-pass)
 };
-
-__device__ __forceinline__ float load_agent(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Per-group barrier among NS workgroups; called by one thread per workgroup, after that
-// thread stored its partial.  Generation counting leaves `cnt` at zero on exit, so the
-// workspace needs zeroing only once.
-__device__ void group_barrier(uint32_t* cnt, uint32_t* gen, int NS, uint32_t* err) {
-  const uint32_t g0 = __hip_atomic_load(gen, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
-  const uint32_t arrived = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-  if (arrived == (uint32_t)NS - 1) {
-    __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_fetch_add(gen, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
-  } else {
-    uint32_t it = 0;
-    while (__hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == g0) {
-      __builtin_amdgcn_s_sleep(2);
-      if (++it > GN_SPIN_LIMIT) {
-        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  }
-}
 
 __device__ __forceinline__ int64_t slice_len(int i, int64_t slice, int64_t E) {
   return (int64_t)(i + 1) * slice <= E ? slice : E - (int64_t)i * slice;
 }
 
-// Merge the NS (mean, M2) partials of one group, in a fixed order so that every
-// workgroup of the group derives bit-identical statistics.
-__device__ __forceinline__ void merge_partials(const float* p, int NS, int64_t slice, int64_t E,
-                                               float& mean, float& var) {
+// Merge NS (mean, M2) partials on one wave (call with all 64 lanes of wave 0):
+//   mean = sum n_i mean_i / E,   M2 = sum (M2_i + n_i (mean_i - mean)^2).
+// Lane l takes i = l, l+64, ... in order; the xor-butterfly then gives every lane the
+// same, order-fixed total, so every workgroup of a group derives bit-identical values.
+template <typename GetMean, typename GetM2>
+__device__ __forceinline__ void wave_merge(int NS, int64_t slice, int64_t E, GetMean gm, GetM2 g2,
+                                           float& mean, float& var) {
+  const int lane = threadIdx.x & 63;
   float sm = 0.f;
-  for (int i = 0; i < NS; ++i) sm += (float)slice_len(i, slice, E) * load_agent(p + 2 * i);
-  mean = sm / (float)E;
+  for (int i = lane; i < NS; i += 64) sm += (float)slice_len(i, slice, E) * gm(i);
+  mean = wave_sum(sm) / (float)E;
   float m2 = 0.f;
-  for (int i = 0; i < NS; ++i) {
-    const float d = load_agent(p + 2 * i) - mean;
-    m2 += load_agent(p + 2 * i + 1) + (float)slice_len(i, slice, E) * d * d;
+  for (int i = lane; i < NS; i += 64) {
+    const float d = gm(i) - mean;
+    m2 += g2(i) + (float)slice_len(i, slice, E) * d * d;
   }
-  var = m2 / (float)E;
+  var = wave_sum(m2) / (float)E;
 }
 
 // scale/shift of absolute channel `c` given the group statistics
@@ -128,12 +129,128 @@ __device__ __forceinline__ uint4 normalize_vec(const Vec16<T>& in, float sc, flo
 // ---------------------------------------------------------------------------------------
 // Register-resident single pass.  Requires S % VEC == 0 and 16B-aligned x / y (host check).
 // ---------------------------------------------------------------------------------------
+// Statistics of one slice of a group: sum, mean, then the sum of squared deviations, in
+// the order i = 0..EPV-1 (vector i of this thread = element s0 + (i*NT + tid)*VEC), k =
+// 0..VEC-1, with plain adds and explicit fmas, then fixed-order block reductions.  The
+// owner runs it on its registers (FROM_REG), a workgroup standing in for a late owner
+// runs it on memory with rolled loops; the arithmetic, and so every bit, is the same.
+// Opaque to the optimiser: keeps it from holding all VEC*EPV elements converted to fp32
+// across phases (that doubles the registers and spills); reconverting is a few VALU ops.
+template <typename T, int EPV>
+__device__ __forceinline__ void reg_fence(Vec16<T>* buf) {
+#pragma unroll
+  for (int i = 0; i < EPV; ++i)
+    asm volatile("" : "+v"(buf[i].raw.x), "+v"(buf[i].raw.y), "+v"(buf[i].raw.z), "+v"(buf[i].raw.w));
+}
+
+template <typename T, int NT, int EPV, bool FROM_REG>
+__device__ __forceinline__ void slice_stats(Vec16<T>* buf, const T* xg, int64_t s0, int64_t E,
+                                            int64_t slice, float* red, float& mean_l, float& m2) {
+  constexpr int VEC = 16 / sizeof(T);
+  const int tid = threadIdx.x;
+  auto get = [&](int i) -> Vec16<T> {
+    if constexpr (FROM_REG) {
+      return buf[i];
+    } else {
+      Vec16<T> v;
+      const int64_t e = s0 + ((int64_t)i * NT + tid) * VEC;
+      if (e < E) v.raw = *reinterpret_cast<const uint4*>(xg + e);
+      else v.raw = make_uint4(0u, 0u, 0u, 0u);
+      return v;
+    }
+  };
+  float sum = 0.f;
+  if constexpr (FROM_REG) {
+#pragma unroll
+    for (int i = 0; i < EPV; ++i) {
+      const Vec16<T> v = get(i);
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) sum += to_f32(v.e[k]);  // lanes past the group hold +0
+    }
+  } else {
+#pragma unroll 1
+    for (int i = 0; i < EPV; ++i) {
+      const Vec16<T> v = get(i);
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) sum += to_f32(v.e[k]);
+    }
+  }
+  const int64_t n_l = (E - s0) < slice ? (E - s0) : slice;
+  sum = block_sum<NT>(sum, red);
+  mean_l = sum / (float)n_l;
+  if constexpr (FROM_REG) reg_fence<T, EPV>(buf);
+  float q = 0.f;
+  auto dev2 = [&](int i) {
+    const int64_t e = s0 + ((int64_t)i * NT + tid) * VEC;
+    if (e < E) {
+      const Vec16<T> v = get(i);
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) {
+        const float d = to_f32(v.e[k]) - mean_l;
+        q = fmaf(d, d, q);
+      }
+    }
+  };
+  if constexpr (FROM_REG) {
+#pragma unroll
+    for (int i = 0; i < EPV; ++i) dev2(i);
+  } else {
+#pragma unroll 1
+    for (int i = 0; i < EPV; ++i) dev2(i);
+  }
+  m2 = block_sum<NT>(q, red);
+  if constexpr (FROM_REG) reg_fence<T, EPV>(buf);
+}
+
+// ---------------------------------------------------------------------------------------
+// Register-resident single pass.  Requires S % VEC == 0 and 16B-aligned x / y (host check).
+// ---------------------------------------------------------------------------------------
+// Statistics of slice `s` of a group, read from `get(i)` (the i-th 16-byte vector of this
+// thread: element s0 + (i*NT + tid)*VEC).  Both the owner (from registers) and a workgroup
+// standing in for a late owner (from memory) run this same arithmetic: plain sums and
+// explicit fmas in a fixed order, fixed-order block reductions.
+template <typename T, int NT, int EPV, typename Get>
+__device__ __forceinline__ void slice_stats(Get get, int64_t s0, int64_t E, int64_t slice, float* red,
+                                            float& mean_l, float& m2) {
+  constexpr int VEC = 16 / sizeof(T);
+  const int tid = threadIdx.x;
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < EPV; ++i) {
+    const Vec16<T> v = get(i);
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) sum += to_f32(v.e[k]);  // lanes past the group hold +0
+  }
+  const int64_t n_l = (E - s0) < slice ? (E - s0) : slice;
+  sum = block_sum<NT>(sum, red);
+  mean_l = sum / (float)n_l;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < EPV; ++i) {
+    const int64_t e = s0 + ((int64_t)i * NT + tid) * VEC;
+    if (e < E) {
+      const Vec16<T> v = get(i);
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) {
+        const float d = to_f32(v.e[k]) - mean_l;
+        q = fmaf(d, d, q);
+      }
+    }
+  }
+  m2 = block_sum<NT>(q, red);
+}
+
+// ---------------------------------------------------------------------------------------
+// Register-resident single pass.  Requires S % VEC == 0 and 16B-aligned x / y (host check).
+// ---------------------------------------------------------------------------------------
 template <typename T, int NT, int EPV>
 __global__ __launch_bounds__(NT) void gn_resident_kernel(GnArgs a) {
   constexpr int VEC = 16 / sizeof(T);
   __shared__ float red[NT / 64];
   __shared__ float s_stat[2];
   __shared__ float aff[2 * GN_MAX_AFF];  // scale[ ], shift[ ] of the slice's channels
+  __shared__ float sl_mean[GN_RES_MAX_NS], sl_m2[GN_RES_MAX_NS];
+  __shared__ int s_missing[GN_RES_MAX_NS + 1];  // [0] = count, then slice indices
 
   const int tid = threadIdx.x;
   const int64_t gi = blockIdx.x / a.NS;
@@ -143,54 +260,20 @@ __global__ __launch_bounds__(NT) void gn_resident_kernel(GnArgs a) {
   const T* __restrict__ xg = static_cast<const T*>(a.x) + gi * E;
   T* __restrict__ yg = static_cast<T*>(a.y) + gi * E;
 
+  // All EPV loads in flight at once, branch-free: one lane offset (tid*16 B) plus a
+  // uniform SGPR offset per vector; lanes past the group take an out-of-range offset and
+  // read 0 (and, below, store nothing).  Offsets are bytes from the group start (< 2^31).
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(xg, (uint32_t)(E * (int64_t)sizeof(T)));
+  const uint32_t lane_off = (uint32_t)tid * 16u;
+  const uint32_t n_vec = (uint32_t)((E - s0 + VEC - 1) / VEC);  // vectors of this slice in the group
+  auto voff = [&](int i) { return (uint32_t)(i * NT + tid) < n_vec ? lane_off : kOOB; };
+  auto soff = [&](int i) { return (uint32_t)((s0 + (int64_t)i * NT * VEC) * (int64_t)sizeof(T)); };
   Vec16<T> buf[EPV];
-  float sum = 0.f;
 #pragma unroll
-  for (int i = 0; i < EPV; ++i) {
-    const int64_t e = s0 + ((int64_t)i * NT + tid) * VEC;
-    if (e < E) buf[i].raw = ld16<true>(xg + e);
-    else buf[i].raw = make_uint4(0u, 0u, 0u, 0u);
-#pragma unroll
-    for (int k = 0; k < VEC; ++k) sum += to_f32(buf[i].e[k]);  // padding lanes hold +0
-  }
-  const int64_t n_l = (E - s0) < a.slice ? (E - s0) : a.slice;
-  sum = block_sum<NT>(sum, red);
-  const float mean_l = sum / (float)n_l;
-  float m2 = 0.f;
-#pragma unroll
-  for (int i = 0; i < EPV; ++i) {
-    const int64_t e = s0 + ((int64_t)i * NT + tid) * VEC;
-    if (e < E) {
-#pragma unroll
-      for (int k = 0; k < VEC; ++k) {
-        const float d = to_f32(buf[i].e[k]) - mean_l;
-        m2 = fmaf(d, d, m2);
-      }
-    }
-  }
-  m2 = block_sum<NT>(m2, red);
+  for (int i = 0; i < EPV; ++i) buf[i].raw = bload16<2>(rx, voff(i), soff(i));
 
-  float mean, var;
-  if (a.NS == 1) {
-    mean = mean_l;
-    var = m2 / (float)n_l;
-  } else {
-    float* part = a.partials + gi * (int64_t)a.NS * 2;
-    if (tid == 0) {
-      __hip_atomic_store(part + 2 * s, mean_l, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(part + 2 * s + 1, m2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      group_barrier(a.counters + 2 * gi, a.counters + 2 * gi + 1, a.NS, a.err);
-      merge_partials(part, a.NS, a.slice, E, mean, var);
-      s_stat[0] = mean;
-      s_stat[1] = var;
-    }
-    __syncthreads();
-    mean = s_stat[0];
-    var = s_stat[1];
-  }
-  const float rstd = 1.0f / sqrtf(var + a.eps);
-
-  // scale/shift of the channels this slice spans (group-local channel range [c_lo, c_hi))
+  // gamma/beta of the channels this slice spans (group-local [c_lo, c_hi)) are fetched now,
+  // while x is in flight, and turned into scale/shift once the statistics are known.
   const int64_t last = (s0 + a.slice < E ? s0 + a.slice : E) - 1;
   const uint32_t c_lo = fdiv((uint32_t)s0, a.div_s);
   const uint32_t c_hi = fdiv((uint32_t)last, a.div_s) + 1;
@@ -199,27 +282,130 @@ __global__ __launch_bounds__(NT) void gn_resident_kernel(GnArgs a) {
   const bool staged = nch <= GN_MAX_AFF;
   if (staged) {
     for (int i = tid; i < nch; i += NT) {
-      float sc, sh;
-      channel_affine(a, cabs0 + i, mean, rstd, sc, sh);
+      aff[i] = a.gamma ? load_param(a.gamma, a.pdt, cabs0 + i) : 1.f;
+      aff[GN_MAX_AFF + i] = a.beta ? load_param(a.beta, a.pdt, cabs0 + i) : 0.f;
+    }
+  }
+  float mean_l, m2;
+  slice_stats<T, NT, EPV, true>(buf, xg, s0, E, a.slice, red, mean_l, m2);
+
+  float mean, var;
+  if (a.NS == 1) {
+    mean = mean_l;
+    var = m2 / (float)((E - s0) < a.slice ? (E - s0) : a.slice);
+  } else {
+    GnSlot* slots = a.slots + gi * (int64_t)a.NS;
+    if (tid == 0) {
+      const unsigned long long hi = 1ull << 32;
+      __hip_atomic_store(&slots[s].w[0], hi | __float_as_uint(mean_l), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&slots[s].w[1], hi | __float_as_uint(m2), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+      s_missing[0] = 0;
+    }
+    __syncthreads();
+    if (tid < 64) {
+      // collect the group's slots, one lane per slot; wait at most wait_ticks in total
+      const uint64_t t0 = wall_clock64();
+      for (int j = tid; j < a.NS; j += 64) {
+        bool ok;
+        if (j == s) {
+          ok = true;
+          sl_mean[j] = mean_l;
+          sl_m2[j] = m2;
+        } else {
+          unsigned long long w0, w1;
+          for (;;) {
+            w0 = __hip_atomic_load(&slots[j].w[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            w1 = __hip_atomic_load(&slots[j].w[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            ok = (w0 >> 32) != 0 && (w1 >> 32) != 0;
+            if (ok || wall_clock64() - t0 > a.wait_ticks) break;
+            __builtin_amdgcn_s_sleep(1);
+          }
+          if (ok) {
+            sl_mean[j] = __uint_as_float((uint32_t)w0);
+            sl_m2[j] = __uint_as_float((uint32_t)w1);
+          }
+        }
+        if (!ok) s_missing[1 + atomicAdd(&s_missing[0], 1)] = j;
+      }
+    }
+    __syncthreads();
+    const int nmiss = s_missing[0];
+    if (nmiss > 0) {
+      // stand in for late owners: the same statistics, computed from x
+      if (tid == 0) __hip_atomic_store(a.diag, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int m = 0; m < nmiss; ++m) {
+        const int j = s_missing[1 + m];
+        const int64_t j0 = (int64_t)j * a.slice;
+        float mj, qj;
+        slice_stats<T, NT, EPV, false>(nullptr, xg, j0, E, a.slice, red, mj, qj);
+        if (tid == 0) {
+          sl_mean[j] = mj;
+          sl_m2[j] = qj;
+        }
+      }
+      __syncthreads();
+    }
+    if (tid < 64) {
+      wave_merge(a.NS, a.slice, E, [&](int i) { return sl_mean[i]; }, [&](int i) { return sl_m2[i]; },
+                 mean, var);
+      if (tid == 0) {
+        s_stat[0] = mean;
+        s_stat[1] = var;
+      }
+      // This workgroup is done with the slots (its lanes' reads returned before this point).
+      // The last of the group's NS workgroups -- every one has published by then -- empties
+      // them for the next launch and resets the counter.
+      uint32_t prev = 0;
+      if (tid == 0)
+        prev = __hip_atomic_fetch_add(a.done + gi, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      prev = __shfl(prev, 0, 64);
+      if (prev == (uint32_t)a.NS - 1) {
+        for (int j = tid; j < a.NS; j += 64) {
+          __hip_atomic_store(&slots[j].w[0], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(&slots[j].w[1], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (tid == 0) __hip_atomic_store(a.done + gi, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    __syncthreads();
+    mean = s_stat[0];
+    var = s_stat[1];
+  }
+  const float rstd = 1.0f / sqrtf(var + a.eps);
+
+  if (staged) {
+    for (int i = tid; i < nch; i += NT) {  // the entries this thread fetched above
+      const float sc = rstd * aff[i];
+      aff[GN_MAX_AFF + i] = aff[GN_MAX_AFF + i] - mean * sc;
       aff[i] = sc;
-      aff[GN_MAX_AFF + i] = sh;
     }
   }
   __syncthreads();
 
+  if (staged) {
+    // Offsets recomputed from an opaque copy of tid: reusing the load phase's per-vector
+    // offsets would keep EPV more registers alive across the reductions.
+    int tid_s = tid;
+    asm volatile("" : "+v"(tid_s));
 #pragma unroll
-  for (int i = 0; i < EPV; ++i) {
-    const int64_t e = s0 + ((int64_t)i * NT + tid) * VEC;
-    if (e < E) {
+    for (int i = 0; i < EPV; ++i) {
+      const bool ok = (uint32_t)(i * NT + tid_s) < n_vec;
+      const int64_t e = ok ? s0 + ((int64_t)i * NT + tid_s) * VEC : s0;
       const int cl = (int)(fdiv((uint32_t)e, a.div_s) - c_lo);
-      float sc, sh;
-      if (staged) {
-        sc = aff[cl];
-        sh = aff[GN_MAX_AFF + cl];
-      } else {
+      if (ok) st16<true>(yg + e, normalize_vec<T>(buf[i], aff[cl], aff[GN_MAX_AFF + cl], a.silu));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < EPV; ++i) {
+      const int64_t e = s0 + ((int64_t)i * NT + tid) * VEC;
+      if (e < E) {
+        const int cl = (int)(fdiv((uint32_t)e, a.div_s) - c_lo);
+        float sc, sh;
         channel_affine(a, cabs0 + cl, mean, rstd, sc, sh);
+        st16<true>(yg + e, normalize_vec<T>(buf[i], sc, sh, a.silu));
       }
-      st16<true>(yg + e, normalize_vec<T>(buf[i], sc, sh, a.silu));
     }
   }
 }
@@ -292,11 +478,15 @@ __global__ __launch_bounds__(GN_TP_NT) void gn_apply_kernel(GnArgs a) {
   const int64_t s1 = s0 + a.slice < E ? s0 + a.slice : E;
   const T* __restrict__ xg = static_cast<const T*>(a.x) + gi * E;
   T* __restrict__ yg = static_cast<T*>(a.y) + gi * E;
-  if (tid == 0) {
+  if (tid < 64) {
+    const float* p = a.partials + gi * (int64_t)a.NS * 2;
     float mean, var;
-    merge_partials(a.partials + gi * (int64_t)a.NS * 2, a.NS, a.slice, E, mean, var);
-    s_stat[0] = mean;
-    s_stat[1] = 1.0f / sqrtf(var + a.eps);
+    wave_merge(a.NS, a.slice, E, [&](int i) { return p[2 * i]; }, [&](int i) { return p[2 * i + 1]; },
+               mean, var);
+    if (tid == 0) {
+      s_stat[0] = mean;
+      s_stat[1] = 1.0f / sqrtf(var + a.eps);
+    }
   }
   __syncthreads();
   const float mean = s_stat[0], rstd = s_stat[1];
@@ -334,6 +524,11 @@ const GnVariant kGnVariants[] = {
     {"res_nt256_v8", 256, 8},
     {"res_nt256_v16", 256, 16},
     {"twopass", GN_TP_NT, 0},
+    {"res_nt256_v4", 256, 4},
+    {"res_nt512_v4", 512, 4},
+    {"res_nt512_v16", 512, 16},
+    {"res_nt512_v32", 512, 32},
+    {"res_nt256_v32", 256, 32},
 };
 constexpr int kNumGn = sizeof(kGnVariants) / sizeof(kGnVariants[0]);
 
@@ -356,6 +551,8 @@ bool plan_gn(int64_t N, int64_t C, int64_t S, int G, int dtype, int variant, GnP
   if (v.epv > 0) {
     p.slice = (int64_t)v.nt * v.epv * vec;
     p.NS = (int)((E + p.slice - 1) / p.slice);
+    if (p.NS > GN_RES_MAX_NS) return false;
+    if (E * (int64_t)dtype_size(dtype) >= (int64_t)kOOB) return false;  // 32-bit buffer offsets
   } else {
     // aim for >= ~2048 workgroups, slices of at least 4K elements
     int64_t ns = (2048 + ngroups - 1) / (ngroups > 0 ? ngroups : 1);
@@ -370,7 +567,7 @@ bool plan_gn(int64_t N, int64_t C, int64_t S, int G, int dtype, int variant, GnP
   }
   if (p.NS > GN_MAX_NS) return false;
   p.zero_bytes = GN_ZERO_BYTES;
-  p.ws_bytes = GN_PARTIALS_OFF + round256((size_t)ngroups * p.NS * 8);
+  p.ws_bytes = GN_PARTIALS_OFF + (v.epv > 0 ? 0 : round256((size_t)ngroups * p.NS * 8));
   return true;
 }
 
@@ -379,30 +576,27 @@ int launch_resident(GnArgs a, int64_t ngroups, hipStream_t s) {
   const int64_t nblk = ngroups * a.NS;
   if (nblk > 0x7fffffff) return fail(ATK_UNSUPPORTED, "group_norm: grid too large");
   auto kern = gn_resident_kernel<T, NT, EPV>;
-  if (a.NS == 1) {
-    hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(NT), 0, s, a);
-    return check_launch("gn_resident_kernel");
+  if (a.NS > 1) {
+    if (ngroups > GN_MAX_SLOTTED || nblk > GN_MAX_SLOTS)
+      return fail(ATK_UNSUPPORTED, "group_norm: %lld groups x %d slices exceed the slot table",
+                  (long long)ngroups, a.NS);
+    // Correct at any grid size (late slices are computed by the waiting workgroups),
+    // but only fast when every workgroup of the grid can be resident at once.
+    static int per_cu_cache[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64)
+      return fail(ATK_ELAUNCH, "group_norm: no current device");
+    if (per_cu_cache[dev] == 0 &&
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu_cache[dev], reinterpret_cast<const void*>(kern),
+                                                     NT, 0) != hipSuccess)
+      return fail(ATK_ELAUNCH, "group_norm: occupancy query failed");
+    const int64_t cap = (int64_t)per_cu_cache[dev] * device_cu_count();
+    if (nblk > cap)
+      return fail(ATK_UNSUPPORTED, "group_norm: %lld workgroups exceed the %lld that can be resident",
+                  (long long)nblk, (long long)cap);
   }
-  if (ngroups > GN_MAX_COOP)
-    return fail(ATK_UNSUPPORTED, "group_norm: %lld groups exceed the cooperative barrier table",
-                (long long)ngroups);
-  int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kern), NT, 0) != hipSuccess)
-    return fail(ATK_ELAUNCH, "group_norm: occupancy query failed");
-  const int64_t cap = (int64_t)per_cu * device_cu_count();
-  if (nblk > cap)
-    return fail(ATK_UNSUPPORTED, "group_norm: %lld workgroups cannot be co-resident (max %lld)",
-                (long long)nblk, (long long)cap);
-  void* args[] = {&a};
-  hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(kern), dim3((unsigned)nblk),
-                                            dim3(NT), args, 0, s);
-  if (e != hipSuccess) {
-    (void)hipGetLastError();
-    if (e == hipErrorCooperativeLaunchTooLarge)
-      return fail(ATK_UNSUPPORTED, "group_norm: cooperative launch too large");
-    return fail(ATK_ELAUNCH, "group_norm: cooperative launch: %s", hipGetErrorString(e));
-  }
-  return ATK_OK;
+  hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(NT), 0, s, a);
+  return check_launch("gn_resident_kernel");
 }
 
 template <typename T>
@@ -417,6 +611,11 @@ int launch_gn(GnArgs a, int64_t ngroups, int variant, bool vec_ok, hipStream_t s
       case 3: return launch_resident<T, 512, 8>(a, ngroups, s);
       case 4: return launch_resident<T, 256, 8>(a, ngroups, s);
       case 5: return launch_resident<T, 256, 16>(a, ngroups, s);
+      case 7: return launch_resident<T, 256, 4>(a, ngroups, s);
+      case 8: return launch_resident<T, 512, 4>(a, ngroups, s);
+      case 9: return launch_resident<T, 512, 16>(a, ngroups, s);
+      case 10: return launch_resident<T, 512, 32>(a, ngroups, s);
+      case 11: return launch_resident<T, 256, 32>(a, ngroups, s);
       default: return fail(ATK_EINVAL, "group_norm: bad variant");
     }
   }
@@ -508,9 +707,15 @@ extern "C" int atk_group_norm_fwd(const void* x, const void* gamma, const void* 
   a.pdt = param_dtype;
   a.div_s = make_fastdiv((uint32_t)S);
   char* ws = static_cast<char*>(workspace);
-  a.err = reinterpret_cast<uint32_t*>(ws);
-  a.counters = reinterpret_cast<uint32_t*>(ws + 256);
+  a.diag = reinterpret_cast<uint32_t*>(ws);
+  a.done = reinterpret_cast<uint32_t*>(ws + 256);
+  a.slots = reinterpret_cast<GnSlot*>(ws + GN_SLOTS_OFF);
   a.partials = reinterpret_cast<float*>(ws + GN_PARTIALS_OFF);
+  const int khz = device_wall_clock_khz();
+  // ATK_GN_WAIT_US overrides the wait (tests set 0 to exercise the stand-in path)
+  const char* wenv = getenv("ATK_GN_WAIT_US");
+  const uint64_t wait_us = wenv ? strtoull(wenv, nullptr, 10) : GN_WAIT_US;
+  a.wait_ticks = (uint64_t)(khz > 0 ? khz : 100000) * wait_us / 1000;
   const int64_t ngroups = N * G;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (dtype) {

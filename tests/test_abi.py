@@ -80,9 +80,11 @@ def test_argument_validation_codes(nat):
     # group norm
     assert lib.atk_group_norm_workspace_bytes(2, 6, 4, 4, 1, 0) == 0
     assert "divisible" in nat.last_error()
-    ws = lib.atk_group_norm_workspace_bytes(8, 512, 4096, 32, 1, 0)
-    zero = lib.atk_group_norm_workspace_zero_bytes(8, 512, 4096, 32, 1, 0)
-    assert 0 < zero < ws
+    tp = nat.variants(nat.OP_GROUP_NORM).index("twopass")
+    ws = lib.atk_group_norm_workspace_bytes(8, 512, 4096, 32, 1, tp)
+    zero = lib.atk_group_norm_workspace_zero_bytes(8, 512, 4096, 32, 1, tp)
+    assert 0 < zero < ws                                            # partials after the zeroed part
+    assert lib.atk_group_norm_workspace_bytes(8, 512, 4096, 32, 1, 0) >= zero
     # the zeroed (barrier) region does not depend on the shape
     assert zero == lib.atk_group_norm_workspace_zero_bytes(1, 64, 7, 2, 0, 6)
     assert lib.atk_group_norm_fwd(None, None, None, None, 2, 6, 4, 3, 1e-5, 0, 1, 1, 0, None, 0, None) == nat.ATK_EINVAL

@@ -31,16 +31,16 @@ def _inputs(shape, dtype, seed=0, affine=True, pdtype=None):
     return x.to(dtype), gamma.to(pdtype), beta.to(pdtype)
 
 
-def _check(y, x, G, gamma, beta, eps, silu=False):
+def _check(y, x, G, gamma, beta, eps, silu=False, what=""):
     ref = O.group_norm(x, G, gamma, beta, eps, silu=silu)
     err = O.max_rel_err(y, ref)
-    assert err <= BAR[y.dtype], f"max_rel_err {err:.3g} > {BAR[y.dtype]}"
+    assert err <= BAR[y.dtype], f"{what} max_rel_err {err:.3g} > {BAR[y.dtype]}"
     return err
 
 
 SHAPES = [
     ((2, 64, 8, 8), 8),           # one small slice per group
-    ((1, 32, 128, 128), 2),       # groups of 262144 elements: several slices, cooperative
+    ((1, 32, 128, 128), 2),       # groups of 262144 elements: several slices per group
     ((2, 12, 5, 7, 8), 3),        # 3-D spatial
     ((3, 10, 24), 5),             # 1-D spatial
 ]
@@ -62,7 +62,7 @@ def test_group_norm_all_variants(dev, shape_g, dtype):
                 assert name != "twopass", "the two-pass variant must accept every shape"
                 continue
             torch.cuda.synchronize()
-            _check(y.cpu(), x, G, gm, bt, 1e-5, silu=silu)
+            _check(y.cpu(), x, G, gm, bt, 1e-5, silu=silu, what=f"{name} silu={silu}")
             ran += 1
     assert ran >= 2
     assert not nat.group_norm_barrier_error(dev)
@@ -109,9 +109,9 @@ def test_group_norm_misaligned_pointer(dev):
         nat.group_norm(xv, 4, gm.to(dev), bt.to(dev), 1e-5, variant=names.index("res_nt1024_v8"))
 
 
-def test_group_norm_repeated_calls_keep_barrier_consistent(dev):
-    """Cooperative variants reuse the workspace barrier: many calls in a row, different
-    slice counts, all correct and no spin-bound hits."""
+def test_group_norm_repeated_calls_keep_slots_consistent(dev):
+    """Register-resident variants reuse the workspace slots: many calls in a row, different
+    slice counts, all correct, and no workgroup ever had to stand in for another."""
     nat = _native()
     names = nat.variants(nat.OP_GROUP_NORM)
     x, gm, bt = _inputs((1, 32, 128, 128), torch.bfloat16, seed=12)
@@ -122,6 +122,60 @@ def test_group_norm_repeated_calls_keep_barrier_consistent(dev):
             y = nat.group_norm(xd, 2, gd, bd, 1e-5, variant=names.index(name))
             torch.cuda.synchronize()
             assert O.max_rel_err(y.cpu(), ref) <= 1e-2
+    assert not nat.group_norm_barrier_error(dev)
+
+
+def test_group_norm_standin_path_is_bit_identical(dev, monkeypatch):
+    """With a zero wait, workgroups compute every slice that is not yet published
+    themselves.  The statistics must come out bit-identical to the normal path (same
+    arithmetic in the same order), so the outputs are equal byte for byte."""
+    nat = _native()
+    names = nat.variants(nat.OP_GROUP_NORM)
+    x, gm, bt = _inputs((1, 64, 32, 32, 16), torch.bfloat16, seed=13)   # 32 groups x 32768
+    xd, gd, bd = x.to(dev), gm.to(dev), bt.to(dev)
+    ref = O.group_norm(x, 32, gm, bt, 1e-5, silu=True)
+    for name in ("res_nt256_v4", "res_nt256_v8"):
+        vi = names.index(name)
+        y0 = nat.group_norm(xd, 32, gd, bd, 1e-5, silu=True, variant=vi)
+        torch.cuda.synchronize()
+        assert not nat.group_norm_barrier_error(dev)
+        monkeypatch.setenv("ATK_GN_WAIT_US", "0")
+        for _ in range(3):
+            y1 = nat.group_norm(xd, 32, gd, bd, 1e-5, silu=True, variant=vi)
+            torch.cuda.synchronize()
+            assert torch.equal(y0.view(torch.int16), y1.view(torch.int16)), name
+        monkeypatch.delenv("ATK_GN_WAIT_US")
+        assert O.max_rel_err(y1.cpu(), ref) <= 1e-2
+        nat.group_norm_clear_diag(dev)
+
+
+def test_group_norm_graph_replay(dev):
+    """Captured in a HIP graph and replayed with new inputs copied in between replays
+    (eager work and synchronisation between them): every replay matches the oracle --
+    each launch empties its slots, so nothing carries over to the next replay."""
+    nat = _native()
+    names = nat.variants(nat.OP_GROUP_NORM)
+    shape, G = (1, 64, 32, 32, 16), 32
+    data = [_inputs(shape, torch.bfloat16, seed=40 + i) for i in range(3)]
+    gm, bt = data[0][1], data[0][2]
+    gd, bd = gm.to(dev), bt.to(dev)
+    static_x = data[0][0].to(dev)
+    for name in ("res_nt256_v4", "res_nt512_v8", "twopass"):
+        vi = names.index(name)
+        out = torch.empty_like(static_x)
+        nat.group_norm(static_x, G, gd, bd, 1e-5, silu=True, variant=vi, out=out)  # allocates workspace
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            nat.group_norm(static_x, G, gd, bd, 1e-5, silu=True, variant=vi, out=out)
+        for _ in range(2):
+            for x, _, _ in data:
+                static_x.copy_(x.to(dev))
+                torch.cuda.synchronize()
+                graph.replay()
+                torch.cuda.synchronize()
+                ref = O.group_norm(x, G, gm, bt, 1e-5, silu=True)
+                assert O.max_rel_err(out.cpu(), ref) <= 1e-2, name
     assert not nat.group_norm_barrier_error(dev)
 
 
@@ -153,9 +207,8 @@ def test_group_norm_config_full_size(dev, cfg, dtype):
 
 def test_group_norm_workspace_shared_across_shapes(dev):
     """Regression: a shape with few groups and many slices writes many partials into the
-    shared workspace; a following cooperative call on a shape with many groups must still
-    find its barrier counters at zero (they live in a fixed region the partials never
-    reach)."""
+    shared workspace; a following multi-slice call on a shape with many groups must not
+    mistake those for its own slots (slots carry a per-launch tag)."""
     nat = _native()
     names = nat.variants(nat.OP_GROUP_NORM)
     xa, ga, ba = _inputs((8, 256, 64, 64), torch.float16, seed=21)    # 256 groups of 32768
