@@ -43,7 +43,7 @@ struct IgArgs {
   int TX, TY, tiles_x, tiles_y;
   int PX, PY;
   int NCX;            // 16-byte chunks per patch row (aligned-down start)
-  int PXS;            // patch row stride in positions = NCX * VEC
+  int PXS;            // patch row stride in positions: NCX * VEC, padded against bank conflicts
   int vec_rows;       // input rows are 16-byte aligned (W % VEC == 0, aligned base)
   int patch_elems;    // elements of one patch buffer (two are allocated)
   uint32_t x_sample_bytes;  // bytes of one input sample (buffer range of the patch loads)
@@ -80,7 +80,7 @@ __device__ __forceinline__ void mfma_block(f32x16& acc, const uint4& a, const ui
 }
 
 // Patch staging.  The patch of a stage is CB channels x PY input rows x NCX 16-byte chunks,
-// stored channels-last as patch[(py * PXS + px') * CBS + cl] with PXS = NCX * VEC: position
+// stored channels-last as patch[(py * PXS + px') * CBS + cl] with PXS >= NCX * VEC: position
 // px' = chunk * VEC + e holds input column gx0 + px', gx0 being the tile's first needed
 // column (ix0) rounded down to a 16-byte boundary, so every chunk is written whole with no
 // per-element bounds test; readers add mis = ix0 - gx0.  Chunk c maps to (row-chunk
@@ -145,6 +145,73 @@ struct PatchLoader {
         v.e[e] = bload_elem<T>(rx, ok ? (row + ix) * (uint32_t)sizeof(T) : kOOB);
       }
       buf[u] = v.raw;
+    }
+  }
+
+  // ---- precomputed quad path (VR only) --------------------------------------------------
+  // A thread owns NQ "quads": 4 consecutive channels x one 16-byte row chunk (VEC positions),
+  // chunks 4g..4g+3 of buf.  Quad q of the tile is (channel quad cq = q % (CB/4), patch row
+  // py, chunk column cx) with py next-fastest after cq: the lanes of one LDS write cycle then
+  // cover several patch rows at the same positions, and the host pads the row pitch (PXS) so
+  // that those rows fall on disjoint banks.  A quad goes to LDS as one 64-bit (16-bit types)
+  // or 128-bit (fp32) store per position -- 4x fewer LDS writes than one per element.  All
+  // offsets are fixed for the tile, so a stage only adds a uniform term: no division is
+  // left in the stage loop.
+  static constexpr int NQ = MAXC / 4;
+  uint32_t goff[MAXC];  // element offset in the sample without the stage term (cc*CB*DHW + iz*HW)
+  int clim[MAXC];       // channel inside the CB block, or a huge value if outside patch/input
+  uint32_t qoff[NQ];    // LDS element offset of the quad's first element
+
+  __device__ __forceinline__ void init(const IgArgs& a, int iy0, int gx0, int total_quads, int tid, int nt) {
+    constexpr int CBS = CB + VEC;
+#pragma unroll
+    for (int g = 0; g < NQ; ++g) {
+      const int q = tid + g * nt;
+      const int cq = q % (CB / 4), rr = q / (CB / 4);
+      const int py = rr % a.PY, cx = rr / a.PY;
+      const int iy = iy0 + py, gx = gx0 + cx * VEC;
+      const bool ok = q < total_quads && (unsigned)iy < (unsigned)a.H && gx >= 0 && gx + VEC <= a.W;
+      qoff[g] = (uint32_t)((py * a.PXS + cx * VEC) * CBS + cq * 4);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int cl = cq * 4 + k;
+        goff[g * 4 + k] = (uint32_t)((cl * a.D * a.H + iy) * a.W + gx);
+        clim[g * 4 + k] = ok ? cl : (1 << 30);
+      }
+    }
+  }
+  // Stage term and channel limit of stage (cc, iz); valid == false or a padding plane (iz
+  // outside [0, D)) gives a limit no chunk passes, so every load reads zero.
+  __device__ __forceinline__ static uint32_t stage_off(const IgArgs& a, int cc, int iz) {
+    return (uint32_t)((cc * CB * a.D + iz) * a.H * a.W);
+  }
+  __device__ __forceinline__ static int stage_lim(const IgArgs& a, int cc, int iz, bool valid) {
+    return (valid && (unsigned)iz < (unsigned)a.D) ? a.Ci - cc * CB : 0;
+  }
+  __device__ __forceinline__ void load_fast(__amdgpu_buffer_rsrc_t rx, int u, uint32_t soff_el, int lim) {
+    buf[u] = bload16(rx, clim[u] < lim ? (goff[u] + soff_el) * (uint32_t)sizeof(T) : kOOB, 0);
+  }
+  __device__ __forceinline__ static uint32_t dw(const uint4& v, int i) {
+    return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+  }
+  __device__ __forceinline__ void store_quad(T* patch, int g, int total_quads, int tid, int nt) const {
+    constexpr int CBS = CB + VEC;
+    if (tid + g * nt >= total_quads) return;
+    T* dst = patch + qoff[g];
+    const uint4 &c0 = buf[4 * g], &c1 = buf[4 * g + 1], &c2 = buf[4 * g + 2], &c3 = buf[4 * g + 3];
+    if constexpr (sizeof(T) == 2) {
+      // position e of the 4 channels: halves e%2 of dword e/2 of each chunk
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+        const uint32_t lo = __builtin_amdgcn_perm(dw(c1, e >> 1), dw(c0, e >> 1), sel);
+        const uint32_t hi = __builtin_amdgcn_perm(dw(c3, e >> 1), dw(c2, e >> 1), sel);
+        *reinterpret_cast<uint2*>(dst + e * CBS) = make_uint2(lo, hi);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e)
+        *reinterpret_cast<uint4*>(dst + e * CBS) = make_uint4(dw(c0, e), dw(c1, e), dw(c2, e), dw(c3, e));
     }
   }
 
@@ -273,30 +340,56 @@ __global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm_kernel(IgArgs a) {
   const int co_blk0 = co_tile * (BN / 32) + wco * FCO;
 
   PatchLoader<T, CB, VR> ld;
+  const int total_quads = total_chunks / 4;
+  if constexpr (VR) ld.init(a, iy0, gx0, total_quads, tid, NT);
+  // stage s = (channel chunk cc, kernel plane kd), walked incrementally
+  int cc = s_begin / a.KD, kd = s_begin - (s_begin / a.KD) * a.KD;
+  const int iz_base = oz * a.sd - a.pd;
   if (s_begin < s_end) {
-    const int cc = s_begin / a.KD, kd = s_begin - (s_begin / a.KD) * a.KD;
-    ld.load(a, rx, cc, oz * a.sd - a.pd + kd * a.dd, iy0, gx0, total_chunks, tid, NT);
-    ld.store(a, reinterpret_cast<T*>(lds_bytes), total_chunks, tid, NT);
+    if constexpr (VR) {
+      const int iz = iz_base + kd * a.dd;
+      const uint32_t so = ld.stage_off(a, cc, iz);
+      const int lim = ld.stage_lim(a, cc, iz, true);
+#pragma unroll
+      for (int u = 0; u < PatchLoader<T, CB, VR>::MAXC; ++u) ld.load_fast(rx, u, so, lim);
+#pragma unroll
+      for (int g = 0; g < PatchLoader<T, CB, VR>::NQ; ++g)
+        ld.store_quad(reinterpret_cast<T*>(lds_bytes), g, total_quads, tid, NT);
+    } else {
+      ld.load(a, rx, cc, iz_base + kd * a.dd, iy0, gx0, total_chunks, tid, NT);
+      ld.store(a, reinterpret_cast<T*>(lds_bytes), total_chunks, tid, NT);
+    }
   }
   __syncthreads();
+
+  const uint32_t tap_bytes = (uint32_t)a.n_kb * a.co_blocks * FRAG;
+  const uint32_t kb_bytes = (uint32_t)a.co_blocks * FRAG;
+  // byte offset of (stage (cc, kd), in-plane tap 0) in the packed weights for this wave
+  // (readfirstlane: the value is wave-uniform; saying so keeps the compiler from wrapping each
+  // buffer load that uses it as an SGPR offset in a waterfall loop)
+  auto wbase = [&](int c, int k) -> uint32_t {
+    return __builtin_amdgcn_readfirstlane((uint32_t)(k * ntaps2d) * tap_bytes + (uint32_t)(c * NKB) * kb_bytes +
+                                          co_blk0 * FRAG);
+  };
 
   if constexpr (KHT > 0) {
     // ---- static schedule for a KHT x KWT kernel plane -----------------------------------
     // Weights stream through NB rotating register buffers PF taps ahead, continuing across
-    // stage boundaries; chunk u of the next stage's patch is issued at tap u.  The tap loop
-    // is straight-line code, so every wait is an exact vmcnt/lgkmcnt count.
+    // stage boundaries.  The next stage's patch chunks are issued two per tap (taps 0-3) and
+    // written to the idle LDS buffer a quad at a time at taps QS0 and QS1, where the wait for
+    // that tap's weights (issued PF taps earlier, after those chunks) has already covered
+    // them; the stage then ends with the barrier alone.  The tap loop is straight-line code,
+    // so every wait is an exact vmcnt/lgkmcnt count.
     constexpr int NT2 = KHT * KWT;
-    constexpr int PF = 2, NB = 3;
+    // NB rotating weight buffers (a divisor of NT2, so the rotation repeats every stage),
+    // prefetching PF taps ahead; only PF + 1 of them are live at once
+    constexpr int NB = NT2 % 3 == 0 ? 3 : NT2 % 5 == 0 ? 5 : 7;
+    constexpr int PF = NB - 1 < 3 ? NB - 1 : 3;
+    constexpr int MAXC = PatchLoader<T, CB, VR>::MAXC;
+    constexpr int NQ = PatchLoader<T, CB, VR>::NQ;
     static_assert(NT2 % NB == 0, "buffer rotation must repeat every stage");
-    const uint32_t tap_bytes = (uint32_t)a.n_kb * a.co_blocks * FRAG;
-    const uint32_t kb_bytes = (uint32_t)a.co_blocks * FRAG;
-    auto w_soff = [&](int s, int t2) -> uint32_t {  // stage s, in-plane tap t2 (may spill into s+1)
-      int ss = s + t2 / NT2;
-      t2 = t2 % NT2;
-      if (ss >= s_end) ss = s_end - 1;               // clamped: a harmless reload
-      const int cc = ss / a.KD, kd = ss - (ss / a.KD) * a.KD;
-      return (uint32_t)(kd * NT2 + t2) * tap_bytes + (uint32_t)(cc * NKB) * kb_bytes + co_blk0 * FRAG;
-    };
+    static_assert(NQ == 2 && MAXC == 8 && NT2 >= 9, "schedule below assumes 8 chunks, 9+ taps");
+    constexpr int QS0 = 5, QS1 = 8;  // chunks 0-3 issued by tap 1, 4-7 by tap 3
     uint4 wb[NB][NKB][FCO];
     auto load_w = [&](uint4 (&w)[NKB][FCO], uint32_t so) {
 #pragma unroll
@@ -306,21 +399,31 @@ __global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm_kernel(IgArgs a) {
     };
     if (s_begin < s_end) {
 #pragma unroll
-      for (int p = 0; p < PF; ++p) load_w(wb[p], w_soff(s_begin, p));
+      for (int p = 0; p < PF; ++p) load_w(wb[p], wbase(cc, kd) + p * tap_bytes);
     }
     for (int s = s_begin; s < s_end; ++s) {
-      const int kd = s - (s / a.KD) * a.KD;
-      const int iz = oz * a.sd - a.pd + kd * a.dd;
+      const int iz = iz_base + kd * a.dd;
       const bool zin = (unsigned)iz < (unsigned)a.D;
       const uint32_t pbuf = ((s - s_begin) & 1) ? patch_bytes : 0u;
       const bool has_next = s + 1 < s_end;
-      const int cc1 = (s + 1) / a.KD, kd1 = (s + 1) - ((s + 1) / a.KD) * a.KD;
-      const int iz1 = oz * a.sd - a.pd + kd1 * a.dd;
+      int cc1 = cc, kd1 = kd + 1;
+      if (kd1 == a.KD) {
+        kd1 = 0;
+        ++cc1;
+      }
+      const int iz1 = iz_base + kd1 * a.dd;
+      const uint32_t so1 = __builtin_amdgcn_readfirstlane(ld.stage_off(a, cc1, iz1));
+      const int lim1 = __builtin_amdgcn_readfirstlane(ld.stage_lim(a, cc1, iz1, has_next));
+      const uint32_t wb_cur = wbase(cc, kd);
+      const uint32_t wb_nxt = has_next ? wbase(cc1, kd1) : wb_cur;  // last stage: harmless reload
 #pragma unroll
       for (int t2 = 0; t2 < NT2; ++t2) {
-        load_w(wb[(t2 + PF) % NB], w_soff(s, t2 + PF));
-        if (t2 < PatchLoader<T, CB, VR>::MAXC)
-          ld.load_one(a, rx, t2, cc1, iz1, iy0, gx0, total_chunks, tid, NT, has_next);
+        const int tp = t2 + PF;
+        load_w(wb[tp % NB], tp < NT2 ? wb_cur + tp * tap_bytes : wb_nxt + (tp - NT2) * tap_bytes);
+        if (2 * t2 < MAXC) {
+          ld.load_fast(rx, 2 * t2, so1, lim1);
+          ld.load_fast(rx, 2 * t2 + 1, so1, lim1);
+        }
         if (zin) {
           const uint32_t toffb = (uint32_t)(t2 / KWT) * kh_step + (uint32_t)(t2 % KWT) * kw_step;
 #pragma unroll
@@ -336,29 +439,37 @@ __global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm_kernel(IgArgs a) {
                 mfma_block(acc[i][j], wb[t2 % NB][kb][i], pf[j], static_cast<T*>(nullptr));
           }
         }
+        // the idle buffer was released by every wave at the previous stage's barrier
+        if ((t2 == QS0 || t2 == QS1) && has_next)
+          ld.store_quad(reinterpret_cast<T*>(lds_bytes + (pbuf ^ patch_bytes)), t2 == QS0 ? 0 : 1,
+                        total_quads, tid, NT);
       }
-#pragma unroll
-      for (int u = NT2; u < PatchLoader<T, CB, VR>::MAXC; ++u)
-        ld.load_one(a, rx, u, cc1, iz1, iy0, gx0, total_chunks, tid, NT, has_next);
-      if (has_next) ld.store(a, reinterpret_cast<T*>(lds_bytes + (pbuf ^ patch_bytes)), total_chunks, tid, NT);
       __syncthreads();
+      cc = cc1;
+      kd = kd1;
     }
   } else
   for (int s = s_begin; s < s_end; ++s) {
-    const int cc = s / a.KD, kd = s - (s / a.KD) * a.KD;
-    const int iz = oz * a.sd - a.pd + kd * a.dd;
+    const int iz = iz_base + kd * a.dd;
     const uint32_t pbuf = ((s - s_begin) & 1) ? patch_bytes : 0u;
-    // prefetch the next stage's patch into registers while this stage computes
     const bool has_next = s + 1 < s_end;
-    {
-      const int cc1 = (s + 1) / a.KD, kd1 = (s + 1) - ((s + 1) / a.KD) * a.KD;
-      ld.load(a, rx, cc1, oz * a.sd - a.pd + kd1 * a.dd, iy0, gx0, total_chunks, tid, NT, has_next);
+    int cc1 = cc, kd1 = kd + 1;
+    if (kd1 == a.KD) {
+      kd1 = 0;
+      ++cc1;
+    }
+    // prefetch the next stage's patch into registers while this stage computes
+    if constexpr (VR) {
+      const int iz1 = iz_base + kd1 * a.dd;
+      const uint32_t so1 = __builtin_amdgcn_readfirstlane(ld.stage_off(a, cc1, iz1));
+      const int lim1 = __builtin_amdgcn_readfirstlane(ld.stage_lim(a, cc1, iz1, has_next));
+#pragma unroll
+      for (int u = 0; u < PatchLoader<T, CB, VR>::MAXC; ++u) ld.load_fast(rx, u, so1, lim1);
+    } else {
+      ld.load(a, rx, cc1, iz_base + kd1 * a.dd, iy0, gx0, total_chunks, tid, NT, has_next);
     }
     if ((unsigned)iz < (unsigned)a.D) {
-      // uniform byte offset of fragment (tap, kb of this chunk, co_blk0) in the packed weights
-      const uint32_t tap_bytes = (uint32_t)a.n_kb * a.co_blocks * FRAG;
-      const uint32_t kb_bytes = (uint32_t)a.co_blocks * FRAG;
-      uint32_t wsoff = (uint32_t)(kd * ntaps2d) * tap_bytes + (uint32_t)(cc * NKB) * kb_bytes + co_blk0 * FRAG;
+      const uint32_t wsoff = wbase(cc, kd);
       uint4 wA[NKB][FCO], wB[NKB][FCO];
       auto load_w = [&](uint4 (&w)[NKB][FCO], uint32_t so) {
 #pragma unroll
@@ -403,8 +514,18 @@ __global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm_kernel(IgArgs a) {
         }
       }
     }
-    if (has_next) ld.store(a, reinterpret_cast<T*>(lds_bytes + (pbuf ^ patch_bytes)), total_chunks, tid, NT);
+    if (has_next) {
+      if constexpr (VR) {
+#pragma unroll
+        for (int g = 0; g < PatchLoader<T, CB, VR>::NQ; ++g)
+          ld.store_quad(reinterpret_cast<T*>(lds_bytes + (pbuf ^ patch_bytes)), g, total_quads, tid, NT);
+      } else {
+        ld.store(a, reinterpret_cast<T*>(lds_bytes + (pbuf ^ patch_bytes)), total_chunks, tid, NT);
+      }
+    }
     __syncthreads();
+    cc = cc1;
+    kd = kd1;
   }
 
   store_tile<T, FCO, FSP, BN>(a, acc, s_bias, n, co_tile, split, oz, oy0, ox0, wco, wsp, half, col);
@@ -663,7 +784,16 @@ int plan_ig(const ConvShape& p, int v, IgPlan& pl) {
   a.n_kb = n_cc * (vr.cb / KB);
   a.co_blocks = (p.Co + pl.bn - 1) / pl.bn * (pl.bn / 32);
   a.NCX = (a.PX + VEC - 1) / VEC + 1;
-  a.PXS = a.NCX * VEC;
+  // Row pitch: padded (0-7 positions) so that consecutive patch rows start CB*es bytes apart
+  // modulo 128 -- the quad writes of one LDS cycle, CB*es bytes per row, then tile 128 bytes
+  // -- unless the padding would cost a resident workgroup per CU (decided below).
+  int row_pad = 0;
+  for (int pad = 0; pad < 8; ++pad) {
+    if (((a.NCX * VEC + pad) * (vr.cb + VEC) * es) % 128 == (vr.cb * es) % 128) {
+      row_pad = pad;
+      break;
+    }
+  }
   const size_t frag = (size_t)32 * KB * es;
   // stage = (ci chunk, kd[, kernel row group]); family 2 also stages the weight slice
   int rps = p.KH;
@@ -671,6 +801,12 @@ int plan_ig(const ConvShape& p, int v, IgPlan& pl) {
     a.rps = rps;
     a.n_rg = p.KH / rps;
     a.PY = (a.TY - 1) * p.sh + (rps - 1) * p.dh + 1;
+    {
+      constexpr size_t kLdsCu = 160 * 1024;
+      const size_t plain = (size_t)2 * a.PY * a.NCX * VEC * (vr.cb + VEC) * es + 1024;
+      const size_t padded = (size_t)2 * a.PY * (a.NCX * VEC + row_pad) * (vr.cb + VEC) * es + 1024;
+      a.PXS = a.NCX * VEC + (kLdsCu / padded == kLdsCu / plain ? row_pad : 0);
+    }
     a.patch_elems = a.PY * a.PXS * (vr.cb + VEC);
     a.w_stage_frags = vr.family == 2 ? rps * p.KW * (vr.cb / KB) * (pl.bn / 32) : 0;
     pl.lds = (size_t)2 * a.patch_elems * es + (size_t)2 * a.w_stage_frags * frag;
@@ -727,6 +863,8 @@ template <typename T, int WCO, int WSP, int FCO, int FSP, int CB>
 int launch_ig_t(const IgPlan& pl, hipStream_t s) {
   if (pl.a.KH == 3 && pl.a.KW == 3 && pl.a.vec_rows)
     return launch_ig_vr<T, WCO, WSP, FCO, FSP, CB, true, 3, 3>(pl, s);
+  if (pl.a.KH == 7 && pl.a.KW == 7 && pl.a.vec_rows)
+    return launch_ig_vr<T, WCO, WSP, FCO, FSP, CB, true, 7, 7>(pl, s);
   return pl.a.vec_rows ? launch_ig_vr<T, WCO, WSP, FCO, FSP, CB, true, 0, 0>(pl, s)
                        : launch_ig_vr<T, WCO, WSP, FCO, FSP, CB, false, 0, 0>(pl, s);
 }
