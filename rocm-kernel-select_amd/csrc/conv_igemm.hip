@@ -89,7 +89,9 @@ __device__ __forceinline__ void mfma_block(f32x16& acc, const uint4& a, const ui
 template <typename T, int CB, bool VR>
 struct PatchLoader {
   static constexpr int VEC = 16 / sizeof(T);
-  static constexpr int MAXC = 8;  // chunks per thread held for the next stage
+  // chunks per thread held for the next stage: CB/4 for 16-bit types, CB/2 for fp32 (the host
+  // plan rejects tiles whose patch needs more)
+  static constexpr int MAXC = sizeof(T) == 2 ? CB / 4 : CB / 2;
   uint4 buf[MAXC];
 
   // rsrc covers sample n of the input; iz may be out of range (a padding plane)
@@ -276,8 +278,11 @@ __device__ __forceinline__ void store_tile(const IgArgs& a, const f32x16 (&acc)[
   }
 }
 
+// Tiles of 8 accumulator blocks (128 AGPRs) are asked to fit 2 waves per SIMD: with their
+// LDS footprint two workgroups share a CU, and one wave per SIMD leaves no latency cover.
 template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, bool VR, int KHT, int KWT>
-__global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm_kernel(IgArgs a) {
+__global__ __launch_bounds__(64 * WCO * WSP)
+__attribute__((amdgpu_waves_per_eu(FCO * FSP >= 8 && CB == 16 ? 2 : 1))) void conv_igemm_kernel(IgArgs a) {
   constexpr int NT = 64 * WCO * WSP;
   constexpr int KB = MfmaTraits<T>::KB, VEC = MfmaTraits<T>::VEC;
   constexpr int ES = sizeof(T);
@@ -388,8 +393,9 @@ __global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm_kernel(IgArgs a) {
     constexpr int MAXC = PatchLoader<T, CB, VR>::MAXC;
     constexpr int NQ = PatchLoader<T, CB, VR>::NQ;
     static_assert(NT2 % NB == 0, "buffer rotation must repeat every stage");
-    static_assert(NQ == 2 && MAXC == 8 && NT2 >= 9, "schedule below assumes 8 chunks, 9+ taps");
-    constexpr int QS0 = 5, QS1 = 8;  // chunks 0-3 issued by tap 1, 4-7 by tap 3
+    static_assert(NQ >= 1 && NQ <= 2 && NT2 >= 9, "schedule below assumes <= 2 quads, 9+ taps");
+    // quad g (chunks 4g..4g+3, issued by tap 2g+1) is written at tap QS0 + 3g
+    constexpr int QS0 = 5, QS1 = NQ > 1 ? 8 : -1;
     uint4 wb[NB][NKB][FCO];
     auto load_w = [&](uint4 (&w)[NKB][FCO], uint32_t so) {
 #pragma unroll
@@ -440,7 +446,7 @@ __global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm_kernel(IgArgs a) {
           }
         }
         // the idle buffer was released by every wave at the previous stage's barrier
-        if ((t2 == QS0 || t2 == QS1) && has_next)
+        if ((t2 == QS0 || t2 == QS1) && has_next)  // QS1 < 0: single quad
           ld.store_quad(reinterpret_cast<T*>(lds_bytes + (pbuf ^ patch_bytes)), t2 == QS0 ? 0 : 1,
                         total_quads, tid, NT);
       }
@@ -748,6 +754,8 @@ const IgVariant kIg[] = {
     {"h2_w22_f42_cb16", 0, 2, 2, 4, 2, 16, 2},
     {"f32_2_w22_f22_cb16", 1, 2, 2, 2, 2, 16, 2},
     {"f32_2_w12_f24_cb16", 1, 1, 2, 2, 4, 16, 2},
+    {"h_w22_f24_cb16", 0, 2, 2, 2, 4, 16, 1},
+    {"h_w41_f24_cb16", 0, 4, 1, 2, 4, 16, 1},
 };
 constexpr int kNumIg = sizeof(kIg) / sizeof(kIg[0]);
 
@@ -810,7 +818,8 @@ int plan_ig(const ConvShape& p, int v, IgPlan& pl) {
     a.patch_elems = a.PY * a.PXS * (vr.cb + VEC);
     a.w_stage_frags = vr.family == 2 ? rps * p.KW * (vr.cb / KB) * (pl.bn / 32) : 0;
     pl.lds = (size_t)2 * a.patch_elems * es + (size_t)2 * a.w_stage_frags * frag;
-    const bool fits = pl.lds <= 150 * 1024 && vr.cb * a.PY * a.NCX <= 8 * pl.nthreads &&
+    const int maxc = f32 ? vr.cb / 2 : vr.cb / 4;  // chunks a thread holds (PatchLoader::MAXC)
+    const bool fits = pl.lds <= 150 * 1024 && vr.cb * a.PY * a.NCX <= maxc * pl.nthreads &&
                       a.w_stage_frags * 64 <= IG2_WMAX * pl.nthreads;
     if (fits) break;
     if (rps == 1 || vr.family != 2)
@@ -933,6 +942,8 @@ int launch_ig(const ConvShape& p, const void* x, const void* w, const void* bias
       case 17: rc = launch_ig2_t<T, 1, 4, 2, 2, 32>(pl, s); break;
       case 18: rc = launch_ig2_t<T, 1, 2, 2, 4, 32>(pl, s); break;
       case 19: rc = launch_ig2_t<T, 2, 2, 4, 2, 16>(pl, s); break;
+      case 22: rc = launch_ig_t<T, 2, 2, 2, 4, 16>(pl, s); break;
+      case 23: rc = launch_ig_t<T, 4, 1, 2, 4, 16>(pl, s); break;
       default: return fail(ATK_EINVAL, "conv: bad variant");
     }
   } else {
