@@ -14,7 +14,8 @@ A step is one such call with x already resident in HBM; `value` is algorithmic H
 
 `roofline` is the dominant kernel alone: the same per-launch bytes divided by its average
 duration from HIP events around back-to-back launches on the launching stream, against
-MI355X's 8 TB/s.  `cpu_baseline` is the reference's CPU path (stock torch.nn.functional,
+MI355X's 8 TB/s.  The `details` timings replay the winning kernel from a captured HIP graph
+(kernel time without host dispatch between launches).  `cpu_baseline` is the reference's CPU path (stock torch.nn.functional,
 fp32, on the host cores) on a bounded sample of the same workload.  `details` carries the
 other BASELINE configs (GroupNorm GB/s, conv3d TFLOP/s, each with its parity error against
 stock fp32 on the GPU).  Exactly one JSON line goes to stdout; progress goes to stderr.
@@ -62,6 +63,32 @@ def event_time_ms(fn, iters: int, warmup: int = 3) -> float:
     b.record(s)
     b.synchronize()
     return a.elapsed_time(b) / iters
+
+
+def graph_time_ms(fn, iters: int) -> float:
+    """Average ms per call of `fn` with no host work between kernels: `iters` calls are
+    captured in one HIP graph and the replay is timed with HIP events (falls back to
+    event_time_ms if the calls cannot be captured)."""
+    import torch
+    try:
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(iters):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        graph.replay()
+        b.record()
+        b.synchronize()
+        return a.elapsed_time(b) / iters
+    except Exception as exc:  # capture unsupported: time eagerly instead
+        log(f"  graph capture failed ({exc!r}); timing eagerly")
+        return event_time_ms(fn, iters)
 
 
 def max_rel_err(y, ref) -> float:
@@ -151,7 +178,7 @@ def bench_gn_detail(shape, G, eps, dtype, silu, dev):
     if won.startswith("native."):
         vi = nat.variants(nat.OP_GROUP_NORM).index(won[7:])
         out = torch.empty_like(x)
-        ms = event_time_ms(lambda: nat.group_norm(x, G, gm, bt, eps, silu=silu, variant=vi, out=out), 50)
+        ms = graph_time_ms(lambda: nat.group_norm(x, G, gm, bt, eps, silu=silu, variant=vi, out=out), 50)
     else:
         ms = event_time_ms(lambda: torch.group_norm(x, G, gm, bt, eps), 50)
     nbytes = 2 * x.numel() * x.element_size()
@@ -163,7 +190,7 @@ def bench_gn_detail(shape, G, eps, dtype, silu, dev):
 # ---------------------------------------------------------------------------
 # configs 4 / 5: conv3d
 # ---------------------------------------------------------------------------
-def bench_conv_detail(xs, ws, pad, dtype, dev, iters=10):
+def bench_conv_detail(xs, ws, pad, dtype, dev, iters=20):
     import torch
     import torch.nn.functional as F
     import amd_tuned_torch  # noqa: F401
@@ -182,7 +209,7 @@ def bench_conv_detail(xs, ws, pad, dtype, dev, iters=10):
     if won.startswith("native."):
         vi = nat.variants(nat.OP_CONV).index(won[7:])
         out = torch.empty_like(y)
-        ms = event_time_ms(lambda: nat.conv3d(x, w, b, 1, pad, 1, variant=vi, out=out), iters)
+        ms = graph_time_ms(lambda: nat.conv3d(x, w, b, 1, pad, 1, variant=vi, out=out), iters)
     else:
         orig = amd_tuned_torch._ORIGINALS[(F, "conv3d")]
         ms = event_time_ms(lambda: orig(x, w, b, 1, pad), iters)
@@ -439,9 +466,9 @@ def main():
         plan += [
             ("c4_conv3d_small_fp16", lambda: bench_conv_detail((1, 64, 16, 32, 32), (64, 64, 3, 3, 3), 1, torch.float16, dev)),
             ("c4_conv3d_small_fp32", lambda: bench_conv_detail((1, 64, 16, 32, 32), (64, 64, 3, 3, 3), 1, torch.float32, dev)),
-            ("c4_conv3d_scaled_bf16", lambda: bench_conv_detail((2, 128, 16, 64, 64), (128, 128, 3, 3, 3), 1, torch.bfloat16, dev, 3)),
-            ("c5_conv3d_bf16", lambda: bench_conv_detail((1, 256, 8, 64, 64), (256, 256, 3, 3, 3), 1, torch.bfloat16, dev, 3)),
-            ("c5_conv3d_k7_fp16", lambda: bench_conv_detail((1, 64, 16, 32, 32), (64, 64, 7, 7, 7), 3, torch.float16, dev, 3)),
+            ("c4_conv3d_scaled_bf16", lambda: bench_conv_detail((2, 128, 16, 64, 64), (128, 128, 3, 3, 3), 1, torch.bfloat16, dev, 10)),
+            ("c5_conv3d_bf16", lambda: bench_conv_detail((1, 256, 8, 64, 64), (256, 256, 3, 3, 3), 1, torch.bfloat16, dev, 10)),
+            ("c5_conv3d_k7_fp16", lambda: bench_conv_detail((1, 64, 16, 32, 32), (64, 64, 7, 7, 7), 3, torch.float16, dev, 10)),
         ]
         for name, fn in plan:
             log(f"detail {name} ...")

@@ -60,10 +60,19 @@ def test_dwconv1d_all_variants(dev, case, dtype):
     nat = _native()
     x, w, b = _inputs(N, C, L, K, dtype, seed=sum(case))
     xd, wd, bd = x.to(dev), w.to(dev), b.to(dev)
+    ran = 0
     for vi, name in enumerate(nat.variants(nat.OP_DWCONV1D)):
-        y = nat.dwconv1d(xd, wd, bd, pad, l_out, variant=vi)
+        try:
+            y = nat.dwconv1d(xd, wd, bd, pad, l_out, variant=vi)
+        except nat.Unsupported:
+            # a tile variant may decline (e.g. its LDS window exceeds 64 KB for fp32);
+            # the direct kernel is the one that must take every shape
+            assert name != "direct", "the direct variant must accept every shape"
+            continue
         torch.cuda.synchronize()
         _check(y.cpu(), x, w, b, pad, l_out)
+        ran += 1
+    assert ran >= 2
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
@@ -89,8 +98,12 @@ def test_dwconv1d_misaligned_pointers(dev, dtype):
     for l_out, pad in ((L, 1), (L + 2, 2)):
         ob = torch.full((N * C * l_out + 5,), float("nan"), dtype=dtype, device=dev)
         yv = ob[3:3 + N * C * l_out].view(N, C, l_out)
-        for vi in range(len(nat.variants(nat.OP_DWCONV1D))):
-            nat.dwconv1d(xv, w.to(dev), b.to(dev), pad, l_out, variant=vi, out=yv)
+        for vi, name in enumerate(nat.variants(nat.OP_DWCONV1D)):
+            try:
+                nat.dwconv1d(xv, w.to(dev), b.to(dev), pad, l_out, variant=vi, out=yv)
+            except nat.Unsupported:
+                assert name != "direct", "the direct variant must accept every shape"
+                continue
             torch.cuda.synchronize()
             _check(yv.cpu(), x, w, b, pad, l_out)
             # the guard elements around the output view are untouched
