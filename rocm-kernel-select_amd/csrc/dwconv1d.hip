@@ -86,19 +86,41 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_lds_kernel(DwArgs a) {
   t0 = (t0 >= 0 ? t0 / VEC : -((-t0 + VEC - 1) / VEC)) * VEC;
   const int64_t I_base = t0 - a.x_off;
   const int nvec = I_hi > I_lo ? (int)((I_hi - I_base + VEC - 1) / VEC) : 0;
-  for (int v = tid; v < nvec; v += DW_NT) {
-    const int64_t gi = I_base + (int64_t)v * VEC;
-    Vec16<T> val;
-    if (gi >= 0 && gi + VEC <= a.total_in) {
-      val.raw = ld16<NTH>(x + gi);
-    } else {
+  // Every load of the window is issued before any is used: MAXV unrolled, branch-free
+  // buffer loads from a resource based at the window start (offsets stay small for any
+  // tensor size); vectors outside the window or not wholly inside the tensor take an
+  // out-of-range offset (zero) and the few partial ones are patched element-wise after.
+  // (The host guarantees nvec <= MAXV * DW_NT.)
+  constexpr int MAXV = U + 2;
+  {
+    const int64_t rem = a.total_in - I_base;  // elements from the window start to the tensor end
+    const __amdgpu_buffer_rsrc_t rx =
+        make_rsrc(x + I_base, (uint32_t)((rem < (int64_t)MAXV * DW_NT * VEC ? rem : (int64_t)MAXV * DW_NT * VEC) *
+                                         (int64_t)sizeof(T)));
+    uint4 stage[MAXV];
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        const int64_t idx = gi + e;
-        val.e[e] = (idx >= 0 && idx < a.total_in) ? x[idx] : static_cast<T>(0.0f);
-      }
+    for (int m = 0; m < MAXV; ++m) {
+      const int v = m * DW_NT + tid;
+      const int64_t gi = I_base + (int64_t)v * VEC;
+      const bool full = v < nvec && gi >= 0 && gi + VEC <= a.total_in;
+      stage[m] = bload16<NTH ? 2 : 0>(rx, full ? (uint32_t)v * 16u : kOOB, 0);
     }
-    reinterpret_cast<uint4*>(win)[v] = val.raw;
+#pragma unroll
+    for (int m = 0; m < MAXV; ++m) {
+      const int v = m * DW_NT + tid;
+      if (v >= nvec) break;
+      const int64_t gi = I_base + (int64_t)v * VEC;
+      if (!(gi >= 0 && gi + VEC <= a.total_in)) {  // partial vector at a tensor end (rare)
+        Vec16<T> val;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          const int64_t idx = gi + e;
+          val.e[e] = (idx >= 0 && idx < a.total_in) ? x[idx] : static_cast<T>(0.0f);
+        }
+        stage[m] = val.raw;
+      }
+      reinterpret_cast<uint4*>(win)[v] = stage[m];
+    }
   }
   // ---- stage per-row weights + bias (fp32) --------------------------------------------
   const int nrows = (int)(rb - ra + 1);
@@ -123,15 +145,41 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_lds_kernel(DwArgs a) {
     const int vi = u * DW_NT + tid;
     const int64_t f = F0 + (int64_t)vi * VEC;
     if (f + VEC <= Fs || f >= Fe) continue;
-    bool fast = (f >= Fs) && (f + VEC <= Fe);
+    const bool whole = (f >= Fs) && (f + VEC <= Fe);
+    bool fast = whole;
     uint32_t r_rel = 0, t = 0;
-    if (fast) {
+    if (whole) {
       const uint32_t q = ta + (uint32_t)(f - Fs);
       r_rel = fdiv(q, a.div_lout);
       t = q - r_rel * Lout;
       fast = (t + VEC <= Lout);
     }
-    if (fast) {
+    if (whole && !fast && rows_in_lds && KT > 0) {
+      // the vector crosses one row boundary (rows are not 16-byte aligned in memory when
+      // Lout % VEC != 0, e.g. the stock-shaped causal output): elements e < eb finish row
+      // r, the rest start row r+1; still one full 16-byte store
+      const uint32_t eb = Lout - t;
+      const int64_t r = ra + r_rel;
+      Vec16<T> o;
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const bool second = (uint32_t)e >= eb;
+        const float* wr = wl + (r_rel + (second ? 1u : 0u)) * per;
+        const int te = second ? e - (int)eb : (int)t + e;
+        const int s = te - pad;
+        const int pb = (int)((r + (second ? 1 : 0)) * (int64_t)L + s - I_base);
+        float acc = wr[K];
+#pragma unroll
+        for (int j = 0; j < (KT > 0 ? KT : 1); ++j) {
+          const int pos = s + j;
+          const float xv = ((unsigned)pos < L) ? to_f32(win[pb + j]) : 0.f;
+          acc = fmaf(wr[j], xv, acc);
+        }
+        if (a.silu) acc = silu_f32(acc);
+        o.e[e] = from_f32<T>(acc);
+      }
+      st16<NTH>(y + f, o.raw);
+    } else if (fast) {
       const int64_t r = ra + r_rel;
       float wk[KT > 0 ? KT : 1];
       float bv;
@@ -253,9 +301,166 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_direct_kernel(DwArgs a) {
   y[f] = from_f32<T>(acc);
 }
 
+// Register-only kernel: one 16-byte output vector per thread, no LDS, no barrier -- the
+// access pattern of a one-vector-per-thread streaming copy, which is what HBM serves best.
+// The vector's input window (VEC + K - 1 elements, starting at an arbitrary element) is
+// cut out of the NBLK aligned 16-byte blocks that cover it with a per-lane funnel shift;
+// neighbouring lanes fetch overlapping blocks, which the L1 serves.  Positions outside
+// the row read as zero (padding), which also masks anything fetched past the tensor ends
+// (those bytes stay inside the 16-byte block that holds the first / last element).  A
+// vector that crosses one row boundary (rows of a stock-shaped causal output are not
+// 16-byte aligned) uses two such windows; only partial vectors at the tensor ends are
+// computed element-wise.  Requires input and output below 2^31 elements (host check).
+template <typename T, int KT>
+struct DwWindow {
+  static constexpr int VEC = 16 / sizeof(T);
+  static constexpr int WN = VEC + KT - 1;                     // window elements
+  static constexpr int NBLK = (VEC - 1 + WN + VEC - 1) / VEC;  // blocks covering it at any start
+  // fetch: the NBLK blocks holding elements g .. g + WN - 1 (g counted from the aligned
+  // base of rx); active == false issues the loads with out-of-range offsets (zeros)
+  __device__ __forceinline__ static void fetch(__amdgpu_buffer_rsrc_t rx, int g, bool active, uint32_t* D,
+                                               int& m) {
+    const int bA = g >= 0 ? g / VEC : -((-g + VEC - 1) / VEC);
+    m = g - bA * VEC;  // 0 .. VEC-1
+#pragma unroll
+    for (int k = 0; k < NBLK; ++k) {
+      const int b = bA + k;
+      const uint4 q = bload16(rx, (active && b >= 0) ? (uint32_t)b * 16u : kOOB, 0);
+      D[4 * k] = q.x; D[4 * k + 1] = q.y; D[4 * k + 2] = q.z; D[4 * k + 3] = q.w;
+    }
+  }
+  // extract: xv[i] = element g + i, zero where the row position p0 + i is outside [0, L)
+  __device__ __forceinline__ static void extract(const uint32_t* D, int m, int p0, uint32_t L, float* xv) {
+    if constexpr (sizeof(T) == 2) {
+      // dword shift by m/2 (select), then half-dword shift by m%2 (alignbyte)
+      constexpr int NS = (WN + 1) / 2;
+      const int qd = m >> 1;
+      uint32_t Tq[NS + 1];
+#pragma unroll
+      for (int j = 0; j <= NS; ++j) {
+        const uint32_t d0 = D[j], d1 = D[j + 1], d2 = D[j + 2], d3 = D[j + 3];
+        Tq[j] = qd == 0 ? d0 : qd == 1 ? d1 : qd == 2 ? d2 : d3;
+      }
+      const bool odd = m & 1;
+#pragma unroll
+      for (int j = 0; j < NS; ++j) {
+        const uint32_t sd = odd ? __builtin_amdgcn_alignbyte(Tq[j + 1], Tq[j], 2) : Tq[j];
+        if (2 * j < WN) xv[2 * j] = to_f32(__builtin_bit_cast(T, (unsigned short)(sd & 0xffffu)));
+        if (2 * j + 1 < WN) xv[2 * j + 1] = to_f32(__builtin_bit_cast(T, (unsigned short)(sd >> 16)));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < WN; ++i) {
+        const uint32_t d0 = D[i], d1 = D[i + 1], d2 = D[i + 2], d3 = D[i + 3];
+        xv[i] = __uint_as_float(m == 0 ? d0 : m == 1 ? d1 : m == 2 ? d2 : d3);
+      }
+    }
+    if (p0 < 0 || p0 + WN > (int)L) {
+#pragma unroll
+      for (int i = 0; i < WN; ++i)
+        if ((unsigned)(p0 + i) >= L) xv[i] = 0.f;
+    }
+  }
+};
+
+template <typename T, int KT, bool NTH>
+__global__ __launch_bounds__(DW_NT) void dwconv1d_reg_kernel(DwArgs a) {
+  using Win = DwWindow<T, KT>;
+  constexpr int VEC = Win::VEC, WN = Win::WN;
+  const T* __restrict__ x = static_cast<const T*>(a.x);
+  const T* __restrict__ w = static_cast<const T*>(a.w);
+  const T* __restrict__ bias = static_cast<const T*>(a.b);
+  T* __restrict__ y = static_cast<T*>(a.y);
+  const uint32_t L = a.L, Lout = a.Lout;
+  const int pad = a.pad;
+
+  const int64_t f = ((int64_t)blockIdx.x * DW_NT + threadIdx.x) * VEC - a.y_off;
+  if (f >= a.total_out || f + VEC <= 0) return;
+  bool whole = f >= 0 && f + VEC <= a.total_out;
+  uint32_t r = 0, t = 0, eb = VEC;
+  if (whole) {
+    r = fdiv((uint32_t)f, a.div_lout);
+    t = (uint32_t)f - r * Lout;
+    // elements e < eb are row r (positions t + e); the rest, if any, start row r + 1 --
+    // which must hold them all (Lout < VEC can put a vector across several rows)
+    eb = t + VEC <= Lout ? (uint32_t)VEC : Lout - t;
+    whole = (uint32_t)VEC - eb <= Lout;
+  }
+  if (whole) {
+    const __amdgpu_buffer_rsrc_t rx =
+        make_rsrc(x - a.x_off, (uint32_t)(((int64_t)a.total_in + a.x_off + VEC - 1) / VEC * 16));
+    // the window, weights and bias loads are all issued before any is used (the bias read
+    // is branch-free: a load under a branch would be waited for inside it)
+    uint32_t DA[4 * Win::NBLK];
+    int mA;
+    Win::fetch(rx, (int)(r * L + t) - pad + a.x_off, true, DA, mA);
+    const uint32_t c = r - fdiv(r, a.div_c) * a.C;
+    const T* bsrc = bias ? bias : w;  // w has >= C elements
+    const float bscale = bias ? 1.f : 0.f;
+    T wr[KT];
+#pragma unroll
+    for (int j = 0; j < KT; ++j) wr[j] = w[c * KT + j];
+    const T br = bsrc[c];
+    float xv[WN], xw[WN], wk[KT], wk2[KT];
+    Win::extract(DA, mA, (int)t - pad, L, xv);
+#pragma unroll
+    for (int j = 0; j < KT; ++j) wk[j] = to_f32(wr[j]);
+    const float bv = to_f32(br) * bscale;
+    float bv2 = bv;
+    // a vector crossing into row r + 1 (once per row for unaligned rows): its second window
+    // and the next channel's weights are fetched here, off the common path
+    const bool split = eb < (uint32_t)VEC;
+    if (split) {
+      uint32_t DB[4 * Win::NBLK];
+      int mB;
+      Win::fetch(rx, (int)((r + 1) * L) - (int)eb - pad + a.x_off, true, DB, mB);
+      const uint32_t c2 = c + 1 == a.C ? 0u : c + 1;
+#pragma unroll
+      for (int j = 0; j < KT; ++j) wk2[j] = to_f32(w[c2 * KT + j]);
+      bv2 = to_f32(bsrc[c2]) * bscale;
+      Win::extract(DB, mB, -(int)eb - pad, L, xw);
+    }
+    Vec16<T> o;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      float acc;
+      if (!split || (uint32_t)e < eb) {
+        acc = bv;
+#pragma unroll
+        for (int j = 0; j < KT; ++j) acc = fmaf(wk[j], xv[e + j], acc);
+      } else {
+        acc = bv2;
+#pragma unroll
+        for (int j = 0; j < KT; ++j) acc = fmaf(wk2[j], xw[e + j], acc);
+      }
+      if (a.silu) acc = silu_f32(acc);
+      o.e[e] = from_f32<T>(acc);
+    }
+    st16<NTH>(y + f, o.raw);
+  } else {
+    // partial vector at a tensor end, or rows shorter than a vector
+#pragma unroll 1
+    for (int e = 0; e < VEC; ++e) {
+      const int64_t fe = f + e;
+      if (fe < 0 || fe >= a.total_out) continue;
+      const uint32_t re = fdiv((uint32_t)fe, a.div_lout);
+      const uint32_t te = (uint32_t)fe - re * Lout;
+      const uint32_t ce = re - fdiv(re, a.div_c) * a.C;
+      float acc = bias ? to_f32(bias[ce]) : 0.f;
+      const int se = (int)te - pad;
+      for (int j = 0; j < KT; ++j) {
+        const int pos = se + j;
+        if ((unsigned)pos < L) acc = fmaf(to_f32(w[ce * KT + j]), to_f32(x[(int64_t)re * L + pos]), acc);
+      }
+      if (a.silu) acc = silu_f32(acc);
+      y[fe] = from_f32<T>(acc);
+    }
+  }
+}
+
 struct DwVariant {
   const char* name;
-  int opt;  // outputs per thread; 0 = direct kernel
+  int opt;  // outputs per thread; 0 = direct kernel, -1 = register kernel (one vector)
   bool nt;  // nontemporal loads/stores
 };
 
@@ -267,6 +472,8 @@ const DwVariant kDwVariants[] = {
     {"lds_opt16_nt", 16, true},
     {"lds_opt32_nt", 32, true},
     {"lds_opt64_nt", 64, true},
+    {"reg_nt", -1, true},
+    {"reg", -1, false},
 };
 constexpr int kNumDw = sizeof(kDwVariants) / sizeof(kDwVariants[0]);
 
@@ -291,10 +498,27 @@ int launch_lds_k(const DwArgs& a, size_t shmem, hipStream_t s) {
   }
 }
 
+template <typename T, bool NTH>
+int launch_reg(const DwArgs& a, hipStream_t s) {
+  constexpr int VEC = 16 / sizeof(T);
+  if (a.total_out + a.y_off >= (1ll << 31) - VEC || a.total_in + a.x_off >= (1ll << 31) / (int64_t)sizeof(T) - VEC)
+    return fail(ATK_UNSUPPORTED, "dwconv1d: tensor too large for the register kernel");
+  const int64_t nblk = (a.total_out + a.y_off + (int64_t)DW_NT * VEC - 1) / ((int64_t)DW_NT * VEC);
+  switch (a.K) {
+    case 2: hipLaunchKernelGGL((dwconv1d_reg_kernel<T, 2, NTH>), dim3((unsigned)nblk), dim3(DW_NT), 0, s, a); break;
+    case 3: hipLaunchKernelGGL((dwconv1d_reg_kernel<T, 3, NTH>), dim3((unsigned)nblk), dim3(DW_NT), 0, s, a); break;
+    case 4: hipLaunchKernelGGL((dwconv1d_reg_kernel<T, 4, NTH>), dim3((unsigned)nblk), dim3(DW_NT), 0, s, a); break;
+    case 5: hipLaunchKernelGGL((dwconv1d_reg_kernel<T, 5, NTH>), dim3((unsigned)nblk), dim3(DW_NT), 0, s, a); break;
+    default: return fail(ATK_UNSUPPORTED, "dwconv1d: register kernel serves K in [2, 5]");
+  }
+  return check_launch("dwconv1d_reg_kernel");
+}
+
 template <typename T>
 int launch_dw(DwArgs a, int variant, hipStream_t s) {
   constexpr int VEC = 16 / sizeof(T);
   const int opt = kDwVariants[variant].opt;
+  if (opt < 0) return kDwVariants[variant].nt ? launch_reg<T, true>(a, s) : launch_reg<T, false>(a, s);
   if (opt == 0 || opt < VEC) {
     const int64_t nblk = (a.total_out + DW_NT - 1) / DW_NT;
     if (nblk > 0x7fffffff) return fail(ATK_UNSUPPORTED, "dwconv1d: grid too large");
@@ -310,6 +534,8 @@ int launch_dw(DwArgs a, int variant, hipStream_t s) {
   need = (need + VEC - 1) / VEC * VEC;
   const size_t shmem = (size_t)need * sizeof(T) + (size_t)DW_MAXR * (a.K + 1) * sizeof(float);
   if (shmem > 64 * 1024) return fail(ATK_UNSUPPORTED, "dwconv1d: LDS window too large for variant");
+  if (need / VEC > (int64_t)(opt / VEC + 2) * DW_NT)  // the kernel stages at most MAXV vectors per thread
+    return fail(ATK_UNSUPPORTED, "dwconv1d: LDS window needs more loads per thread than the variant issues");
   a.win_cap = (int)need;
   if (kDwVariants[variant].nt) {
     switch (opt) {
