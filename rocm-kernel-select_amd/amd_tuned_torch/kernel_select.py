@@ -245,6 +245,12 @@ def _key(kind, input, weight, stride, padding, dilation):
             _norm(padding), _norm(dilation), channels_last)
 
 
+# GPU spin queued ahead of the timed runs (clock cycles): long enough for the host to enqueue
+# every timed call before the GPU reaches the first event, so each event pair brackets GPU
+# time only -- otherwise a kernel shorter than the Python dispatch is timed as the dispatch.
+_LEAD_CYCLES = 2_000_000
+
+
 def _time(fn) -> Optional[float]:
     """Minimum over _ITERS individually event-timed runs, after _WARMUP runs; None if the
     candidate declines or raises a Runtime/Type/AssertionError."""
@@ -255,6 +261,8 @@ def _time(fn) -> Optional[float]:
         torch.cuda.synchronize()
         pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
                  for _ in range(_ITERS)]
+        if _LEAD_CYCLES and hasattr(torch.cuda, "_sleep"):
+            torch.cuda._sleep(_LEAD_CYCLES)
         for a, b in pairs:
             a.record()
             fn()
