@@ -152,8 +152,9 @@ def test_conv3d_contest_over_native_variants_then_cached(monkeypatch, contest):
     monkeypatch.setattr(_dispatch, "_conv_candidates",
                         (lambda orig: (lambda *a: _tag(orig(*a))))(_dispatch._conv_candidates))
     contest.update({"native.h_a": 3.0, "native.h_b": 1.0, "stock": 2.0})
-    x = torch.randn(1, 4, 4, 5, 6).half()
-    w = torch.randn(4, 4, 3, 3, 3).half()
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(1, 4, 4, 5, 6, generator=g).half()
+    w = torch.randn(4, 4, 3, 3, 3, generator=g).half()
     with torch.no_grad():
         y = F.conv3d(x.float(), w.float(), None, 1, 1).half()  # fp32 path: only f32_ variants
     fake.calls.clear()
@@ -166,7 +167,7 @@ def test_conv3d_contest_over_native_variants_then_cached(monkeypatch, contest):
     fake.calls.clear()
     F.conv3d(x32, w32, None, 1, 1)
     assert fake.calls == [("conv3d", "f32_c")]       # cached: straight to the winner
-    assert torch.allclose(out, y.float(), atol=1e-2)
+    assert torch.allclose(out, y.float(), atol=1e-2, rtol=2e-3)  # y went through fp16 rounding
 
 
 def test_conv3d_cached_winner_declining_is_recontested(monkeypatch, contest):
