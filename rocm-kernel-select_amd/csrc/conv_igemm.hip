@@ -86,12 +86,13 @@ __device__ __forceinline__ void mfma_block(f32x16& acc, const uint4& a, const ui
 // per-element bounds test; readers add mis = ix0 - gx0.  Chunk c maps to (row-chunk
 // rc = c / CB, channel cl = c % CB): consecutive lanes write consecutive channels of one
 // patch position.
-template <typename T, int CB, bool VR>
+template <typename T, int CB, bool VR, int NTH = 256>
 struct PatchLoader {
   static constexpr int VEC = 16 / sizeof(T);
-  // chunks per thread held for the next stage: CB/4 for 16-bit types, CB/2 for fp32 (the host
-  // plan rejects tiles whose patch needs more)
-  static constexpr int MAXC = sizeof(T) == 2 ? CB / 4 : CB / 2;
+  // chunks per thread held for the next stage: CB/4 for 16-bit types, CB/2 for fp32, at 256
+  // threads per workgroup (scaled up for smaller workgroups; the host plan rejects tiles whose
+  // patch needs more)
+  static constexpr int MAXC = (sizeof(T) == 2 ? CB / 4 : CB / 2) * (256 / NTH);
   uint4 buf[MAXC];
 
   // rsrc covers sample n of the input; iz may be out of range (a padding plane)
@@ -344,7 +345,7 @@ __attribute__((amdgpu_waves_per_eu(FCO * FSP >= 8 && CB == 16 ? 2 : 1))) void co
   const int ntaps2d = a.KH * a.KW;
   const int co_blk0 = co_tile * (BN / 32) + wco * FCO;
 
-  PatchLoader<T, CB, VR> ld;
+  PatchLoader<T, CB, VR, NT> ld;
   const int total_quads = total_chunks / 4;
   if constexpr (VR) ld.init(a, iy0, gx0, total_quads, tid, NT);
   // stage s = (channel chunk cc, kernel plane kd), walked incrementally
@@ -356,9 +357,9 @@ __attribute__((amdgpu_waves_per_eu(FCO * FSP >= 8 && CB == 16 ? 2 : 1))) void co
       const uint32_t so = ld.stage_off(a, cc, iz);
       const int lim = ld.stage_lim(a, cc, iz, true);
 #pragma unroll
-      for (int u = 0; u < PatchLoader<T, CB, VR>::MAXC; ++u) ld.load_fast(rx, u, so, lim);
+      for (int u = 0; u < PatchLoader<T, CB, VR, NT>::MAXC; ++u) ld.load_fast(rx, u, so, lim);
 #pragma unroll
-      for (int g = 0; g < PatchLoader<T, CB, VR>::NQ; ++g)
+      for (int g = 0; g < PatchLoader<T, CB, VR, NT>::NQ; ++g)
         ld.store_quad(reinterpret_cast<T*>(lds_bytes), g, total_quads, tid, NT);
     } else {
       ld.load(a, rx, cc, iz_base + kd * a.dd, iy0, gx0, total_chunks, tid, NT);
@@ -390,12 +391,15 @@ __attribute__((amdgpu_waves_per_eu(FCO * FSP >= 8 && CB == 16 ? 2 : 1))) void co
     // prefetching PF taps ahead; only PF + 1 of them are live at once
     constexpr int NB = NT2 % 3 == 0 ? 3 : NT2 % 5 == 0 ? 5 : 7;
     constexpr int PF = NB - 1 < 3 ? NB - 1 : 3;
-    constexpr int MAXC = PatchLoader<T, CB, VR>::MAXC;
-    constexpr int NQ = PatchLoader<T, CB, VR>::NQ;
+    constexpr int MAXC = PatchLoader<T, CB, VR, NT>::MAXC;
+    constexpr int NQ = PatchLoader<T, CB, VR, NT>::NQ;
     static_assert(NT2 % NB == 0, "buffer rotation must repeat every stage");
-    static_assert(NQ >= 1 && NQ <= 2 && NT2 >= 9, "schedule below assumes <= 2 quads, 9+ taps");
-    // quad g (chunks 4g..4g+3, issued by tap 2g+1) is written at tap QS0 + 3g
-    constexpr int QS0 = 5, QS1 = NQ > 1 ? 8 : -1;
+    static_assert(NQ >= 1 && NQ <= 4 && NT2 >= 9, "schedule below assumes <= 4 quads, 9+ taps");
+    // chunks are issued LPT per tap over taps 0-3; quads [0, QH) are written at tap QS0 (their
+    // chunks issued by tap 1), quads [QH, NQ) at tap QS1 (chunks issued by tap 3)
+    constexpr int LPT = MAXC <= 8 ? 2 : MAXC / 4;
+    constexpr int QH = (NQ + 1) / 2;
+    constexpr int QS0 = 5, QS1 = 8;
     uint4 wb[NB][NKB][FCO];
     auto load_w = [&](uint4 (&w)[NKB][FCO], uint32_t so) {
 #pragma unroll
@@ -426,9 +430,10 @@ __attribute__((amdgpu_waves_per_eu(FCO * FSP >= 8 && CB == 16 ? 2 : 1))) void co
       for (int t2 = 0; t2 < NT2; ++t2) {
         const int tp = t2 + PF;
         load_w(wb[tp % NB], tp < NT2 ? wb_cur + tp * tap_bytes : wb_nxt + (tp - NT2) * tap_bytes);
-        if (2 * t2 < MAXC) {
-          ld.load_fast(rx, 2 * t2, so1, lim1);
-          ld.load_fast(rx, 2 * t2 + 1, so1, lim1);
+        if (t2 < 4) {
+#pragma unroll
+          for (int l = 0; l < LPT; ++l)
+            if (t2 * LPT + l < MAXC) ld.load_fast(rx, t2 * LPT + l, so1, lim1);
         }
         if (zin) {
           const uint32_t toffb = (uint32_t)(t2 / KWT) * kh_step + (uint32_t)(t2 % KWT) * kw_step;
@@ -446,9 +451,11 @@ __attribute__((amdgpu_waves_per_eu(FCO * FSP >= 8 && CB == 16 ? 2 : 1))) void co
           }
         }
         // the idle buffer was released by every wave at the previous stage's barrier
-        if ((t2 == QS0 || t2 == QS1) && has_next)  // QS1 < 0: single quad
-          ld.store_quad(reinterpret_cast<T*>(lds_bytes + (pbuf ^ patch_bytes)), t2 == QS0 ? 0 : 1,
-                        total_quads, tid, NT);
+        if ((t2 == QS0 || t2 == QS1) && has_next) {
+#pragma unroll
+          for (int g = (t2 == QS0 ? 0 : QH); g < (t2 == QS0 ? QH : NQ); ++g)
+            ld.store_quad(reinterpret_cast<T*>(lds_bytes + (pbuf ^ patch_bytes)), g, total_quads, tid, NT);
+        }
       }
       __syncthreads();
       cc = cc1;
@@ -470,7 +477,7 @@ __attribute__((amdgpu_waves_per_eu(FCO * FSP >= 8 && CB == 16 ? 2 : 1))) void co
       const uint32_t so1 = __builtin_amdgcn_readfirstlane(ld.stage_off(a, cc1, iz1));
       const int lim1 = __builtin_amdgcn_readfirstlane(ld.stage_lim(a, cc1, iz1, has_next));
 #pragma unroll
-      for (int u = 0; u < PatchLoader<T, CB, VR>::MAXC; ++u) ld.load_fast(rx, u, so1, lim1);
+      for (int u = 0; u < PatchLoader<T, CB, VR, NT>::MAXC; ++u) ld.load_fast(rx, u, so1, lim1);
     } else {
       ld.load(a, rx, cc1, iz_base + kd1 * a.dd, iy0, gx0, total_chunks, tid, NT, has_next);
     }
@@ -523,7 +530,7 @@ __attribute__((amdgpu_waves_per_eu(FCO * FSP >= 8 && CB == 16 ? 2 : 1))) void co
     if (has_next) {
       if constexpr (VR) {
 #pragma unroll
-        for (int g = 0; g < PatchLoader<T, CB, VR>::NQ; ++g)
+        for (int g = 0; g < PatchLoader<T, CB, VR, NT>::NQ; ++g)
           ld.store_quad(reinterpret_cast<T*>(lds_bytes + (pbuf ^ patch_bytes)), g, total_quads, tid, NT);
       } else {
         ld.store(a, reinterpret_cast<T*>(lds_bytes + (pbuf ^ patch_bytes)), total_chunks, tid, NT);
@@ -610,7 +617,7 @@ __global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm2_kernel(IgArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  PatchLoader<T, CB, VR> ld;
+  PatchLoader<T, CB, VR, NT> ld;
   uint4 wbuf[WMAX];
   // global byte offset of weight chunk w of stage (cc, kd, rg)
   auto load_stage = [&](int s, bool valid) {
@@ -818,7 +825,7 @@ int plan_ig(const ConvShape& p, int v, IgPlan& pl) {
     a.patch_elems = a.PY * a.PXS * (vr.cb + VEC);
     a.w_stage_frags = vr.family == 2 ? rps * p.KW * (vr.cb / KB) * (pl.bn / 32) : 0;
     pl.lds = (size_t)2 * a.patch_elems * es + (size_t)2 * a.w_stage_frags * frag;
-    const int maxc = f32 ? vr.cb / 2 : vr.cb / 4;  // chunks a thread holds (PatchLoader::MAXC)
+    const int maxc = (f32 ? vr.cb / 2 : vr.cb / 4) * (256 / pl.nthreads);  // PatchLoader::MAXC
     const bool fits = pl.lds <= 150 * 1024 && vr.cb * a.PY * a.NCX <= maxc * pl.nthreads &&
                       a.w_stage_frags * 64 <= IG2_WMAX * pl.nthreads;
     if (fits) break;
