@@ -217,9 +217,44 @@ def bench_conv_detail(xs, ws, pad, dtype, dev, iters=20):
     flops = 2.0 * xs[0] * ws[0] * osp * ws[1] * math.prod(ws[2:])
     tf = flops / (ms * 1e-3) / 1e12
     key = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[dtype]
-    return {"ms": round(ms, 4), "TFLOP/s": round(tf, 2),
-            "roofline_frac": round(tf / MFMA_PEAK_TFLOPS[key], 4), "variant": won,
-            "max_rel_err_vs_stock_fp32": float(f"{err:.3g}")}
+    res = {"ms": round(ms, 4), "TFLOP/s": round(tf, 2),
+           "roofline_frac": round(tf / MFMA_PEAK_TFLOPS[key], 4), "variant": won,
+           "max_rel_err_vs_stock_fp32": float(f"{err:.3g}")}
+    if dtype != torch.float32:
+        # the same GEMM (M = output positions, N = Co, K = Ci*k^3) through torch.matmul
+        # (hipBLASLt), operands already laid out: what a library GEMM does without the gather
+        M, N, K = xs[0] * osp, ws[0], fan_in
+        del x, w, y
+        a = torch.randn(M, K, device=dev).to(dtype)
+        bt = torch.randn(N, K, device=dev).to(dtype)
+        gms = graph_time_ms(lambda: a @ bt.t(), iters)
+        res["same_gemm_torch_matmul_TFLOP/s"] = round(2.0 * M * N * K / (gms * 1e-3) / 1e12, 2)
+    return res
+
+
+def calibration(dev):
+    """Achievable ceilings on this box: a large bf16 GEMM through torch.matmul (hipBLASLt),
+    and torch's device copy at the tensor sizes the HBM-bound configs move."""
+    import torch
+    out = {}
+    n = 8192
+    a = torch.randn(n, n, device=dev).to(torch.bfloat16)
+    bt = torch.randn(n, n, device=dev).to(torch.bfloat16)
+    ms = graph_time_ms(lambda: a @ bt.t(), 10)
+    out["gemm_bf16_8192^3_TFLOP/s"] = round(2.0 * n ** 3 / (ms * 1e-3) / 1e12, 1)
+    del a, bt
+    copies = {}
+    for label, numel in (("c2_537MB", 16 * 2048 * 8192), ("c3a_33.5MB", 8 * 512 * 64 * 64),
+                         ("c3b_67MB", 512 * 16 * 64 * 64), ("c5_16.8MB", 256 * 8 * 64 * 64)):
+        src = torch.randn(numel, device=dev).to(torch.bfloat16)
+        dst = torch.empty_like(src)
+        ms = graph_time_ms(lambda: dst.copy_(src), 20)
+        copies[label] = {"us": round(ms * 1e3, 2),
+                         "GB/s": round(2 * numel * 2 / (ms * 1e-3) / 1e9, 1)}
+        del src, dst
+    out["torch_copy_bf16"] = copies
+    torch.cuda.empty_cache()
+    return out
 
 
 # ---------------------------------------------------------------------------
@@ -423,7 +458,9 @@ def main():
 
     if won.startswith("native."):
         kms = dw_kernel_ms(x, w, b, 3, L + 3, won[7:], iters=max(20, args.steps))
-        kernel_name = "dwconv1d_lds_kernel" if won[7:].startswith("lds") else "dwconv1d_direct_kernel"
+        kernel_name = ("dwconv1d_lds_kernel" if won[7:].startswith("lds") else
+                       "dwconv1d_reg_kernel" if won[7:].startswith("reg") else
+                       "dwconv1d_direct_kernel")
     else:
         kms = event_time_ms(lambda: step(), 20)
         kernel_name = "stock"
@@ -470,6 +507,7 @@ def main():
             ("c5_conv3d_bf16", lambda: bench_conv_detail((1, 256, 8, 64, 64), (256, 256, 3, 3, 3), 1, torch.bfloat16, dev, 10)),
             ("c5_conv3d_k7_fp16", lambda: bench_conv_detail((1, 64, 16, 32, 32), (64, 64, 7, 7, 7), 3, torch.float16, dev, 10)),
         ]
+        plan.append(("calibration", lambda: calibration(dev)))
         for name, fn in plan:
             log(f"detail {name} ...")
             try:

@@ -104,6 +104,27 @@ __device__ __forceinline__ void wave_merge(int NS, int64_t slice, int64_t E, Get
   var = wave_sum(m2) / (float)E;
 }
 
+// The dword holding element i of a gamma/beta array of n elements (dtype pdt; p may be
+// null or 2-byte aligned), loaded through a resource that covers the array rounded out to
+// whole dwords: unconditional, branch-free, and out-of-range (or null) reads return 0.
+// `sel` says which half holds a 16-bit element.
+__device__ __forceinline__ uint32_t param_word(const void* p, int pdt, int64_t i, int64_t n, uint32_t& sel) {
+  const uint32_t es = pdt == ATK_F32 ? 4u : 2u;
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(p);
+  const uint32_t mis = (uint32_t)(addr & 3u);
+  const uint32_t bytes = p ? (uint32_t)(((int64_t)mis + n * es + 3) & ~(int64_t)3) : 0u;
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(reinterpret_cast<const void*>(addr - mis), bytes);
+  const uint32_t off = mis + (uint32_t)i * es;
+  sel = off & 2u;
+  return __builtin_amdgcn_raw_buffer_load_b32(r, (int)(off & ~3u), 0, 0);
+}
+
+__device__ __forceinline__ float param_decode(uint32_t w, uint32_t sel, int pdt) {
+  if (pdt == ATK_F32) return __uint_as_float(w);
+  const unsigned short h = (unsigned short)(sel ? (w >> 16) : (w & 0xffffu));
+  return pdt == ATK_F16 ? (float)__builtin_bit_cast(_Float16, h) : (float)__builtin_bit_cast(__bf16, h);
+}
+
 // scale/shift of absolute channel `c` given the group statistics
 __device__ __forceinline__ void channel_affine(const GnArgs& a, int64_t c, float mean, float rstd,
                                                float& sc, float& sh) {
@@ -129,11 +150,6 @@ __device__ __forceinline__ uint4 normalize_vec(const Vec16<T>& in, float sc, flo
 // ---------------------------------------------------------------------------------------
 // Register-resident single pass.  Requires S % VEC == 0 and 16B-aligned x / y (host check).
 // ---------------------------------------------------------------------------------------
-// Statistics of one slice of a group: sum, mean, then the sum of squared deviations, in
-// the order i = 0..EPV-1 (vector i of this thread = element s0 + (i*NT + tid)*VEC), k =
-// 0..VEC-1, with plain adds and explicit fmas, then fixed-order block reductions.  The
-// owner runs it on its registers (FROM_REG), a workgroup standing in for a late owner
-// runs it on memory with rolled loops; the arithmetic, and so every bit, is the same.
 // Opaque to the optimiser: keeps it from holding all VEC*EPV elements converted to fp32
 // across phases (that doubles the registers and spills); reconverting is a few VALU ops.
 template <typename T, int EPV>
@@ -143,108 +159,85 @@ __device__ __forceinline__ void reg_fence(Vec16<T>* buf) {
     asm volatile("" : "+v"(buf[i].raw.x), "+v"(buf[i].raw.y), "+v"(buf[i].raw.z), "+v"(buf[i].raw.w));
 }
 
+// Statistics of one slice of a group, in one pass over the data as it arrives.  Each thread
+// accumulates d = x - K, sum d and sum d^2, about K = its own first element, and turns them
+// into its (n_t, mean_t, M2_t = sum d^2 - (sum d)^2 / n_t); K being one of its values bounds
+// the cancellation (sum d^2 <= (n_t + 1) M2_t).  The block then merges the threads exactly:
+// mean = sum n_t mean_t / n, M2 = sum M2_t + n_t (mean_t - mean)^2.  Element order is
+// i = 0..EPV-1 (vector i of this thread = element s0 + (i*NT + tid)*VEC), k = 0..VEC-1, with
+// plain adds and explicit fmas, then fixed-order block reductions.  The owner runs it on its
+// registers (FROM_REG), a workgroup standing in for a late owner runs it on memory with
+// rolled loops; the arithmetic, and so every bit, is the same.
 template <typename T, int NT, int EPV, bool FROM_REG>
 __device__ __forceinline__ void slice_stats(Vec16<T>* buf, const T* xg, int64_t s0, int64_t E,
                                             int64_t slice, float* red, float& mean_l, float& m2) {
   constexpr int VEC = 16 / sizeof(T);
   const int tid = threadIdx.x;
+  const int64_t nv = (E - s0) / VEC;  // vectors from s0 to the group end (E % VEC == 0)
+  auto valid = [&](int i) { return (int64_t)i * NT + tid < nv; };
   auto get = [&](int i) -> Vec16<T> {
     if constexpr (FROM_REG) {
       return buf[i];
     } else {
       Vec16<T> v;
-      const int64_t e = s0 + ((int64_t)i * NT + tid) * VEC;
-      if (e < E) v.raw = *reinterpret_cast<const uint4*>(xg + e);
+      if (valid(i)) v.raw = *reinterpret_cast<const uint4*>(xg + s0 + ((int64_t)i * NT + tid) * VEC);
       else v.raw = make_uint4(0u, 0u, 0u, 0u);
       return v;
     }
   };
-  float sum = 0.f;
-  if constexpr (FROM_REG) {
+  // vector 0 is the thread's first; a thread without it has no element in the slice
+  const float K = to_f32(get(0).e[0]);
+  float s1 = 0.f, s2 = 0.f;
+  int nvt = 0;
+  // branch-free: a vector past the group end reads as zeros and is shifted by 0, so it adds
+  // exactly nothing.  On registers, vector i is fenced together with the running sums: it
+  // is converted only after vector i-1 is accumulated (left free, the compiler converts
+  // every vector up front and spills the fp32 copies).
+  auto acc = [&](int i) {
+    const bool ok = valid(i);
+    const float Ki = ok ? K : 0.f;
+    if constexpr (FROM_REG)
+      asm volatile("" : "+v"(buf[i].raw.x), "+v"(buf[i].raw.y), "+v"(buf[i].raw.z), "+v"(buf[i].raw.w),
+                   "+v"(s1), "+v"(s2));
+    const Vec16<T> v = get(i);
 #pragma unroll
-    for (int i = 0; i < EPV; ++i) {
-      const Vec16<T> v = get(i);
-#pragma unroll
-      for (int k = 0; k < VEC; ++k) sum += to_f32(v.e[k]);  // lanes past the group hold +0
+    for (int k = 0; k < VEC; ++k) {
+      const float d = to_f32(v.e[k]) - Ki;
+      s1 += d;
+      s2 = fmaf(d, d, s2);
     }
-  } else {
-#pragma unroll 1
-    for (int i = 0; i < EPV; ++i) {
-      const Vec16<T> v = get(i);
-#pragma unroll
-      for (int k = 0; k < VEC; ++k) sum += to_f32(v.e[k]);
-    }
-  }
-  const int64_t n_l = (E - s0) < slice ? (E - s0) : slice;
-  sum = block_sum<NT>(sum, red);
-  mean_l = sum / (float)n_l;
-  if constexpr (FROM_REG) reg_fence<T, EPV>(buf);
-  float q = 0.f;
-  auto dev2 = [&](int i) {
-    const int64_t e = s0 + ((int64_t)i * NT + tid) * VEC;
-    if (e < E) {
-      const Vec16<T> v = get(i);
-#pragma unroll
-      for (int k = 0; k < VEC; ++k) {
-        const float d = to_f32(v.e[k]) - mean_l;
-        q = fmaf(d, d, q);
-      }
-    }
+    nvt += ok ? 1 : 0;
   };
   if constexpr (FROM_REG) {
 #pragma unroll
-    for (int i = 0; i < EPV; ++i) dev2(i);
+    for (int i = 0; i < EPV; ++i) acc(i);
   } else {
 #pragma unroll 1
-    for (int i = 0; i < EPV; ++i) dev2(i);
+    for (int i = 0; i < EPV; ++i) acc(i);
   }
-  m2 = block_sum<NT>(q, red);
+  const float nt = (float)(nvt * VEC);
+  float mean_t = 0.f, m2_t = 0.f;
+  if (nvt > 0) {
+    const float q = s1 / nt;
+    mean_t = K + q;
+    m2_t = fmaxf(fmaf(-s1, q, s2), 0.f);
+  }
+  const int64_t n_l = (E - s0) < slice ? (E - s0) : slice;
+  mean_l = block_sum<NT>(nt * mean_t, red) / (float)n_l;
+  const float dm = mean_t - mean_l;
+  m2 = block_sum<NT>(fmaf(nt * dm, dm, m2_t), red);
   if constexpr (FROM_REG) reg_fence<T, EPV>(buf);
 }
 
 // ---------------------------------------------------------------------------------------
 // Register-resident single pass.  Requires S % VEC == 0 and 16B-aligned x / y (host check).
 // ---------------------------------------------------------------------------------------
-// Statistics of slice `s` of a group, read from `get(i)` (the i-th 16-byte vector of this
-// thread: element s0 + (i*NT + tid)*VEC).  Both the owner (from registers) and a workgroup
-// standing in for a late owner (from memory) run this same arithmetic: plain sums and
-// explicit fmas in a fixed order, fixed-order block reductions.
-template <typename T, int NT, int EPV, typename Get>
-__device__ __forceinline__ void slice_stats(Get get, int64_t s0, int64_t E, int64_t slice, float* red,
-                                            float& mean_l, float& m2) {
-  constexpr int VEC = 16 / sizeof(T);
-  const int tid = threadIdx.x;
-  float sum = 0.f;
-#pragma unroll
-  for (int i = 0; i < EPV; ++i) {
-    const Vec16<T> v = get(i);
-#pragma unroll
-    for (int k = 0; k < VEC; ++k) sum += to_f32(v.e[k]);  // lanes past the group hold +0
-  }
-  const int64_t n_l = (E - s0) < slice ? (E - s0) : slice;
-  sum = block_sum<NT>(sum, red);
-  mean_l = sum / (float)n_l;
-  float q = 0.f;
-#pragma unroll
-  for (int i = 0; i < EPV; ++i) {
-    const int64_t e = s0 + ((int64_t)i * NT + tid) * VEC;
-    if (e < E) {
-      const Vec16<T> v = get(i);
-#pragma unroll
-      for (int k = 0; k < VEC; ++k) {
-        const float d = to_f32(v.e[k]) - mean_l;
-        q = fmaf(d, d, q);
-      }
-    }
-  }
-  m2 = block_sum<NT>(q, red);
-}
-
-// ---------------------------------------------------------------------------------------
-// Register-resident single pass.  Requires S % VEC == 0 and 16B-aligned x / y (host check).
-// ---------------------------------------------------------------------------------------
+// Up to 16 vectors per thread fit 128 VGPRs: four waves per SIMD, so two 512-thread (or
+// four 256-thread) workgroups share a CU -- left alone, the fp16 build of EPV = 16 takes
+// 144 and halves the residency that a multi-slice launch relies on.
 template <typename T, int NT, int EPV>
-__global__ __launch_bounds__(NT) void gn_resident_kernel(GnArgs a) {
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(EPV <= 16 ? 4 : 1)))
+void gn_resident_kernel(GnArgs a) {
   constexpr int VEC = 16 / sizeof(T);
   __shared__ float red[NT / 64];
   __shared__ float s_stat[2];
@@ -272,22 +265,34 @@ __global__ __launch_bounds__(NT) void gn_resident_kernel(GnArgs a) {
 #pragma unroll
   for (int i = 0; i < EPV; ++i) buf[i].raw = bload16<2>(rx, voff(i), soff(i));
 
-  // gamma/beta of the channels this slice spans (group-local [c_lo, c_hi)) are fetched now,
-  // while x is in flight, and turned into scale/shift once the statistics are known.
+  // gamma/beta of the channels this slice spans (group-local [c_lo, c_hi)): thread t fetches
+  // channel t now, while x is in flight, with unconditional buffer loads that nothing waits
+  // for until the statistics are done (a plain load here is waited for with vmcnt(0), which
+  // also waits for every x load and keeps the sums from overlapping their arrival).
   const int64_t last = (s0 + a.slice < E ? s0 + a.slice : E) - 1;
   const uint32_t c_lo = fdiv((uint32_t)s0, a.div_s);
   const uint32_t c_hi = fdiv((uint32_t)last, a.div_s) + 1;
   const int nch = (int)(c_hi - c_lo);
   const int64_t cabs0 = (int64_t)(gi % a.G) * a.cpg + c_lo;  // absolute channel of c_lo
   const bool staged = nch <= GN_MAX_AFF;
+  const int64_t nchan = (int64_t)a.G * a.cpg;
+  const int64_t cme = cabs0 + (tid < nch ? tid : 0);
+  uint32_t gsel, bsel;
+  const uint32_t gword = param_word(a.gamma, a.pdt, cme, nchan, gsel);
+  const uint32_t bword = param_word(a.beta, a.pdt, cme, nchan, bsel);
+
+  float mean_l, m2;
+  slice_stats<T, NT, EPV, true>(buf, xg, s0, E, a.slice, red, mean_l, m2);
   if (staged) {
-    for (int i = tid; i < nch; i += NT) {
+    if (tid < nch) {
+      aff[tid] = a.gamma ? param_decode(gword, gsel, a.pdt) : 1.f;
+      aff[GN_MAX_AFF + tid] = a.beta ? param_decode(bword, bsel, a.pdt) : 0.f;
+    }
+    for (int i = tid + NT; i < nch; i += NT) {
       aff[i] = a.gamma ? load_param(a.gamma, a.pdt, cabs0 + i) : 1.f;
       aff[GN_MAX_AFF + i] = a.beta ? load_param(a.beta, a.pdt, cabs0 + i) : 0.f;
     }
   }
-  float mean_l, m2;
-  slice_stats<T, NT, EPV, true>(buf, xg, s0, E, a.slice, red, mean_l, m2);
 
   float mean, var;
   if (a.NS == 1) {
@@ -391,6 +396,9 @@ __global__ __launch_bounds__(NT) void gn_resident_kernel(GnArgs a) {
     asm volatile("" : "+v"(tid_s));
 #pragma unroll
     for (int i = 0; i < EPV; ++i) {
+      // vector i is unpacked only after store i-1 has issued: left free, the fp16 build
+      // splits every packed pair up front and spills the halves
+      reg_fence<T, 1>(&buf[i]);
       const bool ok = (uint32_t)(i * NT + tid_s) < n_vec;
       const int64_t e = ok ? s0 + ((int64_t)i * NT + tid_s) * VEC : s0;
       const int cl = (int)(fdiv((uint32_t)e, a.div_s) - c_lo);

@@ -256,6 +256,29 @@ def test_oom_in_candidate_declines_but_other_errors_propagate(monkeypatch, timin
         ks.pick("conv2d", x, w, s, p, d, [("native.a", bug), stock])
 
 
+def test_runoff_reranks_close_finishers_by_interleaved_median(monkeypatch, timings):
+    """Candidates within the runoff band of the fastest are re-timed together and the
+    median order wins; a candidate outside the band is not re-timed."""
+    timings({"native.a": 1.00, "native.b": 1.03, "native.c": 1.50, "stock": 3.0})
+    seen = []
+
+    def fake_interleaved(fns):
+        seen.append([f._name for f in fns])
+        return [{"native.a": 1.2, "native.b": 1.1}[f._name] for f in fns]
+    monkeypatch.setattr(ks, "_time_interleaved", fake_interleaved)
+    x, w, s, p, d = args()
+    out = ks.pick("conv2d", x, w, s, p, d, cands(["native.a", "native.b", "native.c", "stock"]))
+    assert out == "out:native.b"
+    assert seen == [["native.a", "native.b"]]
+
+
+def test_runoff_keeps_first_round_order_when_retiming_fails(monkeypatch, timings):
+    timings({"native.a": 1.00, "native.b": 1.01, "stock": 3.0})
+    monkeypatch.setattr(ks, "_time_interleaved", lambda fns: None)
+    x, w, s, p, d = args()
+    assert ks.pick("conv2d", x, w, s, p, d, cands(["native.a", "native.b", "stock"])) == "out:native.a"
+
+
 def test_time_reports_none_for_decliners_and_errors():
     assert ks._time(lambda: None) is None
 
