@@ -70,6 +70,25 @@ __device__ __forceinline__ uint4 ld16(const void* p) {
   }
   return r;
 }
+// 16 bytes of T from VEC = 16 / sizeof(T) fp32 values, round-to-nearest-even, converted in
+// pairs (v_cvt_pk_bf16_f32 for bf16) rather than one element at a time.
+template <typename T>
+__device__ __forceinline__ uint4 pack16(const float* v) {
+  if constexpr (sizeof(T) == 4) {
+    return make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3]));
+  } else {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef T t2 __attribute__((ext_vector_type(2)));
+    uint32_t d[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f2 pr = {v[2 * i], v[2 * i + 1]};
+      d[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(pr, t2));
+    }
+    return make_uint4(d[0], d[1], d[2], d[3]);
+  }
+}
+
 template <bool NT>
 __device__ __forceinline__ void st16(void* p, uint4 r) {
   if (NT) {

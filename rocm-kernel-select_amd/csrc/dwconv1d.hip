@@ -48,7 +48,7 @@ struct DwArgs {
   int win_cap;             // LDS window capacity, elements
 };
 
-template <typename T, int KT, int OPT, bool NTH>
+template <typename T, int KT, int OPT, bool NTH, bool SILU>
 __global__ __launch_bounds__(DW_NT) void dwconv1d_lds_kernel(DwArgs a) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int U = OPT / VEC;
@@ -175,7 +175,7 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_lds_kernel(DwArgs a) {
           const float xv = ((unsigned)pos < L) ? to_f32(win[pb + j]) : 0.f;
           acc = fmaf(wr[j], xv, acc);
         }
-        if (a.silu) acc = silu_f32(acc);
+        if constexpr (SILU) acc = silu_f32(acc);
         o.e[e] = from_f32<T>(acc);
       }
       st16<NTH>(y + f, o.raw);
@@ -240,14 +240,11 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_lds_kernel(DwArgs a) {
           }
         }
       }
-      Vec16<T> o;
+      if constexpr (SILU) {
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        float v = acc[e];
-        if (a.silu) v = silu_f32(v);
-        o.e[e] = from_f32<T>(v);
+        for (int e = 0; e < VEC; ++e) acc[e] = silu_f32(acc[e]);
       }
-      st16<NTH>(y + f, o.raw);
+      st16<NTH>(y + f, pack16<T>(acc));
     } else {
       // row boundary inside the vector, or a partial vector at the tensor ends
 #pragma unroll 1
@@ -271,7 +268,7 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_lds_kernel(DwArgs a) {
           wj = rows_in_lds ? wl[rr * per + j] : to_f32(w[(int64_t)ch * K + j]);
           acc = fmaf(wj, to_f32(win[p0 + j]), acc);
         }
-        if (a.silu) acc = silu_f32(acc);
+        if constexpr (SILU) acc = silu_f32(acc);
         y[fe] = from_f32<T>(acc);
       }
     }
@@ -279,7 +276,7 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_lds_kernel(DwArgs a) {
 }
 
 // One output per thread, straight from global memory.  Generic fallback.
-template <typename T>
+template <typename T, bool SILU>
 __global__ __launch_bounds__(DW_NT) void dwconv1d_direct_kernel(DwArgs a) {
   const T* __restrict__ x = static_cast<const T*>(a.x);
   const T* __restrict__ w = static_cast<const T*>(a.w);
@@ -297,7 +294,7 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_direct_kernel(DwArgs a) {
     if (pos < 0 || pos >= (int64_t)a.L) continue;
     acc = fmaf(to_f32(w[ch * a.K + j]), to_f32(x[r * (int64_t)a.L + pos]), acc);
   }
-  if (a.silu) acc = silu_f32(acc);
+  if constexpr (SILU) acc = silu_f32(acc);
   y[f] = from_f32<T>(acc);
 }
 
@@ -363,8 +360,9 @@ struct DwWindow {
   }
 };
 
-template <typename T, int KT, bool NTH>
-__global__ __launch_bounds__(DW_NT) void dwconv1d_reg_kernel(DwArgs a) {
+// The output vector at flat element f (f counted from y, may be negative at the start).
+template <typename T, int KT, bool NTH, bool SILU>
+__device__ __forceinline__ void reg_vector(const DwArgs& a, int64_t f) {
   using Win = DwWindow<T, KT>;
   constexpr int VEC = Win::VEC, WN = Win::WN;
   const T* __restrict__ x = static_cast<const T*>(a.x);
@@ -374,7 +372,6 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_reg_kernel(DwArgs a) {
   const uint32_t L = a.L, Lout = a.Lout;
   const int pad = a.pad;
 
-  const int64_t f = ((int64_t)blockIdx.x * DW_NT + threadIdx.x) * VEC - a.y_off;
   if (f >= a.total_out || f + VEC <= 0) return;
   bool whole = f >= 0 && f + VEC <= a.total_out;
   uint32_t r = 0, t = 0, eb = VEC;
@@ -433,7 +430,7 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_reg_kernel(DwArgs a) {
 #pragma unroll
         for (int j = 0; j < KT; ++j) acc = fmaf(wk2[j], xw[e + j], acc);
       }
-      if (a.silu) acc = silu_f32(acc);
+      if constexpr (SILU) acc = silu_f32(acc);
       o.e[e] = from_f32<T>(acc);
     }
     st16<NTH>(y + f, o.raw);
@@ -452,15 +449,180 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_reg_kernel(DwArgs a) {
         const int pos = se + j;
         if ((unsigned)pos < L) acc = fmaf(to_f32(w[ce * KT + j]), to_f32(x[(int64_t)re * L + pos]), acc);
       }
-      if (a.silu) acc = silu_f32(acc);
+      if constexpr (SILU) acc = silu_f32(acc);
       y[fe] = from_f32<T>(acc);
     }
   }
 }
 
+template <typename T, int KT, bool NTH, bool SILU>
+__global__ __launch_bounds__(DW_NT) void dwconv1d_reg_kernel(DwArgs a) {
+  constexpr int VEC = 16 / sizeof(T);
+  reg_vector<T, KT, NTH, SILU>(a, ((int64_t)blockIdx.x * DW_NT + threadIdx.x) * VEC - a.y_off);
+}
+
+// Weights w[c, 0..KT) and bias[c] of one wave-uniform channel through scalar loads of the
+// dwords that hold them: no vector-memory instruction, and every read stays inside a dword
+// that holds an element of the array (w and b are element-aligned).
+template <typename T, int KT>
+__device__ __forceinline__ void uniform_params(const void* wp, const void* bp, uint32_t c, float* wk,
+                                               float& bv) {
+  typedef const __attribute__((address_space(4))) uint32_t* cptr;
+  if constexpr (sizeof(T) == 4) {
+    const cptr q = (cptr)((uintptr_t)wp + (uintptr_t)c * KT * 4u);
+#pragma unroll
+    for (int j = 0; j < KT; ++j) wk[j] = __uint_as_float(q[j]);
+    bv = bp ? __uint_as_float(((cptr)((uintptr_t)bp + (uintptr_t)c * 4u))[0]) : 0.f;
+  } else {
+    auto half = [](uint32_t d, uint32_t byte) {
+      return to_f32(__builtin_bit_cast(T, (unsigned short)((byte & 2u) ? (d >> 16) : (d & 0xffffu))));
+    };
+    const uintptr_t a0 = (uintptr_t)wp + (uintptr_t)c * KT * 2u;
+    const uintptr_t al = a0 & ~(uintptr_t)3;
+    const uint32_t sh = (uint32_t)(a0 - al);  // 0 or 2
+    constexpr int NDM = (2 + 2 * KT + 3) / 4;
+    const int nd = (int)((sh + 2u * KT + 3u) / 4u);
+    const cptr q = (cptr)al;
+    uint32_t d[NDM];
+#pragma unroll
+    for (int i = 0; i < NDM; ++i) d[i] = q[i < nd ? i : nd - 1];
+#pragma unroll
+    for (int j = 0; j < KT; ++j) {
+      const uint32_t o = sh + 2u * j;
+      wk[j] = half(d[o >> 2], o);
+    }
+    if (bp) {
+      const uintptr_t ab = (uintptr_t)bp + (uintptr_t)c * 2u;
+      bv = half(((cptr)(ab & ~(uintptr_t)3))[0], (uint32_t)ab);
+    } else {
+      bv = 0.f;
+    }
+  }
+}
+
+// Element e of a window held as packed dwords D (e is a compile-time index after unrolling).
+template <typename T>
+__device__ __forceinline__ float win_elem(const uint32_t* D, int e) {
+  if constexpr (sizeof(T) == 4) {
+    return __uint_as_float(D[e]);
+  } else {
+    const uint32_t d = D[e >> 1];
+    return to_f32(__builtin_bit_cast(T, (unsigned short)((e & 1) ? (d >> 16) : (d & 0xffffu))));
+  }
+}
+
+// Tail of the cross-lane kernel for a wave-uniform window offset M (the window's first
+// element is element M of block bA + lane).  Fixed per M: which neighbour blocks are
+// exchanged and which register holds each window element, so the window costs only its
+// conversions -- no per-lane selects or shifts.  The padding mask runs only in waves with
+// a lane at a row edge.
+template <typename T, int KT, bool NTH, bool SILU, int M>
+__device__ __forceinline__ void xlane_tail(const uint4& E, const uint4& X, int lane, bool edge, int p0,
+                                           uint32_t L, const float* wk, float bv, T* dst) {
+  using Win = DwWindow<T, KT>;
+  constexpr int VEC = Win::VEC, WN = Win::WN;
+  // lanes 0 and 1 stand in with the blocks past the wave, which lanes 62 and 63 need
+  const uint4 Z1 = lane == 0 ? X : E;
+  const int src1 = ((lane + 1) & 63) * 4;
+  uint32_t D[12];
+  D[0] = E.x; D[1] = E.y; D[2] = E.z; D[3] = E.w;
+  D[4] = (uint32_t)__builtin_amdgcn_ds_bpermute(src1, (int)Z1.x);
+  D[5] = (uint32_t)__builtin_amdgcn_ds_bpermute(src1, (int)Z1.y);
+  D[6] = (uint32_t)__builtin_amdgcn_ds_bpermute(src1, (int)Z1.z);
+  D[7] = (uint32_t)__builtin_amdgcn_ds_bpermute(src1, (int)Z1.w);
+  if constexpr (M + WN > 2 * VEC) {
+    const uint4 Z2 = lane < 2 ? X : E;
+    const int src2 = ((lane + 2) & 63) * 4;
+    D[8] = (uint32_t)__builtin_amdgcn_ds_bpermute(src2, (int)Z2.x);
+    D[9] = (uint32_t)__builtin_amdgcn_ds_bpermute(src2, (int)Z2.y);
+    D[10] = (uint32_t)__builtin_amdgcn_ds_bpermute(src2, (int)Z2.z);
+    D[11] = (uint32_t)__builtin_amdgcn_ds_bpermute(src2, (int)Z2.w);
+  } else {
+    D[8] = D[9] = D[10] = D[11] = 0u;
+  }
+  float xv[WN];
+#pragma unroll
+  for (int i = 0; i < WN; ++i) xv[i] = win_elem<T>(D, M + i);
+  if (edge) {
+#pragma unroll
+    for (int i = 0; i < WN; ++i)
+      if ((unsigned)(p0 + i) >= L) xv[i] = 0.f;
+  }
+  float acc[VEC];
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) {
+    acc[e] = bv;
+#pragma unroll
+    for (int j = 0; j < KT; ++j) acc[e] = fmaf(wk[j], xv[e + j], acc[e]);
+    if constexpr (SILU) acc[e] = silu_f32(acc[e]);
+  }
+  // SiLU is a template parameter: as a runtime flag the compiler evaluates it for every
+  // output (two quarter-rate transcendentals each) and selects
+  uint4 o = pack16<T>(acc);
+  // whole vector in registers first: otherwise the plain store may be split into pieces
+  asm volatile("" : "+v"(o.x), "+v"(o.y), "+v"(o.z), "+v"(o.w));
+  st16<NTH>(dst, o);
+}
+
+// Uniform dispatch of the window offset m to its xlane_tail (a scalar compare chain).
+template <typename T, int KT, bool NTH, bool SILU, int M = 0>
+__device__ __forceinline__ void xlane_dispatch(int m, const uint4& E, const uint4& X, int lane, bool edge,
+                                               int p0, uint32_t L, const float* wk, float bv, T* dst) {
+  if constexpr (M < (int)(16 / sizeof(T))) {
+    if (m == M) xlane_tail<T, KT, NTH, SILU, M>(E, X, lane, edge, p0, L, wk, bv, dst);
+    else xlane_dispatch<T, KT, NTH, SILU, M + 1>(m, E, X, lane, edge, p0, L, wk, bv, dst);
+  }
+}
+
+// Cross-lane register kernel: the one-vector-per-thread kernel above with the window
+// shared across the wave.  In a wave whose 64 vectors all lie in one row (all but the few
+// waves that meet a row boundary or a tensor end), lane t's window starts VEC elements
+// after lane t-1's, so it is cut from blocks bA+t, bA+t+1, bA+t+2 of the input: each lane
+// loads only block bA+t, lanes 0 and 1 also load the two blocks past the wave, and the
+// neighbours' blocks arrive through ds_bpermute.  The channel is uniform there, so weights
+// and bias come through scalar loads.  Vector-memory instructions per output vector: about
+// 1 load and 1 store, the access pattern of a streaming copy.  Other waves take the
+// per-lane path of the register kernel.
+template <typename T, int KT, bool NTH, bool SILU>
+__global__ __launch_bounds__(DW_NT) void dwconv1d_xlane_kernel(DwArgs a) {
+  using Win = DwWindow<T, KT>;
+  constexpr int VEC = Win::VEC, WN = Win::WN;
+  static_assert(Win::NBLK <= 3, "window spans at most three blocks");
+  const int lane = threadIdx.x & 63;
+  const int64_t f = ((int64_t)blockIdx.x * DW_NT + threadIdx.x) * VEC - a.y_off;
+  uint32_t r = 0, t = 0;
+  bool inrow = f >= 0 && f + VEC <= a.total_out;
+  if (inrow) {
+    r = fdiv((uint32_t)f, a.div_lout);
+    t = (uint32_t)f - r * a.Lout;
+    inrow = t + VEC <= a.Lout;
+  }
+  const uint32_t r0 = __builtin_amdgcn_readfirstlane(r);
+  if (__builtin_amdgcn_ballot_w64(inrow && r == r0) != ~0ull) {
+    reg_vector<T, KT, NTH, SILU>(a, f);
+    return;
+  }
+  // every lane: row r0, position t = t0 + VEC * lane
+  const uint32_t t0 = __builtin_amdgcn_readfirstlane(t);
+  const int g0 = (int)(r0 * a.L + t0) - a.pad + a.x_off;  // lane 0's window start, from x's aligned base
+  const int bA = g0 >= 0 ? g0 / VEC : -((-g0 + VEC - 1) / VEC);
+  const int m = g0 - bA * VEC;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(
+      static_cast<const T*>(a.x) - a.x_off, (uint32_t)(((int64_t)a.total_in + a.x_off + VEC - 1) / VEC * 16));
+  const int be = bA + lane, bx = bA + 64 + lane;
+  const uint4 E = bload16<NTH ? 2 : 0>(rx, be >= 0 ? (uint32_t)be * 16u : kOOB, 0);
+  const uint4 X = bload16(rx, lane < 2 && bx >= 0 ? (uint32_t)bx * 16u : kOOB, 0);
+  float wk[KT], bv;
+  uniform_params<T, KT>(a.w, a.b, r0 - fdiv(r0, a.div_c) * a.C, wk, bv);
+  // lanes whose window reaches past a row edge need the zero-padding mask (uniform test)
+  const bool edge = (int)t0 - a.pad < 0 || (int)(t0 + VEC * 63) - a.pad + WN > (int)a.L;
+  xlane_dispatch<T, KT, NTH, SILU>(m, E, X, lane, edge, (int)t - a.pad, a.L, wk, bv, static_cast<T*>(a.y) + f);
+}
+
 struct DwVariant {
   const char* name;
-  int opt;  // outputs per thread; 0 = direct kernel, -1 = register kernel (one vector)
+  int opt;  // outputs per thread; 0 = direct kernel, -1 = register kernel (one vector),
+            // -2 = cross-lane register kernel
   bool nt;  // nontemporal loads/stores
 };
 
@@ -474,6 +636,8 @@ const DwVariant kDwVariants[] = {
     {"lds_opt64_nt", 64, true},
     {"reg_nt", -1, true},
     {"reg", -1, false},
+    {"xlane_nt", -2, true},
+    {"xlane", -2, false},
 };
 constexpr int kNumDw = sizeof(kDwVariants) / sizeof(kDwVariants[0]);
 
@@ -482,8 +646,10 @@ int launch_lds_t(const DwArgs& a, size_t shmem, hipStream_t s) {
   constexpr int TO = DW_NT * OPT;
   const int64_t nblk = (a.total_out + a.y_off + TO - 1) / TO;
   if (nblk > 0x7fffffff) return fail(ATK_UNSUPPORTED, "dwconv1d: grid too large");
-  hipLaunchKernelGGL((dwconv1d_lds_kernel<T, KT, OPT, NTH>), dim3((unsigned)nblk), dim3(DW_NT),
-                     shmem, s, a);
+  if (a.silu)
+    hipLaunchKernelGGL((dwconv1d_lds_kernel<T, KT, OPT, NTH, true>), dim3((unsigned)nblk), dim3(DW_NT), shmem, s, a);
+  else
+    hipLaunchKernelGGL((dwconv1d_lds_kernel<T, KT, OPT, NTH, false>), dim3((unsigned)nblk), dim3(DW_NT), shmem, s, a);
   return check_launch("dwconv1d_lds_kernel");
 }
 
@@ -498,31 +664,45 @@ int launch_lds_k(const DwArgs& a, size_t shmem, hipStream_t s) {
   }
 }
 
-template <typename T, bool NTH>
+template <typename T, int KT, bool NTH, bool XL>
+void launch_reg_k(dim3 grid, dim3 block, hipStream_t s, const DwArgs& a) {
+  if constexpr (XL) {
+    if (a.silu) hipLaunchKernelGGL((dwconv1d_xlane_kernel<T, KT, NTH, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((dwconv1d_xlane_kernel<T, KT, NTH, false>), grid, block, 0, s, a);
+  } else {
+    if (a.silu) hipLaunchKernelGGL((dwconv1d_reg_kernel<T, KT, NTH, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((dwconv1d_reg_kernel<T, KT, NTH, false>), grid, block, 0, s, a);
+  }
+}
+
+template <typename T, bool NTH, bool XL>
 int launch_reg(const DwArgs& a, hipStream_t s) {
   constexpr int VEC = 16 / sizeof(T);
   if (a.total_out + a.y_off >= (1ll << 31) - VEC || a.total_in + a.x_off >= (1ll << 31) / (int64_t)sizeof(T) - VEC)
     return fail(ATK_UNSUPPORTED, "dwconv1d: tensor too large for the register kernel");
   const int64_t nblk = (a.total_out + a.y_off + (int64_t)DW_NT * VEC - 1) / ((int64_t)DW_NT * VEC);
+  const dim3 grid((unsigned)nblk), block(DW_NT);
   switch (a.K) {
-    case 2: hipLaunchKernelGGL((dwconv1d_reg_kernel<T, 2, NTH>), dim3((unsigned)nblk), dim3(DW_NT), 0, s, a); break;
-    case 3: hipLaunchKernelGGL((dwconv1d_reg_kernel<T, 3, NTH>), dim3((unsigned)nblk), dim3(DW_NT), 0, s, a); break;
-    case 4: hipLaunchKernelGGL((dwconv1d_reg_kernel<T, 4, NTH>), dim3((unsigned)nblk), dim3(DW_NT), 0, s, a); break;
-    case 5: hipLaunchKernelGGL((dwconv1d_reg_kernel<T, 5, NTH>), dim3((unsigned)nblk), dim3(DW_NT), 0, s, a); break;
-    default: return fail(ATK_UNSUPPORTED, "dwconv1d: register kernel serves K in [2, 5]");
+    case 2: launch_reg_k<T, 2, NTH, XL>(grid, block, s, a); break;
+    case 3: launch_reg_k<T, 3, NTH, XL>(grid, block, s, a); break;
+    case 4: launch_reg_k<T, 4, NTH, XL>(grid, block, s, a); break;
+    case 5: launch_reg_k<T, 5, NTH, XL>(grid, block, s, a); break;
+    default: return fail(ATK_UNSUPPORTED, "dwconv1d: register kernels serve K in [2, 5]");
   }
-  return check_launch("dwconv1d_reg_kernel");
+  return check_launch(XL ? "dwconv1d_xlane_kernel" : "dwconv1d_reg_kernel");
 }
 
 template <typename T>
 int launch_dw(DwArgs a, int variant, hipStream_t s) {
   constexpr int VEC = 16 / sizeof(T);
   const int opt = kDwVariants[variant].opt;
-  if (opt < 0) return kDwVariants[variant].nt ? launch_reg<T, true>(a, s) : launch_reg<T, false>(a, s);
+  if (opt == -1) return kDwVariants[variant].nt ? launch_reg<T, true, false>(a, s) : launch_reg<T, false, false>(a, s);
+  if (opt == -2) return kDwVariants[variant].nt ? launch_reg<T, true, true>(a, s) : launch_reg<T, false, true>(a, s);
   if (opt == 0 || opt < VEC) {
     const int64_t nblk = (a.total_out + DW_NT - 1) / DW_NT;
     if (nblk > 0x7fffffff) return fail(ATK_UNSUPPORTED, "dwconv1d: grid too large");
-    hipLaunchKernelGGL((dwconv1d_direct_kernel<T>), dim3((unsigned)nblk), dim3(DW_NT), 0, s, a);
+    if (a.silu) hipLaunchKernelGGL((dwconv1d_direct_kernel<T, true>), dim3((unsigned)nblk), dim3(DW_NT), 0, s, a);
+    else hipLaunchKernelGGL((dwconv1d_direct_kernel<T, false>), dim3((unsigned)nblk), dim3(DW_NT), 0, s, a);
     return check_launch("dwconv1d_direct_kernel");
   }
   // LDS window bound for one tile (see the kernel): TO outputs span at most

@@ -134,17 +134,18 @@ __device__ __forceinline__ void channel_affine(const GnArgs& a, int64_t c, float
   sh = bt - mean * sc;
 }
 
-template <typename T>
-__device__ __forceinline__ uint4 normalize_vec(const Vec16<T>& in, float sc, float sh, int silu) {
+// SiLU is a template parameter: as a runtime flag the compiler evaluates it for every
+// element (two quarter-rate transcendentals each) and selects.
+template <typename T, bool SILU>
+__device__ __forceinline__ uint4 normalize_vec(const Vec16<T>& in, float sc, float sh) {
   constexpr int VEC = 16 / sizeof(T);
-  Vec16<T> o;
+  float v[VEC];
 #pragma unroll
   for (int k = 0; k < VEC; ++k) {
-    float v = fmaf(to_f32(in.e[k]), sc, sh);
-    if (silu) v = silu_f32(v);
-    o.e[k] = from_f32<T>(v);
+    v[k] = fmaf(to_f32(in.e[k]), sc, sh);
+    if constexpr (SILU) v[k] = silu_f32(v[k]);
   }
-  return o.raw;
+  return pack16<T>(v);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -235,7 +236,7 @@ __device__ __forceinline__ void slice_stats(Vec16<T>* buf, const T* xg, int64_t 
 // Up to 16 vectors per thread fit 128 VGPRs: four waves per SIMD, so two 512-thread (or
 // four 256-thread) workgroups share a CU -- left alone, the fp16 build of EPV = 16 takes
 // 144 and halves the residency that a multi-slice launch relies on.
-template <typename T, int NT, int EPV>
+template <typename T, int NT, int EPV, bool SILU>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(EPV <= 16 ? 4 : 1)))
 void gn_resident_kernel(GnArgs a) {
   constexpr int VEC = 16 / sizeof(T);
@@ -402,7 +403,7 @@ void gn_resident_kernel(GnArgs a) {
       const bool ok = (uint32_t)(i * NT + tid_s) < n_vec;
       const int64_t e = ok ? s0 + ((int64_t)i * NT + tid_s) * VEC : s0;
       const int cl = (int)(fdiv((uint32_t)e, a.div_s) - c_lo);
-      if (ok) st16<true>(yg + e, normalize_vec<T>(buf[i], aff[cl], aff[GN_MAX_AFF + cl], a.silu));
+      if (ok) st16<true>(yg + e, normalize_vec<T, SILU>(buf[i], aff[cl], aff[GN_MAX_AFF + cl]));
     }
   } else {
 #pragma unroll
@@ -412,7 +413,7 @@ void gn_resident_kernel(GnArgs a) {
         const int cl = (int)(fdiv((uint32_t)e, a.div_s) - c_lo);
         float sc, sh;
         channel_affine(a, cabs0 + cl, mean, rstd, sc, sh);
-        st16<true>(yg + e, normalize_vec<T>(buf[i], sc, sh, a.silu));
+        st16<true>(yg + e, normalize_vec<T, SILU>(buf[i], sc, sh));
       }
     }
   }
@@ -474,7 +475,7 @@ __global__ __launch_bounds__(GN_TP_NT) void gn_stats_kernel(GnArgs a) {
   }
 }
 
-template <typename T, bool VECOK>
+template <typename T, bool VECOK, bool SILU>
 __global__ __launch_bounds__(GN_TP_NT) void gn_apply_kernel(GnArgs a) {
   constexpr int VEC = VECOK ? 16 / sizeof(T) : 1;
   __shared__ float s_stat[2];
@@ -510,10 +511,10 @@ __global__ __launch_bounds__(GN_TP_NT) void gn_apply_kernel(GnArgs a) {
     if (VECOK) {
       Vec16<T> b;
       b.raw = *reinterpret_cast<const uint4*>(xg + e);
-      st16<true>(yg + e, normalize_vec<T>(b, sc, sh, a.silu));
+      st16<true>(yg + e, normalize_vec<T, SILU>(b, sc, sh));
     } else {
       float v = fmaf(to_f32(xg[e]), sc, sh);
-      if (a.silu) v = silu_f32(v);
+      if constexpr (SILU) v = silu_f32(v);
       yg[e] = from_f32<T>(v);
     }
   }
@@ -579,11 +580,11 @@ bool plan_gn(int64_t N, int64_t C, int64_t S, int G, int dtype, int variant, GnP
   return true;
 }
 
-template <typename T, int NT, int EPV>
-int launch_resident(GnArgs a, int64_t ngroups, hipStream_t s) {
+template <typename T, int NT, int EPV, bool SILU>
+int launch_resident_s(GnArgs a, int64_t ngroups, hipStream_t s) {
   const int64_t nblk = ngroups * a.NS;
   if (nblk > 0x7fffffff) return fail(ATK_UNSUPPORTED, "group_norm: grid too large");
-  auto kern = gn_resident_kernel<T, NT, EPV>;
+  auto kern = gn_resident_kernel<T, NT, EPV, SILU>;
   if (a.NS > 1) {
     if (ngroups > GN_MAX_SLOTTED || nblk > GN_MAX_SLOTS)
       return fail(ATK_UNSUPPORTED, "group_norm: %lld groups x %d slices exceed the slot table",
@@ -605,6 +606,22 @@ int launch_resident(GnArgs a, int64_t ngroups, hipStream_t s) {
   }
   hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(NT), 0, s, a);
   return check_launch("gn_resident_kernel");
+}
+
+template <typename T, int NT, int EPV>
+int launch_resident(GnArgs a, int64_t ngroups, hipStream_t s) {
+  return a.silu ? launch_resident_s<T, NT, EPV, true>(a, ngroups, s)
+                : launch_resident_s<T, NT, EPV, false>(a, ngroups, s);
+}
+
+template <typename T, bool VECOK>
+int launch_twopass(const GnArgs& a, int64_t nblk, hipStream_t s) {
+  hipLaunchKernelGGL((gn_stats_kernel<T, VECOK>), dim3((unsigned)nblk), dim3(GN_TP_NT), 0, s, a);
+  const int rc = check_launch("gn_stats_kernel");
+  if (rc) return rc;
+  if (a.silu) hipLaunchKernelGGL((gn_apply_kernel<T, VECOK, true>), dim3((unsigned)nblk), dim3(GN_TP_NT), 0, s, a);
+  else hipLaunchKernelGGL((gn_apply_kernel<T, VECOK, false>), dim3((unsigned)nblk), dim3(GN_TP_NT), 0, s, a);
+  return check_launch("gn_apply_kernel");
 }
 
 template <typename T>
@@ -629,18 +646,7 @@ int launch_gn(GnArgs a, int64_t ngroups, int variant, bool vec_ok, hipStream_t s
   }
   const int64_t nblk = ngroups * a.NS;
   if (nblk > 0x7fffffff) return fail(ATK_UNSUPPORTED, "group_norm: grid too large");
-  if (vec_ok) {
-    hipLaunchKernelGGL((gn_stats_kernel<T, true>), dim3((unsigned)nblk), dim3(GN_TP_NT), 0, s, a);
-    int rc = check_launch("gn_stats_kernel");
-    if (rc) return rc;
-    hipLaunchKernelGGL((gn_apply_kernel<T, true>), dim3((unsigned)nblk), dim3(GN_TP_NT), 0, s, a);
-    return check_launch("gn_apply_kernel");
-  }
-  hipLaunchKernelGGL((gn_stats_kernel<T, false>), dim3((unsigned)nblk), dim3(GN_TP_NT), 0, s, a);
-  int rc = check_launch("gn_stats_kernel");
-  if (rc) return rc;
-  hipLaunchKernelGGL((gn_apply_kernel<T, false>), dim3((unsigned)nblk), dim3(GN_TP_NT), 0, s, a);
-  return check_launch("gn_apply_kernel");
+  return vec_ok ? launch_twopass<T, true>(a, nblk, s) : launch_twopass<T, false>(a, nblk, s);
 }
 
 int validate_gn(int64_t N, int64_t C, int64_t S, int G, int dtype, int variant) {

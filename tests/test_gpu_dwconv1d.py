@@ -50,6 +50,11 @@ CASES = [
     (2, 16, 8, 1, 0, 8),         # K = 1
     (1, 8, 4096, 4, 3, 4099),    # long rows, stock causal
     (4, 64, 333, 3, 1, 333),     # many short rows per tile
+    # rows longer than a wave's 64 vectors: the cross-lane kernel's in-row path
+    (2, 4, 2500, 4, 3, 2503),    # causal, stock shape (row starts at every alignment)
+    (1, 6, 2048, 3, 1, 2048),    # symmetric, aligned rows
+    (1, 5, 1100, 2, 1, 1101),    # K = 2
+    (1, 3, 2000, 5, 2, 2000),    # K = 5
 ]
 
 
