@@ -292,20 +292,34 @@ def cpu_baseline(rows_sample: int = 1):
 # ---------------------------------------------------------------------------
 # HBM traffic of the headline kernel, from rocprofv3 FETCH_SIZE / WRITE_SIZE passes
 # ---------------------------------------------------------------------------
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "dwconv1d_lds_kernel_c2_traffic.txt")
 CALIB_ELEMS = 16 * 2048 * 8192  # bf16 elements read and written by the calibration kernel
 
 
-def traffic_probe(variant: str, iters: int = 10):
-    """Workload for the counter passes: `iters` launches of the headline dwconv1d variant,
-    then `iters` launches of torch.neg over a bf16 tensor of CALIB_ELEMS elements — an
-    elementwise kernel that reads and writes exactly CALIB_ELEMS*2 bytes each, so its
-    FETCH_SIZE / WRITE_SIZE readings calibrate the counters' units and overheads."""
+def dw_kernel_name(variant: str) -> str:
+    """The HIP kernel a dwconv1d variant launches."""
+    for prefix, kernel in (("lds", "dwconv1d_lds_kernel"), ("reg", "dwconv1d_reg_kernel"),
+                           ("xlane", "dwconv1d_xlane_kernel")):
+        if variant.startswith(prefix):
+            return kernel
+    return "dwconv1d_direct_kernel"
+
+
+def traffic_file(kernel: str) -> str:
+    return os.path.join(ROOT, "profiles", f"{kernel}_c2_traffic.txt")
+
+
+def traffic_probe(variants: str, iters: int = 10):
+    """Workload for the counter passes: `iters` launches of each listed dwconv1d variant
+    (comma-separated, one per kernel) on the headline workload, then `iters` launches of
+    torch.neg over a bf16 tensor of CALIB_ELEMS elements — an elementwise kernel that reads
+    and writes exactly CALIB_ELEMS*2 bytes each, so its FETCH_SIZE / WRITE_SIZE readings
+    calibrate the counters' units and overheads."""
     import torch
     dev = torch.device("cuda", 0)
     x, w, b = c2_inputs(torch.bfloat16, 4, dev)
     L = x.shape[-1]
-    dw_kernel_ms(x, w, b, 3, L + 3, variant, iters=iters)
+    for variant in variants.split(","):
+        dw_kernel_ms(x, w, b, 3, L + 3, variant, iters=iters)
     src = torch.randn(CALIB_ELEMS, device=dev, dtype=torch.bfloat16)
     dst = torch.empty_like(src)
     for _ in range(iters):
@@ -333,11 +347,18 @@ def _pick(means: "dict[str, float]", *needles: str) -> "tuple[str, float]":
     return hits[0]
 
 
-def summarize_traffic(fetch_dir: str, write_dir: str, variant: str, command: str):
-    """Turn the two counter passes into the committed traffic summary (TRAFFIC_FILE)."""
+def summarize_traffic(fetch_dir: str, write_dir: str, variants: str, command: str):
+    """Turn the two counter passes into one committed traffic summary per probed variant's
+    kernel (traffic_file(kernel))."""
+    for variant in variants.split(","):
+        _summarize_traffic_one(fetch_dir, write_dir, variant, command)
+
+
+def _summarize_traffic_one(fetch_dir: str, write_dir: str, variant: str, command: str):
     fetch, write = _counter_means(fetch_dir, "FETCH_SIZE"), _counter_means(write_dir, "WRITE_SIZE")
-    kname, k_fetch = _pick(fetch, "dwconv1d_lds_kernel")
-    _, k_write = _pick(write, "dwconv1d_lds_kernel")
+    kernel = dw_kernel_name(variant)
+    kname, k_fetch = _pick(fetch, kernel)
+    _, k_write = _pick(write, kernel)
     cname, c_fetch = _pick(fetch, "neg")
     _, c_write = _pick(write, "neg")
     calib_bytes = CALIB_ELEMS * 2
@@ -352,7 +373,7 @@ def summarize_traffic(fetch_dir: str, write_dir: str, variant: str, command: str
            "fetch_kib_calib": c_fetch, "write_kib_calib": c_write,
            "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4)}
     lines = [
-        "# HBM traffic per launch of the headline dwconv1d kernel (config 2, bf16, causal k=4)",
+        f"# HBM traffic per launch of dwconv1d variant {variant} (config 2, bf16, causal k=4, stock output shape)",
         f"# commands: {command}",
         f"# kernel: {kname[:160]}",
         f"# calibration kernel (torch.neg over {CALIB_ELEMS} bf16 = {calib_bytes} B read + written): {cname[:120]}",
@@ -361,7 +382,7 @@ def summarize_traffic(fetch_dir: str, write_dir: str, variant: str, command: str
         f"# traffic = {rd:.4g} B read + {wr:.4g} B written = {(rd + wr) / algo:.4f} x algorithmic {algo} B",
         "TRAFFIC_JSON " + json.dumps(rec),
     ]
-    with open(TRAFFIC_FILE, "w") as f:
+    with open(traffic_file(kernel), "w") as f:
         f.write("\n".join(lines) + "\n")
     print("\n".join(lines))
 
@@ -386,9 +407,9 @@ def summarize_stats(stats_dir: str, out_path: str, command: str, top: int = 25):
     print("\n".join(lines))
 
 
-def load_traffic() -> "dict | None":
+def load_traffic(kernel: str) -> "dict | None":
     try:
-        for line in open(TRAFFIC_FILE):
+        for line in open(traffic_file(kernel)):
             if line.startswith("TRAFFIC_JSON "):
                 return json.loads(line[len("TRAFFIC_JSON "):])
     except OSError:
@@ -409,7 +430,8 @@ def main():
                     help="write the traffic summary from two rocprofv3 --pmc output folders")
     ap.add_argument("--summarize-stats", nargs=2, metavar=("STATS_DIR", "OUT"),
                     help="write a text summary of a rocprofv3 --kernel-trace --stats folder")
-    ap.add_argument("--variant", default="lds_opt32_nt", help="dwconv1d variant for --traffic-probe")
+    ap.add_argument("--variant", default="xlane,lds_opt32_nt",
+                    help="dwconv1d variants (comma-separated, one per kernel) for --traffic-probe")
     ap.add_argument("--command", default="", help="command line recorded by --summarize-traffic")
     args = ap.parse_args()
     if args.summarize_stats:
@@ -458,14 +480,12 @@ def main():
 
     if won.startswith("native."):
         kms = dw_kernel_ms(x, w, b, 3, L + 3, won[7:], iters=max(20, args.steps))
-        kernel_name = ("dwconv1d_lds_kernel" if won[7:].startswith("lds") else
-                       "dwconv1d_reg_kernel" if won[7:].startswith("reg") else
-                       "dwconv1d_direct_kernel")
+        kernel_name = dw_kernel_name(won[7:])
     else:
         kms = event_time_ms(lambda: step(), 20)
         kernel_name = "stock"
     achieved = nbytes / (kms * 1e-3) / 1e9
-    tr = load_traffic()
+    tr = load_traffic(kernel_name) if kernel_name != "stock" else None
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                 "traffic": tr["traffic_bytes"] if tr else None,
@@ -475,7 +495,7 @@ def main():
         roofline["traffic_detail"] = {
             "read_bytes": tr["read_bytes"], "write_bytes": tr["write_bytes"],
             "measured_variant": tr["variant"],
-            "source": "profiles/" + os.path.basename(TRAFFIC_FILE) +
+            "source": "profiles/" + os.path.basename(traffic_file(kernel_name)) +
                       " (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, scaled by a torch.neg copy "
                       "of known size)"}
     y = step()
