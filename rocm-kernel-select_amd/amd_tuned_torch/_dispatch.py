@@ -217,7 +217,7 @@ def _conv_variant_names(dtype) -> "list[str]":
 
 
 def _conv_variant_dtype_ok(name: str, dtype) -> bool:
-    """Variant names carry their operand class: "f32_*" fp32, "h*" (h_, h2_) fp16/bf16."""
+    """Variant names carry their operand class: "f32_*" fp32, "h_*" fp16/bf16."""
     if name.startswith("f32_"):
         return dtype == torch.float32
     if name.startswith("h"):

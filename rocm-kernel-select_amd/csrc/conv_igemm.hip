@@ -48,9 +48,6 @@ struct IgArgs {
   int patch_elems;    // elements of one patch buffer (two are allocated)
   uint32_t x_sample_bytes;  // bytes of one input sample (buffer range of the patch loads)
   uint32_t wp_bytes;        // bytes of the packed weights
-  int rps;                  // kernel rows per stage (stage-prefetch family)
-  int n_rg;                 // row groups = KH / rps
-  int w_stage_frags;        // weight fragments one stage stages into LDS
   int n_stages;       // n_cc * KD
   int stages_per_split;
   int n_kb;           // ci k-blocks in the packed weights = n_cc * CB / KB
@@ -544,161 +541,6 @@ __attribute__((amdgpu_waves_per_eu(FCO * FSP >= 8 && CB == 16 ? 2 : 1))) void co
   store_tile<T, FCO, FSP, BN>(a, acc, s_bias, n, co_tile, split, oz, oy0, ox0, wco, wsp, half, col);
 }
 
-// ---------------------------------------------------------------------------------------
-// Stage-prefetch family: every global load a stage needs -- its input patch AND its weight
-// slice (rps kernel rows x KW taps x CB channels x BN output channels, already in MFMA
-// fragment order) -- is issued into registers at the start of the PREVIOUS stage and
-// written to the other half of a double-buffered LDS arena at its end.  The tap loop then
-// issues only LDS reads and MFMAs, so no global-load latency (and no in-order vmcnt wait on
-// a long-distance prefetch) ever sits between two MFMAs.  Stage = (ci chunk, kd, row group).
-// ---------------------------------------------------------------------------------------
-template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, bool VR, int WMAX>
-__global__ __launch_bounds__(64 * WCO * WSP) void conv_igemm2_kernel(IgArgs a) {
-  constexpr int NT = 64 * WCO * WSP;
-  constexpr int KB = MfmaTraits<T>::KB, VEC = MfmaTraits<T>::VEC;
-  constexpr int ES = sizeof(T);
-  constexpr int CBS = CB + VEC;
-  constexpr int BN = WCO * FCO * 32;
-  constexpr int NF = BN / 32;             // weight fragments per (tap, kb) in a stage
-  constexpr int NKB = CB / KB;
-  constexpr uint32_t FRAG = 32 * KB * ES;
-  extern __shared__ uint4 lds_raw[];
-  char* lds = reinterpret_cast<char*>(lds_raw);
-
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-  const int wco = wv % WCO, wsp = wv / WCO;
-  const int half = lane >> 5, col = lane & 31;
-
-  int t = blockIdx.x;
-  const int tx_t = t % a.tiles_x; t /= a.tiles_x;
-  const int ty_t = t % a.tiles_y; t /= a.tiles_y;
-  const int oz = t % a.Do;
-  const int n = t / a.Do;
-  const int co_tile = blockIdx.y;
-  const int split = blockIdx.z;
-  __shared__ float s_bias[BN];
-  stage_bias<T, BN, NT>(a, co_tile, s_bias);  // visible after the prologue's barrier
-  const int s_begin = split * a.stages_per_split;
-  const int s_end = min(a.n_stages, s_begin + a.stages_per_split);
-  const int oy0 = ty_t * a.TY, ox0 = tx_t * a.TX;
-  const int iy0 = oy0 * a.sh - a.ph, ix0 = ox0 * a.sw - a.pw;
-  const int gx0 = (ix0 >= 0 ? ix0 / VEC : -((-ix0 + VEC - 1) / VEC)) * VEC;
-  const int mis = ix0 - gx0;
-  const int total_chunks = CB * a.PY * a.NCX;
-  const int taps_stage = a.rps * a.KW;
-  const int wchunks = a.w_stage_frags * 64;
-
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(
-      static_cast<const T*>(a.x) + (int64_t)n * a.Ci * a.D * a.H * a.W, a.x_sample_bytes);
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(a.wp, a.wp_bytes);
-
-  const uint32_t patch_bytes = (uint32_t)a.patch_elems * ES;
-  const uint32_t wst_bytes = (uint32_t)a.w_stage_frags * FRAG;
-  // LDS arena: [patch 0][patch 1][weights 0][weights 1]
-  const uint32_t w_base = 2 * patch_bytes;
-
-  uint32_t pb[FSP];
-#pragma unroll
-  for (int j = 0; j < FSP; ++j) {
-    const int m = (wsp * FSP + j) * 32 + col;
-    const int ty = m / a.TX, tx = m - (m / a.TX) * a.TX;
-    pb[j] = (uint32_t)(((ty * a.sh) * a.PXS + tx * a.sw + mis) * CBS + half * VEC) * ES;
-  }
-  const uint32_t kh_step = (uint32_t)(a.dh * a.PXS * CBS) * ES;
-  const uint32_t kw_step = (uint32_t)(a.dw * CBS) * ES;
-  // byte offset of this lane's 16 bytes inside a packed 32 x KB fragment (staged verbatim)
-  const uint32_t lane16 = (uint32_t)(col * KB + half * VEC) * ES;
-
-  f32x16 acc[FCO][FSP];
-#pragma unroll
-  for (int i = 0; i < FCO; ++i)
-#pragma unroll
-    for (int j = 0; j < FSP; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-  PatchLoader<T, CB, VR, NT> ld;
-  uint4 wbuf[WMAX];
-  // global byte offset of weight chunk w of stage (cc, kd, rg)
-  auto load_stage = [&](int s, bool valid) {
-    const int rg = s % a.n_rg;
-    const int ckd = s / a.n_rg;
-    const int cc = ckd / a.KD, kd = ckd - (ckd / a.KD) * a.KD;
-    ld.load(a, rx, cc, oz * a.sd - a.pd + kd * a.dd, iy0 + rg * a.rps * a.dh, gx0, total_chunks, tid, NT,
-            valid);
-#pragma unroll
-    for (int u = 0; u < WMAX; ++u) {
-      const int w = tid + u * NT;
-      const int frag = w >> 6, l16 = w & 63;
-      const int tt = frag / (NKB * NF);
-      const int rem = frag - tt * (NKB * NF);
-      const int kb = rem / NF, f = rem - (rem / NF) * NF;
-      const int r = tt / a.KW, kw = tt - (tt / a.KW) * a.KW;
-      const int tap = (kd * a.KH + rg * a.rps + r) * a.KW + kw;
-      const uint32_t src = ((uint32_t)(tap * a.n_kb + cc * NKB + kb) * a.co_blocks + co_tile * NF + f) * FRAG
-                           + (uint32_t)l16 * 16;
-      wbuf[u] = bload16(rw, valid && w < wchunks ? src : kOOB, 0);
-    }
-  };
-  auto store_stage = [&](int buf) {
-    ld.store(a, reinterpret_cast<T*>(lds + buf * patch_bytes), total_chunks, tid, NT);
-    char* wdst = lds + w_base + buf * wst_bytes;
-#pragma unroll
-    for (int u = 0; u < WMAX; ++u) {
-      const int w = tid + u * NT;
-      if (w < wchunks) *reinterpret_cast<uint4*>(wdst + (uint32_t)w * 16) = wbuf[u];
-    }
-  };
-
-  if (s_begin < s_end) {
-    load_stage(s_begin, true);
-    store_stage(0);
-  }
-  __syncthreads();
-
-  for (int s = s_begin; s < s_end; ++s) {
-    const int buf = (s - s_begin) & 1;
-    const bool has_next = s + 1 < s_end;
-    load_stage(s + 1, has_next);
-    const int ckd = s / a.n_rg;
-    const int kd = ckd - (ckd / a.KD) * a.KD;
-    const int iz = oz * a.sd - a.pd + kd * a.dd;
-    if ((unsigned)iz < (unsigned)a.D) {
-      const char* pbase = lds + buf * patch_bytes;
-      const char* wbase = lds + w_base + buf * wst_bytes + lane16;
-      int r = 0, kw = 0;
-      uint32_t toffb = 0;
-      for (int tt = 0; tt < taps_stage; ++tt) {
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) {
-          uint4 wf[FCO], pf[FSP];
-#pragma unroll
-          for (int i = 0; i < FCO; ++i)
-            wf[i] = *reinterpret_cast<const uint4*>(wbase + ((uint32_t)((tt * NKB + kb) * NF + wco * FCO + i)) * 1024);
-#pragma unroll
-          for (int j = 0; j < FSP; ++j)
-            pf[j] = *reinterpret_cast<const uint4*>(pbase + pb[j] + toffb + kb * KB * ES);
-#pragma unroll
-          for (int i = 0; i < FCO; ++i)
-#pragma unroll
-            for (int j = 0; j < FSP; ++j) mfma_block(acc[i][j], wf[i], pf[j], static_cast<T*>(nullptr));
-        }
-        if (++kw == a.KW) {
-          kw = 0;
-          ++r;
-          toffb = r * kh_step;
-        } else {
-          toffb += kw_step;
-        }
-      }
-    }
-    if (has_next) store_stage(buf ^ 1);
-    __syncthreads();
-  }
-
-  store_tile<T, FCO, FSP, BN>(a, acc, s_bias, n, co_tile, split, oz, oy0, ox0, wco, wsp, half, col);
-}
-
 // Packed weights Wp[tap][kb][co_block][32][KB] from w[Co][Ci][taps]; zero beyond Co / Ci.
 template <typename T>
 __global__ __launch_bounds__(256) void pack_weights_kernel(const T* __restrict__ w, T* __restrict__ wp,
@@ -734,35 +576,22 @@ struct IgVariant {
   const char* name;
   int dtype_class;  // 0 = 16-bit, 1 = fp32
   int wco, wsp, fco, fsp, cb;
-  int family;       // 1 = weights from L2 per tap, 2 = stage-prefetch (weights via LDS)
 };
-constexpr int IG2_WMAX = 16;  // weight chunks per thread a stage-prefetch stage may hold
 
 const IgVariant kIg[] = {
-    {"h_w22_f22_cb32", 0, 2, 2, 2, 2, 32, 1},
-    {"h_w22_f42_cb32", 0, 2, 2, 4, 2, 32, 1},
-    {"h_w22_f24_cb32", 0, 2, 2, 2, 4, 32, 1},
-    {"h_w14_f22_cb32", 0, 1, 4, 2, 2, 32, 1},
-    {"h_w22_f22_cb16", 0, 2, 2, 2, 2, 16, 1},
-    {"h_w41_f24_cb32", 0, 4, 1, 2, 4, 32, 1},
-    {"h_w41_f22_cb32", 0, 4, 1, 2, 2, 32, 1},
-    {"h_w21_f24_cb32", 0, 2, 1, 2, 4, 32, 1},
-    {"h_w22_f12_cb32", 0, 2, 2, 1, 2, 32, 1},
-    {"h_w21_f14_cb32", 0, 2, 1, 1, 4, 32, 1},
-    {"f32_w22_f22_cb16", 1, 2, 2, 2, 2, 16, 1},
-    {"f32_w14_f22_cb16", 1, 1, 4, 2, 2, 16, 1},
-    {"f32_w22_f12_cb16", 1, 2, 2, 1, 2, 16, 1},
-    {"f32_w21_f14_cb16", 1, 2, 1, 1, 4, 16, 1},
-    {"h2_w22_f24_cb16", 0, 2, 2, 2, 4, 16, 2},
-    {"h2_w22_f24_cb32", 0, 2, 2, 2, 4, 32, 2},
-    {"h2_w22_f22_cb32", 0, 2, 2, 2, 2, 32, 2},
-    {"h2_w14_f22_cb32", 0, 1, 4, 2, 2, 32, 2},
-    {"h2_w12_f24_cb32", 0, 1, 2, 2, 4, 32, 2},
-    {"h2_w22_f42_cb16", 0, 2, 2, 4, 2, 16, 2},
-    {"f32_2_w22_f22_cb16", 1, 2, 2, 2, 2, 16, 2},
-    {"f32_2_w12_f24_cb16", 1, 1, 2, 2, 4, 16, 2},
-    {"h_w22_f24_cb16", 0, 2, 2, 2, 4, 16, 1},
-    {"h_w41_f24_cb16", 0, 4, 1, 2, 4, 16, 1},
+    {"h_w22_f22_cb32", 0, 2, 2, 2, 2, 32},
+    {"h_w22_f24_cb32", 0, 2, 2, 2, 4, 32},
+    {"h_w14_f22_cb32", 0, 1, 4, 2, 2, 32},
+    {"h_w22_f22_cb16", 0, 2, 2, 2, 2, 16},
+    {"h_w41_f22_cb32", 0, 4, 1, 2, 2, 32},
+    {"h_w21_f24_cb32", 0, 2, 1, 2, 4, 32},
+    {"h_w22_f12_cb32", 0, 2, 2, 1, 2, 32},
+    {"h_w21_f14_cb32", 0, 2, 1, 1, 4, 32},
+    {"h_w22_f24_cb16", 0, 2, 2, 2, 4, 16},
+    {"f32_w22_f22_cb16", 1, 2, 2, 2, 2, 16},
+    {"f32_w14_f22_cb16", 1, 1, 4, 2, 2, 16},
+    {"f32_w22_f12_cb16", 1, 2, 2, 1, 2, 16},
+    {"f32_w21_f14_cb16", 1, 2, 1, 1, 4, 16},
 };
 constexpr int kNumIg = sizeof(kIg) / sizeof(kIg[0]);
 
@@ -809,31 +638,22 @@ int plan_ig(const ConvShape& p, int v, IgPlan& pl) {
       break;
     }
   }
-  const size_t frag = (size_t)32 * KB * es;
-  // stage = (ci chunk, kd[, kernel row group]); family 2 also stages the weight slice
-  int rps = p.KH;
-  for (;;) {
-    a.rps = rps;
-    a.n_rg = p.KH / rps;
-    a.PY = (a.TY - 1) * p.sh + (rps - 1) * p.dh + 1;
-    {
-      constexpr size_t kLdsCu = 160 * 1024;
-      const size_t plain = (size_t)2 * a.PY * a.NCX * VEC * (vr.cb + VEC) * es + 1024;
-      const size_t padded = (size_t)2 * a.PY * (a.NCX * VEC + row_pad) * (vr.cb + VEC) * es + 1024;
-      a.PXS = a.NCX * VEC + (kLdsCu / padded == kLdsCu / plain ? row_pad : 0);
-    }
-    a.patch_elems = a.PY * a.PXS * (vr.cb + VEC);
-    a.w_stage_frags = vr.family == 2 ? rps * p.KW * (vr.cb / KB) * (pl.bn / 32) : 0;
-    pl.lds = (size_t)2 * a.patch_elems * es + (size_t)2 * a.w_stage_frags * frag;
-    const int maxc = (f32 ? vr.cb / 2 : vr.cb / 4) * (256 / pl.nthreads);  // PatchLoader::MAXC
-    const bool fits = pl.lds <= 150 * 1024 && vr.cb * a.PY * a.NCX <= maxc * pl.nthreads &&
-                      a.w_stage_frags * 64 <= IG2_WMAX * pl.nthreads;
-    if (fits) break;
-    if (rps == 1 || vr.family != 2)
-      return fail(ATK_UNSUPPORTED, "conv %s: stage of %zu LDS bytes does not fit the variant", vr.name, pl.lds);
-    rps = 1;
+  // stage = (ci chunk, kd): the patch of all KH x KW taps of one input plane
+  a.PY = (a.TY - 1) * p.sh + (p.KH - 1) * p.dh + 1;
+  {
+    constexpr size_t kLdsCu = 160 * 1024;
+    const size_t plain = (size_t)2 * a.PY * a.NCX * VEC * (vr.cb + VEC) * es + 1024;
+    const size_t padded = (size_t)2 * a.PY * (a.NCX * VEC + row_pad) * (vr.cb + VEC) * es + 1024;
+    a.PXS = a.NCX * VEC + (kLdsCu / padded == kLdsCu / plain ? row_pad : 0);
   }
-  a.n_stages = n_cc * p.KD * a.n_rg;
+  a.patch_elems = a.PY * a.PXS * (vr.cb + VEC);
+  pl.lds = (size_t)2 * a.patch_elems * es;
+  {
+    const int maxc = (f32 ? vr.cb / 2 : vr.cb / 4) * (256 / pl.nthreads);  // PatchLoader::MAXC
+    if (pl.lds > 150 * 1024 || vr.cb * a.PY * a.NCX > maxc * pl.nthreads)
+      return fail(ATK_UNSUPPORTED, "conv %s: stage of %zu LDS bytes does not fit the variant", vr.name, pl.lds);
+  }
+  a.n_stages = n_cc * p.KD;
   pl.tiles = (int64_t)p.N * p.Do * a.tiles_y * a.tiles_x;
   const int co_tiles = (p.Co + pl.bn - 1) / pl.bn;
   if (pl.tiles > 0x7fffffff || co_tiles > 65535) return fail(ATK_UNSUPPORTED, "conv %s: grid too large", vr.name);
@@ -885,29 +705,6 @@ int launch_ig_t(const IgPlan& pl, hipStream_t s) {
                        : launch_ig_vr<T, WCO, WSP, FCO, FSP, CB, false, 0, 0>(pl, s);
 }
 
-template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, bool VR>
-int launch_ig2_vr(const IgPlan& pl, hipStream_t s) {
-  auto kern = conv_igemm2_kernel<T, WCO, WSP, FCO, FSP, CB, VR, IG2_WMAX>;
-  if (pl.lds > 64 * 1024) {
-    static bool raised = false;
-    if (!raised) {
-      if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
-                              150 * 1024) != hipSuccess)
-        return fail(ATK_UNSUPPORTED, "conv: cannot raise the LDS limit");
-      raised = true;
-    }
-  }
-  dim3 grid((unsigned)pl.tiles, (unsigned)((pl.a.Co + pl.bn - 1) / pl.bn), (unsigned)pl.splits);
-  hipLaunchKernelGGL(kern, grid, dim3(64 * WCO * WSP), pl.lds, s, pl.a);
-  return check_launch("conv_igemm2_kernel");
-}
-
-template <typename T, int WCO, int WSP, int FCO, int FSP, int CB>
-int launch_ig2_t(const IgPlan& pl, hipStream_t s) {
-  return pl.a.vec_rows ? launch_ig2_vr<T, WCO, WSP, FCO, FSP, CB, true>(pl, s)
-                       : launch_ig2_vr<T, WCO, WSP, FCO, FSP, CB, false>(pl, s);
-}
-
 template <typename T>
 int launch_ig(const ConvShape& p, const void* x, const void* w, const void* bias, void* y, int v,
               void* ws, size_t ws_bytes, hipStream_t s) {
@@ -934,33 +731,22 @@ int launch_ig(const ConvShape& p, const void* x, const void* w, const void* bias
   if constexpr (sizeof(T) == 2) {
     switch (v) {
       case 0: rc = launch_ig_t<T, 2, 2, 2, 2, 32>(pl, s); break;
-      case 1: rc = launch_ig_t<T, 2, 2, 4, 2, 32>(pl, s); break;
-      case 2: rc = launch_ig_t<T, 2, 2, 2, 4, 32>(pl, s); break;
-      case 3: rc = launch_ig_t<T, 1, 4, 2, 2, 32>(pl, s); break;
-      case 4: rc = launch_ig_t<T, 2, 2, 2, 2, 16>(pl, s); break;
-      case 5: rc = launch_ig_t<T, 4, 1, 2, 4, 32>(pl, s); break;
-      case 6: rc = launch_ig_t<T, 4, 1, 2, 2, 32>(pl, s); break;
-      case 7: rc = launch_ig_t<T, 2, 1, 2, 4, 32>(pl, s); break;
-      case 8: rc = launch_ig_t<T, 2, 2, 1, 2, 32>(pl, s); break;
-      case 9: rc = launch_ig_t<T, 2, 1, 1, 4, 32>(pl, s); break;
-      case 14: rc = launch_ig2_t<T, 2, 2, 2, 4, 16>(pl, s); break;
-      case 15: rc = launch_ig2_t<T, 2, 2, 2, 4, 32>(pl, s); break;
-      case 16: rc = launch_ig2_t<T, 2, 2, 2, 2, 32>(pl, s); break;
-      case 17: rc = launch_ig2_t<T, 1, 4, 2, 2, 32>(pl, s); break;
-      case 18: rc = launch_ig2_t<T, 1, 2, 2, 4, 32>(pl, s); break;
-      case 19: rc = launch_ig2_t<T, 2, 2, 4, 2, 16>(pl, s); break;
-      case 22: rc = launch_ig_t<T, 2, 2, 2, 4, 16>(pl, s); break;
-      case 23: rc = launch_ig_t<T, 4, 1, 2, 4, 16>(pl, s); break;
+      case 1: rc = launch_ig_t<T, 2, 2, 2, 4, 32>(pl, s); break;
+      case 2: rc = launch_ig_t<T, 1, 4, 2, 2, 32>(pl, s); break;
+      case 3: rc = launch_ig_t<T, 2, 2, 2, 2, 16>(pl, s); break;
+      case 4: rc = launch_ig_t<T, 4, 1, 2, 2, 32>(pl, s); break;
+      case 5: rc = launch_ig_t<T, 2, 1, 2, 4, 32>(pl, s); break;
+      case 6: rc = launch_ig_t<T, 2, 2, 1, 2, 32>(pl, s); break;
+      case 7: rc = launch_ig_t<T, 2, 1, 1, 4, 32>(pl, s); break;
+      case 8: rc = launch_ig_t<T, 2, 2, 2, 4, 16>(pl, s); break;
       default: return fail(ATK_EINVAL, "conv: bad variant");
     }
   } else {
     switch (v) {
-      case 10: rc = launch_ig_t<T, 2, 2, 2, 2, 16>(pl, s); break;
-      case 11: rc = launch_ig_t<T, 1, 4, 2, 2, 16>(pl, s); break;
-      case 12: rc = launch_ig_t<T, 2, 2, 1, 2, 16>(pl, s); break;
-      case 13: rc = launch_ig_t<T, 2, 1, 1, 4, 16>(pl, s); break;
-      case 20: rc = launch_ig2_t<T, 2, 2, 2, 2, 16>(pl, s); break;
-      case 21: rc = launch_ig2_t<T, 1, 2, 2, 4, 16>(pl, s); break;
+      case 9: rc = launch_ig_t<T, 2, 2, 2, 2, 16>(pl, s); break;
+      case 10: rc = launch_ig_t<T, 1, 4, 2, 2, 16>(pl, s); break;
+      case 11: rc = launch_ig_t<T, 2, 2, 1, 2, 16>(pl, s); break;
+      case 12: rc = launch_ig_t<T, 2, 1, 1, 4, 16>(pl, s); break;
       default: return fail(ATK_EINVAL, "conv: bad variant");
     }
   }
