@@ -148,6 +148,37 @@ def bench_dw_detail(dtype, mode, dev):
 # ---------------------------------------------------------------------------
 # configs 3 / 5: GroupNorm
 # ---------------------------------------------------------------------------
+def bench_dw_backward_detail(dev):
+    """Backward of the headline (causal, stock output shape, bf16): dx through the forward
+    kernel with reversed weights, dw / db through the streaming reduction kernel.
+    Algorithmic bytes: dy read twice (once per kernel), x read once, dx written once."""
+    import torch
+    from amd_tuned_torch import _native as nat
+    x, w, b = c2_inputs(torch.bfloat16, 4, dev)
+    N, C, L = x.shape
+    K, pad = 4, 3
+    w2 = w.squeeze(1).contiguous()
+    g = _gen(1005)
+    dy = torch.randn(N, C, L + K - 1, generator=g).to(torch.bfloat16).to(dev)
+    dx, dw, db = nat.dwconv1d_backward(dy, x, w2, pad, (True, True, True))
+    xp = torch.nn.functional.pad(x, (pad, 0))
+    sdx, sdw, sdb = torch.ops.aten.convolution_backward(dy, xp, w, [C], [1], [0], [1], False, [0], C,
+                                                        [True, True, True])
+    sdx = sdx[..., pad:]
+    err = max(max_rel_err(dx, sdx.float()), max_rel_err(dw.reshape(C, 1, K), sdw.float()),
+              max_rel_err(db, sdb.float()))
+    del dx, dw, db, sdx, sdw, sdb
+    ms = graph_time_ms(lambda: nat.dwconv1d_backward(dy, x, w2, pad, (True, True, True)), 10)
+    stock_ms = event_time_ms(lambda: torch.ops.aten.convolution_backward(
+        dy, xp, w, [C], [1], [0], [1], False, [0], C, [True, True, True]), 3)
+    nbytes = x.element_size() * N * C * (2 * (L + K - 1) + 2 * L)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"ms": round(ms, 4), "GB/s": round(gbs, 1), "roofline_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "variant": "native.xlane(dx) + dwconv1d_bwd_w_kernel(dw, db)",
+            "stock_convolution_backward_ms": round(stock_ms, 3),
+            "max_rel_err_vs_stock": float(f"{err:.3g}")}
+
+
 def bench_gn_detail(shape, G, eps, dtype, silu, dev):
     import torch
     import torch.nn.functional as F
@@ -510,6 +541,7 @@ def main():
             ("c2_causal_fp16", lambda: bench_dw_detail(torch.float16, "causal", dev)),
             ("c2_sym_k3_bf16", lambda: bench_dw_detail(torch.bfloat16, "sym", dev)),
             ("c2_sym_k3_fp16", lambda: bench_dw_detail(torch.float16, "sym", dev)),
+            ("c2_causal_backward_bf16", lambda: bench_dw_backward_detail(dev)),
         ]
         for dt_name, dtype in (("fp16", torch.float16), ("bf16", torch.bfloat16)):
             for silu in (False, True):

@@ -84,11 +84,30 @@ const char* atk_variant_name(int op, int variant);
  * x: [N, C, L], w: [C, K], bias: [C] or NULL, y: [N, C, L_out]; all of `dtype`.
  * Accumulation is fp32 for every dtype.  fuse_silu != 0 applies y*sigmoid(y)
  * before the store (the causal kernel's `silu_activation` flag).
- * K in [1, 64]; pad_left in [0, 64].  variant < 0 picks the default.
+ * K in [1, 64]; pad_left in [0, 64].  variant < 0 takes the first of xlane,
+ * lds_opt32_nt, lds_opt16, direct that accepts the shape.
  * ------------------------------------------------------------------------- */
 int atk_dwconv1d_fwd(const void* x, const void* w, const void* bias, void* y,
                      int64_t N, int64_t C, int64_t L, int K, int pad_left, int64_t L_out,
                      int dtype, int fuse_silu, int variant, atk_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Depthwise / causal conv1d backward, weight and bias gradients (replaces the
+ * dweight / dbias half of `conv1d_backward(dout, u, weight, bias, padding, is_bhl)`,
+ * amd_tuned_torch/_vendor/flashfftconv_depthwise_conv1d/conv1d_bwd_hip_bhl.hip:
+ * 78-116, and of `causal_conv1d_bwd(x, weight, bias, dout, ...)`,
+ * src/causal-conv1d-amd/csrc/causal_conv1d.cpp:240-380):
+ *   dw[c,k] = sum_{n,t} dy[n,c,t] * x[n,c,t-pad_left+k],  db[c] = sum_{n,t} dy[n,c,t].
+ * x: [N, C, L], dy: [N, C, L_out], both of `dtype`; dw: [C, K] fp32, db: [C] fp32 or
+ * NULL.  The input gradient is atk_dwconv1d_fwd run on dy with the weights reversed
+ * along K and pad_left' = K-1-pad_left (output length L).  K in [1, 5].  The
+ * workspace (atk_dwconv1d_bwd_weight_workspace_bytes) holds per-row partials; it
+ * needs no initialisation.  Sums over n are taken in a fixed order (deterministic).
+ * ------------------------------------------------------------------------- */
+size_t atk_dwconv1d_bwd_weight_workspace_bytes(int64_t N, int64_t C, int K);
+int atk_dwconv1d_bwd_weight(const void* x, const void* dy, float* dw, float* db,
+                            int64_t N, int64_t C, int64_t L, int K, int pad_left, int64_t L_out,
+                            int dtype, void* workspace, size_t ws_bytes, atk_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * GroupNorm forward, NC[spatial] layout (replaces `group_norm(input, num_groups,

@@ -34,6 +34,49 @@ void oracle_dwconv1d(const double* x, const double* w, const double* b, double* 
     }
 }
 
+/* Gradients of oracle_dwconv1d (no SiLU) for an upstream gradient dy [N, C, L_out], in
+ * the form of the reference's depthwise backward (amd_tuned_torch/_vendor/
+ * flashfftconv_depthwise_conv1d/conv1d_bwd_hip_bhl.hip:39-57 correlates dout with the
+ * reversed kernel for du; :62-116 builds dk and sums dk . dout over the batch for
+ * dweight and dout over batch and length for dbias; the causal form is
+ * src/causal-conv1d-amd/csrc/causal_conv1d_bwd.cu:100-235):
+ *   dx[n,c,s] = sum_j w[c,j] * dy[n,c,s+pad_left-j]     (dy = 0 outside [0, L_out))
+ *   dw[c,j]   = sum_{n,t} dy[n,c,t] * x[n,c,t-pad_left+j] (x = 0 outside [0, L))
+ *   db[c]     = sum_{n,t} dy[n,c,t]
+ * Any of dx / dw / db may be NULL. */
+void oracle_dwconv1d_bwd(const double* x, const double* w, const double* dy, double* dx, double* dw,
+                         double* db, int64_t N, int64_t C, int64_t L, int64_t K, int64_t pad_left,
+                         int64_t L_out) {
+  if (dw)
+    for (int64_t i = 0; i < C * K; ++i) dw[i] = 0.0;
+  if (db)
+    for (int64_t c = 0; c < C; ++c) db[c] = 0.0;
+  for (int64_t n = 0; n < N; ++n)
+    for (int64_t c = 0; c < C; ++c) {
+      const double* xr = x + (n * C + c) * L;
+      const double* gr = dy + (n * C + c) * L_out;
+      if (dx) {
+        double* dr = dx + (n * C + c) * L;
+        for (int64_t s = 0; s < L; ++s) {
+          double acc = 0.0;
+          for (int64_t j = 0; j < K; ++j) {
+            const int64_t t = s + pad_left - j;
+            if (t >= 0 && t < L_out) acc += w[c * K + j] * gr[t];
+          }
+          dr[s] = acc;
+        }
+      }
+      for (int64_t t = 0; t < L_out; ++t) {
+        if (db) db[c] += gr[t];
+        if (dw)
+          for (int64_t j = 0; j < K; ++j) {
+            const int64_t p = t - pad_left + j;
+            if (p >= 0 && p < L) dw[c * K + j] += gr[t] * xr[p];
+          }
+      }
+    }
+}
+
 /* GroupNorm over NC[S] (src/cuda/group_norm.cu:41-104; fused SiLU of
  * amd_tuned_torch/conv_fusion_ops.py:192-242): group (n, g) = channels [g*C/G, (g+1)*C/G)
  * x all S positions; population variance (divide by the group size), eps inside the

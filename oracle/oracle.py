@@ -43,6 +43,7 @@ def lib():
         L = ctypes.CDLL(LIB)
         d, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
         L.oracle_dwconv1d.argtypes = [d, d, d, d, i64, i64, i64, i64, i64, i64, i32]
+        L.oracle_dwconv1d_bwd.argtypes = [d, d, d, d, d, d, i64, i64, i64, i64, i64, i64]
         L.oracle_group_norm.argtypes = [d, d, d, d, i64, i64, i64, i64, ctypes.c_double, i32, d, d]
         L.oracle_conv3d.argtypes = [d, d, d, d] + [i64] * 18 + [d, i64]
         _lib = L
@@ -75,6 +76,21 @@ def dwconv1d(x, w, b, pad_left: int, l_out: int, silu: bool = False) -> np.ndarr
     lib().oracle_dwconv1d(_p(x), _p(w), _p(b), _p(y), N, C, L, w.shape[1], pad_left, l_out,
                           int(bool(silu)))
     return y
+
+
+def dwconv1d_bwd(x, w, dy, pad_left: int):
+    """(dx [N,C,L], dw [C,K], db [C]) of dwconv1d(x, w, b, pad_left, L_out) for the upstream
+    gradient dy [N,C,L_out]; w [C,K] or [C,1,K]."""
+    x, w, dy = f64(x), f64(w), f64(dy)
+    N, C, L = x.shape
+    w = w.reshape(C, -1)
+    K = w.shape[1]
+    dx = np.empty_like(x)
+    dw = np.empty((C, K), dtype=np.float64)
+    db = np.empty((C,), dtype=np.float64)
+    lib().oracle_dwconv1d_bwd(_p(x), _p(w), _p(dy), _p(dx), _p(dw), _p(db), N, C, L, K, pad_left,
+                              dy.shape[-1])
+    return dx, dw, db
 
 
 def conv1d_out_len(length: int, padding: int, width: int) -> int:

@@ -34,7 +34,8 @@ _DTYPE_CODE = {torch.float32: ATK_F32, torch.float16: ATK_F16, torch.bfloat16: A
 # Every symbol the header declares (include/amd_tuned_torch_hip.h).
 EXPORTED_SYMBOLS = (
     "atk_abi_version", "atk_last_error", "atk_num_variants", "atk_variant_name",
-    "atk_dwconv1d_fwd", "atk_group_norm_workspace_bytes",
+    "atk_dwconv1d_fwd", "atk_dwconv1d_bwd_weight_workspace_bytes", "atk_dwconv1d_bwd_weight",
+    "atk_group_norm_workspace_bytes",
     "atk_group_norm_workspace_zero_bytes", "atk_group_norm_fwd", "atk_conv_workspace_bytes",
     "atk_conv_fwd",
 )
@@ -59,6 +60,10 @@ def _declare(lib) -> None:
     lib.atk_variant_name.restype = c.c_char_p
     lib.atk_dwconv1d_fwd.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, i32, i64, i32, i32, i32, vp]
     lib.atk_dwconv1d_fwd.restype = i32
+    lib.atk_dwconv1d_bwd_weight_workspace_bytes.argtypes = [i64, i64, i32]
+    lib.atk_dwconv1d_bwd_weight_workspace_bytes.restype = sz
+    lib.atk_dwconv1d_bwd_weight.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, i32, i64, i32, vp, sz, vp]
+    lib.atk_dwconv1d_bwd_weight.restype = i32
     lib.atk_group_norm_workspace_bytes.argtypes = [i64, i64, i64, i32, i32, i32]
     lib.atk_group_norm_workspace_bytes.restype = sz
     lib.atk_group_norm_workspace_zero_bytes.argtypes = [i64, i64, i64, i32, i32, i32]
@@ -224,6 +229,55 @@ def dwconv1d(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]
                                 l_out, _DTYPE_CODE[x.dtype], int(bool(silu)), variant, _stream(x))
     _check(rc, "dwconv1d")
     return y
+
+
+def dwconv1d_bwd_weight(x: torch.Tensor, dy: torch.Tensor, K: int, pad_left: int,
+                        with_bias: bool = True):
+    """Weight and bias gradients of dwconv1d, fp32: dw [C, K], db [C] (None without bias).
+    x [N,C,L] and dy [N,C,L_out] contiguous, same dtype.  Raises Unsupported for K > 5."""
+    _require_cuda(x, dy)
+    if x.dim() != 3 or dy.dim() != 3 or dy.shape[:2] != x.shape[:2]:
+        raise RuntimeError("dwconv1d_bwd_weight expects x [N, C, L] and dy [N, C, L_out]")
+    if x.dtype not in _DTYPE_CODE or dy.dtype != x.dtype:
+        raise RuntimeError("dwconv1d_bwd_weight: x and dy must share a float16/bfloat16/float32 dtype")
+    if not (x.is_contiguous() and dy.is_contiguous()):
+        raise RuntimeError("dwconv1d_bwd_weight: x and dy must be contiguous")
+    N, C, L = x.shape
+    l_out = dy.shape[-1]
+    dw = torch.empty((C, K), dtype=torch.float32, device=x.device)
+    db = torch.empty((C,), dtype=torch.float32, device=x.device) if with_bias else None
+    if N == 0:
+        dw.zero_()
+        if db is not None:
+            db.zero_()
+        return dw, db
+    L_ = lib()
+    nbytes = L_.atk_dwconv1d_bwd_weight_workspace_bytes(N, C, K)
+    ws = workspace(x.device, "dwconv1d_bwd", nbytes)
+    rc = L_.atk_dwconv1d_bwd_weight(_ptr(x), _ptr(dy), _ptr(dw), _ptr(db), N, C, L, K, pad_left, l_out,
+                                    _DTYPE_CODE[x.dtype], _ptr(ws), ws.numel(), _stream(x))
+    _check(rc, "dwconv1d_bwd_weight")
+    return dw, db
+
+
+def dwconv1d_backward(dy: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, pad_left: int,
+                      needs=(True, True, False)):
+    """(dx, dw, db) of y = dwconv1d(x, weight, bias, pad_left, L_out) for dy [N,C,L_out]:
+    dx is the forward kernel run on dy with the weights reversed along K and
+    pad_left' = K-1-pad_left (output length L); dw [C,K] and db [C] come back in fp32.
+    Entries not asked for in `needs` are None.  Raises Unsupported when pad_left > K-1
+    (dx) or K > 5 (dw, db)."""
+    K = weight.shape[-1]
+    dx = dw = db = None
+    if needs[0]:
+        if pad_left > K - 1:
+            raise Unsupported("dwconv1d_backward: pad_left > K-1 has no forward-kernel form")
+        dx = dwconv1d(dy, weight.reshape(weight.shape[0], K).flip(-1), None, K - 1 - pad_left, x.shape[-1])
+    if needs[1] or needs[2]:
+        dw, db = dwconv1d_bwd_weight(x, dy, K, pad_left, with_bias=bool(needs[2]))
+        if not needs[1]:
+            dw = None
+    return dx, dw, db
 
 
 def conv1d_forward(u: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, padding: int,

@@ -5,8 +5,10 @@ Interface of the reference's depthwise_conv1d_ops (amd_tuned_torch/depthwise_con
 `amd_tuned_torch::depthwise_conv1d_forward/backward` with fake (meta) implementations,
 `conv1d_forward`/`conv1d_backward`, `DepthwiseConv1dFn` and `depthwise_conv1d_candidate`.
 The forward runs this package's gfx950 kernel (any width K <= 64, fp32 accumulation); the
-reference's kernel only accepted odd K (conv1d.h:76).  The backward is stock PyTorch
-(aten.convolution_backward), not a native kernel.
+reference's kernel only accepted odd K (conv1d.h:76).  The backward is native too
+(`_native.dwconv1d_backward`: du through the forward kernel with reversed weights, dweight /
+dbias through one streaming reduction kernel) where it applies -- K <= 5 for the weight
+gradient, padding <= K-1 for du -- and stock aten.convolution_backward for the rest.
 """
 from __future__ import annotations
 
@@ -34,14 +36,44 @@ def _out_len(length: int, padding: int, width: int) -> int:
     return length + 2 * padding - width + 1
 
 
-def _stock_backward(dout, input_, weight, bias, padding: int, is_bhl: bool):
+def _stock_backward(dout, input_, weight, bias, padding: int, is_bhl: bool, needs=(True, True, True)):
     if not is_bhl:
         raise RuntimeError("depthwise_conv1d_backward: only the (B, C, L) layout is built")
     C, K = weight.shape
     du, dw, db = torch.ops.aten.convolution_backward(
         dout.contiguous(), input_, weight.unsqueeze(1), [C], [1], [padding], [1], False, [0], C,
-        [True, True, True])
-    return du, dw.reshape(C, K).to(weight.dtype), db.to(dout.dtype)
+        list(needs))
+    return (du, None if dw is None else dw.reshape(C, K).to(weight.dtype),
+            None if db is None else db.to(dout.dtype))
+
+
+def _backward(dout, input_, weight, bias, padding: int, is_bhl: bool):
+    """(du, dweight, dbias) of conv1d_forward (conv1d_bwd_hip_bhl.hip:78-116 semantics:
+    dweight in weight's dtype, dbias in dout's dtype): each part native where the library
+    serves it, the rest stock."""
+    if not is_bhl:
+        raise RuntimeError("depthwise_conv1d_backward: only the (B, C, L) layout is built")
+    du = dw = db = None
+    if input_.is_cuda and _native.available():
+        dout = dout.contiguous()
+        K = weight.shape[-1]
+        try:
+            if padding <= K - 1:
+                du = _native.dwconv1d_backward(dout, input_, weight, padding, (True, False, False))[0]
+        except _native.Unsupported:
+            du = None
+        try:
+            _, dw32, db32 = _native.dwconv1d_backward(dout, input_, weight, padding, (False, True, True))
+            dw, db = dw32.to(weight.dtype), db32.to(dout.dtype)
+        except _native.Unsupported:
+            dw = db = None
+    if du is None or dw is None:
+        su, sw, sb = _stock_backward(dout, input_, weight, bias, padding, is_bhl,
+                                     (du is None, dw is None, dw is None))
+        du = su if du is None else du
+        if dw is None:
+            dw, db = sw, sb
+    return du, dw, db
 
 
 def _already_registered(name: str) -> bool:
@@ -68,7 +100,7 @@ if hasattr(torch.library, "custom_op") and not _already_registered("depthwise_co
     def _bwd_op(dout: torch.Tensor, input_: torch.Tensor, weight: torch.Tensor,
                 bias: torch.Tensor, padding: int, is_bhl: bool
                 ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-        du, dw, db = _stock_backward(dout, input_, weight, bias, padding, is_bhl)
+        du, dw, db = _backward(dout, input_, weight, bias, padding, is_bhl)
         return du.contiguous(), dw.contiguous(), db.contiguous()
 
     @_bwd_op.register_fake
@@ -87,7 +119,7 @@ else:
         return _native.conv1d_forward(input_, weight, bias, padding, is_bhl)
 
     def _bwd_impl(dout, input_, weight, bias, padding, is_bhl):
-        return _stock_backward(dout, input_, weight, bias, padding, is_bhl)
+        return _backward(dout, input_, weight, bias, padding, is_bhl)
 
 
 def conv1d_forward(input: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, padding: int,

@@ -106,7 +106,7 @@ def _is_oom(exc: BaseException) -> bool:
 def _reference_scale(reference_out) -> Optional[float]:
     """RMS of a strided sample of the reference output (None if not measurable)."""
     try:
-        flat = reference_out.flatten()
+        flat = reference_out.detach().flatten()
         step = max(1, flat.numel() // _VERIFY_SCALE_SAMPLE)
         rms = float(flat[::step].float().pow(2).mean().sqrt())
     except (RuntimeError, TypeError, ValueError, AttributeError, ZeroDivisionError):
@@ -119,6 +119,7 @@ def _verify(candidate_out, reference_out, tolerance=None) -> Optional[bool]:
     memory).  A comparison that cannot run for a reason about the candidate (shape, type)
     is a failure, never a pass."""
     try:
+        candidate_out, reference_out = candidate_out.detach(), reference_out.detach()
         rtol, atol = tolerance if tolerance is not None else _TOLERANCES.get(
             candidate_out.dtype, _DEFAULT_TOLERANCE)
         scale = _reference_scale(reference_out)

@@ -125,7 +125,10 @@ def _is_depthwise_conv1d_eligible(input, weight, bias, stride, padding, dilation
 
 
 class _DwConv1dFn(torch.autograd.Function):
-    """Native forward, stock backward (aten.convolution_backward)."""
+    """Native forward; native backward where the library serves it (input gradient through
+    the forward kernel with reversed weights when pad_left <= K-1, weight and bias gradients
+    through the streaming reduction kernel when K <= 5), stock aten.convolution_backward for
+    the rest."""
 
     @staticmethod
     def forward(ctx, input, weight, bias, pad_left, l_out, variant):
@@ -139,13 +142,43 @@ class _DwConv1dFn(torch.autograd.Function):
         input, weight = ctx.saved_tensors
         C, _, K = weight.shape
         L = input.shape[-1]
+        needs = [bool(ctx.needs_input_grad[0]), bool(ctx.needs_input_grad[1]),
+                 ctx.has_bias and bool(ctx.needs_input_grad[2])]
+        gi = gw = gb = None
+        if dout.is_cuda and _native.available():
+            dout = dout.contiguous()
+            x = input.detach()
+            if needs[0] and ctx.pad_left <= K - 1:
+                try:
+                    gi = _native.dwconv1d_backward(dout, x, weight.detach(), ctx.pad_left,
+                                                   (True, False, False))[0]
+                    needs[0] = False
+                except _native.Unsupported:
+                    pass
+            if needs[1] or needs[2]:
+                try:
+                    _, dw32, db32 = _native.dwconv1d_backward(dout, x, weight.detach(), ctx.pad_left,
+                                                              (False, needs[1], needs[2]))
+                    gw = None if dw32 is None else dw32.to(weight.dtype).view(C, 1, K)
+                    gb = None if db32 is None else db32.to(dout.dtype)
+                    needs[1] = needs[2] = False
+                except _native.Unsupported:
+                    pass
+            if not any(needs):
+                return gi, gw, gb, None, None, None
+        sgi, sgw, sgb = _DwConv1dFn._stock_backward(ctx, dout, input, weight, needs)
+        return (gi if gi is not None else sgi, gw if gw is not None else sgw,
+                gb if gb is not None else sgb, None, None, None)
+
+    @staticmethod
+    def _stock_backward(ctx, dout, input, weight, needs):
+        C, _, K = weight.shape
+        L = input.shape[-1]
         # stock semantics of a left-pad / right-crop: pad so the stock conv spans l_out
         pad_right = ctx.l_out - (L + ctx.pad_left - K + 1)
         xin = torch.nn.functional.pad(input.detach(), (ctx.pad_left, max(0, pad_right)))
         if pad_right < 0:
             xin = xin[..., :xin.shape[-1] + pad_right]
-        needs = [bool(ctx.needs_input_grad[0]), bool(ctx.needs_input_grad[1]),
-                 ctx.has_bias and bool(ctx.needs_input_grad[2])]
         gi, gw, gb = torch.ops.aten.convolution_backward(
             dout.contiguous(), xin, weight, [C] if ctx.has_bias else None, [1], [0], [1], False,
             [0], C, needs)
@@ -153,7 +186,7 @@ class _DwConv1dFn(torch.autograd.Function):
             gi = gi[..., ctx.pad_left:ctx.pad_left + L]
             if gi.shape[-1] < L:
                 gi = torch.nn.functional.pad(gi, (0, L - gi.shape[-1]))
-        return gi, gw, gb, None, None, None
+        return gi, gw, gb
 
 
 def _dw_call(input, weight, bias, pad_left, l_out, variant):

@@ -23,6 +23,8 @@
 //     fp32 and read as broadcasts.
 // A "direct" variant (one output per thread, global loads, no LDS) covers shapes whose
 // LDS window would not fit.
+#include <cstring>
+
 #include "atk_common.h"
 
 namespace atk {
@@ -733,6 +735,91 @@ int launch_dw(DwArgs a, int variant, hipStream_t s) {
   }
 }
 
+// ---------------------------------------------------------------------------------------
+// Backward.  The input gradient needs no kernel of its own: dx[s] = sum_k w[k] dy[s+pad-k]
+// is the forward kernel run on dy with w'[j] = w[K-1-j] and pad' = K-1-pad (the identity
+// the reference's backward uses, _vendor/flashfftconv_depthwise_conv1d/
+// conv1d_bwd_hip_bhl.hip:39-57).  The weight and bias gradients
+//   dw[c,k] = sum_{n,t} dy[n,c,t] * x[n,c,t-pad+k],   db[c] = sum_{n,t} dy[n,c,t]
+// are one streaming pass over x and dy: a workgroup per (n, c) row reduces its row into
+// K+1 fp32 partials, a finalize kernel sums the partials over n in a fixed order.  Both
+// windows (dy's VEC outputs, x's VEC+K-1 inputs) are cut from aligned 16-byte blocks as in
+// the register kernel, so rows need not be 16-byte aligned (the stock-shaped causal dy).
+// HBM traffic: one read of x and one of dy; the reference materialises dk[B,C,K,L] and
+// multiplies it with dy (conv1d_bwd_hip_bhl.hip:62-116).
+struct DwBwdArgs {
+  const void* x;
+  const void* dy;
+  float* part;        // [N*C][K+1]
+  uint32_t L, Lout;
+  int pad;
+  int x_off, dy_off;  // misalignment of the x / dy base pointers, in elements
+  int64_t total_in, total_out;
+};
+
+template <typename T, int KT>
+__global__ __launch_bounds__(DW_NT) void dwconv1d_bwd_w_kernel(DwBwdArgs a) {
+  using Win = DwWindow<T, KT>;
+  using Dyw = DwWindow<T, 1>;
+  constexpr int VEC = Win::VEC, WN = Win::WN;
+  __shared__ float red[DW_NT / 64];
+  const uint32_t r = blockIdx.x;  // row n*C + c
+  const uint32_t L = a.L, Lout = a.Lout;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(
+      static_cast<const T*>(a.x) - a.x_off, (uint32_t)((a.total_in + a.x_off + VEC - 1) / VEC * 16));
+  const __amdgpu_buffer_rsrc_t rd = make_rsrc(
+      static_cast<const T*>(a.dy) - a.dy_off, (uint32_t)((a.total_out + a.dy_off + VEC - 1) / VEC * 16));
+  float acc[KT + 1];
+#pragma unroll
+  for (int k = 0; k <= KT; ++k) acc[k] = 0.f;
+  for (uint32_t t = threadIdx.x * VEC; t < Lout; t += DW_NT * VEC) {
+    uint32_t DD[4 * Dyw::NBLK], DX[4 * Win::NBLK];
+    int md, mx;
+    Dyw::fetch(rd, (int)(r * Lout + t) + a.dy_off, true, DD, md);
+    Win::fetch(rx, (int)(r * L + t) - a.pad + a.x_off, true, DX, mx);
+    float dv[VEC], xv[WN];
+    Dyw::extract(DD, md, (int)t, Lout, dv);       // zero past the row end
+    Win::extract(DX, mx, (int)t - a.pad, L, xv);  // zero outside [0, L)
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      acc[KT] += dv[e];
+#pragma unroll
+      for (int k = 0; k < KT; ++k) acc[k] = fmaf(dv[e], xv[e + k], acc[k]);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k <= KT; ++k) {
+    const float v = block_sum<DW_NT>(acc[k], red);
+    if (threadIdx.x == 0) a.part[(int64_t)r * (KT + 1) + k] = v;
+  }
+}
+
+// dw[c,k] (k < K) and db[c] (k == K) = sum over n of the row partials, n in order.
+__global__ __launch_bounds__(256) void dwconv1d_bwd_finalize_kernel(const float* __restrict__ part, float* __restrict__ dw,
+                                                                    float* __restrict__ db, int N, int C, int K) {
+  const int i = blockIdx.x * 256 + threadIdx.x;  // c * (K+1) + k
+  if (i >= C * (K + 1)) return;
+  const int c = i / (K + 1), k = i - c * (K + 1);
+  float s = 0.f;
+  for (int n = 0; n < N; ++n) s += part[((int64_t)n * C + c) * (K + 1) + k];
+  if (k < K) dw[c * K + k] = s;
+  else if (db) db[c] = s;
+}
+
+template <typename T>
+int launch_dw_bwd_w(const DwBwdArgs& a, int64_t rows, int K, hipStream_t s) {
+  const dim3 grid((unsigned)rows), block(DW_NT);
+  switch (K) {
+    case 1: hipLaunchKernelGGL((dwconv1d_bwd_w_kernel<T, 1>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((dwconv1d_bwd_w_kernel<T, 2>), grid, block, 0, s, a); break;
+    case 3: hipLaunchKernelGGL((dwconv1d_bwd_w_kernel<T, 3>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((dwconv1d_bwd_w_kernel<T, 4>), grid, block, 0, s, a); break;
+    case 5: hipLaunchKernelGGL((dwconv1d_bwd_w_kernel<T, 5>), grid, block, 0, s, a); break;
+    default: return fail(ATK_UNSUPPORTED, "dwconv1d backward: K %d outside [1, 5]", K);
+  }
+  return check_launch("dwconv1d_bwd_w_kernel");
+}
+
 }  // namespace
 
 int dwconv1d_num_variants() { return kNumDw; }
@@ -751,7 +838,6 @@ extern "C" int atk_dwconv1d_fwd(const void* x, const void* w, const void* bias, 
   if (N < 0 || C <= 0 || L < 0 || L_out < 0) return fail(ATK_EINVAL, "dwconv1d: bad sizes");
   if (K < 1 || K > DW_KMAX) return fail(ATK_UNSUPPORTED, "dwconv1d: kernel width %d outside [1, %d]", K, DW_KMAX);
   if (pad_left < 0 || pad_left > DW_PADMAX) return fail(ATK_UNSUPPORTED, "dwconv1d: padding %d outside [0, %d]", pad_left, DW_PADMAX);
-  if (variant < 0) variant = 0;
   if (variant >= kNumDw) return fail(ATK_EINVAL, "dwconv1d: variant %d out of range", variant);
   const int64_t total_out = N * C * L_out;
   if (total_out == 0) return ATK_OK;
@@ -777,9 +863,70 @@ extern "C" int atk_dwconv1d_fwd(const void* x, const void* w, const void* bias, 
   // fdiv() needs numerators below 2^31: row-relative offsets stay below L_out + tile.
   if ((uint64_t)L_out + 65536 >= (1ull << 31)) return fail(ATK_UNSUPPORTED, "dwconv1d: L_out too large");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  switch (dtype) {
-    case ATK_F32: return launch_dw<float>(a, variant, s);
-    case ATK_F16: return launch_dw<_Float16>(a, variant, s);
-    default: return launch_dw<__bf16>(a, variant, s);
+  auto run = [&](int v) {
+    switch (dtype) {
+      case ATK_F32: return launch_dw<float>(a, v, s);
+      case ATK_F16: return launch_dw<_Float16>(a, v, s);
+      default: return launch_dw<__bf16>(a, v, s);
+    }
+  };
+  if (variant >= 0) return run(variant);
+  // default: the first of these that takes the shape (a declining variant enqueues nothing)
+  for (const char* name : {"xlane", "lds_opt32_nt", "lds_opt16", "direct"}) {
+    int v = 0;
+    while (v < kNumDw && std::strcmp(kDwVariants[v].name, name) != 0) ++v;
+    const int rc = run(v);
+    if (rc != ATK_UNSUPPORTED) return rc;
   }
+  return fail(ATK_UNSUPPORTED, "dwconv1d: no variant takes the shape");
+}
+
+extern "C" size_t atk_dwconv1d_bwd_weight_workspace_bytes(int64_t N, int64_t C, int K) {
+  if (N <= 0 || C <= 0 || K < 1) return 0;
+  return (size_t)N * (size_t)C * (size_t)(K + 1) * sizeof(float);
+}
+
+extern "C" int atk_dwconv1d_bwd_weight(const void* x, const void* dy, float* dw, float* db, int64_t N,
+                                       int64_t C, int64_t L, int K, int pad_left, int64_t L_out, int dtype,
+                                       void* workspace, size_t ws_bytes, atk_stream_t stream) {
+  using namespace atk;
+  if (!dtype_ok(dtype)) return fail(ATK_EINVAL, "dwconv1d backward: unknown dtype code %d", dtype);
+  if (N <= 0 || C <= 0 || L < 0 || L_out < 0) return fail(ATK_EINVAL, "dwconv1d backward: bad sizes");
+  if (K < 1 || K > 5) return fail(ATK_UNSUPPORTED, "dwconv1d backward: K %d outside [1, 5]", K);
+  if (pad_left < 0 || pad_left > DW_PADMAX)
+    return fail(ATK_UNSUPPORTED, "dwconv1d backward: padding %d outside [0, %d]", pad_left, DW_PADMAX);
+  if (!x || !dy || !dw) return fail(ATK_EINVAL, "dwconv1d backward: null pointer");
+  const size_t need = atk_dwconv1d_bwd_weight_workspace_bytes(N, C, K);
+  if (!workspace || ws_bytes < need) return fail(ATK_EINVAL, "dwconv1d backward: workspace of %zu bytes needed", need);
+  const size_t es = dtype_size(dtype);
+  const int64_t rows = N * C;
+  const int64_t vec = 16 / (int64_t)es;
+  // windows are addressed with 32-bit element offsets and 32-bit buffer byte ranges
+  if (rows >= (1ll << 31) || rows * L + vec >= (1ll << 31) / (int64_t)es ||
+      rows * L_out + vec >= (1ll << 31) / (int64_t)es)
+    return fail(ATK_UNSUPPORTED, "dwconv1d backward: tensor too large");
+  const uintptr_t xa = reinterpret_cast<uintptr_t>(x), da = reinterpret_cast<uintptr_t>(dy);
+  if ((xa % es) || (da % es)) return fail(ATK_EINVAL, "dwconv1d backward: misaligned element pointer");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // (L_out == 0 needs no special case: every row reduces nothing and the gradients are 0)
+  DwBwdArgs a;
+  a.x = x; a.dy = dy;
+  a.part = static_cast<float*>(workspace);
+  a.L = (uint32_t)L; a.Lout = (uint32_t)L_out;
+  a.pad = pad_left;
+  a.x_off = (int)((xa & 15u) / es);
+  a.dy_off = (int)((da & 15u) / es);
+  a.total_in = rows * L;
+  a.total_out = rows * L_out;
+  int rc;
+  switch (dtype) {
+    case ATK_F32: rc = launch_dw_bwd_w<float>(a, rows, K, s); break;
+    case ATK_F16: rc = launch_dw_bwd_w<_Float16>(a, rows, K, s); break;
+    default: rc = launch_dw_bwd_w<__bf16>(a, rows, K, s); break;
+  }
+  if (rc) return rc;
+  const int outs = (int)(C * (K + 1));
+  hipLaunchKernelGGL(dwconv1d_bwd_finalize_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s,
+                     a.part, dw, db, (int)N, (int)C, K);
+  return check_launch("dwconv1d_bwd_finalize_kernel");
 }

@@ -77,6 +77,13 @@ def test_argument_validation_codes(nat):
     assert lib.atk_dwconv1d_fwd(None, None, None, None, 1, 4, 16, 3, 1, 16, 0, 0, 0, None) == nat.ATK_EINVAL
     assert "null" in nat.last_error()
     assert lib.atk_dwconv1d_fwd(None, None, None, None, 0, 4, 16, 3, 1, 16, 0, 0, 0, None) == nat.ATK_OK
+    # dwconv1d backward (weight / bias gradients)
+    assert lib.atk_dwconv1d_bwd_weight_workspace_bytes(2, 3, 4) == 2 * 3 * 5 * 4
+    assert lib.atk_dwconv1d_bwd_weight_workspace_bytes(0, 3, 4) == 0
+    assert lib.atk_dwconv1d_bwd_weight(None, None, None, None, 1, 4, 16, 6, 1, 16, 0, None, 0, None) == nat.ATK_UNSUPPORTED
+    assert lib.atk_dwconv1d_bwd_weight(None, None, None, None, 1, 4, 16, 3, 1, 16, 0, None, 0, None) == nat.ATK_EINVAL
+    assert "null" in nat.last_error()
+    assert lib.atk_dwconv1d_bwd_weight(None, None, None, None, 1, 4, 16, 3, 1, 16, 7, None, 0, None) == nat.ATK_EINVAL
     # group norm
     assert lib.atk_group_norm_workspace_bytes(2, 6, 4, 4, 1, 0) == 0
     assert "divisible" in nat.last_error()

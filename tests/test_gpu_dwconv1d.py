@@ -146,3 +146,77 @@ def test_dwconv1d_config2_full_size(dev, dtype, mode):
     y = nat.dwconv1d(x.to(dev), w.to(dev), b.to(dev), pad, l_out)
     torch.cuda.synchronize()
     _check(y.cpu(), x, w, b, pad, l_out)
+
+
+# ---------------------------------------------------------------------------
+# backward: dx through the forward kernel (reversed weights), dw / db through the
+# streaming reduction kernel -- against the float64 oracle
+# ---------------------------------------------------------------------------
+BWD_BAR_W = {torch.float32: 1e-5, torch.float16: 1e-4, torch.bfloat16: 1e-4}  # fp32 dw/db from exact inputs
+
+BWD_CASES = [
+    (2, 3, 37, 3, 1, 37),        # symmetric
+    (2, 3, 37, 4, 3, 40),        # causal, stock output shape
+    (2, 3, 37, 4, 3, 37),        # causal, truncated
+    (2, 5, 64, 2, 1, 65),        # K = 2
+    (1, 4, 100, 5, 2, 100),      # K = 5
+    (1, 3, 40, 1, 0, 40),        # K = 1
+    (1, 2, 30, 3, 0, 28),        # 'valid'
+    (1, 8, 4096, 4, 3, 4099),    # long rows
+    (2, 4, 2500, 4, 3, 2503),    # long unaligned rows
+    (3, 7, 1, 3, 1, 1),          # L = 1
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("case", BWD_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_dwconv1d_backward_native(dev, case, dtype):
+    N, C, L, K, pad, l_out = case
+    nat = _native()
+    x, w, _ = _inputs(N, C, L, K, dtype, seed=sum(case) + 5)
+    dy = torch.randn(N, C, l_out, generator=torch.Generator().manual_seed(sum(case))).to(dtype)
+    dx, dw, db = nat.dwconv1d_backward(dy.to(dev), x.to(dev), w.to(dev), pad, (True, True, True))
+    torch.cuda.synchronize()
+    rdx, rdw, rdb = O.dwconv1d_bwd(x, w, dy, pad)
+    assert dx.dtype == dtype and dw.dtype == torch.float32 and db.dtype == torch.float32
+    assert O.max_rel_err(dx.cpu(), rdx) <= BAR[dtype]
+    assert O.max_rel_err(dw.cpu(), rdw) <= BWD_BAR_W[dtype]
+    assert O.max_rel_err(db.cpu(), rdb) <= BWD_BAR_W[dtype]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_dwconv1d_autograd_through_patched_conv1d(dev, dtype):
+    """Training path: the patched F.conv1d (causal stock shape and symmetric) with
+    requires_grad inputs runs the native forward and backward; gradients match the oracle."""
+    import torch.nn.functional as F
+    import amd_tuned_torch  # noqa: F401  (installs the patch)
+    for K, pad, trunc in ((4, 3, True), (4, 3, False), (3, 1, False)):
+        N, C, L = 2, 6, 300
+        x, w, b = _inputs(N, C, L, K, dtype, seed=11 + K + pad)
+        xd = x.to(dev).requires_grad_(True)
+        wd = w.to(dev).unsqueeze(1).requires_grad_(True)
+        bd = b.to(dev).requires_grad_(True)
+        y = F.conv1d(xd, wd, bd, padding=pad, groups=C)
+        if trunc:
+            y = y[..., :L]
+        dy = torch.randn(y.shape, generator=torch.Generator().manual_seed(K)).to(dtype)
+        gx, gw, gb = torch.autograd.grad(y, (xd, wd, bd), dy.to(dev))
+        rdx, rdw, rdb = O.dwconv1d_bwd(x, w, dy, pad)
+        assert O.max_rel_err(gx.cpu(), rdx) <= BAR[dtype]
+        assert O.max_rel_err(gw.cpu().reshape(C, K), rdw) <= BAR[dtype]
+        assert O.max_rel_err(gb.cpu(), rdb) <= BAR[dtype]
+
+
+def test_dwconv1d_backward_config2_full_size(dev):
+    """BASELINE config 2 at its full size, bf16 causal with the stock output shape: every
+    gradient element checked against the oracle."""
+    N, C, L, K, pad = 16, 2048, 8192, 4, 3
+    nat = _native()
+    x, w, _ = _inputs(N, C, L, K, torch.bfloat16, seed=2002)
+    dy = torch.randn(N, C, L + 3, generator=torch.Generator().manual_seed(2003)).to(torch.bfloat16)
+    dx, dw, db = nat.dwconv1d_backward(dy.to(dev), x.to(dev), w.to(dev), pad, (True, True, True))
+    torch.cuda.synchronize()
+    rdx, rdw, rdb = O.dwconv1d_bwd(x, w, dy, pad)
+    assert O.max_rel_err(dx.cpu(), rdx) <= BAR[torch.bfloat16]
+    assert O.max_rel_err(dw.cpu(), rdw) <= BWD_BAR_W[torch.bfloat16]
+    assert O.max_rel_err(db.cpu(), rdb) <= BWD_BAR_W[torch.bfloat16]

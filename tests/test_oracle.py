@@ -246,3 +246,57 @@ def test_max_rel_err_metric():
     """max|y - ref| / max|ref| (tools/bench_fast.py:147-162 of the reference)."""
     assert O.max_rel_err(np.array([1.0, 2.0, 4.5]), np.array([1.0, 2.0, 4.0])) == pytest.approx(0.125)
     assert O.max_rel_err(np.zeros(3), np.zeros(3)) == 0.0
+
+
+# ---------------------------------------------------------------------------
+# depthwise conv1d backward
+# ---------------------------------------------------------------------------
+def _stock_dw_grads(x, w, b, pad, l_out, dy):
+    """Gradients through stock F.conv1d (float64 autograd) of y = conv1d(pad both sides)[..., :l_out]."""
+    xt = torch.tensor(x, requires_grad=True)
+    wt = torch.tensor(w[:, None, :], requires_grad=True)
+    bt = torch.tensor(b, requires_grad=True)
+    K = w.shape[-1]
+    L = x.shape[-1]
+    right = max(0, l_out + K - 1 - L - pad)
+    y = F.conv1d(F.pad(xt, (pad, right)), wt, bt, groups=x.shape[1])[..., :l_out]
+    gx, gw, gb = torch.autograd.grad(y, (xt, wt, bt), torch.tensor(dy))
+    return gx.numpy(), gw.numpy()[:, 0, :], gb.numpy()
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 17, 3, 1, 17), (2, 3, 17, 4, 3, 20), (2, 3, 17, 4, 3, 17),
+                                   (1, 4, 9, 2, 1, 10), (1, 2, 12, 5, 2, 12), (1, 2, 8, 3, 0, 6)])
+def test_dwconv1d_bwd_matches_stock_autograd(shape):
+    """Symmetric, causal stock-shape, causal truncated, K=2/5 and 'valid' forms."""
+    N, C, L, K, pad, l_out = shape
+    rng = np.random.default_rng(sum(shape))
+    x, w, b = rng.normal(size=(N, C, L)), rng.normal(size=(C, K)), rng.normal(size=C)
+    dy = rng.normal(size=(N, C, l_out))
+    got = O.dwconv1d_bwd(x, w, dy, pad)
+    for a, r in zip(got, _stock_dw_grads(x, w, b, pad, l_out, dy)):
+        np.testing.assert_allclose(a, r, rtol=0, atol=1e-11)
+
+
+def test_dwconv1d_bwd_brute_force_and_planted_mistakes():
+    """Brute force on a tiny case (each gradient = the forward's change per unit change of
+    one input, by linearity), and mistakes the pins must catch: a shifted padding, a
+    reversed kernel, a dropped batch."""
+    rng = np.random.default_rng(9)
+    N, C, L, K, pad, l_out = 2, 2, 6, 3, 2, 7
+    x, w = rng.normal(size=(N, C, L)), rng.normal(size=(C, K))
+    dy = rng.normal(size=(N, C, l_out))
+    dx, dw, db = O.dwconv1d_bwd(x, w, dy, pad)
+    # d<dy, y>/dx[n,c,s] = <dy, y(e_{n,c,s})> with y linear in x (no bias)
+    for n, c, s in itertools.product(range(N), range(C), range(L)):
+        e = np.zeros_like(x)
+        e[n, c, s] = 1.0
+        assert abs((dy * O.dwconv1d(e, w, None, pad, l_out)).sum() - dx[n, c, s]) < 1e-12
+    for c, j in itertools.product(range(C), range(K)):
+        e = np.zeros_like(w)
+        e[c, j] = 1.0
+        assert abs((dy * O.dwconv1d(x, e, None, pad, l_out)).sum() - dw[c, j]) < 1e-12
+    np.testing.assert_allclose(db, dy.sum(axis=(0, 2)), atol=1e-12)
+    assert _far(O.dwconv1d_bwd(x, w, dy, pad - 1)[0], dx)
+    assert _far(O.dwconv1d_bwd(x, w[:, ::-1].copy(), dy, pad)[0], dx)
+    assert _far(O.dwconv1d_bwd(x, w, dy, pad - 1)[1], dw)
+    assert _far(O.dwconv1d_bwd(x[:1], w, dy[:1], pad)[1], dw)
