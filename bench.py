@@ -179,6 +179,31 @@ def bench_dw_backward_detail(dev):
             "max_rel_err_vs_stock": float(f"{err:.3g}")}
 
 
+def bench_gn_backward_detail(shape, G, dev):
+    """GroupNorm backward (dx, dgamma, dbeta), bf16: native kernels against the torch-op
+    backward that the reference uses.  Algorithmic bytes: read x and dy, write dx (the
+    kernels make 5 tensor-passes: x and dy are read twice)."""
+    import torch
+    from amd_tuned_torch import _native as nat
+    from amd_tuned_torch import _dispatch
+    g = _gen(1006)
+    C = shape[1]
+    x = (torch.randn(*shape, generator=g) + 1.0).to(torch.bfloat16).to(dev)
+    dy = torch.randn(*shape, generator=g).to(torch.bfloat16).to(dev)
+    gm = (1 + 0.1 * torch.randn(C, generator=g)).to(torch.bfloat16).to(dev)
+    dx, dg, db = nat.group_norm_backward(dy, x, G, gm, 1e-5, (True, True, True))
+    rx, rg, rb = _dispatch._group_norm_backward(dy.float(), x.float(), G, gm.float(), 1e-5, (True, True, True))
+    err = max(max_rel_err(dx, rx), max_rel_err(dg, rg), max_rel_err(db, rb))
+    del dx, dg, db, rx, rg, rb
+    ms = graph_time_ms(lambda: nat.group_norm_backward(dy, x, G, gm, 1e-5, (True, True, True)), 20)
+    torch_ms = event_time_ms(lambda: _dispatch._group_norm_backward(dy, x, G, gm, 1e-5, (True, True, True)), 10)
+    nbytes = 3 * x.numel() * x.element_size()
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"ms": round(ms, 4), "GB/s": round(gbs, 1), "roofline_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "variant": "native gn_bwd_rows/apply/finalize", "torch_op_backward_ms": round(torch_ms, 4),
+            "max_rel_err_vs_fp32_torch_ops": float(f"{err:.3g}")}
+
+
 def bench_gn_detail(shape, G, eps, dtype, silu, dev):
     import torch
     import torch.nn.functional as F
@@ -550,6 +575,8 @@ def main():
                              bench_gn_detail((8, 512, 64, 64), 32, 1e-5, dtype, silu, dev)))
                 plan.append((f"c3_ncdhw_{dt_name}{sfx}", lambda dtype=dtype, silu=silu:
                              bench_gn_detail((1, 512, 16, 64, 64), 32, 1e-5, dtype, silu, dev)))
+        plan.append(("c3_nchw_backward_bf16", lambda: bench_gn_backward_detail((8, 512, 64, 64), 32, dev)))
+        plan.append(("c3_ncdhw_backward_bf16", lambda: bench_gn_backward_detail((1, 512, 16, 64, 64), 32, dev)))
         plan.append(("c5_gn_silu_bf16", lambda: bench_gn_detail((1, 256, 8, 64, 64), 32, 1e-6,
                                                                 torch.bfloat16, True, dev)))
         plan += [

@@ -140,6 +140,24 @@ int atk_group_norm_fwd(const void* x, const void* gamma, const void* beta, void*
                        size_t workspace_bytes, atk_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * GroupNorm backward, NC[spatial] layout (replaces the torch-op backward of
+ * amd_tuned_torch/_dispatch.py:2212-2302 behind _GroupNormFn, 2305-2359):
+ *   x_hat = (x - mu) * rstd,  g = gamma_c * dy,
+ *   dx = rstd * (g - mean_group(g) - x_hat * mean_group(g * x_hat)),
+ *   dgamma_c = sum_{n,s} dy * x_hat,  dbeta_c = sum_{n,s} dy.
+ * x, dy, dx: [N, C, S] of `dtype`; gamma: [C] of `param_dtype` or NULL (ones);
+ * dgamma / dbeta: [C] fp32.  Any of dx / dgamma / dbeta may be NULL.  The group
+ * statistics are recomputed from x with the forward's eps.  Needs S * sizeof(dtype)
+ * to be a multiple of 16 and 16-byte aligned x / dy / dx (else ATK_UNSUPPORTED).
+ * The workspace (atk_group_norm_bwd_workspace_bytes) needs no initialisation.
+ * Sums over n are taken in a fixed order (deterministic).
+ * ------------------------------------------------------------------------- */
+size_t atk_group_norm_bwd_workspace_bytes(int64_t N, int64_t C);
+int atk_group_norm_bwd(const void* x, const void* dy, const void* gamma, void* dx, float* dgamma,
+                       float* dbeta, int64_t N, int64_t C, int64_t S, int G, float eps, int dtype,
+                       int param_dtype, void* workspace, size_t ws_bytes, atk_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Dense convolution forward, groups = 1, NCDHW layout, as an implicit GEMM on
  * MFMA (replaces `conv3d(input, weight, bias?, stride, padding, dilation)`,
  * src/main_rocm.cpp:798-854, and `conv2d(...)`, src/main_rocm.cpp:669-715):

@@ -114,6 +114,50 @@ void oracle_group_norm(const double* x, const double* gamma, const double* beta,
   }
 }
 
+/* Gradients of oracle_group_norm (no SiLU) for an upstream gradient dy, in the form of the
+ * reference's backward (amd_tuned_torch/_dispatch.py:2212-2302, torch ops over an (N, G,
+ * M, S) view):  x_hat = (x - mu) * rstd,  g = gamma_c * dy,
+ *   dx = rstd * (g - mean_group(g) - x_hat * mean_group(g * x_hat)),
+ *   dgamma_c = sum_{n,s} dy * x_hat,  dbeta_c = sum_{n,s} dy.
+ * gamma may be NULL (ones); any output may be NULL.  Statistics by two passes. */
+void oracle_group_norm_bwd(const double* x, const double* gamma, const double* dy, double* dx,
+                           double* dgamma, double* dbeta, int64_t N, int64_t C, int64_t S, int64_t G,
+                           double eps) {
+  const int64_t cpg = C / G, E = cpg * S;
+  if (dgamma)
+    for (int64_t c = 0; c < C; ++c) dgamma[c] = 0.0;
+  if (dbeta)
+    for (int64_t c = 0; c < C; ++c) dbeta[c] = 0.0;
+  for (int64_t gi = 0; gi < N * G; ++gi) {
+    const double* xg = x + gi * E;
+    const double* dg = dy + gi * E;
+    const int64_t c0 = (gi % G) * cpg;
+    double s = 0.0;
+    for (int64_t e = 0; e < E; ++e) s += xg[e];
+    const double mu = s / (double)E;
+    double q = 0.0;
+    for (int64_t e = 0; e < E; ++e) q += (xg[e] - mu) * (xg[e] - mu);
+    const double rstd = 1.0 / sqrt(q / (double)E + eps);
+    double m1 = 0.0, m2 = 0.0;
+    for (int64_t e = 0; e < E; ++e) {
+      const double gam = gamma ? gamma[c0 + e / S] : 1.0;
+      const double gg = gam * dg[e];
+      m1 += gg;
+      m2 += gg * (xg[e] - mu) * rstd;
+    }
+    m1 /= (double)E;
+    m2 /= (double)E;
+    for (int64_t e = 0; e < E; ++e) {
+      const int64_t c = c0 + e / S;
+      const double xh = (xg[e] - mu) * rstd;
+      const double gam = gamma ? gamma[c] : 1.0;
+      if (dx) dx[gi * E + e] = rstd * (gam * dg[e] - m1 - xh * m2);
+      if (dgamma) dgamma[c] += dg[e] * xh;
+      if (dbeta) dbeta[c] += dg[e];
+    }
+  }
+}
+
 /* Dense conv3d, groups = 1, NCDHW (the implicit GEMM of src/cuda/generated/
  * conv3d_fp16_bm256_bn128_bk32_s2.cu:84-324 and the direct kernel of src/cuda/conv3d_fp32.cu:
  * 33-149 both compute this):

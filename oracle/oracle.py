@@ -45,6 +45,7 @@ def lib():
         L.oracle_dwconv1d.argtypes = [d, d, d, d, i64, i64, i64, i64, i64, i64, i32]
         L.oracle_dwconv1d_bwd.argtypes = [d, d, d, d, d, d, i64, i64, i64, i64, i64, i64]
         L.oracle_group_norm.argtypes = [d, d, d, d, i64, i64, i64, i64, ctypes.c_double, i32, d, d]
+        L.oracle_group_norm_bwd.argtypes = [d, d, d, d, d, d, i64, i64, i64, i64, ctypes.c_double]
         L.oracle_conv3d.argtypes = [d, d, d, d] + [i64] * 18 + [d, i64]
         _lib = L
     return _lib
@@ -110,6 +111,18 @@ def group_norm(x, G: int, gamma=None, beta=None, eps: float = 1e-5, silu: bool =
     if return_stats:
         return y, mean.reshape(N, G), rstd.reshape(N, G)
     return y
+
+
+def group_norm_bwd(x, G: int, gamma, dy, eps: float = 1e-5):
+    """(dx, dgamma [C], dbeta [C]) of group_norm(x, G, gamma, beta, eps) for dy (x's shape)."""
+    x, gamma, dy = f64(x), f64(gamma), f64(dy)
+    N, C = x.shape[:2]
+    S = x.size // (N * C) if N * C else 0
+    dx = np.empty_like(x)
+    dg = np.empty((C,), dtype=np.float64)
+    db = np.empty((C,), dtype=np.float64)
+    lib().oracle_group_norm_bwd(_p(x), _p(gamma), _p(dy), _p(dx), _p(dg), _p(db), N, C, S, G, eps)
+    return dx, dg, db
 
 
 def _t3(v):

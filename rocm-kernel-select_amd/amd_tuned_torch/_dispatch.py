@@ -519,7 +519,8 @@ def _group_norm_backward(grad_output, input, num_groups, weight, eps, needs, bia
 
 
 class _GroupNormFn(torch.autograd.Function):
-    """Accelerated forward + textbook backward (reference _GroupNormFn, 2305-2359)."""
+    """Accelerated forward; native backward kernels (atk_group_norm_bwd) for contiguous GPU
+    inputs, the textbook torch-op backward otherwise (reference _GroupNormFn, 2305-2359)."""
 
     @staticmethod
     def forward(ctx, input, weight, bias, num_groups, eps):
@@ -534,7 +535,19 @@ class _GroupNormFn(torch.autograd.Function):
         input, weight = ctx.saved_tensors
         needs = (ctx.needs_input_grad[0], weight is not None and ctx.needs_input_grad[1],
                  ctx.has_bias and ctx.needs_input_grad[2])
-        return _group_norm_backward(grad_output.contiguous(), input, ctx.num_groups, weight,
+        dy = grad_output.contiguous()
+        if input.is_cuda and input.is_contiguous() and _native.available():
+            try:
+                gx, gw, gb = _native.group_norm_backward(dy, input.detach(), ctx.num_groups,
+                                                         None if weight is None else weight.detach(),
+                                                         ctx.eps, needs)
+                gw = None if gw is None else gw.to(weight.dtype)
+                gb = None if gb is None else gb.to(ctx.bias_dtype if ctx.bias_dtype is not None
+                                                   else input.dtype)
+                return gx, gw, gb, None, None
+            except _native.Unsupported:
+                pass
+        return _group_norm_backward(dy, input, ctx.num_groups, weight,
                                     ctx.eps, needs, bias_dtype=ctx.bias_dtype) + (None, None)
 
 

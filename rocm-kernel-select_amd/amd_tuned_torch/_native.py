@@ -36,7 +36,8 @@ EXPORTED_SYMBOLS = (
     "atk_abi_version", "atk_last_error", "atk_num_variants", "atk_variant_name",
     "atk_dwconv1d_fwd", "atk_dwconv1d_bwd_weight_workspace_bytes", "atk_dwconv1d_bwd_weight",
     "atk_group_norm_workspace_bytes",
-    "atk_group_norm_workspace_zero_bytes", "atk_group_norm_fwd", "atk_conv_workspace_bytes",
+    "atk_group_norm_workspace_zero_bytes", "atk_group_norm_fwd", "atk_group_norm_bwd_workspace_bytes",
+    "atk_group_norm_bwd", "atk_conv_workspace_bytes",
     "atk_conv_fwd",
 )
 
@@ -64,6 +65,10 @@ def _declare(lib) -> None:
     lib.atk_dwconv1d_bwd_weight_workspace_bytes.restype = sz
     lib.atk_dwconv1d_bwd_weight.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, i32, i64, i32, vp, sz, vp]
     lib.atk_dwconv1d_bwd_weight.restype = i32
+    lib.atk_group_norm_bwd_workspace_bytes.argtypes = [i64, i64]
+    lib.atk_group_norm_bwd_workspace_bytes.restype = sz
+    lib.atk_group_norm_bwd.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i32, c.c_float, i32, i32, vp, sz, vp]
+    lib.atk_group_norm_bwd.restype = i32
     lib.atk_group_norm_workspace_bytes.argtypes = [i64, i64, i64, i32, i32, i32]
     lib.atk_group_norm_workspace_bytes.restype = sz
     lib.atk_group_norm_workspace_zero_bytes.argtypes = [i64, i64, i64, i32, i32, i32]
@@ -345,6 +350,40 @@ def group_norm(input: torch.Tensor, num_groups: int, weight: Optional[torch.Tens
                               _stream(input))
     _check(rc, "group_norm")
     return y
+
+
+def group_norm_backward(dy: torch.Tensor, x: torch.Tensor, num_groups: int,
+                        weight: Optional[torch.Tensor], eps: float, needs=(True, True, True)):
+    """(dx, dgamma, dbeta) of group_norm(x, num_groups, weight, bias, eps) for dy: dx in x's
+    dtype, dgamma / dbeta in fp32 ([C]); entries not asked for in `needs` are None.
+    x and dy contiguous NC[spatial]; raises Unsupported when the spatial size is not a
+    multiple of 16 bytes or a tensor is not 16-byte aligned."""
+    _require_cuda(x, dy, weight)
+    if x.dim() < 2 or dy.shape != x.shape:
+        raise RuntimeError("group_norm_backward: dy must have x's shape (N, C, ...)")
+    if x.dtype not in _DTYPE_CODE or dy.dtype != x.dtype:
+        raise RuntimeError("group_norm_backward: x and dy must share a float16/bfloat16/float32 dtype")
+    if not (x.is_contiguous() and dy.is_contiguous()):
+        raise RuntimeError("group_norm_backward: x and dy must be contiguous")
+    if weight is not None and weight.dtype not in _DTYPE_CODE:
+        raise RuntimeError("group_norm_backward: weight must be float16, bfloat16 or float32")
+    N, C = x.shape[0], x.shape[1]
+    S = x.numel() // max(1, N * C)
+    if N == 0 or S == 0:
+        raise Unsupported("group_norm_backward: empty input")
+    weight = weight.contiguous() if weight is not None else None
+    dx = torch.empty_like(x) if needs[0] else None
+    dg = torch.empty(C, dtype=torch.float32, device=x.device) if needs[1] else None
+    db = torch.empty(C, dtype=torch.float32, device=x.device) if needs[2] else None
+    L_ = lib()
+    nbytes = L_.atk_group_norm_bwd_workspace_bytes(N, C)
+    ws = workspace(x.device, "group_norm_bwd", nbytes)
+    rc = L_.atk_group_norm_bwd(_ptr(x), _ptr(dy), _ptr(weight), _ptr(dx), _ptr(dg), _ptr(db), N, C, S,
+                               int(num_groups), float(eps), _DTYPE_CODE[x.dtype],
+                               _DTYPE_CODE[weight.dtype] if weight is not None else 0, _ptr(ws), ws.numel(),
+                               _stream(x))
+    _check(rc, "group_norm_backward")
+    return dx, dg, db
 
 
 # ---------------------------------------------------------------------------

@@ -659,6 +659,158 @@ int validate_gn(int64_t N, int64_t C, int64_t S, int G, int dtype, int variant) 
   return ATK_OK;
 }
 
+// ---------------------------------------------------------------------------------------
+// Backward (reference: textbook torch ops, amd_tuned_torch/_dispatch.py:2212-2302):
+//   g = gamma_c * dy,  x_hat = (x - mu) * rstd,
+//   dx = rstd * (g - mean_group(g) - x_hat * mean_group(g * x_hat)),
+//   dgamma_c = sum_{n,s} dy * x_hat,  dbeta_c = sum_{n,s} dy.
+// Three kernels, 5 tensor-passes of HBM traffic (x and dy read twice, dx written once):
+//   rows:     one workgroup per (n, c) row: x's mean / M2 about a row-wide shift K (the
+//             row's first element), A = sum dy, B = sum dy * (x - K);
+//   apply:    one workgroup per row: one wave merges the group's rows (Chan, fixed order, so
+//             every row of a group derives the same statistics), then dx; also the row's
+//             dgamma term rstd * sum dy * (x - mu) = rstd * (B + (K - mu) * A);
+//   finalize: dgamma / dbeta summed over n in order.
+// Requires S % VEC == 0 and 16-byte aligned x / dy / dx (host check).
+struct GnBwdArgs {
+  const void* x;
+  const void* dy;
+  const void* gamma;
+  void* dx;           // may be null (parameter gradients only)
+  float* rows;        // [N*C][5]: mean, M2, A, B, K
+  float* dg_part;     // [N*C]
+  float* dgamma;      // [C] or null
+  float* dbeta;       // [C] or null
+  int64_t S;
+  uint32_t C, cpg;
+  int N;
+  float eps;
+  int pdt;
+};
+
+template <typename T>
+__global__ __launch_bounds__(GN_TP_NT) void gn_bwd_rows_kernel(GnBwdArgs a) {
+  constexpr int VEC = 16 / sizeof(T);
+  __shared__ float red[GN_TP_NT / 64];
+  const int64_t r = blockIdx.x;
+  const T* __restrict__ xr = static_cast<const T*>(a.x) + r * a.S;
+  const T* __restrict__ gr = static_cast<const T*>(a.dy) + r * a.S;
+  const float K = to_f32(xr[0]);
+  float s1 = 0.f, s2 = 0.f, sa = 0.f, sb = 0.f;
+  for (int64_t e = (int64_t)threadIdx.x * VEC; e < a.S; e += (int64_t)GN_TP_NT * VEC) {
+    Vec16<T> xv, gv;
+    xv.raw = ld16<false>(xr + e);  // cached: the apply kernel reads x and dy again
+    gv.raw = ld16<false>(gr + e);
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+      const float d = to_f32(xv.e[k]) - K;
+      const float g = to_f32(gv.e[k]);
+      s1 += d;
+      s2 = fmaf(d, d, s2);
+      sa += g;
+      sb = fmaf(g, d, sb);
+    }
+  }
+  s1 = block_sum<GN_TP_NT>(s1, red);
+  s2 = block_sum<GN_TP_NT>(s2, red);
+  sa = block_sum<GN_TP_NT>(sa, red);
+  sb = block_sum<GN_TP_NT>(sb, red);
+  if (threadIdx.x == 0) {
+    const float q = s1 / (float)a.S;
+    float* o = a.rows + r * 5;
+    o[0] = K + q;
+    o[1] = fmaxf(fmaf(-s1, q, s2), 0.f);
+    o[2] = sa;
+    o[3] = sb;
+    o[4] = K;
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(GN_TP_NT) void gn_bwd_apply_kernel(GnBwdArgs a) {
+  constexpr int VEC = 16 / sizeof(T);
+  __shared__ float st[5];  // mu, rstd, c1, c2, gamma_c
+  const int64_t r = blockIdx.x;
+  const uint32_t c = (uint32_t)(r % a.C);
+  const int64_t n = r / a.C;
+  const uint32_t g0 = c - c % a.cpg;          // first channel of the group
+  const int64_t r0 = n * a.C + g0;            // its row
+  const float E = (float)((int64_t)a.cpg * a.S);
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const float* rows = a.rows + r0 * 5;
+    float sm = 0.f;
+    for (uint32_t j = lane; j < a.cpg; j += 64) sm += rows[j * 5];
+    const float mu = wave_sum(sm) / (float)a.cpg;  // equal row sizes
+    float m2 = 0.f, sg = 0.f, sgx = 0.f;
+    for (uint32_t j = lane; j < a.cpg; j += 64) {
+      const float* o = rows + j * 5;
+      const float dm = o[0] - mu;
+      m2 += o[1] + (float)a.S * dm * dm;
+      const float gam = a.gamma ? load_param(a.gamma, a.pdt, g0 + j) : 1.f;
+      sg = fmaf(gam, o[2], sg);
+      sgx = fmaf(gam, o[3] + (o[4] - mu) * o[2], sgx);
+    }
+    m2 = wave_sum(m2);
+    sg = wave_sum(sg);
+    sgx = wave_sum(sgx);
+    if (lane == 0) {
+      const float rstd = 1.0f / sqrtf(m2 / E + a.eps);
+      const float* o = a.rows + r * 5;
+      st[0] = mu;
+      st[1] = rstd;
+      st[2] = sg / E;
+      st[3] = rstd * sgx / E;
+      st[4] = a.gamma ? load_param(a.gamma, a.pdt, c) : 1.f;
+      a.dg_part[r] = rstd * (o[3] + (o[4] - mu) * o[2]);
+    }
+  }
+  __syncthreads();
+  if (!a.dx) return;
+  const float mu = st[0], rstd = st[1], c1 = st[2], c2 = st[3], gam = st[4];
+  const T* __restrict__ xr = static_cast<const T*>(a.x) + r * a.S;
+  const T* __restrict__ gr = static_cast<const T*>(a.dy) + r * a.S;
+  T* __restrict__ dxr = static_cast<T*>(a.dx) + r * a.S;
+  for (int64_t e = (int64_t)threadIdx.x * VEC; e < a.S; e += (int64_t)GN_TP_NT * VEC) {
+    Vec16<T> xv, gv;
+    xv.raw = ld16<true>(xr + e);
+    gv.raw = ld16<true>(gr + e);
+    float o[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+      const float xh = (to_f32(xv.e[k]) - mu) * rstd;
+      o[k] = rstd * (fmaf(gam, to_f32(gv.e[k]), -c1) - xh * c2);
+    }
+    st16<true>(dxr + e, pack16<T>(o));
+  }
+}
+
+__global__ __launch_bounds__(256) void gn_bwd_finalize_kernel(GnBwdArgs a) {
+  const uint32_t c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= a.C) return;
+  float sgm = 0.f, sbt = 0.f;
+  for (int n = 0; n < a.N; ++n) {
+    const int64_t r = (int64_t)n * a.C + c;
+    sgm += a.dg_part[r];
+    sbt += a.rows[r * 5 + 2];
+  }
+  if (a.dgamma) a.dgamma[c] = sgm;
+  if (a.dbeta) a.dbeta[c] = sbt;
+}
+
+template <typename T>
+int launch_gn_bwd(const GnBwdArgs& a, int64_t rows, hipStream_t s) {
+  hipLaunchKernelGGL((gn_bwd_rows_kernel<T>), dim3((unsigned)rows), dim3(GN_TP_NT), 0, s, a);
+  int rc = check_launch("gn_bwd_rows_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL((gn_bwd_apply_kernel<T>), dim3((unsigned)rows), dim3(GN_TP_NT), 0, s, a);
+  rc = check_launch("gn_bwd_apply_kernel");
+  if (rc) return rc;
+  if (!a.dgamma && !a.dbeta) return ATK_OK;
+  hipLaunchKernelGGL(gn_bwd_finalize_kernel, dim3((a.C + 255) / 256), dim3(256), 0, s, a);
+  return check_launch("gn_bwd_finalize_kernel");
+}
+
 }  // namespace
 
 int group_norm_num_variants() { return kNumGn; }
@@ -736,5 +888,44 @@ extern "C" int atk_group_norm_fwd(const void* x, const void* gamma, const void* 
     case ATK_F32: return launch_gn<float>(a, ngroups, variant, vec_ok, s);
     case ATK_F16: return launch_gn<_Float16>(a, ngroups, variant, vec_ok, s);
     default: return launch_gn<__bf16>(a, ngroups, variant, vec_ok, s);
+  }
+}
+
+extern "C" size_t atk_group_norm_bwd_workspace_bytes(int64_t N, int64_t C) {
+  if (N <= 0 || C <= 0) return 0;
+  return (size_t)N * (size_t)C * 6 * sizeof(float);
+}
+
+extern "C" int atk_group_norm_bwd(const void* x, const void* dy, const void* gamma, void* dx, float* dgamma,
+                                  float* dbeta, int64_t N, int64_t C, int64_t S, int G, float eps, int dtype,
+                                  int param_dtype, void* workspace, size_t ws_bytes, atk_stream_t stream) {
+  using namespace atk;
+  if (!dtype_ok(dtype) || (gamma && !dtype_ok(param_dtype)))
+    return fail(ATK_EINVAL, "group_norm backward: unknown dtype code");
+  if (N <= 0 || C <= 0 || S <= 0 || G <= 0) return fail(ATK_EINVAL, "group_norm backward: bad sizes");
+  if (C % G) return fail(ATK_EINVAL, "group_norm backward: channels (%lld) not divisible by groups (%d)",
+                         (long long)C, G);
+  if (!x || !dy) return fail(ATK_EINVAL, "group_norm backward: null pointer");
+  const size_t need = atk_group_norm_bwd_workspace_bytes(N, C);
+  if (!workspace || ws_bytes < need) return fail(ATK_EINVAL, "group_norm backward: workspace of %zu bytes needed", need);
+  const int64_t es = (int64_t)dtype_size(dtype), vec = 16 / es;
+  if (S % vec || !aligned16(x) || !aligned16(dy) || (dx && !aligned16(dx)))
+    return fail(ATK_UNSUPPORTED, "group_norm backward: needs spatial size %% %lld == 0 and 16-byte aligned tensors",
+                (long long)vec);
+  const int64_t rows = N * C;
+  if (rows >= (1ll << 31) || C >= (1ll << 31) || N >= (1ll << 31))
+    return fail(ATK_UNSUPPORTED, "group_norm backward: too many rows");
+  GnBwdArgs a;
+  a.x = x; a.dy = dy; a.gamma = gamma; a.dx = dx;
+  a.rows = static_cast<float*>(workspace);
+  a.dg_part = a.rows + rows * 5;
+  a.dgamma = dgamma; a.dbeta = dbeta;
+  a.S = S; a.C = (uint32_t)C; a.cpg = (uint32_t)(C / G); a.N = (int)N;
+  a.eps = eps; a.pdt = param_dtype;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case ATK_F32: return launch_gn_bwd<float>(a, rows, s);
+    case ATK_F16: return launch_gn_bwd<_Float16>(a, rows, s);
+    default: return launch_gn_bwd<__bf16>(a, rows, s);
   }
 }

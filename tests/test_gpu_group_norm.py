@@ -224,3 +224,69 @@ def test_group_norm_workspace_shared_across_shapes(dev):
             assert O.max_rel_err(yb.cpu(), ref_b) <= 1e-2
             assert O.max_rel_err(ya.cpu(), ref_a) <= 1e-2
     assert not nat.group_norm_barrier_error(dev)
+
+
+# ---------------------------------------------------------------------------
+# backward (atk_group_norm_bwd) against the float64 oracle
+# ---------------------------------------------------------------------------
+# dgamma / dbeta are fp32 sums of exact products: tighter than the 16-bit output bar
+BWD_BAR_P = {torch.float32: 1e-5, torch.float16: 1e-4, torch.bfloat16: 1e-4}
+
+BWD_SHAPES = [
+    ((2, 64, 8, 8), 8, True),
+    ((1, 32, 128, 128), 2, True),     # large groups
+    ((2, 12, 4, 6, 8), 3, False),     # 3-D spatial, no affine
+    ((3, 10, 24), 5, True),           # 1-D spatial
+    ((8, 512, 16, 16), 32, True),     # C3-like channel count
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("case", BWD_SHAPES, ids=lambda s: "x".join(map(str, s[0])) + f"_g{s[1]}")
+def test_group_norm_backward_native(dev, case, dtype):
+    shape, G, affine = case
+    nat = _native()
+    x, gm, _ = _inputs(shape, dtype, seed=len(shape) + G + 100, affine=affine)
+    dy = torch.randn(*shape, generator=torch.Generator().manual_seed(G)).to(dtype)
+    dx, dg, db = nat.group_norm_backward(dy.to(dev), x.to(dev), G, None if gm is None else gm.to(dev),
+                                         1e-5, (True, True, True))
+    torch.cuda.synchronize()
+    rdx, rdg, rdb = O.group_norm_bwd(x, G, gm, dy, 1e-5)
+    assert dx.dtype == dtype
+    assert O.max_rel_err(dx.cpu(), rdx) <= BAR[dtype], O.max_rel_err(dx.cpu(), rdx)
+    assert O.max_rel_err(dg.cpu(), rdg) <= BWD_BAR_P[dtype], O.max_rel_err(dg.cpu(), rdg)
+    assert O.max_rel_err(db.cpu(), rdb) <= BWD_BAR_P[dtype], O.max_rel_err(db.cpu(), rdb)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_group_norm_autograd_through_patched_group_norm(dev, dtype):
+    """Training path: the patched F.group_norm with requires_grad inputs runs the native
+    forward and the native backward; gradients match the oracle.  A spatial size that is
+    not a multiple of 16 bytes takes the torch-op backward and must agree too."""
+    import torch.nn.functional as F
+    import amd_tuned_torch  # noqa: F401
+    for shape, G in (((2, 16, 8, 8), 4), ((2, 8, 3, 5), 2)):
+        x, gm, bt = _inputs(shape, dtype, seed=7 + G)
+        xd = x.to(dev).requires_grad_(True)
+        gd, bd = gm.to(dev).requires_grad_(True), bt.to(dev).requires_grad_(True)
+        y = F.group_norm(xd, G, gd, bd, 1e-5)
+        dy = torch.randn(*shape, generator=torch.Generator().manual_seed(3)).to(dtype)
+        gx, gg, gb = torch.autograd.grad(y, (xd, gd, bd), dy.to(dev))
+        rdx, rdg, rdb = O.group_norm_bwd(x, G, gm, dy, 1e-5)
+        assert O.max_rel_err(gx.cpu(), rdx) <= BAR[dtype]
+        assert O.max_rel_err(gg.cpu(), rdg) <= BAR[dtype]
+        assert O.max_rel_err(gb.cpu(), rdb) <= BAR[dtype]
+
+
+def test_group_norm_backward_c3_full_size(dev):
+    """C3's NCDHW shape at full size, bf16: every gradient element against the oracle."""
+    nat = _native()
+    shape, G = (1, 512, 16, 64, 64), 32
+    x, gm, _ = _inputs(shape, torch.bfloat16, seed=3003)
+    dy = torch.randn(*shape, generator=torch.Generator().manual_seed(3004)).to(torch.bfloat16)
+    dx, dg, db = nat.group_norm_backward(dy.to(dev), x.to(dev), G, gm.to(dev), 1e-5, (True, True, True))
+    torch.cuda.synchronize()
+    rdx, rdg, rdb = O.group_norm_bwd(x, G, gm, dy, 1e-5)
+    assert O.max_rel_err(dx.cpu(), rdx) <= BAR[torch.bfloat16]
+    assert O.max_rel_err(dg.cpu(), rdg) <= BWD_BAR_P[torch.bfloat16]
+    assert O.max_rel_err(db.cpu(), rdb) <= BWD_BAR_P[torch.bfloat16]

@@ -300,3 +300,46 @@ def test_dwconv1d_bwd_brute_force_and_planted_mistakes():
     assert _far(O.dwconv1d_bwd(x, w[:, ::-1].copy(), dy, pad)[0], dx)
     assert _far(O.dwconv1d_bwd(x, w, dy, pad - 1)[1], dw)
     assert _far(O.dwconv1d_bwd(x[:1], w, dy[:1], pad)[1], dw)
+
+
+# ---------------------------------------------------------------------------
+# GroupNorm backward
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("shape,G,affine", [((2, 6, 5, 3), 3, True), ((1, 8, 7), 2, False),
+                                            ((3, 4, 2, 2, 2), 4, True), ((2, 4, 9), 1, True)])
+def test_group_norm_bwd_matches_stock_autograd(shape, G, affine):
+    rng = np.random.default_rng(len(shape) * 10 + G)
+    x = rng.normal(size=shape) * 2 + 3
+    C = shape[1]
+    gm, bt = (rng.normal(size=C), rng.normal(size=C)) if affine else (None, None)
+    dy = rng.normal(size=shape)
+    xt = torch.tensor(x, requires_grad=True)
+    params = [torch.tensor(v, requires_grad=True) for v in (gm, bt)] if affine else [None, None]
+    y = F.group_norm(xt, G, params[0], params[1], 1e-5)
+    want = [xt] + ([params[0], params[1]] if affine else [])
+    ref = torch.autograd.grad(y, want, torch.tensor(dy))
+    dx, dg, db = O.group_norm_bwd(x, G, gm, dy, 1e-5)
+    np.testing.assert_allclose(dx, ref[0].numpy(), rtol=0, atol=1e-10)
+    if affine:
+        np.testing.assert_allclose(dg, ref[1].numpy(), rtol=0, atol=1e-10)
+        np.testing.assert_allclose(db, ref[2].numpy(), rtol=0, atol=1e-10)
+
+
+def test_group_norm_bwd_identities_and_planted_mistakes():
+    """dx sums to zero over each group and is orthogonal to x_hat there (the normalisation
+    removes mean and scale); the pins catch a wrong group count, a dropped gamma and a
+    wrong eps."""
+    rng = np.random.default_rng(17)
+    N, C, S, G = 2, 6, 10, 3
+    x, gm, dy = rng.normal(size=(N, C, S)), rng.normal(size=C), rng.normal(size=(N, C, S))
+    # exact at eps = 0 (with eps, sum x_hat^2 = E var / (var + eps) instead of E)
+    dx0 = O.group_norm_bwd(x, G, gm, dy, 0.0)[0]
+    xg = x.reshape(N, G, -1)
+    xh = (xg - xg.mean(-1, keepdims=True)) / np.sqrt(xg.var(-1, keepdims=True))
+    np.testing.assert_allclose(dx0.reshape(N, G, -1).sum(-1), 0, atol=1e-10)
+    np.testing.assert_allclose((dx0.reshape(N, G, -1) * xh).sum(-1), 0, atol=1e-9)
+    dx, dg, db = O.group_norm_bwd(x, G, gm, dy, 1e-5)
+    assert _far(O.group_norm_bwd(x, 2, gm, dy, 1e-5)[0], dx)
+    assert _far(O.group_norm_bwd(x, G, None, dy, 1e-5)[0], dx)
+    assert _far(O.group_norm_bwd(x, G, gm, dy, 1e-1)[0], dx)
+    np.testing.assert_allclose(db, dy.sum(axis=(0, 2)), atol=1e-12)
