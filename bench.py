@@ -179,6 +179,30 @@ def bench_dw_backward_detail(dev):
             "max_rel_err_vs_stock": float(f"{err:.3g}")}
 
 
+def bench_decode_detail(dev):
+    """Decode step of the causal conv at config 2's batch and channels (B=16, D=2048,
+    W=4, bf16): latency per step, graph-replayed, against the reference interface's torch
+    statement of the same step (causal_conv1d_update_ref)."""
+    import torch
+    from amd_tuned_torch import causal_conv1d as cc
+    g = _gen(1007)
+    B, D, W = 16, 2048, 4
+    x = torch.randn(B, D, generator=g).to(torch.bfloat16).to(dev)
+    st = torch.randn(B, D, W, generator=g).to(torch.bfloat16).to(dev)
+    w = (0.5 * torch.randn(D, W, generator=g)).to(torch.bfloat16).to(dev)
+    b = (0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).to(dev)
+    st_ref = st.clone()
+    y = cc.causal_conv1d_update(x, st, w, b)
+    yr = cc.causal_conv1d_update_ref(x, st_ref, w, b)
+    err = max_rel_err(y, yr.float())
+    same_state = bool(torch.equal(st, st_ref))
+    ms = graph_time_ms(lambda: cc.causal_conv1d_update(x, st, w, b), 50)
+    ref_ms = event_time_ms(lambda: cc.causal_conv1d_update_ref(x, st_ref, w, b), 20)
+    return {"us": round(ms * 1e3, 2), "torch_ref_us": round(ref_ms * 1e3, 2),
+            "variant": "causal_conv1d_update_kernel", "state_matches_ref": same_state,
+            "max_rel_err_vs_torch_ref": float(f"{err:.3g}")}
+
+
 def bench_gn_backward_detail(shape, G, dev):
     """GroupNorm backward (dx, dgamma, dbeta), bf16: native kernels against the torch-op
     backward that the reference uses.  Algorithmic bytes: read x and dy, write dx (the
@@ -567,6 +591,7 @@ def main():
             ("c2_sym_k3_bf16", lambda: bench_dw_detail(torch.bfloat16, "sym", dev)),
             ("c2_sym_k3_fp16", lambda: bench_dw_detail(torch.float16, "sym", dev)),
             ("c2_causal_backward_bf16", lambda: bench_dw_backward_detail(dev)),
+            ("c2_decode_step_bf16", lambda: bench_decode_detail(dev)),
         ]
         for dt_name, dtype in (("fp16", torch.float16), ("bf16", torch.bfloat16)):
             for silu in (False, True):

@@ -92,6 +92,18 @@ int atk_dwconv1d_fwd(const void* x, const void* w, const void* bias, void* y,
                      int dtype, int fuse_silu, int variant, atk_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Causal conv1d decode step (replaces `causal_conv1d_update(x, conv_state, weight,
+ * bias?, silu_activation)`, src/causal-conv1d-amd/csrc/causal_conv1d.cpp:385-440 ->
+ * causal_conv1d_update.cu:27-66):
+ *   conv_state[b,d,:] <- (conv_state[b,d,1:], x[b,d]),
+ *   y[b,d] = bias[d] + sum_j w[d,j] * conv_state[b,d,j]   (+ SiLU if fuse_silu).
+ * x, y: [B, D]; conv_state: [B, D, W] (updated in place); w: [D, W]; bias: [D] or
+ * NULL; all of `dtype`.  W in [1, 64] (the reference: [2, 4]).
+ * ------------------------------------------------------------------------- */
+int atk_causal_conv1d_update(const void* x, void* conv_state, const void* w, const void* bias, void* y,
+                             int64_t B, int64_t D, int W, int dtype, int fuse_silu, atk_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Depthwise / causal conv1d backward, weight and bias gradients (replaces the
  * dweight / dbias half of `conv1d_backward(dout, u, weight, bias, padding, is_bhl)`,
  * amd_tuned_torch/_vendor/flashfftconv_depthwise_conv1d/conv1d_bwd_hip_bhl.hip:

@@ -77,6 +77,23 @@ void oracle_dwconv1d_bwd(const double* x, const double* w, const double* dy, dou
     }
 }
 
+/* Decode step of the causal conv (src/causal-conv1d-amd/csrc/causal_conv1d_update.cu:27-66;
+ * causal_conv1d_interface.py:192-213): state [B, D, W] <- (state[..., 1:], x[b, d]),
+ * y[b, d] = b[d] + sum_j w[d, j] * state[b, d, j]; silu != 0 applies y / (1 + exp(-y)).
+ * The state is updated in place. */
+void oracle_causal_conv1d_update(const double* x, double* state, const double* w, const double* b, double* y,
+                                 int64_t B, int64_t D, int64_t W, int silu) {
+  for (int64_t i = 0; i < B * D; ++i) {
+    const int64_t d = i % D;
+    double* st = state + i * W;
+    for (int64_t j = 0; j + 1 < W; ++j) st[j] = st[j + 1];
+    st[W - 1] = x[i];
+    double acc = b ? b[d] : 0.0;
+    for (int64_t j = 0; j < W; ++j) acc += w[d * W + j] * st[j];
+    y[i] = silu ? acc / (1.0 + exp(-acc)) : acc;
+  }
+}
+
 /* GroupNorm over NC[S] (src/cuda/group_norm.cu:41-104; fused SiLU of
  * amd_tuned_torch/conv_fusion_ops.py:192-242): group (n, g) = channels [g*C/G, (g+1)*C/G)
  * x all S positions; population variance (divide by the group size), eps inside the

@@ -44,6 +44,7 @@ def lib():
         d, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
         L.oracle_dwconv1d.argtypes = [d, d, d, d, i64, i64, i64, i64, i64, i64, i32]
         L.oracle_dwconv1d_bwd.argtypes = [d, d, d, d, d, d, i64, i64, i64, i64, i64, i64]
+        L.oracle_causal_conv1d_update.argtypes = [d, d, d, d, d, i64, i64, i64, i32]
         L.oracle_group_norm.argtypes = [d, d, d, d, i64, i64, i64, i64, ctypes.c_double, i32, d, d]
         L.oracle_group_norm_bwd.argtypes = [d, d, d, d, d, d, i64, i64, i64, i64, ctypes.c_double]
         L.oracle_conv3d.argtypes = [d, d, d, d] + [i64] * 18 + [d, i64]
@@ -92,6 +93,17 @@ def dwconv1d_bwd(x, w, dy, pad_left: int):
     lib().oracle_dwconv1d_bwd(_p(x), _p(w), _p(dy), _p(dx), _p(dw), _p(db), N, C, L, K, pad_left,
                               dy.shape[-1])
     return dx, dw, db
+
+
+def causal_conv1d_update(x, state, w, b=None, silu: bool = False):
+    """(y [B, D], new state [B, D, W]) of one decode step; inputs are not modified."""
+    x, w, b = f64(x), f64(w), f64(b)
+    st = f64(state).copy()
+    B, D = x.shape
+    W = w.shape[-1]
+    y = np.empty((B, D), dtype=np.float64)
+    lib().oracle_causal_conv1d_update(_p(x), _p(st), _p(w.reshape(D, W)), _p(b), _p(y), B, D, W, int(bool(silu)))
+    return y, st
 
 
 def conv1d_out_len(length: int, padding: int, width: int) -> int:

@@ -34,7 +34,8 @@ _DTYPE_CODE = {torch.float32: ATK_F32, torch.float16: ATK_F16, torch.bfloat16: A
 # Every symbol the header declares (include/amd_tuned_torch_hip.h).
 EXPORTED_SYMBOLS = (
     "atk_abi_version", "atk_last_error", "atk_num_variants", "atk_variant_name",
-    "atk_dwconv1d_fwd", "atk_dwconv1d_bwd_weight_workspace_bytes", "atk_dwconv1d_bwd_weight",
+    "atk_dwconv1d_fwd", "atk_causal_conv1d_update", "atk_dwconv1d_bwd_weight_workspace_bytes",
+    "atk_dwconv1d_bwd_weight",
     "atk_group_norm_workspace_bytes",
     "atk_group_norm_workspace_zero_bytes", "atk_group_norm_fwd", "atk_group_norm_bwd_workspace_bytes",
     "atk_group_norm_bwd", "atk_conv_workspace_bytes",
@@ -61,6 +62,8 @@ def _declare(lib) -> None:
     lib.atk_variant_name.restype = c.c_char_p
     lib.atk_dwconv1d_fwd.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, i32, i64, i32, i32, i32, vp]
     lib.atk_dwconv1d_fwd.restype = i32
+    lib.atk_causal_conv1d_update.argtypes = [vp, vp, vp, vp, vp, i64, i64, i32, i32, i32, vp]
+    lib.atk_causal_conv1d_update.restype = i32
     lib.atk_dwconv1d_bwd_weight_workspace_bytes.argtypes = [i64, i64, i32]
     lib.atk_dwconv1d_bwd_weight_workspace_bytes.restype = sz
     lib.atk_dwconv1d_bwd_weight.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, i32, i64, i32, vp, sz, vp]
@@ -233,6 +236,33 @@ def dwconv1d(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]
     rc = lib().atk_dwconv1d_fwd(_ptr(x), _ptr(weight), _ptr(bias), _ptr(y), N, C, L, K, pad_left,
                                 l_out, _DTYPE_CODE[x.dtype], int(bool(silu)), variant, _stream(x))
     _check(rc, "dwconv1d")
+    return y
+
+
+def causal_conv1d_update(x: torch.Tensor, conv_state: torch.Tensor, weight: torch.Tensor,
+                         bias: Optional[torch.Tensor] = None, *, silu: bool = False) -> torch.Tensor:
+    """Decode step: conv_state [B, D, W] <- (conv_state[..., 1:], x); returns
+    y [B, D] = bias + sum_j weight[:, j] * conv_state[..., j] (+ SiLU).  x [B, D],
+    weight [D, W], bias [D] or None, all one dtype; conv_state contiguous (updated in place)."""
+    _require_cuda(x, conv_state, weight, bias)
+    if x.dim() != 2 or conv_state.dim() != 3 or weight.dim() != 2:
+        raise RuntimeError("causal_conv1d_update expects x [B, D], conv_state [B, D, W], weight [D, W]")
+    B, D = x.shape
+    W = weight.shape[1]
+    if tuple(conv_state.shape) != (B, D, W) or weight.shape[0] != D:
+        raise RuntimeError("causal_conv1d_update: conv_state must be [B, D, W] and weight [D, W]")
+    if x.dtype not in _DTYPE_CODE or conv_state.dtype != x.dtype or weight.dtype != x.dtype or \
+            (bias is not None and bias.dtype != x.dtype):
+        raise RuntimeError("causal_conv1d_update: x, conv_state, weight and bias must share a dtype")
+    if not conv_state.is_contiguous():
+        raise RuntimeError("causal_conv1d_update: conv_state must be contiguous (it is updated in place)")
+    x = x.contiguous()
+    weight = weight.contiguous()
+    bias = bias.contiguous() if bias is not None else None
+    y = torch.empty_like(x)
+    rc = lib().atk_causal_conv1d_update(_ptr(x), _ptr(conv_state), _ptr(weight), _ptr(bias), _ptr(y), B, D, W,
+                                        _DTYPE_CODE[x.dtype], int(bool(silu)), _stream(x))
+    _check(rc, "causal_conv1d_update")
     return y
 
 

@@ -820,6 +820,49 @@ int launch_dw_bwd_w(const DwBwdArgs& a, int64_t rows, int K, hipStream_t s) {
   return check_launch("dwconv1d_bwd_w_kernel");
 }
 
+// ---------------------------------------------------------------------------------------
+// Decode step of the causal conv (reference: src/causal-conv1d-amd/csrc/
+// causal_conv1d_update.cu:27-66, interface causal_conv1d_interface.py:175-213):
+//   state[b,d,:] <- (state[b,d,1:], x[b,d]),   y[b,d] = bias[d] + sum_j w[d,j] * state[b,d,j]
+// (+ SiLU).  One thread per (b, d); the state row is shifted in place in order, so every
+// element is read before it is overwritten.  Latency-bound: B*D*(W+2) elements per step.
+template <typename T, bool SILU>
+__global__ __launch_bounds__(256) void causal_conv1d_update_kernel(const T* __restrict__ x, T* __restrict__ state,
+                                                                   const T* __restrict__ w,
+                                                                   const T* __restrict__ bias, T* __restrict__ y,
+                                                                   int64_t rows, uint32_t D, int W) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // b * D + d
+  if (i >= rows) return;
+  const uint32_t d = (uint32_t)(i % D);
+  T* st = state + i * W;
+  const T* wd = w + (int64_t)d * W;
+  float acc = bias ? to_f32(bias[d]) : 0.f;
+  for (int j = 0; j + 1 < W; ++j) {
+    const T v = st[j + 1];
+    st[j] = v;
+    acc = fmaf(to_f32(wd[j]), to_f32(v), acc);
+  }
+  const T v = x[i];
+  st[W - 1] = v;
+  acc = fmaf(to_f32(wd[W - 1]), to_f32(v), acc);
+  if constexpr (SILU) acc = silu_f32(acc);
+  y[i] = from_f32<T>(acc);
+}
+
+template <typename T>
+int launch_update(const void* x, void* state, const void* w, const void* bias, void* y, int64_t rows, int64_t D,
+                  int W, int silu, hipStream_t s) {
+  const dim3 grid((unsigned)((rows + 255) / 256)), block(256);
+  auto args = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, block, 0, s, static_cast<const T*>(x), static_cast<T*>(state),
+                       static_cast<const T*>(w), static_cast<const T*>(bias), static_cast<T*>(y), rows,
+                       (uint32_t)D, W);
+  };
+  if (silu) args(causal_conv1d_update_kernel<T, true>);
+  else args(causal_conv1d_update_kernel<T, false>);
+  return check_launch("causal_conv1d_update_kernel");
+}
+
 }  // namespace
 
 int dwconv1d_num_variants() { return kNumDw; }
@@ -929,4 +972,23 @@ extern "C" int atk_dwconv1d_bwd_weight(const void* x, const void* dy, float* dw,
   hipLaunchKernelGGL(dwconv1d_bwd_finalize_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s,
                      a.part, dw, db, (int)N, (int)C, K);
   return check_launch("dwconv1d_bwd_finalize_kernel");
+}
+
+extern "C" int atk_causal_conv1d_update(const void* x, void* conv_state, const void* w, const void* bias, void* y,
+                                        int64_t B, int64_t D, int W, int dtype, int fuse_silu,
+                                        atk_stream_t stream) {
+  using namespace atk;
+  if (!dtype_ok(dtype)) return fail(ATK_EINVAL, "causal_conv1d_update: unknown dtype code %d", dtype);
+  if (B < 0 || D <= 0) return fail(ATK_EINVAL, "causal_conv1d_update: bad sizes");
+  if (W < 1 || W > DW_KMAX) return fail(ATK_UNSUPPORTED, "causal_conv1d_update: width %d outside [1, %d]", W, DW_KMAX);
+  const int64_t rows = B * D;
+  if (rows == 0) return ATK_OK;
+  if (!x || !conv_state || !w || !y) return fail(ATK_EINVAL, "causal_conv1d_update: null pointer");
+  if (rows >= (1ll << 31) * 256ll) return fail(ATK_UNSUPPORTED, "causal_conv1d_update: too many rows");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case ATK_F32: return launch_update<float>(x, conv_state, w, bias, y, rows, D, W, fuse_silu, s);
+    case ATK_F16: return launch_update<_Float16>(x, conv_state, w, bias, y, rows, D, W, fuse_silu, s);
+    default: return launch_update<__bf16>(x, conv_state, w, bias, y, rows, D, W, fuse_silu, s);
+  }
 }

@@ -77,6 +77,10 @@ def test_argument_validation_codes(nat):
     assert lib.atk_dwconv1d_fwd(None, None, None, None, 1, 4, 16, 3, 1, 16, 0, 0, 0, None) == nat.ATK_EINVAL
     assert "null" in nat.last_error()
     assert lib.atk_dwconv1d_fwd(None, None, None, None, 0, 4, 16, 3, 1, 16, 0, 0, 0, None) == nat.ATK_OK
+    # decode step
+    assert lib.atk_causal_conv1d_update(None, None, None, None, None, 2, 4, 4, 2, 0, None) == nat.ATK_EINVAL
+    assert lib.atk_causal_conv1d_update(None, None, None, None, None, 2, 4, 65, 2, 0, None) == nat.ATK_UNSUPPORTED
+    assert lib.atk_causal_conv1d_update(None, None, None, None, None, 0, 4, 4, 2, 0, None) == nat.ATK_OK
     # dwconv1d backward (weight / bias gradients)
     assert lib.atk_dwconv1d_bwd_weight_workspace_bytes(2, 3, 4) == 2 * 3 * 5 * 4
     assert lib.atk_dwconv1d_bwd_weight_workspace_bytes(0, 3, 4) == 0

@@ -220,3 +220,46 @@ def test_dwconv1d_backward_config2_full_size(dev):
     assert O.max_rel_err(dx.cpu(), rdx) <= BAR[torch.bfloat16]
     assert O.max_rel_err(dw.cpu(), rdw) <= BWD_BAR_W[torch.bfloat16]
     assert O.max_rel_err(db.cpu(), rdb) <= BWD_BAR_W[torch.bfloat16]
+
+
+# ---------------------------------------------------------------------------
+# decode step (atk_causal_conv1d_update)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("W,silu", [(2, False), (3, True), (4, False), (4, True)])
+def test_causal_conv1d_update_native(dev, W, silu, dtype):
+    from amd_tuned_torch import causal_conv1d as cc
+    g = torch.Generator().manual_seed(W + 10 * silu)
+    B, D = 5, 300
+    x = torch.randn(B, D, generator=g).to(dtype)
+    st = torch.randn(B, D, W, generator=g).to(dtype)
+    w = (torch.randn(D, W, generator=g) * 0.5).to(dtype)
+    b = (0.1 * torch.randn(D, generator=g)).to(dtype)
+    sd = st.to(dev)
+    y = cc.causal_conv1d_update(x.to(dev), sd, w.to(dev), b.to(dev), activation="silu" if silu else None)
+    torch.cuda.synchronize()
+    ry, rs = O.causal_conv1d_update(x, st, w, b, silu)
+    assert O.max_rel_err(y.cpu(), ry) <= BAR[dtype]
+    assert torch.equal(sd.cpu().double(), torch.from_numpy(rs))          # the state is moved, not recomputed
+    # the reference interface's torch statement agrees
+    sr = st.to(dev)
+    yr = cc.causal_conv1d_update_ref(x.to(dev), sr, w.to(dev), b.to(dev), activation="silu" if silu else None)
+    assert torch.equal(sr.cpu(), sd.cpu())
+    assert O.max_rel_err(yr.cpu(), ry) <= BAR[dtype]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_causal_conv1d_update_streaming_equals_forward(dev, dtype):
+    """Decoding a sequence step by step from a zero state gives the causal forward kernel's
+    output (the same fp32 arithmetic), and ends with the last W inputs as the state."""
+    from amd_tuned_torch import causal_conv1d as cc
+    B, D, L, W = 3, 64, 40, 4
+    x, w, b = _inputs(B, D, L, W, dtype, seed=77)
+    xd, wd, bd = x.to(dev), w.to(dev), b.to(dev)
+    st = torch.zeros(B, D, W, dtype=dtype, device=dev)
+    ys = [cc.causal_conv1d_update(xd[:, :, t].contiguous(), st, wd, bd) for t in range(L)]
+    full = cc.causal_conv1d_fn(xd, wd, bd)
+    torch.cuda.synchronize()
+    assert O.max_rel_err(torch.stack(ys, -1).cpu(), O.dwconv1d(x, w, b, W - 1, L)) <= BAR[dtype]
+    assert O.max_rel_err(full.cpu(), O.dwconv1d(x, w, b, W - 1, L)) <= BAR[dtype]
+    assert torch.equal(st.cpu(), x[:, :, L - W:])

@@ -343,3 +343,33 @@ def test_group_norm_bwd_identities_and_planted_mistakes():
     assert _far(O.group_norm_bwd(x, G, None, dy, 1e-5)[0], dx)
     assert _far(O.group_norm_bwd(x, G, gm, dy, 1e-1)[0], dx)
     np.testing.assert_allclose(db, dy.sum(axis=(0, 2)), atol=1e-12)
+
+
+# ---------------------------------------------------------------------------
+# causal conv1d decode step
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("W,silu", [(2, False), (3, True), (4, False), (4, True)])
+def test_causal_update_streaming_equals_causal_forward(W, silu):
+    """L decode steps from a zero state produce the causal conv of the whole sequence
+    (the forward with pad_left = W-1, truncated to L), and leave the last W inputs as the
+    state."""
+    rng = np.random.default_rng(W * 2 + silu)
+    B, D, L = 2, 3, 9
+    x, w, b = rng.normal(size=(B, D, L)), rng.normal(size=(D, W)), rng.normal(size=D)
+    st = np.zeros((B, D, W))
+    ys = []
+    for t in range(L):
+        y, st = O.causal_conv1d_update(x[:, :, t], st, w, b, silu)
+        ys.append(y)
+    np.testing.assert_allclose(np.stack(ys, -1), O.dwconv1d(x, w, b, W - 1, L, silu=silu), atol=1e-12)
+    np.testing.assert_allclose(st, x[:, :, L - W:], atol=0)
+
+
+def test_causal_update_planted_mistakes():
+    rng = np.random.default_rng(5)
+    x, st, w, b = rng.normal(size=(2, 3)), rng.normal(size=(2, 3, 4)), rng.normal(size=(3, 4)), rng.normal(size=3)
+    y, s2 = O.causal_conv1d_update(x, st, w, b)
+    assert _far(O.causal_conv1d_update(x, st, w[:, ::-1].copy(), b)[0], y)     # reversed taps
+    assert _far(O.causal_conv1d_update(x, st, w, None)[0], y)                   # dropped bias
+    np.testing.assert_allclose(s2[..., :3], st[..., 1:], atol=0)                 # shift direction
+    np.testing.assert_allclose(s2[..., 3], x, atol=0)
