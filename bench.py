@@ -203,6 +203,37 @@ def bench_decode_detail(dev):
             "max_rel_err_vs_torch_ref": float(f"{err:.3g}")}
 
 
+def bench_gn_cl_detail(shape, G, silu, dev):
+    """Channels-last GroupNorm (+ SiLU), bf16: the native NHWC / NDHWC kernel against stock
+    F.group_norm on the same channels-last tensor (the reference contests CK here)."""
+    import torch
+    import torch.nn.functional as F
+    import amd_tuned_torch
+    from amd_tuned_torch import _native as nat
+    g = _gen(1008)
+    C = shape[1]
+    fmt = torch.channels_last if len(shape) == 4 else torch.channels_last_3d
+    x = (torch.randn(*shape, generator=g) + 0.5).to(torch.bfloat16).to(dev).contiguous(memory_format=fmt)
+    gm = (1 + 0.1 * torch.randn(C, generator=g)).to(torch.bfloat16).to(dev)
+    bt = (0.1 * torch.randn(C, generator=g)).to(torch.bfloat16).to(dev)
+    orig = amd_tuned_torch._ORIGINALS[(F, "group_norm")]
+
+    def stock():
+        y = orig(x, G, gm, bt, 1e-5)
+        return F.silu(y) if silu else y
+    y = nat.group_norm_cl(x, G, gm, bt, 1e-5, silu=silu)
+    ref = orig(x.float(), G, gm.float(), bt.float(), 1e-5)
+    ref = F.silu(ref) if silu else ref
+    err = max_rel_err(y, ref)
+    del y, ref
+    ms = graph_time_ms(lambda: nat.group_norm_cl(x, G, gm, bt, 1e-5, silu=silu), 20)
+    stock_ms = event_time_ms(stock, 10)
+    nbytes = 2 * x.numel() * x.element_size()
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"ms": round(ms, 4), "GB/s": round(gbs, 1), "roofline_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "variant": "native.cl", "stock_ms": round(stock_ms, 4), "max_rel_err_vs_stock_fp32": float(f"{err:.3g}")}
+
+
 def bench_gn_backward_detail(shape, G, dev):
     """GroupNorm backward (dx, dgamma, dbeta), bf16: native kernels against the torch-op
     backward that the reference uses.  Algorithmic bytes: read x and dy, write dx (the
@@ -600,6 +631,9 @@ def main():
                              bench_gn_detail((8, 512, 64, 64), 32, 1e-5, dtype, silu, dev)))
                 plan.append((f"c3_ncdhw_{dt_name}{sfx}", lambda dtype=dtype, silu=silu:
                              bench_gn_detail((1, 512, 16, 64, 64), 32, 1e-5, dtype, silu, dev)))
+        plan.append(("c3_nhwc_bf16", lambda: bench_gn_cl_detail((8, 512, 64, 64), 32, False, dev)))
+        plan.append(("c3_nhwc_bf16_silu", lambda: bench_gn_cl_detail((8, 512, 64, 64), 32, True, dev)))
+        plan.append(("c3_ndhwc_bf16", lambda: bench_gn_cl_detail((1, 512, 16, 64, 64), 32, False, dev)))
         plan.append(("c3_nchw_backward_bf16", lambda: bench_gn_backward_detail((8, 512, 64, 64), 32, dev)))
         plan.append(("c3_ncdhw_backward_bf16", lambda: bench_gn_backward_detail((1, 512, 16, 64, 64), 32, dev)))
         plan.append(("c5_gn_silu_bf16", lambda: bench_gn_detail((1, 256, 8, 64, 64), 32, 1e-6,

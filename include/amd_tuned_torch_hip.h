@@ -152,6 +152,22 @@ int atk_group_norm_fwd(const void* x, const void* gamma, const void* beta, void*
                        size_t workspace_bytes, atk_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * GroupNorm forward, channels-last layout (NHWC / NDHWC memory: x[n][s][c]), optional
+ * fused SiLU.  The reference serves this layout with Composable Kernel's groupnorm
+ * (amd_tuned_torch/ck_norm_ops.py:9-27,93-103, picked by the contest in
+ * amd_tuned_torch/_dispatch.py:2140-2200); same arithmetic and parameters as
+ * atk_group_norm_fwd.  Needs (C/G)*sizeof(dtype) % 16 == 0, C*sizeof(dtype)/16 dividing
+ * 256 (C <= 2048 for 16-bit types), G <= 256 and 16-byte aligned x / y (else
+ * ATK_UNSUPPORTED).  The workspace (atk_group_norm_cl_workspace_bytes) needs no
+ * initialisation.  Deterministic.
+ * ------------------------------------------------------------------------- */
+size_t atk_group_norm_cl_workspace_bytes(int64_t N, int64_t C, int64_t S, int G);
+int atk_group_norm_cl_fwd(const void* x, const void* gamma, const void* beta, void* y,
+                          int64_t N, int64_t C, int64_t S, int G, float eps, int fuse_silu,
+                          int dtype, int param_dtype, void* workspace, size_t workspace_bytes,
+                          atk_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * GroupNorm backward, NC[spatial] layout (replaces the torch-op backward of
  * amd_tuned_torch/_dispatch.py:2212-2302 behind _GroupNormFn, 2305-2359):
  *   x_hat = (x - mu) * rstd,  g = gamma_c * dy,

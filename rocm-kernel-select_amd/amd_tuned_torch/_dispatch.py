@@ -440,8 +440,39 @@ def _channels_last(x: torch.Tensor) -> bool:
     return False
 
 
+def _group_norm_channels_last(input, num_groups, weight, bias, eps, orig):
+    """Channels-last input: one native candidate (`native.cl`, the NHWC / NDHWC kernel)
+    against stock, keyed with the memory format like every GroupNorm contest (the
+    reference contests CK there, _dispatch.py:2140-2200)."""
+    if not (_usable(input, dtypes=_GROUPNORM_DTYPES) and _usable(weight, bias, dtypes=_GROUPNORM_DTYPES)
+            and isinstance(num_groups, int) and num_groups > 0 and input.shape[1] % num_groups == 0
+            and _native.available() and not _is_compiling()):
+        if _DEBUG:
+            _debug("group_norm", "stock", "channels-last outside this tier", input=input)
+        return orig(input, num_groups, weight, bias, eps)
+    native = _native_thunk(_native.group_norm_cl, input, num_groups, weight, bias, eps)
+    if kernel_select.enabled():
+        key = (input.dtype, tuple(input.shape), int(num_groups), True)
+        won = kernel_select.cached_key("group_norm", key)
+        if won == _NATIVE_PREFIX + "cl":
+            out = native()
+            if out is not None:
+                return out
+        elif won == "stock":
+            return orig(input, num_groups, weight, bias, eps)
+        out = kernel_select.pick_key("group_norm", key, [
+            (_NATIVE_PREFIX + "cl", native),
+            ("stock", lambda: orig(input, num_groups, weight, bias, eps))])
+        if out is not None:
+            return out
+    out = native()
+    return out if out is not None else orig(input, num_groups, weight, bias, eps)
+
+
 def _group_norm_accelerated_forward(input, num_groups, weight, bias, eps):
     orig = _ORIGINALS[(F, "group_norm")]
+    if isinstance(input, torch.Tensor) and _channels_last(input):
+        return _group_norm_channels_last(input, num_groups, weight, bias, eps, orig)
     if not (isinstance(input, torch.Tensor) and input.dim() >= 2 and input.is_contiguous()
             and _usable(input, dtypes=_GROUPNORM_DTYPES)
             and _usable(weight, bias, dtypes=_GROUPNORM_DTYPES)

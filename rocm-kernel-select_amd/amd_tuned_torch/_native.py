@@ -37,7 +37,8 @@ EXPORTED_SYMBOLS = (
     "atk_dwconv1d_fwd", "atk_causal_conv1d_update", "atk_dwconv1d_bwd_weight_workspace_bytes",
     "atk_dwconv1d_bwd_weight",
     "atk_group_norm_workspace_bytes",
-    "atk_group_norm_workspace_zero_bytes", "atk_group_norm_fwd", "atk_group_norm_bwd_workspace_bytes",
+    "atk_group_norm_workspace_zero_bytes", "atk_group_norm_fwd", "atk_group_norm_cl_workspace_bytes",
+    "atk_group_norm_cl_fwd", "atk_group_norm_bwd_workspace_bytes",
     "atk_group_norm_bwd", "atk_conv_workspace_bytes",
     "atk_conv_fwd",
 )
@@ -68,6 +69,10 @@ def _declare(lib) -> None:
     lib.atk_dwconv1d_bwd_weight_workspace_bytes.restype = sz
     lib.atk_dwconv1d_bwd_weight.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, i32, i64, i32, vp, sz, vp]
     lib.atk_dwconv1d_bwd_weight.restype = i32
+    lib.atk_group_norm_cl_workspace_bytes.argtypes = [i64, i64, i64, i32]
+    lib.atk_group_norm_cl_workspace_bytes.restype = sz
+    lib.atk_group_norm_cl_fwd.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, c.c_float, i32, i32, i32, vp, sz, vp]
+    lib.atk_group_norm_cl_fwd.restype = i32
     lib.atk_group_norm_bwd_workspace_bytes.argtypes = [i64, i64]
     lib.atk_group_norm_bwd_workspace_bytes.restype = sz
     lib.atk_group_norm_bwd.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i32, c.c_float, i32, i32, vp, sz, vp]
@@ -379,6 +384,50 @@ def group_norm(input: torch.Tensor, num_groups: int, weight: Optional[torch.Tens
                               float(eps), int(bool(silu)), dt, pdt, v, ws.data_ptr(), ws.numel(),
                               _stream(input))
     _check(rc, "group_norm")
+    return y
+
+
+def is_channels_last(x: torch.Tensor) -> bool:
+    """4-D channels_last or 5-D channels_last_3d memory that is not also plain contiguous."""
+    if x.dim() == 4:
+        return x.is_contiguous(memory_format=torch.channels_last) and not x.is_contiguous()
+    if x.dim() == 5:
+        return x.is_contiguous(memory_format=torch.channels_last_3d) and not x.is_contiguous()
+    return False
+
+
+def group_norm_cl(input: torch.Tensor, num_groups: int, weight: Optional[torch.Tensor] = None,
+                  bias: Optional[torch.Tensor] = None, eps: float = 1e-5, *, silu: bool = False,
+                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """group_norm for channels-last input (NHWC / NDHWC memory, the layout the reference
+    serves with CK, ck_norm_ops.py:9-27); the output keeps the input's memory format.
+    Raises Unsupported for shapes the kernel does not take (C/G not a multiple of 16 bytes,
+    C above 2048 16-bit channels, misaligned data)."""
+    _require_cuda(input, weight, bias)
+    if not is_channels_last(input):
+        raise RuntimeError("group_norm_cl: input must be channels_last / channels_last_3d")
+    if input.dtype not in _DTYPE_CODE:
+        raise RuntimeError("group_norm_cl: input must be float16, bfloat16 or float32")
+    N, C = input.shape[0], input.shape[1]
+    G = int(num_groups)
+    if G <= 0 or C % G:
+        raise RuntimeError("group_norm_cl: channels must be divisible by num_groups")
+    if weight is not None and bias is not None and weight.dtype != bias.dtype:
+        raise RuntimeError("group_norm_cl: weight and bias must share a dtype")
+    S = input.numel() // max(1, N * C)
+    pdt = weight.dtype if weight is not None else (bias.dtype if bias is not None else input.dtype)
+    if pdt not in _DTYPE_CODE:
+        raise RuntimeError("group_norm_cl: weight/bias must be float16, bfloat16 or float32")
+    weight = weight.contiguous() if weight is not None else None
+    bias = bias.contiguous() if bias is not None else None
+    y = out if out is not None else torch.empty_like(input)  # same memory format
+    L_ = lib()
+    nbytes = L_.atk_group_norm_cl_workspace_bytes(N, C, S, G)
+    ws = workspace(input.device, "group_norm_cl", max(nbytes, 1))
+    rc = L_.atk_group_norm_cl_fwd(_ptr(input), _ptr(weight), _ptr(bias), _ptr(y), N, C, S, G, float(eps),
+                                  int(bool(silu)), _DTYPE_CODE[input.dtype], _DTYPE_CODE[pdt], _ptr(ws),
+                                  ws.numel(), _stream(input))
+    _check(rc, "group_norm_cl")
     return y
 
 

@@ -47,13 +47,16 @@ def _stock_group_norm_silu(x, num_groups, weight, bias, eps):
 
 
 def _layout(x: torch.Tensor) -> str:
-    return ("nhwc" if x.dim() == 4 and x.is_contiguous(memory_format=torch.channels_last)
-            and not x.is_contiguous() else "nchw")
+    if _native.is_channels_last(x):
+        return "nhwc" if x.dim() == 4 else "ndhwc"
+    return "nchw"
 
 
-def _eligible(x, num_groups, weight, bias) -> bool:
+def _eligible(x, num_groups, weight, bias, layout_ok: bool = False) -> bool:
+    """Native-eligible input: enabled, GPU, a supported dtype, contiguous (or, with
+    layout_ok, any layout the caller handles), plain tensor types, no gradient needed."""
     if not (enabled() and isinstance(x, torch.Tensor) and x.is_cuda and x.dim() >= 3
-            and x.dtype in _DTYPES and x.is_contiguous()
+            and x.dtype in _DTYPES and (layout_ok or x.is_contiguous())
             and type(x) in (torch.Tensor, nn.Parameter)):
         return False
     if not isinstance(num_groups, int) or num_groups <= 0 or x.shape[1] % num_groups != 0:
@@ -67,13 +70,42 @@ def _eligible(x, num_groups, weight, bias) -> bool:
     return True
 
 
+def _group_norm_silu_cl(x, num_groups, weight, bias, eps, stock):
+    if not _eligible(x, num_groups, weight, bias, layout_ok=True):
+        return stock()
+
+    def native():
+        try:
+            return _native.group_norm_cl(x, num_groups, weight, bias, eps, silu=True)
+        except _native.Unsupported:
+            return None
+
+    key = ("gn_silu", tuple(x.shape), str(x.dtype), num_groups, weight is not None,
+           bias is not None, _layout(x))
+    won = kernel_select.cached_key("group_norm_silu", key)
+    if won == "stock":
+        return stock()
+    if won == "native.cl":
+        out = native()
+        if out is not None:
+            return out
+    out = kernel_select.pick_key("group_norm_silu", key, [("native.cl", native), ("stock", stock)])
+    if out is not None:
+        return out
+    out = native()
+    return out if out is not None else stock()
+
+
 def group_norm_silu(x: torch.Tensor, num_groups: int, weight: Optional[torch.Tensor] = None,
                     bias: Optional[torch.Tensor] = None, eps: float = 1e-5) -> torch.Tensor:
-    """SiLU(GroupNorm(x)) -- fused native kernel where it wins, stock where it does not."""
-    if not _eligible(x, num_groups, weight, bias):
+    """SiLU(GroupNorm(x)) -- fused native kernel where it wins, stock where it does not.
+    Channels-last input takes the NHWC / NDHWC kernel (`native.cl`) with the SiLU fused."""
+    def stock():
         return _stock_group_norm_silu(x, num_groups, weight, bias, eps)
 
-    def stock():
+    if isinstance(x, torch.Tensor) and x.is_cuda and _native.is_channels_last(x):
+        return _group_norm_silu_cl(x, num_groups, weight, bias, eps, stock)
+    if not _eligible(x, num_groups, weight, bias):
         return _stock_group_norm_silu(x, num_groups, weight, bias, eps)
 
     key = ("gn_silu", tuple(x.shape), str(x.dtype), num_groups, weight is not None,

@@ -26,6 +26,7 @@
 //            HBM traffic: one read + one write of the tensor.
 //   twopass  Streaming fallback for any size / alignment: a statistics kernel writes
 //            per-slice (mean, M2) partials, an apply kernel merges them and normalises.
+#include <algorithm>
 #include <cstdlib>
 
 #include "atk_common.h"
@@ -811,6 +812,184 @@ int launch_gn_bwd(const GnBwdArgs& a, int64_t rows, hipStream_t s) {
   return check_launch("gn_bwd_finalize_kernel");
 }
 
+// ---------------------------------------------------------------------------------------
+// Channels-last GroupNorm forward (NHWC / NDHWC memory: x[n][s][c]).  The reference serves
+// this layout with Composable Kernel's groupnorm (amd_tuned_torch/ck_norm_ops.py:9-27,
+// 93-103); the arithmetic is the NC[S] kernel's: group (n, g) = channels [g*cpg, (g+1)*cpg)
+// at every spatial position.  Two kernels, deterministic:
+//   stats: a workgroup per (n, spatial chunk); thread t owns one 16-byte channel vector
+//          (column t % CV, so one group: cpg % VEC == 0) on rows t / CV, t / CV + R, ... and
+//          accumulates shifted sums; one thread per group then merges that group's
+//          per-thread (n, mean, M2) with Chan's formula in a fixed order;
+//   merge: one wave per (n, g) merges the group's chunk partials (the fixed-order butterfly
+//          of the NC[S] kernels) into (mean, rstd);
+//   apply: a workgroup per (n, chunk) stages per-channel scale / shift in LDS and
+//          normalises its chunk (+ SiLU).
+// Requires C / VEC to divide the workgroup size (C <= 2048 for 16-bit types) and 16-byte
+// aligned x / y (host check).  Traffic: x read twice (the second read mostly from the
+// Infinity Cache), y written once.
+constexpr int GN_CL_NT = 256;
+constexpr int GN_CL_MAXC = 2048;
+constexpr int GN_CL_MAXG = 256;
+
+struct GnClArgs {
+  const void* x;
+  const void* gamma;
+  const void* beta;
+  void* y;
+  float* part;        // [N][NCH][G][2] (mean, M2) of each chunk's slice of each group
+  float* stat;        // [N][G][2] (mean, rstd)
+  int64_t S, SC;      // spatial positions, positions per chunk
+  uint32_t C, G, cpg;
+  int NCH;
+  float eps;
+  int pdt;
+};
+
+template <typename T>
+__global__ __launch_bounds__(GN_CL_NT) void gn_cl_stats_kernel(GnClArgs a) {
+  constexpr int VEC = 16 / sizeof(T);
+  __shared__ float sm[GN_CL_NT], sq[GN_CL_NT], sn[GN_CL_NT];
+  const int n = blockIdx.y, ch = blockIdx.x;
+  const int CV = (int)(a.C / VEC), R = GN_CL_NT / CV;
+  const int v = threadIdx.x % CV, rr = threadIdx.x / CV;
+  const int64_t s0 = (int64_t)ch * a.SC, s1 = min(a.S, s0 + a.SC);
+  const T* __restrict__ xn = static_cast<const T*>(a.x) + (int64_t)n * a.S * a.C + v * VEC;
+  float K = 0.f, t1 = 0.f, t2 = 0.f, cnt = 0.f;
+  if (s0 + rr < s1) K = to_f32(xn[(s0 + rr) * a.C]);
+  for (int64_t s = s0 + rr; s < s1; s += R) {
+    Vec16<T> xv;
+    xv.raw = ld16<false>(xn + s * a.C);  // cached: the apply kernel reads x again
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+      const float d = to_f32(xv.e[k]) - K;
+      t1 += d;
+      t2 = fmaf(d, d, t2);
+    }
+    cnt += (float)VEC;
+  }
+  float mean_t = 0.f, m2_t = 0.f;
+  if (cnt > 0.f) {
+    const float q = t1 / cnt;
+    mean_t = K + q;
+    m2_t = fmaxf(fmaf(-t1, q, t2), 0.f);
+  }
+  sm[threadIdx.x] = mean_t;
+  sq[threadIdx.x] = m2_t;
+  sn[threadIdx.x] = cnt;
+  __syncthreads();
+  const int cpv = (int)(a.cpg / VEC);  // vectors per group
+  for (int g = threadIdx.x; g < (int)a.G; g += GN_CL_NT) {
+    // entries of group g: rows rr' in [0, R), columns [g*cpv, (g+1)*cpv)
+    float nt = 0.f, mt = 0.f;
+    for (int r2 = 0; r2 < R; ++r2)
+      for (int c2 = 0; c2 < cpv; ++c2) {
+        const int e = r2 * CV + g * cpv + c2;
+        nt += sn[e];
+        mt = fmaf(sn[e], sm[e], mt);
+      }
+    const float mean = nt > 0.f ? mt / nt : 0.f;
+    float m2 = 0.f;
+    for (int r2 = 0; r2 < R; ++r2)
+      for (int c2 = 0; c2 < cpv; ++c2) {
+        const int e = r2 * CV + g * cpv + c2;
+        const float d = sm[e] - mean;
+        m2 += sq[e] + sn[e] * d * d;
+      }
+    float* o = a.part + (((int64_t)n * a.NCH + ch) * a.G + g) * 2;
+    o[0] = mean;
+    o[1] = m2;
+  }
+}
+
+__global__ __launch_bounds__(64) void gn_cl_merge_kernel(GnClArgs a) {
+  const int64_t ng = blockIdx.x;  // n * G + g
+  const int64_t n = ng / a.G, g = ng - n * a.G;
+  const float* p = a.part + (n * a.NCH * a.G + g) * 2;
+  const int64_t step = (int64_t)a.G * 2;
+  float mean, var;
+  wave_merge(a.NCH, a.SC * a.cpg, a.S * a.cpg, [&](int i) { return p[i * step]; },
+             [&](int i) { return p[i * step + 1]; }, mean, var);
+  if (threadIdx.x == 0) {
+    a.stat[ng * 2] = mean;
+    a.stat[ng * 2 + 1] = 1.0f / sqrtf(var + a.eps);
+  }
+}
+
+template <typename T, bool SILU>
+__global__ __launch_bounds__(GN_CL_NT) void gn_cl_apply_kernel(GnClArgs a) {
+  constexpr int VEC = 16 / sizeof(T);
+  __shared__ float scs[GN_CL_MAXC], shs[GN_CL_MAXC];
+  __shared__ float gmean[GN_CL_MAXG], grstd[GN_CL_MAXG];
+  const int n = blockIdx.y, ch = blockIdx.x;
+  for (int g = threadIdx.x; g < (int)a.G; g += GN_CL_NT) {
+    gmean[g] = a.stat[((int64_t)n * a.G + g) * 2];
+    grstd[g] = a.stat[((int64_t)n * a.G + g) * 2 + 1];
+  }
+  __syncthreads();
+  for (uint32_t c = threadIdx.x; c < a.C; c += GN_CL_NT) {
+    const uint32_t g = c / a.cpg;
+    const float gm = a.gamma ? load_param(a.gamma, a.pdt, c) : 1.f;
+    const float bt = a.beta ? load_param(a.beta, a.pdt, c) : 0.f;
+    const float sc = grstd[g] * gm;
+    scs[c] = sc;
+    shs[c] = bt - gmean[g] * sc;
+  }
+  __syncthreads();
+  const int CV = (int)(a.C / VEC), R = GN_CL_NT / CV;
+  const int v = threadIdx.x % CV, rr = threadIdx.x / CV;
+  const int64_t s0 = (int64_t)ch * a.SC, s1 = min(a.S, s0 + a.SC);
+  const int64_t base = (int64_t)n * a.S * a.C + v * VEC;
+  const T* __restrict__ xn = static_cast<const T*>(a.x) + base;
+  T* __restrict__ yn = static_cast<T*>(a.y) + base;
+  float sc[VEC], sh[VEC];
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) {
+    sc[k] = scs[v * VEC + k];
+    sh[k] = shs[v * VEC + k];
+  }
+  for (int64_t s = s0 + rr; s < s1; s += R) {
+    Vec16<T> xv;
+    xv.raw = ld16<true>(xn + s * a.C);
+    float o[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+      o[k] = fmaf(to_f32(xv.e[k]), sc[k], sh[k]);
+      if constexpr (SILU) o[k] = silu_f32(o[k]);
+    }
+    st16<true>(yn + s * a.C, pack16<T>(o));
+  }
+}
+
+struct GnClPlan {
+  int NCH;
+  int64_t SC;
+};
+
+inline GnClPlan plan_gn_cl(int64_t N, int64_t S) {
+  // about 2048 workgroups over the chip, at least 64 positions per chunk
+  int64_t nch = (2048 + N - 1) / N;
+  nch = std::max<int64_t>(1, std::min<int64_t>(nch, (S + 63) / 64));
+  GnClPlan p;
+  p.SC = (S + nch - 1) / nch;
+  p.NCH = (int)((S + p.SC - 1) / p.SC);
+  return p;
+}
+
+template <typename T>
+int launch_gn_cl(const GnClArgs& a, int N, int silu, hipStream_t s) {
+  const dim3 grid((unsigned)a.NCH, (unsigned)N), block(GN_CL_NT);
+  hipLaunchKernelGGL((gn_cl_stats_kernel<T>), grid, block, 0, s, a);
+  int rc = check_launch("gn_cl_stats_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(gn_cl_merge_kernel, dim3((unsigned)(N * a.G)), dim3(64), 0, s, a);
+  rc = check_launch("gn_cl_merge_kernel");
+  if (rc) return rc;
+  if (silu) hipLaunchKernelGGL((gn_cl_apply_kernel<T, true>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((gn_cl_apply_kernel<T, false>), grid, block, 0, s, a);
+  return check_launch("gn_cl_apply_kernel");
+}
+
 }  // namespace
 
 int group_norm_num_variants() { return kNumGn; }
@@ -927,5 +1106,47 @@ extern "C" int atk_group_norm_bwd(const void* x, const void* dy, const void* gam
     case ATK_F32: return launch_gn_bwd<float>(a, rows, s);
     case ATK_F16: return launch_gn_bwd<_Float16>(a, rows, s);
     default: return launch_gn_bwd<__bf16>(a, rows, s);
+  }
+}
+
+extern "C" size_t atk_group_norm_cl_workspace_bytes(int64_t N, int64_t C, int64_t S, int G) {
+  if (N <= 0 || C <= 0 || S <= 0 || G <= 0) return 0;
+  const atk::GnClPlan p = atk::plan_gn_cl(N, S);
+  return ((size_t)N * (size_t)p.NCH + (size_t)N) * (size_t)G * 2 * sizeof(float);
+}
+
+extern "C" int atk_group_norm_cl_fwd(const void* x, const void* gamma, const void* beta, void* y, int64_t N,
+                                     int64_t C, int64_t S, int G, float eps, int fuse_silu, int dtype,
+                                     int param_dtype, void* workspace, size_t ws_bytes, atk_stream_t stream) {
+  using namespace atk;
+  if (!dtype_ok(dtype) || ((gamma || beta) && !dtype_ok(param_dtype)))
+    return fail(ATK_EINVAL, "group_norm (channels-last): unknown dtype code");
+  if (N < 0 || C <= 0 || S < 0 || G <= 0) return fail(ATK_EINVAL, "group_norm (channels-last): bad sizes");
+  if (C % G) return fail(ATK_EINVAL, "group_norm (channels-last): channels (%lld) not divisible by groups (%d)",
+                         (long long)C, G);
+  if (N == 0 || S == 0) return ATK_OK;
+  if (!x || !y) return fail(ATK_EINVAL, "group_norm (channels-last): null pointer");
+  const int64_t es = (int64_t)dtype_size(dtype), vec = 16 / es;
+  const int64_t cpg = C / G;
+  if (cpg % vec || C > GN_CL_MAXC || G > GN_CL_MAXG || GN_CL_NT % (C / vec) || !aligned16(x) || !aligned16(y))
+    return fail(ATK_UNSUPPORTED, "group_norm (channels-last): needs C/G %% %lld == 0, C/%lld dividing %d and "
+                "16-byte aligned tensors", (long long)vec, (long long)vec, GN_CL_NT);
+  if (N >= 65536) return fail(ATK_UNSUPPORTED, "group_norm (channels-last): batch too large");
+  const GnClPlan p = plan_gn_cl(N, S);
+  const size_t need = ((size_t)N * (size_t)p.NCH + (size_t)N) * (size_t)G * 2 * sizeof(float);
+  if (!workspace || ws_bytes < need)
+    return fail(ATK_EINVAL, "group_norm (channels-last): workspace of %zu bytes needed", need);
+  GnClArgs a;
+  a.x = x; a.gamma = gamma; a.beta = beta; a.y = y;
+  a.part = static_cast<float*>(workspace);
+  a.stat = a.part + (size_t)N * p.NCH * G * 2;
+  a.S = S; a.SC = p.SC; a.NCH = p.NCH;
+  a.C = (uint32_t)C; a.G = (uint32_t)G; a.cpg = (uint32_t)cpg;
+  a.eps = eps; a.pdt = param_dtype;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case ATK_F32: return launch_gn_cl<float>(a, (int)N, fuse_silu, s);
+    case ATK_F16: return launch_gn_cl<_Float16>(a, (int)N, fuse_silu, s);
+    default: return launch_gn_cl<__bf16>(a, (int)N, fuse_silu, s);
   }
 }

@@ -100,6 +100,11 @@ def test_argument_validation_codes(nat):
     assert zero == lib.atk_group_norm_workspace_zero_bytes(1, 64, 7, 2, 0, 6)
     assert lib.atk_group_norm_fwd(None, None, None, None, 2, 6, 4, 3, 1e-5, 0, 1, 1, 0, None, 0, None) == nat.ATK_EINVAL
     assert lib.atk_group_norm_fwd(None, None, None, None, 2, 6, 4, 3, 1e-5, 0, 1, 1, 99, None, 0, None) == nat.ATK_EINVAL
+    # group norm, channels-last
+    assert lib.atk_group_norm_cl_workspace_bytes(2, 64, 100, 8) > 0
+    assert lib.atk_group_norm_cl_fwd(None, None, None, None, 2, 6, 4, 4, 1e-5, 0, 1, 1, None, 0, None) == nat.ATK_EINVAL
+    assert lib.atk_group_norm_cl_fwd(None, None, None, None, 2, 64, 4, 8, 1e-5, 0, 1, 1, None, 0, None) == nat.ATK_EINVAL
+    assert lib.atk_group_norm_cl_fwd(None, None, None, None, 0, 64, 4, 8, 1e-5, 0, 1, 1, None, 0, None) == nat.ATK_OK
     # group norm backward
     assert lib.atk_group_norm_bwd_workspace_bytes(2, 6) == 2 * 6 * 6 * 4
     assert lib.atk_group_norm_bwd(None, None, None, None, None, None, 2, 6, 4, 4, 1e-5, 1, 1, None, 0, None) == nat.ATK_EINVAL

@@ -290,3 +290,45 @@ def test_group_norm_backward_c3_full_size(dev):
     assert O.max_rel_err(dx.cpu(), rdx) <= BAR[torch.bfloat16]
     assert O.max_rel_err(dg.cpu(), rdg) <= BWD_BAR_P[torch.bfloat16]
     assert O.max_rel_err(db.cpu(), rdb) <= BWD_BAR_P[torch.bfloat16]
+
+
+# ---------------------------------------------------------------------------
+# channels-last forward (atk_group_norm_cl_fwd)
+# ---------------------------------------------------------------------------
+CL_SHAPES = [
+    ((2, 64, 8, 8), 8),
+    ((8, 512, 16, 16), 32),         # C3-like channels, NHWC
+    ((1, 256, 4, 16, 16), 32),      # C5-like channels, NDHWC
+    ((3, 32, 7, 5), 4),             # odd spatial sizes
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("shape_g", CL_SHAPES, ids=lambda s: "x".join(map(str, s[0])) + f"_g{s[1]}")
+def test_group_norm_channels_last(dev, shape_g, dtype):
+    shape, G = shape_g
+    nat = _native()
+    x, gm, bt = _inputs(shape, dtype, seed=len(shape) + G + 200)
+    fmt = torch.channels_last if len(shape) == 4 else torch.channels_last_3d
+    xd = x.to(dev).contiguous(memory_format=fmt)
+    for silu in (False, True):
+        y = nat.group_norm_cl(xd, G, gm.to(dev), bt.to(dev), 1e-5, silu=silu)
+        torch.cuda.synchronize()
+        assert y.is_contiguous(memory_format=fmt)
+        _check(y.cpu().contiguous(), x, G, gm, bt, 1e-5, silu=silu, what=f"cl silu={silu}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+def test_group_norm_channels_last_through_patched_api(dev, dtype):
+    """F.group_norm and conv_fusion_ops.group_norm_silu on channels-last tensors take the
+    native channels-last kernel (or stock, whichever the contest keeps) and match the oracle."""
+    import torch.nn.functional as F
+    import amd_tuned_torch  # noqa: F401
+    from amd_tuned_torch import conv_fusion_ops
+    shape, G = (4, 128, 12, 12), 16
+    x, gm, bt = _inputs(shape, dtype, seed=303)
+    xd = x.to(dev).contiguous(memory_format=torch.channels_last)
+    y = F.group_norm(xd, G, gm.to(dev), bt.to(dev), 1e-5)
+    _check(y.cpu().contiguous(), x, G, gm, bt, 1e-5, what="F.group_norm channels-last")
+    y2 = conv_fusion_ops.group_norm_silu(xd, G, gm.to(dev), bt.to(dev), 1e-5)
+    _check(y2.cpu().contiguous(), x, G, gm, bt, 1e-5, silu=True, what="group_norm_silu channels-last")
