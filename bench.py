@@ -343,6 +343,42 @@ def bench_conv_detail(xs, ws, pad, dtype, dev, iters=20):
     return res
 
 
+def bench_conv_dgrad_detail(xs, ws, pad, dtype, dev, iters=10):
+    """Input gradient of a stride-1 conv3d through the accelerated forward on dy with
+    transposed / flipped weights (what _ConvFn's backward does), against stock
+    aten.convolution_backward computing the same input gradient."""
+    import torch
+    import torch.nn.functional as F
+    import amd_tuned_torch
+    from amd_tuned_torch import _dispatch
+    g = _gen(1009)
+    fan_in = math.prod(ws[1:])
+    x = torch.randn(*xs, generator=g).to(dtype).to(dev)
+    w = (torch.randn(*ws, generator=g) * math.sqrt(2.0 / fan_in)).to(dtype).to(dev)
+    orig = amd_tuned_torch._ORIGINALS[(F, "conv3d")]
+    dy = torch.randn(xs[0], ws[0], *[xs[2 + i] + 2 * pad - ws[2 + i] + 1 for i in range(3)],
+                     generator=g).to(dtype).to(dev)
+    pad_t = _dispatch._dgrad_padding(w, 1, pad, 1, 1, 3)
+
+    def fwd(i, ww, b, s, p, d, gr):
+        return _dispatch._conv_accelerated_forward(3, i, ww, b, s, p, d, gr, orig)
+    gi = _dispatch._dgrad_via_forward(dy, w, pad_t, 3, fwd)
+    ref = torch.ops.aten.convolution_backward(dy.float(), x.float(), w.float(), None, [1] * 3, [pad] * 3,
+                                              [1] * 3, False, [0] * 3, 1, [True, False, False])[0]
+    err = max_rel_err(gi, ref)
+    del gi, ref
+    ms = event_time_ms(lambda: _dispatch._dgrad_via_forward(dy, w, pad_t, 3, fwd), iters)
+    stock_ms = event_time_ms(lambda: torch.ops.aten.convolution_backward(
+        dy, x, w, None, [1] * 3, [pad] * 3, [1] * 3, False, [0] * 3, 1, [True, False, False]), 3)
+    osp = math.prod(dy.shape[2:])
+    flops = 2.0 * xs[0] * ws[0] * osp * ws[1] * math.prod(ws[2:])
+    key = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[dtype]
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"ms": round(ms, 4), "TFLOP/s": round(tf, 2), "roofline_frac": round(tf / MFMA_PEAK_TFLOPS[key], 4),
+            "variant": "forward conv on dy (transposed, flipped weights)",
+            "stock_dgrad_ms": round(stock_ms, 3), "max_rel_err_vs_stock_fp32": float(f"{err:.3g}")}
+
+
 def calibration(dev):
     """Achievable ceilings on this box: a large bf16 GEMM through torch.matmul (hipBLASLt),
     and torch's device copy at the tensor sizes the HBM-bound configs move."""
@@ -644,6 +680,8 @@ def main():
             ("c4_conv3d_scaled_bf16", lambda: bench_conv_detail((2, 128, 16, 64, 64), (128, 128, 3, 3, 3), 1, torch.bfloat16, dev, 10)),
             ("c5_conv3d_bf16", lambda: bench_conv_detail((1, 256, 8, 64, 64), (256, 256, 3, 3, 3), 1, torch.bfloat16, dev, 10)),
             ("c5_conv3d_k7_fp16", lambda: bench_conv_detail((1, 64, 16, 32, 32), (64, 64, 7, 7, 7), 3, torch.float16, dev, 10)),
+            ("c5_conv3d_dgrad_bf16", lambda: bench_conv_dgrad_detail((1, 256, 8, 64, 64), (256, 256, 3, 3, 3), 1, torch.bfloat16, dev)),
+            ("c4_conv3d_scaled_dgrad_bf16", lambda: bench_conv_dgrad_detail((2, 128, 16, 64, 64), (128, 128, 3, 3, 3), 1, torch.bfloat16, dev)),
         ]
         plan.append(("calibration", lambda: calibration(dev)))
         for name, fn in plan:

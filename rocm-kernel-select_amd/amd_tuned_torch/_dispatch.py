@@ -331,15 +331,45 @@ def _conv_accelerated_forward(nd: int, input, weight, bias, stride, padding, dil
     return orig(input, weight, bias, stride, padding, dilation, groups)
 
 
+def _dgrad_padding(weight, stride, padding, dilation, groups, nd):
+    """Padding of the forward conv that computes the input gradient (k-1-p per dim), or None
+    when that identity does not apply (stride or dilation != 1, groups != 1, string padding,
+    p outside [0, k-1])."""
+    tup = _triple if nd == 3 else _pair
+    if groups != 1 or isinstance(padding, str):
+        return None
+    try:
+        s, p, d = tup(stride), tup(padding), tup(dilation)
+    except (TypeError, ValueError):
+        return None
+    if any(v != 1 for v in s) or any(v != 1 for v in d):
+        return None
+    ks = weight.shape[2:]
+    if any(not (0 <= pi <= k - 1) for pi, k in zip(p, ks)):
+        return None
+    return [k - 1 - pi for pi, k in zip(p, ks)]
+
+
+def _dgrad_via_forward(grad_output, weight, pad_t, nd, fwd):
+    """dL/dx of a stride-1, dilation-1 conv: the forward conv of dy with the weights swapped
+    in (Co, Ci) and flipped in space, padding k-1-p -- so the input gradient runs on the
+    forward path (and its per-shape contest) instead of a separate dgrad."""
+    wt = weight.transpose(0, 1).flip(list(range(2, 2 + nd))).contiguous()
+    return fwd(grad_output.contiguous(), wt, None, 1, pad_t, 1, 1)
+
+
 class _ConvFn(torch.autograd.Function):
-    """Accelerated forward, stock backward through aten.convolution_backward -- the op
-    autograd would have used unpatched (reference _Conv3dFn, _dispatch.py:2029-2075)."""
+    """Accelerated forward; the input gradient (stride 1, dilation 1, groups 1) through the
+    same accelerated forward on dy with transposed, flipped weights; the rest through
+    aten.convolution_backward -- the op autograd would have used unpatched (reference
+    _Conv3dFn, _dispatch.py:2029-2075)."""
 
     @staticmethod
     def forward(ctx, input, weight, bias, stride, padding, dilation, groups, nd, fwd):
         ctx.save_for_backward(input, weight)
         ctx.bias_sizes = [bias.shape[0]] if bias is not None else None
         ctx.conf = (stride, padding, dilation, groups, nd)
+        ctx.fwd = fwd
         return fwd(input, weight, bias, stride, padding, dilation, groups)
 
     @staticmethod
@@ -350,10 +380,22 @@ class _ConvFn(torch.autograd.Function):
                  ctx.bias_sizes is not None and bool(ctx.needs_input_grad[2])]
         if not any(needs):
             return (None,) * 9
-        tup = _triple if nd == 3 else _pair
-        gi, gw, gb = torch.ops.aten.convolution_backward(
-            grad_output.contiguous(), input, weight, ctx.bias_sizes, list(tup(stride)),
-            list(tup(padding)), list(tup(dilation)), False, [0] * nd, groups, needs)
+        gi = None
+        if needs[0] and input.is_cuda:
+            pad_t = _dgrad_padding(weight, stride, padding, dilation, groups, nd)
+            if pad_t is not None:
+                gi = _dgrad_via_forward(grad_output, weight.detach(), pad_t, nd, ctx.fwd)
+                if tuple(gi.shape) != tuple(input.shape):
+                    gi = None
+                else:
+                    needs[0] = False
+        gw = gb = None
+        if any(needs):
+            tup = _triple if nd == 3 else _pair
+            ai, gw, gb = torch.ops.aten.convolution_backward(
+                grad_output.contiguous(), input, weight, ctx.bias_sizes, list(tup(stride)),
+                list(tup(padding)), list(tup(dilation)), False, [0] * nd, groups, needs)
+            gi = ai if gi is None else gi
         return gi, gw, gb, None, None, None, None, None, None
 
 
@@ -697,7 +739,8 @@ __all__ = [
     "_grad_safe", "_is_plain_tensor", "_usable", "_install", "_restore", "_triple", "_pair",
     "_is_pointwise_conv2d", "_conv_accelerated_forward", "_ConvFn", "_patched_conv2d",
     "_patched_conv3d", "_group_norm_native", "_group_norm_accelerated_forward",
-    "_group_norm_backward", "_GroupNormFn", "_patched_group_norm", "_patched_sequential_forward",
+    "_group_norm_backward", "_GroupNormFn", "_dgrad_padding", "_dgrad_via_forward",
+    "_patched_group_norm", "_patched_sequential_forward",
     "enable", "disable", "is_enabled", "_ORIG_JIT_SCRIPT", "_ORIG_JIT_TRACE",
     "_script_with_stock_ops", "_trace_with_stock_ops",
 ]

@@ -354,3 +354,29 @@ def test_conv1d_padding_resolution():
     assert miopen_fallback._resolve_padding("same", 4, 10) == (1, 10)
     assert miopen_fallback._resolve_padding(65, 3, 10) is None
     assert miopen_fallback._resolve_padding("circular", 3, 10) is None
+
+
+def test_conv_dgrad_as_forward_conv_matches_stock():
+    """The input gradient of a stride-1 conv equals the forward conv of dy with the weights
+    swapped in (Co, Ci) and flipped in space, padding k-1-p -- the identity _ConvFn's
+    backward uses on the GPU -- for conv3d and conv2d, asymmetric kernels and paddings."""
+    torch.manual_seed(4)
+    for nd, xs, ws, pad in ((3, (2, 3, 5, 6, 7), (4, 3, 3, 2, 3), (1, 0, 2)),
+                            (2, (1, 2, 7, 6), (3, 2, 3, 3), (1, 1)),
+                            (3, (1, 2, 6, 6, 6), (2, 2, 3, 3, 3), (0, 0, 0))):
+        x = torch.randn(*xs, dtype=torch.float64, requires_grad=True)
+        w = torch.randn(*ws, dtype=torch.float64)
+        conv = torch.nn.functional.conv3d if nd == 3 else torch.nn.functional.conv2d
+        stock = _dispatch._ORIGINALS[(torch.nn.functional, "conv3d" if nd == 3 else "conv2d")]
+        y = stock(x, w, None, 1, pad, 1, 1)
+        dy = torch.randn_like(y)
+        ref, = torch.autograd.grad(y, x, dy)
+        pad_t = _dispatch._dgrad_padding(w, 1, pad, 1, 1, nd)
+        got = _dispatch._dgrad_via_forward(dy, w, pad_t, nd, lambda i, ww, b, s, p, d, g: stock(i, ww, b, s, p, d, g))
+        torch.testing.assert_close(got, ref)
+        del conv
+    w = torch.zeros(2, 2, 3, 3, 3)
+    assert _dispatch._dgrad_padding(w, 2, 1, 1, 1, 3) is None          # stride 2
+    assert _dispatch._dgrad_padding(w, 1, 1, 2, 1, 3) is None          # dilation 2
+    assert _dispatch._dgrad_padding(w, 1, 3, 1, 1, 3) is None          # padding > k-1
+    assert _dispatch._dgrad_padding(w, 1, "same", 1, 1, 3) is None

@@ -152,3 +152,29 @@ def test_conv3d_config_full_size(dev, cfg):
         ran += 1
     del stock
     assert ran >= 1
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+def test_conv3d_autograd_dgrad_through_forward(dev, dtype):
+    """Training path: patched F.conv3d with requires_grad runs the accelerated forward, the
+    input gradient through the same forward on dy with transposed / flipped weights, and
+    the weight / bias gradients through aten -- all equal to float64 autograd on the CPU."""
+    import torch.nn.functional as F
+    import amd_tuned_torch  # noqa: F401
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(2, 32, 6, 16, 16, generator=g)
+    w = torch.randn(48, 32, 3, 3, 3, generator=g) * 0.05
+    b = torch.randn(48, generator=g) * 0.1
+    xd = x.to(dtype).to(dev).requires_grad_(True)
+    wd = w.to(dtype).to(dev).requires_grad_(True)
+    bd = b.to(dtype).to(dev).requires_grad_(True)
+    y = F.conv3d(xd, wd, bd, 1, 1)
+    dy = torch.randn(y.shape, generator=g)
+    gx, gw, gb = torch.autograd.grad(y, (xd, wd, bd), dy.to(dtype).to(dev))
+    x64, w64, b64 = (t.to(dtype).double().requires_grad_(True) for t in (x, w, b))
+    y64 = torch.nn.functional.conv3d(x64, w64, b64, 1, 1)
+    rx, rw, rb = torch.autograd.grad(y64, (x64, w64, b64), dy.to(dtype).double())
+    bar = 1e-5 if dtype == torch.float32 else 1e-2
+    for got, ref in ((gx, rx), (gw, rw), (gb, rb)):
+        err = (got.double().cpu() - ref).abs().max().item() / ref.abs().max().item()
+        assert err <= bar, err
