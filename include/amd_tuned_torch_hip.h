@@ -122,6 +122,68 @@ int atk_dwconv1d_bwd_weight(const void* x, const void* dy, float* dw, float* db,
                             int dtype, void* workspace, size_t ws_bytes, atk_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Channels-last depthwise conv1d forward (replaces `conv1d_forward(u, weight, bias,
+ * padding, is_bhl=false)`, amd_tuned_torch/_vendor/flashfftconv_depthwise_conv1d/
+ * conv1d.h:56-83 -> conv1d_blh.hip:54-220, and the channel-last branch of
+ * `causal_conv1d_fwd(x, weight, bias, seq_idx, initial_states, final_states, silu)`,
+ * src/causal-conv1d-amd/csrc/causal_conv1d.cpp:131-238 -> causal_conv1d_fwd.cu:194-365):
+ *   y[b,t,c] = act(bias[c] + sum_{k<K} m * w[c,k] * x[b, t-pad_left+k, c]),  t < L_out.
+ * Element (b, t, c) of x sits at b*x_stride_b + t*x_stride_l + c (channel stride 1),
+ * of y at b*y_stride_b + t*y_stride_l + c; w[c,k] at c*w_stride_c + k*w_stride_k in
+ * w_dtype (fp32 or `dtype`), bias [D] in w_dtype or NULL.  x = 0 outside [0, L), except
+ * that positions -(K-1)..-1 read initial_states[b, p+K-1, c] (at b*is_stride_b +
+ * j*is_stride_l + c) when given.  seq_idx: int32 [B, L] or NULL; seq_mode 1 drops taps
+ * whose seq differs from the output position's (causal form, pad_left = K-1), 2 from
+ * the first tap's (pad_left = 0: the input gradient on reversed weights); positions < 0
+ * have seq -1.  final_states[b, j, c] (at b*fs_stride_b + j*fs_stride_l + c) receives
+ * x[b, L-(K-1)+j, c].  States need the causal form (pad_left = K-1, L_out = L).
+ * K <= 8 (seq_idx: K <= 4); D, every stride and pointer in 16-byte units.
+ * ------------------------------------------------------------------------- */
+int atk_dwconv1d_cl_fwd(const void* x, const void* w, const void* bias, void* y, const int* seq_idx,
+                        const void* initial_states, void* final_states, int64_t B, int64_t D, int64_t L,
+                        int K, int pad_left, int64_t L_out, int64_t x_stride_b, int64_t x_stride_l,
+                        int64_t y_stride_b, int64_t y_stride_l, int64_t w_stride_c, int64_t w_stride_k,
+                        int64_t is_stride_b, int64_t is_stride_l, int64_t fs_stride_b, int64_t fs_stride_l,
+                        int dtype, int w_dtype, int fuse_silu, int seq_mode, atk_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Channels-last depthwise conv1d weight / bias gradients (replaces the dweight /
+ * dbias half of `conv1d_backward(..., is_bhl=false)`, amd_tuned_torch/_vendor/
+ * flashfftconv_depthwise_conv1d/conv1d_bwd_hip_blh.hip:21-127):
+ *   dw[c,k] = sum_{b,t} dy[b,t,c] * m * x[b, t-pad_left+k, c],  db[c] = sum_{b,t} dy[b,t,c],
+ * x extended and masked as in atk_dwconv1d_cl_fwd (seq_mode 0 or 1).  dw [D, K] fp32,
+ * db [D] fp32 or NULL.  K <= 5.  The workspace holds per-span partials, summed in a
+ * fixed order (deterministic); it needs no initialisation.
+ * ------------------------------------------------------------------------- */
+size_t atk_dwconv1d_cl_bwd_weight_workspace_bytes(int64_t B, int64_t D, int64_t L_out, int K, int dtype);
+int atk_dwconv1d_cl_bwd_weight(const void* x, const void* dy, const int* seq_idx, const void* initial_states,
+                               float* dw, float* db, int64_t B, int64_t D, int64_t L, int K, int pad_left,
+                               int64_t L_out, int64_t x_stride_b, int64_t x_stride_l, int64_t dy_stride_b,
+                               int64_t dy_stride_l, int64_t is_stride_b, int64_t is_stride_l, int dtype,
+                               int seq_mode, void* workspace, size_t ws_bytes, atk_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Causal channel-last conv1d backward, fused (replaces the channel-last branch of
+ * `causal_conv1d_bwd(x, weight, bias, dout, seq_idx, initial_states, dfinal_states, dx,
+ * return_dinitial_states, silu)`, src/causal-conv1d-amd/csrc/causal_conv1d.cpp:240-380):
+ * with z the recomputed fp32 pre-activation and g = dout * silu'(z) (dout without SiLU),
+ *   dx[b,q,c] = sum_k w[c,k] * g[b, q+K-1-k, c] * [seq(q) == seq(q+K-1-k)],
+ *   dw[c,k]   = sum_{b,t} g[b,t,c] * x[b, t-K+1+k, c] * [seq(t-K+1+k) == seq(t)],
+ *   db[c]     = sum_{b,t} g[b,t,c].
+ * Layouts and operands as in atk_dwconv1d_cl_fwd (x, dout, dx: channel stride 1).
+ * initial_states feed x at negative positions; their gradient and dfinal_states are
+ * the caller's (a few K-1-wide slices).  K in [2, 4].  dw [D, K], db [D] fp32.  The
+ * workspace holds per-span partials (deterministic fixed-order sum).
+ * ------------------------------------------------------------------------- */
+size_t atk_causal_conv1d_cl_bwd_workspace_bytes(int64_t B, int64_t D, int64_t L, int K, int dtype);
+int atk_causal_conv1d_cl_bwd(const void* x, const void* dout, const void* w, const void* bias, const int* seq_idx,
+                             const void* initial_states, void* dx, float* dw, float* db, int64_t B, int64_t D,
+                             int64_t L, int K, int64_t x_stride_b, int64_t x_stride_l, int64_t dout_stride_b,
+                             int64_t dout_stride_l, int64_t dx_stride_b, int64_t dx_stride_l, int64_t w_stride_c,
+                             int64_t w_stride_k, int64_t is_stride_b, int64_t is_stride_l, int dtype,
+                             int w_dtype, int silu, void* workspace, size_t ws_bytes, atk_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * GroupNorm forward, NC[spatial] layout (replaces `group_norm(input, num_groups,
  * weight?, bias?, eps)`, src/main_rocm.cpp:556-599 -> src/cuda/group_norm.cu:41-136,
  * and the fused GroupNorm+SiLU of amd_tuned_torch/conv_fusion_ops.py:192-275):

@@ -226,3 +226,92 @@ void oracle_conv3d(const double* x, const double* w, const double* b, double* y,
     y[q] = acc;
   }
 }
+
+/* Causal depthwise conv with seq_idx and initial / final states: the reference's channel-last
+ * kernel (src/causal-conv1d-amd/csrc/causal_conv1d_fwd.cu:194-332) restated on plain arrays,
+ * x [B, D, L], w [D, K], b [D] or NULL, seq [B, L] int32 or NULL, init [B, D, K-1] or NULL,
+ * y [B, D, L], fin [B, D, K-1] or NULL.  With H = K-1:
+ *   xv(p)  = x[p] for p >= 0, init[p + H] for p < 0 (0 without init);
+ *   sq(p)  = seq[p] for p >= 0, -1 for p < 0 (fwd.cu:293-299);
+ *   y[t]   = act(b + sum_j [sq(t-H+j) == sq(t)] * w[j] * xv(t-H+j))      (fwd.cu:302-315);
+ *   fin[j] = xv(L - H + j)                                                (fwd.cu:259-266). */
+static double xv_at(const double* xr, const double* ir, int64_t p, int64_t H) {
+  if (p >= 0) return xr[p];
+  return ir ? ir[p + H] : 0.0;
+}
+
+void oracle_causal_conv1d_states(const double* x, const double* w, const double* b, const int* seq,
+                                 const double* init, double* y, double* fin, int64_t B, int64_t D,
+                                 int64_t L, int64_t K, int silu) {
+  const int64_t H = K - 1;
+  for (int64_t n = 0; n < B; ++n)
+    for (int64_t c = 0; c < D; ++c) {
+      const double* xr = x + (n * D + c) * L;
+      const double* ir = init ? init + (n * D + c) * H : 0;
+      const int* sr = seq ? seq + n * L : 0;
+      for (int64_t t = 0; t < L; ++t) {
+        double acc = b ? b[c] : 0.0;
+        for (int64_t j = 0; j < K; ++j) {
+          const int64_t p = t - H + j;
+          if (sr && (p >= 0 ? sr[p] : -1) != sr[t]) continue;
+          acc += w[c * K + j] * xv_at(xr, ir, p, H);
+        }
+        y[(n * D + c) * L + t] = silu ? acc / (1.0 + exp(-acc)) : acc;
+      }
+      if (fin)
+        for (int64_t j = 0; j < H; ++j) fin[(n * D + c) * H + j] = xv_at(xr, ir, L - H + j, H);
+    }
+}
+
+/* Gradients of oracle_causal_conv1d_states for dout [B, D, L] and dfinal [B, D, K-1] (or NULL),
+ * the reference's causal_conv1d_bwd (causal_conv1d.cpp:240-380): with z the pre-activation and
+ * g[t] = dout[t] * silu'(z[t]) (dout[t] without the activation), every term
+ * w[j] * xv(p), p = t-H+j, kept by the mask adds g[t] * w[j] to dxv(p), g[t] * xv(p) to dw[j]
+ * and g[t] to db; dfinal[j] adds to dxv(L - H + j).  dxv(p) is dx[p] for p >= 0 and
+ * dinit[p + H] for p < 0.  Any of dx / dw / db / dinit may be NULL. */
+void oracle_causal_conv1d_states_bwd(const double* x, const double* w, const double* b, const int* seq,
+                                     const double* init, const double* dout, const double* dfinal,
+                                     double* dx, double* dw, double* db, double* dinit, int64_t B,
+                                     int64_t D, int64_t L, int64_t K, int silu) {
+  const int64_t H = K - 1;
+  if (dw) for (int64_t i = 0; i < D * K; ++i) dw[i] = 0.0;
+  if (db) for (int64_t c = 0; c < D; ++c) db[c] = 0.0;
+  if (dx) for (int64_t i = 0; i < B * D * L; ++i) dx[i] = 0.0;
+  if (dinit) for (int64_t i = 0; i < B * D * H; ++i) dinit[i] = 0.0;
+  for (int64_t n = 0; n < B; ++n)
+    for (int64_t c = 0; c < D; ++c) {
+      const double* xr = x + (n * D + c) * L;
+      const double* ir = init ? init + (n * D + c) * H : 0;
+      const int* sr = seq ? seq + n * L : 0;
+      double* dxr = dx ? dx + (n * D + c) * L : 0;
+      double* dir = dinit ? dinit + (n * D + c) * H : 0;
+      for (int64_t t = 0; t < L; ++t) {
+        double g = dout[(n * D + c) * L + t];
+        if (silu) {
+          double z = b ? b[c] : 0.0;
+          for (int64_t j = 0; j < K; ++j) {
+            const int64_t p = t - H + j;
+            if (sr && (p >= 0 ? sr[p] : -1) != sr[t]) continue;
+            z += w[c * K + j] * xv_at(xr, ir, p, H);
+          }
+          const double s = 1.0 / (1.0 + exp(-z));
+          g *= s * (1.0 + z * (1.0 - s));
+        }
+        if (db) db[c] += g;
+        for (int64_t j = 0; j < K; ++j) {
+          const int64_t p = t - H + j;
+          if (sr && (p >= 0 ? sr[p] : -1) != sr[t]) continue;
+          if (dw) dw[c * K + j] += g * xv_at(xr, ir, p, H);
+          if (p >= 0) { if (dxr) dxr[p] += g * w[c * K + j]; }
+          else if (dir) dir[p + H] += g * w[c * K + j];
+        }
+      }
+      if (dfinal)
+        for (int64_t j = 0; j < H; ++j) {
+          const int64_t p = L - H + j;
+          const double v = dfinal[(n * D + c) * H + j];
+          if (p >= 0) { if (dxr) dxr[p] += v; }
+          else if (dir) dir[p + H] += v;
+        }
+    }
+}

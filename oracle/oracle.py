@@ -45,6 +45,8 @@ def lib():
         L.oracle_dwconv1d.argtypes = [d, d, d, d, i64, i64, i64, i64, i64, i64, i32]
         L.oracle_dwconv1d_bwd.argtypes = [d, d, d, d, d, d, i64, i64, i64, i64, i64, i64]
         L.oracle_causal_conv1d_update.argtypes = [d, d, d, d, d, i64, i64, i64, i32]
+        L.oracle_causal_conv1d_states.argtypes = [d, d, d, d, d, d, d, i64, i64, i64, i64, i32]
+        L.oracle_causal_conv1d_states_bwd.argtypes = [d] * 11 + [i64, i64, i64, i64, i32]
         L.oracle_group_norm.argtypes = [d, d, d, d, i64, i64, i64, i64, ctypes.c_double, i32, d, d]
         L.oracle_group_norm_bwd.argtypes = [d, d, d, d, d, d, i64, i64, i64, i64, ctypes.c_double]
         L.oracle_conv3d.argtypes = [d, d, d, d] + [i64] * 18 + [d, i64]
@@ -104,6 +106,51 @@ def causal_conv1d_update(x, state, w, b=None, silu: bool = False):
     y = np.empty((B, D), dtype=np.float64)
     lib().oracle_causal_conv1d_update(_p(x), _p(st), _p(w.reshape(D, W)), _p(b), _p(y), B, D, W, int(bool(silu)))
     return y, st
+
+
+def _seq32(seq_idx):
+    if seq_idx is None:
+        return None
+    try:
+        import torch
+        if isinstance(seq_idx, torch.Tensor):
+            seq_idx = seq_idx.detach().cpu().numpy()
+    except ImportError:
+        pass
+    return np.ascontiguousarray(np.asarray(seq_idx, dtype=np.int32))
+
+
+def causal_conv1d_states(x, w, b=None, seq_idx=None, initial_states=None, silu: bool = False):
+    """(y [B, D, L], final_states [B, D, K-1]) of the causal conv with seq_idx [B, L] and
+    initial_states [B, D, K-1] (either may be None); layouts are logical, any strides."""
+    x, w, b, init = f64(x), f64(w), f64(b), f64(initial_states)
+    seq = _seq32(seq_idx)
+    B, D, L = x.shape
+    K = w.reshape(D, -1).shape[1]
+    y = np.empty((B, D, L), dtype=np.float64)
+    fin = np.empty((B, D, K - 1), dtype=np.float64)
+    lib().oracle_causal_conv1d_states(_p(x), _p(w.reshape(D, K)), _p(b), _p(seq), _p(init), _p(y), _p(fin),
+                                      B, D, L, K, int(bool(silu)))
+    return y, fin
+
+
+def causal_conv1d_states_bwd(x, w, b, dout, seq_idx=None, initial_states=None, dfinal=None,
+                             silu: bool = False):
+    """(dx [B, D, L], dw [D, K], db [D], dinit [B, D, K-1] or None) of causal_conv1d_states
+    for the upstream gradients dout and dfinal (None = zero)."""
+    x, w, b, dout = f64(x), f64(w), f64(b), f64(dout)
+    init, dfin = f64(initial_states), f64(dfinal)
+    seq = _seq32(seq_idx)
+    B, D, L = x.shape
+    K = w.reshape(D, -1).shape[1]
+    dx = np.empty_like(x)
+    dw = np.empty((D, K), dtype=np.float64)
+    db = np.empty((D,), dtype=np.float64)
+    dinit = np.empty((B, D, K - 1), dtype=np.float64) if init is not None else None
+    lib().oracle_causal_conv1d_states_bwd(_p(x), _p(w.reshape(D, K)), _p(b), _p(seq), _p(init), _p(dout),
+                                          _p(dfin), _p(dx), _p(dw), _p(db), _p(dinit), B, D, L, K,
+                                          int(bool(silu)))
+    return dx, dw, db, dinit
 
 
 def conv1d_out_len(length: int, padding: int, width: int) -> int:

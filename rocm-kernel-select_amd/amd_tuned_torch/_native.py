@@ -35,7 +35,8 @@ _DTYPE_CODE = {torch.float32: ATK_F32, torch.float16: ATK_F16, torch.bfloat16: A
 EXPORTED_SYMBOLS = (
     "atk_abi_version", "atk_last_error", "atk_num_variants", "atk_variant_name",
     "atk_dwconv1d_fwd", "atk_causal_conv1d_update", "atk_dwconv1d_bwd_weight_workspace_bytes",
-    "atk_dwconv1d_bwd_weight",
+    "atk_dwconv1d_bwd_weight", "atk_dwconv1d_cl_fwd", "atk_dwconv1d_cl_bwd_weight_workspace_bytes",
+    "atk_dwconv1d_cl_bwd_weight", "atk_causal_conv1d_cl_bwd_workspace_bytes", "atk_causal_conv1d_cl_bwd",
     "atk_group_norm_workspace_bytes",
     "atk_group_norm_workspace_zero_bytes", "atk_group_norm_fwd", "atk_group_norm_cl_workspace_bytes",
     "atk_group_norm_cl_fwd", "atk_group_norm_bwd_workspace_bytes",
@@ -69,6 +70,18 @@ def _declare(lib) -> None:
     lib.atk_dwconv1d_bwd_weight_workspace_bytes.restype = sz
     lib.atk_dwconv1d_bwd_weight.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, i32, i64, i32, vp, sz, vp]
     lib.atk_dwconv1d_bwd_weight.restype = i32
+    lib.atk_dwconv1d_cl_fwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i32, i32, i64] + [i64] * 10 + \
+        [i32, i32, i32, i32, vp]
+    lib.atk_dwconv1d_cl_fwd.restype = i32
+    lib.atk_dwconv1d_cl_bwd_weight_workspace_bytes.argtypes = [i64, i64, i64, i32, i32]
+    lib.atk_dwconv1d_cl_bwd_weight_workspace_bytes.restype = sz
+    lib.atk_dwconv1d_cl_bwd_weight.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i32, i32, i64] + [i64] * 6 + \
+        [i32, i32, vp, sz, vp]
+    lib.atk_dwconv1d_cl_bwd_weight.restype = i32
+    lib.atk_causal_conv1d_cl_bwd_workspace_bytes.argtypes = [i64, i64, i64, i32, i32]
+    lib.atk_causal_conv1d_cl_bwd_workspace_bytes.restype = sz
+    lib.atk_causal_conv1d_cl_bwd.argtypes = [vp] * 9 + [i64, i64, i64, i32] + [i64] * 10 + [i32, i32, i32, vp, sz, vp]
+    lib.atk_causal_conv1d_cl_bwd.restype = i32
     lib.atk_group_norm_cl_workspace_bytes.argtypes = [i64, i64, i64, i32]
     lib.atk_group_norm_cl_workspace_bytes.restype = sz
     lib.atk_group_norm_cl_fwd.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, c.c_float, i32, i32, i32, vp, sz, vp]
@@ -300,6 +313,155 @@ def dwconv1d_bwd_weight(x: torch.Tensor, dy: torch.Tensor, K: int, pad_left: int
     return dw, db
 
 
+def _bld_view(t: torch.Tensor, what: str) -> None:
+    if t.dim() != 3 or (t.stride(2) != 1 and t.shape[2] > 1):
+        raise RuntimeError(f"{what} must be a (B, L, D) view with unit channel stride")
+
+
+def _bld_strides(t: Optional[torch.Tensor]):
+    """(batch, position) element strides of a (B, L, D) view; a size-1 dimension's stride is
+    never stepped, so it is reported as a dense one (the kernels check stride layouts)."""
+    if t is None:
+        return 0, 0
+    B, L, D = t.shape
+    sl = t.stride(1) if L > 1 else D
+    sb = t.stride(0) if B > 1 else L * sl
+    return sb, sl
+
+
+def dwconv1d_cl(x: torch.Tensor, weight_dk: torch.Tensor, bias: Optional[torch.Tensor], pad_left: int,
+                l_out: int, *, silu: bool = False, seq_idx: Optional[torch.Tensor] = None, seq_mode: int = 0,
+                initial_states: Optional[torch.Tensor] = None, final_states: Optional[torch.Tensor] = None,
+                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Channels-last depthwise conv1d:
+    y[b,t,c] = act(bias[c] + sum_j m * weight_dk[c,j] * x[b, t-pad_left+j, c]), t < l_out.
+    x: (B, L, D) view with unit channel stride (any batch / position strides); weight_dk: (D, K)
+    view of any strides, float32 or x's dtype; bias: (D,) in weight's dtype.  seq_idx: int32
+    (B, L); seq_mode 1 masks taps whose seq differs from the output position's (pad K-1), 2 from
+    the first tap's (pad 0).  initial_states / final_states: (B, K-1, D) views with unit channel
+    stride, causal form only (pad K-1, l_out = L).  Returns a (B, l_out, D) tensor (or `out`)."""
+    _require_cuda(x, weight_dk, bias, seq_idx, initial_states, final_states)
+    _bld_view(x, "dwconv1d_cl: x")
+    if weight_dk.dim() != 2 or weight_dk.shape[0] != x.shape[2]:
+        raise RuntimeError("dwconv1d_cl: weight must be (D, K)")
+    if x.dtype not in _DTYPE_CODE or weight_dk.dtype not in (torch.float32, x.dtype):
+        raise RuntimeError("dwconv1d_cl: x float16/bfloat16/float32, weight float32 or x's dtype")
+    if bias is not None and (bias.dtype != weight_dk.dtype or bias.shape != (x.shape[2],)):
+        raise RuntimeError("dwconv1d_cl: bias must be (D,) in the weight's dtype")
+    B, L, D = x.shape
+    K = weight_dk.shape[1]
+    if out is None:
+        out = torch.empty((B, l_out, D), dtype=x.dtype, device=x.device)
+    _bld_view(out, "dwconv1d_cl: out")
+    if out.dtype != x.dtype or tuple(out.shape) != (B, l_out, D):
+        raise RuntimeError("dwconv1d_cl: out must be (B, l_out, D) in x's dtype")
+    for t, nm in ((initial_states, "initial_states"), (final_states, "final_states")):
+        if t is not None:
+            _bld_view(t, f"dwconv1d_cl: {nm}")
+            if tuple(t.shape) != (B, K - 1, D) or t.dtype != x.dtype:
+                raise RuntimeError(f"dwconv1d_cl: {nm} must be (B, K-1, D) in x's dtype")
+    if seq_idx is not None:
+        if seq_idx.dtype != torch.int32 or tuple(seq_idx.shape) != (B, L):
+            raise RuntimeError("dwconv1d_cl: seq_idx must be int32 (B, L)")
+        seq_idx = seq_idx.contiguous()
+    bias = bias.contiguous() if bias is not None else None
+    if B == 0 or l_out == 0 or D == 0:
+        return out
+    ist, fst = _bld_strides(initial_states), _bld_strides(final_states)
+    rc = lib().atk_dwconv1d_cl_fwd(
+        _ptr(x), _ptr(weight_dk), _ptr(bias), _ptr(out), _ptr(seq_idx), _ptr(initial_states),
+        _ptr(final_states), B, D, L, K, int(pad_left), int(l_out), *_bld_strides(x), *_bld_strides(out),
+        weight_dk.stride(0), weight_dk.stride(1), ist[0], ist[1], fst[0], fst[1],
+        _DTYPE_CODE[x.dtype], _DTYPE_CODE[weight_dk.dtype], int(bool(silu)), int(seq_mode), _stream(x))
+    _check(rc, "dwconv1d_cl")
+    return out
+
+
+def dwconv1d_cl_bwd_weight(x: torch.Tensor, dy: torch.Tensor, K: int, pad_left: int, *,
+                           seq_idx: Optional[torch.Tensor] = None,
+                           initial_states: Optional[torch.Tensor] = None, with_bias: bool = True):
+    """fp32 weight / bias gradients of dwconv1d_cl: dw (D, K), db (D,) (None without bias).
+    x (B, L, D) and dy (B, L_out, D) views with unit channel stride, one dtype; seq_idx int32
+    (B, L) (causal form); initial_states (B, K-1, D).  Raises Unsupported for K > 5."""
+    _require_cuda(x, dy, seq_idx, initial_states)
+    _bld_view(x, "dwconv1d_cl_bwd_weight: x")
+    _bld_view(dy, "dwconv1d_cl_bwd_weight: dy")
+    if x.dtype not in _DTYPE_CODE or dy.dtype != x.dtype or dy.shape[0] != x.shape[0] or dy.shape[2] != x.shape[2]:
+        raise RuntimeError("dwconv1d_cl_bwd_weight: x (B, L, D) and dy (B, L_out, D) of one dtype")
+    B, L, D = x.shape
+    l_out = dy.shape[1]
+    dw = torch.empty((D, K), dtype=torch.float32, device=x.device)
+    db = torch.empty((D,), dtype=torch.float32, device=x.device) if with_bias else None
+    if B == 0 or l_out == 0:
+        dw.zero_()
+        if db is not None:
+            db.zero_()
+        return dw, db
+    if seq_idx is not None:
+        seq_idx = seq_idx.contiguous()
+    if initial_states is not None:
+        _bld_view(initial_states, "dwconv1d_cl_bwd_weight: initial_states")
+    ist = _bld_strides(initial_states)
+    L_ = lib()
+    nbytes = L_.atk_dwconv1d_cl_bwd_weight_workspace_bytes(B, D, l_out, K, _DTYPE_CODE[x.dtype])
+    ws = workspace(x.device, "dwconv1d_cl_bwd", nbytes)
+    rc = L_.atk_dwconv1d_cl_bwd_weight(
+        _ptr(x), _ptr(dy), _ptr(seq_idx), _ptr(initial_states), _ptr(dw), _ptr(db), B, D, L, K, int(pad_left),
+        l_out, *_bld_strides(x), *_bld_strides(dy), ist[0], ist[1], _DTYPE_CODE[x.dtype],
+        1 if seq_idx is not None else 0, _ptr(ws), ws.numel(), _stream(x))
+    _check(rc, "dwconv1d_cl_bwd_weight")
+    return dw, db
+
+
+def causal_conv1d_cl_bwd(x: torch.Tensor, dout: torch.Tensor, weight_dk: torch.Tensor,
+                         bias: Optional[torch.Tensor], *, silu: bool = False,
+                         seq_idx: Optional[torch.Tensor] = None,
+                         initial_states: Optional[torch.Tensor] = None, dx: Optional[torch.Tensor] = None):
+    """Fused backward of the causal channels-last conv (pad K-1, output length L), width 2..4:
+    returns (dx (B, L, D) in x's dtype -- written into `dx` when given --, dw (D, K) fp32,
+    db (D,) fp32).  x, dout, dx, initial_states: (B, *, D) views with unit channel stride;
+    weight_dk (D, K) float32 or x's dtype; bias in the weight's dtype (used to recompute the
+    pre-activation when `silu`)."""
+    _require_cuda(x, dout, weight_dk, bias, seq_idx, initial_states)
+    _bld_view(x, "causal_conv1d_cl_bwd: x")
+    _bld_view(dout, "causal_conv1d_cl_bwd: dout")
+    if dout.shape != x.shape or dout.dtype != x.dtype or x.dtype not in _DTYPE_CODE:
+        raise RuntimeError("causal_conv1d_cl_bwd: dout must match x")
+    if weight_dk.dim() != 2 or weight_dk.shape[0] != x.shape[2] or weight_dk.dtype not in (torch.float32, x.dtype):
+        raise RuntimeError("causal_conv1d_cl_bwd: weight (D, K), float32 or x's dtype")
+    if bias is not None and bias.dtype != weight_dk.dtype:
+        raise RuntimeError("causal_conv1d_cl_bwd: bias must be in the weight's dtype")
+    B, L, D = x.shape
+    K = weight_dk.shape[1]
+    if dx is None:
+        dx = torch.empty_like(x, memory_format=torch.contiguous_format)
+    _bld_view(dx, "causal_conv1d_cl_bwd: dx")
+    dw = torch.empty((D, K), dtype=torch.float32, device=x.device)
+    db = torch.empty((D,), dtype=torch.float32, device=x.device)
+    if B == 0 or L == 0:
+        dw.zero_()
+        db.zero_()
+        return dx, dw, db
+    if seq_idx is not None:
+        if seq_idx.dtype != torch.int32 or tuple(seq_idx.shape) != (B, L):
+            raise RuntimeError("causal_conv1d_cl_bwd: seq_idx must be int32 (B, L)")
+        seq_idx = seq_idx.contiguous()
+    if initial_states is not None:
+        _bld_view(initial_states, "causal_conv1d_cl_bwd: initial_states")
+    ist = _bld_strides(initial_states)
+    bias = bias.contiguous() if bias is not None else None
+    L_ = lib()
+    nbytes = L_.atk_causal_conv1d_cl_bwd_workspace_bytes(B, D, L, K, _DTYPE_CODE[x.dtype])
+    ws = workspace(x.device, "causal_conv1d_cl_bwd", nbytes)
+    rc = L_.atk_causal_conv1d_cl_bwd(
+        _ptr(x), _ptr(dout), _ptr(weight_dk), _ptr(bias), _ptr(seq_idx), _ptr(initial_states), _ptr(dx),
+        _ptr(dw), _ptr(db), B, D, L, K, *_bld_strides(x), *_bld_strides(dout), *_bld_strides(dx),
+        weight_dk.stride(0), weight_dk.stride(1), ist[0], ist[1],
+        _DTYPE_CODE[x.dtype], _DTYPE_CODE[weight_dk.dtype], int(bool(silu)), _ptr(ws), ws.numel(), _stream(x))
+    _check(rc, "causal_conv1d_cl_bwd")
+    return dx, dw, db
+
+
 def dwconv1d_backward(dy: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, pad_left: int,
                       needs=(True, True, False)):
     """(dx, dw, db) of y = dwconv1d(x, weight, bias, pad_left, L_out) for dy [N,C,L_out]:
@@ -324,10 +486,22 @@ def conv1d_forward(u: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, pa
                    is_bhl: bool = True, *, variant: int = -1) -> torch.Tensor:
     """Reference signature `conv1d_forward(u, weight, bias, padding, is_bhl)`
     (_vendor/flashfftconv_depthwise_conv1d/host.cpp:10): symmetric padding, output length
-    L + 2*padding - K + 1 (depthwise_conv1d_ops.py:112-118).  Only the BHL layout (B, C, L)
-    is built; is_bhl=False raises."""
+    L + 2*padding - K + 1 (depthwise_conv1d_ops.py:112-118).  is_bhl: u (B, C, L), weight
+    [C, K]; otherwise u (B, L, C), weight [K, C] (conv1d.h:56-83), served by the
+    channels-last kernel (output (B, L_out, C) contiguous)."""
     if not is_bhl:
-        raise Unsupported("conv1d_forward: channels-last (BLH) layout is not built")
+        if u.dim() != 3 or weight.dim() != 2 or weight.shape[1] != u.shape[2]:
+            raise RuntimeError("conv1d_forward: BLH expects u (B, L, C) and weight [K, C]")
+        if bias is not None and bias.dtype != weight.dtype:
+            raise RuntimeError("conv1d_forward: weight and bias must have the same dtype")
+        K = weight.shape[0]
+        l_out = u.shape[1] + 2 * int(padding) - K + 1
+        if l_out <= 0:
+            raise RuntimeError("conv1d_forward: output length must be positive")
+        if weight.dtype not in (torch.float32, u.dtype):
+            weight = weight.float()
+            bias = bias.float() if bias is not None else None
+        return dwconv1d_cl(u, weight.t(), bias, int(padding), l_out)
     K = weight.shape[-1]
     l_out = u.shape[-1] + 2 * int(padding) - K + 1
     if l_out <= 0:

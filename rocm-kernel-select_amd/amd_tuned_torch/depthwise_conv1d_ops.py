@@ -4,8 +4,10 @@ Interface of the reference's depthwise_conv1d_ops (amd_tuned_torch/depthwise_con
 95-247): `available`, `maybe_contiguous`, `_out_len`, the torch.library ops
 `amd_tuned_torch::depthwise_conv1d_forward/backward` with fake (meta) implementations,
 `conv1d_forward`/`conv1d_backward`, `DepthwiseConv1dFn` and `depthwise_conv1d_candidate`.
-The forward runs this package's gfx950 kernel (any width K <= 64, fp32 accumulation); the
-reference's kernel only accepted odd K (conv1d.h:76).  The backward is native too
+The forward runs this package's gfx950 kernels (fp32 accumulation): the (B, C, L) layout
+for any width K <= 64, the (B, L, C) layout (weight [K, C]) through the channels-last kernel
+for K <= 8, stock F.conv1d on the transposed view beyond that; the reference's kernel only
+accepted odd K (conv1d.h:76).  The backward is native too
 (`_native.dwconv1d_backward`: du through the forward kernel with reversed weights, dweight /
 dbias through one streaming reduction kernel) where it applies -- K <= 5 for the weight
 gradient, padding <= K-1 for du -- and stock aten.convolution_backward for the rest.
@@ -36,9 +38,36 @@ def _out_len(length: int, padding: int, width: int) -> int:
     return length + 2 * padding - width + 1
 
 
+def _stock_forward_blh(input_, weight, bias, padding: int):
+    """BLH forward through stock F.conv1d on the transposed view (shapes the kernel declines)."""
+    K, C = weight.shape
+    w = weight.t().unsqueeze(1)
+    if w.dtype != input_.dtype:
+        w = w.to(input_.dtype)
+    b = bias.to(input_.dtype) if bias is not None else None
+    y = torch.nn.functional.conv1d(input_.transpose(1, 2), w, b, padding=padding, groups=C)
+    return y.transpose(1, 2).contiguous()
+
+
+def _forward(input_, weight, bias, padding: int, is_bhl: bool):
+    if is_bhl:
+        return _native.conv1d_forward(input_, weight, bias, padding, True)
+    try:
+        return _native.conv1d_forward(input_, weight, bias, padding, False)
+    except _native.Unsupported:
+        return _stock_forward_blh(input_, weight, bias, padding)
+
+
 def _stock_backward(dout, input_, weight, bias, padding: int, is_bhl: bool, needs=(True, True, True)):
     if not is_bhl:
-        raise RuntimeError("depthwise_conv1d_backward: only the (B, C, L) layout is built")
+        # (B, L, C) tensors through the (B, C, L) op on transposed views; weight [K, C]
+        K, C = weight.shape
+        du, dw, db = torch.ops.aten.convolution_backward(
+            dout.transpose(1, 2), input_.transpose(1, 2), weight.t().unsqueeze(1).to(input_.dtype), [C], [1],
+            [padding], [1], False, [0], C, list(needs))
+        return (None if du is None else du.transpose(1, 2).contiguous(),
+                None if dw is None else dw.reshape(C, K).t().contiguous().to(weight.dtype),
+                None if db is None else db.to(dout.dtype))
     C, K = weight.shape
     du, dw, db = torch.ops.aten.convolution_backward(
         dout.contiguous(), input_, weight.unsqueeze(1), [C], [1], [padding], [1], False, [0], C,
@@ -51,10 +80,23 @@ def _backward(dout, input_, weight, bias, padding: int, is_bhl: bool):
     """(du, dweight, dbias) of conv1d_forward (conv1d_bwd_hip_bhl.hip:78-116 semantics:
     dweight in weight's dtype, dbias in dout's dtype): each part native where the library
     serves it, the rest stock."""
-    if not is_bhl:
-        raise RuntimeError("depthwise_conv1d_backward: only the (B, C, L) layout is built")
     du = dw = db = None
-    if input_.is_cuda and _native.available():
+    if not is_bhl and input_.is_cuda and _native.available():
+        # (B, L, C) layout, weight [K, C]: du through the channels-last forward kernel on dout
+        # with the taps reversed; dweight / dbias through its channels-last reduction
+        K = weight.shape[0]
+        wf = weight if weight.dtype in (torch.float32, input_.dtype) else weight.float()
+        try:
+            if padding <= K - 1:
+                du = _native.dwconv1d_cl(dout, wf.t().flip(-1), None, K - 1 - padding, input_.shape[1])
+        except _native.Unsupported:
+            du = None
+        try:
+            dw32, db32 = _native.dwconv1d_cl_bwd_weight(input_, dout, K, padding)
+            dw, db = dw32.t().contiguous().to(weight.dtype), db32.to(dout.dtype)
+        except _native.Unsupported:
+            dw = db = None
+    elif input_.is_cuda and _native.available():
         dout = dout.contiguous()
         K = weight.shape[-1]
         try:
@@ -85,7 +127,7 @@ if hasattr(torch.library, "custom_op") and not _already_registered("depthwise_co
     @torch.library.custom_op("amd_tuned_torch::depthwise_conv1d_forward", mutates_args=())
     def _fwd_op(input_: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, padding: int,
                 is_bhl: bool) -> torch.Tensor:
-        return _native.conv1d_forward(input_, weight, bias, padding, is_bhl)
+        return _forward(input_, weight, bias, padding, is_bhl)
 
     @_fwd_op.register_fake
     def _fwd_fake(input_, weight, bias, padding, is_bhl):
@@ -116,7 +158,7 @@ elif _already_registered("depthwise_conv1d_forward"):
     _bwd_impl = torch.ops.amd_tuned_torch.depthwise_conv1d_backward
 else:
     def _fwd_impl(input_, weight, bias, padding, is_bhl):
-        return _native.conv1d_forward(input_, weight, bias, padding, is_bhl)
+        return _forward(input_, weight, bias, padding, is_bhl)
 
     def _bwd_impl(dout, input_, weight, bias, padding, is_bhl):
         return _backward(dout, input_, weight, bias, padding, is_bhl)
