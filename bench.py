@@ -203,6 +203,52 @@ def bench_decode_detail(dev):
             "max_rel_err_vs_torch_ref": float(f"{err:.3g}")}
 
 
+def bench_dw_cl_detail(dev, silu=False):
+    """Config 2 (B=16, D=2048, L=8192, k=4, bf16) in the channel-last layout (x.stride(1) == 1,
+    the reference's causal_conv1d channel-last kernel): forward through causal_conv1d_fn and
+    the fused backward (dx, dw, db), against stock F.conv1d / aten.convolution_backward on the
+    same channel-last tensor.  Algorithmic bytes: forward x read + y written; backward x and
+    dout read + dx written."""
+    import torch
+    import torch.nn.functional as F
+    import amd_tuned_torch
+    from amd_tuned_torch import _native as nat
+    from amd_tuned_torch.causal_conv1d import causal_conv1d_fn
+    g = _gen(1010)
+    B, D, L, K = 16, 2048, 8192, 4
+    x = torch.randn(B, L, D, generator=g).to(torch.bfloat16).to(dev).transpose(1, 2)
+    w = (torch.randn(D, K, generator=g) * 0.5).to(torch.bfloat16).to(dev)
+    b = (torch.randn(D, generator=g) * 0.3).to(torch.bfloat16).to(dev)
+    dy = torch.randn(B, L, D, generator=g).to(torch.bfloat16).to(dev).transpose(1, 2)
+    act = "silu" if silu else None
+    orig = amd_tuned_torch.miopen_fallback._original_conv1d
+
+    def stock(xx, ww, bb):
+        y = orig(xx, ww.unsqueeze(1), bb, 1, K - 1, 1, D)[..., :L]
+        return F.silu(y) if silu else y
+    y = causal_conv1d_fn(x, w, b, activation=act)
+    err = max_rel_err(y, stock(x.float(), w.float(), b.float()))
+    del y
+    ms = graph_time_ms(lambda: causal_conv1d_fn(x, w, b, activation=act), 10)
+    stock_ms = event_time_ms(lambda: stock(x, w, b), 3)
+    xv, gv = x.transpose(1, 2), dy.transpose(1, 2)
+    dx = torch.empty_like(xv)
+    bwd = lambda: nat.causal_conv1d_cl_bwd(xv, gv, w, b, silu=silu, dx=dx)
+    bwd()
+    bms = graph_time_ms(bwd, 10)
+    xp = F.pad(x, (K - 1, 0))
+    stock_bms = event_time_ms(lambda: torch.ops.aten.convolution_backward(
+        dy, xp, w.unsqueeze(1), [D], [1], [0], [1], False, [0], D, [True, True, True]), 2)
+    n = B * D * L * x.element_size()
+    fgbs = 2 * n / (ms * 1e-3) / 1e9
+    bgbs = 3 * n / (bms * 1e-3) / 1e9
+    return {"fwd_ms": round(ms, 4), "fwd_GB/s": round(fgbs, 1), "fwd_roofline_frac": round(fgbs / HBM_PEAK_GBS, 4),
+            "stock_fwd_ms": round(stock_ms, 3), "fwd_max_rel_err_vs_stock_fp32": float(f"{err:.3g}"),
+            "bwd_ms": round(bms, 4), "bwd_GB/s": round(bgbs, 1), "bwd_roofline_frac": round(bgbs / HBM_PEAK_GBS, 4),
+            "stock_convolution_backward_ms": round(stock_bms, 3),
+            "variant": "dwconv1d_cl_kernel / dwconv1d_cl_causal_bwd_kernel"}
+
+
 def bench_gn_cl_detail(shape, G, silu, dev):
     """Channels-last GroupNorm (+ SiLU), bf16: the native NHWC / NDHWC kernel against stock
     F.group_norm on the same channels-last tensor (the reference contests CK here)."""
@@ -571,6 +617,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-details", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--details", default="",
+                    help="comma-separated substrings: run only the details whose names contain one")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="run only the workload of the FETCH_SIZE/WRITE_SIZE counter passes")
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -659,6 +707,8 @@ def main():
             ("c2_sym_k3_fp16", lambda: bench_dw_detail(torch.float16, "sym", dev)),
             ("c2_causal_backward_bf16", lambda: bench_dw_backward_detail(dev)),
             ("c2_decode_step_bf16", lambda: bench_decode_detail(dev)),
+            ("c2_channel_last_bf16", lambda: bench_dw_cl_detail(dev)),
+            ("c2_channel_last_silu_bf16", lambda: bench_dw_cl_detail(dev, silu=True)),
         ]
         for dt_name, dtype in (("fp16", torch.float16), ("bf16", torch.bfloat16)):
             for silu in (False, True):
@@ -684,6 +734,9 @@ def main():
             ("c4_conv3d_scaled_dgrad_bf16", lambda: bench_conv_dgrad_detail((2, 128, 16, 64, 64), (128, 128, 3, 3, 3), 1, torch.bfloat16, dev)),
         ]
         plan.append(("calibration", lambda: calibration(dev)))
+        if args.details:
+            keep = [k for k in args.details.split(",") if k]
+            plan = [(n, f) for n, f in plan if any(k in n for k in keep)]
         for name, fn in plan:
             log(f"detail {name} ...")
             try:

@@ -33,7 +33,7 @@ namespace atk {
 namespace {
 
 constexpr int CL_NT = 256;      // threads per block
-constexpr int CL_RUN = 32;      // output positions per thread (forward)
+constexpr int CL_RUN = 16;      // output positions per thread (forward)
 constexpr int CL_KMAX = 8;      // widest kernel served
 constexpr int CLW_STEP = 16;    // rows per unrolled step of the weight-gradient loop
 constexpr int CLW_MAXRUN = 512; // longest per-thread run of the weight-gradient kernel
@@ -45,6 +45,7 @@ struct DwClArgs {
   const void* b;
   int wdt;                    // weight / bias dtype code
   int64_t wc, wk;             // weight strides (elements): channel, tap
+  int wmode, bvec;            // weight / bias load forms (cl_params)
   const int* seq;             // [B, L] int32 or null
   const void* init;           // initial states or null
   int64_t ib, il;             // their batch / position strides (channel stride 1)
@@ -64,6 +65,74 @@ __device__ __forceinline__ void unpack16(uint4 raw, float* f) {
   v.raw = raw;
 #pragma unroll
   for (int i = 0; i < Vec16<T>::N; ++i) f[i] = to_f32(v.e[i]);
+}
+
+// Weight / bias loads.  wmode 1: w is (D, K) contiguous, so a thread's VEC*K weights are one
+// contiguous, 16-byte aligned block; wmode 2: w is tap-major (channel stride 1, tap stride a
+// multiple of 16 bytes): one or two 16-byte loads per tap; wmode 0: element loads at any
+// strides.  bvec: the bias is 16-byte aligned (vector load).  Weights and bias are fp32 or T.
+template <typename T, int KT>
+__device__ __forceinline__ void cl_params(const void* w, const void* bp, int wdt, int64_t wc, int64_t wk, int wmode,
+                                          int bvec, uint32_t c0, float (&wv)[KT][16 / sizeof(T)],
+                                          float (&bv)[16 / sizeof(T)]) {
+  constexpr int VEC = 16 / sizeof(T);
+  const bool f32 = wdt == ATK_F32;
+  if (wmode == 1) {
+    float f[VEC * KT];
+    if (f32) {
+      const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(w) + (size_t)c0 * KT);
+#pragma unroll
+      for (int i = 0; i < VEC * KT / 4; ++i) {
+        const float4 u = q[i];
+        f[4 * i] = u.x; f[4 * i + 1] = u.y; f[4 * i + 2] = u.z; f[4 * i + 3] = u.w;
+      }
+    } else {
+      const uint4* q = reinterpret_cast<const uint4*>(static_cast<const T*>(w) + (size_t)c0 * KT);
+#pragma unroll
+      for (int i = 0; i < KT; ++i) unpack16<T>(q[i], f + i * VEC);
+    }
+#pragma unroll
+    for (int v = 0; v < VEC; ++v)
+#pragma unroll
+      for (int j = 0; j < KT; ++j) wv[j][v] = f[v * KT + j];
+  } else if (wmode == 2) {
+#pragma unroll
+    for (int j = 0; j < KT; ++j) {
+      if (f32) {
+        const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(w) + (size_t)j * wk + c0);
+#pragma unroll
+        for (int i = 0; i < VEC / 4; ++i) {
+          const float4 u = q[i];
+          wv[j][4 * i] = u.x; wv[j][4 * i + 1] = u.y; wv[j][4 * i + 2] = u.z; wv[j][4 * i + 3] = u.w;
+        }
+      } else {
+        unpack16<T>(*reinterpret_cast<const uint4*>(static_cast<const T*>(w) + (size_t)j * wk + c0), wv[j]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v)
+#pragma unroll
+      for (int j = 0; j < KT; ++j) wv[j][v] = load_param(w, wdt, (int64_t)(c0 + v) * wc + (int64_t)j * wk);
+  }
+  if (!bp) {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) bv[v] = 0.f;
+  } else if (bvec) {
+    if (f32) {
+      const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(bp) + c0);
+#pragma unroll
+      for (int i = 0; i < VEC / 4; ++i) {
+        const float4 u = q[i];
+        bv[4 * i] = u.x; bv[4 * i + 1] = u.y; bv[4 * i + 2] = u.z; bv[4 * i + 3] = u.w;
+      }
+    } else {
+      unpack16<T>(*reinterpret_cast<const uint4*>(static_cast<const T*>(bp) + c0), bv);
+    }
+  } else {
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) bv[v] = load_param(bp, wdt, c0 + v);
+  }
 }
 
 // SEQ: 0 = no seq_idx, 1 = compare with the last tap's row (causal forward, pad = K-1),
@@ -103,12 +172,7 @@ __global__ __launch_bounds__(CL_NT) void dwconv1d_cl_kernel(DwClArgs a) {
     }
   }
   float wv[KT][VEC], bv[VEC];
-#pragma unroll
-  for (int v = 0; v < VEC; ++v) {
-#pragma unroll
-    for (int j = 0; j < KT; ++j) wv[j][v] = load_param(a.w, a.wdt, (int64_t)(c0 + v) * a.wc + (int64_t)j * a.wk);
-    bv[v] = a.b ? load_param(a.b, a.wdt, c0 + v) : 0.f;
-  }
+  cl_params<T, KT>(a.w, a.b, a.wdt, a.wc, a.wk, a.wmode, a.bvec, c0, wv, bv);
   // rows before the sequence come from the initial states (causal form only: pad == K-1)
   if (a.init && p0 < 0) {
     const T* ip = static_cast<const T*>(a.init) + (int64_t)b * a.ib + c0;
@@ -323,6 +387,7 @@ struct DwClCbArgs {
   const void* b;
   int wdt;
   int64_t wc, wk;
+  int wmode, bvec;
   const int* seq;
   const void* init;
   int64_t ib, il;
@@ -374,12 +439,7 @@ __global__ __launch_bounds__(CL_NT) void dwconv1d_cl_causal_bwd_kernel(DwClCbArg
   };
 
   float wv[KT][VEC], bv[VEC];
-#pragma unroll
-  for (int v = 0; v < VEC; ++v) {
-#pragma unroll
-    for (int j = 0; j < KT; ++j) wv[j][v] = load_param(a.w, a.wdt, (int64_t)(c0 + v) * a.wc + (int64_t)j * a.wk);
-    bv[v] = (SILU && a.b) ? load_param(a.b, a.wdt, c0 + v) : 0.f;
-  }
+  cl_params<T, KT>(a.w, SILU ? a.b : nullptr, a.wdt, a.wc, a.wk, a.wmode, a.bvec, c0, wv, bv);
 
   float xc[XC][VEC];  // x rows [p - H, p + H)
   int sc[XC];
@@ -605,6 +665,19 @@ uint32_t clw_run(int64_t B, int64_t D, int64_t Lout, int vec) {
   return (uint32_t)run;
 }
 
+// Load forms of cl_params for a weight at (w_stride_c, w_stride_k) and a bias.
+void cl_param_modes(const void* w, const void* bias, int w_dtype, int K, int64_t wc, int64_t wk, int vec, int* wmode,
+                    int* bvec) {
+  const int64_t wes = (int64_t)dtype_size(w_dtype);
+  *wmode = 0;
+  if (aligned16(w)) {
+    if (wk == 1 && wc == K) *wmode = 1;  // c0 * K * wes is a multiple of 16 since c0 is of vec
+    else if (wc == 1 && (wk * wes) % 16 == 0 && (vec * wes) % 16 == 0) *wmode = 2;
+  }
+  if (*wmode == 1 && (vec * K * wes) % 16 != 0) *wmode = 0;
+  *bvec = bias && aligned16(bias) && (vec * wes) % 16 == 0;
+}
+
 // Checks shared by both entry points; returns the vector width or an error code (< 0).
 int cl_check(const void* x, int64_t B, int64_t D, int64_t L, int K, int dtype, int64_t xb, int64_t xl) {
   if (!x || !dtype_ok(dtype)) return -ATK_EINVAL;
@@ -666,6 +739,7 @@ extern "C" int atk_dwconv1d_cl_fwd(const void* x, const void* w, const void* bia
     a.x = static_cast<const char*>(x) + b0 * x_stride_b * (int64_t)es;
     a.y = static_cast<char*>(y) + b0 * y_stride_b * (int64_t)es;
     a.w = w; a.b = bias; a.wdt = w_dtype; a.wc = w_stride_c; a.wk = w_stride_k;
+    cl_param_modes(w, bias, w_dtype, K, w_stride_c, w_stride_k, vec, &a.wmode, &a.bvec);
     a.seq = seq_idx ? seq_idx + b0 * L : nullptr;
     a.init = initial_states ? static_cast<const char*>(initial_states) + b0 * is_stride_b * (int64_t)es : nullptr;
     a.ib = is_stride_b; a.il = is_stride_l;
@@ -795,6 +869,7 @@ extern "C" int atk_causal_conv1d_cl_bwd(const void* x, const void* dout, const v
     return fail(ATK_UNSUPPORTED, "causal_conv1d_cl_bwd: tensors over 2 GiB");
   DwClCbArgs a{};
   a.x = x; a.dy = dout; a.dx = dx; a.w = w; a.b = bias; a.wdt = w_dtype; a.wc = w_stride_c; a.wk = w_stride_k;
+  cl_param_modes(w, bias, w_dtype, K, w_stride_c, w_stride_k, vec, &a.wmode, &a.bvec);
   a.seq = seq_idx; a.init = initial_states; a.ib = is_stride_b; a.il = is_stride_l;
   a.xb = x_stride_b; a.xl = x_stride_l; a.gb = dout_stride_b; a.gl = dout_stride_l;
   a.ob = dx_stride_b; a.ol = dx_stride_l;
