@@ -249,6 +249,43 @@ def bench_dw_cl_detail(dev, silu=False):
             "variant": "dwconv1d_cl_kernel / dwconv1d_cl_causal_bwd_kernel"}
 
 
+def bench_vae_block_detail(dev):
+    """Config 5's block as one unit, bf16: Conv3d(256->256, k3, pad 1) on [1, 256, 8, 64, 64] ->
+    GroupNorm(32, eps 1e-6) -> SiLU, fused by replace_conv_blocks (accelerated conv, then one
+    GroupNorm+SiLU pass), against the same block on stock F.conv3d / F.group_norm / F.silu."""
+    import copy
+    import torch
+    import torch.nn as nn
+    import torch.nn.functional as F
+    import amd_tuned_torch
+    from amd_tuned_torch import conv_fusion_ops
+    torch.manual_seed(1011)
+    C = 256
+    block = nn.Sequential(nn.Conv3d(C, C, 3, padding=1), nn.GroupNorm(32, C, eps=1e-6), nn.SiLU())
+    model = nn.Sequential(copy.deepcopy(block)).to(dev, torch.bfloat16)
+    conv_fusion_ops.replace_conv_blocks(model)
+    x = torch.randn(1, C, 8, 64, 64, generator=_gen(1012)).to(torch.bfloat16).to(dev)
+    conv3d = amd_tuned_torch._ORIGINALS[(F, "conv3d")]
+    gn = amd_tuned_torch._ORIGINALS[(F, "group_norm")]
+    m = model[0]
+
+    def stock(xx=x, f32=False):
+        cv = (lambda t: t.float()) if f32 else (lambda t: t)
+        h = conv3d(xx, cv(m.conv.weight), cv(m.conv.bias), 1, 1)
+        return F.silu(gn(h, 32, cv(m.norm.weight), cv(m.norm.bias), 1e-6))
+    with torch.no_grad():
+        y = model(x)
+        ref = stock(x.float(), True)
+        ms = graph_time_ms(lambda: model(x), 10)
+        stock_ms = event_time_ms(stock, 3)
+    err = max_rel_err(y, ref)
+    flops = 2.0 * C * 8 * 64 * 64 * C * 27
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"ms": round(ms, 4), "conv_TFLOP/s_over_block": round(tf, 1),
+            "roofline_frac": round(tf / MFMA_PEAK_TFLOPS["bf16"], 4), "stock_block_ms": round(stock_ms, 3),
+            "variant": type(m).__name__, "max_rel_err_vs_stock_fp32": float(f"{err:.3g}")}
+
+
 def bench_gn_cl_detail(shape, G, silu, dev):
     """Channels-last GroupNorm (+ SiLU), bf16: the native NHWC / NDHWC kernel against stock
     F.group_norm on the same channels-last tensor (the reference contests CK here)."""
@@ -730,6 +767,7 @@ def main():
             ("c4_conv3d_scaled_bf16", lambda: bench_conv_detail((2, 128, 16, 64, 64), (128, 128, 3, 3, 3), 1, torch.bfloat16, dev, 10)),
             ("c5_conv3d_bf16", lambda: bench_conv_detail((1, 256, 8, 64, 64), (256, 256, 3, 3, 3), 1, torch.bfloat16, dev, 10)),
             ("c5_conv3d_k7_fp16", lambda: bench_conv_detail((1, 64, 16, 32, 32), (64, 64, 7, 7, 7), 3, torch.float16, dev, 10)),
+            ("c5_vae_block_bf16", lambda: bench_vae_block_detail(dev)),
             ("c5_conv3d_dgrad_bf16", lambda: bench_conv_dgrad_detail((1, 256, 8, 64, 64), (256, 256, 3, 3, 3), 1, torch.bfloat16, dev)),
             ("c4_conv3d_scaled_dgrad_bf16", lambda: bench_conv_dgrad_detail((2, 128, 16, 64, 64), (128, 128, 3, 3, 3), 1, torch.bfloat16, dev)),
         ]

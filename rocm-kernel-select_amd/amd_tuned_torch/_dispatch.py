@@ -634,7 +634,8 @@ def _patched_group_norm(input, num_groups, weight=None, bias=None, eps=1e-5):
 
 
 # ---------------------------------------------------------------------------
-# nn.Sequential(GroupNorm(affine), SiLU, Conv2d) auto-fusion (reference 2722-2738)
+# nn.Sequential(GroupNorm(affine), SiLU, Conv2d) auto-fusion (reference 2722-2738), and the
+# conv-first order nn.Sequential(Conv2d | Conv3d, GroupNorm(affine), SiLU)
 # ---------------------------------------------------------------------------
 _SEQ_FORWARD_ORIG = None
 
@@ -650,6 +651,14 @@ def _patched_sequential_forward(self, input):
             h = conv_fusion_ops.group_norm_silu(input, norm.num_groups, norm.weight, norm.bias,
                                                 norm.eps)
             return conv(h)
+        # the decoder-block order of a video VAE: Conv2d | Conv3d, GroupNorm(affine), SiLU
+        conv, norm, act = mods.values()
+        if (type(act) is torch.nn.SiLU and isinstance(norm, torch.nn.GroupNorm) and norm.affine
+                and isinstance(conv, (torch.nn.Conv2d, torch.nn.Conv3d))):
+            if _DEBUG:
+                _debug("sequential", "conv_fusion", "conv then GroupNorm+SiLU fused", input=input)
+            return conv_fusion_ops.group_norm_silu(conv(input), norm.num_groups, norm.weight, norm.bias,
+                                                   norm.eps)
     return _SEQ_FORWARD_ORIG(self, input)
 
 

@@ -70,6 +70,10 @@ def _eligible(x, num_groups, weight, bias, layout_ok: bool = False) -> bool:
     return True
 
 
+def _grad_needed(x, weight, bias) -> bool:
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (x, weight, bias))
+
+
 def _group_norm_silu_cl(x, num_groups, weight, bias, eps, stock):
     if not _eligible(x, num_groups, weight, bias, layout_ok=True):
         return stock()
@@ -103,6 +107,9 @@ def group_norm_silu(x: torch.Tensor, num_groups: int, weight: Optional[torch.Ten
     def stock():
         return _stock_group_norm_silu(x, num_groups, weight, bias, eps)
 
+    if isinstance(x, torch.Tensor) and x.is_cuda and _grad_needed(x, weight, bias):
+        # training: F.group_norm as installed (the native forward / backward when patched)
+        return F.silu(F.group_norm(x, num_groups, weight, bias, eps))
     if isinstance(x, torch.Tensor) and x.is_cuda and _native.is_channels_last(x):
         return _group_norm_silu_cl(x, num_groups, weight, bias, eps, stock)
     if not _eligible(x, num_groups, weight, bias):
@@ -166,6 +173,35 @@ class FusedGroupNormSiLUConv2d(nn.Module):
         return "fused=GroupNorm+SiLU"
 
 
+class FusedConvGroupNormSiLU(nn.Module):
+    """Drop-in for nn.Sequential(Conv2d | Conv3d, GroupNorm(affine), SiLU): the decoder-block
+    order of a video VAE (Conv3d 256->256 k3 -> GroupNorm(32) -> SiLU).  The
+    original submodules stay under the Sequential's indices "0" and "1", so parameters and
+    state_dict keys survive.  The conv runs through F.conv2d / F.conv3d (the accelerated
+    forward when patched), GroupNorm + SiLU through group_norm_silu: one fused pass over the
+    conv output instead of a GroupNorm pass and a SiLU pass."""
+
+    def __init__(self, conv: nn.Module, norm: nn.GroupNorm):
+        super().__init__()
+        self.add_module("0", conv)
+        self.add_module("1", norm)
+
+    @property
+    def conv(self) -> nn.Module:
+        return getattr(self, "0")
+
+    @property
+    def norm(self) -> nn.GroupNorm:
+        return getattr(self, "1")
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        n = self.norm
+        return group_norm_silu(self.conv(x), n.num_groups, n.weight, n.bias, n.eps)
+
+    def extra_repr(self) -> str:
+        return "fused=GroupNorm+SiLU after conv"
+
+
 def _is_target(seq: nn.Module) -> bool:
     if not isinstance(seq, nn.Sequential) or len(seq) != 3:
         return False
@@ -174,10 +210,20 @@ def _is_target(seq: nn.Module) -> bool:
             and isinstance(c, nn.Conv2d))
 
 
+def _is_vae_target(seq: nn.Module) -> bool:
+    """nn.Sequential(Conv2d | Conv3d, GroupNorm(affine), SiLU)."""
+    if not isinstance(seq, nn.Sequential) or len(seq) != 3:
+        return False
+    a, b, c = seq[0], seq[1], seq[2]
+    return (isinstance(a, (nn.Conv2d, nn.Conv3d)) and isinstance(b, nn.GroupNorm) and b.affine
+            and type(c) is nn.SiLU)
+
+
 def replace_conv_blocks(model: nn.Module) -> int:
     """Replace every nn.Sequential(GroupNorm(affine), SiLU, Conv2d) under `model` (in place,
-    recursively) with FusedGroupNormSiLUConv2d; returns the count.  No-op (0) when fusion
-    is not enabled.  Idempotent."""
+    recursively) with FusedGroupNormSiLUConv2d, and every nn.Sequential(Conv2d | Conv3d,
+    GroupNorm(affine), SiLU) with FusedConvGroupNormSiLU; returns the count.  No-op (0) when
+    fusion is not enabled.  Idempotent."""
     if not enabled():
         return 0
     n = 0
@@ -185,17 +231,23 @@ def replace_conv_blocks(model: nn.Module) -> int:
         if _is_target(child):
             setattr(model, name, FusedGroupNormSiLUConv2d(child[0], child[2]))
             n += 1
+        elif _is_vae_target(child):
+            setattr(model, name, FusedConvGroupNormSiLU(child[0], child[1]))
+            n += 1
         else:
             n += replace_conv_blocks(child)
     return n
 
 
 def unfuse_conv_blocks(model: nn.Module) -> int:
-    """Undo replace_conv_blocks (same GroupNorm/Conv2d objects, a fresh SiLU)."""
+    """Undo replace_conv_blocks (same GroupNorm / conv objects, a fresh SiLU)."""
     n = 0
     for name, child in list(model.named_children()):
         if isinstance(child, FusedGroupNormSiLUConv2d):
             setattr(model, name, nn.Sequential(child.norm, nn.SiLU(), child.conv))
+            n += 1
+        elif isinstance(child, FusedConvGroupNormSiLU):
+            setattr(model, name, nn.Sequential(child.conv, child.norm, nn.SiLU()))
             n += 1
         else:
             n += unfuse_conv_blocks(child)

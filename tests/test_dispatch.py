@@ -246,6 +246,46 @@ def test_sequential_groupnorm_silu_conv_fusion(monkeypatch):
     assert calls == []
 
 
+def test_sequential_conv_groupnorm_silu_fusion(monkeypatch):
+    """The conv-first (video VAE decoder) order: Conv3d, GroupNorm(affine), SiLU."""
+    calls = []
+    monkeypatch.setattr(conv_fusion_ops, "group_norm_silu",
+                        lambda x, G, w, b, eps: calls.append(G) or F.silu(
+                            _dispatch._ORIGINALS[(F, "group_norm")](x, G, w, b, eps)))
+    if (nn.Sequential, "forward") not in _dispatch._ORIGINALS:
+        monkeypatch.setattr(_dispatch, "_SEQ_FORWARD_ORIG", nn.Sequential.forward)
+    fwd = _dispatch._patched_sequential_forward
+    seq = nn.Sequential(nn.Conv3d(4, 4, 3, padding=1), nn.GroupNorm(2, 4, eps=1e-6), nn.SiLU())
+    x = torch.randn(1, 4, 3, 5, 5)
+    with torch.no_grad():
+        ref = F.silu(seq[1](seq[0](x)))
+        out = fwd(seq, x)
+    assert calls == [2] and torch.allclose(out, ref, atol=1e-6)
+    calls.clear()
+    with torch.no_grad():
+        fwd(nn.Sequential(nn.Conv3d(4, 4, 3, padding=1), nn.GroupNorm(2, 4), nn.ReLU()), x)
+        fwd(nn.Sequential(nn.Conv3d(4, 4, 3, padding=1), nn.GroupNorm(2, 4, affine=False), nn.SiLU()), x)
+    assert calls == []
+
+
+def test_replace_and_unfuse_vae_blocks(monkeypatch):
+    monkeypatch.setattr(conv_fusion_ops, "enabled", lambda: True)
+    model = nn.Sequential(nn.Sequential(nn.Conv3d(4, 4, 3, padding=1), nn.GroupNorm(2, 4), nn.SiLU()),
+                          nn.Sequential(nn.Conv2d(4, 4, 3, padding=1), nn.GroupNorm(2, 4), nn.SiLU()))
+    keys = set(model.state_dict().keys())
+    conv3 = model[0][0]
+    assert conv_fusion_ops.replace_conv_blocks(model) == 2
+    assert isinstance(model[0], conv_fusion_ops.FusedConvGroupNormSiLU)
+    assert model[0].conv is conv3 and set(model.state_dict().keys()) == keys
+    assert conv_fusion_ops.replace_conv_blocks(model) == 0
+    x = torch.randn(1, 4, 3, 5, 5)
+    with torch.no_grad():
+        fused = model[0](x)
+    assert conv_fusion_ops.unfuse_conv_blocks(model) == 2
+    with torch.no_grad():
+        assert torch.allclose(model[0](x), fused, atol=1e-6)
+
+
 def test_replace_and_unfuse_conv_blocks(monkeypatch):
     monkeypatch.setattr(conv_fusion_ops, "enabled", lambda: True)
     model = nn.Sequential(nn.Sequential(nn.GroupNorm(2, 4), nn.SiLU(), nn.Conv2d(4, 4, 3, padding=1)),

@@ -178,3 +178,52 @@ def test_conv3d_autograd_dgrad_through_forward(dev, dtype):
     for got, ref in ((gx, rx), (gw, rw), (gb, rb)):
         err = (got.double().cpu() - ref).abs().max().item() / ref.abs().max().item()
         assert err <= bar, err
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_vae_block_fused_forward_and_grads(dtype):
+    """Config 5's block order, Conv3d(C->C, k3, pad 1) -> GroupNorm(32, eps 1e-6) -> SiLU, at a
+    reduced size: replace_conv_blocks fuses it (accelerated conv, fused GroupNorm+SiLU);
+    the output and, with gradients live, the parameter and input gradients match a float64
+    CPU run of the unfused stock block."""
+    import torch.nn as nn
+    import amd_tuned_torch
+    from amd_tuned_torch import conv_fusion_ops
+    torch.manual_seed(0)
+    C = 64
+    block = nn.Sequential(nn.Conv3d(C, C, 3, padding=1), nn.GroupNorm(32, C, eps=1e-6), nn.SiLU())
+    with torch.no_grad():
+        block[1].weight.normal_(1.0, 0.1)
+        block[1].bias.normal_(0.0, 0.1)
+    import copy
+    ref_block = copy.deepcopy(block).double()
+    model = nn.Sequential(copy.deepcopy(block)).to("cuda", dtype)
+    assert conv_fusion_ops.replace_conv_blocks(model) == 1
+    assert isinstance(model[0], conv_fusion_ops.FusedConvGroupNormSiLU)
+    x = torch.randn(1, C, 4, 16, 16)
+    bar = 1e-2 if dtype == torch.bfloat16 else 1e-4
+    with torch.no_grad():
+        y = model(x.to("cuda", dtype))
+        amd_tuned_torch.disable()
+        try:
+            ref = ref_block(x.double())
+        finally:
+            amd_tuned_torch.enable()
+    assert O.max_rel_err(y.float(), ref) <= bar
+    # training: gradients through the accelerated conv (dgrad on the forward kernels) and the
+    # native GroupNorm backward
+    xg = x.to("cuda", dtype).requires_grad_()
+    out = model(xg)
+    g = torch.randn(out.shape, generator=torch.Generator().manual_seed(1))
+    out.backward(g.to("cuda", dtype))
+    xr = x.double().requires_grad_()
+    amd_tuned_torch.disable()
+    try:
+        ref_block(xr).backward(g.double())
+    finally:
+        amd_tuned_torch.enable()
+    assert O.max_rel_err(xg.grad.float(), xr.grad) <= bar
+    fused = model[0]
+    for got, want in ((fused.conv.weight.grad, ref_block[0].weight.grad), (fused.conv.bias.grad, ref_block[0].bias.grad),
+                      (fused.norm.weight.grad, ref_block[1].weight.grad), (fused.norm.bias.grad, ref_block[1].bias.grad)):
+        assert O.max_rel_err(got.float(), want) <= bar
