@@ -249,6 +249,36 @@ def bench_dw_cl_detail(dev, silu=False):
             "variant": "dwconv1d_cl_kernel / dwconv1d_cl_causal_bwd_kernel"}
 
 
+def bench_conv_cl_detail(dev):
+    """Config 5's Conv3d (C5a: 256->256, k3, pad 1, [1, 256, 8, 64, 64], bf16) on channels-last
+    (NDHWC) input and weight, through patched F.conv3d (the contest's winner, conversions
+    included), against stock F.conv3d on the same channels-last tensors."""
+    import torch
+    import torch.nn.functional as F
+    import amd_tuned_torch
+    from amd_tuned_torch import kernel_select
+    g = _gen(1013)
+    fmt = torch.channels_last_3d
+    x = torch.randn(1, 256, 8, 64, 64, generator=g).to(torch.bfloat16).to(dev).contiguous(memory_format=fmt)
+    w = (torch.randn(256, 256, 3, 3, 3, generator=g) * math.sqrt(2.0 / (256 * 27))).to(torch.bfloat16)
+    w = w.to(dev).contiguous(memory_format=fmt)
+    b = (torch.randn(256, generator=g) * 0.1).to(torch.bfloat16).to(dev)
+    orig = amd_tuned_torch._ORIGINALS[(F, "conv3d")]
+    y = F.conv3d(x, w, b, 1, 1)
+    won = kernel_select.cached("conv3d", x, w, 1, 1, 1) or "?"
+    ref = orig(x.float(), w.float(), b.float(), 1, 1)
+    err = max_rel_err(y, ref)
+    layout_ok = bool(y.is_contiguous(memory_format=fmt))
+    del y, ref
+    ms = graph_time_ms(lambda: F.conv3d(x, w, b, 1, 1), 10)
+    stock_ms = event_time_ms(lambda: orig(x, w, b, 1, 1), 3)
+    flops = 2.0 * 256 * 8 * 64 * 64 * 256 * 27
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "roofline_frac": round(tf / MFMA_PEAK_TFLOPS["bf16"], 4),
+            "winner": won, "stock_ms": round(stock_ms, 3), "output_channels_last": layout_ok,
+            "max_rel_err_vs_stock_fp32": float(f"{err:.3g}")}
+
+
 def bench_vae_block_detail(dev):
     """Config 5's block as one unit, bf16: Conv3d(256->256, k3, pad 1) on [1, 256, 8, 64, 64] ->
     GroupNorm(32, eps 1e-6) -> SiLU, fused by replace_conv_blocks (accelerated conv, then one
@@ -768,6 +798,7 @@ def main():
             ("c5_conv3d_bf16", lambda: bench_conv_detail((1, 256, 8, 64, 64), (256, 256, 3, 3, 3), 1, torch.bfloat16, dev, 10)),
             ("c5_conv3d_k7_fp16", lambda: bench_conv_detail((1, 64, 16, 32, 32), (64, 64, 7, 7, 7), 3, torch.float16, dev, 10)),
             ("c5_vae_block_bf16", lambda: bench_vae_block_detail(dev)),
+            ("c5_conv3d_ndhwc_bf16", lambda: bench_conv_cl_detail(dev)),
             ("c5_conv3d_dgrad_bf16", lambda: bench_conv_dgrad_detail((1, 256, 8, 64, 64), (256, 256, 3, 3, 3), 1, torch.bfloat16, dev)),
             ("c4_conv3d_scaled_dgrad_bf16", lambda: bench_conv_dgrad_detail((2, 128, 16, 64, 64), (128, 128, 3, 3, 3), 1, torch.bfloat16, dev)),
         ]

@@ -281,7 +281,8 @@ def _conv_accelerated_forward(nd: int, input, weight, bias, stride, padding, dil
     eligible = (isinstance(input, torch.Tensor) and isinstance(weight, torch.Tensor)
                 and not isinstance(padding, str)
                 and input.dim() == nd + 2 and weight.dim() == nd + 2
-                and input.is_contiguous() and weight.is_contiguous()
+                and (input.is_contiguous() or _channels_last(input))
+                and (weight.is_contiguous() or _channels_last(weight))
                 and _usable(input, weight, bias, dtypes=_CONV_NATIVE_DTYPES)
                 and (bias is None or bias.dtype == input.dtype)
                 and _native.available())
@@ -290,6 +291,12 @@ def _conv_accelerated_forward(nd: int, input, weight, bias, stride, padding, dil
             _debug(op, "stock", "layout/dtype/device outside the native tier",
                    input=input, weight=weight)
         return orig(input, weight, bias, stride, padding, dilation, groups)
+    if not (input.is_contiguous() and weight.is_contiguous()):
+        # channels-last (NHWC / NDHWC) tensors: the MFMA kernels read NC(D)HW, so a native
+        # candidate converts the input (and weight) and hands its output back in the input's
+        # layout, as stock does; the contest times the conversions with the kernel, and the
+        # winner cache keys on the memory format
+        fn = _in_ncdhw(fn, _channels_last(input), nd)
 
     if kernel_select.enabled():
         won = kernel_select.cached(kind, input, weight, stride, padding, dilation)
@@ -329,6 +336,17 @@ def _conv_accelerated_forward(nd: int, input, weight, bias, stride, padding, dil
     if _DEBUG:
         _debug(op, "stock", "every native variant declined", input=input, weight=weight)
     return orig(input, weight, bias, stride, padding, dilation, groups)
+
+
+def _in_ncdhw(fn: Callable, cl_out: bool, nd: int) -> Callable:
+    """`fn` on contiguous (NC(D)HW) copies of input and weight; the output converted to
+    channels-last when `cl_out`."""
+    fmt = torch.channels_last_3d if nd == 3 else torch.channels_last
+
+    def run(i, w, b, s, p, d, variant: int = -1):
+        y = fn(i.contiguous(), w.contiguous(), b, s, p, d, variant=variant)
+        return y.contiguous(memory_format=fmt) if cl_out else y
+    return run
 
 
 def _dgrad_padding(weight, stride, padding, dilation, groups, nd):

@@ -188,10 +188,33 @@ def test_conv_gates_send_to_stock(monkeypatch, contest):
     x, w = torch.randn(1, 4, 6, 6), torch.randn(4, 1, 3, 3)
     F.conv2d(x, w, None, 1, 1, 1, 4)                               # grouped
     F.conv2d(x, torch.randn(4, 4, 1, 1))                           # pointwise 1x1
-    F.conv2d(x.to(memory_format=torch.channels_last), torch.randn(4, 4, 3, 3), None, 1, 1)
+    F.conv2d(x.transpose(2, 3), torch.randn(4, 4, 3, 3), None, 1, 1)  # neither contiguous nor channels-last
     F.conv2d(x, torch.randn(4, 4, 3, 3), None, 1, "same")          # string padding
     F.conv2d(x.double(), torch.randn(4, 4, 3, 3).double())         # dtype outside the tier
     assert fake.calls == []
+
+
+def test_conv_channels_last_contests_native_on_nchw_copies(monkeypatch, contest):
+    """Channels-last input and weight enter the contest: the native candidates run on NCHW
+    copies, hand the output back channels-last like stock, and the winner is keyed on the
+    memory format."""
+    fake = FakeNative(monkeypatch, ["f32_a"], ["res"])
+    seen = []
+    orig_conv2d = _native.conv2d
+
+    def spy(input, weight, *a, **k):
+        seen.append((input.is_contiguous(), weight.is_contiguous()))
+        return orig_conv2d(input, weight, *a, **k)
+    monkeypatch.setattr(_native, "conv2d", spy)
+    contest.update({"native.f32_a": 0.5, "stock": 2.0})
+    x = torch.randn(1, 4, 6, 6).to(memory_format=torch.channels_last)
+    w = torch.randn(5, 4, 3, 3).to(memory_format=torch.channels_last)
+    y = F.conv2d(x, w, None, 1, 1)
+    assert set(fake.calls) == {("conv2d", "f32_a")} and seen and set(seen) == {(True, True)}
+    assert y.is_contiguous(memory_format=torch.channels_last)
+    assert torch.allclose(y, _dispatch._ORIGINALS[(F, "conv2d")](x, w, None, 1, 1), atol=1e-5)
+    assert kernel_select.cached("conv2d", x, w, 1, 1, 1) == "native.f32_a"
+    assert kernel_select.cached("conv2d", x.contiguous(), w, 1, 1, 1) is None  # layout in the key
 
 
 def test_group_norm_contest_and_key(monkeypatch, contest):

@@ -227,3 +227,37 @@ def test_vae_block_fused_forward_and_grads(dtype):
     for got, want in ((fused.conv.weight.grad, ref_block[0].weight.grad), (fused.conv.bias.grad, ref_block[0].bias.grad),
                       (fused.norm.weight.grad, ref_block[1].weight.grad), (fused.norm.bias.grad, ref_block[1].bias.grad)):
         assert O.max_rel_err(got.float(), want) <= bar
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("nd", [2, 3])
+def test_channels_last_conv_through_patched_functional(nd, dtype):
+    """Channels-last (NHWC / NDHWC) input and weight through patched F.conv2d / F.conv3d:
+    the contest includes the native tiles (on NC(D)HW copies) and returns the output in the
+    input's channels-last layout, like stock; values match the float64 oracle."""
+    import torch.nn.functional as F
+    import amd_tuned_torch
+    from amd_tuned_torch import kernel_select
+    g = torch.Generator().manual_seed(nd)
+    if nd == 3:
+        x = torch.randn(1, 32, 6, 20, 20, generator=g)
+        w = torch.randn(48, 32, 3, 3, 3, generator=g) / math.sqrt(32 * 27)
+        fmt, conv = torch.channels_last_3d, F.conv3d
+    else:
+        x = torch.randn(2, 32, 24, 24, generator=g)
+        w = torch.randn(48, 32, 3, 3, generator=g) / math.sqrt(32 * 9)
+        fmt, conv = torch.channels_last, F.conv2d
+    b = torch.randn(48, generator=g) * 0.1
+    xd = x.to("cuda", dtype).contiguous(memory_format=fmt)
+    wd = w.to("cuda", dtype).contiguous(memory_format=fmt)
+    bd = b.to("cuda", dtype)
+    assert amd_tuned_torch.is_enabled()
+    y = conv(xd, wd, bd, 1, 1)
+    assert y.is_contiguous(memory_format=fmt)
+    won = kernel_select.cached("conv3d" if nd == 3 else "conv2d", xd, wd, 1, 1, 1)
+    assert won is not None
+    ref = (O.conv3d if nd == 3 else O.conv2d)(x.to(dtype), w.to(dtype), b.to(dtype), 1, 1, 1)
+    bar = 1e-5 if dtype == torch.float32 else 1e-2
+    assert O.max_rel_err(y.float().contiguous(), ref) <= bar, won
+    y2 = conv(xd, wd, bd, 1, 1)  # cached-winner path
+    assert y2.is_contiguous(memory_format=fmt) and O.max_rel_err(y2.float().contiguous(), ref) <= bar
