@@ -279,6 +279,30 @@ def bench_conv_cl_detail(dev):
             "max_rel_err_vs_stock_fp32": float(f"{err:.3g}")}
 
 
+def bench_conv_wgrad_detail(xs, co, dev, iters=10):
+    """Weight gradient of a stride-1 'same' 3x3x3 conv3d, bf16: the native wgrad kernel
+    against stock aten.convolution_backward computing the same weight gradient."""
+    import torch
+    from amd_tuned_torch import _native as nat
+    g = _gen(1014)
+    x = torch.randn(*xs, generator=g).to(torch.bfloat16).to(dev)
+    dy = torch.randn(xs[0], co, *xs[2:], generator=g).to(torch.bfloat16).to(dev)
+    w = torch.zeros(co, xs[1], 3, 3, 3, dtype=torch.bfloat16, device=dev)
+    dw = nat.conv_wgrad(x, dy, 3)
+    ref = torch.ops.aten.convolution_backward(dy.float(), x.float(), w.float(), None, [1] * 3, [1] * 3, [1] * 3,
+                                              False, [0] * 3, 1, [False, True, False])[1]
+    err = max_rel_err(dw, ref)
+    del ref
+    ms = graph_time_ms(lambda: nat.conv_wgrad(x, dy, 3), iters)
+    stock_ms = event_time_ms(lambda: torch.ops.aten.convolution_backward(
+        dy, x, w, None, [1] * 3, [1] * 3, [1] * 3, False, [0] * 3, 1, [False, True, False]), 3)
+    flops = 2.0 * xs[0] * co * xs[2] * xs[3] * xs[4] * xs[1] * 27
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "roofline_frac": round(tf / MFMA_PEAK_TFLOPS["bf16"], 4),
+            "variant": "conv_wgrad_kernel + reduce", "stock_wgrad_ms": round(stock_ms, 3),
+            "max_rel_err_vs_stock_fp32": float(f"{err:.3g}")}
+
+
 def bench_vae_block_detail(dev):
     """Config 5's block as one unit, bf16: Conv3d(256->256, k3, pad 1) on [1, 256, 8, 64, 64] ->
     GroupNorm(32, eps 1e-6) -> SiLU, fused by replace_conv_blocks (accelerated conv, then one
@@ -798,6 +822,8 @@ def main():
             ("c5_conv3d_bf16", lambda: bench_conv_detail((1, 256, 8, 64, 64), (256, 256, 3, 3, 3), 1, torch.bfloat16, dev, 10)),
             ("c5_conv3d_k7_fp16", lambda: bench_conv_detail((1, 64, 16, 32, 32), (64, 64, 7, 7, 7), 3, torch.float16, dev, 10)),
             ("c5_vae_block_bf16", lambda: bench_vae_block_detail(dev)),
+            ("c5_conv3d_wgrad_bf16", lambda: bench_conv_wgrad_detail((1, 256, 8, 64, 64), 256, dev)),
+            ("c4_conv3d_scaled_wgrad_bf16", lambda: bench_conv_wgrad_detail((2, 128, 16, 64, 64), 128, dev)),
             ("c5_conv3d_ndhwc_bf16", lambda: bench_conv_cl_detail(dev)),
             ("c5_conv3d_dgrad_bf16", lambda: bench_conv_dgrad_detail((1, 256, 8, 64, 64), (256, 256, 3, 3, 3), 1, torch.bfloat16, dev)),
             ("c4_conv3d_scaled_dgrad_bf16", lambda: bench_conv_dgrad_detail((2, 128, 16, 64, 64), (128, 128, 3, 3, 3), 1, torch.bfloat16, dev)),

@@ -272,6 +272,21 @@ int atk_conv_fwd(const void* x, const void* w, const void* bias, void* y, int64_
                  int dw, int dtype, int variant, void* workspace, size_t workspace_bytes,
                  atk_stream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * Conv weight gradient (replaces the dweight part of `aten.convolution_backward` that the
+ * reference's _Conv3dFn.backward calls, amd_tuned_torch/_dispatch.py:2064-2075), for
+ * stride-1, dilation-1 convs with kernel (KD, 3, 3), KD in {1, 3}, and "same" padding
+ * (KD/2, 1, 1):
+ *   dw[co,ci,kz,ky,kx] = sum_{n,z,y,x} dy[n,co,z,y,x] * x[n,ci,z+kz-KD/2,y+ky-1,x+kx-1].
+ * x: [N, Ci, D, H, W], dy: [N, Co, D, H, W], fp16 / bf16, contiguous; dw: [Co, Ci, KD, 3, 3]
+ * fp32.  Ci % 32 == 0, Co % 128 == 0, W % 16 == 0, W <= 64.  conv2d is D = 1, KD = 1.  The
+ * workspace holds per-chunk fp32 partials, summed in a fixed order (deterministic); it
+ * needs no initialisation.
+ * ------------------------------------------------------------------------- */
+size_t atk_conv_wgrad_workspace_bytes(int64_t N, int64_t Ci, int64_t D, int64_t H, int64_t W, int64_t Co, int KD);
+int atk_conv_wgrad(const void* x, const void* dy, float* dw, int64_t N, int64_t Ci, int64_t D, int64_t H,
+                   int64_t W, int64_t Co, int KD, int dtype, void* workspace, size_t ws_bytes, atk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

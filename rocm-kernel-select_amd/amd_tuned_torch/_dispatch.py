@@ -376,11 +376,43 @@ def _dgrad_via_forward(grad_output, weight, pad_t, nd, fwd):
     return fwd(grad_output.contiguous(), wt, None, 1, pad_t, 1, 1)
 
 
+def _wgrad_native(input, grad_output, weight, stride, padding, dilation, groups, nd):
+    """Weight gradient through the native kernel for stride-1, dilation-1, groups-1 'same'
+    convs with 3x3 (2D) or 3x3x3 / 1x3x3 (3D) kernels in 16-bit types; None otherwise (or when
+    the kernel declines the shape)."""
+    if groups != 1 or isinstance(padding, str) or weight.dtype not in (torch.float16, torch.bfloat16):
+        return None
+    tup = _triple if nd == 3 else _pair
+    try:
+        s, p, d = tup(stride), tup(padding), tup(dilation)
+    except (TypeError, ValueError):
+        return None
+    if any(v != 1 for v in s) or any(v != 1 for v in d):
+        return None
+    k = tuple(weight.shape[2:])
+    if nd == 3:
+        if k not in ((3, 3, 3), (1, 3, 3)) or p != (k[0] // 2, 1, 1):
+            return None
+        kd, x5, g5 = k[0], input, grad_output
+    else:
+        if k != (3, 3) or p != (1, 1):
+            return None
+        kd, x5, g5 = 1, input.unsqueeze(2), grad_output.unsqueeze(2)
+    if g5.dtype != x5.dtype or tuple(g5.shape[2:]) != tuple(x5.shape[2:]):
+        return None
+    try:
+        dw = _native.conv_wgrad(x5.contiguous(), g5.contiguous(), kd)
+    except _native.Unsupported:
+        return None
+    return dw.reshape(weight.shape).to(weight.dtype)
+
+
 class _ConvFn(torch.autograd.Function):
     """Accelerated forward; the input gradient (stride 1, dilation 1, groups 1) through the
-    same accelerated forward on dy with transposed, flipped weights; the rest through
-    aten.convolution_backward -- the op autograd would have used unpatched (reference
-    _Conv3dFn, _dispatch.py:2029-2075)."""
+    same accelerated forward on dy with transposed, flipped weights; the weight gradient of
+    'same' 3x3(x3) convs through the native wgrad kernel (and then the bias gradient as a
+    reduction of dy); the rest through aten.convolution_backward -- the op autograd would
+    have used unpatched (reference _Conv3dFn, _dispatch.py:2029-2075)."""
 
     @staticmethod
     def forward(ctx, input, weight, bias, stride, padding, dilation, groups, nd, fwd):
@@ -408,12 +440,22 @@ class _ConvFn(torch.autograd.Function):
                 else:
                     needs[0] = False
         gw = gb = None
+        if needs[1] and input.is_cuda:
+            gw = _wgrad_native(input, grad_output, weight, stride, padding, dilation, groups, nd)
+            if gw is not None:
+                needs[1] = False
+        if needs[2] and not needs[0] and not needs[1]:
+            # every other gradient is native: the bias gradient is a reduction of dy
+            gb = grad_output.sum(dim=[0] + list(range(2, 2 + nd)), dtype=torch.float32).to(weight.dtype)
+            needs[2] = False
         if any(needs):
             tup = _triple if nd == 3 else _pair
-            ai, gw, gb = torch.ops.aten.convolution_backward(
+            ai, aw, ab = torch.ops.aten.convolution_backward(
                 grad_output.contiguous(), input, weight, ctx.bias_sizes, list(tup(stride)),
                 list(tup(padding)), list(tup(dilation)), False, [0] * nd, groups, needs)
             gi = ai if gi is None else gi
+            gw = aw if gw is None else gw
+            gb = ab if gb is None else gb
         return gi, gw, gb, None, None, None, None, None, None
 
 

@@ -41,7 +41,7 @@ EXPORTED_SYMBOLS = (
     "atk_group_norm_workspace_zero_bytes", "atk_group_norm_fwd", "atk_group_norm_cl_workspace_bytes",
     "atk_group_norm_cl_fwd", "atk_group_norm_bwd_workspace_bytes",
     "atk_group_norm_bwd", "atk_conv_workspace_bytes",
-    "atk_conv_fwd",
+    "atk_conv_fwd", "atk_conv_wgrad_workspace_bytes", "atk_conv_wgrad",
 )
 
 
@@ -102,6 +102,10 @@ def _declare(lib) -> None:
     lib.atk_conv_workspace_bytes.restype = sz
     lib.atk_conv_fwd.argtypes = [vp, vp, vp, vp] + conv_geom + [i32, i32, vp, sz, vp]
     lib.atk_conv_fwd.restype = i32
+    lib.atk_conv_wgrad_workspace_bytes.argtypes = [i64, i64, i64, i64, i64, i64, i32]
+    lib.atk_conv_wgrad_workspace_bytes.restype = sz
+    lib.atk_conv_wgrad.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, i64, i32, i32, vp, sz, vp]
+    lib.atk_conv_wgrad.restype = i32
 
 
 def load(path: str = LIB_PATH):
@@ -719,3 +723,29 @@ def conv3d(input, weight, bias=None, stride: Sequence[int] = (1, 1, 1), padding=
     """Reference signature `conv3d(input, weight, bias?, stride, padding, dilation)`
     (src/main_rocm.cpp:798-854), groups = 1, NCDHW."""
     return _conv(input, weight, bias, stride, padding, dilation, 3, variant, out)
+
+
+def conv_wgrad(x: torch.Tensor, dy: torch.Tensor, kd: int) -> torch.Tensor:
+    """fp32 weight gradient [Co, Ci, kd, 3, 3] of a stride-1, dilation-1, 'same'-padded
+    (kd // 2, 1, 1) conv3d with kernel (kd, 3, 3), kd in {1, 3}: x [N, Ci, D, H, W] and
+    dy [N, Co, D, H, W] contiguous, one 16-bit dtype.  Raises Unsupported outside
+    Ci % 32 == 0, Co % 128 == 0, W % 16 == 0, W <= 64."""
+    _require_cuda(x, dy)
+    if x.dim() != 5 or dy.dim() != 5 or x.shape[0] != dy.shape[0] or x.shape[2:] != dy.shape[2:]:
+        raise RuntimeError("conv_wgrad expects x [N, Ci, D, H, W] and dy [N, Co, D, H, W]")
+    if x.dtype not in (torch.float16, torch.bfloat16) or dy.dtype != x.dtype:
+        raise Unsupported("conv_wgrad: float16 / bfloat16 only")
+    if not (x.is_contiguous() and dy.is_contiguous()):
+        raise RuntimeError("conv_wgrad: x and dy must be contiguous")
+    N, Ci, D, H, W = x.shape
+    Co = dy.shape[1]
+    if kd not in (1, 3) or Ci % 32 or Co % 128 or W % 16 or W > 64 or x.numel() == 0 or dy.numel() == 0:
+        raise Unsupported("conv_wgrad: needs kd in {1, 3}, Ci % 32, Co % 128, W % 16 == 0, W <= 64")
+    dw = torch.empty((Co, Ci, kd, 3, 3), dtype=torch.float32, device=x.device)
+    L_ = lib()
+    nbytes = L_.atk_conv_wgrad_workspace_bytes(N, Ci, D, H, W, Co, kd)
+    ws = workspace(x.device, "conv_wgrad", nbytes)
+    rc = L_.atk_conv_wgrad(_ptr(x), _ptr(dy), _ptr(dw), N, Ci, D, H, W, Co, kd, _DTYPE_CODE[x.dtype],
+                           _ptr(ws), ws.numel(), _stream(x))
+    _check(rc, "conv_wgrad")
+    return dw

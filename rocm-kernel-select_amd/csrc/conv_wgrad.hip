@@ -1,0 +1,283 @@
+// Weight gradient of a stride-1 "same" 3x3(x3) conv2d / conv3d on gfx950 MFMA.
+//
+//   dW[co, ci, kz, ky, kx] = sum_{n, z, y, x} dy[n, co, z, y, x] * x[n, ci, z+kz-pd, y+ky-1, x+kx-1]
+//
+// (x = 0 outside the input).  The reference computes this with aten.convolution_backward
+// (amd_tuned_torch/_dispatch.py:2064-2075).  As a GEMM it is M = Co, N = Ci, K = output
+// positions, once per tap:
+//  * A operand (32 co x 16 positions): dy rows are contiguous along x, so a lane's fragment
+//    (8 positions of one co) is one 16-byte global load, shared by all 9 in-plane taps.
+//  * B operand (16 positions x 32 ci): for a workgroup's 32 input channels, TY+2 input rows
+//    of the plane z+kz-pd are staged in LDS with 8 zero elements on either side of each row.
+//    For 8 output positions a lane reads input elements [x0+7, x0+17) of a row (covering
+//    the kx = 0, 1, 2 shifts) as one b32 + one b128 + one b32 LDS read; the three shifted
+//    fragments are byte-aligned from those six dwords (v_alignbyte).
+//  * A workgroup = 4 waves = 128 output channels x 32 input channels x one kz; each wave
+//    holds 3x3 accumulator tiles (144 fp32 registers) for its 32 output channels.
+//  * The position range is split into chunks of (n, z) output planes across workgroups;
+//    each writes fp32 partials in the final weight layout, summed in a fixed order by a
+//    reduce kernel (deterministic).
+// The next stage's input rows are loaded into registers while the current stage computes.
+#include <algorithm>
+
+#include "conv_common.h"
+
+namespace atk {
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int WG_NT = 256;   // 4 waves
+constexpr int WG_CO = 128;   // output channels per workgroup (32 per wave)
+constexpr int WG_CI = 32;    // input channels per workgroup
+constexpr int WG_TY = 4;     // output rows per stage
+constexpr int WG_R = WG_TY + 2;
+constexpr int WG_PAD = 8;    // zero elements left / right of each staged row
+constexpr int WG_MAXW = 64;  // staging map: 32 ci x 6 rows x W / 8 chunks over 256 threads x 6 loads
+constexpr int WG_LD = 6;     // 16-byte staging loads per thread
+
+struct WgArgs {
+  const void* x;
+  const void* dy;
+  float* part;                 // [chunks][Co][Ci][KD*9]
+  float* dw;                   // [Co][Ci][KD*9]
+  int N, Ci, Co, D, H, W, KD, pd;
+  int planes_per_chunk, chunks;
+  int pitch;                   // staged row pitch in elements (W + 2*PAD)
+  int slab;                    // elements per input channel in LDS (R * pitch, bank padded)
+  int chunks16;                // 16-byte chunks per staged stage = WG_CI * R * W / 8
+  uint32_t x_bytes, dy_bytes;
+};
+
+template <typename T>
+__device__ __forceinline__ void mfma(f32x16& acc, const uint4& a, const uint4& b) {
+  if constexpr (sizeof(T) == 2 && __is_same(T, __bf16))
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*reinterpret_cast<const bf16x8*>(&a),
+                                                  *reinterpret_cast<const bf16x8*>(&b), acc, 0, 0, 0);
+  else
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const f16x8*>(&a),
+                                                 *reinterpret_cast<const f16x8*>(&b), acc, 0, 0, 0);
+}
+
+template <typename T>
+__global__ __launch_bounds__(WG_NT, 2) void conv_wgrad_kernel(WgArgs a) {
+  extern __shared__ __align__(16) unsigned char smem_raw[];
+  T* s_x = reinterpret_cast<T*>(smem_raw);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 31, half = lane >> 5;
+  const int n_ci = a.Ci / WG_CI;
+  const int ci_base = (blockIdx.x % n_ci) * WG_CI;
+  const int co_base = (blockIdx.x / n_ci) * WG_CO + wave * 32;
+  const int kz = blockIdx.y;
+  const int chunk = blockIdx.z;
+  const int HW = a.H * a.W;
+  const int64_t plane_x = (int64_t)a.D * HW;  // elements per (n, channel) volume
+
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.x_bytes);
+  const __amdgpu_buffer_rsrc_t rg = make_rsrc(a.dy, a.dy_bytes);
+
+  // zero the row pads once (never overwritten by the staged data)
+  for (int i = tid; i < WG_CI * WG_R * 2; i += WG_NT) {
+    const int side = i & 1, row = (i >> 1) % WG_R, c = (i >> 1) / WG_R;
+    *reinterpret_cast<uint4*>(s_x + c * a.slab + row * a.pitch + (side ? WG_PAD + a.W : 0)) = make_uint4(0, 0, 0, 0);
+  }
+
+  f32x16 acc[3][3];
+#pragma unroll
+  for (int i = 0; i < 3; ++i)
+#pragma unroll
+    for (int j = 0; j < 3; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  // staging map: chunk q of 16 bytes -> (ci c, row r, x0)
+  const int xq = a.W >> 3;  // 16-byte chunks per row
+  auto stage_load = [&](int n, int zi, int y0, uint4 (&buf)[WG_LD]) {
+#pragma unroll
+    for (int k = 0; k < WG_LD; ++k) {
+      const int q = tid + k * WG_NT;
+      const int c = q / (WG_R * xq), rem = q - c * (WG_R * xq);
+      const int r = rem / xq, x0 = (rem - r * xq) * 8;
+      const int yi = y0 - 1 + r;
+      const bool ok = q < a.chunks16 && zi >= 0 && zi < a.D && yi >= 0 && yi < a.H;
+      const int64_t e = ((int64_t)n * a.Ci + ci_base + c) * plane_x + ((int64_t)zi * a.H + yi) * a.W + x0;
+      buf[k] = bload16(rx, ok ? (uint32_t)(e * (int64_t)sizeof(T)) : kOOB, 0);
+    }
+  };
+  auto stage_store = [&](const uint4 (&buf)[WG_LD]) {
+#pragma unroll
+    for (int k = 0; k < WG_LD; ++k) {
+      const int q = tid + k * WG_NT;
+      if (q < a.chunks16) {
+        const int c = q / (WG_R * xq), rem = q - c * (WG_R * xq);
+        const int r = rem / xq, x0 = (rem - r * xq) * 8;
+        *reinterpret_cast<uint4*>(s_x + c * a.slab + r * a.pitch + WG_PAD + x0) = buf[k];
+      }
+    }
+  };
+
+  const int total_planes = a.N * a.D;
+  const int p_begin = chunk * a.planes_per_chunk;
+  const int p_end = min(p_begin + a.planes_per_chunk, total_planes);
+  const int n_ystages = (a.H + WG_TY - 1) / WG_TY;
+  const int ksteps_row = a.W >> 4;
+  // LDS read base of this lane: input channel `col`, first 8 output positions of its half
+  const T* s_lane = s_x + col * a.slab + half * 8;
+
+  uint4 buf[WG_LD];
+  int st = p_begin * n_ystages;
+  const int st_end = p_end * n_ystages;
+  if (st < st_end) {
+    const int pl = st / n_ystages, ys = st - (st / n_ystages) * n_ystages;
+    stage_load(pl / a.D, pl % a.D + kz - a.pd, ys * WG_TY, buf);
+  }
+  for (; st < st_end; ++st) {
+    const int pl = st / n_ystages, ys = st - pl * n_ystages;
+    const int n = pl / a.D, z = pl - n * a.D;
+    const int y0 = ys * WG_TY;
+    __syncthreads();  // previous stage's reads done
+    stage_store(buf);
+    __syncthreads();
+    if (st + 1 < st_end) {
+      const int pl2 = (st + 1) / n_ystages, ys2 = (st + 1) - pl2 * n_ystages;
+      stage_load(pl2 / a.D, pl2 % a.D + kz - a.pd, ys2 * WG_TY, buf);
+    }
+    const int zi = z + kz - a.pd;
+    if (zi < 0 || zi >= a.D) continue;  // this kz tap reads only zero padding here (uniform)
+    const int64_t gbase = ((int64_t)n * a.Co + co_base + col) * plane_x + (int64_t)z * HW;
+    const int rows = min(WG_TY, a.H - y0);
+    const int nk = rows * ksteps_row;
+    uint4 an = bload16(rg, (uint32_t)((gbase + (int64_t)y0 * a.W + half * 8) * (int64_t)sizeof(T)), 0);
+    for (int ks = 0; ks < nk; ++ks) {
+      const int ty = ks / ksteps_row, xs = ks - ty * ksteps_row;
+      const uint4 av = an;
+      if (ks + 1 < nk) {
+        const int ty2 = (ks + 1) / ksteps_row, xs2 = (ks + 1) - ty2 * ksteps_row;
+        an = bload16(rg, (uint32_t)((gbase + (int64_t)(y0 + ty2) * a.W + xs2 * 16 + half * 8) *
+                                    (int64_t)sizeof(T)), 0);
+      }
+#pragma unroll
+      for (int ky = 0; ky < 3; ++ky) {
+        // staged element index of input x' = x0 - 1 + e is PAD + x0 - 1 + e; read dwords
+        // covering [PAD + x0 - 2, PAD + x0 + 10): D3 = b32 at PAD+x0-2, D4..7 = b128 at
+        // PAD+x0, D8 = b32 at PAD+x0+8  (x0 = xs*16 + half*8, PAD = 8 keeps them aligned)
+        const T* p = s_lane + (ty + ky) * a.pitch + WG_PAD + xs * 16;
+        const uint32_t d3 = *reinterpret_cast<const uint32_t*>(p - 2);
+        const uint4 d47 = *reinterpret_cast<const uint4*>(p);
+        const uint32_t d8 = *reinterpret_cast<const uint32_t*>(p + 8);
+        // kx = 0: elements start at x0 - 1 (odd): bytes 2.. of (d3, d4, ..., d7)
+        uint4 f0, f2;
+        f0.x = __builtin_amdgcn_alignbyte(d47.x, d3, 2);
+        f0.y = __builtin_amdgcn_alignbyte(d47.y, d47.x, 2);
+        f0.z = __builtin_amdgcn_alignbyte(d47.z, d47.y, 2);
+        f0.w = __builtin_amdgcn_alignbyte(d47.w, d47.z, 2);
+        // kx = 2: elements start at x0 + 1
+        f2.x = __builtin_amdgcn_alignbyte(d47.y, d47.x, 2);
+        f2.y = __builtin_amdgcn_alignbyte(d47.z, d47.y, 2);
+        f2.z = __builtin_amdgcn_alignbyte(d47.w, d47.z, 2);
+        f2.w = __builtin_amdgcn_alignbyte(d8, d47.w, 2);
+        mfma<T>(acc[ky][0], av, f0);
+        mfma<T>(acc[ky][1], av, d47);
+        mfma<T>(acc[ky][2], av, f2);
+      }
+    }
+  }
+
+  // partials in the weight layout: part[chunk][co][ci][kz*9 + ky*3 + kx]
+  const int taps = a.KD * 9;
+#pragma unroll
+  for (int ky = 0; ky < 3; ++ky)
+#pragma unroll
+    for (int kx = 0; kx < 3; ++kx)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int co = co_base + (r >> 2) * 8 + half * 4 + (r & 3);
+        const int ci = ci_base + col;
+        a.part[(((int64_t)chunk * a.Co + co) * a.Ci + ci) * taps + kz * 9 + ky * 3 + kx] = acc[ky][kx][r];
+      }
+}
+
+__global__ __launch_bounds__(256) void conv_wgrad_reduce_kernel(WgArgs a) {
+  const int64_t total = (int64_t)a.Co * a.Ci * a.KD * 9;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  float s0 = 0.f, s1 = 0.f;
+  int c = 0;
+  for (; c + 2 <= a.chunks; c += 2) {
+    s0 += a.part[(int64_t)c * total + i];
+    s1 += a.part[(int64_t)(c + 1) * total + i];
+  }
+  if (c < a.chunks) s0 += a.part[(int64_t)c * total + i];
+  a.dw[i] = s0 + s1;
+}
+
+int wgrad_plan(int64_t N, int64_t Ci, int64_t Co, int64_t D, int64_t H, int64_t W, int KD, WgArgs* a) {
+  a->N = (int)N; a->Ci = (int)Ci; a->Co = (int)Co; a->D = (int)D; a->H = (int)H; a->W = (int)W;
+  a->KD = KD; a->pd = (KD - 1) / 2;
+  a->pitch = (int)W + 2 * WG_PAD;
+  int slab = WG_R * a->pitch;               // elements; keep the per-channel stride off a multiple
+  while (((slab / 2) & 31) != 4) slab += 8;  // of the bank count (ds_read_b128 across 32 channels)
+  a->slab = slab;
+  a->chunks16 = (int)(WG_CI * WG_R * (W / 8));
+  const int64_t groups = std::max<int64_t>(1, (Ci / WG_CI) * (Co / WG_CO) * KD);
+  const int64_t planes = N * D;
+  int64_t chunks = (512 + groups - 1) / groups;
+  if (chunks > planes) chunks = planes;
+  if (chunks < 1) chunks = 1;
+  a->planes_per_chunk = (int)((planes + chunks - 1) / chunks);
+  a->chunks = (int)((planes + a->planes_per_chunk - 1) / a->planes_per_chunk);
+  return ATK_OK;
+}
+
+}  // namespace
+}  // namespace atk
+
+extern "C" size_t atk_conv_wgrad_workspace_bytes(int64_t N, int64_t Ci, int64_t D, int64_t H, int64_t W, int64_t Co,
+                                                 int KD) {
+  using namespace atk;
+  if (N <= 0 || Ci <= 0 || Co <= 0 || D <= 0 || H <= 0 || W <= 0 || (KD != 1 && KD != 3)) return 0;
+  if (Ci % WG_CI || Co % WG_CO || W % 16 || W > WG_MAXW) return 0;  // shapes the kernel declines
+  WgArgs a{};
+  wgrad_plan(N, Ci, Co, D, H, W, KD, &a);
+  return (size_t)a.chunks * (size_t)Co * (size_t)Ci * (size_t)KD * 9 * sizeof(float);
+}
+
+extern "C" int atk_conv_wgrad(const void* x, const void* dy, float* dw, int64_t N, int64_t Ci, int64_t D, int64_t H,
+                              int64_t W, int64_t Co, int KD, int dtype, void* workspace, size_t ws_bytes,
+                              atk_stream_t stream) {
+  using namespace atk;
+  if (!x || !dy || !dw) return fail(ATK_EINVAL, "conv_wgrad: null pointer");
+  if (dtype != ATK_F16 && dtype != ATK_BF16) return fail(ATK_UNSUPPORTED, "conv_wgrad: 16-bit types only");
+  if (N <= 0 || Ci <= 0 || Co <= 0 || D <= 0 || H <= 0 || W <= 0) return fail(ATK_EINVAL, "conv_wgrad: bad sizes");
+  if (KD != 1 && KD != 3) return fail(ATK_UNSUPPORTED, "conv_wgrad: kernel depth 1 or 3");
+  if (Ci % WG_CI || Co % WG_CO || W % 16 || W > WG_MAXW)
+    return fail(ATK_UNSUPPORTED, "conv_wgrad: needs Ci %% 32, Co %% 128, W %% 16 == 0 and W <= 64");
+  if (!aligned16(x) || !aligned16(dy)) return fail(ATK_UNSUPPORTED, "conv_wgrad: 16-byte aligned tensors");
+  const int64_t xe = N * Ci * D * H * W, ge = N * Co * D * H * W;
+  if (xe * 2 >= ((int64_t)1 << 31) || ge * 2 >= ((int64_t)1 << 31))
+    return fail(ATK_UNSUPPORTED, "conv_wgrad: tensors over 2 GiB");
+  WgArgs a{};
+  wgrad_plan(N, Ci, Co, D, H, W, KD, &a);
+  if ((int64_t)WG_CI * WG_R * (W / 8) > (int64_t)WG_LD * WG_NT)
+    return fail(ATK_UNSUPPORTED, "conv_wgrad: staging map too small for W");
+  const size_t need = (size_t)a.chunks * Co * Ci * KD * 9 * sizeof(float);
+  if (!workspace || ws_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 15u))
+    return fail(ATK_EINVAL, "conv_wgrad: workspace too small or misaligned");
+  a.x = x; a.dy = dy; a.dw = dw; a.part = static_cast<float*>(workspace);
+  a.x_bytes = (uint32_t)(xe * 2);
+  a.dy_bytes = (uint32_t)(ge * 2);
+  const size_t lds = (size_t)WG_CI * a.slab * 2;
+  if (lds > 64 * 1024) return fail(ATK_UNSUPPORTED, "conv_wgrad: LDS stage too large");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  dim3 grid((unsigned)((Ci / WG_CI) * (Co / WG_CO)), (unsigned)KD, (unsigned)a.chunks);
+  if (dtype == ATK_BF16) hipLaunchKernelGGL((conv_wgrad_kernel<__bf16>), grid, dim3(WG_NT), lds, s, a);
+  else hipLaunchKernelGGL((conv_wgrad_kernel<_Float16>), grid, dim3(WG_NT), lds, s, a);
+  int rc = check_launch("conv_wgrad_kernel");
+  if (rc != ATK_OK) return rc;
+  const int64_t total = Co * Ci * KD * 9;
+  hipLaunchKernelGGL(conv_wgrad_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a);
+  return check_launch("conv_wgrad_reduce_kernel");
+}

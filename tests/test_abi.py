@@ -137,3 +137,13 @@ def test_fastdiv_exact():
     for d in divisors:
         for n in [0, 1, d - 1, d, d + 1, 2 * d - 1, (1 << 31) - 1] + [rng.randrange(1 << 31) for _ in range(2000)]:
             assert _fastdiv(n, d) == n // d, (n, d)
+
+
+def test_conv_wgrad_workspace_query_declines_unserved_shapes(nat):
+    """The size query is host arithmetic only: for channel counts the kernel does not serve
+    (Ci % 32, Co % 128) or rows it cannot stage it returns 0 instead of planning a grid."""
+    L = nat.lib()
+    assert L.atk_conv_wgrad_workspace_bytes(2, 32, 6, 16, 16, 48, 3) == 0     # Co = 48
+    assert L.atk_conv_wgrad_workspace_bytes(2, 16, 6, 16, 16, 128, 3) == 0    # Ci = 16
+    assert L.atk_conv_wgrad_workspace_bytes(1, 32, 4, 8, 80, 128, 3) == 0     # W > 64
+    assert L.atk_conv_wgrad_workspace_bytes(1, 256, 8, 64, 64, 256, 3) > 0

@@ -261,3 +261,82 @@ def test_channels_last_conv_through_patched_functional(nd, dtype):
     assert O.max_rel_err(y.float().contiguous(), ref) <= bar, won
     y2 = conv(xd, wd, bd, 1, 1)  # cached-winner path
     assert y2.is_contiguous(memory_format=fmt) and O.max_rel_err(y2.float().contiguous(), ref) <= bar
+
+
+WGRAD_CASES = [
+    # (N, Ci, Co, D, H, W, KD)
+    (1, 32, 128, 4, 8, 16, 3),
+    (2, 64, 128, 3, 5, 32, 3),     # H not a multiple of the 4-row stage
+    (1, 32, 256, 1, 8, 64, 1),     # conv2d form
+    (2, 32, 128, 2, 4, 48, 3),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("case", WGRAD_CASES)
+def test_conv_wgrad_kernel_matches_float64(case, dtype):
+    """atk_conv_wgrad against float64 aten.convolution_backward on the CPU (same quantised
+    inputs): fp32 accumulation of exact 16-bit products, bar 1e-4 of the largest entry."""
+    from amd_tuned_torch import _native
+    N, Ci, Co, D, H, W, KD = case
+    g = torch.Generator().manual_seed(Ci + Co + W)
+    x = torch.randn(N, Ci, D, H, W, generator=g).to(dtype)
+    dy = torch.randn(N, Co, D, H, W, generator=g).to(dtype)
+    dw = _native.conv_wgrad(x.cuda(), dy.cuda(), KD)
+    w = torch.zeros(Co, Ci, KD, 3, 3, dtype=torch.float64)
+    ref = torch.ops.aten.convolution_backward(dy.double(), x.double(), w, None, [1, 1, 1], [KD // 2, 1, 1],
+                                              [1, 1, 1], False, [0, 0, 0], 1, [False, True, False])[1]
+    err = O.max_rel_err(dw, ref)
+    assert err <= 1e-4, f"max_rel_err {err:.3g}"
+
+
+def test_conv_wgrad_full_size_c5a():
+    """C5a's shape (1, 256 -> 256, 8x64x64, k3) bf16 against fp32 aten on the GPU."""
+    from amd_tuned_torch import _native
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn(1, 256, 8, 64, 64, device="cuda", generator=g).to(torch.bfloat16)
+    dy = torch.randn(1, 256, 8, 64, 64, device="cuda", generator=g).to(torch.bfloat16)
+    dw = _native.conv_wgrad(x, dy, 3)
+    w = torch.zeros(256, 256, 3, 3, 3, device="cuda")
+    ref = torch.ops.aten.convolution_backward(dy.float(), x.float(), w, None, [1] * 3, [1] * 3, [1] * 3, False,
+                                              [0] * 3, 1, [False, True, False])[1]
+    assert O.max_rel_err(dw, ref) <= 1e-4
+
+
+@pytest.mark.parametrize("nd", [2, 3])
+def test_conv_autograd_native_wgrad(nd):
+    """Weight and bias gradients through patched F.conv2d / F.conv3d (bf16) come from the
+    native wgrad kernel and a reduction of dy, against float64 CPU autograd."""
+    import torch.nn.functional as F
+    from amd_tuned_torch import _native
+    calls = []
+    orig = _native.conv_wgrad
+
+    def spy(*a, **k):
+        calls.append(1)
+        return orig(*a, **k)
+    _native.conv_wgrad = spy
+    try:
+        g = torch.Generator().manual_seed(nd)
+        shape = (2, 32, 4, 8, 32) if nd == 3 else (2, 32, 16, 32)
+        x = torch.randn(*shape, generator=g).to(torch.bfloat16)
+        w = (torch.randn(128, 32, *([3] * nd), generator=g) * 0.05).to(torch.bfloat16)
+        b = (torch.randn(128, generator=g) * 0.1).to(torch.bfloat16)
+        conv = F.conv3d if nd == 3 else F.conv2d
+        xg, wg, bg = (t.cuda().requires_grad_() for t in (x, w, b))
+        y = conv(xg, wg, bg, 1, 1)
+        dy = torch.randn(y.shape, generator=g).to(torch.bfloat16)
+        y.backward(dy.cuda())
+        xr, wr, br = (t.double().requires_grad_() for t in (x, w, b))
+        import amd_tuned_torch
+        amd_tuned_torch.disable()
+        try:
+            getattr(F, "conv3d" if nd == 3 else "conv2d")(xr, wr, br, 1, 1).backward(dy.double())
+        finally:
+            amd_tuned_torch.enable()
+    finally:
+        _native.conv_wgrad = orig
+    assert calls, "native wgrad not used"
+    assert O.max_rel_err(wg.grad.float(), wr.grad) <= 1e-2
+    assert O.max_rel_err(bg.grad.float(), br.grad) <= 1e-2
+    assert O.max_rel_err(xg.grad.float(), xr.grad) <= 1e-2
