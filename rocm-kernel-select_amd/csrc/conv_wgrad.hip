@@ -9,9 +9,9 @@
 //    (8 positions of one co) is one 16-byte global load, shared by all 9 in-plane taps.
 //  * B operand (16 positions x 32 ci): for a workgroup's 32 input channels, TY+2 input rows
 //    of the plane z+kz-pd are staged in LDS with 8 zero elements on either side of each row.
-//    For 8 output positions a lane reads input elements [x0+7, x0+17) of a row (covering
-//    the kx = 0, 1, 2 shifts) as one b32 + one b128 + one b32 LDS read; the three shifted
-//    fragments are byte-aligned from those six dwords (v_alignbyte).
+//    For 8 output positions a lane needs input elements [x0-1, x0+9) of a row (covering the
+//    kx = 0, 1, 2 shifts): one b32 + one b128 + one b32 LDS read; the three shifted fragments
+//    are byte-aligned from those six dwords (v_alignbyte).
 //  * A workgroup = 4 waves = 128 output channels x 32 input channels x one kz; each wave
 //    holds 3x3 accumulator tiles (144 fp32 registers) for its 32 output channels.
 //  * The position range is split into chunks of (n, z) output planes across workgroups;
@@ -38,6 +38,7 @@ constexpr int WG_R = WG_TY + 2;
 constexpr int WG_PAD = 8;    // zero elements left / right of each staged row
 constexpr int WG_MAXW = 64;  // staging map: 32 ci x 6 rows x W / 8 chunks over 256 threads x 6 loads
 constexpr int WG_LD = 6;     // 16-byte staging loads per thread
+constexpr int WG_PF = 4;     // dy fragments in flight per lane
 
 struct WgArgs {
   const void* x;
@@ -147,41 +148,52 @@ __global__ __launch_bounds__(WG_NT, 2) void conv_wgrad_kernel(WgArgs a) {
     }
     const int zi = z + kz - a.pd;
     if (zi < 0 || zi >= a.D) continue;  // this kz tap reads only zero padding here (uniform)
-    const int64_t gbase = ((int64_t)n * a.Co + co_base + col) * plane_x + (int64_t)z * HW;
+    // a stage covers whole output rows, so k-step ks (16 positions) starts at position
+    // y0*W + ks*16 of the plane: the dy offset is linear in ks
+    const uint32_t g0 = (uint32_t)((((int64_t)n * a.Co + co_base + col) * plane_x + (int64_t)z * HW +
+                                    (int64_t)y0 * a.W + half * 8) * (int64_t)sizeof(T));
     const int rows = min(WG_TY, a.H - y0);
     const int nk = rows * ksteps_row;
-    uint4 an = bload16(rg, (uint32_t)((gbase + (int64_t)y0 * a.W + half * 8) * (int64_t)sizeof(T)), 0);
-    for (int ks = 0; ks < nk; ++ks) {
-      const int ty = ks / ksteps_row, xs = ks - ty * ksteps_row;
-      const uint4 av = an;
-      if (ks + 1 < nk) {
-        const int ty2 = (ks + 1) / ksteps_row, xs2 = (ks + 1) - ty2 * ksteps_row;
-        an = bload16(rg, (uint32_t)((gbase + (int64_t)(y0 + ty2) * a.W + xs2 * 16 + half * 8) *
-                                    (int64_t)sizeof(T)), 0);
-      }
+    uint4 ar[WG_PF];  // dy fragments stream through a ring, WG_PF k-steps ahead
 #pragma unroll
-      for (int ky = 0; ky < 3; ++ky) {
-        // staged element index of input x' = x0 - 1 + e is PAD + x0 - 1 + e; read dwords
-        // covering [PAD + x0 - 2, PAD + x0 + 10): D3 = b32 at PAD+x0-2, D4..7 = b128 at
-        // PAD+x0, D8 = b32 at PAD+x0+8  (x0 = xs*16 + half*8, PAD = 8 keeps them aligned)
-        const T* p = s_lane + (ty + ky) * a.pitch + WG_PAD + xs * 16;
-        const uint32_t d3 = *reinterpret_cast<const uint32_t*>(p - 2);
-        const uint4 d47 = *reinterpret_cast<const uint4*>(p);
-        const uint32_t d8 = *reinterpret_cast<const uint32_t*>(p + 8);
-        // kx = 0: elements start at x0 - 1 (odd): bytes 2.. of (d3, d4, ..., d7)
-        uint4 f0, f2;
-        f0.x = __builtin_amdgcn_alignbyte(d47.x, d3, 2);
-        f0.y = __builtin_amdgcn_alignbyte(d47.y, d47.x, 2);
-        f0.z = __builtin_amdgcn_alignbyte(d47.z, d47.y, 2);
-        f0.w = __builtin_amdgcn_alignbyte(d47.w, d47.z, 2);
-        // kx = 2: elements start at x0 + 1
-        f2.x = __builtin_amdgcn_alignbyte(d47.y, d47.x, 2);
-        f2.y = __builtin_amdgcn_alignbyte(d47.z, d47.y, 2);
-        f2.z = __builtin_amdgcn_alignbyte(d47.w, d47.z, 2);
-        f2.w = __builtin_amdgcn_alignbyte(d8, d47.w, 2);
-        mfma<T>(acc[ky][0], av, f0);
-        mfma<T>(acc[ky][1], av, d47);
-        mfma<T>(acc[ky][2], av, f2);
+    for (int u = 0; u < WG_PF; ++u) ar[u] = bload16(rg, u < nk ? g0 + (uint32_t)u * 32u : kOOB, 0);
+    int xs = 0;                   // 16-position column block of the current k-step
+    const T* prow = s_lane + WG_PAD;  // staged row ty (+ ky below) of the current k-step
+    for (int ks0 = 0; ks0 < nk; ks0 += WG_PF) {
+#pragma unroll
+      for (int u = 0; u < WG_PF; ++u) {
+        const int ks = ks0 + u;
+        if (ks >= nk) break;
+        const uint4 av = ar[u];
+        ar[u] = bload16(rg, ks + WG_PF < nk ? g0 + (uint32_t)(ks + WG_PF) * 32u : kOOB, 0);
+#pragma unroll
+        for (int ky = 0; ky < 3; ++ky) {
+          // staged element index of input x' = x0 - 1 + e is PAD + x0 - 1 + e; read dwords
+          // covering [PAD + x0 - 2, PAD + x0 + 10): D3 = b32 at PAD+x0-2, D4..7 = b128 at
+          // PAD+x0, D8 = b32 at PAD+x0+8  (x0 = xs*16 + half*8, PAD = 8 keeps them aligned)
+          const T* p = prow + ky * a.pitch + xs * 16;
+          const uint32_t d3 = *reinterpret_cast<const uint32_t*>(p - 2);
+          const uint4 d47 = *reinterpret_cast<const uint4*>(p);
+          const uint32_t d8 = *reinterpret_cast<const uint32_t*>(p + 8);
+          // kx = 0: elements start at x0 - 1 (odd): bytes 2.. of (d3, d4, ..., d7)
+          uint4 f0, f2;
+          f0.x = __builtin_amdgcn_alignbyte(d47.x, d3, 2);
+          f0.y = __builtin_amdgcn_alignbyte(d47.y, d47.x, 2);
+          f0.z = __builtin_amdgcn_alignbyte(d47.z, d47.y, 2);
+          f0.w = __builtin_amdgcn_alignbyte(d47.w, d47.z, 2);
+          // kx = 2: elements start at x0 + 1
+          f2.x = __builtin_amdgcn_alignbyte(d47.y, d47.x, 2);
+          f2.y = __builtin_amdgcn_alignbyte(d47.z, d47.y, 2);
+          f2.z = __builtin_amdgcn_alignbyte(d47.w, d47.z, 2);
+          f2.w = __builtin_amdgcn_alignbyte(d8, d47.w, 2);
+          mfma<T>(acc[ky][0], av, f0);
+          mfma<T>(acc[ky][1], av, d47);
+          mfma<T>(acc[ky][2], av, f2);
+        }
+        if (++xs == ksteps_row) {
+          xs = 0;
+          prow += a.pitch;
+        }
       }
     }
   }
