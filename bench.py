@@ -227,25 +227,34 @@ def bench_dw_cl_detail(dev, silu=False):
         y = orig(xx, ww.unsqueeze(1), bb, 1, K - 1, 1, D)[..., :L]
         return F.silu(y) if silu else y
     y = causal_conv1d_fn(x, w, b, activation=act)
-    err = max_rel_err(y, stock(x.float(), w.float(), b.float()))
+    # the fp32 stock reference on two batch rows (a full-size fp32 copy is 1 GiB per tensor)
+    err = max_rel_err(y[:2], stock(x[:2].float(), w.float(), b.float()))
     del y
     ms = graph_time_ms(lambda: causal_conv1d_fn(x, w, b, activation=act), 10)
-    stock_ms = event_time_ms(lambda: stock(x, w, b), 3)
+
+    def stock_time(fn, iters):
+        # MIOpen has failed here on channel-last tensors ("No invoker was registered"): a
+        # stock failure leaves its timing null instead of dropping the native numbers
+        try:
+            return round(event_time_ms(fn, iters), 3)
+        except RuntimeError:
+            return None
+    stock_ms = stock_time(lambda: stock(x, w, b), 3)
     xv, gv = x.transpose(1, 2), dy.transpose(1, 2)
     dx = torch.empty_like(xv)
     bwd = lambda: nat.causal_conv1d_cl_bwd(xv, gv, w, b, silu=silu, dx=dx)
     bwd()
     bms = graph_time_ms(bwd, 10)
     xp = F.pad(x, (K - 1, 0))
-    stock_bms = event_time_ms(lambda: torch.ops.aten.convolution_backward(
+    stock_bms = stock_time(lambda: torch.ops.aten.convolution_backward(
         dy, xp, w.unsqueeze(1), [D], [1], [0], [1], False, [0], D, [True, True, True]), 2)
     n = B * D * L * x.element_size()
     fgbs = 2 * n / (ms * 1e-3) / 1e9
     bgbs = 3 * n / (bms * 1e-3) / 1e9
     return {"fwd_ms": round(ms, 4), "fwd_GB/s": round(fgbs, 1), "fwd_roofline_frac": round(fgbs / HBM_PEAK_GBS, 4),
-            "stock_fwd_ms": round(stock_ms, 3), "fwd_max_rel_err_vs_stock_fp32": float(f"{err:.3g}"),
+            "stock_fwd_ms": stock_ms, "fwd_max_rel_err_vs_stock_fp32": float(f"{err:.3g}"),
             "bwd_ms": round(bms, 4), "bwd_GB/s": round(bgbs, 1), "bwd_roofline_frac": round(bgbs / HBM_PEAK_GBS, 4),
-            "stock_convolution_backward_ms": round(stock_bms, 3),
+            "stock_convolution_backward_ms": stock_bms,
             "variant": "dwconv1d_cl_kernel / dwconv1d_cl_causal_bwd_kernel"}
 
 
