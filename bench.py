@@ -3,7 +3,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-details] [--no-cpu]
     python bench.py --traffic-probe [--variant V]          # workload of the counter passes
     python bench.py --summarize-traffic FETCH_DIR WRITE_DIR [--variant V] [--command C]
-    python bench.py --summarize-stats STATS_DIR OUT.txt [--command C]
+    python bench.py --summarize-stats STATS_DIR OUT.txt [--command C] [--summarize-filter atk]
 
 Headline workload (config 2): causal depthwise conv1d
 (Mamba-style) through the patched torch.nn.functional API,
@@ -680,14 +680,18 @@ def _summarize_traffic_one(fetch_dir: str, write_dir: str, variant: str, command
     print("\n".join(lines))
 
 
-def summarize_stats(stats_dir: str, out_path: str, command: str, top: int = 25):
+def summarize_stats(stats_dir: str, out_path: str, command: str, top: int = 25, name_filter: str = ""):
     """Write a rocprofv3 --kernel-trace --stats summary (per-kernel calls, average, min,
-    max duration, share of GPU time) as a short text file."""
+    max duration, share of GPU time) as a short text file; with `name_filter`, only the
+    kernels whose names contain it (all of them, not just the top ones)."""
     import csv
     import glob
     rows = []
     for f in glob.glob(os.path.join(stats_dir, "**", "*kernel_stats.csv"), recursive=True):
         rows += list(csv.DictReader(open(f)))
+    if name_filter:
+        rows = [r for r in rows if name_filter in r["Name"]]
+        top = len(rows)
     rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
     lines = [f"# rocprofv3 --kernel-trace --stats summary", f"# command: {command}",
              f"# {'calls':>6} {'avg_us':>10} {'min_us':>10} {'max_us':>10} {'pct':>6}  kernel"]
@@ -723,6 +727,8 @@ def main():
                     help="run only the workload of the FETCH_SIZE/WRITE_SIZE counter passes")
     ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="write the traffic summary from two rocprofv3 --pmc output folders")
+    ap.add_argument("--summarize-filter", default="",
+                    help="with --summarize-stats: keep only kernels whose names contain this")
     ap.add_argument("--summarize-stats", nargs=2, metavar=("STATS_DIR", "OUT"),
                     help="write a text summary of a rocprofv3 --kernel-trace --stats folder")
     ap.add_argument("--variant", default="xlane,lds_opt32_nt",
@@ -730,7 +736,7 @@ def main():
     ap.add_argument("--command", default="", help="command line recorded by --summarize-traffic")
     args = ap.parse_args()
     if args.summarize_stats:
-        summarize_stats(*args.summarize_stats, args.command)
+        summarize_stats(*args.summarize_stats, args.command, name_filter=args.summarize_filter)
         return
     if args.summarize_traffic:
         summarize_traffic(*args.summarize_traffic, args.variant, args.command)

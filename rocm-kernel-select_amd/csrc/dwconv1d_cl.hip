@@ -345,25 +345,35 @@ __global__ __launch_bounds__(CL_NT) void dwconv1d_cl_bwd_w_kernel(DwClBwArgs a) 
     *reinterpret_cast<float4*>(pp + (size_t)KT * a.D + v) = make_float4(accb[v], accb[v + 1], accb[v + 2], accb[v + 3]);
 }
 
-// Sum the P partial rows of each (tap, channel) in a fixed order.
-__global__ __launch_bounds__(CL_NT) void dwconv1d_cl_bwd_finalize_kernel(DwClBwArgs a, int K) {
-  const uint32_t i = blockIdx.x * CL_NT + threadIdx.x;  // over (K + 1) * D
-  if (i >= (uint32_t)(K + 1) * a.D) return;
-  const uint32_t j = i / a.D, c = i - j * a.D;
-  const size_t stride = (size_t)(K + 1) * a.D;
-  const float* p = a.part + i;
-  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-  uint32_t q = 0;
-  for (; q + 4 <= a.P; q += 4) {
-    s0 += p[(size_t)q * stride];
-    s1 += p[(size_t)(q + 1) * stride];
-    s2 += p[(size_t)(q + 2) * stride];
-    s3 += p[(size_t)(q + 3) * stride];
+// Sum the P partial rows of each (tap, channel) in a fixed order: a block covers CLF_COLS
+// columns, CLF_SPLIT threads per column each sum every CLF_SPLIT-th row, and the CLF_SPLIT
+// sums are added in order through LDS (deterministic for a given P).
+constexpr int CLF_COLS = 32, CLF_SPLIT = 8;
+__global__ __launch_bounds__(CLF_COLS * CLF_SPLIT) void dwconv1d_cl_bwd_finalize_kernel(DwClBwArgs a, int K) {
+  __shared__ float red[CLF_SPLIT][CLF_COLS];
+  const int tx = threadIdx.x % CLF_COLS, ty = threadIdx.x / CLF_COLS;
+  const uint32_t ncol = (uint32_t)(K + 1) * a.D;
+  const uint32_t i = blockIdx.x * CLF_COLS + tx;  // column: (tap or bias row) * D + channel
+  float s0 = 0.f, s1 = 0.f;
+  if (i < ncol) {
+    const float* p = a.part + i;
+    uint32_t q = ty;
+    for (; q + CLF_SPLIT < a.P; q += 2 * CLF_SPLIT) {
+      s0 += p[(size_t)q * ncol];
+      s1 += p[(size_t)(q + CLF_SPLIT) * ncol];
+    }
+    if (q < a.P) s0 += p[(size_t)q * ncol];
   }
-  for (; q < a.P; ++q) s0 += p[(size_t)q * stride];
-  const float s = (s0 + s1) + (s2 + s3);
-  if (j < (uint32_t)K) a.dw[(size_t)c * K + j] = s;
-  else if (a.db) a.db[c] = s;
+  red[ty][tx] = s0 + s1;
+  __syncthreads();
+  if (ty == 0 && i < ncol) {
+    float s = 0.f;
+#pragma unroll
+    for (int t = 0; t < CLF_SPLIT; ++t) s += red[t][tx];
+    const uint32_t j = i / a.D, c = i - j * a.D;
+    if (j < (uint32_t)K) a.dw[(size_t)c * K + j] = s;
+    else if (a.db) a.db[c] = s;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -830,8 +840,8 @@ extern "C" int atk_dwconv1d_cl_bwd_weight(const void* x, const void* dy, const i
   else if (dtype == ATK_F16) rc = launch_clw<_Float16>(a, K, blocks, seq_mode, s);
   else rc = launch_clw<__bf16>(a, K, blocks, seq_mode, s);
   if (rc != ATK_OK) return fail(rc, "dwconv1d_cl_bwd_weight: kernel width not served");
-  const uint32_t fblocks = (uint32_t)(((K + 1) * D + CL_NT - 1) / CL_NT);
-  hipLaunchKernelGGL(dwconv1d_cl_bwd_finalize_kernel, dim3(fblocks), dim3(CL_NT), 0, s, a, K);
+  const uint32_t fblocks = (uint32_t)(((K + 1) * D + CLF_COLS - 1) / CLF_COLS);
+  hipLaunchKernelGGL(dwconv1d_cl_bwd_finalize_kernel, dim3(fblocks), dim3(CLF_COLS * CLF_SPLIT), 0, s, a, K);
   return check_launch("dwconv1d_cl_bwd_weight");
 }
 
@@ -894,7 +904,7 @@ extern "C" int atk_causal_conv1d_cl_bwd(const void* x, const void* dout, const v
   if (rc != ATK_OK) return fail(rc, "causal_conv1d_cl_bwd: kernel width not served");
   DwClBwArgs f{};
   f.D = (uint32_t)D; f.part = a.part; f.dw = dw; f.db = db; f.P = (uint32_t)(B * a.nspan);
-  const uint32_t fblocks = (uint32_t)(((K + 1) * D + CL_NT - 1) / CL_NT);
-  hipLaunchKernelGGL(dwconv1d_cl_bwd_finalize_kernel, dim3(fblocks), dim3(CL_NT), 0, s, f, K);
+  const uint32_t fblocks = (uint32_t)(((K + 1) * D + CLF_COLS - 1) / CLF_COLS);
+  hipLaunchKernelGGL(dwconv1d_cl_bwd_finalize_kernel, dim3(fblocks), dim3(CLF_COLS * CLF_SPLIT), 0, s, f, K);
   return check_launch("causal_conv1d_cl_bwd");
 }
