@@ -45,7 +45,10 @@ def _stock_forward_blh(input_, weight, bias, padding: int):
     if w.dtype != input_.dtype:
         w = w.to(input_.dtype)
     b = bias.to(input_.dtype) if bias is not None else None
-    y = torch.nn.functional.conv1d(input_.transpose(1, 2), w, b, padding=padding, groups=C)
+    # the original F.conv1d: the patched one would route this channel-last view back here
+    from . import miopen_fallback
+    conv1d = miopen_fallback._original_conv1d or torch.nn.functional.conv1d
+    y = conv1d(input_.transpose(1, 2), w, b, 1, padding, 1, C)
     return y.transpose(1, 2).contiguous()
 
 

@@ -252,9 +252,47 @@ def _try_depthwise_fastpath(input, weight, bias, stride, padding, dilation, grou
         return None
 
 
+def _is_channel_last(x) -> bool:
+    """(B, D, L) with unit channel stride: the layout causal_conv1d_fn treats as channel-last
+    (src/causal-conv1d-amd/csrc/causal_conv1d.cpp:156)."""
+    return isinstance(x, torch.Tensor) and x.dim() == 3 and x.stride(1) == 1 and x.stride(2) > 1
+
+
+def _try_channel_last_fastpath(input, weight, bias, stride, padding, dilation, groups):
+    """Depthwise conv1d on a channel-last x: the channels-last kernel through the BLH op on
+    transposed views (native forward and backward), output in the same channel-last layout
+    causal_conv1d_fn returns.  None (-> stock) outside that kernel's shapes."""
+    if not (_native.available() and _is_channel_last(input) and input.is_cuda
+            and _depthwise_shape_ok(input, weight, stride, dilation, groups)
+            and all(_is_plain_tensor(t) for t in (input, weight, bias))
+            and input.dtype in _DTYPES and weight.dtype == input.dtype
+            and (bias is None or (bias.is_cuda and bias.dtype == input.dtype))):
+        return None
+    if isinstance(padding, str):
+        return None
+    r = _resolve_padding(padding, weight.shape[2], input.shape[2])
+    if r is None or r[1] <= 0:
+        return None
+    pad = r[0]
+    D = input.shape[1]
+    w_kd = weight.squeeze(1).t()  # [K, D], the BLH weight layout
+    b = bias if bias is not None else torch.zeros(D, dtype=input.dtype, device=input.device)
+    try:
+        if _grad_safe(input, weight, bias):
+            y = depthwise_conv1d_ops.conv1d_forward(input.transpose(1, 2), w_kd, b, pad, False)
+        else:
+            y = depthwise_conv1d_ops.DepthwiseConv1dFn.apply(input.transpose(1, 2), w_kd, b, pad, False)
+    except _native.Unsupported:
+        return None
+    return y.transpose(1, 2)
+
+
 def _miopen_safe_conv(op_name: str, orig_fn: Callable) -> Callable:
     def wrapped(input, weight, bias=None, stride=1, padding=0, dilation=1, groups=1):
         out = _try_causal_conv1d_fastpath(input, weight, bias, stride, padding, dilation, groups)
+        if out is not None:
+            return out
+        out = _try_channel_last_fastpath(input, weight, bias, stride, padding, dilation, groups)
         if out is not None:
             return out
         out = _try_depthwise_fastpath(input, weight, bias, stride, padding, dilation, groups,

@@ -242,3 +242,31 @@ def test_causal_channel_last_full_size_matches_bcl_kernel():
     assert O.max_rel_err(br.grad, db_ref) <= 1e-4
     del x_cl, y, y_ref, xr, out, dy, dyc, dx_ref
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("K,pad", [(4, 3), (3, 1), (5, 0)])
+def test_fconv1d_on_channel_last_input_takes_the_channels_last_kernel(K, pad, dtype):
+    """Patched F.conv1d on a channel-last x (sliced like the reference test's inputs): the
+    depthwise call runs the channels-last kernel (output returned channel-last, like
+    causal_conv1d_fn's) and its backward; values and gradients match the oracle."""
+    import torch.nn.functional as F
+    import amd_tuned_torch  # noqa: F401
+    B, D, L = 2, 64, 300
+    g = torch.Generator(device="cuda").manual_seed(K * 10 + pad)
+    big = torch.randn(B, L, D + 64, device="cuda", generator=g).to(dtype)
+    x = big[:, :, 32:32 + D].transpose(1, 2)
+    w = (torch.randn(D, 1, K, device="cuda", generator=g) / K ** 0.5).to(dtype)
+    b = (torch.randn(D, device="cuda", generator=g) * 0.3).to(dtype)
+    l_out = L + 2 * pad - K + 1
+    y = F.conv1d(x, w, b, padding=pad, groups=D)
+    assert y.shape == (B, D, l_out) and y.stride(1) == 1, "not the channels-last route"
+    _close(y, O.dwconv1d(x, w, b, pad, l_out), dtype, "F.conv1d channel-last forward")
+    xg, wg, bg = (t.detach().requires_grad_() for t in (x, w, b))
+    yg = F.conv1d(xg, wg, bg, padding=pad, groups=D)
+    dy = torch.randn(yg.shape, device="cuda", generator=g).to(dtype)
+    yg.backward(dy)
+    dx, dw, db = O.dwconv1d_bwd(x, w, dy, pad)
+    _close(xg.grad, dx, dtype, "F.conv1d channel-last dx")
+    _grad_close(wg.grad.reshape(D, K), dw, "dweight", 1e-5 if dtype == torch.float32 else 1e-2)
+    _grad_close(bg.grad, db, "dbias", 1e-5 if dtype == torch.float32 else 1e-2)
