@@ -825,12 +825,14 @@ int launch_gn_bwd(const GnBwdArgs& a, int64_t rows, hipStream_t s) {
 //          of the NC[S] kernels) into (mean, rstd);
 //   apply: a workgroup per (n, chunk) stages per-channel scale / shift in LDS and
 //          normalises its chunk (+ SiLU).
-// Requires C / VEC to divide the workgroup size (C <= 2048 for 16-bit types) and 16-byte
-// aligned x / y (host check).  Traffic: x read twice (the second read mostly from the
-// Infinity Cache), y written once.
+// Requires C / VEC to divide the workgroup size (C <= 2048 for 16-bit types), 16-byte
+// aligned x / y and samples under 2 GiB (host check).  Traffic: x read twice (the second
+// read mostly from the Infinity Cache), y written once.  Both streaming kernels keep
+// GN_CL_U rows of loads in flight per thread.
 constexpr int GN_CL_NT = 256;
 constexpr int GN_CL_MAXC = 2048;
 constexpr int GN_CL_MAXG = 256;
+constexpr int GN_CL_U = 8;  // rows in flight per thread
 
 struct GnClArgs {
   const void* x;
@@ -840,6 +842,7 @@ struct GnClArgs {
   float* part;        // [N][NCH][G][2] (mean, M2) of each chunk's slice of each group
   float* stat;        // [N][G][2] (mean, rstd)
   int64_t S, SC;      // spatial positions, positions per chunk
+  uint32_t sample_bytes;  // bytes of one sample (buffer-load range; host checks < 2 GiB)
   uint32_t C, G, cpg;
   int NCH;
   float eps;
@@ -855,18 +858,30 @@ __global__ __launch_bounds__(GN_CL_NT) void gn_cl_stats_kernel(GnClArgs a) {
   const int v = threadIdx.x % CV, rr = threadIdx.x / CV;
   const int64_t s0 = (int64_t)ch * a.SC, s1 = min(a.S, s0 + a.SC);
   const T* __restrict__ xn = static_cast<const T*>(a.x) + (int64_t)n * a.S * a.C + v * VEC;
+  // GN_CL_U rows per batch as branch-free buffer loads (rows past the chunk read zero and are
+  // masked out of the sums), so a thread has GN_CL_U loads in flight instead of one
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(static_cast<const T*>(a.x) + (int64_t)n * a.S * a.C, a.sample_bytes);
+  const uint32_t vb = (uint32_t)(v * VEC * sizeof(T)), rowb = (uint32_t)(a.C * sizeof(T));
   float K = 0.f, t1 = 0.f, t2 = 0.f, cnt = 0.f;
   if (s0 + rr < s1) K = to_f32(xn[(s0 + rr) * a.C]);
-  for (int64_t s = s0 + rr; s < s1; s += R) {
-    Vec16<T> xv;
-    xv.raw = ld16<false>(xn + s * a.C);  // cached: the apply kernel reads x again
+  for (int64_t s = s0 + rr; s < s1; s += (int64_t)R * GN_CL_U) {
+    Vec16<T> xv[GN_CL_U];
 #pragma unroll
-    for (int k = 0; k < VEC; ++k) {
-      const float d = to_f32(xv.e[k]) - K;
-      t1 += d;
-      t2 = fmaf(d, d, t2);
+    for (int u = 0; u < GN_CL_U; ++u) {
+      const int64_t sp = s + (int64_t)u * R;
+      xv[u].raw = bload16(rx, sp < s1 ? (uint32_t)sp * rowb + vb : kOOB, 0);  // cached: x is read again
     }
-    cnt += (float)VEC;
+#pragma unroll
+    for (int u = 0; u < GN_CL_U; ++u) {
+      const float m = (s + (int64_t)u * R < s1) ? 1.f : 0.f;
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) {
+        const float d = (to_f32(xv[u].e[k]) - K) * m;
+        t1 += d;
+        t2 = fmaf(d, d, t2);
+      }
+      cnt += m * (float)VEC;
+    }
   }
   float mean_t = 0.f, m2_t = 0.f;
   if (cnt > 0.f) {
@@ -948,16 +963,27 @@ __global__ __launch_bounds__(GN_CL_NT) void gn_cl_apply_kernel(GnClArgs a) {
     sc[k] = scs[v * VEC + k];
     sh[k] = shs[v * VEC + k];
   }
-  for (int64_t s = s0 + rr; s < s1; s += R) {
-    Vec16<T> xv;
-    xv.raw = ld16<true>(xn + s * a.C);
-    float o[VEC];
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(static_cast<const T*>(a.x) + (int64_t)n * a.S * a.C, a.sample_bytes);
+  const uint32_t vb = (uint32_t)(v * VEC * sizeof(T)), rowb = (uint32_t)(a.C * sizeof(T));
+  (void)xn;
+  for (int64_t s = s0 + rr; s < s1; s += (int64_t)R * GN_CL_U) {
+    Vec16<T> xv[GN_CL_U];
 #pragma unroll
-    for (int k = 0; k < VEC; ++k) {
-      o[k] = fmaf(to_f32(xv.e[k]), sc[k], sh[k]);
-      if constexpr (SILU) o[k] = silu_f32(o[k]);
+    for (int u = 0; u < GN_CL_U; ++u) {
+      const int64_t sp = s + (int64_t)u * R;
+      xv[u].raw = bload16<2>(rx, sp < s1 ? (uint32_t)sp * rowb + vb : kOOB, 0);  // last read of x
     }
-    st16<true>(yn + s * a.C, pack16<T>(o));
+#pragma unroll
+    for (int u = 0; u < GN_CL_U; ++u) {
+      const int64_t sp = s + (int64_t)u * R;
+      float o[VEC];
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) {
+        o[k] = fmaf(to_f32(xv[u].e[k]), sc[k], sh[k]);
+        if constexpr (SILU) o[k] = silu_f32(o[k]);
+      }
+      if (sp < s1) st16<true>(yn + sp * a.C, pack16<T>(o));
+    }
   }
 }
 
@@ -1132,6 +1158,8 @@ extern "C" int atk_group_norm_cl_fwd(const void* x, const void* gamma, const voi
     return fail(ATK_UNSUPPORTED, "group_norm (channels-last): needs C/G %% %lld == 0, C/%lld dividing %d and "
                 "16-byte aligned tensors", (long long)vec, (long long)vec, GN_CL_NT);
   if (N >= 65536) return fail(ATK_UNSUPPORTED, "group_norm (channels-last): batch too large");
+  if (S * C * es >= ((int64_t)1 << 31))
+    return fail(ATK_UNSUPPORTED, "group_norm (channels-last): one sample over 2 GiB (32-bit buffer offsets)");
   const GnClPlan p = plan_gn_cl(N, S);
   const size_t need = ((size_t)N * (size_t)p.NCH + (size_t)N) * (size_t)G * 2 * sizeof(float);
   if (!workspace || ws_bytes < need)
@@ -1141,6 +1169,7 @@ extern "C" int atk_group_norm_cl_fwd(const void* x, const void* gamma, const voi
   a.part = static_cast<float*>(workspace);
   a.stat = a.part + (size_t)N * p.NCH * G * 2;
   a.S = S; a.SC = p.SC; a.NCH = p.NCH;
+  a.sample_bytes = (uint32_t)(S * C * es);
   a.C = (uint32_t)C; a.G = (uint32_t)G; a.cpg = (uint32_t)cpg;
   a.eps = eps; a.pdt = param_dtype;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
