@@ -52,6 +52,7 @@ constexpr size_t GN_SLOTS_OFF = 256 + 8 * (size_t)GN_MAX_SLOTTED;
 constexpr size_t GN_ZERO_BYTES = GN_SLOTS_OFF + 16 * (size_t)GN_MAX_SLOTS;
 constexpr size_t GN_PARTIALS_OFF = GN_ZERO_BYTES;
 constexpr int GN_TP_NT = 256;                 // two-pass kernels
+constexpr int GN_BWD_U = 4;                   // backward: vectors of x and dy in flight per thread
 constexpr int GN_MAX_AFF = 512;               // channels per slice whose affine is staged in LDS
 
 // One slot = two 64-bit words (1 << 32 | bits(mean)), (1 << 32 | bits(M2)), each stored
@@ -698,18 +699,31 @@ __global__ __launch_bounds__(GN_TP_NT) void gn_bwd_rows_kernel(GnBwdArgs a) {
   const T* __restrict__ gr = static_cast<const T*>(a.dy) + r * a.S;
   const float K = to_f32(xr[0]);
   float s1 = 0.f, s2 = 0.f, sa = 0.f, sb = 0.f;
-  for (int64_t e = (int64_t)threadIdx.x * VEC; e < a.S; e += (int64_t)GN_TP_NT * VEC) {
-    Vec16<T> xv, gv;
-    xv.raw = ld16<false>(xr + e);  // cached: the apply kernel reads x and dy again
-    gv.raw = ld16<false>(gr + e);
+  // GN_BWD_U vectors of x and of dy in flight per thread (branch-free buffer loads; vectors
+  // past the row read zero and are masked out of the sums)
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(xr, (uint32_t)(a.S * (int64_t)sizeof(T)));
+  const __amdgpu_buffer_rsrc_t rg = make_rsrc(gr, (uint32_t)(a.S * (int64_t)sizeof(T)));
+  for (int64_t e0 = (int64_t)threadIdx.x * VEC; e0 < a.S; e0 += (int64_t)GN_TP_NT * VEC * GN_BWD_U) {
+    Vec16<T> xv[GN_BWD_U], gv[GN_BWD_U];
 #pragma unroll
-    for (int k = 0; k < VEC; ++k) {
-      const float d = to_f32(xv.e[k]) - K;
-      const float g = to_f32(gv.e[k]);
-      s1 += d;
-      s2 = fmaf(d, d, s2);
-      sa += g;
-      sb = fmaf(g, d, sb);
+    for (int u = 0; u < GN_BWD_U; ++u) {
+      const int64_t e = e0 + (int64_t)u * GN_TP_NT * VEC;
+      const uint32_t off = e < a.S ? (uint32_t)(e * (int64_t)sizeof(T)) : kOOB;
+      xv[u].raw = bload16(rx, off, 0);  // cached: the apply kernel reads x and dy again
+      gv[u].raw = bload16(rg, off, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < GN_BWD_U; ++u) {
+      const float m = (e0 + (int64_t)u * GN_TP_NT * VEC < a.S) ? 1.f : 0.f;
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) {
+        const float d = (to_f32(xv[u].e[k]) - K) * m;
+        const float g = to_f32(gv[u].e[k]);
+        s1 += d;
+        s2 = fmaf(d, d, s2);
+        sa += g;
+        sb = fmaf(g, d, sb);
+      }
     }
   }
   s1 = block_sum<GN_TP_NT>(s1, red);
@@ -772,17 +786,28 @@ __global__ __launch_bounds__(GN_TP_NT) void gn_bwd_apply_kernel(GnBwdArgs a) {
   const T* __restrict__ xr = static_cast<const T*>(a.x) + r * a.S;
   const T* __restrict__ gr = static_cast<const T*>(a.dy) + r * a.S;
   T* __restrict__ dxr = static_cast<T*>(a.dx) + r * a.S;
-  for (int64_t e = (int64_t)threadIdx.x * VEC; e < a.S; e += (int64_t)GN_TP_NT * VEC) {
-    Vec16<T> xv, gv;
-    xv.raw = ld16<true>(xr + e);
-    gv.raw = ld16<true>(gr + e);
-    float o[VEC];
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(xr, (uint32_t)(a.S * (int64_t)sizeof(T)));
+  const __amdgpu_buffer_rsrc_t rg = make_rsrc(gr, (uint32_t)(a.S * (int64_t)sizeof(T)));
+  for (int64_t e0 = (int64_t)threadIdx.x * VEC; e0 < a.S; e0 += (int64_t)GN_TP_NT * VEC * GN_BWD_U) {
+    Vec16<T> xv[GN_BWD_U], gv[GN_BWD_U];
 #pragma unroll
-    for (int k = 0; k < VEC; ++k) {
-      const float xh = (to_f32(xv.e[k]) - mu) * rstd;
-      o[k] = rstd * (fmaf(gam, to_f32(gv.e[k]), -c1) - xh * c2);
+    for (int u = 0; u < GN_BWD_U; ++u) {
+      const int64_t e = e0 + (int64_t)u * GN_TP_NT * VEC;
+      const uint32_t off = e < a.S ? (uint32_t)(e * (int64_t)sizeof(T)) : kOOB;
+      xv[u].raw = bload16<2>(rx, off, 0);  // last reads of x and dy
+      gv[u].raw = bload16<2>(rg, off, 0);
     }
-    st16<true>(dxr + e, pack16<T>(o));
+#pragma unroll
+    for (int u = 0; u < GN_BWD_U; ++u) {
+      const int64_t e = e0 + (int64_t)u * GN_TP_NT * VEC;
+      float o[VEC];
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) {
+        const float xh = (to_f32(xv[u].e[k]) - mu) * rstd;
+        o[k] = rstd * (fmaf(gam, to_f32(gv[u].e[k]), -c1) - xh * c2);
+      }
+      if (e < a.S) st16<true>(dxr + e, pack16<T>(o));
+    }
   }
 }
 
@@ -1120,6 +1145,7 @@ extern "C" int atk_group_norm_bwd(const void* x, const void* dy, const void* gam
   const int64_t rows = N * C;
   if (rows >= (1ll << 31) || C >= (1ll << 31) || N >= (1ll << 31))
     return fail(ATK_UNSUPPORTED, "group_norm backward: too many rows");
+  if (S * es >= (1ll << 31)) return fail(ATK_UNSUPPORTED, "group_norm backward: rows over 2 GiB (32-bit buffer offsets)");
   GnBwdArgs a;
   a.x = x; a.dy = dy; a.gamma = gamma; a.dx = dx;
   a.rows = static_cast<float*>(workspace);
