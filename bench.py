@@ -349,6 +349,40 @@ def bench_vae_block_detail(dev):
             "variant": type(m).__name__, "max_rel_err_vs_stock_fp32": float(f"{err:.3g}")}
 
 
+def bench_causal_silu_backward_detail(dev):
+    """Config 2 (B=16, D=2048, L=8192, k=4, bf16, (B, C, L) layout) through causal_conv1d_fn
+    with activation='silu', forward + backward (dx, dweight, dbias), against stock autograd of
+    the same function (F.conv1d + F.silu) on the same tensors."""
+    import torch
+    import torch.nn.functional as F
+    import amd_tuned_torch
+    from amd_tuned_torch.causal_conv1d import causal_conv1d_fn
+    x, w3, b = c2_inputs(torch.bfloat16, 4, dev)
+    w = w3.squeeze(1).contiguous()
+    L = x.shape[-1]
+    dy = torch.randn(x.shape, generator=_gen(1015)).to(torch.bfloat16).to(dev)
+    xg, wg, bg = (t.detach().requires_grad_() for t in (x, w, b))
+    orig = amd_tuned_torch.miopen_fallback._original_conv1d
+
+    def native():
+        xg.grad = wg.grad = bg.grad = None
+        causal_conv1d_fn(xg, wg, bg, activation="silu").backward(dy)
+
+    def stock():
+        xg.grad = wg.grad = bg.grad = None
+        F.silu(orig(xg, wg.unsqueeze(1), bg, 1, 3, 1, x.shape[1])[..., :L]).backward(dy)
+    native()
+    got = (xg.grad.clone(), wg.grad.clone(), bg.grad.clone())
+    stock()
+    err = max(max_rel_err(got[0], xg.grad.float()), max_rel_err(got[1], wg.grad.float()),
+              max_rel_err(got[2], bg.grad.float()))
+    ms = event_time_ms(native, 5)
+    stock_ms = event_time_ms(stock, 2)
+    return {"fwd_bwd_ms": round(ms, 3), "stock_fwd_bwd_ms": round(stock_ms, 3),
+            "variant": "causal_conv1d_fn (B, C, L) + SiLU: xlane forward, causal_bwd_bcl_kernel backward",
+            "max_rel_err_vs_stock_bf16": float(f"{err:.3g}")}
+
+
 def bench_gn_cl_detail(shape, G, silu, dev):
     """Channels-last GroupNorm (+ SiLU), bf16: the native NHWC / NDHWC kernel against stock
     F.group_norm on the same channels-last tensor (the reference contests CK here)."""
@@ -813,6 +847,7 @@ def main():
             ("c2_sym_k3_fp16", lambda: bench_dw_detail(torch.float16, "sym", dev)),
             ("c2_causal_backward_bf16", lambda: bench_dw_backward_detail(dev)),
             ("c2_decode_step_bf16", lambda: bench_decode_detail(dev)),
+            ("c2_causal_silu_backward_bf16", lambda: bench_causal_silu_backward_detail(dev)),
             ("c2_channel_last_bf16", lambda: bench_dw_cl_detail(dev)),
             ("c2_channel_last_silu_bf16", lambda: bench_dw_cl_detail(dev, silu=True)),
         ]

@@ -122,6 +122,21 @@ int atk_dwconv1d_bwd_weight(const void* x, const void* dy, float* dw, float* db,
                             int dtype, void* workspace, size_t ws_bytes, atk_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Causal conv1d backward, fused, (B, C, L) layout (replaces the non-channel-last branch
+ * of `causal_conv1d_bwd(x, weight, bias, dout, ..., silu)`,
+ * src/causal-conv1d-amd/csrc/causal_conv1d.cpp:240-380 -> causal_conv1d_bwd.cu:100-235):
+ * with z the recomputed fp32 pre-activation and g = dout * silu'(z) (dout without SiLU),
+ *   dx[p] = sum_k w[k] g[p+K-1-k],  dw[c,k] = sum_{b,p} g[p] x[p-K+1+k],  db[c] = sum g.
+ * x, dout, dx: [B, D, L] of `dtype`, contiguous, 16-byte aligned, L a multiple of 16 bytes;
+ * w[c,k] at c*w_stride_c + k*w_stride_k in w_dtype (fp32 or `dtype`), bias [D] in w_dtype
+ * or NULL; dw [D, K], db [D] fp32.  K in [2, 4].  The workspace (B*D*(K+1) floats) holds
+ * per-row partials, summed over b in a fixed order.
+ * ------------------------------------------------------------------------- */
+int atk_causal_conv1d_bwd(const void* x, const void* dout, const void* w, const void* bias, void* dx, float* dw,
+                          float* db, int64_t B, int64_t D, int64_t L, int K, int64_t w_stride_c, int64_t w_stride_k,
+                          int dtype, int w_dtype, int silu, void* workspace, size_t ws_bytes, atk_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Channels-last depthwise conv1d forward (replaces `conv1d_forward(u, weight, bias,
  * padding, is_bhl=false)`, amd_tuned_torch/_vendor/flashfftconv_depthwise_conv1d/
  * conv1d.h:56-83 -> conv1d_blh.hip:54-220, and the channel-last branch of

@@ -35,7 +35,7 @@ _DTYPE_CODE = {torch.float32: ATK_F32, torch.float16: ATK_F16, torch.bfloat16: A
 EXPORTED_SYMBOLS = (
     "atk_abi_version", "atk_last_error", "atk_num_variants", "atk_variant_name",
     "atk_dwconv1d_fwd", "atk_causal_conv1d_update", "atk_dwconv1d_bwd_weight_workspace_bytes",
-    "atk_dwconv1d_bwd_weight", "atk_dwconv1d_cl_fwd", "atk_dwconv1d_cl_bwd_weight_workspace_bytes",
+    "atk_dwconv1d_bwd_weight", "atk_causal_conv1d_bwd", "atk_dwconv1d_cl_fwd", "atk_dwconv1d_cl_bwd_weight_workspace_bytes",
     "atk_dwconv1d_cl_bwd_weight", "atk_causal_conv1d_cl_bwd_workspace_bytes", "atk_causal_conv1d_cl_bwd",
     "atk_group_norm_workspace_bytes",
     "atk_group_norm_workspace_zero_bytes", "atk_group_norm_fwd", "atk_group_norm_cl_workspace_bytes",
@@ -70,6 +70,9 @@ def _declare(lib) -> None:
     lib.atk_dwconv1d_bwd_weight_workspace_bytes.restype = sz
     lib.atk_dwconv1d_bwd_weight.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, i32, i64, i32, vp, sz, vp]
     lib.atk_dwconv1d_bwd_weight.restype = i32
+    lib.atk_causal_conv1d_bwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i32, i64, i64, i32, i32, i32,
+                                          vp, sz, vp]
+    lib.atk_causal_conv1d_bwd.restype = i32
     lib.atk_dwconv1d_cl_fwd.argtypes = [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i32, i32, i64] + [i64] * 10 + \
         [i32, i32, i32, i32, vp]
     lib.atk_dwconv1d_cl_fwd.restype = i32
@@ -415,6 +418,36 @@ def dwconv1d_cl_bwd_weight(x: torch.Tensor, dy: torch.Tensor, K: int, pad_left: 
         1 if seq_idx is not None else 0, _ptr(ws), ws.numel(), _stream(x))
     _check(rc, "dwconv1d_cl_bwd_weight")
     return dw, db
+
+
+def causal_conv1d_bwd(x: torch.Tensor, dout: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor],
+                      *, silu: bool = False):
+    """Fused backward of the causal (B, C, L) conv (pad K-1, output length L), width 2..4:
+    (dx in x's dtype, dw (D, K) fp32, db (D,) fp32).  x, dout contiguous (B, D, L) of one dtype;
+    weight (D, K) float32 or x's dtype, bias in the weight's dtype (recomputes the SiLU
+    pre-activation).  Raises Unsupported when L is not a multiple of 16 bytes."""
+    _require_cuda(x, dout, weight, bias)
+    if x.dim() != 3 or dout.shape != x.shape or dout.dtype != x.dtype or x.dtype not in _DTYPE_CODE:
+        raise RuntimeError("causal_conv1d_bwd: x and dout must be (B, D, L) of one dtype")
+    if weight.dim() != 2 or weight.shape[0] != x.shape[1] or weight.dtype not in (torch.float32, x.dtype):
+        raise RuntimeError("causal_conv1d_bwd: weight (D, K), float32 or x's dtype")
+    if bias is not None and bias.dtype != weight.dtype:
+        raise RuntimeError("causal_conv1d_bwd: bias must be in the weight's dtype")
+    if not (x.is_contiguous() and dout.is_contiguous()):
+        raise RuntimeError("causal_conv1d_bwd: x and dout must be contiguous")
+    B, D, L = x.shape
+    K = weight.shape[1]
+    dx = torch.empty_like(x)
+    dw = torch.empty((D, K), dtype=torch.float32, device=x.device)
+    db = torch.empty((D,), dtype=torch.float32, device=x.device)
+    bias = bias.contiguous() if bias is not None else None
+    L_ = lib()
+    ws = workspace(x.device, "causal_conv1d_bwd", B * D * (K + 1) * 4)
+    rc = L_.atk_causal_conv1d_bwd(_ptr(x), _ptr(dout), _ptr(weight), _ptr(bias), _ptr(dx), _ptr(dw), _ptr(db),
+                                  B, D, L, K, weight.stride(0), weight.stride(1), _DTYPE_CODE[x.dtype],
+                                  _DTYPE_CODE[weight.dtype], int(bool(silu)), _ptr(ws), ws.numel(), _stream(x))
+    _check(rc, "causal_conv1d_bwd")
+    return dx, dw, db
 
 
 def causal_conv1d_cl_bwd(x: torch.Tensor, dout: torch.Tensor, weight_dk: torch.Tensor,

@@ -85,7 +85,14 @@ def _backward(x, weight, bias, dout, seq_idx, initial_states, dfinal, silu: bool
         # the forward used the weights and bias in x's dtype: differentiate that function
         xc, g = x.contiguous(), dout.contiguous()
         wq = weight.to(x.dtype)
-        if silu:
+        fused = None
+        try:
+            fused = _native.causal_conv1d_bwd(xc, g, wq, bias.to(x.dtype) if bias is not None else None, silu=silu)
+        except _native.Unsupported:
+            fused = None
+        if fused is not None:
+            dx, dw, db = fused
+        elif silu:
             # the SiLU derivative needs the fp32 pre-activation: run both kernels in fp32
             xf, wf = xc.float(), wq.float()
             z = _native.dwconv1d(xf, wf, bias.to(x.dtype).float() if bias is not None else None, K - 1, L)

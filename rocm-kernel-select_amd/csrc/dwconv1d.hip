@@ -863,6 +863,129 @@ int launch_update(const void* x, void* state, const void* w, const void* bias, v
   return check_launch("causal_conv1d_update_kernel");
 }
 
+// ---------------------------------------------------------------------------------------
+// Causal conv1d backward, fused, (B, C, L) layout (src/causal-conv1d-amd/csrc/
+// causal_conv1d_bwd.cu:100-235, the non-channel-last kernel): with H = K-1, z the forward's
+// pre-activation (recomputed in fp32) and g = dout * silu'(z) (dout without the activation),
+//   dx[p] = sum_j w[j] * g[p + H - j],  dw[j] = sum_p g[p] * x[p - H + j],  db = sum_p g[p].
+// One workgroup per (b, c) row; a thread owns CB_T consecutive positions and loads, as aligned
+// 16-byte buffer loads (positions < 0 or >= L read zero), the x window [p0 - PRE*VEC,
+// p0 + CB_T + POST*VEC) and the dout window [p0, p0 + CB_T + POST*VEC): x and dout are read once
+// (the halos are L1/L2 hits) and dx written once.  dw / db: per-thread sums, a fixed-order block
+// reduction into per-row partials, and the per-channel finalize above (sum over b in order).
+// ---------------------------------------------------------------------------------------
+constexpr int CB_T = 32;  // positions per thread
+
+struct CbArgs {
+  const void* x;
+  const void* dy;
+  void* dx;
+  const void* w;
+  const void* b;
+  int wdt;
+  int64_t wc, wk;
+  float* part;    // [B*D][K+1]
+  uint32_t D, L;
+  uint32_t row_bytes;
+};
+
+template <typename T, int KT, bool SILU>
+__global__ __launch_bounds__(DW_NT) void causal_bwd_bcl_kernel(CbArgs a) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int H = KT - 1;
+  constexpr int NV = CB_T / VEC;               // vectors of the thread's own positions
+  constexpr int PRE = (2 * H + VEC - 1) / VEC;  // x vectors before p0 (SiLU recompute reaches p0 - 2H)
+  constexpr int POST = (H + VEC - 1) / VEC;     // vectors after p0 + CB_T (g reaches p0 + CB_T + H - 1)
+  constexpr int XV = PRE + NV + POST, GV = NV + POST;
+  __shared__ float red[DW_NT / 64];
+  const int64_t row = blockIdx.x;
+  const uint32_t d = (uint32_t)(row % a.D);
+  float wv[KT], bv = 0.f;
+#pragma unroll
+  for (int j = 0; j < KT; ++j) wv[j] = load_param(a.w, a.wdt, (int64_t)d * a.wc + (int64_t)j * a.wk);
+  if (SILU && a.b) bv = load_param(a.b, a.wdt, d);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(static_cast<const T*>(a.x) + row * a.L, a.row_bytes);
+  const __amdgpu_buffer_rsrc_t rg = make_rsrc(static_cast<const T*>(a.dy) + row * a.L, a.row_bytes);
+  T* dxr = static_cast<T*>(a.dx) + row * a.L;
+  const int L = (int)a.L;
+  float accw[KT], accb = 0.f;
+#pragma unroll
+  for (int j = 0; j < KT; ++j) accw[j] = 0.f;
+  for (int base = 0; base < L; base += DW_NT * CB_T) {
+    const int p0 = base + (int)threadIdx.x * CB_T;
+    if (p0 >= L) break;
+    Vec16<T> xr[XV], gr[GV];
+#pragma unroll
+    for (int v = 0; v < XV; ++v) {
+      const int p = p0 + (v - PRE) * VEC;
+      xr[v].raw = bload16(rx, (p >= 0 && p < L) ? (uint32_t)p * (uint32_t)sizeof(T) : kOOB, 0);
+    }
+#pragma unroll
+    for (int v = 0; v < GV; ++v) {
+      const int p = p0 + v * VEC;
+      gr[v].raw = bload16(rg, p < L ? (uint32_t)p * (uint32_t)sizeof(T) : kOOB, 0);
+    }
+    // x element of position p0 + i:  xe(i) = xr[(PRE*VEC + i) / VEC].e[(PRE*VEC + i) % VEC]
+#define XE(i) to_f32(xr[(PRE * VEC + (i)) / VEC].e[(PRE * VEC + (i)) % VEC])
+    // g for positions p0 .. p0 + CB_T + H - 1
+    float g[CB_T + H];
+#pragma unroll
+    for (int i = 0; i < CB_T + H; ++i) {
+      float gi = to_f32(gr[i / VEC].e[i % VEC]);
+      if constexpr (SILU) {
+        float z = bv;
+#pragma unroll
+        for (int j = 0; j < KT; ++j) z = __builtin_fmaf(wv[j], XE(i - H + j), z);
+        const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-z));
+        gi *= sg * (1.0f + z * (1.0f - sg));
+      }
+      g[i] = gi;
+    }
+    // dx for the thread's positions, and the dw / db sums (g past L is zero: dout read zero)
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+      float o[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        const int i = v * VEC + e;
+        float acc = 0.f;
+#pragma unroll
+        for (int j = 0; j < KT; ++j) acc = __builtin_fmaf(wv[j], g[i + H - j], acc);
+        o[e] = acc;
+        accb += g[i];
+#pragma unroll
+        for (int j = 0; j < KT; ++j) accw[j] = __builtin_fmaf(g[i], XE(i - H + j), accw[j]);
+      }
+      if (p0 + v * VEC < L) st16<false>(dxr + p0 + v * VEC, pack16<T>(o));
+    }
+#undef XE
+  }
+#pragma unroll
+  for (int j = 0; j < KT; ++j) {
+    const float sj = block_sum<DW_NT>(accw[j], red);
+    if (threadIdx.x == 0) a.part[row * (KT + 1) + j] = sj;
+  }
+  const float sb = block_sum<DW_NT>(accb, red);
+  if (threadIdx.x == 0) a.part[row * (KT + 1) + KT] = sb;
+}
+
+template <typename T, int KT>
+void launch_cb_kt(const CbArgs& a, int64_t rows, int silu, hipStream_t s) {
+  if (silu) hipLaunchKernelGGL((causal_bwd_bcl_kernel<T, KT, true>), dim3((unsigned)rows), dim3(DW_NT), 0, s, a);
+  else hipLaunchKernelGGL((causal_bwd_bcl_kernel<T, KT, false>), dim3((unsigned)rows), dim3(DW_NT), 0, s, a);
+}
+
+template <typename T>
+int launch_cb(const CbArgs& a, int64_t rows, int K, int silu, hipStream_t s) {
+  switch (K) {
+    case 2: launch_cb_kt<T, 2>(a, rows, silu, s); break;
+    case 3: launch_cb_kt<T, 3>(a, rows, silu, s); break;
+    case 4: launch_cb_kt<T, 4>(a, rows, silu, s); break;
+    default: return fail(ATK_UNSUPPORTED, "causal_conv1d_bwd: width %d outside [2, 4]", K);
+  }
+  return check_launch("causal_bwd_bcl_kernel");
+}
+
 }  // namespace
 
 int dwconv1d_num_variants() { return kNumDw; }
@@ -991,4 +1114,40 @@ extern "C" int atk_causal_conv1d_update(const void* x, void* conv_state, const v
     case ATK_F16: return launch_update<_Float16>(x, conv_state, w, bias, y, rows, D, W, fuse_silu, s);
     default: return launch_update<__bf16>(x, conv_state, w, bias, y, rows, D, W, fuse_silu, s);
   }
+}
+
+extern "C" int atk_causal_conv1d_bwd(const void* x, const void* dout, const void* w, const void* bias, void* dx,
+                                     float* dw, float* db, int64_t B, int64_t D, int64_t L, int K,
+                                     int64_t w_stride_c, int64_t w_stride_k, int dtype, int w_dtype, int silu,
+                                     void* workspace, size_t ws_bytes, atk_stream_t stream) {
+  using namespace atk;
+  if (!dtype_ok(dtype) || !dtype_ok(w_dtype)) return fail(ATK_EINVAL, "causal_conv1d_bwd: unknown dtype code");
+  if (B <= 0 || D <= 0 || L <= 0) return fail(ATK_EINVAL, "causal_conv1d_bwd: bad sizes");
+  if (!x || !dout || !dx || !w || !dw) return fail(ATK_EINVAL, "causal_conv1d_bwd: null pointer");
+  if (K < 2 || K > 4) return fail(ATK_UNSUPPORTED, "causal_conv1d_bwd: width %d outside [2, 4]", K);
+  const int64_t es = (int64_t)dtype_size(dtype), vec = 16 / es;
+  if (L % vec || !aligned16(x) || !aligned16(dout) || !aligned16(dx))
+    return fail(ATK_UNSUPPORTED, "causal_conv1d_bwd: needs L %% %lld == 0 and 16-byte aligned tensors",
+                (long long)vec);
+  const int64_t rows = B * D;
+  if (rows >= (1ll << 31) || L * es >= (1ll << 31)) return fail(ATK_UNSUPPORTED, "causal_conv1d_bwd: too large");
+  const size_t need = (size_t)rows * (size_t)(K + 1) * sizeof(float);
+  if (!workspace || ws_bytes < need) return fail(ATK_EINVAL, "causal_conv1d_bwd: workspace of %zu bytes needed", need);
+  CbArgs a;
+  a.x = x; a.dy = dout; a.dx = dx; a.w = w; a.b = bias; a.wdt = w_dtype; a.wc = w_stride_c; a.wk = w_stride_k;
+  a.part = static_cast<float*>(workspace);
+  a.D = (uint32_t)D; a.L = (uint32_t)L;
+  a.row_bytes = (uint32_t)(L * es);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int rc;
+  switch (dtype) {
+    case ATK_F32: rc = launch_cb<float>(a, rows, K, silu, s); break;
+    case ATK_F16: rc = launch_cb<_Float16>(a, rows, K, silu, s); break;
+    default: rc = launch_cb<__bf16>(a, rows, K, silu, s); break;
+  }
+  if (rc) return rc;
+  const int outs = (int)(D * (K + 1));
+  hipLaunchKernelGGL(dwconv1d_bwd_finalize_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s,
+                     a.part, dw, db, (int)B, (int)D, K);
+  return check_launch("dwconv1d_bwd_finalize_kernel");
 }

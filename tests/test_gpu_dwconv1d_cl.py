@@ -191,11 +191,13 @@ def test_causal_channel_last_seq_idx(seqlen, width, dtype):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("silu", [False, True])
-def test_causal_bcl_autograd(dtype, silu):
-    """The (B, C, L) layout through causal_conv1d_fn's backward (fp32 weights)."""
+@pytest.mark.parametrize("L,K", [(256, 4), (4096, 4), (1024, 2), (512, 3), (300, 4)])
+def test_causal_bcl_autograd(dtype, silu, L, K):
+    """The (B, C, L) layout through causal_conv1d_fn's backward (fp32 weights): the fused
+    kernel (L a multiple of 16 bytes) and the composition it falls back to (L = 300)."""
     from amd_tuned_torch.causal_conv1d import causal_conv1d_fn
-    g = torch.Generator().manual_seed(3)
-    B, D, L, K = 2, 64, 300, 4
+    g = torch.Generator().manual_seed(3 + L + K)
+    B, D = 2, 64
     x = torch.randn(B, D, L, generator=g).to(dtype).cuda().requires_grad_()
     w = torch.randn(D, K, generator=g).cuda().requires_grad_()
     b = torch.randn(D, generator=g).cuda().requires_grad_()
@@ -270,3 +272,23 @@ def test_fconv1d_on_channel_last_input_takes_the_channels_last_kernel(K, pad, dt
     _close(xg.grad, dx, dtype, "F.conv1d channel-last dx")
     _grad_close(wg.grad.reshape(D, K), dw, "dweight", 1e-5 if dtype == torch.float32 else 1e-2)
     _grad_close(bg.grad, db, "dbias", 1e-5 if dtype == torch.float32 else 1e-2)
+
+
+def test_causal_bcl_fused_backward_full_size():
+    """Config 2's shape (16, 2048, 8192) bf16, K = 4: the fused (B, C, L) backward against the
+    composition of parity-tested kernels (forward kernel on the flipped weights for dx, the
+    weight-gradient kernel for dw / db)."""
+    from amd_tuned_torch import _native
+    g = torch.Generator(device="cuda").manual_seed(1)
+    B, D, L, K = 16, 2048, 8192, 4
+    x = torch.randn(B, D, L, device="cuda", generator=g).to(torch.bfloat16)
+    dy = torch.randn(B, D, L, device="cuda", generator=g).to(torch.bfloat16)
+    w = (torch.randn(D, K, device="cuda", generator=g) / 2).to(torch.bfloat16)
+    dx, dw, db = _native.causal_conv1d_bwd(x, dy, w, None, silu=False)
+    dx_ref = _native.dwconv1d(dy, w.flip(-1), None, 0, L)
+    dw_ref, db_ref = _native.dwconv1d_bwd_weight(x, dy, K, K - 1)
+    assert O.max_rel_err(dx.float(), dx_ref.float()) <= 1e-2
+    assert (dx == dx_ref).float().mean().item() > 0.99
+    assert O.max_rel_err(dw, dw_ref) <= 1e-4 and O.max_rel_err(db, db_ref) <= 1e-4
+    del x, dy, dx, dx_ref
+    torch.cuda.empty_cache()
