@@ -776,9 +776,9 @@ def main():
         summarize_traffic(*args.summarize_traffic, args.variant, args.command)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one MI355X; the hot path has no multi-GPU "
-              "component (see DESIGN.md for how it would shard). Run with --gpus 1.",
-              file=sys.stderr)
+        print("bench.py: this build measures one MI355X; the hot path has no multi-GPU component "
+              "(conv1d and GroupNorm would shard over batch or channels with no exchange, conv3d over "
+              "batch or output channels). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch
