@@ -545,18 +545,31 @@ __attribute__((amdgpu_waves_per_eu(FCO * FSP >= 8 && CB == 16 ? 2 : 1))) void co
 template <typename T>
 __global__ __launch_bounds__(256) void pack_weights_kernel(const T* __restrict__ w, T* __restrict__ wp,
                                                            int Co, int Ci, int taps, int n_kb,
-                                                           int co_blocks, int64_t total) {
+                                                           int co_blocks, uint32_t chunks) {
+  // one thread per 16-byte chunk of the packed layout [tap][kb][co_block][32][KB] (KB is a
+  // multiple of the chunk's E elements, so a chunk never crosses a row); 32-bit index math
+  // (the host keeps the packed weights under 2 GiB)
   constexpr int KB = MfmaTraits<T>::KB;
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= total) return;
-  const int k = (int)(i % KB);
-  int64_t r = i / KB;
-  const int row = (int)(r % 32); r /= 32;
-  const int cb = (int)(r % co_blocks); r /= co_blocks;
-  const int kb = (int)(r % n_kb);
-  const int tap = (int)(r / n_kb);
-  const int co = cb * 32 + row, ci = kb * KB + k;
-  wp[i] = (co < Co && ci < Ci) ? w[((int64_t)co * Ci + ci) * taps + tap] : static_cast<T>(0.0f);
+  constexpr int E = 16 / sizeof(T);
+  const uint32_t c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= chunks) return;
+  const uint32_t i = c * E;
+  const uint32_t k0 = i % KB;
+  uint32_t r = i / KB;
+  const uint32_t row = r % 32;
+  r /= 32;
+  const uint32_t cb = r % (uint32_t)co_blocks;
+  r /= (uint32_t)co_blocks;
+  const uint32_t kb = r % (uint32_t)n_kb;
+  const uint32_t tap = r / (uint32_t)n_kb;
+  const int co = (int)(cb * 32 + row);
+  Vec16<T> v;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int ci = (int)(kb * KB + k0) + e;
+    v.e[e] = (co < Co && ci < Ci) ? w[((int64_t)co * Ci + ci) * taps + tap] : static_cast<T>(0.0f);
+  }
+  *reinterpret_cast<uint4*>(wp + i) = v.raw;
 }
 
 // y = sum over splits of the fp32 partials + bias
@@ -722,9 +735,9 @@ int launch_ig(const ConvShape& p, const void* x, const void* w, const void* bias
   a.part = pl.splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + align256(pl.wp_bytes)) : nullptr;
   // pack the weights
   const int taps = p.KD * p.KH * p.KW;
-  const int64_t wtotal = (int64_t)pl.wp_bytes / sizeof(T);
-  hipLaunchKernelGGL((pack_weights_kernel<T>), dim3((unsigned)((wtotal + 255) / 256)), dim3(256), 0, s,
-                     static_cast<const T*>(w), static_cast<T*>(ws), p.Co, p.Ci, taps, a.n_kb, a.co_blocks, wtotal);
+  const uint32_t chunks = (uint32_t)(pl.wp_bytes / 16);  // wp_bytes: a multiple of 32 rows x KB elements
+  hipLaunchKernelGGL((pack_weights_kernel<T>), dim3((chunks + 255) / 256), dim3(256), 0, s,
+                     static_cast<const T*>(w), static_cast<T*>(ws), p.Co, p.Ci, taps, a.n_kb, a.co_blocks, chunks);
   rc = check_launch("pack_weights_kernel");
   if (rc) return rc;
   // instantiate only the variants of this element type's class
