@@ -83,13 +83,13 @@ __device__ __forceinline__ void mfma_block(f32x16& acc, const uint4& a, const ui
 // per-element bounds test; readers add mis = ix0 - gx0.  Chunk c maps to (row-chunk
 // rc = c / CB, channel cl = c % CB): consecutive lanes write consecutive channels of one
 // patch position.
-template <typename T, int CB, bool VR, int NTH = 256>
+template <typename T, int CB, bool VR, int NTH = 256, int XC = 1>
 struct PatchLoader {
   static constexpr int VEC = 16 / sizeof(T);
   // chunks per thread held for the next stage: CB/4 for 16-bit types, CB/2 for fp32, at 256
-  // threads per workgroup (scaled up for smaller workgroups; the host plan rejects tiles whose
-  // patch needs more)
-  static constexpr int MAXC = (sizeof(T) == 2 ? CB / 4 : CB / 2) * (256 / NTH);
+  // threads per workgroup (scaled up for smaller workgroups), times XC for tiles whose patch
+  // has a wide halo (7x7 planes); the host plan rejects tiles whose patch needs more
+  static constexpr int MAXC = (sizeof(T) == 2 ? CB / 4 : CB / 2) * (256 / NTH) * XC;
   uint4 buf[MAXC];
 
   // rsrc covers sample n of the input; iz may be out of range (a padding plane)
@@ -278,9 +278,9 @@ __device__ __forceinline__ void store_tile(const IgArgs& a, const f32x16 (&acc)[
 
 // Tiles of 8 accumulator blocks (128 AGPRs) are asked to fit 2 waves per SIMD: with their
 // LDS footprint two workgroups share a CU, and one wave per SIMD leaves no latency cover.
-template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, bool VR, int KHT, int KWT>
+template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, int XC, bool VR, int KHT, int KWT>
 __global__ __launch_bounds__(64 * WCO * WSP)
-__attribute__((amdgpu_waves_per_eu(FCO * FSP >= 8 && CB == 16 ? 2 : 1))) void conv_igemm_kernel(IgArgs a) {
+__attribute__((amdgpu_waves_per_eu((FCO * FSP >= 8 && CB == 16) || XC > 1 ? 2 : 1))) void conv_igemm_kernel(IgArgs a) {
   constexpr int NT = 64 * WCO * WSP;
   constexpr int KB = MfmaTraits<T>::KB, VEC = MfmaTraits<T>::VEC;
   constexpr int ES = sizeof(T);
@@ -342,7 +342,7 @@ __attribute__((amdgpu_waves_per_eu(FCO * FSP >= 8 && CB == 16 ? 2 : 1))) void co
   const int ntaps2d = a.KH * a.KW;
   const int co_blk0 = co_tile * (BN / 32) + wco * FCO;
 
-  PatchLoader<T, CB, VR, NT> ld;
+  PatchLoader<T, CB, VR, NT, XC> ld;
   const int total_quads = total_chunks / 4;
   if constexpr (VR) ld.init(a, iy0, gx0, total_quads, tid, NT);
   // stage s = (channel chunk cc, kernel plane kd), walked incrementally
@@ -354,9 +354,9 @@ __attribute__((amdgpu_waves_per_eu(FCO * FSP >= 8 && CB == 16 ? 2 : 1))) void co
       const uint32_t so = ld.stage_off(a, cc, iz);
       const int lim = ld.stage_lim(a, cc, iz, true);
 #pragma unroll
-      for (int u = 0; u < PatchLoader<T, CB, VR, NT>::MAXC; ++u) ld.load_fast(rx, u, so, lim);
+      for (int u = 0; u < PatchLoader<T, CB, VR, NT, XC>::MAXC; ++u) ld.load_fast(rx, u, so, lim);
 #pragma unroll
-      for (int g = 0; g < PatchLoader<T, CB, VR, NT>::NQ; ++g)
+      for (int g = 0; g < PatchLoader<T, CB, VR, NT, XC>::NQ; ++g)
         ld.store_quad(reinterpret_cast<T*>(lds_bytes), g, total_quads, tid, NT);
     } else {
       ld.load(a, rx, cc, iz_base + kd * a.dd, iy0, gx0, total_chunks, tid, NT);
@@ -388,8 +388,8 @@ __attribute__((amdgpu_waves_per_eu(FCO * FSP >= 8 && CB == 16 ? 2 : 1))) void co
     // prefetching PF taps ahead; only PF + 1 of them are live at once
     constexpr int NB = NT2 % 3 == 0 ? 3 : NT2 % 5 == 0 ? 5 : 7;
     constexpr int PF = NB - 1 < 3 ? NB - 1 : 3;
-    constexpr int MAXC = PatchLoader<T, CB, VR, NT>::MAXC;
-    constexpr int NQ = PatchLoader<T, CB, VR, NT>::NQ;
+    constexpr int MAXC = PatchLoader<T, CB, VR, NT, XC>::MAXC;
+    constexpr int NQ = PatchLoader<T, CB, VR, NT, XC>::NQ;
     static_assert(NT2 % NB == 0, "buffer rotation must repeat every stage");
     static_assert(NQ >= 1 && NQ <= 4 && NT2 >= 9, "schedule below assumes <= 4 quads, 9+ taps");
     // chunks are issued LPT per tap over taps 0-3; quads [0, QH) are written at tap QS0 (their
@@ -474,7 +474,7 @@ __attribute__((amdgpu_waves_per_eu(FCO * FSP >= 8 && CB == 16 ? 2 : 1))) void co
       const uint32_t so1 = __builtin_amdgcn_readfirstlane(ld.stage_off(a, cc1, iz1));
       const int lim1 = __builtin_amdgcn_readfirstlane(ld.stage_lim(a, cc1, iz1, has_next));
 #pragma unroll
-      for (int u = 0; u < PatchLoader<T, CB, VR, NT>::MAXC; ++u) ld.load_fast(rx, u, so1, lim1);
+      for (int u = 0; u < PatchLoader<T, CB, VR, NT, XC>::MAXC; ++u) ld.load_fast(rx, u, so1, lim1);
     } else {
       ld.load(a, rx, cc1, iz_base + kd1 * a.dd, iy0, gx0, total_chunks, tid, NT, has_next);
     }
@@ -527,7 +527,7 @@ __attribute__((amdgpu_waves_per_eu(FCO * FSP >= 8 && CB == 16 ? 2 : 1))) void co
     if (has_next) {
       if constexpr (VR) {
 #pragma unroll
-        for (int g = 0; g < PatchLoader<T, CB, VR, NT>::NQ; ++g)
+        for (int g = 0; g < PatchLoader<T, CB, VR, NT, XC>::NQ; ++g)
           ld.store_quad(reinterpret_cast<T*>(lds_bytes + (pbuf ^ patch_bytes)), g, total_quads, tid, NT);
       } else {
         ld.store(a, reinterpret_cast<T*>(lds_bytes + (pbuf ^ patch_bytes)), total_chunks, tid, NT);
@@ -589,22 +589,26 @@ struct IgVariant {
   const char* name;
   int dtype_class;  // 0 = 16-bit, 1 = fp32
   int wco, wsp, fco, fsp, cb;
+  int xc;           // patch-loader capacity multiplier (PatchLoader XC)
 };
 
 const IgVariant kIg[] = {
-    {"h_w22_f22_cb32", 0, 2, 2, 2, 2, 32},
-    {"h_w22_f24_cb32", 0, 2, 2, 2, 4, 32},
-    {"h_w14_f22_cb32", 0, 1, 4, 2, 2, 32},
-    {"h_w22_f22_cb16", 0, 2, 2, 2, 2, 16},
-    {"h_w41_f22_cb32", 0, 4, 1, 2, 2, 32},
-    {"h_w21_f24_cb32", 0, 2, 1, 2, 4, 32},
-    {"h_w22_f12_cb32", 0, 2, 2, 1, 2, 32},
-    {"h_w21_f14_cb32", 0, 2, 1, 1, 4, 32},
-    {"h_w22_f24_cb16", 0, 2, 2, 2, 4, 16},
-    {"f32_w22_f22_cb16", 1, 2, 2, 2, 2, 16},
-    {"f32_w14_f22_cb16", 1, 1, 4, 2, 2, 16},
-    {"f32_w22_f12_cb16", 1, 2, 2, 1, 2, 16},
-    {"f32_w21_f14_cb16", 1, 2, 1, 1, 4, 16},
+    {"h_w22_f22_cb32", 0, 2, 2, 2, 2, 32, 1},
+    {"h_w22_f24_cb32", 0, 2, 2, 2, 4, 32, 1},
+    {"h_w14_f22_cb32", 0, 1, 4, 2, 2, 32, 1},
+    {"h_w22_f22_cb16", 0, 2, 2, 2, 2, 16, 1},
+    {"h_w41_f22_cb32", 0, 4, 1, 2, 2, 32, 1},
+    {"h_w21_f24_cb32", 0, 2, 1, 2, 4, 32, 1},
+    {"h_w22_f12_cb32", 0, 2, 2, 1, 2, 32, 1},
+    {"h_w21_f14_cb32", 0, 2, 1, 1, 4, 32, 1},
+    {"h_w22_f24_cb16", 0, 2, 2, 2, 4, 16, 1},
+    {"f32_w22_f22_cb16", 1, 2, 2, 2, 2, 16, 1},
+    {"f32_w14_f22_cb16", 1, 1, 4, 2, 2, 16, 1},
+    {"f32_w22_f12_cb16", 1, 2, 2, 1, 2, 16, 1},
+    {"f32_w21_f14_cb16", 1, 2, 1, 1, 4, 16, 1},
+    // 64 output channels with a 7x7 plane: the 32x32-position tile's 14-row patch needs twice
+    // the default loader capacity
+    {"h_w14_f22_cb16x2", 0, 1, 4, 2, 2, 16, 2},
 };
 constexpr int kNumIg = sizeof(kIg) / sizeof(kIg[0]);
 
@@ -662,7 +666,7 @@ int plan_ig(const ConvShape& p, int v, IgPlan& pl) {
   a.patch_elems = a.PY * a.PXS * (vr.cb + VEC);
   pl.lds = (size_t)2 * a.patch_elems * es;
   {
-    const int maxc = (f32 ? vr.cb / 2 : vr.cb / 4) * (256 / pl.nthreads);  // PatchLoader::MAXC
+    const int maxc = (f32 ? vr.cb / 2 : vr.cb / 4) * (256 / pl.nthreads) * vr.xc;  // PatchLoader::MAXC
     if (pl.lds > 150 * 1024 || vr.cb * a.PY * a.NCX > maxc * pl.nthreads)
       return fail(ATK_UNSUPPORTED, "conv %s: stage of %zu LDS bytes does not fit the variant", vr.name, pl.lds);
   }
@@ -690,9 +694,9 @@ int plan_ig(const ConvShape& p, int v, IgPlan& pl) {
 
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, bool VR, int KHT, int KWT>
+template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, int XC, bool VR, int KHT, int KWT>
 int launch_ig_vr(const IgPlan& pl, hipStream_t s) {
-  auto kern = conv_igemm_kernel<T, WCO, WSP, FCO, FSP, CB, VR, KHT, KWT>;
+  auto kern = conv_igemm_kernel<T, WCO, WSP, FCO, FSP, CB, XC, VR, KHT, KWT>;
   if (pl.lds > 64 * 1024) {
     // opt in to more than 64 KB of dynamic LDS (gfx950 has 160 KB per CU); once per kernel
     static bool raised = false;
@@ -708,14 +712,20 @@ int launch_ig_vr(const IgPlan& pl, hipStream_t s) {
   return check_launch("conv_igemm_kernel");
 }
 
-template <typename T, int WCO, int WSP, int FCO, int FSP, int CB>
+template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, int XC = 1>
 int launch_ig_t(const IgPlan& pl, hipStream_t s) {
   if (pl.a.KH == 3 && pl.a.KW == 3 && pl.a.vec_rows)
-    return launch_ig_vr<T, WCO, WSP, FCO, FSP, CB, true, 3, 3>(pl, s);
+    return launch_ig_vr<T, WCO, WSP, FCO, FSP, CB, XC, true, 3, 3>(pl, s);
   if (pl.a.KH == 7 && pl.a.KW == 7 && pl.a.vec_rows)
-    return launch_ig_vr<T, WCO, WSP, FCO, FSP, CB, true, 7, 7>(pl, s);
-  return pl.a.vec_rows ? launch_ig_vr<T, WCO, WSP, FCO, FSP, CB, true, 0, 0>(pl, s)
-                       : launch_ig_vr<T, WCO, WSP, FCO, FSP, CB, false, 0, 0>(pl, s);
+    return launch_ig_vr<T, WCO, WSP, FCO, FSP, CB, XC, true, 7, 7>(pl, s);
+  if constexpr (XC > 1) {
+    // the element-wise loader of unaligned rows spills at this capacity
+    if (!pl.a.vec_rows) return fail(ATK_UNSUPPORTED, "conv: this tile needs 16-byte aligned input rows");
+    return launch_ig_vr<T, WCO, WSP, FCO, FSP, CB, XC, true, 0, 0>(pl, s);
+  } else {
+    return pl.a.vec_rows ? launch_ig_vr<T, WCO, WSP, FCO, FSP, CB, XC, true, 0, 0>(pl, s)
+                         : launch_ig_vr<T, WCO, WSP, FCO, FSP, CB, XC, false, 0, 0>(pl, s);
+  }
 }
 
 template <typename T>
@@ -752,6 +762,7 @@ int launch_ig(const ConvShape& p, const void* x, const void* w, const void* bias
       case 6: rc = launch_ig_t<T, 2, 2, 1, 2, 32>(pl, s); break;
       case 7: rc = launch_ig_t<T, 2, 1, 1, 4, 32>(pl, s); break;
       case 8: rc = launch_ig_t<T, 2, 2, 2, 4, 16>(pl, s); break;
+      case 13: rc = launch_ig_t<T, 1, 4, 2, 2, 16, 2>(pl, s); break;
       default: return fail(ATK_EINVAL, "conv: bad variant");
     }
   } else {
