@@ -693,7 +693,7 @@ struct GnBwdArgs {
 template <typename T>
 __global__ __launch_bounds__(GN_TP_NT) void gn_bwd_rows_kernel(GnBwdArgs a) {
   constexpr int VEC = 16 / sizeof(T);
-  __shared__ float red[GN_TP_NT / 64];
+  __shared__ float red[4 * (GN_TP_NT / 64)];
   const int64_t r = blockIdx.x;
   const T* __restrict__ xr = static_cast<const T*>(a.x) + r * a.S;
   const T* __restrict__ gr = static_cast<const T*>(a.dy) + r * a.S;
@@ -726,11 +726,29 @@ __global__ __launch_bounds__(GN_TP_NT) void gn_bwd_rows_kernel(GnBwdArgs a) {
       }
     }
   }
-  s1 = block_sum<GN_TP_NT>(s1, red);
-  s2 = block_sum<GN_TP_NT>(s2, red);
-  sa = block_sum<GN_TP_NT>(sa, red);
-  sb = block_sum<GN_TP_NT>(sb, red);
+  // only thread 0 needs the totals: the four wave sums go through LDS in one exchange
+  // (four block_sum calls would cost eight barriers in a workgroup this short-lived)
+  s1 = wave_sum(s1);
+  s2 = wave_sum(s2);
+  sa = wave_sum(sa);
+  sb = wave_sum(sb);
+  if ((threadIdx.x & 63) == 0) {
+    const int w = threadIdx.x >> 6;
+    red[w] = s1;
+    red[GN_TP_NT / 64 + w] = s2;
+    red[2 * (GN_TP_NT / 64) + w] = sa;
+    red[3 * (GN_TP_NT / 64) + w] = sb;
+  }
+  __syncthreads();
   if (threadIdx.x == 0) {
+    s1 = s2 = sa = sb = 0.f;
+#pragma unroll
+    for (int w = 0; w < GN_TP_NT / 64; ++w) {  // the order block_sum uses
+      s1 += red[w];
+      s2 += red[GN_TP_NT / 64 + w];
+      sa += red[2 * (GN_TP_NT / 64) + w];
+      sb += red[3 * (GN_TP_NT / 64) + w];
+    }
     const float q = s1 / (float)a.S;
     float* o = a.rows + r * 5;
     o[0] = K + q;
@@ -942,15 +960,46 @@ __global__ __launch_bounds__(GN_CL_NT) void gn_cl_stats_kernel(GnClArgs a) {
   }
 }
 
-__global__ __launch_bounds__(64) void gn_cl_merge_kernel(GnClArgs a) {
+// One workgroup per (n, g): thread t takes chunks t, t + NT, ... (up to GN_CL_MERGE_U each),
+// all of whose (mean, M2) loads are issued before any is used -- walked one dependent load
+// at a time, the merge of C3b's 1024 chunks took longer than the stats kernel -- and two
+// fixed-order block sums give mean = sum n_i mean_i / E, M2 = sum (M2_i + n_i (mean_i - mean)^2).
+constexpr int GN_CL_MERGE_NT = 256;
+constexpr int GN_CL_MERGE_U = 16;  // chunks per thread: NCH <= 4096 (host check)
+__global__ __launch_bounds__(GN_CL_MERGE_NT) void gn_cl_merge_kernel(GnClArgs a) {
+  __shared__ float red[GN_CL_MERGE_NT / 64];
   const int64_t ng = blockIdx.x;  // n * G + g
   const int64_t n = ng / a.G, g = ng - n * a.G;
-  const float* p = a.part + (n * a.NCH * a.G + g) * 2;
-  const int64_t step = (int64_t)a.G * 2;
-  float mean, var;
-  wave_merge(a.NCH, a.SC * a.cpg, a.S * a.cpg, [&](int i) { return p[i * step]; },
-             [&](int i) { return p[i * step + 1]; }, mean, var);
-  if (threadIdx.x == 0) {
+  const int tid = threadIdx.x;
+  // the partials of sample n: [NCH][G][2] floats; chunks past NCH read zero
+  const __amdgpu_buffer_rsrc_t rp = make_rsrc(a.part + n * a.NCH * a.G * 2, (uint32_t)a.NCH * a.G * 8u);
+  float mv[GN_CL_MERGE_U], qv[GN_CL_MERGE_U];
+#pragma unroll
+  for (int u = 0; u < GN_CL_MERGE_U; ++u) {
+    const int i = tid + u * GN_CL_MERGE_NT;
+    const uint32_t off = i < a.NCH ? ((uint32_t)i * a.G + (uint32_t)g) * 8u : kOOB;
+    mv[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, (int)off, 0, 0));
+    qv[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rp, (int)(off + (i < a.NCH ? 4u : 0u)), 0, 0));
+  }
+  const int64_t slice = a.SC * a.cpg, E = a.S * a.cpg;
+  float sm = 0.f;
+#pragma unroll
+  for (int u = 0; u < GN_CL_MERGE_U; ++u) {
+    const int i = tid + u * GN_CL_MERGE_NT;
+    const float len = i < a.NCH ? (float)slice_len(i, slice, E) : 0.f;
+    sm = fmaf(len, mv[u], sm);
+  }
+  const float mean = block_sum<GN_CL_MERGE_NT>(sm, red) / (float)E;
+  float m2 = 0.f;
+#pragma unroll
+  for (int u = 0; u < GN_CL_MERGE_U; ++u) {
+    const int i = tid + u * GN_CL_MERGE_NT;
+    const float len = i < a.NCH ? (float)slice_len(i, slice, E) : 0.f;
+    const float d = mv[u] - mean;
+    m2 += qv[u] + len * d * d;
+  }
+  const float var = block_sum<GN_CL_MERGE_NT>(m2, red) / (float)E;
+  if (tid == 0) {
     a.stat[ng * 2] = mean;
     a.stat[ng * 2 + 1] = 1.0f / sqrtf(var + a.eps);
   }
@@ -1033,7 +1082,8 @@ int launch_gn_cl(const GnClArgs& a, int N, int silu, hipStream_t s) {
   hipLaunchKernelGGL((gn_cl_stats_kernel<T>), grid, block, 0, s, a);
   int rc = check_launch("gn_cl_stats_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL(gn_cl_merge_kernel, dim3((unsigned)(N * a.G)), dim3(64), 0, s, a);
+  if (a.NCH > GN_CL_MERGE_NT * GN_CL_MERGE_U) return fail(ATK_UNSUPPORTED, "group_norm (channels-last): too many chunks");
+  hipLaunchKernelGGL(gn_cl_merge_kernel, dim3((unsigned)(N * a.G)), dim3(GN_CL_MERGE_NT), 0, s, a);
   rc = check_launch("gn_cl_merge_kernel");
   if (rc) return rc;
   if (silu) hipLaunchKernelGGL((gn_cl_apply_kernel<T, true>), grid, block, 0, s, a);
