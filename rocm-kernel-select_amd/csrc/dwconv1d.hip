@@ -762,7 +762,10 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_bwd_w_kernel(DwBwdArgs a) {
   using Win = DwWindow<T, KT>;
   using Dyw = DwWindow<T, 1>;
   constexpr int VEC = Win::VEC, WN = Win::WN;
-  __shared__ float red[DW_NT / 64];
+  // output vectors fetched per thread before any is used (4 measured slower than 1 on
+  // config 2's 8195-output rows)
+  constexpr int BWD_U = 1;
+  __shared__ float red[(KT + 1) * (DW_NT / 64)];
   const uint32_t r = blockIdx.x;  // row n*C + c
   const uint32_t L = a.L, Lout = a.Lout;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(
@@ -772,25 +775,49 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_bwd_w_kernel(DwBwdArgs a) {
   float acc[KT + 1];
 #pragma unroll
   for (int k = 0; k <= KT; ++k) acc[k] = 0.f;
-  for (uint32_t t = threadIdx.x * VEC; t < Lout; t += DW_NT * VEC) {
-    uint32_t DD[4 * Dyw::NBLK], DX[4 * Win::NBLK];
-    int md, mx;
-    Dyw::fetch(rd, (int)(r * Lout + t) + a.dy_off, true, DD, md);
-    Win::fetch(rx, (int)(r * L + t) - a.pad + a.x_off, true, DX, mx);
-    float dv[VEC], xv[WN];
-    Dyw::extract(DD, md, (int)t, Lout, dv);       // zero past the row end
-    Win::extract(DX, mx, (int)t - a.pad, L, xv);  // zero outside [0, L)
+  // BWD_U output vectors per thread are fetched before any is used (positions past the row
+  // issue out-of-range loads that read zero); the sums still run over t in order
+  for (uint32_t t0 = threadIdx.x * VEC; t0 < Lout; t0 += BWD_U * DW_NT * VEC) {
+    uint32_t DD[BWD_U][4 * Dyw::NBLK], DX[BWD_U][4 * Win::NBLK];
+    int md[BWD_U], mx[BWD_U];
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      acc[KT] += dv[e];
+    for (int u = 0; u < BWD_U; ++u) {
+      const uint32_t t = t0 + u * DW_NT * VEC;
+      const bool act = t < Lout;
+      const uint32_t tc = act ? t : 0u;
+      Dyw::fetch(rd, (int)(r * Lout + tc) + a.dy_off, act, DD[u], md[u]);
+      Win::fetch(rx, (int)(r * L + tc) - a.pad + a.x_off, act, DX[u], mx[u]);
+    }
 #pragma unroll
-      for (int k = 0; k < KT; ++k) acc[k] = fmaf(dv[e], xv[e + k], acc[k]);
+    for (int u = 0; u < BWD_U; ++u) {
+      const uint32_t t = t0 + u * DW_NT * VEC;
+      float dv[VEC], xv[WN];
+      Dyw::extract(DD[u], md[u], (int)t, Lout, dv);       // zero past the row end
+      Win::extract(DX[u], mx[u], (int)t - a.pad, L, xv);  // zero outside [0, L)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        acc[KT] += dv[e];
+#pragma unroll
+        for (int k = 0; k < KT; ++k) acc[k] = fmaf(dv[e], xv[e + k], acc[k]);
+      }
     }
   }
+  // only thread 0 writes the row's partials: one LDS exchange for all K+1 sums
 #pragma unroll
-  for (int k = 0; k <= KT; ++k) {
-    const float v = block_sum<DW_NT>(acc[k], red);
-    if (threadIdx.x == 0) a.part[(int64_t)r * (KT + 1) + k] = v;
+  for (int k = 0; k <= KT; ++k) acc[k] = wave_sum(acc[k]);
+  if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+    for (int k = 0; k <= KT; ++k) red[k * (DW_NT / 64) + (threadIdx.x >> 6)] = acc[k];
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int k = 0; k <= KT; ++k) {
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < DW_NT / 64; ++w) v += red[k * (DW_NT / 64) + w];  // block_sum's order
+      a.part[(int64_t)r * (KT + 1) + k] = v;
+    }
   }
 }
 

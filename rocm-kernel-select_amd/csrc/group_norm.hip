@@ -769,6 +769,24 @@ __global__ __launch_bounds__(GN_TP_NT) void gn_bwd_apply_kernel(GnBwdArgs a) {
   const uint32_t g0 = c - c % a.cpg;          // first channel of the group
   const int64_t r0 = n * a.C + g0;            // its row
   const float E = (float)((int64_t)a.cpg * a.S);
+  const T* __restrict__ xr = static_cast<const T*>(a.x) + r * a.S;
+  const T* __restrict__ gr = static_cast<const T*>(a.dy) + r * a.S;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(xr, (uint32_t)(a.S * (int64_t)sizeof(T)));
+  const __amdgpu_buffer_rsrc_t rg = make_rsrc(gr, (uint32_t)(a.S * (int64_t)sizeof(T)));
+  Vec16<T> xv[GN_BWD_U], gv[GN_BWD_U];
+  auto issue = [&](int64_t e0) {
+#pragma unroll
+    for (int u = 0; u < GN_BWD_U; ++u) {
+      const int64_t e = e0 + (int64_t)u * GN_TP_NT * VEC;
+      const uint32_t off = e < a.S ? (uint32_t)(e * (int64_t)sizeof(T)) : kOOB;
+      xv[u].raw = bload16<2>(rx, off, 0);  // last reads of x and dy
+      gv[u].raw = bload16<2>(rg, off, 0);
+    }
+  };
+  // the first batch of x and dy does not depend on the statistics: its loads are issued
+  // before the group merge below, so their latency overlaps it (a C3-sized row is one batch)
+  const int64_t e_first = (int64_t)threadIdx.x * VEC;
+  issue(e_first);
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
     const float* rows = a.rows + r0 * 5;
@@ -801,20 +819,9 @@ __global__ __launch_bounds__(GN_TP_NT) void gn_bwd_apply_kernel(GnBwdArgs a) {
   __syncthreads();
   if (!a.dx) return;
   const float mu = st[0], rstd = st[1], c1 = st[2], c2 = st[3], gam = st[4];
-  const T* __restrict__ xr = static_cast<const T*>(a.x) + r * a.S;
-  const T* __restrict__ gr = static_cast<const T*>(a.dy) + r * a.S;
   T* __restrict__ dxr = static_cast<T*>(a.dx) + r * a.S;
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(xr, (uint32_t)(a.S * (int64_t)sizeof(T)));
-  const __amdgpu_buffer_rsrc_t rg = make_rsrc(gr, (uint32_t)(a.S * (int64_t)sizeof(T)));
-  for (int64_t e0 = (int64_t)threadIdx.x * VEC; e0 < a.S; e0 += (int64_t)GN_TP_NT * VEC * GN_BWD_U) {
-    Vec16<T> xv[GN_BWD_U], gv[GN_BWD_U];
-#pragma unroll
-    for (int u = 0; u < GN_BWD_U; ++u) {
-      const int64_t e = e0 + (int64_t)u * GN_TP_NT * VEC;
-      const uint32_t off = e < a.S ? (uint32_t)(e * (int64_t)sizeof(T)) : kOOB;
-      xv[u].raw = bload16<2>(rx, off, 0);  // last reads of x and dy
-      gv[u].raw = bload16<2>(rg, off, 0);
-    }
+  for (int64_t e0 = e_first; e0 < a.S; e0 += (int64_t)GN_TP_NT * VEC * GN_BWD_U) {
+    if (e0 != e_first) issue(e0);
 #pragma unroll
     for (int u = 0; u < GN_BWD_U; ++u) {
       const int64_t e = e0 + (int64_t)u * GN_TP_NT * VEC;
@@ -1011,6 +1018,22 @@ __global__ __launch_bounds__(GN_CL_NT) void gn_cl_apply_kernel(GnClArgs a) {
   __shared__ float scs[GN_CL_MAXC], shs[GN_CL_MAXC];
   __shared__ float gmean[GN_CL_MAXG], grstd[GN_CL_MAXG];
   const int n = blockIdx.y, ch = blockIdx.x;
+  const int CV = (int)(a.C / VEC), R = GN_CL_NT / CV;
+  const int v = threadIdx.x % CV, rr = threadIdx.x / CV;
+  const int64_t s0 = (int64_t)ch * a.SC, s1 = min(a.S, s0 + a.SC);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(static_cast<const T*>(a.x) + (int64_t)n * a.S * a.C, a.sample_bytes);
+  const uint32_t vb = (uint32_t)(v * VEC * sizeof(T)), rowb = (uint32_t)(a.C * sizeof(T));
+  Vec16<T> xv[GN_CL_U];
+  auto issue = [&](int64_t s) {
+#pragma unroll
+    for (int u = 0; u < GN_CL_U; ++u) {
+      const int64_t sp = s + (int64_t)u * R;
+      xv[u].raw = bload16<2>(rx, sp < s1 ? (uint32_t)sp * rowb + vb : kOOB, 0);  // last read of x
+    }
+  };
+  // the first rows do not depend on the statistics: their loads overlap the prologue
+  const int64_t s_first = s0 + rr;
+  issue(s_first);
   for (int g = threadIdx.x; g < (int)a.G; g += GN_CL_NT) {
     gmean[g] = a.stat[((int64_t)n * a.G + g) * 2];
     grstd[g] = a.stat[((int64_t)n * a.G + g) * 2 + 1];
@@ -1025,28 +1048,15 @@ __global__ __launch_bounds__(GN_CL_NT) void gn_cl_apply_kernel(GnClArgs a) {
     shs[c] = bt - gmean[g] * sc;
   }
   __syncthreads();
-  const int CV = (int)(a.C / VEC), R = GN_CL_NT / CV;
-  const int v = threadIdx.x % CV, rr = threadIdx.x / CV;
-  const int64_t s0 = (int64_t)ch * a.SC, s1 = min(a.S, s0 + a.SC);
-  const int64_t base = (int64_t)n * a.S * a.C + v * VEC;
-  const T* __restrict__ xn = static_cast<const T*>(a.x) + base;
-  T* __restrict__ yn = static_cast<T*>(a.y) + base;
+  T* __restrict__ yn = static_cast<T*>(a.y) + (int64_t)n * a.S * a.C + v * VEC;
   float sc[VEC], sh[VEC];
 #pragma unroll
   for (int k = 0; k < VEC; ++k) {
     sc[k] = scs[v * VEC + k];
     sh[k] = shs[v * VEC + k];
   }
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(static_cast<const T*>(a.x) + (int64_t)n * a.S * a.C, a.sample_bytes);
-  const uint32_t vb = (uint32_t)(v * VEC * sizeof(T)), rowb = (uint32_t)(a.C * sizeof(T));
-  (void)xn;
-  for (int64_t s = s0 + rr; s < s1; s += (int64_t)R * GN_CL_U) {
-    Vec16<T> xv[GN_CL_U];
-#pragma unroll
-    for (int u = 0; u < GN_CL_U; ++u) {
-      const int64_t sp = s + (int64_t)u * R;
-      xv[u].raw = bload16<2>(rx, sp < s1 ? (uint32_t)sp * rowb + vb : kOOB, 0);  // last read of x
-    }
+  for (int64_t s = s_first; s < s1; s += (int64_t)R * GN_CL_U) {
+    if (s != s_first) issue(s);
 #pragma unroll
     for (int u = 0; u < GN_CL_U; ++u) {
       const int64_t sp = s + (int64_t)u * R;
