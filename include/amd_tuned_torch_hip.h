@@ -302,6 +302,21 @@ size_t atk_conv_wgrad_workspace_bytes(int64_t N, int64_t Ci, int64_t D, int64_t 
 int atk_conv_wgrad(const void* x, const void* dy, float* dw, int64_t N, int64_t Ci, int64_t D, int64_t H,
                    int64_t W, int64_t Co, int KD, int dtype, void* workspace, size_t ws_bytes, atk_stream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * Layout conversion between channels-last and channels-first memory (replaces the strided
+ * `.contiguous(memory_format=...)` copies around the channels-last conv candidates; the
+ * reference runs channels-last convs through CK or stock instead, amd_tuned_torch/
+ * _dispatch.py:1840-1920, and has no counterpart kernel): a batched transpose of the last
+ * two axes,
+ *   out[b][c][r] = in[b][r][c],   in: [B, R, C], out: [B, C, R], both dense.
+ * NDHWC [N][S][C] -> NCDHW [N][C][S] is (B, R, C) = (N, S, C); the reverse is (N, C, S).
+ * Any element type of the dtype codes (2 or 4 bytes; the bytes are copied unchanged).
+ * in and out must not overlap.  16-byte vectors when R and C are multiples of a vector and
+ * both bases are 16-byte aligned, element-wise otherwise.  Needs no workspace.
+ * ------------------------------------------------------------------------- */
+int atk_transpose_last2(const void* in, void* out, int64_t B, int64_t R, int64_t C, int dtype,
+                        atk_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -338,14 +338,19 @@ def _conv_accelerated_forward(nd: int, input, weight, bias, stride, padding, dil
     return orig(input, weight, bias, stride, padding, dilation, groups)
 
 
+def _to_ncdhw(t: torch.Tensor) -> torch.Tensor:
+    """Contiguous form of a conv operand: channels-last tensors through the native
+    transpose kernel, anything else through torch."""
+    return _native.channels_last_to_contiguous(t) if _channels_last(t) else t.contiguous()
+
+
 def _in_ncdhw(fn: Callable, cl_out: bool, nd: int) -> Callable:
     """`fn` on contiguous (NC(D)HW) copies of input and weight; the output converted to
-    channels-last when `cl_out`."""
-    fmt = torch.channels_last_3d if nd == 3 else torch.channels_last
+    channels-last when `cl_out`.  The conversions run on the native transpose kernel."""
 
     def run(i, w, b, s, p, d, variant: int = -1):
-        y = fn(i.contiguous(), w.contiguous(), b, s, p, d, variant=variant)
-        return y.contiguous(memory_format=fmt) if cl_out else y
+        y = fn(_to_ncdhw(i), _to_ncdhw(w), b, s, p, d, variant=variant)
+        return _native.contiguous_to_channels_last(y) if cl_out else y
     return run
 
 

@@ -41,7 +41,7 @@ EXPORTED_SYMBOLS = (
     "atk_group_norm_workspace_zero_bytes", "atk_group_norm_fwd", "atk_group_norm_cl_workspace_bytes",
     "atk_group_norm_cl_fwd", "atk_group_norm_bwd_workspace_bytes",
     "atk_group_norm_bwd", "atk_conv_workspace_bytes",
-    "atk_conv_fwd", "atk_conv_wgrad_workspace_bytes", "atk_conv_wgrad",
+    "atk_conv_fwd", "atk_conv_wgrad_workspace_bytes", "atk_conv_wgrad", "atk_transpose_last2",
 )
 
 
@@ -109,6 +109,8 @@ def _declare(lib) -> None:
     lib.atk_conv_wgrad_workspace_bytes.restype = sz
     lib.atk_conv_wgrad.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, i64, i32, i32, vp, sz, vp]
     lib.atk_conv_wgrad.restype = i32
+    lib.atk_transpose_last2.argtypes = [vp, vp, i64, i64, i64, i32, vp]
+    lib.atk_transpose_last2.restype = i32
 
 
 def load(path: str = LIB_PATH):
@@ -596,6 +598,44 @@ def group_norm(input: torch.Tensor, num_groups: int, weight: Optional[torch.Tens
                               _stream(input))
     _check(rc, "group_norm")
     return y
+
+
+def transpose_last2(x: torch.Tensor, B: int, R: int, C: int, out: torch.Tensor) -> torch.Tensor:
+    """out[b][c][r] = x[b][r][c] over the dense memory of x and out (B*R*C elements each,
+    same dtype, no overlap): the layout conversion kernel of atk_transpose_last2."""
+    _require_cuda(x, out)
+    if x.dtype not in _DTYPE_CODE or out.dtype != x.dtype:
+        raise RuntimeError("transpose_last2: float16, bfloat16 or float32 tensors of one dtype")
+    if x.numel() != B * R * C or out.numel() != B * R * C:
+        raise RuntimeError("transpose_last2: element count does not match B*R*C")
+    rc = lib().atk_transpose_last2(_ptr(x), _ptr(out), int(B), int(R), int(C), _DTYPE_CODE[x.dtype],
+                                   _stream(x))
+    _check(rc, "transpose_last2")
+    return out
+
+
+def channels_last_to_contiguous(x: torch.Tensor) -> torch.Tensor:
+    """NC(D)HW-contiguous copy of a channels-last tensor (memory [N][S][C] -> [N][C][S])."""
+    if not is_channels_last(x):
+        raise RuntimeError("channels_last_to_contiguous: input is not channels-last")
+    N, C = x.shape[0], x.shape[1]
+    out = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+    if x.numel() == 0:
+        return out
+    return transpose_last2(x, N, x.numel() // (N * C), C, out)
+
+
+def contiguous_to_channels_last(x: torch.Tensor) -> torch.Tensor:
+    """Channels-last (channels_last / channels_last_3d) copy of an NC(D)HW-contiguous tensor
+    (memory [N][C][S] -> [N][S][C])."""
+    if not x.is_contiguous() or x.dim() not in (4, 5):
+        raise RuntimeError("contiguous_to_channels_last: needs a contiguous 4-D or 5-D tensor")
+    fmt = torch.channels_last if x.dim() == 4 else torch.channels_last_3d
+    out = torch.empty_like(x, memory_format=fmt)
+    if x.numel() == 0:
+        return out
+    N, C = x.shape[0], x.shape[1]
+    return transpose_last2(x, N, C, x.numel() // (N * C), out)
 
 
 def is_channels_last(x: torch.Tensor) -> bool:

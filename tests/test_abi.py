@@ -119,6 +119,13 @@ def test_argument_validation_codes(nat):
     neg = (1, 8, 2, 8, 8, 16, 5, 3, 3, 1, 1, 1, 0, 0, 0, 1, 1, 1)   # output depth <= 0
     assert lib.atk_conv_fwd(None, None, None, None, *neg, 1, 0, None, 0, None) == nat.ATK_EINVAL
     assert lib.atk_conv_fwd(None, None, None, None, *geom, 5, 0, None, 0, None) == nat.ATK_EINVAL
+    # layout transpose: argument checks come before any device work
+    assert lib.atk_transpose_last2(None, None, 2, 3, 4, 7, None) == nat.ATK_EINVAL    # dtype code
+    assert lib.atk_transpose_last2(None, None, 2, -3, 4, 1, None) == nat.ATK_EINVAL   # negative size
+    assert lib.atk_transpose_last2(None, None, 0, 3, 4, 1, None) == nat.ATK_OK        # empty: no-op
+    assert lib.atk_transpose_last2(None, None, 2, 3, 4, 1, None) == nat.ATK_EINVAL    # null pointers
+    assert lib.atk_transpose_last2(4096, 4096, 2, 3, 4, 1, None) == nat.ATK_EINVAL    # in-place
+    assert "alias" in nat.last_error()
 
 
 def _fastdiv(n, d):

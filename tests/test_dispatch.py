@@ -112,10 +112,20 @@ class FakeNative:
             return {_native.OP_CONV: conv_names, _native.OP_GROUP_NORM: list(gn_variants),
                     _native.OP_DWCONV1D: ["lds_opt16"]}[op]
 
+        def to_contiguous(x):
+            self.calls.append(("layout", "to_ncdhw"))
+            return x.contiguous()
+
+        def to_channels_last(x):
+            self.calls.append(("layout", "to_channels_last"))
+            return x.contiguous(memory_format=torch.channels_last if x.dim() == 4 else torch.channels_last_3d)
+
         monkeypatch.setattr(_native, "conv2d", conv(2))
         monkeypatch.setattr(_native, "conv3d", conv(3))
         monkeypatch.setattr(_native, "group_norm", gn)
         monkeypatch.setattr(_native, "variants", variants)
+        monkeypatch.setattr(_native, "channels_last_to_contiguous", to_contiguous)
+        monkeypatch.setattr(_native, "contiguous_to_channels_last", to_channels_last)
         monkeypatch.setattr(_native, "available", lambda: True)
         monkeypatch.setattr(_dispatch, "_variant_cache", {})
         # everything _usable checks except the device (these are CPU tensors)
@@ -210,7 +220,8 @@ def test_conv_channels_last_contests_native_on_nchw_copies(monkeypatch, contest)
     x = torch.randn(1, 4, 6, 6).to(memory_format=torch.channels_last)
     w = torch.randn(5, 4, 3, 3).to(memory_format=torch.channels_last)
     y = F.conv2d(x, w, None, 1, 1)
-    assert set(fake.calls) == {("conv2d", "f32_a")} and seen and set(seen) == {(True, True)}
+    assert set(fake.calls) == {("conv2d", "f32_a"), ("layout", "to_ncdhw"), ("layout", "to_channels_last")}
+    assert seen and set(seen) == {(True, True)}
     assert y.is_contiguous(memory_format=torch.channels_last)
     assert torch.allclose(y, _dispatch._ORIGINALS[(F, "conv2d")](x, w, None, 1, 1), atol=1e-5)
     assert kernel_select.cached("conv2d", x, w, 1, 1, 1) == "native.f32_a"

@@ -263,6 +263,56 @@ def test_channels_last_conv_through_patched_functional(nd, dtype):
     assert y2.is_contiguous(memory_format=fmt) and O.max_rel_err(y2.float().contiguous(), ref) <= bar
 
 
+TRANSPOSE_CASES = [
+    # (B, R, C): vector path, odd rows / columns (element path), partial tiles, one row
+    (2, 4096, 256), (1, 64, 64), (3, 100, 40), (2, 67, 13), (1, 1, 520), (5, 33, 1),
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("case", TRANSPOSE_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_transpose_last2_bit_exact(dtype, case):
+    """atk_transpose_last2 copies every element to its transposed place: bit-exact against
+    torch's transpose on the same buffer, also from a misaligned base (element path)."""
+    nat = _native()
+    B, R, C = case
+    g = torch.Generator().manual_seed(B * 131 + R * 7 + C)
+    x = torch.randn(B * R * C + 1, generator=g).to(dtype).cuda()
+    for base in (x[:-1], x[1:]):          # 16-byte aligned, then offset by one element
+        out = torch.empty(B * C * R + 1, dtype=dtype, device="cuda")[1:]
+        nat.transpose_last2(base, B, R, C, out)
+        ref = base.view(B, R, C).transpose(1, 2).contiguous().view(-1)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16 if dtype != torch.float32 else torch.int32),
+                           ref.view(torch.int16 if dtype != torch.float32 else torch.int32))
+
+
+def test_transpose_last2_many_batches():
+    """More batch entries than the grid's y extent (65535): the kernel strides over them."""
+    nat = _native()
+    B, R, C = 70000, 2, 8
+    x = torch.arange(B * R * C, dtype=torch.float32, device="cuda").to(torch.bfloat16)
+    out = torch.empty_like(x)
+    nat.transpose_last2(x, B, R, C, out)
+    assert torch.equal(out, x.view(B, R, C).transpose(1, 2).contiguous().view(-1))
+
+
+@pytest.mark.parametrize("nd", [2, 3])
+def test_channels_last_round_trip(nd):
+    """channels_last_to_contiguous / contiguous_to_channels_last equal torch's
+    .contiguous(memory_format=...) exactly, and round-trip."""
+    nat = _native()
+    shape = (2, 48, 5, 9, 11) if nd == 3 else (3, 40, 17, 19)
+    fmt = torch.channels_last_3d if nd == 3 else torch.channels_last
+    x = torch.randn(*shape, device="cuda").to(torch.bfloat16)
+    xc = x.contiguous(memory_format=fmt)
+    a = nat.channels_last_to_contiguous(xc)
+    assert a.is_contiguous() and torch.equal(a, x)
+    b = nat.contiguous_to_channels_last(a)
+    assert b.is_contiguous(memory_format=fmt) and not b.is_contiguous()
+    assert torch.equal(b, x) and b.stride() == xc.stride()
+
+
 WGRAD_CASES = [
     # (N, Ci, Co, D, H, W, KD)
     (1, 32, 128, 4, 8, 16, 3),
