@@ -378,7 +378,9 @@ def _dgrad_via_forward(grad_output, weight, pad_t, nd, fwd):
     in (Co, Ci) and flipped in space, padding k-1-p -- so the input gradient runs on the
     forward path (and its per-shape contest) instead of a separate dgrad."""
     wt = weight.transpose(0, 1).flip(list(range(2, 2 + nd))).contiguous()
-    return fwd(grad_output.contiguous(), wt, None, 1, pad_t, 1, 1)
+    # a channels-last dy goes in as is: the forward path converts it with the native transpose
+    dy = grad_output if _channels_last(grad_output) else grad_output.contiguous()
+    return fwd(dy, wt, None, 1, pad_t, 1, 1)
 
 
 def _wgrad_native(input, grad_output, weight, stride, padding, dilation, groups, nd):
@@ -406,7 +408,7 @@ def _wgrad_native(input, grad_output, weight, stride, padding, dilation, groups,
     if g5.dtype != x5.dtype or tuple(g5.shape[2:]) != tuple(x5.shape[2:]):
         return None
     try:
-        dw = _native.conv_wgrad(x5.contiguous(), g5.contiguous(), kd)
+        dw = _native.conv_wgrad(_to_ncdhw(x5), _to_ncdhw(g5), kd)
     except _native.Unsupported:
         return None
     return dw.reshape(weight.shape).to(weight.dtype)

@@ -353,10 +353,12 @@ def test_conv_wgrad_full_size_c5a():
     assert O.max_rel_err(dw, ref) <= 1e-4
 
 
+@pytest.mark.parametrize("channels_last", [False, True], ids=["ncdhw", "channels_last"])
 @pytest.mark.parametrize("nd", [2, 3])
-def test_conv_autograd_native_wgrad(nd):
+def test_conv_autograd_native_wgrad(nd, channels_last):
     """Weight and bias gradients through patched F.conv2d / F.conv3d (bf16) come from the
-    native wgrad kernel and a reduction of dy, against float64 CPU autograd."""
+    native wgrad kernel and a reduction of dy, against float64 CPU autograd; channels-last
+    input, weight and dy take the native layout conversions on the way."""
     import torch.nn.functional as F
     from amd_tuned_torch import _native
     calls = []
@@ -373,10 +375,15 @@ def test_conv_autograd_native_wgrad(nd):
         w = (torch.randn(128, 32, *([3] * nd), generator=g) * 0.05).to(torch.bfloat16)
         b = (torch.randn(128, generator=g) * 0.1).to(torch.bfloat16)
         conv = F.conv3d if nd == 3 else F.conv2d
-        xg, wg, bg = (t.cuda().requires_grad_() for t in (x, w, b))
+        fmt = torch.channels_last_3d if nd == 3 else torch.channels_last
+        lay = (lambda t: t.contiguous(memory_format=fmt)) if channels_last else (lambda t: t)
+        xg, wg = (lay(t.cuda()).requires_grad_() for t in (x, w))
+        bg = b.cuda().requires_grad_()
         y = conv(xg, wg, bg, 1, 1)
+        if channels_last:
+            assert y.is_contiguous(memory_format=fmt)
         dy = torch.randn(y.shape, generator=g).to(torch.bfloat16)
-        y.backward(dy.cuda())
+        y.backward(lay(dy.cuda()))
         xr, wr, br = (t.double().requires_grad_() for t in (x, w, b))
         import amd_tuned_torch
         amd_tuned_torch.disable()
