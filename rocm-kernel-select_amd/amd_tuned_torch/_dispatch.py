@@ -675,19 +675,24 @@ class _GroupNormFn(torch.autograd.Function):
         input, weight = ctx.saved_tensors
         needs = (ctx.needs_input_grad[0], weight is not None and ctx.needs_input_grad[1],
                  ctx.has_bias and ctx.needs_input_grad[2])
-        dy = grad_output.contiguous()
-        if input.is_cuda and input.is_contiguous() and _native.available():
+        cl = _channels_last(input)
+        if input.is_cuda and (input.is_contiguous() or cl) and _native.available():
             try:
-                gx, gw, gb = _native.group_norm_backward(dy, input.detach(), ctx.num_groups,
+                # channels-last x and dy go to NC[S] through the native transpose, and dx
+                # comes back in the input's layout
+                x = _native.channels_last_to_contiguous(input.detach()) if cl else input.detach()
+                gx, gw, gb = _native.group_norm_backward(_to_ncdhw(grad_output), x, ctx.num_groups,
                                                          None if weight is None else weight.detach(),
                                                          ctx.eps, needs)
+                if cl and gx is not None:
+                    gx = _native.contiguous_to_channels_last(gx)
                 gw = None if gw is None else gw.to(weight.dtype)
                 gb = None if gb is None else gb.to(ctx.bias_dtype if ctx.bias_dtype is not None
                                                    else input.dtype)
                 return gx, gw, gb, None, None
             except _native.Unsupported:
                 pass
-        return _group_norm_backward(dy, input, ctx.num_groups, weight,
+        return _group_norm_backward(grad_output.contiguous(), input, ctx.num_groups, weight,
                                     ctx.eps, needs, bias_dtype=ctx.bias_dtype) + (None, None)
 
 

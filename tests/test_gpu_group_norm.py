@@ -278,6 +278,28 @@ def test_group_norm_autograd_through_patched_group_norm(dev, dtype):
         assert O.max_rel_err(gb.cpu(), rdb) <= BAR[dtype]
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_group_norm_autograd_channels_last(dev, dtype):
+    """Channels-last (NHWC / NDHWC) input through the patched F.group_norm with gradients:
+    x and dy reach the native backward through the native layout conversion, dx comes back
+    channels-last; every gradient matches the oracle."""
+    import torch.nn.functional as F
+    import amd_tuned_torch  # noqa: F401
+    for shape, G, fmt in (((2, 64, 8, 8), 8, torch.channels_last),
+                          ((1, 32, 4, 8, 8), 4, torch.channels_last_3d)):
+        x, gm, bt = _inputs(shape, dtype, seed=11 + G)
+        xd = x.to(dev).contiguous(memory_format=fmt).requires_grad_(True)
+        gd, bd = gm.to(dev).requires_grad_(True), bt.to(dev).requires_grad_(True)
+        y = F.group_norm(xd, G, gd, bd, 1e-5)
+        dy = torch.randn(*shape, generator=torch.Generator().manual_seed(5)).to(dtype)
+        gx, gg, gb = torch.autograd.grad(y, (xd, gd, bd), dy.to(dev).contiguous(memory_format=fmt))
+        assert gx.is_contiguous(memory_format=fmt)
+        rdx, rdg, rdb = O.group_norm_bwd(x, G, gm, dy, 1e-5)
+        assert O.max_rel_err(gx.cpu().contiguous(), rdx) <= BAR[dtype]
+        assert O.max_rel_err(gg.cpu(), rdg) <= BAR[dtype]
+        assert O.max_rel_err(gb.cpu(), rdb) <= BAR[dtype]
+
+
 def test_group_norm_backward_c3_full_size(dev):
     """C3's NCDHW shape at full size, bf16: every gradient element against the oracle."""
     nat = _native()
