@@ -547,29 +547,33 @@ __global__ __launch_bounds__(256) void pack_weights_kernel(const T* __restrict__
                                                            int Co, int Ci, int taps, int n_kb,
                                                            int co_blocks, uint32_t chunks) {
   // one thread per 16-byte chunk of the packed layout [tap][kb][co_block][32][KB] (KB is a
-  // multiple of the chunk's E elements, so a chunk never crosses a row); 32-bit index math
-  // (the host keeps the packed weights under 2 GiB)
+  // multiple of the chunk's E elements, so a chunk never crosses a row).  Consecutive threads
+  // take consecutive taps of one chunk position: tap is w's contiguous axis, so each of the E
+  // loads of a wave reads a few contiguous runs instead of 64 rows Ci*taps apart; only the one
+  // 16-byte store per thread is scattered.  32-bit index math (the host keeps the packed
+  // weights under 2 GiB).
   constexpr int KB = MfmaTraits<T>::KB;
   constexpr int E = 16 / sizeof(T);
+  constexpr uint32_t KPR = KB / E;  // chunks per packed row
   const uint32_t c = blockIdx.x * 256 + threadIdx.x;
   if (c >= chunks) return;
-  const uint32_t i = c * E;
-  const uint32_t k0 = i % KB;
-  uint32_t r = i / KB;
+  const uint32_t tap = c % (uint32_t)taps;
+  uint32_t r = c / (uint32_t)taps;
+  const uint32_t k8 = r % KPR;
+  r /= KPR;
   const uint32_t row = r % 32;
   r /= 32;
   const uint32_t cb = r % (uint32_t)co_blocks;
-  r /= (uint32_t)co_blocks;
-  const uint32_t kb = r % (uint32_t)n_kb;
-  const uint32_t tap = r / (uint32_t)n_kb;
+  const uint32_t kb = r / (uint32_t)co_blocks;
   const int co = (int)(cb * 32 + row);
+  const uint32_t dst = ((((tap * (uint32_t)n_kb + kb) * (uint32_t)co_blocks + cb) * 32 + row) * KPR + k8) * E;
   Vec16<T> v;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    const int ci = (int)(kb * KB + k0) + e;
+    const int ci = (int)(kb * KB + k8 * E) + e;
     v.e[e] = (co < Co && ci < Ci) ? w[((int64_t)co * Ci + ci) * taps + tap] : static_cast<T>(0.0f);
   }
-  *reinterpret_cast<uint4*>(wp + i) = v.raw;
+  *reinterpret_cast<uint4*>(wp + dst) = v.raw;
 }
 
 // y = sum over splits of the fp32 partials + bias
