@@ -52,7 +52,7 @@ constexpr size_t GN_SLOTS_OFF = 256 + 8 * (size_t)GN_MAX_SLOTTED;
 constexpr size_t GN_ZERO_BYTES = GN_SLOTS_OFF + 16 * (size_t)GN_MAX_SLOTS;
 constexpr size_t GN_PARTIALS_OFF = GN_ZERO_BYTES;
 constexpr int GN_TP_NT = 256;                 // two-pass kernels
-constexpr int GN_BWD_U = 4;                   // backward: vectors of x and dy in flight per thread
+constexpr int GN_BWD_U = 4;                   // backward: vectors of x and dy in flight per thread (most)
 constexpr int GN_MAX_AFF = 512;               // channels per slice whose affine is staged in LDS
 
 // One slot = two 64-bit words (1 << 32 | bits(mean)), (1 << 32 | bits(M2)), each stored
@@ -690,7 +690,7 @@ struct GnBwdArgs {
   int pdt;
 };
 
-template <typename T>
+template <typename T, int U>
 __global__ __launch_bounds__(GN_TP_NT) void gn_bwd_rows_kernel(GnBwdArgs a) {
   constexpr int VEC = 16 / sizeof(T);
   __shared__ float red[4 * (GN_TP_NT / 64)];
@@ -699,21 +699,21 @@ __global__ __launch_bounds__(GN_TP_NT) void gn_bwd_rows_kernel(GnBwdArgs a) {
   const T* __restrict__ gr = static_cast<const T*>(a.dy) + r * a.S;
   const float K = to_f32(xr[0]);
   float s1 = 0.f, s2 = 0.f, sa = 0.f, sb = 0.f;
-  // GN_BWD_U vectors of x and of dy in flight per thread (branch-free buffer loads; vectors
+  // U vectors of x and of dy in flight per thread (branch-free buffer loads; vectors
   // past the row read zero and are masked out of the sums)
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(xr, (uint32_t)(a.S * (int64_t)sizeof(T)));
   const __amdgpu_buffer_rsrc_t rg = make_rsrc(gr, (uint32_t)(a.S * (int64_t)sizeof(T)));
-  for (int64_t e0 = (int64_t)threadIdx.x * VEC; e0 < a.S; e0 += (int64_t)GN_TP_NT * VEC * GN_BWD_U) {
-    Vec16<T> xv[GN_BWD_U], gv[GN_BWD_U];
+  for (int64_t e0 = (int64_t)threadIdx.x * VEC; e0 < a.S; e0 += (int64_t)GN_TP_NT * VEC * U) {
+    Vec16<T> xv[U], gv[U];
 #pragma unroll
-    for (int u = 0; u < GN_BWD_U; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int64_t e = e0 + (int64_t)u * GN_TP_NT * VEC;
       const uint32_t off = e < a.S ? (uint32_t)(e * (int64_t)sizeof(T)) : kOOB;
       xv[u].raw = bload16(rx, off, 0);  // cached: the apply kernel reads x and dy again
       gv[u].raw = bload16(rg, off, 0);
     }
 #pragma unroll
-    for (int u = 0; u < GN_BWD_U; ++u) {
+    for (int u = 0; u < U; ++u) {
       const float m = (e0 + (int64_t)u * GN_TP_NT * VEC < a.S) ? 1.f : 0.f;
 #pragma unroll
       for (int k = 0; k < VEC; ++k) {
@@ -759,7 +759,7 @@ __global__ __launch_bounds__(GN_TP_NT) void gn_bwd_rows_kernel(GnBwdArgs a) {
   }
 }
 
-template <typename T>
+template <typename T, int U>
 __global__ __launch_bounds__(GN_TP_NT) void gn_bwd_apply_kernel(GnBwdArgs a) {
   constexpr int VEC = 16 / sizeof(T);
   __shared__ float st[5];  // mu, rstd, c1, c2, gamma_c
@@ -773,10 +773,10 @@ __global__ __launch_bounds__(GN_TP_NT) void gn_bwd_apply_kernel(GnBwdArgs a) {
   const T* __restrict__ gr = static_cast<const T*>(a.dy) + r * a.S;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(xr, (uint32_t)(a.S * (int64_t)sizeof(T)));
   const __amdgpu_buffer_rsrc_t rg = make_rsrc(gr, (uint32_t)(a.S * (int64_t)sizeof(T)));
-  Vec16<T> xv[GN_BWD_U], gv[GN_BWD_U];
+  Vec16<T> xv[U], gv[U];
   auto issue = [&](int64_t e0) {
 #pragma unroll
-    for (int u = 0; u < GN_BWD_U; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int64_t e = e0 + (int64_t)u * GN_TP_NT * VEC;
       const uint32_t off = e < a.S ? (uint32_t)(e * (int64_t)sizeof(T)) : kOOB;
       xv[u].raw = bload16<2>(rx, off, 0);  // last reads of x and dy
@@ -820,10 +820,10 @@ __global__ __launch_bounds__(GN_TP_NT) void gn_bwd_apply_kernel(GnBwdArgs a) {
   if (!a.dx) return;
   const float mu = st[0], rstd = st[1], c1 = st[2], c2 = st[3], gam = st[4];
   T* __restrict__ dxr = static_cast<T*>(a.dx) + r * a.S;
-  for (int64_t e0 = e_first; e0 < a.S; e0 += (int64_t)GN_TP_NT * VEC * GN_BWD_U) {
+  for (int64_t e0 = e_first; e0 < a.S; e0 += (int64_t)GN_TP_NT * VEC * U) {
     if (e0 != e_first) issue(e0);
 #pragma unroll
-    for (int u = 0; u < GN_BWD_U; ++u) {
+    for (int u = 0; u < U; ++u) {
       const int64_t e = e0 + (int64_t)u * GN_TP_NT * VEC;
       float o[VEC];
 #pragma unroll
@@ -849,13 +849,22 @@ __global__ __launch_bounds__(256) void gn_bwd_finalize_kernel(GnBwdArgs a) {
   if (a.dbeta) a.dbeta[c] = sbt;
 }
 
+template <typename T, int U>
+void launch_gn_bwd_u(const GnBwdArgs& a, int64_t rows, hipStream_t s) {
+  hipLaunchKernelGGL((gn_bwd_rows_kernel<T, U>), dim3((unsigned)rows), dim3(GN_TP_NT), 0, s, a);
+  hipLaunchKernelGGL((gn_bwd_apply_kernel<T, U>), dim3((unsigned)rows), dim3(GN_TP_NT), 0, s, a);
+}
+
 template <typename T>
 int launch_gn_bwd(const GnBwdArgs& a, int64_t rows, hipStream_t s) {
-  hipLaunchKernelGGL((gn_bwd_rows_kernel<T>), dim3((unsigned)rows), dim3(GN_TP_NT), 0, s, a);
-  int rc = check_launch("gn_bwd_rows_kernel");
-  if (rc) return rc;
-  hipLaunchKernelGGL((gn_bwd_apply_kernel<T>), dim3((unsigned)rows), dim3(GN_TP_NT), 0, s, a);
-  rc = check_launch("gn_bwd_apply_kernel");
+  // vectors per thread and batch: no more than a row holds (C3a's 4096-element rows are two
+  // per thread; four would leave half the loads reading past the row)
+  constexpr int VEC = 16 / sizeof(T);
+  const int64_t vpt = (a.S + (int64_t)GN_TP_NT * VEC - 1) / ((int64_t)GN_TP_NT * VEC);
+  if (vpt <= 1) launch_gn_bwd_u<T, 1>(a, rows, s);
+  else if (vpt <= 2) launch_gn_bwd_u<T, 2>(a, rows, s);
+  else launch_gn_bwd_u<T, GN_BWD_U>(a, rows, s);
+  const int rc = check_launch("gn_bwd_rows_kernel / gn_bwd_apply_kernel");
   if (rc) return rc;
   if (!a.dgamma && !a.dbeta) return ATK_OK;
   hipLaunchKernelGGL(gn_bwd_finalize_kernel, dim3((a.C + 255) / 256), dim3(256), 0, s, a);
