@@ -762,9 +762,10 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_bwd_w_kernel(DwBwdArgs a) {
   using Win = DwWindow<T, KT>;
   using Dyw = DwWindow<T, 1>;
   constexpr int VEC = Win::VEC, WN = Win::WN;
-  // output vectors fetched per thread before any is used (4 measured slower than 1 on
-  // config 2's 8195-output rows)
-  constexpr int BWD_U = 1;
+  // output vectors fetched per thread before any is used: config 2's 8195-output rows take 5
+  // serial load rounds with 1, 3 with 2; 2 measured level with or up to 3% faster than 1 over
+  // the whole backward, 4 (more registers, fewer resident workgroups) 8% slower
+  constexpr int BWD_U = 2;
   __shared__ float red[(KT + 1) * (DW_NT / 64)];
   const uint32_t r = blockIdx.x;  // row n*C + c
   const uint32_t L = a.L, Lout = a.Lout;
