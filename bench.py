@@ -688,6 +688,84 @@ def traffic_probe(variants: str, iters: int = 10):
     log("traffic probe done")
 
 
+# conv tiles profiled by --conv-probe: (label, x shape, w shape, padding, dtype name, variant)
+CONV_PROBE = [
+    ("C4s fp16", (1, 64, 16, 32, 32), (64, 64, 3, 3, 3), 1, "float16", "h_w14_f22_cb32"),
+    ("C4b bf16", (2, 128, 16, 64, 64), (128, 128, 3, 3, 3), 1, "bfloat16", "h_w22_f24_cb16"),
+    ("C5a bf16", (1, 256, 8, 64, 64), (256, 256, 3, 3, 3), 1, "bfloat16", "h_w41_f22_cb32"),
+    ("C5b fp16", (1, 64, 16, 32, 32), (64, 64, 7, 7, 7), 3, "float16", "h_w14_f22_cb16x2"),
+]
+
+
+def conv_probe(iters: int = 10):
+    """Workload for the MFMA counter pass: `iters` launches of each CONV_PROBE tile (the
+    per-shape contest's usual winners) through the C ABI."""
+    import torch
+    from amd_tuned_torch import _native as nat
+    dev = torch.device("cuda", 0)
+    names = nat.variants(nat.OP_CONV)
+    for label, xs, ws, pad, dt, vn in CONV_PROBE:
+        dtype = getattr(torch, dt)
+        g = _gen(1004)
+        x = torch.randn(*xs, generator=g).to(dtype).to(dev)
+        w = (torch.randn(*ws, generator=g) * math.sqrt(2.0 / math.prod(ws[1:]))).to(dtype).to(dev)
+        b = (0.1 * torch.randn(ws[0], generator=g)).to(dtype).to(dev)
+        out = nat.conv3d(x, w, b, 1, pad, 1, variant=names.index(vn))
+        for _ in range(iters):
+            nat.conv3d(x, w, b, 1, pad, 1, variant=names.index(vn), out=out)
+        torch.cuda.synchronize()
+        log(f"conv probe {label} {vn} done")
+
+
+def summarize_mfma(run_dir: str, out_path: str, command: str, iters: int = 10):
+    """MFMA utilisation of the CONV_PROBE conv kernels from one rocprofv3 --pmc run
+    (SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_VALU_MFMA_MOPS_F16/BF16, with --kernel-trace for the
+    durations of the same dispatches).  The probe launches each tile iters + 1 times in
+    CONV_PROBE order, so the conv_igemm dispatches are attributed by order (the trace names
+    some instantiations mangled and some not).  MFMA busy % = busy cycles summed over the
+    SIMDs / (SIMDs x duration x engine clock); counted MFMA FLOPs = MOPS x 512."""
+    import csv
+    import glob
+    per: "dict[int, dict]" = {}
+    for f in glob.glob(os.path.join(run_dir, "**", "*counter_collection.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            if "conv_igemm_kernel" not in r["Kernel_Name"]:
+                continue
+            d = per.setdefault(int(r["Dispatch_Id"]), {"name": r["Kernel_Name"],
+                                                        "ns": float(r["End_Timestamp"]) - float(r["Start_Timestamp"])})
+            d[r["Counter_Name"]] = float(r["Counter_Value"])
+    simds, clk_mhz = 1024, 2400.0
+    for f in glob.glob(os.path.join(run_dir, "**", "*agent_info.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            if r.get("Agent_Type") == "GPU":
+                simds = int(r["Simd_Count"]) or simds
+                clk_mhz = float(r["Max_Engine_Clk_Fcompute"]) or clk_mhz
+    order = [per[k] for k in sorted(per)]
+    n = iters + 1
+    lines = ["# MFMA utilisation of the conv implicit-GEMM kernels (rocprofv3 --pmc, one pass)",
+             f"# command: {command}",
+             f"# {simds} SIMDs at {clk_mhz:.0f} MHz; mfma_busy% = sum SQ_VALU_MFMA_BUSY_CYCLES / "
+             "(SIMDs x duration x clock); counted = (MOPS_F16 + MOPS_BF16) x 512 / algorithmic FLOPs",
+             f"# {'calls':>5} {'avg_us':>8} {'algo_TF/s':>9} {'of_peak':>7} {'mfma_busy%':>10} {'counted':>7}  config / kernel"]
+    if len(order) != n * len(CONV_PROBE):
+        lines.append(f"  ({len(order)} conv dispatches, expected {n * len(CONV_PROBE)}: not attributed)")
+    else:
+        for j, (label, xs, ws, pad, dt, vn) in enumerate(CONV_PROBE):
+            chunk = order[j * n:(j + 1) * n]
+            ns = sum(d["ns"] for d in chunk) / n
+            busy = sum(d.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) for d in chunk) / n
+            mops = sum(d.get("SQ_INSTS_VALU_MFMA_MOPS_F16", 0.0) + d.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0)
+                       for d in chunk) / n
+            algo = 2.0 * xs[0] * ws[0] * math.prod(xs[2:]) * math.prod(ws[1:])  # stride 1, 'same'
+            tfs = algo / ns / 1e3
+            lines.append(f"  {n:5d} {ns / 1e3:8.2f} {tfs:9.1f} {tfs / MFMA_PEAK_TFLOPS['bf16']:7.3f} "
+                         f"{100.0 * busy / (simds * ns * 1e-9 * clk_mhz * 1e6):10.1f} {mops * 512 / algo:7.3f}"
+                         f"  {label} {vn}: {chunk[0]['name'][:100]}")
+    with open(out_path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def _counter_means(run_dir: str, counter: str) -> "dict[str, float]":
     """Mean per-dispatch value of `counter` for each kernel name in a rocprofv3 --pmc run."""
     import csv
@@ -801,12 +879,19 @@ def main():
     ap.add_argument("--variant", default="xlane,lds_opt32_nt",
                     help="dwconv1d variants (comma-separated, one per kernel) for --traffic-probe")
     ap.add_argument("--command", default="", help="command line recorded by --summarize-traffic")
+    ap.add_argument("--conv-probe", action="store_true",
+                    help="run only the workload of the MFMA counter pass (CONV_PROBE conv tiles)")
+    ap.add_argument("--summarize-mfma", nargs=2, metavar=("PMC_DIR", "OUT"),
+                    help="write the MFMA utilisation summary from a rocprofv3 --pmc output folder")
     args = ap.parse_args()
     if args.summarize_stats:
         summarize_stats(*args.summarize_stats, args.command, name_filter=args.summarize_filter)
         return
     if args.summarize_traffic:
         summarize_traffic(*args.summarize_traffic, args.variant, args.command)
+        return
+    if args.summarize_mfma:
+        summarize_mfma(*args.summarize_mfma, args.command)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; the hot path has no multi-GPU component "
@@ -822,6 +907,9 @@ def main():
     dev = torch.device("cuda", 0)
     if args.traffic_probe:
         traffic_probe(args.variant)
+        return
+    if args.conv_probe:
+        conv_probe()
         return
 
     # ---- headline: causal depthwise conv1d bf16 (config 2) --------------------------
