@@ -717,6 +717,87 @@ def conv_probe(iters: int = 10):
         log(f"conv probe {label} {vn} done")
 
 
+# GroupNorm kernels profiled by --gn-probe: (label, shape, eps, silu, variant); bf16, G = 32
+GN_PROBE = [
+    ("C3a bf16", (8, 512, 64, 64), 1e-5, False, "res_nt1024_v8"),
+    ("C3a bf16 +SiLU", (8, 512, 64, 64), 1e-5, True, "res_nt1024_v8"),
+    ("C3b bf16", (1, 512, 16, 64, 64), 1e-5, False, "res_nt512_v16"),
+    ("C5 bf16 +SiLU", (1, 256, 8, 64, 64), 1e-6, True, "res_nt1024_v4"),
+]
+
+
+def gn_probe(iters: int = 10):
+    """Workload for the GroupNorm traffic passes: `iters` launches of each GN_PROBE kernel in
+    order, then `iters` launches of the torch.neg calibration copy (as traffic_probe)."""
+    import torch
+    from amd_tuned_torch import _native as nat
+    dev = torch.device("cuda", 0)
+    names = nat.variants(nat.OP_GROUP_NORM)
+    for label, shape, eps, silu, vn in GN_PROBE:
+        g = _gen(1003)
+        C = shape[1]
+        x = torch.randn(*shape, generator=g).to(torch.bfloat16).to(dev)
+        gm = (1 + 0.1 * torch.randn(C, generator=g)).to(torch.bfloat16).to(dev)
+        bt = (0.1 * torch.randn(C, generator=g)).to(torch.bfloat16).to(dev)
+        out = torch.empty_like(x)
+        for _ in range(iters):
+            nat.group_norm(x, 32, gm, bt, eps, silu=silu, variant=names.index(vn), out=out)
+        torch.cuda.synchronize()
+        log(f"gn probe {label} {vn} done")
+    src = torch.randn(CALIB_ELEMS, device=dev, dtype=torch.bfloat16)
+    dst = torch.empty_like(src)
+    for _ in range(iters):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    log("gn probe done")
+
+
+def _dispatch_counter(run_dir: str, counter: str, needle: str) -> "list[tuple[int, str, float]]":
+    """(dispatch id, kernel name, value) of `counter` for the dispatches whose kernel name
+    contains `needle`, in dispatch order."""
+    import csv
+    import glob
+    out = []
+    for f in glob.glob(os.path.join(run_dir, "**", "*counter_collection.csv"), recursive=True):
+        for r in csv.DictReader(open(f)):
+            if r["Counter_Name"] == counter and needle in r["Kernel_Name"]:
+                out.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"])))
+    return sorted(out)
+
+
+def summarize_gn_traffic(fetch_dir: str, write_dir: str, out_path: str, command: str, iters: int = 10):
+    """HBM traffic per launch of the GN_PROBE GroupNorm kernels from a FETCH_SIZE pass and a
+    WRITE_SIZE pass over `bench.py --gn-probe`, each scaled by what the counter reads for the
+    torch.neg copy of known size in the same run.  Dispatches are attributed by order."""
+    rows = {}
+    for tag, run_dir, counter in (("fetch", fetch_dir, "FETCH_SIZE"), ("write", write_dir, "WRITE_SIZE")):
+        gn = _dispatch_counter(run_dir, counter, "gn_resident_kernel")
+        neg = [v for _, _, v in _dispatch_counter(run_dir, counter, "neg")]
+        if len(gn) != iters * len(GN_PROBE) or not neg:
+            raise SystemExit(f"{counter}: {len(gn)} GroupNorm dispatches, {len(neg)} calibration ones")
+        rows[tag] = (gn, sum(neg) / len(neg))
+    calib_bytes = CALIB_ELEMS * 2
+    f_scale = rows["fetch"][1] * 1024.0 / calib_bytes
+    w_scale = rows["write"][1] * 1024.0 / calib_bytes
+    lines = ["# HBM traffic per launch of the register-resident GroupNorm kernels (bf16, G = 32)",
+             f"# commands: {command}",
+             f"# FETCH_SIZE scale {f_scale:.4f}, WRITE_SIZE scale {w_scale:.4f} (counter KiB x 1024 per true "
+             f"byte, from torch.neg over {calib_bytes} B read + written in the same runs)",
+             f"# {'read_MB':>8} {'write_MB':>8} {'algo_MB':>8} {'traffic/algo':>12}  config / kernel"]
+    for j, (label, shape, eps, silu, vn) in enumerate(GN_PROBE):
+        fk = [v for _, _, v in rows["fetch"][0][j * iters:(j + 1) * iters]]
+        wk = [v for _, _, v in rows["write"][0][j * iters:(j + 1) * iters]]
+        rd = sum(fk) / iters * 1024.0 / f_scale
+        wr = sum(wk) / iters * 1024.0 / w_scale
+        algo = 2 * math.prod(shape) * 2
+        name = rows["fetch"][0][j * iters][1]
+        lines.append(f"  {rd / 1e6:8.2f} {wr / 1e6:8.2f} {algo / 1e6:8.2f} {(rd + wr) / algo:12.4f}  "
+                     f"{label} {vn}: {name[:100]}")
+    with open(out_path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def summarize_mfma(run_dir: str, out_path: str, command: str, iters: int = 10):
     """MFMA utilisation of the CONV_PROBE conv kernels from one rocprofv3 --pmc run
     (SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_VALU_MFMA_MOPS_F16/BF16, with --kernel-trace for the
@@ -883,6 +964,10 @@ def main():
                     help="run only the workload of the MFMA counter pass (CONV_PROBE conv tiles)")
     ap.add_argument("--summarize-mfma", nargs=2, metavar=("PMC_DIR", "OUT"),
                     help="write the MFMA utilisation summary from a rocprofv3 --pmc output folder")
+    ap.add_argument("--gn-probe", action="store_true",
+                    help="run only the workload of the GroupNorm traffic passes (GN_PROBE kernels)")
+    ap.add_argument("--summarize-gn-traffic", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "OUT"),
+                    help="write the GroupNorm traffic summary from the two rocprofv3 --pmc folders")
     args = ap.parse_args()
     if args.summarize_stats:
         summarize_stats(*args.summarize_stats, args.command, name_filter=args.summarize_filter)
@@ -892,6 +977,9 @@ def main():
         return
     if args.summarize_mfma:
         summarize_mfma(*args.summarize_mfma, args.command)
+        return
+    if args.summarize_gn_traffic:
+        summarize_gn_traffic(*args.summarize_gn_traffic, args.command)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; the hot path has no multi-GPU component "
@@ -910,6 +998,9 @@ def main():
         return
     if args.conv_probe:
         conv_probe()
+        return
+    if args.gn_probe:
+        gn_probe()
         return
 
     # ---- headline: causal depthwise conv1d bf16 (config 2) --------------------------
