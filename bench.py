@@ -149,9 +149,9 @@ def bench_dw_detail(dtype, mode, dev):
 # configs 3 / 5: GroupNorm
 # ---------------------------------------------------------------------------
 def bench_dw_backward_detail(dev):
-    """Backward of the headline (causal, stock output shape, bf16): dx through the forward
-    kernel with reversed weights, dw / db through the streaming reduction kernel.
-    Algorithmic bytes: dy read twice (once per kernel), x read once, dx written once."""
+    """Backward of the headline (causal, stock output shape, bf16): dx, dw and db in one pass
+    (dwconv1d_bwd_fused_kernel + the per-channel finalize).  Algorithmic bytes: x and dy read
+    once, dx written once."""
     import torch
     from amd_tuned_torch import _native as nat
     x, w, b = c2_inputs(torch.bfloat16, 4, dev)
@@ -171,10 +171,10 @@ def bench_dw_backward_detail(dev):
     ms = graph_time_ms(lambda: nat.dwconv1d_backward(dy, x, w2, pad, (True, True, True)), 10)
     stock_ms = event_time_ms(lambda: torch.ops.aten.convolution_backward(
         dy, xp, w, [C], [1], [0], [1], False, [0], C, [True, True, True]), 3)
-    nbytes = x.element_size() * N * C * (2 * (L + K - 1) + 2 * L)
+    nbytes = x.element_size() * N * C * ((L + K - 1) + 2 * L)
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"ms": round(ms, 4), "GB/s": round(gbs, 1), "roofline_frac": round(gbs / HBM_PEAK_GBS, 4),
-            "variant": "native.xlane(dx) + dwconv1d_bwd_w_kernel(dw, db)",
+            "variant": "native dwconv1d_bwd_fused_kernel (dx, dw, db in one pass) + finalize",
             "stock_convolution_backward_ms": round(stock_ms, 3),
             "max_rel_err_vs_stock": float(f"{err:.3g}")}
 

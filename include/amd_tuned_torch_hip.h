@@ -199,6 +199,24 @@ int atk_causal_conv1d_cl_bwd(const void* x, const void* dout, const void* w, con
                              int w_dtype, int silu, void* workspace, size_t ws_bytes, atk_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Depthwise conv1d backward in one pass (replaces `conv1d_backward(dout, u, weight, bias,
+ * padding, is_bhl=True)`, _vendor/flashfftconv_depthwise_conv1d/conv1d_bwd_hip_bhl.hip:39-116,
+ * behind amd_tuned_torch/depthwise_conv1d_ops.py's backward, and the (B, C, L) backward of a
+ * depthwise F.conv1d): for y = dwconv1d(x, w, bias, pad_left, L_out),
+ *   dx[n,c,s] = sum_j w[c,j] * dy[n,c,s+pad_left-j],
+ *   dw[c,j]   = sum_{n,t} dy[n,c,t] * x[n,c,t-pad_left+j],   db[c] = sum_{n,t} dy[n,c,t],
+ * x, dx [N,C,L]; dy [N,C,L_out]; w [C,K] of `dtype`; dw [C,K], db [C] fp32.  x and dy are
+ * read once (atk_dwconv1d_fwd on dy plus atk_dwconv1d_bwd_weight read dy twice).  dw / db
+ * may be NULL (dx only; db needs dw), and then no workspace is needed; otherwise the
+ * workspace is atk_dwconv1d_bwd_weight_workspace_bytes(N, C, K), no initialisation.
+ * K in [1, 5], pad_left <= 64; dx rows must be 16-byte aligned (L * sizeof(dtype) a
+ * multiple of 16 and an aligned dx), else ATK_UNSUPPORTED.  Sums over n in a fixed order.
+ * ------------------------------------------------------------------------- */
+int atk_dwconv1d_bwd(const void* x, const void* dy, const void* w, void* dx, float* dw, float* db,
+                     int64_t N, int64_t C, int64_t L, int K, int pad_left, int64_t L_out, int dtype,
+                     void* workspace, size_t workspace_bytes, atk_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * GroupNorm forward, NC[spatial] layout (replaces `group_norm(input, num_groups,
  * weight?, bias?, eps)`, src/main_rocm.cpp:556-599 -> src/cuda/group_norm.cu:41-136,
  * and the fused GroupNorm+SiLU of amd_tuned_torch/conv_fusion_ops.py:192-275):

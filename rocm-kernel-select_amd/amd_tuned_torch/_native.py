@@ -42,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "atk_group_norm_cl_fwd", "atk_group_norm_bwd_workspace_bytes",
     "atk_group_norm_bwd", "atk_conv_workspace_bytes",
     "atk_conv_fwd", "atk_conv_wgrad_workspace_bytes", "atk_conv_wgrad", "atk_transpose_last2",
+    "atk_dwconv1d_bwd",
 )
 
 
@@ -111,6 +112,8 @@ def _declare(lib) -> None:
     lib.atk_conv_wgrad.restype = i32
     lib.atk_transpose_last2.argtypes = [vp, vp, i64, i64, i64, i32, vp]
     lib.atk_transpose_last2.restype = i32
+    lib.atk_dwconv1d_bwd.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i32, i32, i64, i32, vp, sz, vp]
+    lib.atk_dwconv1d_bwd.restype = i32
 
 
 def load(path: str = LIB_PATH):
@@ -501,6 +504,31 @@ def causal_conv1d_cl_bwd(x: torch.Tensor, dout: torch.Tensor, weight_dk: torch.T
     return dx, dw, db
 
 
+def _dwconv1d_backward_fused(dy: torch.Tensor, x: torch.Tensor, w: torch.Tensor, pad_left: int, needs):
+    """(dx, dw, db) through atk_dwconv1d_bwd: x [N,C,L], dy [N,C,L_out], w [C,K] (x's dtype).
+    Raises Unsupported where the fused kernel declines (K > 5, unaligned dx rows, ...)."""
+    _require_cuda(x, dy, w)
+    if x.dim() != 3 or dy.dim() != 3 or dy.shape[:2] != x.shape[:2] or w.shape[0] != x.shape[1]:
+        raise RuntimeError("dwconv1d_backward expects x [N, C, L], dy [N, C, L_out], w [C, K]")
+    if x.dtype not in _DTYPE_CODE or dy.dtype != x.dtype or w.dtype != x.dtype:
+        raise Unsupported("dwconv1d_backward: x, dy and w of one float16/bfloat16/float32 dtype")
+    x, dy, w = x.contiguous(), dy.contiguous(), w.contiguous()
+    N, C, L = x.shape
+    K = w.shape[1]
+    dx = torch.empty_like(x)
+    dw = torch.empty((C, K), dtype=torch.float32, device=x.device) if (needs[1] or needs[2]) else None
+    db = torch.empty((C,), dtype=torch.float32, device=x.device) if needs[2] else None
+    L_ = lib()
+    ws = None
+    if dw is not None:
+        ws = workspace(x.device, "dwconv1d_bwd", L_.atk_dwconv1d_bwd_weight_workspace_bytes(N, C, K))
+    rc = L_.atk_dwconv1d_bwd(_ptr(x), _ptr(dy), _ptr(w), _ptr(dx), _ptr(dw), _ptr(db), N, C, L, K, int(pad_left),
+                             dy.shape[-1], _DTYPE_CODE[x.dtype], _ptr(ws), ws.numel() if ws is not None else 0,
+                             _stream(x))
+    _check(rc, "dwconv1d_backward")
+    return dx, (dw if needs[1] else None), db
+
+
 def dwconv1d_backward(dy: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, pad_left: int,
                       needs=(True, True, False)):
     """(dx, dw, db) of y = dwconv1d(x, weight, bias, pad_left, L_out) for dy [N,C,L_out]:
@@ -509,6 +537,11 @@ def dwconv1d_backward(dy: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, p
     Entries not asked for in `needs` are None.  Raises Unsupported when pad_left > K-1
     (dx) or K > 5 (dw, db)."""
     K = weight.shape[-1]
+    if needs[0]:
+        try:  # one pass over x and dy for dx (and dw / db)
+            return _dwconv1d_backward_fused(dy, x, weight.reshape(weight.shape[0], K), pad_left, needs)
+        except Unsupported:
+            pass
     dx = dw = db = None
     if needs[0]:
         if pad_left > K - 1:

@@ -102,16 +102,17 @@ def _backward(dout, input_, weight, bias, padding: int, is_bhl: bool):
     elif input_.is_cuda and _native.available():
         dout = dout.contiguous()
         K = weight.shape[-1]
-        try:
-            if padding <= K - 1:
-                du = _native.dwconv1d_backward(dout, input_, weight, padding, (True, False, False))[0]
-        except _native.Unsupported:
-            du = None
-        try:
-            _, dw32, db32 = _native.dwconv1d_backward(dout, input_, weight, padding, (False, True, True))
+        try:  # du, dw and db together (one pass over x and dout where the fused kernel applies)
+            du, dw32, db32 = _native.dwconv1d_backward(dout, input_, weight, padding, (True, True, True))
             dw, db = dw32.to(weight.dtype), db32.to(dout.dtype)
         except _native.Unsupported:
-            dw = db = None
+            du = dw = db = None
+        if du is None:
+            try:
+                _, dw32, db32 = _native.dwconv1d_backward(dout, input_, weight, padding, (False, True, True))
+                dw, db = dw32.to(weight.dtype), db32.to(dout.dtype)
+            except _native.Unsupported:
+                dw = db = None
     if du is None or dw is None:
         su, sw, sb = _stock_backward(dout, input_, weight, bias, padding, is_bhl,
                                      (du is None, dw is None, dw is None))

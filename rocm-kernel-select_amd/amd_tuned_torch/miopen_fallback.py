@@ -148,11 +148,15 @@ class _DwConv1dFn(torch.autograd.Function):
         if dout.is_cuda and _native.available():
             dout = dout.contiguous()
             x = input.detach()
-            if needs[0] and ctx.pad_left <= K - 1:
-                try:
-                    gi = _native.dwconv1d_backward(dout, x, weight.detach(), ctx.pad_left,
-                                                   (True, False, False))[0]
+            if needs[0]:
+                try:  # dx with dw / db, one pass over x and dout where the fused kernel applies
+                    gi, dw32, db32 = _native.dwconv1d_backward(dout, x, weight.detach(), ctx.pad_left,
+                                                               (True, needs[1], needs[2]))
                     needs[0] = False
+                    if dw32 is not None:
+                        gw, needs[1] = dw32.to(weight.dtype).view(C, 1, K), False
+                    if db32 is not None:
+                        gb, needs[2] = db32.to(dout.dtype), False
                 except _native.Unsupported:
                     pass
             if needs[1] or needs[2]:

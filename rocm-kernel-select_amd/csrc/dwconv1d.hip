@@ -822,6 +822,108 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_bwd_w_kernel(DwBwdArgs a) {
   }
 }
 
+// dx, dw and db in one pass over each (n, c) row: x and dy are read once and dx written once
+// (the two-kernel form -- the forward kernel on dy for dx, dwconv1d_bwd_w_kernel for dw / db --
+// reads dy twice).  A thread walks x positions p0 = p_lo + (tid + m * DW_NT) * VEC over
+// [p_lo, p_end); at each it cuts the dy window dy[p0 + pad - (K-1) ... + VEC + K - 2] and the x
+// vector x[p0 ... p0 + VEC - 1] from aligned 16-byte blocks (so neither row needs alignment)
+// and computes
+//   dx[p0 + e] = sum_j w[j] * dy[p0 + e + pad - j]            (stored for p0 in [0, L)),
+//   dw[j]     += sum_e x[p0 + e] * dy[p0 + e + pad - j],
+//   db        += sum_e dy[p0 + pad - (K-1) + e].
+// Positions outside [0, L) / [0, L_out) read as zero.  The host picks p_lo <= min(0, K-1-pad)
+// (a multiple of VEC) and p_end >= max(L, L_out + K-1-pad), so every x position and every dy
+// position is visited exactly once.  dx rows must be 16-byte aligned (L % VEC == 0, aligned
+// base: host check).
+struct DwBwdFusedArgs {
+  const void* x;
+  const void* dy;
+  const void* w;      // [C][K], the dtype of x
+  void* dx;
+  float* part;        // [N*C][K+1], or null (dx only)
+  uint32_t L, Lout, C;
+  int pad;
+  int x_off, dy_off;  // misalignment of the x / dy base pointers, in elements
+  int64_t total_in, total_out;
+  int p_lo, p_end;
+};
+
+template <typename T, int KT>
+__global__ __launch_bounds__(DW_NT) void dwconv1d_bwd_fused_kernel(DwBwdFusedArgs a) {
+  using Dyw = DwWindow<T, KT>;
+  using Xw = DwWindow<T, 1>;
+  constexpr int VEC = Dyw::VEC, WN = Dyw::WN;
+  __shared__ float red[(KT + 1) * (DW_NT / 64)];
+  const uint32_t r = blockIdx.x;  // row n*C + c
+  const uint32_t c = r % a.C;
+  float wv[KT];
+#pragma unroll
+  for (int j = 0; j < KT; ++j) wv[j] = to_f32(static_cast<const T*>(a.w)[c * KT + j]);
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(
+      static_cast<const T*>(a.x) - a.x_off, (uint32_t)((a.total_in + a.x_off + VEC - 1) / VEC * 16));
+  const __amdgpu_buffer_rsrc_t rd = make_rsrc(
+      static_cast<const T*>(a.dy) - a.dy_off, (uint32_t)((a.total_out + a.dy_off + VEC - 1) / VEC * 16));
+  T* __restrict__ dxr = static_cast<T*>(a.dx) + (int64_t)r * a.L;
+  const int L = (int)a.L;
+  float acc[KT + 1];
+#pragma unroll
+  for (int k = 0; k <= KT; ++k) acc[k] = 0.f;
+  for (int p0 = a.p_lo + (int)threadIdx.x * VEC; p0 < a.p_end; p0 += DW_NT * VEC) {
+    uint32_t DD[4 * Dyw::NBLK], DX[4 * Xw::NBLK];
+    int md, mx;
+    const int g = p0 + a.pad - (KT - 1);  // row position of the window's first dy element
+    Dyw::fetch(rd, (int)(r * a.Lout) + g + a.dy_off, true, DD, md);
+    Xw::fetch(rx, (int)(r * a.L) + p0 + a.x_off, true, DX, mx);
+    float dv[WN], xv[VEC];
+    Dyw::extract(DD, md, g, a.Lout, dv);  // zero outside [0, L_out)
+    Xw::extract(DX, mx, p0, a.L, xv);     // zero outside [0, L)
+    float o[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      float sx = 0.f;
+#pragma unroll
+      for (int j = 0; j < KT; ++j) sx = fmaf(wv[j], dv[e + KT - 1 - j], sx);
+      o[e] = sx;
+      acc[KT] += dv[e];
+#pragma unroll
+      for (int j = 0; j < KT; ++j) acc[j] = fmaf(xv[e], dv[e + KT - 1 - j], acc[j]);
+    }
+    if (p0 >= 0 && p0 < L) st16<false>(dxr + p0, pack16<T>(o));
+  }
+  if (!a.part) return;
+  // thread 0 writes the row's K+1 partials: one LDS exchange
+#pragma unroll
+  for (int k = 0; k <= KT; ++k) acc[k] = wave_sum(acc[k]);
+  if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+    for (int k = 0; k <= KT; ++k) red[k * (DW_NT / 64) + (threadIdx.x >> 6)] = acc[k];
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int k = 0; k <= KT; ++k) {
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < DW_NT / 64; ++w) v += red[k * (DW_NT / 64) + w];
+      a.part[(int64_t)r * (KT + 1) + k] = v;
+    }
+  }
+}
+
+template <typename T>
+int launch_dw_bwd_fused(const DwBwdFusedArgs& a, int64_t rows, int K, hipStream_t s) {
+  const dim3 grid((unsigned)rows), block(DW_NT);
+  switch (K) {
+    case 1: hipLaunchKernelGGL((dwconv1d_bwd_fused_kernel<T, 1>), grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL((dwconv1d_bwd_fused_kernel<T, 2>), grid, block, 0, s, a); break;
+    case 3: hipLaunchKernelGGL((dwconv1d_bwd_fused_kernel<T, 3>), grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL((dwconv1d_bwd_fused_kernel<T, 4>), grid, block, 0, s, a); break;
+    case 5: hipLaunchKernelGGL((dwconv1d_bwd_fused_kernel<T, 5>), grid, block, 0, s, a); break;
+    default: return fail(ATK_UNSUPPORTED, "dwconv1d backward: K %d outside [1, 5]", K);
+  }
+  return check_launch("dwconv1d_bwd_fused_kernel");
+}
+
 // dw[c,k] (k < K) and db[c] (k == K) = sum over n of the row partials, n in order.
 __global__ __launch_bounds__(256) void dwconv1d_bwd_finalize_kernel(const float* __restrict__ part, float* __restrict__ dw,
                                                                     float* __restrict__ db, int N, int C, int K) {
@@ -1119,6 +1221,57 @@ extern "C" int atk_dwconv1d_bwd_weight(const void* x, const void* dy, float* dw,
     default: rc = launch_dw_bwd_w<__bf16>(a, rows, K, s); break;
   }
   if (rc) return rc;
+  const int outs = (int)(C * (K + 1));
+  hipLaunchKernelGGL(dwconv1d_bwd_finalize_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s,
+                     a.part, dw, db, (int)N, (int)C, K);
+  return check_launch("dwconv1d_bwd_finalize_kernel");
+}
+
+extern "C" int atk_dwconv1d_bwd(const void* x, const void* dy, const void* w, void* dx, float* dw, float* db,
+                                int64_t N, int64_t C, int64_t L, int K, int pad_left, int64_t L_out, int dtype,
+                                void* workspace, size_t ws_bytes, atk_stream_t stream) {
+  using namespace atk;
+  if (!dtype_ok(dtype)) return fail(ATK_EINVAL, "dwconv1d backward: unknown dtype code %d", dtype);
+  if (N <= 0 || C <= 0 || L <= 0 || L_out < 0) return fail(ATK_EINVAL, "dwconv1d backward: bad sizes");
+  if (K < 1 || K > 5) return fail(ATK_UNSUPPORTED, "dwconv1d backward: K %d outside [1, 5]", K);
+  if (pad_left < 0 || pad_left > DW_PADMAX)
+    return fail(ATK_UNSUPPORTED, "dwconv1d backward: padding %d outside [0, %d]", pad_left, DW_PADMAX);
+  if (!x || !dy || !w || !dx) return fail(ATK_EINVAL, "dwconv1d backward: null pointer");
+  if (db && !dw) return fail(ATK_EINVAL, "dwconv1d backward: db needs dw");
+  const bool with_w = dw != nullptr;
+  const size_t need = with_w ? atk_dwconv1d_bwd_weight_workspace_bytes(N, C, K) : 0;
+  if (with_w && (!workspace || ws_bytes < need))
+    return fail(ATK_EINVAL, "dwconv1d backward: workspace of %zu bytes needed", need);
+  const size_t es = dtype_size(dtype);
+  const int64_t rows = N * C;
+  const int64_t vec = 16 / (int64_t)es;
+  if (rows >= (1ll << 31) || rows * L + vec >= (1ll << 31) / (int64_t)es ||
+      rows * L_out + 2 * vec + K + DW_PADMAX >= (1ll << 31) / (int64_t)es)
+    return fail(ATK_UNSUPPORTED, "dwconv1d backward: tensor too large");
+  const uintptr_t xa = reinterpret_cast<uintptr_t>(x), da = reinterpret_cast<uintptr_t>(dy);
+  if ((xa % es) || (da % es)) return fail(ATK_EINVAL, "dwconv1d backward: misaligned element pointer");
+  if (L % vec || !aligned16(dx))
+    return fail(ATK_UNSUPPORTED, "dwconv1d backward: the fused kernel needs 16-byte aligned dx rows");
+  DwBwdFusedArgs a;
+  a.x = x; a.dy = dy; a.w = w; a.dx = dx;
+  a.part = with_w ? static_cast<float*>(workspace) : nullptr;
+  a.L = (uint32_t)L; a.Lout = (uint32_t)L_out; a.C = (uint32_t)C;
+  a.pad = pad_left;
+  a.x_off = (int)((xa & 15u) / es);
+  a.dy_off = (int)((da & 15u) / es);
+  a.total_in = rows * L;
+  a.total_out = rows * L_out;
+  const int lo = std::min(0, K - 1 - pad_left);
+  a.p_lo = lo >= 0 ? 0 : -(int)(((-lo) + vec - 1) / vec * vec);
+  a.p_end = (int)std::max<int64_t>(L, L_out + K - 1 - pad_left);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int rc;
+  switch (dtype) {
+    case ATK_F32: rc = launch_dw_bwd_fused<float>(a, rows, K, s); break;
+    case ATK_F16: rc = launch_dw_bwd_fused<_Float16>(a, rows, K, s); break;
+    default: rc = launch_dw_bwd_fused<__bf16>(a, rows, K, s); break;
+  }
+  if (rc || !with_w) return rc;
   const int outs = (int)(C * (K + 1));
   hipLaunchKernelGGL(dwconv1d_bwd_finalize_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0, s,
                      a.part, dw, db, (int)N, (int)C, K);

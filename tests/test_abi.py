@@ -119,6 +119,13 @@ def test_argument_validation_codes(nat):
     neg = (1, 8, 2, 8, 8, 16, 5, 3, 3, 1, 1, 1, 0, 0, 0, 1, 1, 1)   # output depth <= 0
     assert lib.atk_conv_fwd(None, None, None, None, *neg, 1, 0, None, 0, None) == nat.ATK_EINVAL
     assert lib.atk_conv_fwd(None, None, None, None, *geom, 5, 0, None, 0, None) == nat.ATK_EINVAL
+    # fused conv1d backward: argument checks come before any device work
+    f = lib.atk_dwconv1d_bwd
+    assert f(None, None, None, None, None, None, 2, 3, 64, 3, 1, 64, 7, None, 0, None) == nat.ATK_EINVAL  # dtype
+    assert f(None, None, None, None, None, None, 2, 3, 64, 6, 1, 64, 1, None, 0, None) == nat.ATK_UNSUPPORTED  # K
+    assert f(None, None, None, None, None, None, 2, 3, 64, 3, 1, 64, 1, None, 0, None) == nat.ATK_EINVAL  # null
+    assert f(16, 16, 16, 16, None, 16, 2, 3, 64, 3, 1, 64, 1, None, 0, None) == nat.ATK_EINVAL  # db without dw
+    assert f(16, 16, 16, 16, 16, None, 2, 3, 64, 3, 1, 64, 1, None, 0, None) == nat.ATK_EINVAL  # no workspace
     # layout transpose: argument checks come before any device work
     assert lib.atk_transpose_last2(None, None, 2, 3, 4, 7, None) == nat.ATK_EINVAL    # dtype code
     assert lib.atk_transpose_last2(None, None, 2, -3, 4, 1, None) == nat.ATK_EINVAL   # negative size

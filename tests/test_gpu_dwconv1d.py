@@ -165,6 +165,8 @@ BWD_CASES = [
     (1, 8, 4096, 4, 3, 4099),    # long rows
     (2, 4, 2500, 4, 3, 2503),    # long unaligned rows
     (3, 7, 1, 3, 1, 1),          # L = 1
+    (1, 3, 64, 3, 4, 70),        # padding above K-1 (fused kernel; the two-kernel form declines dx)
+    (2, 2, 32, 3, 0, 30),        # 'valid', aligned rows (fused kernel)
 ]
 
 
