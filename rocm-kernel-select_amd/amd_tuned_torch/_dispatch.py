@@ -12,6 +12,10 @@ kernel variants ("native.<variant>") and stock, decided per shape by kernel_sele
 from __future__ import annotations
 
 import atexit
+import collections
+import contextlib
+import functools
+import inspect
 import logging
 import os
 from typing import Any, Callable
@@ -20,56 +24,95 @@ import torch
 import torch.nn.functional as F
 
 from . import _native
+from . import compile_ops
 from . import conv_fusion_ops
 from . import kernel_select
 
+
 # ---------------------------------------------------------------------------
-# Route debugging (reference _dispatch.py:57-219): AMD_TUNED_TORCH_DISPATCH_DEBUG=1 or
-# AMD_TUNED_TORCH_DISPATCH_DEBUG_FILE=<path>; every call site is `if _DEBUG: _debug(...)`.
+# Route debugging (the reference's AMD_TUNED_TORCH_DISPATCH_DEBUG / _DEBUG_FILE switches and
+# dispatch_debug_* API, _dispatch.py:57-219).  Every call site is `if _DEBUG: _debug(...)`,
+# so with the switches unset a decision costs one global read.
 # ---------------------------------------------------------------------------
+class _RouteLog:
+    """Counts (op, route) decisions and, when the logger is at DEBUG, writes one line each."""
+
+    def __init__(self, logger: logging.Logger):
+        self.logger = logger
+        self.counts: "collections.Counter[tuple[str, str]]" = collections.Counter()
+
+    @staticmethod
+    def describe(v: Any) -> str:
+        """dtype(shape) of a tensor, plus layout / grad / subclass marks when they apply."""
+        if not isinstance(v, torch.Tensor):
+            return repr(v)
+        marks = []
+        if v.layout != torch.strided:
+            marks.append(str(v.layout).rsplit(".", 1)[-1])
+        if v.requires_grad:
+            marks.append("grad")
+        if type(v) not in _PLAIN_TENSOR_TYPES:
+            marks.append(type(v).__name__)
+        base = "%s%s" % (str(v.dtype).rsplit(".", 1)[-1], tuple(v.shape))
+        return base + "".join("[%s]" % m for m in marks)
+
+    def record(self, op: str, route: str, why: str, fields: dict) -> None:
+        self.counts[(op, route)] += 1
+        if self.logger.isEnabledFor(logging.DEBUG):
+            text = "%s -> %s" % (op, route)
+            if why:
+                text += " (%s)" % why
+            if fields:
+                text += " " + " ".join("%s=%s" % (k, self.describe(v)) for k, v in fields.items())
+            self.logger.debug(text)
+
+    def report(self) -> str:
+        if not self.counts:
+            return ("amd_tuned_torch dispatch: no routing decisions recorded"
+                    + ("" if _DEBUG else " (AMD_TUNED_TORCH_DISPATCH_DEBUG is not set)"))
+        by_op: "dict[str, collections.Counter]" = collections.defaultdict(collections.Counter)
+        for (op, route), n in self.counts.items():
+            by_op[op][route] += n
+        out = ["amd_tuned_torch dispatch routes (%d decisions):" % sum(self.counts.values())]
+        for op, routes in sorted(by_op.items(), key=lambda kv: -sum(kv[1].values())):
+            total = sum(routes.values())
+            out.append("  %-12s %d" % (op, total))
+            out.extend("      %-18s %8d  %5.1f%%" % (r, n, 100.0 * n / total)
+                       for r, n in routes.most_common())
+        return "\n".join(out)
+
+
+def _debug_switches() -> "tuple[bool, str]":
+    flag = os.environ.get("AMD_TUNED_TORCH_DISPATCH_DEBUG", "0").strip() not in ("", "0", "false", "False")
+    return flag, os.environ.get("AMD_TUNED_TORCH_DISPATCH_DEBUG_FILE", "")
+
+
 _dbg_log = logging.getLogger("amd_tuned_torch.dispatch")
-_DEBUG_ENV_SET = os.environ.get("AMD_TUNED_TORCH_DISPATCH_DEBUG", "0") not in ("0", "", "false", "False")
-_DEBUG_FILE = os.environ.get("AMD_TUNED_TORCH_DISPATCH_DEBUG_FILE", "")
+_DEBUG_ENV_SET, _DEBUG_FILE = _debug_switches()
 _DEBUG = _DEBUG_ENV_SET or bool(_DEBUG_FILE)
+_ROUTES = _RouteLog(_dbg_log)
+_ROUTE_COUNTS = _ROUTES.counts
 
 if _DEBUG:
     _dbg_log.setLevel(logging.DEBUG)
-    _fmt = logging.Formatter("[amd_tuned_torch.dispatch] %(asctime)s %(levelname)s %(message)s")
+    _line_format = logging.Formatter("[amd_tuned_torch.dispatch] %(asctime)s %(levelname)s %(message)s")
+    _sinks = []
     if _DEBUG_ENV_SET and not any(type(h) is logging.StreamHandler for h in _dbg_log.handlers):
-        _h = logging.StreamHandler()
-        _h.setFormatter(_fmt)
-        _dbg_log.addHandler(_h)
+        _sinks.append(logging.StreamHandler())
     if _DEBUG_FILE and not any(isinstance(h, logging.FileHandler) for h in _dbg_log.handlers):
-        _fh = logging.FileHandler(_DEBUG_FILE)
-        _fh.setFormatter(_fmt)
-        _dbg_log.addHandler(_fh)
-
-_ROUTE_COUNTS: dict = {}
+        _sinks.append(logging.FileHandler(_DEBUG_FILE))
+    for _sink in _sinks:
+        _sink.setFormatter(_line_format)
+        _dbg_log.addHandler(_sink)
+    atexit.register(lambda: _ROUTES.counts and _dbg_log.info("%s", _ROUTES.report()))
 
 
 def _dbg_t(t: Any) -> str:
-    if not isinstance(t, torch.Tensor):
-        return repr(t)
-    s = "%s%s" % (str(t.dtype).replace("torch.", ""), tuple(t.shape))
-    if t.layout != torch.strided:
-        s += ":" + str(t.layout).replace("torch.", "")
-    if t.requires_grad:
-        s += "+grad"
-    if type(t) not in _PLAIN_TENSOR_TYPES:
-        s += ":" + type(t).__name__
-    return s
+    return _RouteLog.describe(t)
 
 
 def _debug(op: str, route: str, why: str = "", **fields: Any) -> None:
-    _ROUTE_COUNTS[(op, route)] = _ROUTE_COUNTS.get((op, route), 0) + 1
-    if not _dbg_log.isEnabledFor(logging.DEBUG):
-        return
-    parts = ["%-10s -> %-16s" % (op, route)]
-    if why:
-        parts.append(why)
-    for k, v in fields.items():
-        parts.append("%s=%s" % (k, _dbg_t(v) if isinstance(v, torch.Tensor) else v))
-    _dbg_log.debug("  ".join(parts))
+    _ROUTES.record(op, route, why, fields)
 
 
 def dispatch_debug_enabled() -> bool:
@@ -77,37 +120,16 @@ def dispatch_debug_enabled() -> bool:
 
 
 def dispatch_debug_counts() -> dict:
-    return dict(_ROUTE_COUNTS)
+    return dict(_ROUTES.counts)
 
 
 def dispatch_debug_reset() -> None:
-    _ROUTE_COUNTS.clear()
+    _ROUTES.counts.clear()
 
 
 def dispatch_debug_report() -> str:
-    if not _ROUTE_COUNTS:
-        return ("amd_tuned_torch dispatch: no routing decisions recorded"
-                + ("" if _DEBUG else " (AMD_TUNED_TORCH_DISPATCH_DEBUG is not set)"))
-    per_op: dict = {}
-    for (op, route), n in _ROUTE_COUNTS.items():
-        per_op.setdefault(op, {})[route] = n
-    lines = ["amd_tuned_torch dispatch routes (%d decisions):" % sum(_ROUTE_COUNTS.values())]
-    for op in sorted(per_op, key=lambda o: -sum(per_op[o].values())):
-        tot = sum(per_op[op].values())
-        lines.append("  %-12s %d" % (op, tot))
-        for route in sorted(per_op[op], key=lambda r: -per_op[op][r]):
-            n = per_op[op][route]
-            lines.append("      %-18s %8d  %5.1f%%" % (route, n, 100.0 * n / tot))
-    return "\n".join(lines)
+    return _ROUTES.report()
 
-
-def _dbg_atexit_report() -> None:
-    if _ROUTE_COUNTS:
-        _dbg_log.info("%s", dispatch_debug_report())
-
-
-if _DEBUG:
-    atexit.register(_dbg_atexit_report)
 
 # Raw, unpatched handle on the native kernels (reference `ops = _C`).
 ops = _native
@@ -117,32 +139,24 @@ _CONV_NATIVE_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 _CONV3D_KIND = "conv3d"
 
 _ORIGINALS: "dict[tuple[Any, str], Callable]" = {}
+# The stock torch.nn.functional entry points by name, as _install found them: the patched
+# functions read them from here (a string-keyed dict, which torch.compile can trace; a
+# module-keyed one it cannot).
+_STOCK_F: "dict[str, Callable]" = {n: getattr(F, n) for n in ("conv2d", "conv3d", "group_norm") if hasattr(F, n)}
 _ENABLED = False
 _HAS_INFERENCE_MODE = hasattr(torch, "is_inference_mode_enabled")
 _PLAIN_TENSOR_TYPES = (torch.Tensor, torch.nn.Parameter)
 
 
-def _is_compiling() -> bool:
-    try:
-        return bool(torch.compiler.is_compiling())
-    except AttributeError:
-        try:
-            return bool(torch._dynamo.is_compiling())
-        except Exception:
-            return False
+_is_compiling = compile_ops.is_compiling
 
 
 def _grad_safe(*tensors: Any) -> bool:
-    """True when no backward will run through this call (inference mode, no_grad, or no
-    argument requires grad) -- reference _dispatch.py:528-553."""
-    if _HAS_INFERENCE_MODE and torch.is_inference_mode_enabled():
+    """No backward can run through this call: inference mode, grad mode off, or no tensor
+    argument that requires grad (the reference's eligibility rule, _dispatch.py:528-553)."""
+    if not torch.is_grad_enabled() or (_HAS_INFERENCE_MODE and torch.is_inference_mode_enabled()):
         return True
-    if not torch.is_grad_enabled():
-        return True
-    for t in tensors:
-        if isinstance(t, torch.Tensor) and t.requires_grad:
-            return False
-    return True
+    return not any(isinstance(t, torch.Tensor) and t.requires_grad for t in tensors)
 
 
 def _is_plain_tensor(t: Any) -> bool:
@@ -163,16 +177,17 @@ def _usable(*tensors: Any, dtypes: tuple = _CONV_NATIVE_DTYPES) -> bool:
 
 
 def _install(target: Any, name: str, wrapper: Callable) -> None:
-    key = (target, name)
-    if key not in _ORIGINALS:
-        _ORIGINALS[key] = getattr(target, name)
+    """Point target.name at wrapper; the first original seen is kept for _restore."""
+    _ORIGINALS.setdefault((target, name), getattr(target, name))
+    if target is F:
+        _STOCK_F[name] = _ORIGINALS[(target, name)]
     setattr(target, name, wrapper)
 
 
 def _restore(target: Any, name: str) -> None:
-    original = _ORIGINALS.pop((target, name), None)
-    if original is not None:
-        setattr(target, name, original)
+    """Put back the original of target.name, if _install replaced it."""
+    if (target, name) in _ORIGINALS:
+        setattr(target, name, _ORIGINALS.pop((target, name)))
 
 
 def _triple(v):
@@ -414,12 +429,46 @@ def _wgrad_native(input, grad_output, weight, stride, padding, dilation, groups,
     return dw.reshape(weight.shape).to(weight.dtype)
 
 
+def _conv_grads(grad_output, input, weight, bias_sizes, conf, needs, fwd):
+    """(dx, dw, db) of a patched conv for `needs` = [dx, dw, db] wanted:
+    * dx of a stride-1, dilation-1, groups-1 conv through `fwd` (the accelerated forward) on dy
+      with transposed, flipped weights;
+    * dw of a 'same' 3x3(x3) conv in a 16-bit type through the native wgrad kernel;
+    * db as a reduction of dy once every other gradient is native;
+    * whatever is left through aten.convolution_backward, the op autograd uses unpatched."""
+    stride, padding, dilation, groups, nd = conf
+    needs = list(needs)
+    gi = gw = gb = None
+    if needs[0] and input.is_cuda:
+        pad_t = _dgrad_padding(weight, stride, padding, dilation, groups, nd)
+        if pad_t is not None:
+            gi = _dgrad_via_forward(grad_output, weight.detach(), pad_t, nd, fwd)
+            if tuple(gi.shape) == tuple(input.shape):
+                needs[0] = False
+            else:
+                gi = None
+    if needs[1] and input.is_cuda:
+        gw = _wgrad_native(input, grad_output, weight, stride, padding, dilation, groups, nd)
+        if gw is not None:
+            needs[1] = False
+    if needs[2] and not needs[0] and not needs[1]:
+        gb = grad_output.sum(dim=[0] + list(range(2, 2 + nd)), dtype=torch.float32).to(weight.dtype)
+        needs[2] = False
+    if any(needs):
+        tup = _triple if nd == 3 else _pair
+        ai, aw, ab = torch.ops.aten.convolution_backward(
+            grad_output.contiguous(), input, weight, bias_sizes, list(tup(stride)),
+            list(tup(padding)), list(tup(dilation)), False, [0] * nd, groups, needs)
+        gi = ai if gi is None else gi
+        gw = aw if gw is None else gw
+        gb = ab if gb is None else gb
+    return gi, gw, gb
+
+
 class _ConvFn(torch.autograd.Function):
-    """Accelerated forward; the input gradient (stride 1, dilation 1, groups 1) through the
-    same accelerated forward on dy with transposed, flipped weights; the weight gradient of
-    'same' 3x3(x3) convs through the native wgrad kernel (and then the bias gradient as a
-    reduction of dy); the rest through aten.convolution_backward -- the op autograd would
-    have used unpatched (reference _Conv3dFn, _dispatch.py:2029-2075)."""
+    """Accelerated forward; the backward of _conv_grads (native input and weight gradients
+    where they apply, aten.convolution_backward for the rest -- the reference's _Conv3dFn,
+    _dispatch.py:2029-2075, uses aten for all of it)."""
 
     @staticmethod
     def forward(ctx, input, weight, bias, stride, padding, dilation, groups, nd, fwd):
@@ -432,42 +481,59 @@ class _ConvFn(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_output):
         input, weight = ctx.saved_tensors
-        stride, padding, dilation, groups, nd = ctx.conf
         needs = [bool(ctx.needs_input_grad[0]), bool(ctx.needs_input_grad[1]),
                  ctx.bias_sizes is not None and bool(ctx.needs_input_grad[2])]
         if not any(needs):
             return (None,) * 9
-        gi = None
-        if needs[0] and input.is_cuda:
-            pad_t = _dgrad_padding(weight, stride, padding, dilation, groups, nd)
-            if pad_t is not None:
-                gi = _dgrad_via_forward(grad_output, weight.detach(), pad_t, nd, ctx.fwd)
-                if tuple(gi.shape) != tuple(input.shape):
-                    gi = None
-                else:
-                    needs[0] = False
-        gw = gb = None
-        if needs[1] and input.is_cuda:
-            gw = _wgrad_native(input, grad_output, weight, stride, padding, dilation, groups, nd)
-            if gw is not None:
-                needs[1] = False
-        if needs[2] and not needs[0] and not needs[1]:
-            # every other gradient is native: the bias gradient is a reduction of dy
-            gb = grad_output.sum(dim=[0] + list(range(2, 2 + nd)), dtype=torch.float32).to(weight.dtype)
-            needs[2] = False
-        if any(needs):
-            tup = _triple if nd == 3 else _pair
-            ai, aw, ab = torch.ops.aten.convolution_backward(
-                grad_output.contiguous(), input, weight, ctx.bias_sizes, list(tup(stride)),
-                list(tup(padding)), list(tup(dilation)), False, [0] * nd, groups, needs)
-            gi = ai if gi is None else gi
-            gw = aw if gw is None else gw
-            gb = ab if gb is None else gb
+        gi, gw, gb = _conv_grads(grad_output, input, weight, ctx.bias_sizes, ctx.conf, needs, ctx.fwd)
         return gi, gw, gb, None, None, None, None, None, None
 
 
+def _stock_conv(nd: int) -> Callable:
+    """The unpatched F.conv2d / F.conv3d."""
+    return _STOCK_F["conv%dd" % nd]
+
+
+def _conv_selected(nd: int, input, weight, bias, stride, padding, dilation):
+    """Eager body of the conv custom ops: the per-shape selection of the patched API."""
+    orig = _stock_conv(nd)
+    return _conv_accelerated_forward(nd, input, weight, bias, stride, padding, dilation, 1, orig)
+
+
+def _conv_grads_eager(grad_output, input, weight, has_bias, stride, padding, dilation, nd, needs):
+    """Eager body of the conv backward custom op."""
+    orig = _stock_conv(nd)
+
+    def fwd(i, w, b, s, p, d, g):
+        return _conv_accelerated_forward(nd, i, w, b, s, p, d, g, orig)
+    bias_sizes = [weight.shape[0]] if has_bias else None
+    return _conv_grads(grad_output, input, weight, bias_sizes, (stride, padding, dilation, 1, nd),
+                       needs, fwd)
+
+
+def _traced_conv(nd: int, input, weight, bias, stride, padding, dilation, groups, orig):
+    """Under torch.compile: an eligible conv becomes one custom-op node (its body selects the
+    kernel when the graph runs; autograd included), anything else the stock conv."""
+    ok = (groups == 1 and not isinstance(padding, str)
+          and isinstance(input, torch.Tensor) and isinstance(weight, torch.Tensor)
+          and input.dim() == nd + 2 and weight.dim() == nd + 2
+          and input.is_contiguous() and weight.is_contiguous()
+          and _usable(input, weight, bias, dtypes=_CONV_NATIVE_DTYPES)
+          and input.dtype == weight.dtype and (bias is None or bias.dtype == input.dtype)
+          and compile_ops.native_loaded())
+    if not ok:
+        return orig(input, weight, bias, stride, padding, dilation, groups)
+    op = compile_ops.conv3d_native if nd == 3 else compile_ops.conv2d_native
+    return op(input, weight, bias, stride, padding, dilation)
+
+
 def _patched_conv2d(input, weight, bias=None, stride=1, padding=0, dilation=1, groups=1):
-    orig = _ORIGINALS[(F, "conv2d")]
+    orig = _STOCK_F["conv2d"]
+    if _is_compiling():
+        if (isinstance(weight, torch.Tensor) and weight.dim() == 4 and not isinstance(padding, str)
+                and _is_pointwise_conv2d(weight, stride, padding, dilation)):
+            return orig(input, weight, bias, stride, padding, dilation, groups)
+        return _traced_conv(2, input, weight, bias, stride, padding, dilation, groups, orig)
     if groups != 1:
         if _DEBUG:
             _debug("conv2d", "stock", "grouped conv: no tier here supports groups != 1",
@@ -491,7 +557,9 @@ def _patched_conv2d(input, weight, bias=None, stride=1, padding=0, dilation=1, g
 
 
 def _patched_conv3d(input, weight, bias=None, stride=1, padding=0, dilation=1, groups=1):
-    orig = _ORIGINALS[(F, "conv3d")]
+    orig = _STOCK_F["conv3d"]
+    if _is_compiling():
+        return _traced_conv(3, input, weight, bias, stride, padding, dilation, groups, orig)
 
     def fwd(i, w, b, s, p, d, g):
         return _conv_accelerated_forward(3, i, w, b, s, p, d, g, orig)
@@ -529,11 +597,7 @@ def _group_norm_candidates(input, num_groups, weight, bias, eps, silu: bool = Fa
 
 
 def _group_norm_native(input, num_groups, weight, bias, eps, name=None):
-    """Native GroupNorm: the named variant, or the first one that accepts the shape.
-    Under Dynamo tracing the torch.library op is used instead (graph-break free)."""
-    if _is_compiling():
-        from . import compile_ops
-        return compile_ops.group_norm(input, num_groups, weight, bias, eps)
+    """Native GroupNorm: the named variant, or the first one that accepts the shape."""
     if name is not None:
         return _run_named_native(name, _native.group_norm, _native.OP_GROUP_NORM, input,
                                  num_groups, weight, bias, eps)
@@ -579,7 +643,7 @@ def _group_norm_channels_last(input, num_groups, weight, bias, eps, orig):
 
 
 def _group_norm_accelerated_forward(input, num_groups, weight, bias, eps):
-    orig = _ORIGINALS[(F, "group_norm")]
+    orig = _STOCK_F["group_norm"]
     if isinstance(input, torch.Tensor) and _channels_last(input):
         return _group_norm_channels_last(input, num_groups, weight, bias, eps, orig)
     if not (isinstance(input, torch.Tensor) and input.dim() >= 2 and input.is_contiguous()
@@ -658,9 +722,30 @@ def _group_norm_backward(grad_output, input, num_groups, weight, eps, needs, bia
     return gx, gw, gb
 
 
+def _group_norm_grads(grad_output, input, num_groups, weight, eps, needs):
+    """(dx, dgamma, dbeta) of GroupNorm for `needs` = (dx, dgamma, dbeta) wanted: the native
+    backward kernels for contiguous or channels-last GPU input (channels-last x and dy go to
+    NC[S] through the native transpose, dx comes back in the input's layout; dgamma / dbeta
+    in fp32), the textbook torch-op backward otherwise (dgamma / dbeta in the parameter
+    dtypes).  Entries not asked for are None."""
+    cl = _channels_last(input)
+    if input.is_cuda and (input.is_contiguous() or cl) and _native.available():
+        try:
+            x = _native.channels_last_to_contiguous(input.detach()) if cl else input.detach()
+            gx, gw, gb = _native.group_norm_backward(_to_ncdhw(grad_output), x, num_groups,
+                                                     None if weight is None else weight.detach(),
+                                                     eps, needs)
+            if cl and gx is not None:
+                gx = _native.contiguous_to_channels_last(gx)
+            return gx, gw, gb
+        except _native.Unsupported:
+            pass
+    return _group_norm_backward(grad_output.contiguous(), input, num_groups, weight, eps, needs)
+
+
 class _GroupNormFn(torch.autograd.Function):
-    """Accelerated forward; native backward kernels (atk_group_norm_bwd) for contiguous GPU
-    inputs, the textbook torch-op backward otherwise (reference _GroupNormFn, 2305-2359)."""
+    """Accelerated forward; the backward of _group_norm_grads (native kernels where they
+    apply; the reference's _GroupNormFn, 2305-2359, uses the torch-op formula)."""
 
     @staticmethod
     def forward(ctx, input, weight, bias, num_groups, eps):
@@ -675,28 +760,28 @@ class _GroupNormFn(torch.autograd.Function):
         input, weight = ctx.saved_tensors
         needs = (ctx.needs_input_grad[0], weight is not None and ctx.needs_input_grad[1],
                  ctx.has_bias and ctx.needs_input_grad[2])
-        cl = _channels_last(input)
-        if input.is_cuda and (input.is_contiguous() or cl) and _native.available():
-            try:
-                # channels-last x and dy go to NC[S] through the native transpose, and dx
-                # comes back in the input's layout
-                x = _native.channels_last_to_contiguous(input.detach()) if cl else input.detach()
-                gx, gw, gb = _native.group_norm_backward(_to_ncdhw(grad_output), x, ctx.num_groups,
-                                                         None if weight is None else weight.detach(),
-                                                         ctx.eps, needs)
-                if cl and gx is not None:
-                    gx = _native.contiguous_to_channels_last(gx)
-                gw = None if gw is None else gw.to(weight.dtype)
-                gb = None if gb is None else gb.to(ctx.bias_dtype if ctx.bias_dtype is not None
-                                                   else input.dtype)
-                return gx, gw, gb, None, None
-            except _native.Unsupported:
-                pass
-        return _group_norm_backward(grad_output.contiguous(), input, ctx.num_groups, weight,
-                                    ctx.eps, needs, bias_dtype=ctx.bias_dtype) + (None, None)
+        gx, gw, gb = _group_norm_grads(grad_output, input, ctx.num_groups, weight, ctx.eps, needs)
+        gw = None if gw is None else gw.to(weight.dtype)
+        gb = None if gb is None else gb.to(ctx.bias_dtype if ctx.bias_dtype is not None else input.dtype)
+        return gx, gw, gb, None, None
+
+
+def _traced_group_norm(input, num_groups, weight, bias, eps, orig):
+    """Under torch.compile: an eligible GroupNorm becomes one custom-op node (selection at run
+    time, native backward through the op's autograd formula), anything else stock."""
+    ok = (isinstance(input, torch.Tensor) and input.dim() >= 2
+          and (input.is_contiguous() or _channels_last(input))
+          and _usable(input, dtypes=_GROUPNORM_DTYPES) and _usable(weight, bias, dtypes=_GROUPNORM_DTYPES)
+          and isinstance(num_groups, int) and num_groups > 0 and input.shape[1] % num_groups == 0
+          and compile_ops.native_loaded())
+    if not ok:
+        return orig(input, num_groups, weight, bias, eps)
+    return compile_ops.group_norm(input, num_groups, weight, bias, eps)
 
 
 def _patched_group_norm(input, num_groups, weight=None, bias=None, eps=1e-5):
+    if _is_compiling():
+        return _traced_group_norm(input, num_groups, weight, bias, eps, _STOCK_F["group_norm"])
     if _grad_safe(input, weight, bias):
         return _group_norm_accelerated_forward(input, num_groups, weight, bias, eps)
     if _DEBUG:
@@ -735,10 +820,20 @@ def _patched_sequential_forward(self, input):
 
 
 # ---------------------------------------------------------------------------
-# enable / disable
+# enable / disable (reference _dispatch.py:2913-3050): the functional entry points, the
+# Sequential fusion when conv fusion is available, conv3d where torch has it.
 # ---------------------------------------------------------------------------
+def _patch_table() -> "list[tuple[Any, str, Callable]]":
+    table = [(F, "group_norm", _patched_group_norm), (F, "conv2d", _patched_conv2d)]
+    if conv_fusion_ops.enabled():
+        table.append((torch.nn.Sequential, "forward", _patched_sequential_forward))
+    if hasattr(F, "conv3d"):
+        table.append((F, "conv3d", _patched_conv3d))
+    return table
+
+
 def enable() -> None:
-    """Patch torch.nn.functional so eligible calls route through amd_tuned_torch."""
+    """Patch torch.nn.functional so eligible calls route through amd_tuned_torch (idempotent)."""
     global _ENABLED, _SEQ_FORWARD_ORIG
     if _ENABLED:
         if _DEBUG:
@@ -747,13 +842,11 @@ def enable() -> None:
     if _DEBUG:
         _debug("enable", "backends", "", native=_native.available(),
                kernel_select=kernel_select.enabled(), conv_fusion=conv_fusion_ops.enabled())
-    _install(F, "group_norm", _patched_group_norm)
-    _install(F, "conv2d", _patched_conv2d)
-    if conv_fusion_ops.enabled():
-        _install(torch.nn.Sequential, "forward", _patched_sequential_forward)
-        _SEQ_FORWARD_ORIG = _ORIGINALS[(torch.nn.Sequential, "forward")]
-    if hasattr(F, "conv3d"):
-        _install(F, "conv3d", _patched_conv3d)
+    table = _patch_table()
+    compile_ops.keep_traceable([wrapper for _, _, wrapper in table])
+    for target, name, wrapper in table:
+        _install(target, name, wrapper)
+    _SEQ_FORWARD_ORIG = _ORIGINALS.get((torch.nn.Sequential, "forward"), _SEQ_FORWARD_ORIG)
     _ENABLED = True
     if _DEBUG:
         _debug("enable", "installed", "", patched=",".join(sorted(n for _, n in _ORIGINALS)))
@@ -764,7 +857,7 @@ def disable() -> None:
     global _ENABLED
     if _DEBUG:
         _debug("disable", "restored", "", patched=",".join(sorted(n for _, n in _ORIGINALS)))
-    for target, name in list(_ORIGINALS.keys()):
+    for target, name in list(_ORIGINALS):
         _restore(target, name)
     _ENABLED = False
 
@@ -774,41 +867,45 @@ def is_enabled() -> bool:
 
 
 # ---------------------------------------------------------------------------
-# TorchScript guard (reference 3099-3155): script/trace compile against stock ops, since a
-# scripted or traced graph cannot call these Python wrappers.  Installed at import time.
+# TorchScript guard (reference 3099-3155): a scripted or traced graph cannot call these
+# Python wrappers, so torch.jit.script / torch.jit.trace run with the stock functions in
+# place and the patches come back afterwards.  Installed at import time.
 # ---------------------------------------------------------------------------
+@contextlib.contextmanager
+def _stock_functions():
+    """Lift every patch for the duration of the block (nothing to do when not enabled)."""
+    lifted = _ENABLED
+    if lifted:
+        disable()
+    try:
+        yield
+    finally:
+        if lifted:
+            enable()
+
+
+def _jit_under_stock(jit_fn: Callable) -> Callable:
+    """jit_fn run inside _stock_functions().  Class scripting resolves names a given number
+    of frames above torch.jit.script (its `_frames_up` argument); this wrapper is one more
+    frame between the user and jit_fn, so that count is raised by one."""
+    params = inspect.signature(jit_fn).parameters
+    shifts_frames = "_frames_up" in params
+
+    @functools.wraps(jit_fn)
+    def entry(*args, **kwargs):
+        if shifts_frames:
+            bound = inspect.signature(jit_fn).bind(*args, **kwargs)
+            bound.arguments["_frames_up"] = bound.arguments.get("_frames_up", 0) + 1
+            args, kwargs = bound.args, bound.kwargs
+        with _stock_functions():
+            return jit_fn(*args, **kwargs)
+    return entry
+
+
 _ORIG_JIT_SCRIPT = torch.jit.script
 _ORIG_JIT_TRACE = torch.jit.trace
-
-
-def _script_with_stock_ops(obj, *args, **kwargs):
-    # one extra Python frame between the caller and torch.jit.script: class scripting
-    # resolves names _frames_up frames above, so compensate
-    if len(args) >= 2:
-        args = args[:1] + (args[1] + 1,) + args[2:]
-    else:
-        kwargs["_frames_up"] = kwargs.get("_frames_up", 0) + 1
-    if not _ENABLED:
-        return _ORIG_JIT_SCRIPT(obj, *args, **kwargs)
-    disable()
-    try:
-        return _ORIG_JIT_SCRIPT(obj, *args, **kwargs)
-    finally:
-        enable()
-
-
-def _trace_with_stock_ops(*args, **kwargs):
-    if not _ENABLED:
-        return _ORIG_JIT_TRACE(*args, **kwargs)
-    disable()
-    try:
-        return _ORIG_JIT_TRACE(*args, **kwargs)
-    finally:
-        enable()
-
-
-_script_with_stock_ops.__doc__ = _ORIG_JIT_SCRIPT.__doc__
-_trace_with_stock_ops.__doc__ = _ORIG_JIT_TRACE.__doc__
+_script_with_stock_ops = _jit_under_stock(_ORIG_JIT_SCRIPT)
+_trace_with_stock_ops = _jit_under_stock(_ORIG_JIT_TRACE)
 torch.jit.script = _script_with_stock_ops
 torch.jit.trace = _trace_with_stock_ops
 

@@ -197,44 +197,64 @@ def _require_cuda(*tensors) -> None:
 
 
 # ---------------------------------------------------------------------------
-# Workspaces: one zero-initialised byte buffer per (device, purpose), grown on demand.
-# Calls that share a workspace are ordered on the caller's stream; callers issuing the
-# same op concurrently on different streams must not share one.
+# Workspaces.  Scratch bytes are pooled per (device, stream, purpose): work queued on one
+# stream runs in order, so calls on that stream can share a buffer, while two streams never
+# do -- a conv or GroupNorm issued on a second stream gets buffers of its own.  A buffer that
+# must grow is replaced, and the one it replaces is retired, not freed: a HIP graph captured
+# earlier still holds its address, and freeing it would let the caching allocator hand that
+# memory to a tensor the replay would then overwrite.  Growth is geometric, so the retired
+# buffers of a pool add up to less than its live one.
 # ---------------------------------------------------------------------------
 _ws_lock = threading.Lock()
-_workspaces: dict = {}
+_ws_live: dict = {}     # (device index, stream handle, purpose) -> uint8 tensor
+_ws_retired: list = []  # superseded buffers, kept for the life of the process
+
+
+def _device_index(device: torch.device) -> int:
+    return device.index if device.index is not None else torch.cuda.current_device()
 
 
 def workspace(device: torch.device, purpose: str, nbytes: int) -> torch.Tensor:
-    key = (device.index if device.index is not None else torch.cuda.current_device(), purpose)
+    """A zero-initialised uint8 buffer of at least `nbytes` for `purpose`, private to the
+    current stream of `device`.  The zeroing (torch's fill kernel, ordered on that stream)
+    happens only when a buffer is created; kernels that need zeroed scratch leave it zero."""
+    stream = torch.cuda.current_stream(device)
+    key = (_device_index(device), stream.cuda_stream, purpose)
     with _ws_lock:
-        buf = _workspaces.get(key)
-        if buf is None or buf.numel() < nbytes:
-            size = max(nbytes, 1 << 16)
-            if buf is not None:
-                size = max(size, 2 * buf.numel())
-            buf = torch.zeros(size, dtype=torch.uint8, device=device)
-            _workspaces[key] = buf
-        return buf
+        buf = _ws_live.get(key)
+        if buf is not None and buf.numel() >= nbytes:
+            return buf
+        size = max(int(nbytes), 1 << 16, 2 * buf.numel() if buf is not None else 0)
+        fresh = torch.zeros(size, dtype=torch.uint8, device=device)
+        if buf is not None:
+            _ws_retired.append(buf)
+        _ws_live[key] = fresh
+        return fresh
+
+
+def workspace_keys() -> list:
+    """(device, stream, purpose) of every live workspace (for tests and diagnostics)."""
+    with _ws_lock:
+        return sorted(_ws_live.keys())
+
+
+def _group_norm_buffers(device: Optional[torch.device]) -> list:
+    idx = _device_index(device or torch.device("cuda", torch.cuda.current_device()))
+    with _ws_lock:
+        return [b for (d, _, p), b in _ws_live.items() if d == idx and p == "group_norm"]
 
 
 def group_norm_clear_diag(device: Optional[torch.device] = None) -> None:
-    """Reset the diagnostics word that group_norm_barrier_error() reads."""
-    dev = device or torch.device("cuda", torch.cuda.current_device())
-    key = (dev.index if dev.index is not None else torch.cuda.current_device(), "group_norm")
-    buf = _workspaces.get(key)
-    if buf is not None:
+    """Reset the diagnostics word that group_norm_barrier_error() reads, on every stream."""
+    for buf in _group_norm_buffers(device):
         buf[:4].zero_()
 
 
 def group_norm_barrier_error(device: Optional[torch.device] = None) -> bool:
-    """True if a register-resident GroupNorm launch on `device` ever gave up waiting for
-    another workgroup's slice statistics and computed them itself (results stay exact;
-    it only means the grid was not fully resident, e.g. under concurrent kernels)."""
-    dev = device or torch.device("cuda", torch.cuda.current_device())
-    key = (dev.index if dev.index is not None else torch.cuda.current_device(), "group_norm")
-    buf = _workspaces.get(key)
-    return bool(buf is not None and int(buf[:4].view(torch.int32).item()) != 0)
+    """True if a register-resident GroupNorm launch on `device` (any stream) ever gave up
+    waiting for another workgroup's slice statistics and computed them itself (results stay
+    exact; it only means the grid was not fully resident, e.g. under concurrent kernels)."""
+    return any(int(buf[:4].view(torch.int32).item()) != 0 for buf in _group_norm_buffers(device))
 
 
 # ---------------------------------------------------------------------------
@@ -534,8 +554,10 @@ def dwconv1d_backward(dy: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, p
     """(dx, dw, db) of y = dwconv1d(x, weight, bias, pad_left, L_out) for dy [N,C,L_out]:
     dx is the forward kernel run on dy with the weights reversed along K and
     pad_left' = K-1-pad_left (output length L); dw [C,K] and db [C] come back in fp32.
-    Entries not asked for in `needs` are None.  Raises Unsupported when pad_left > K-1
-    (dx) or K > 5 (dw, db)."""
+    Entries not asked for in `needs` are None, and so are dw / db when the weight-gradient
+    kernel declines (K > 5) while dx was computed: the caller keeps the native dx and takes
+    the parameter gradients elsewhere.  Raises Unsupported when no asked-for part is served
+    (pad_left > K-1 for dx, K > 5 for dw / db)."""
     K = weight.shape[-1]
     if needs[0]:
         try:  # one pass over x and dy for dx (and dw / db)
@@ -548,7 +570,12 @@ def dwconv1d_backward(dy: torch.Tensor, x: torch.Tensor, weight: torch.Tensor, p
             raise Unsupported("dwconv1d_backward: pad_left > K-1 has no forward-kernel form")
         dx = dwconv1d(dy, weight.reshape(weight.shape[0], K).flip(-1), None, K - 1 - pad_left, x.shape[-1])
     if needs[1] or needs[2]:
-        dw, db = dwconv1d_bwd_weight(x, dy, K, pad_left, with_bias=bool(needs[2]))
+        try:
+            dw, db = dwconv1d_bwd_weight(x, dy, K, pad_left, with_bias=bool(needs[2]))
+        except Unsupported:
+            if dx is None:
+                raise
+            return dx, None, None
         if not needs[1]:
             dw = None
     return dx, dw, db

@@ -193,29 +193,33 @@ def causal_conv1d_fn(x, weight, bias=None, seq_idx=None, initial_states=None,
                                 final_states_out, activation)
 
 
-def causal_conv1d_ref(x, weight, bias=None, initial_states=None, return_final_states=False,
-                      final_states_out=None, activation=None):
-    """Stock-PyTorch statement of the same operator (the reference's causal_conv1d_ref)."""
+def _check_activation(activation) -> None:
     if activation not in (None, "silu", "swish"):
         raise NotImplementedError("activation must be None, silu, or swish")
-    dtype_in = x.dtype
-    x = x.to(weight.dtype)
-    seqlen = x.shape[-1]
+
+
+def causal_conv1d_ref(x, weight, bias=None, initial_states=None, return_final_states=False,
+                      final_states_out=None, activation=None):
+    """Stock-PyTorch statement of causal_conv1d_fn (the reference keeps one beside its kernel,
+    causal_conv1d_interface.py:133-172): in the weight's dtype, the sequence is prefixed by
+    its width-1 positions of left context -- initial_states, or zeros -- and a 'valid'
+    depthwise F.conv1d over that gives the seqlen outputs; final states are the last width-1
+    positions of the prefixed sequence."""
+    _check_activation(activation)
     dim, width = weight.shape
-    if initial_states is None:
-        out = F.conv1d(x, weight.unsqueeze(1), bias, padding=width - 1, groups=dim)
-    else:
-        x = torch.cat([initial_states, x], dim=-1)
-        out = F.conv1d(x, weight.unsqueeze(1), bias, padding=0, groups=dim)
-    out = out[..., :seqlen]
-    final_states = None
-    if return_final_states:
-        final_states = F.pad(x, (width - 1 - x.shape[-1], 0)).to(dtype_in)
-        if final_states_out is not None:
-            final_states_out.copy_(final_states)
-            final_states = final_states_out
-    out = (out if activation is None else F.silu(out)).to(dtype=dtype_in)
-    return out if not return_final_states else (out, final_states)
+    context = (initial_states if initial_states is not None
+               else x.new_zeros((x.shape[0], dim, width - 1)))
+    prefixed = torch.cat([context.to(weight.dtype), x.to(weight.dtype)], dim=-1)
+    out = F.conv1d(prefixed, weight.unsqueeze(1), bias, groups=dim)
+    if activation is not None:
+        out = F.silu(out)
+    out = out.to(x.dtype)
+    if not return_final_states:
+        return out
+    tail = prefixed[..., prefixed.shape[-1] - (width - 1):].to(x.dtype)
+    if final_states_out is not None:
+        tail = final_states_out.copy_(tail)
+    return out, tail
 
 
 def causal_conv1d_update(x, conv_state, weight, bias=None, activation=None):
@@ -235,18 +239,19 @@ def causal_conv1d_update(x, conv_state, weight, bias=None, activation=None):
 
 
 def causal_conv1d_update_ref(x, conv_state, weight, bias=None, activation=None):
-    """Stock-PyTorch statement of the decode step (the reference's causal_conv1d_update_ref,
-    causal_conv1d_interface.py:192-213)."""
-    if activation not in (None, "silu", "swish"):
-        raise NotImplementedError("activation must be None, silu, or swish")
-    dtype_in = x.dtype
+    """Stock-PyTorch statement of the decode step (the reference keeps one beside its kernel,
+    causal_conv1d_interface.py:192-213): the state window slides one position, x entering
+    at the newest end (conv_state is updated in place), and the output is the window's dot
+    product with the weights, plus bias, optionally SiLU, in x's dtype."""
+    _check_activation(activation)
     batch, dim = x.shape
-    width = weight.shape[1]
-    assert conv_state.shape == (batch, dim, width)
-    assert weight.shape == (dim, width)
-    conv_state.copy_(torch.roll(conv_state, shifts=-1, dims=-1))
-    conv_state[:, :, -1] = x
-    out = torch.sum(conv_state * weight, dim=-1)
+    if conv_state.shape != (batch, dim, weight.shape[1]) or weight.shape[0] != dim:
+        raise AssertionError("conv_state must be (batch, dim, width) and weight (dim, width)")
+    window = torch.cat([conv_state[..., 1:], x.unsqueeze(-1).to(conv_state.dtype)], dim=-1)
+    conv_state.copy_(window)
+    out = (conv_state * weight).sum(dim=-1)
     if bias is not None:
-        out += bias
-    return (out if activation is None else F.silu(out)).to(dtype=dtype_in)
+        out = out + bias
+    if activation is not None:
+        out = F.silu(out)
+    return out.to(x.dtype)

@@ -19,6 +19,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import _native
+from . import compile_ops
 from . import kernel_select
 
 _ENV = "AMD_TUNED_TORCH_CONV_FUSION"
@@ -35,15 +36,12 @@ def enabled() -> bool:
 
 
 def _stock_group_norm_silu(x, num_groups, weight, bias, eps):
-    """Unfused reference: the ORIGINAL F.group_norm (not the patched one), then SiLU."""
-    try:
-        from . import _dispatch
-        gn = _dispatch._ORIGINALS.get((F, "group_norm"))
-    except Exception:
-        gn = None
-    if gn is None:
-        gn = torch.group_norm
-    return F.silu(gn(x, num_groups, weight, bias, eps))
+    """The selector's reference for the fused kernels: F.silu after the UNPATCHED GroupNorm
+    (enable() replaces F.group_norm, so the one it captured is taken; aten's
+    torch.group_norm when nothing was captured)."""
+    from . import _dispatch  # imports this module, so resolved at call time
+    stock_gn = _dispatch._STOCK_F.get("group_norm", torch.group_norm)
+    return F.silu(stock_gn(x, num_groups, weight, bias, eps))
 
 
 def _layout(x: torch.Tensor) -> str:
@@ -100,6 +98,22 @@ def _group_norm_silu_cl(x, num_groups, weight, bias, eps, stock):
     return out if out is not None else stock()
 
 
+def _traced_group_norm_silu(x, num_groups, weight, bias, eps):
+    """Under torch.compile: with a gradient live, the patched F.group_norm (its own graph node
+    with the native backward) then F.silu; otherwise one forward-only graph node whose body
+    runs this function's eager selection; stock outside the kernels' reach."""
+    if _grad_needed(x, weight, bias):
+        return F.silu(F.group_norm(x, num_groups, weight, bias, eps))
+    ok = (os.environ.get(_ENV, "1") != "0" and compile_ops.native_loaded()
+          and isinstance(x, torch.Tensor) and x.is_cuda and x.dim() >= 3 and x.dtype in _DTYPES
+          and (x.is_contiguous() or _native.is_channels_last(x))
+          and isinstance(num_groups, int) and num_groups > 0 and x.shape[1] % num_groups == 0
+          and all(p is None or (p.is_cuda and p.dtype in _DTYPES) for p in (weight, bias)))
+    if not ok:
+        return _stock_group_norm_silu(x, num_groups, weight, bias, eps)
+    return compile_ops.group_norm_silu(x, num_groups, weight, bias, eps)
+
+
 def group_norm_silu(x: torch.Tensor, num_groups: int, weight: Optional[torch.Tensor] = None,
                     bias: Optional[torch.Tensor] = None, eps: float = 1e-5) -> torch.Tensor:
     """SiLU(GroupNorm(x)) -- fused native kernel where it wins, stock where it does not.
@@ -107,6 +121,8 @@ def group_norm_silu(x: torch.Tensor, num_groups: int, weight: Optional[torch.Ten
     def stock():
         return _stock_group_norm_silu(x, num_groups, weight, bias, eps)
 
+    if compile_ops.is_compiling():
+        return _traced_group_norm_silu(x, num_groups, weight, bias, eps)
     if isinstance(x, torch.Tensor) and x.is_cuda and _grad_needed(x, weight, bias):
         # training: F.group_norm as installed (the native forward / backward when patched)
         return F.silu(F.group_norm(x, num_groups, weight, bias, eps))
@@ -147,56 +163,58 @@ def group_norm_silu(x: torch.Tensor, num_groups: int, weight: Optional[torch.Ten
     return stock()
 
 
-class FusedGroupNormSiLUConv2d(nn.Module):
-    """Drop-in for nn.Sequential(GroupNorm, SiLU, Conv2d) holding the ORIGINAL submodules
-    under the Sequential's indices "0" and "2", so parameters, optimizer state and
-    state_dict keys survive (reference conv_fusion_ops.py:355-386)."""
+class _FusedBlock(nn.Module):
+    """A fused replacement for a 3-module nn.Sequential that keeps the ORIGINAL conv and
+    GroupNorm objects registered under their Sequential indices (the SiLU, which holds no
+    state, is dropped): parameters, optimizer state and state_dict keys carry over unchanged
+    (the reference's replace_conv_blocks contract, conv_fusion_ops.py:355-439)."""
 
-    def __init__(self, norm: nn.GroupNorm, conv: nn.Conv2d):
+    NORM_AT = CONV_AT = ""
+
+    def __init__(self, norm: nn.GroupNorm, conv: nn.Module):
         super().__init__()
-        self.add_module("0", norm)
-        self.add_module("2", conv)
+        for index, module in sorted(((self.NORM_AT, norm), (self.CONV_AT, conv))):
+            self.add_module(index, module)
 
     @property
     def norm(self) -> nn.GroupNorm:
-        return getattr(self, "0")
+        return self._modules[self.NORM_AT]
 
     @property
-    def conv(self) -> nn.Conv2d:
-        return getattr(self, "2")
+    def conv(self) -> nn.Module:
+        return self._modules[self.CONV_AT]
+
+    def _gn_silu(self, h: torch.Tensor) -> torch.Tensor:
+        n = self.norm
+        return group_norm_silu(h, n.num_groups, n.weight, n.bias, n.eps)
+
+
+class FusedGroupNormSiLUConv2d(_FusedBlock):
+    """nn.Sequential(GroupNorm(affine), SiLU, Conv2d) -> GroupNorm+SiLU in one pass, then the
+    conv.  Submodules "0" (GroupNorm) and "2" (Conv2d)."""
+
+    NORM_AT, CONV_AT = "0", "2"
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        n = self.norm
-        return self.conv(group_norm_silu(x, n.num_groups, n.weight, n.bias, n.eps))
+        return self.conv(self._gn_silu(x))
 
     def extra_repr(self) -> str:
         return "fused=GroupNorm+SiLU"
 
 
-class FusedConvGroupNormSiLU(nn.Module):
-    """Drop-in for nn.Sequential(Conv2d | Conv3d, GroupNorm(affine), SiLU): the decoder-block
-    order of a video VAE (Conv3d 256->256 k3 -> GroupNorm(32) -> SiLU).  The
-    original submodules stay under the Sequential's indices "0" and "1", so parameters and
-    state_dict keys survive.  The conv runs through F.conv2d / F.conv3d (the accelerated
-    forward when patched), GroupNorm + SiLU through group_norm_silu: one fused pass over the
-    conv output instead of a GroupNorm pass and a SiLU pass."""
+class FusedConvGroupNormSiLU(_FusedBlock):
+    """nn.Sequential(Conv2d | Conv3d, GroupNorm(affine), SiLU): the decoder-block order of a
+    video VAE (Conv3d 256->256 k3 -> GroupNorm(32) -> SiLU).  The conv runs
+    through F.conv2d / F.conv3d (the accelerated forward when patched), GroupNorm + SiLU in
+    one pass over its output.  Submodules "0" (conv) and "1" (GroupNorm)."""
+
+    NORM_AT, CONV_AT = "1", "0"
 
     def __init__(self, conv: nn.Module, norm: nn.GroupNorm):
-        super().__init__()
-        self.add_module("0", conv)
-        self.add_module("1", norm)
-
-    @property
-    def conv(self) -> nn.Module:
-        return getattr(self, "0")
-
-    @property
-    def norm(self) -> nn.GroupNorm:
-        return getattr(self, "1")
+        super().__init__(norm, conv)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        n = self.norm
-        return group_norm_silu(self.conv(x), n.num_groups, n.weight, n.bias, n.eps)
+        return self._gn_silu(self.conv(x))
 
     def extra_repr(self) -> str:
         return "fused=GroupNorm+SiLU after conv"

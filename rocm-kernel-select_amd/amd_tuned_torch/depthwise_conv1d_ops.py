@@ -102,9 +102,11 @@ def _backward(dout, input_, weight, bias, padding: int, is_bhl: bool):
     elif input_.is_cuda and _native.available():
         dout = dout.contiguous()
         K = weight.shape[-1]
-        try:  # du, dw and db together (one pass over x and dout where the fused kernel applies)
+        try:  # du, dw and db together (one pass over x and dout where the fused kernel applies);
+            # dw / db come back None when only du is native (K > 5)
             du, dw32, db32 = _native.dwconv1d_backward(dout, input_, weight, padding, (True, True, True))
-            dw, db = dw32.to(weight.dtype), db32.to(dout.dtype)
+            if dw32 is not None:
+                dw, db = dw32.to(weight.dtype), db32.to(dout.dtype)
         except _native.Unsupported:
             du = dw = db = None
         if du is None:

@@ -30,6 +30,7 @@ plus "stock".  Policies kept from the reference because callers and tests depend
 """
 from __future__ import annotations
 
+import contextlib
 import json
 import math
 import os
@@ -114,31 +115,49 @@ def _reference_scale(reference_out) -> Optional[float]:
     return rms if (math.isfinite(rms) and rms > 0.0) else None
 
 
-def _verify(candidate_out, reference_out, tolerance=None) -> Optional[bool]:
-    """True = agrees, False = disagrees, None = indeterminate (the comparison ran out of
-    memory).  A comparison that cannot run for a reason about the candidate (shape, type)
-    is a failure, never a pass."""
-    try:
-        candidate_out, reference_out = candidate_out.detach(), reference_out.detach()
-        rtol, atol = tolerance if tolerance is not None else _TOLERANCES.get(
-            candidate_out.dtype, _DEFAULT_TOLERANCE)
-        scale = _reference_scale(reference_out)
-        if scale is not None:
-            atol = max(atol, rtol * scale)
-        if candidate_out.shape != reference_out.shape:
-            return False
-        if candidate_out.dim() == 0:
-            return bool(torch.allclose(candidate_out.float(), reference_out.float(),
-                                       rtol=rtol, atol=atol, equal_nan=True))
-        rows = candidate_out.shape[0]
-        per_row = max(1, candidate_out.numel() // max(1, rows))
-        step = max(1, _VERIFY_CHUNK_ELEMENTS // per_row)
-        for lo in range(0, rows, step):
-            hi = min(rows, lo + step)
-            if not torch.allclose(candidate_out[lo:hi].float(), reference_out[lo:hi].float(),
-                                  rtol=rtol, atol=atol, equal_nan=True):
-                return False
+def _block_disagrees(cand: torch.Tensor, ref: torch.Tensor, rtol: float, atol: float) -> bool:
+    """True if some element of the fp32 block pair is not within atol + rtol * |ref| of the
+    reference.  NaN matches only NaN and an infinity only the same infinity (torch.allclose
+    with equal_nan semantics)."""
+    c, r = cand.float(), ref.float()
+    finite = torch.isfinite(c) & torch.isfinite(r)
+    off = (c - r).abs_() > r.abs().mul_(rtol).add_(atol)
+    if bool((off & finite).any()):
         return True
+    odd = ~finite
+    if not bool(odd.any()):
+        return False
+    both_nan = c.isnan() & r.isnan()
+    same_inf = torch.isinf(c) & (c == r)
+    return bool((odd & ~(both_nan | same_inf)).any())
+
+
+def _row_blocks(n_rows: int, per_row: int):
+    """[lo, hi) ranges of dim-0 rows holding about _VERIFY_CHUNK_ELEMENTS elements each: a
+    slice along dim 0 is always a view, so no full-size copy is ever made."""
+    rows = max(1, _VERIFY_CHUNK_ELEMENTS // max(1, per_row))
+    return ((lo, min(n_rows, lo + rows)) for lo in range(0, n_rows, rows))
+
+
+def _verify(candidate_out, reference_out, tolerance=None) -> Optional[bool]:
+    """Does the candidate's output agree with the reference's?  True / False, or None when the
+    comparison itself ran out of memory (no verdict about the kernel).  The bar is the
+    reference's (kernel_select.py:164-295): max(atol, rtol * RMS(reference)) absolute plus
+    rtol relative, with (rtol, atol) from `tolerance` or the dtype table.  Anything that
+    keeps the comparison from running for a reason of the candidate's own (wrong shape, not
+    a tensor) is a disagreement."""
+    try:
+        cand, ref = candidate_out.detach(), reference_out.detach()
+        rtol, atol = tolerance or _TOLERANCES.get(cand.dtype, _DEFAULT_TOLERANCE)
+        scale = _reference_scale(ref)
+        atol = atol if scale is None else max(atol, rtol * scale)
+        if cand.shape != ref.shape:
+            return False
+        if cand.dim() == 0:
+            return not _block_disagrees(cand.reshape(1), ref.reshape(1), rtol, atol)
+        per_row = cand.numel() // max(1, cand.shape[0])
+        return not any(_block_disagrees(cand[lo:hi], ref[lo:hi], rtol, atol)
+                       for lo, hi in _row_blocks(cand.shape[0], per_row))
     except (RuntimeError, TypeError, ValueError, AttributeError) as exc:
         return None if _is_oom(exc) else False
 
@@ -185,54 +204,70 @@ def _decode_key(s: str):
     return tuple(_decode(e) for e in json.loads(s))
 
 
+def _file_payload() -> dict:
+    """The cache file's content (call with _lock held).  Sections: the verification-bar
+    version, winner names and excluded names per encoded key -- the reference's format
+    (kernel_select.py:310-423), so either package reads the other's file."""
+    return {
+        "verify_bar": _VERIFY_BAR_VERSION,
+        "winners": {_key_str(k): name for k, name in _winners.items()},
+        "bad": {_key_str(k): sorted(names) for k, names in _bad_candidates.items() if names},
+    }
+
+
+def _absorb_payload(raw) -> None:
+    """Merge a cache file's content into memory (entries already in memory win).  A flat
+    {key: winner} file from before the sections existed is read as winners.  Exclusions
+    judged under another verification bar are not evidence under this one: they are
+    dropped, and so are the winners of their keys, so those shapes are contested again."""
+    if not isinstance(raw, dict):
+        return
+    sectioned = "winners" in raw or "bad" in raw
+    winners = raw.get("winners", {}) if sectioned else raw
+    excluded = raw.get("bad", {}) if sectioned else {}
+    current = raw.get("verify_bar") == _VERIFY_BAR_VERSION
+
+    def decoded(items):
+        for text, value in items:
+            try:
+                yield _decode_key(text), text, value
+            except (ValueError, TypeError, AttributeError):
+                continue
+
+    with _lock:
+        for key, text, name in decoded(winners.items()):
+            if current or text not in excluded:
+                _winners.setdefault(key, name)
+        if current:
+            for key, _, names in decoded(excluded.items()):
+                _bad_candidates.setdefault(key, set()).update(names)
+
+
 def _load_disk_cache() -> None:
-    """Best effort; accepts the sectioned format and the older flat {key: winner} one."""
+    """Read this GPU's cache file, if enabled and readable (a missing or corrupt file is an
+    empty cache, never an error)."""
     if not _DISK_CACHE_ENABLED:
         return
     try:
         with open(_cache_path(), "r") as f:
-            raw = json.load(f)
+            _absorb_payload(json.load(f))
     except (OSError, ValueError):
         return
-    if not isinstance(raw, dict):
-        return
-    if "winners" in raw or "bad" in raw:
-        winners, bad = raw.get("winners", {}), raw.get("bad", {})
-    else:
-        winners, bad = raw, {}
-    stale = raw.get("verify_bar") != _VERIFY_BAR_VERSION
-    with _lock:
-        for ks, name in winners.items():
-            if stale and ks in bad:
-                continue
-            try:
-                _winners.setdefault(_decode_key(ks), name)
-            except (ValueError, TypeError, AttributeError):
-                continue
-        if not stale:
-            for ks, names in bad.items():
-                try:
-                    _bad_candidates.setdefault(_decode_key(ks), set()).update(names)
-                except (ValueError, TypeError, AttributeError):
-                    continue
 
 
 def _save_disk_cache() -> None:
-    """Rewrite the whole file atomically (temp file + os.replace)."""
+    """Write the whole cache file: a per-process temporary file renamed over the old one, so
+    readers only ever see a complete file."""
     if not _DISK_CACHE_ENABLED:
         return
     path = _cache_path()
+    with _lock:
+        payload = _file_payload()
+    tmp = f"{path}.tmp{os.getpid()}"
     try:
         os.makedirs(os.path.dirname(path), exist_ok=True)
-        with _lock:
-            raw = {
-                "verify_bar": _VERIFY_BAR_VERSION,
-                "winners": {_key_str(k): v for k, v in _winners.items()},
-                "bad": {_key_str(k): sorted(v) for k, v in _bad_candidates.items() if v},
-            }
-        tmp = f"{path}.tmp{os.getpid()}"
         with open(tmp, "w") as f:
-            json.dump(raw, f)
+            json.dump(payload, f)
         os.replace(tmp, path)
     except OSError:
         pass
@@ -466,15 +501,12 @@ def debug_bad_candidates() -> dict:
 
 
 def reset() -> None:
-    """Forget every winner and exclusion, in memory and this GPU's cache file."""
+    """Forget every winner and exclusion, in memory and in this GPU's cache file."""
     global _disk_loaded
-    _disk_loaded = True
     with _lock:
         _winners.clear()
         _bad_candidates.clear()
+    _disk_loaded = True  # the file is gone too: nothing to merge back in later
     if _DISK_CACHE_ENABLED:
-        try:
+        with contextlib.suppress(OSError):
             os.remove(_cache_path())
-        except OSError:
-            pass
-

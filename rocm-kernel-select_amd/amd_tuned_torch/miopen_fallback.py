@@ -28,6 +28,7 @@ from typing import Any, Callable, Optional
 import torch
 
 from . import _native
+from . import compile_ops
 from . import depthwise_conv1d_ops
 from . import kernel_select
 
@@ -291,68 +292,94 @@ def _try_channel_last_fastpath(input, weight, bias, stride, padding, dilation, g
     return y.transpose(1, 2)
 
 
-def _miopen_safe_conv(op_name: str, orig_fn: Callable) -> Callable:
-    def wrapped(input, weight, bias=None, stride=1, padding=0, dilation=1, groups=1):
-        out = _try_causal_conv1d_fastpath(input, weight, bias, stride, padding, dilation, groups)
-        if out is not None:
-            return out
-        out = _try_channel_last_fastpath(input, weight, bias, stride, padding, dilation, groups)
-        if out is not None:
-            return out
-        out = _try_depthwise_fastpath(input, weight, bias, stride, padding, dilation, groups,
-                                      orig_fn)
-        if out is not None:
-            return out
+def _traced_conv1d(input, weight, bias, stride, padding, dilation, groups, orig_fn):
+    """Under torch.compile: a (B, C, L) depthwise conv with integer padding becomes the
+    `amd_tuned_torch::depthwise_conv1d_forward` node (with its backward op under autograd);
+    anything else is the stock conv, which Dynamo traces as usual."""
+    pad = _scalar(padding)
+    ok = (compile_ops.native_loaded() and isinstance(pad, int) and not isinstance(pad, bool)
+          and _is_depthwise_conv1d_eligible(input, weight, bias, stride, padding, dilation, groups))
+    if not ok:
+        return orig_fn(input, weight, bias, stride, padding, dilation, groups)
+    w = weight.squeeze(1)
+    b = bias if bias is not None else input.new_zeros((weight.shape[0],))
+    # (inference mode cannot be queried while tracing; grad mode and requires_grad can)
+    if not (torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (input, weight, bias))):
+        return depthwise_conv1d_ops.conv1d_forward(input, w, b, pad, True)
+    return depthwise_conv1d_ops.DepthwiseConv1dFn.apply(input, w, b, pad, True)
+
+
+def _is_miopen_failure(exc: BaseException) -> bool:
+    return isinstance(exc, RuntimeError) and "miopenStatus" in str(exc)
+
+
+def _stock_with_rescue(op_name: str, orig_fn: Callable, input, weight, bias, stride, padding,
+                       dilation, groups):
+    """The stock conv, rescued from MIOpen failures the way the reference's wrapper does
+    (miopen_fallback.py:434-485): a GPU call that fails with a `miopenStatus` error is tried
+    once more after torch.cuda.empty_cache() (MIOpen's workspace allocation is the usual
+    cause), and if that fails too the conv runs on the CPU in fp32 and the result comes back
+    to the input's device and dtype.  Every other error propagates."""
+    attempts = 2 if input.is_cuda else 1
+    for attempt in range(attempts):
+        if attempt:
+            torch.cuda.empty_cache()
         try:
             return orig_fn(input, weight, bias, stride, padding, dilation, groups)
-        except RuntimeError as e:
-            if "miopenStatus" not in str(e):
+        except RuntimeError as exc:
+            if not _is_miopen_failure(exc):
                 raise
-            if input.is_cuda:
-                torch.cuda.empty_cache()
-                try:
-                    return orig_fn(input, weight, bias, stride, padding, dilation, groups)
-                except RuntimeError as e2:
-                    if "miopenStatus" not in str(e2):
-                        raise
-            print(f"MIOpen fallback ({op_name}): CPU used for this convolution (slow). "
-                  f"x shape: {tuple(input.shape)}, weight shape: {tuple(weight.shape)}")
-            dev, dt = input.device, input.dtype
-            out = orig_fn(input.float().cpu(), weight.float().cpu(),
-                          bias.float().cpu() if bias is not None else None,
-                          stride, padding, dilation, groups)
-            return out.to(device=dev, dtype=dt)
+    print(f"MIOpen fallback ({op_name}): CPU used for this convolution (slow). "
+          f"x shape: {tuple(input.shape)}, weight shape: {tuple(weight.shape)}")
+    on_cpu = [None if t is None else t.float().cpu() for t in (input, weight, bias)]
+    out = orig_fn(*on_cpu, stride, padding, dilation, groups)
+    return out.to(device=input.device, dtype=input.dtype)
+
+
+def _miopen_safe_conv(op_name: str, orig_fn: Callable) -> Callable:
+    """The F.conv1d replacement: the native paths in the reference's order, then stock."""
+
+    def wrapped(input, weight, bias=None, stride=1, padding=0, dilation=1, groups=1):
+        if compile_ops.is_compiling():
+            return _traced_conv1d(input, weight, bias, stride, padding, dilation, groups, orig_fn)
+        args = (input, weight, bias, stride, padding, dilation, groups)
+        for fast_path in (_try_causal_conv1d_fastpath, _try_channel_last_fastpath):
+            out = fast_path(*args)
+            if out is not None:
+                return out
+        out = _try_depthwise_fastpath(*args, orig_fn)
+        if out is not None:
+            return out
+        return _stock_with_rescue(op_name, orig_fn, *args)
 
     return wrapped
 
 
+# The installed wrapper and the F.conv1d it replaced (None while not installed).
 _original_conv1d: Optional[Callable] = None
-_CONV1D_FALLBACK_ENABLED = False
 
 
 def enable_conv1d_fallback() -> None:
     """Install the F.conv1d wrapper (idempotent)."""
-    global _original_conv1d, _CONV1D_FALLBACK_ENABLED
-    if _CONV1D_FALLBACK_ENABLED:
-        return
-    _original_conv1d = torch.nn.functional.conv1d
-    torch.nn.functional.conv1d = _miopen_safe_conv("conv1d", _original_conv1d)
-    _CONV1D_FALLBACK_ENABLED = True
+    global _original_conv1d
+    if _original_conv1d is None:
+        stock = torch.nn.functional.conv1d
+        torch.nn.functional.conv1d = _miopen_safe_conv("conv1d", stock)
+        _original_conv1d = stock
 
 
 def disable_conv1d_fallback() -> None:
-    """Restore stock F.conv1d."""
-    global _original_conv1d, _CONV1D_FALLBACK_ENABLED
-    if not _CONV1D_FALLBACK_ENABLED or _original_conv1d is None:
-        return
-    torch.nn.functional.conv1d = _original_conv1d
-    _original_conv1d = None
-    _CONV1D_FALLBACK_ENABLED = False
+    """Put stock F.conv1d back (idempotent)."""
+    global _original_conv1d
+    if _original_conv1d is not None:
+        torch.nn.functional.conv1d, _original_conv1d = _original_conv1d, None
 
 
 def is_conv1d_fallback_enabled() -> bool:
-    return _CONV1D_FALLBACK_ENABLED
+    return _original_conv1d is not None
 
 
+# Installed at import, independently of enable(); AMD_TUNED_TORCH_MIOPEN_CONV1D_FALLBACK=0
+# leaves F.conv1d alone.
 if _env_flag("AMD_TUNED_TORCH_MIOPEN_CONV1D_FALLBACK", default="1"):
     enable_conv1d_fallback()

@@ -27,6 +27,7 @@
 //   twopass  Streaming fallback for any size / alignment: a statistics kernel writes
 //            per-slice (mean, M2) partials, an apply kernel merges them and normalises.
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 
 #include "atk_common.h"
@@ -55,10 +56,12 @@ constexpr int GN_TP_NT = 256;                 // two-pass kernels
 constexpr int GN_BWD_U = 4;                   // backward: vectors of x and dy in flight per thread (most)
 constexpr int GN_MAX_AFF = 512;               // channels per slice whose affine is staged in LDS
 
-// One slot = two 64-bit words (1 << 32 | bits(mean)), (1 << 32 | bits(M2)), each stored
-// and read with single-copy-atomic relaxed agent-scope accesses: a reader that sees the
-// marker in both words has both values, with no fence on either side (agent-scope
-// acquire/release would write back / invalidate the XCD's L2 on every poll).  Empty = 0.
+// One slot = two 64-bit words (tag << 32 | bits(mean)), (tag << 32 | bits(M2)), each
+// stored and read with single-copy-atomic relaxed agent-scope accesses: a reader that sees
+// this launch's tag in both words has both values, with no fence on either side
+// (agent-scope acquire/release would write back / invalidate the XCD's L2 on every poll).
+// The tag is a nonzero per-launch number chosen by the host, so a slot left over from any
+// other launch (another shape, another tensor) never passes for this launch's; empty = 0.
 struct GnSlot {
   unsigned long long w[2];
 };
@@ -77,6 +80,7 @@ struct GnArgs {
   int pdt;            // dtype of gamma/beta
   FastDiv div_s;
   uint64_t wait_ticks;// wall-clock ticks to wait for a slot
+  uint32_t tag;       // this launch's slot marker (nonzero)
   uint32_t* diag;     // workspace: diagnostics word
   uint32_t* done;     // workspace: [ngroups] workgroups that finished reading the slots
   GnSlot* slots;      // workspace: [ngroups][NS] (register-resident)
@@ -303,8 +307,8 @@ void gn_resident_kernel(GnArgs a) {
     var = m2 / (float)((E - s0) < a.slice ? (E - s0) : a.slice);
   } else {
     GnSlot* slots = a.slots + gi * (int64_t)a.NS;
+    const unsigned long long hi = (unsigned long long)a.tag << 32;
     if (tid == 0) {
-      const unsigned long long hi = 1ull << 32;
       __hip_atomic_store(&slots[s].w[0], hi | __float_as_uint(mean_l), __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(&slots[s].w[1], hi | __float_as_uint(m2), __ATOMIC_RELAXED,
@@ -326,7 +330,7 @@ void gn_resident_kernel(GnArgs a) {
           for (;;) {
             w0 = __hip_atomic_load(&slots[j].w[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             w1 = __hip_atomic_load(&slots[j].w[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            ok = (w0 >> 32) != 0 && (w1 >> 32) != 0;
+            ok = (w0 >> 32) == a.tag && (w1 >> 32) == a.tag;
             if (ok || wall_clock64() - t0 > a.wait_ticks) break;
             __builtin_amdgcn_s_sleep(1);
           }
@@ -364,10 +368,15 @@ void gn_resident_kernel(GnArgs a) {
       }
       // This workgroup is done with the slots (its lanes' reads returned before this point).
       // The last of the group's NS workgroups -- every one has published by then -- empties
-      // them for the next launch and resets the counter.
+      // them for the next launch and resets the counter.  Thread 0 published this
+      // workgroup's slot; it waits for those stores to complete before counting itself
+      // done, so the last workgroup's clear can never be overtaken by a late publish (which
+      // would leave a filled slot behind).  One wait per workgroup, none per poll.
       uint32_t prev = 0;
-      if (tid == 0)
+      if (tid == 0) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         prev = __hip_atomic_fetch_add(a.done + gi, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
       prev = __shfl(prev, 0, 64);
       if (prev == (uint32_t)a.NS - 1) {
         for (int j = tid; j < a.NS; j += 64) {
@@ -551,6 +560,16 @@ struct GnPlan {
 };
 
 inline size_t round256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Per-launch slot marker: a process-wide counter, never 0 (0 marks an empty slot).  A HIP
+// graph replays the tag it captured; its launches still start from empty slots, because
+// the last workgroup of every group clears them.
+std::atomic<uint32_t> g_slot_tag{0};
+uint32_t next_slot_tag() {
+  uint32_t t = g_slot_tag.fetch_add(1u, std::memory_order_relaxed) + 1u;
+  while (t == 0u) t = g_slot_tag.fetch_add(1u, std::memory_order_relaxed) + 1u;
+  return t;
+}
 
 // Slicing and workspace size (layout: see GN_ZERO_BYTES / GN_PARTIALS_OFF)
 bool plan_gn(int64_t N, int64_t C, int64_t S, int G, int dtype, int variant, GnPlan& p) {
@@ -1181,6 +1200,7 @@ extern "C" int atk_group_norm_fwd(const void* x, const void* gamma, const void* 
   const char* wenv = getenv("ATK_GN_WAIT_US");
   const uint64_t wait_us = wenv ? strtoull(wenv, nullptr, 10) : GN_WAIT_US;
   a.wait_ticks = (uint64_t)(khz > 0 ? khz : 100000) * wait_us / 1000;
+  a.tag = next_slot_tag();
   const int64_t ngroups = N * G;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (dtype) {

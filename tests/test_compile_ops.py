@@ -62,3 +62,111 @@ def test_depthwise_conv1d_backward_fake_shapes_and_dtypes():
     assert du.shape == x.shape and du.dtype == x.dtype
     assert dweight.shape == w.shape and dweight.dtype == w.dtype
     assert dbias.shape == b.shape and dbias.dtype == dout.dtype
+
+
+# ---------------------------------------------------------------------------
+# torch.compile routing of the patched API (fake cuda tensors: Dynamo traces without a GPU)
+# ---------------------------------------------------------------------------
+def _capture(fn, *args):
+    """Compile fn with fullgraph=True (any graph break raises) and return the call targets
+    of the one captured FX graph."""
+    import torch._dynamo
+    torch._dynamo.reset()
+    graphs = []
+
+    def backend(gm, example_inputs):
+        graphs.append(gm)
+        return gm.forward
+    out = torch.compile(fn, backend=backend, fullgraph=True)(*args)
+    assert len(graphs) == 1
+    return out, [n.target for n in graphs[0].graph.nodes if n.op == "call_function"]
+
+
+def _fake_cuda(*shapes, dtype=torch.bfloat16, requires_grad=False):
+    with FakeTensorMode(allow_non_fake_inputs=True):
+        out = [torch.empty(s, device="cuda", dtype=dtype) for s in shapes]
+    return [t.requires_grad_(requires_grad) for t in out]
+
+
+def test_compiled_patched_ops_are_custom_op_nodes():
+    """Each patched entry point becomes one amd_tuned_torch node; no graph break, no Python
+    dispatch (ctypes, the selector) in the graph."""
+    x, w3, b3, g, b, x1, w1, b1, x2, w2 = _fake_cuda(
+        (1, 8, 4, 8, 8), (8, 8, 3, 3, 3), (8,), (8,), (8,), (2, 16, 64), (16, 1, 3), (16,),
+        (1, 8, 8, 8), (8, 8, 3, 3))
+
+    def block(x, w3, b3, g, b, x1, w1, b1, x2, w2):
+        y = F.conv3d(x, w3, b3, 1, 1)
+        y = F.group_norm(y, 4, g, b, 1e-5)
+        y = amd_tuned_torch.group_norm_silu(y, 4, g, b, 1e-5)
+        z = F.conv1d(x1, w1, b1, padding=1, groups=16)
+        u = F.conv2d(x2, w2, None, 1, 1)
+        return y, z, u
+
+    (y, z, u), targets = _capture(block, x, w3, b3, g, b, x1, w1, b1, x2, w2)
+    assert y.shape == x.shape and z.shape == x1.shape and u.shape == x2.shape
+    names = [str(t) for t in targets]
+    for op in ("conv3d_native", "group_norm", "group_norm_silu", "depthwise_conv1d_forward",
+               "conv2d_native"):
+        assert "amd_tuned_torch.%s" % op in names, names
+
+
+def test_compiled_routes_leave_ineligible_calls_to_stock():
+    """Grouped conv, 1x1 pointwise conv2d and string padding trace as stock aten calls."""
+    x, w_grp, w_pt = _fake_cuda((1, 8, 8, 8), (8, 4, 3, 3), (8, 8, 1, 1))
+
+    def f(x, w_grp, w_pt):
+        return F.conv2d(x, w_grp, None, 1, 1, 1, 2), F.conv2d(x, w_pt), F.conv2d(x, w_pt, padding="same")
+
+    _, targets = _capture(f, x, w_grp, w_pt)
+    assert not any("amd_tuned_torch" in str(t) for t in targets), targets
+
+
+def test_compiled_routes_with_gradients_keep_custom_ops():
+    """With parameters that require grad the same nodes appear (their autograd formulas are
+    registered); GroupNorm+SiLU becomes the GroupNorm node followed by F.silu."""
+    x, w3, g, b, x1, w1, b1 = _fake_cuda((1, 8, 4, 8, 8), (8, 8, 3, 3, 3), (8,), (8,), (2, 16, 64),
+                                         (16, 1, 3), (16,), requires_grad=True)
+
+    def f(x, w3, g, b, x1, w1, b1):
+        y = amd_tuned_torch.group_norm_silu(F.conv3d(x, w3, None, 1, 1), 4, g, b, 1e-5)
+        return y, F.conv1d(x1, w1, b1, padding=2, groups=16)
+
+    (y, z), targets = _capture(f, x, w3, g, b, x1, w1, b1)
+    names = [str(t) for t in targets]
+    assert "amd_tuned_torch.conv3d_native" in names and "amd_tuned_torch.group_norm" in names
+    assert "amd_tuned_torch.group_norm_silu" not in names
+    assert z.shape == (2, 16, 66)
+
+
+def test_custom_op_autograd_formulas_on_cpu():
+    """The registered backward of the conv and GroupNorm ops (on CPU tensors their eager
+    bodies take the stock paths) matches stock autograd; unrequested gradients stay None."""
+    torch.manual_seed(0)
+    x = torch.randn(2, 4, 5, 6, 6, dtype=torch.float64, requires_grad=True)
+    w = torch.randn(6, 4, 3, 3, 3, dtype=torch.float64, requires_grad=True)
+    b = torch.randn(6, dtype=torch.float64, requires_grad=True)
+    y = ops.conv3d_native(x, w, b, [1, 1, 1], [1, 1, 1], [1, 1, 1])
+    gy = torch.randn_like(y)
+    got = torch.autograd.grad(y, (x, w, b), gy)
+    ref = torch.autograd.grad(F.conv3d(x, w, b, 1, 1), (x, w, b), gy)
+    for a, r in zip(got, ref):
+        assert torch.allclose(a, r, atol=1e-10)
+    y2 = ops.conv2d_native(x[:, :, 0], w[:, :, 0], None, [1, 1], [0, 0], [1, 1])
+    (gx2,) = torch.autograd.grad(y2.sum(), (x,))
+    (rx2,) = torch.autograd.grad(F.conv2d(x[:, :, 0], w[:, :, 0]).sum(), (x,))
+    assert torch.allclose(gx2, rx2, atol=1e-10)
+
+    xg = torch.randn(3, 8, 5, 5, dtype=torch.float64, requires_grad=True)
+    gm = torch.randn(8, dtype=torch.float64, requires_grad=True)
+    bt = torch.randn(8, dtype=torch.float64, requires_grad=True)
+    out = ops.group_norm(xg, 4, gm, bt, 1e-5)
+    go = torch.randn_like(out)
+    got = torch.autograd.grad(out, (xg, gm, bt), go)
+    ref = torch.autograd.grad(F.group_norm(xg, 4, gm, bt, 1e-5), (xg, gm, bt), go)
+    for a, r in zip(got, ref):
+        assert torch.allclose(a, r, atol=1e-9)
+    # only the input needs a gradient: the parameter slots come back None
+    xg2 = xg.detach().requires_grad_(True)
+    (gx_only,) = torch.autograd.grad(ops.group_norm(xg2, 4, gm.detach(), bt.detach(), 1e-5).sum(), (xg2,))
+    assert gx_only.shape == xg2.shape

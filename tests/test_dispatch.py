@@ -454,3 +454,104 @@ def test_conv_dgrad_as_forward_conv_matches_stock():
     assert _dispatch._dgrad_padding(w, 1, 1, 2, 1, 3) is None          # dilation 2
     assert _dispatch._dgrad_padding(w, 1, 3, 1, 1, 3) is None          # padding > k-1
     assert _dispatch._dgrad_padding(w, 1, "same", 1, 1, 3) is None
+
+
+# ---------------------------------------------------------------------------
+# MIOpen rescue and the reference-shape causal mode (reference tests/test_miopen_fallback.py,
+# miopen_fallback.py:450-483)
+# ---------------------------------------------------------------------------
+def _conv1d_args(dtype=torch.float16):
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(2, 4, 16, generator=g).to(dtype)
+    w = torch.randn(6, 4, 3, generator=g).to(dtype)
+    b = torch.randn(6, generator=g).to(dtype)
+    return x, w, b
+
+
+def test_miopen_failure_is_rescued_on_cpu_in_fp32(capsys):
+    """An `orig` raising a miopenStatus error: the conv runs on the CPU in fp32 and comes back
+    in the input's dtype (a CPU input has no GPU retry), with the reference's notice."""
+    x, w, b = _conv1d_args()
+    calls = []
+
+    def flaky(inp, wt, bs, stride, padding, dilation, groups):
+        calls.append(inp.dtype)
+        if inp.dtype != torch.float32:
+            raise RuntimeError("miopenStatusUnknownError: conv failed")
+        return STOCK_CONV1D(inp, wt, bs, stride, padding, dilation, groups)
+
+    wrapped = miopen_fallback._miopen_safe_conv("conv1d", flaky)
+    y = wrapped(x, w, b, 1, 1)
+    ref = STOCK_CONV1D(x.float(), w.float(), b.float(), 1, 1).to(torch.float16)
+    assert y.dtype == torch.float16 and torch.equal(y, ref)
+    assert calls == [torch.float16, torch.float32]
+    assert "MIOpen fallback (conv1d): CPU used" in capsys.readouterr().out
+
+
+def test_miopen_rescue_leaves_other_errors_alone():
+    x, w, b = _conv1d_args()
+
+    def broken(*a):
+        raise RuntimeError("shape mismatch")
+    with pytest.raises(RuntimeError, match="shape mismatch"):
+        miopen_fallback._miopen_safe_conv("conv1d", broken)(x, w, b, 1, 1)
+
+
+def test_miopen_rescue_retries_gpu_call_after_empty_cache(monkeypatch):
+    """A GPU input is tried twice (the second time after torch.cuda.empty_cache()) before
+    the CPU fallback; a retry that succeeds is returned as is."""
+    x, w, b = _conv1d_args()
+
+    class GpuLike:  # stands in for a tensor that reports is_cuda (no GPU here)
+        is_cuda = True
+        shape = x.shape
+
+    attempts, emptied = [], []
+    monkeypatch.setattr(torch.cuda, "empty_cache", lambda: emptied.append(len(attempts)))
+
+    def once_flaky(inp, *rest):
+        attempts.append(1)
+        if len(attempts) == 1:
+            raise RuntimeError("miopenStatusInternalError")
+        return "second try"
+    out = miopen_fallback._stock_with_rescue("conv1d", once_flaky, GpuLike(), w, b, 1, 1, 1, 1)
+    assert out == "second try" and len(attempts) == 2 and emptied == [1]
+
+
+def test_causal_truncate_mode_gate(monkeypatch):
+    """AMD_TUNED_TORCH_CAUSAL_CONV1D_TRUNCATE=1 turns on the length-L causal path; it stays
+    off by default and never serves CPU tensors."""
+    x = torch.randn(2, 4, 32)
+    w = torch.randn(4, 1, 4)
+    monkeypatch.setattr(miopen_fallback, "_CAUSAL_TRUNCATE", False)
+    assert miopen_fallback._try_causal_conv1d_fastpath(x, w, None, 1, 3, 1, 4) is None
+    monkeypatch.setattr(miopen_fallback, "_CAUSAL_TRUNCATE", True)
+    assert miopen_fallback._try_causal_conv1d_fastpath(x, w, None, 1, 3, 1, 4) is None  # CPU
+    assert miopen_fallback._is_causal_conv1d_eligible(x, w, 1, 3, 1, 4) is False       # not cuda
+    y = F.conv1d(x, w, None, 1, 3, 1, 4)  # CPU: stock shape either way
+    assert y.shape == (2, 4, 35)
+
+
+def test_workspaces_are_private_per_stream_and_retired_on_growth(monkeypatch):
+    """Scratch is pooled per (device, stream, purpose); a grown buffer replaces the old one,
+    which stays alive (a captured graph may still point at it)."""
+    class FakeStream:
+        def __init__(self, h):
+            self.cuda_stream = h
+    current = [FakeStream(11)]
+    monkeypatch.setattr(torch.cuda, "current_stream", lambda device=None: current[0])
+    real_zeros = torch.zeros
+    monkeypatch.setattr(torch, "zeros", lambda n, dtype=None, device=None: real_zeros(n, dtype=dtype))
+    monkeypatch.setattr(_native, "_ws_live", {})
+    monkeypatch.setattr(_native, "_ws_retired", [])
+    dev = torch.device("cuda", 0)
+    a = _native.workspace(dev, "conv", 100)
+    assert _native.workspace(dev, "conv", 50) is a            # same stream, fits: reused
+    current[0] = FakeStream(22)
+    b = _native.workspace(dev, "conv", 100)
+    assert b is not a                                         # another stream: its own buffer
+    current[0] = FakeStream(11)
+    grown = _native.workspace(dev, "conv", 1 << 20)
+    assert grown.numel() >= 1 << 20 and grown is not a
+    assert any(r is a for r in _native._ws_retired)           # retired, not freed
+    assert _native.workspace_keys() == [(0, 11, "conv"), (0, 22, "conv")]
