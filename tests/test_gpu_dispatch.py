@@ -86,15 +86,16 @@ def test_depthwise_autograd_k7_same_keeps_native_dx(dev, dtype, monkeypatch):
     xd = x.to(dev).requires_grad_(True)
     wd = w.to(dev).unsqueeze(1).requires_grad_(True)
     bd = b.to(dev).requires_grad_(True)
-    y = F.conv1d(xd, wd, bd, padding=pad, groups=C)
+    y = F.conv1d(xd, wd, bd, padding=pad, groups=C)   # first call: the contest runs every variant
     assert O.max_rel_err(y.detach().cpu(), O.dwconv1d(x, w, b, pad, L)) <= BAR[dtype]
+    calls.clear()
     gx, gw, gb = torch.autograd.grad(y, (xd, wd, bd), dy.to(dev))
     rdx, rdw, rdb = O.dwconv1d_bwd(x, w, dy, pad)
     assert O.max_rel_err(gx.cpu(), rdx) <= BAR[dtype]
     assert O.max_rel_err(gw.cpu().reshape(C, K), rdw) <= max(BAR[dtype], 1e-4)
     assert O.max_rel_err(gb.cpu(), rdb) <= max(BAR[dtype], 1e-4)
-    # forward on x plus the input gradient as the forward kernel on dy
-    assert len(calls) == 2 and calls[1] == (N, C, L)
+    # the backward ran the input gradient as the forward kernel on dy, once
+    assert calls == [(N, C, L)]
     direct = nat.dwconv1d_backward(dy.to(dev), x.to(dev), w.to(dev), pad, (True, True, True))
     assert direct[0] is not None and direct[1] is None and direct[2] is None
 
@@ -238,13 +239,24 @@ def test_two_streams_do_not_share_scratch(dev):
     gn_v = names.index("res_nt256_v8")
     streams = [torch.cuda.Stream(dev), torch.cuda.Stream(dev)]
     dev_jobs = [[t.to(dev) for t in job] for job in jobs]
+
+    def mfma_variant(xc, wc):  # an implicit-GEMM tile taking the shape (it packs weights in scratch)
+        for vi, name in enumerate(nat.variants(nat.OP_CONV)):
+            if name.startswith("h_"):
+                try:
+                    nat.conv3d(xc, wc, None, 1, 1, 1, variant=vi)
+                    return vi
+                except nat.Unsupported:
+                    continue
+        raise AssertionError("no MFMA tile takes the shape")
+    conv_v = [mfma_variant(job[3], job[4]) for job in dev_jobs]
     torch.cuda.synchronize()
     outs = [[], []]
     for rep in range(4):
         for k, (s, (xg, gm, bt, xc, wc)) in enumerate(zip(streams, dev_jobs)):
             with torch.cuda.stream(s):
                 outs[k].append((nat.group_norm(xg, 32, gm, bt, 1e-5, variant=gn_v),
-                                nat.conv3d(xc, wc, None, 1, 1, 1)))
+                                nat.conv3d(xc, wc, None, 1, 1, 1, variant=conv_v[k])))
     torch.cuda.synchronize()
     keys = nat.workspace_keys()
     handles = {s.cuda_stream for s in streams}
