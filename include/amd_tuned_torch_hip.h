@@ -247,6 +247,23 @@ int atk_group_norm_fwd(const void* x, const void* gamma, const void* beta, void*
                        size_t workspace_bytes, atk_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * GroupNorm forward that allocates nothing and takes no workspace.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory or hand over scratch --
+ * code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.  Same
+ * arguments (minus the workspace), kernels and results as atk_group_norm_fwd; the caller
+ * still passes x and y.  The scratch is a static device array of
+ * atk_group_norm_noalloc_scratch_bytes() bytes (about 2.1 MB) that each GPU the library
+ * runs on holds until the process ends; shapes needing more (two-pass partials above 1 MiB)
+ * are rejected with ATK_EINVAL.  Every call on one GPU shares that GPU's array, so calls that
+ * overlap on one GPU (e.g. on two streams) race; calls ordered on one stream do not.  The
+ * first call on a device resolves the array's address there (make it outside graph capture).
+ * ------------------------------------------------------------------------- */
+size_t atk_group_norm_noalloc_scratch_bytes(void);
+int atk_group_norm_fwd_noalloc(const void* x, const void* gamma, const void* beta, void* y,
+                               int64_t N, int64_t C, int64_t S, int G, float eps, int fuse_silu,
+                               int dtype, int param_dtype, int variant, atk_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * GroupNorm forward, channels-last layout (NHWC / NDHWC memory: x[n][s][c]), optional
  * fused SiLU.  The reference serves this layout with Composable Kernel's groupnorm
  * (amd_tuned_torch/ck_norm_ops.py:9-27,93-103, picked by the contest in

@@ -42,7 +42,7 @@ EXPORTED_SYMBOLS = (
     "atk_group_norm_cl_fwd", "atk_group_norm_bwd_workspace_bytes",
     "atk_group_norm_bwd", "atk_conv_workspace_bytes",
     "atk_conv_fwd", "atk_conv_wgrad_workspace_bytes", "atk_conv_wgrad", "atk_transpose_last2",
-    "atk_dwconv1d_bwd",
+    "atk_dwconv1d_bwd", "atk_group_norm_noalloc_scratch_bytes", "atk_group_norm_fwd_noalloc",
 )
 
 
@@ -114,6 +114,11 @@ def _declare(lib) -> None:
     lib.atk_transpose_last2.restype = i32
     lib.atk_dwconv1d_bwd.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i32, i32, i64, i32, vp, sz, vp]
     lib.atk_dwconv1d_bwd.restype = i32
+    lib.atk_group_norm_noalloc_scratch_bytes.argtypes = []
+    lib.atk_group_norm_noalloc_scratch_bytes.restype = sz
+    lib.atk_group_norm_fwd_noalloc.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, c.c_float, i32, i32, i32,
+                                               i32, vp]
+    lib.atk_group_norm_fwd_noalloc.restype = i32
 
 
 def load(path: str = LIB_PATH):
@@ -658,6 +663,33 @@ def group_norm(input: torch.Tensor, num_groups: int, weight: Optional[torch.Tens
                               _stream(input))
     _check(rc, "group_norm")
     return y
+
+
+def group_norm_noalloc(input: torch.Tensor, num_groups: int, out: torch.Tensor,
+                       weight: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None,
+                       eps: float = 1e-5, *, silu: bool = False, variant: int = -1) -> torch.Tensor:
+    """group_norm through atk_group_norm_fwd_noalloc: no workspace, the library's static
+    per-GPU scratch instead (calls overlapping on one GPU race on it).  `out` is the caller's
+    output tensor (input's shape and dtype, contiguous); nothing is allocated on the device."""
+    _require_cuda(input, weight, bias, out)
+    if not (input.is_contiguous() and out.is_contiguous()) or out.shape != input.shape or out.dtype != input.dtype:
+        raise RuntimeError("group_norm_noalloc: contiguous input and an out of the same shape and dtype")
+    if input.dtype not in _DTYPE_CODE or input.dim() < 2:
+        raise RuntimeError("group_norm_noalloc: (N, C, ...) input of float16, bfloat16 or float32")
+    if weight is not None and bias is not None and weight.dtype != bias.dtype:
+        raise RuntimeError("group_norm_noalloc: weight and bias must share a dtype")
+    for p in (weight, bias):
+        if p is not None and (not p.is_contiguous() or p.dtype not in _DTYPE_CODE):
+            raise RuntimeError("group_norm_noalloc: weight / bias must be contiguous float16/bfloat16/float32")
+    N, C = input.shape[0], input.shape[1]
+    S = input.numel() // max(1, N * C) if N * C > 0 else 1
+    pdt = _DTYPE_CODE[(weight if weight is not None else bias).dtype] if (weight is not None or bias is not None) \
+        else ATK_F32
+    rc = lib().atk_group_norm_fwd_noalloc(_ptr(input), _ptr(weight), _ptr(bias), _ptr(out), N, C, S,
+                                          int(num_groups), float(eps), int(bool(silu)), _DTYPE_CODE[input.dtype],
+                                          pdt, int(variant), _stream(input))
+    _check(rc, "group_norm_noalloc")
+    return out
 
 
 def transpose_last2(x: torch.Tensor, B: int, R: int, C: int, out: torch.Tensor) -> torch.Tensor:

@@ -29,6 +29,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cstdlib>
+#include <mutex>
 
 #include "atk_common.h"
 
@@ -1158,11 +1159,13 @@ extern "C" size_t atk_group_norm_workspace_zero_bytes(int64_t N, int64_t C, int6
   return p.zero_bytes;
 }
 
-extern "C" int atk_group_norm_fwd(const void* x, const void* gamma, const void* beta, void* y,
-                                  int64_t N, int64_t C, int64_t S, int G, float eps, int fuse_silu,
-                                  int dtype, int param_dtype, int variant, void* workspace,
-                                  size_t workspace_bytes, atk_stream_t stream) {
-  using namespace atk;
+namespace atk {
+namespace {
+
+// The forward behind both entry points: `ws` is the caller's workspace or the static scratch.
+int gn_fwd(const void* x, const void* gamma, const void* beta, void* y, int64_t N, int64_t C, int64_t S,
+           int G, float eps, int fuse_silu, int dtype, int param_dtype, int variant, void* workspace,
+           size_t workspace_bytes, hipStream_t s, size_t* need_out) {
   if (variant < 0) variant = 0;
   int rc = validate_gn(N, C, S, G, dtype, variant);
   if (rc) return rc;
@@ -1173,6 +1176,7 @@ extern "C" int atk_group_norm_fwd(const void* x, const void* gamma, const void* 
   GnPlan p;
   if (!plan_gn(N, C, S, G, dtype, variant, p))
     return fail(ATK_UNSUPPORTED, "group_norm: too many slices per group for %s", kGnVariants[variant].name);
+  if (need_out) *need_out = p.ws_bytes;
   if (!workspace || workspace_bytes < p.ws_bytes)
     return fail(ATK_EINVAL, "group_norm: workspace of %zu bytes needed", p.ws_bytes);
   const size_t es = dtype_size(dtype);
@@ -1202,12 +1206,89 @@ extern "C" int atk_group_norm_fwd(const void* x, const void* gamma, const void* 
   a.wait_ticks = (uint64_t)(khz > 0 ? khz : 100000) * wait_us / 1000;
   a.tag = next_slot_tag();
   const int64_t ngroups = N * G;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (dtype) {
     case ATK_F32: return launch_gn<float>(a, ngroups, variant, vec_ok, s);
     case ATK_F16: return launch_gn<_Float16>(a, ngroups, variant, vec_ok, s);
     default: return launch_gn<__bf16>(a, ngroups, variant, vec_ok, s);
   }
+}
+
+}  // namespace
+}  // namespace atk
+
+extern "C" int atk_group_norm_fwd(const void* x, const void* gamma, const void* beta, void* y,
+                                  int64_t N, int64_t C, int64_t S, int G, float eps, int fuse_silu,
+                                  int dtype, int param_dtype, int variant, void* workspace,
+                                  size_t workspace_bytes, atk_stream_t stream) {
+  return atk::gn_fwd(x, gamma, beta, y, N, C, S, G, eps, fuse_silu, dtype, param_dtype, variant, workspace,
+                     workspace_bytes, reinterpret_cast<hipStream_t>(stream), nullptr);
+}
+
+// ---------------------------------------------------------------------------------------
+// No-allocation GroupNorm forward.  The scratch that atk_group_norm_fwd takes from the caller
+// (diagnostics word, per-group counters, slot table, two-pass partials) lives in a fixed
+// device array instead.  Static device memory starts zeroed, and every launch leaves the
+// counters and slots zero again, which is the state the kernels need.  Each GPU holds its own
+// copy for the life of the process; its address is looked up once per device with
+// hipGetSymbolAddress, and that address -- never the array's name, which in host code is only
+// a stand-in -- is what the kernels get.
+// ---------------------------------------------------------------------------------------
+namespace atk {
+namespace {
+
+constexpr size_t GN_NOALLOC_PARTIAL_BYTES = (size_t)1 << 20;  // 131072 (mean, M2) pairs
+constexpr size_t GN_NOALLOC_BYTES = GN_PARTIALS_OFF + GN_NOALLOC_PARTIAL_BYTES;
+constexpr int GN_NOALLOC_MAX_DEVICES = 64;
+
+static __device__ __align__(256) unsigned char scratch[GN_NOALLOC_BYTES];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[GN_NOALLOC_MAX_DEVICES] = {};
+
+// The current device's copy of `scratch`, resolved on the first call on that device.
+int current_scratch(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= GN_NOALLOC_MAX_DEVICES)
+    return fail(ATK_ELAUNCH, "group_norm (no-alloc): no current device (or device index >= %d)",
+                GN_NOALLOC_MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(ATK_ELAUNCH, "group_norm (no-alloc): hipGetSymbolAddress failed on device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return ATK_OK;
+}
+
+}  // namespace
+}  // namespace atk
+
+extern "C" size_t atk_group_norm_noalloc_scratch_bytes(void) { return atk::GN_NOALLOC_BYTES; }
+
+extern "C" int atk_group_norm_fwd_noalloc(const void* x, const void* gamma, const void* beta, void* y,
+                                          int64_t N, int64_t C, int64_t S, int G, float eps, int fuse_silu,
+                                          int dtype, int param_dtype, int variant, atk_stream_t stream) {
+  using namespace atk;
+  if (variant < 0) variant = 0;
+  int rc = validate_gn(N, C, S, G, dtype, variant);
+  if (rc) return rc;
+  if (N == 0) return ATK_OK;
+  GnPlan p;
+  if (!plan_gn(N, C, S, G, dtype, variant, p))
+    return fail(ATK_UNSUPPORTED, "group_norm: too many slices per group for %s", kGnVariants[variant].name);
+  if (p.ws_bytes > GN_NOALLOC_BYTES)
+    return fail(ATK_EINVAL, "group_norm (no-alloc): this shape and variant need %zu bytes of scratch; the "
+                "static scratch holds %zu (use atk_group_norm_fwd with a workspace)", p.ws_bytes,
+                GN_NOALLOC_BYTES);
+  void* ws = nullptr;
+  rc = current_scratch(&ws);
+  if (rc) return rc;
+  return gn_fwd(x, gamma, beta, y, N, C, S, G, eps, fuse_silu, dtype, param_dtype, variant, ws, GN_NOALLOC_BYTES,
+                reinterpret_cast<hipStream_t>(stream), nullptr);
 }
 
 extern "C" size_t atk_group_norm_bwd_workspace_bytes(int64_t N, int64_t C) {
