@@ -91,6 +91,36 @@ def graph_time_ms(fn, iters: int) -> float:
         return event_time_ms(fn, iters)
 
 
+def cold_graph_time_ms(fn, like, bytes_per_call: int, footprint: int = 768 << 20, rounds: int = 4) -> float:
+    """Average ms per call of fn(x_i, y_i) over rotating input/output sets whose total size
+    (>= `footprint`, three times the 256 MB Infinity Cache) keeps every call's data out of the
+    caches: each set is touched once per round, so every call reads and writes HBM.  The
+    calls are captured in one HIP graph (no host work between them) and the replay is timed."""
+    import torch
+    sets = max(2, -(-footprint // max(1, bytes_per_call)))
+    xs = [like.clone() for _ in range(sets)]
+    ys = [torch.empty_like(like) for _ in range(sets)]
+    for i in range(sets):
+        fn(xs[i], ys[i])
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(rounds):
+            for i in range(sets):
+                fn(xs[i], ys[i])
+    graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    graph.replay()
+    b.record()
+    b.synchronize()
+    ms = a.elapsed_time(b) / (rounds * sets)
+    del graph, xs, ys
+    torch.cuda.empty_cache()
+    return ms
+
+
 def max_rel_err(y, ref) -> float:
     y, ref = y.float(), ref.float()
     den = ref.abs().max().item()
@@ -143,6 +173,74 @@ def bench_dw_detail(dtype, mode, dev):
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"ms": round(ms, 4), "GB/s": round(gbs, 1), "roofline_frac": round(gbs / HBM_PEAK_GBS, 4),
             "variant": won, "max_rel_err_vs_stock_fp32": float(f"{err:.3g}")}
+
+
+# ---------------------------------------------------------------------------
+# config 1: the reference's CPU-runnable depthwise conv1d ([8,256,2048], k3, p1, bias)
+# ---------------------------------------------------------------------------
+def c1_inputs(dtype, dev=None):
+    """x ~ N(0,1), w ~ N(0,1/3), b ~ N(0,0.1) (second argument = variance), seed 1001."""
+    import torch
+    g = _gen(1001)
+    x = torch.randn(8, 256, 2048, generator=g)
+    w = torch.randn(256, 1, 3, generator=g) * (1.0 / 3.0) ** 0.5
+    b = torch.randn(256, generator=g) * 0.1 ** 0.5
+    out = [t.to(dtype) for t in (x, w, b)]
+    return [t.to(dev) for t in out] if dev is not None else out
+
+
+def bench_c1_gpu_detail(dtype, dev):
+    """Config 1's workload on the GPU through the patched F.conv1d: the winning kernel alone
+    (graph-replayed) and the whole patched call (eager, per call), GB/s on the algorithmic
+    bytes (x read + y written + w + b)."""
+    import torch
+    import torch.nn.functional as F
+    import amd_tuned_torch
+    from amd_tuned_torch import kernel_select
+    x, w, b = c1_inputs(dtype, dev)
+    y = F.conv1d(x, w, b, padding=1, groups=256)
+    ref = amd_tuned_torch.miopen_fallback._original_conv1d(x.float(), w.float(), b.float(), 1, 1, 1, 256)
+    err = max_rel_err(y, ref)
+    won = kernel_select.cached("conv1d", x, w, 1, 1, 1) or "?"
+    if won.startswith("native."):
+        from amd_tuned_torch import _native as nat
+        vi = nat.variants(nat.OP_DWCONV1D).index(won[7:])
+        out = torch.empty_like(y)
+        w2 = w.squeeze(1).contiguous()
+        ms = graph_time_ms(lambda: nat.dwconv1d(x, w2, b, 1, 2048, variant=vi, out=out), 100)
+    else:
+        ms = event_time_ms(lambda: F.conv1d(x, w, b, padding=1, groups=256), 100)
+    call_ms = event_time_ms(lambda: F.conv1d(x, w, b, padding=1, groups=256), 200)
+    nbytes = 2 * x.numel() * x.element_size() + (w.numel() + b.numel()) * w.element_size()
+    return {"kernel_us": round(ms * 1e3, 2), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "roofline_frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "patched_call_us": round(call_ms * 1e3, 2),
+            "patched_call_GB/s": round(nbytes / (call_ms * 1e-3) / 1e9, 1),
+            "variant": won, "bytes": nbytes, "max_rel_err_vs_stock_fp32": float(f"{err:.3g}")}
+
+
+def bench_c1_cpu_dispatch_overhead():
+    """Config 1 exactly as the reference runs it: fp32 on the CPU, where the patched F.conv1d
+    declines every native path and calls stock.  Reports both per-call times (min over
+    alternating rounds), the wrapper's overhead and whether the outputs are bit-identical."""
+    import torch
+    import torch.nn.functional as F
+    import amd_tuned_torch
+    stock = amd_tuned_torch.miopen_fallback._original_conv1d
+    x, w, b = c1_inputs(torch.float32)
+    patched = lambda: F.conv1d(x, w, b, padding=1, groups=256)  # noqa: E731
+    plain = lambda: stock(x, w, b, 1, 1, 1, 256)  # noqa: E731
+    exact = bool(torch.equal(patched(), plain()))
+    best = {"stock": float("inf"), "patched": float("inf")}
+    for _ in range(15):
+        for name, fn in (("stock", plain), ("patched", patched)):
+            t0 = time.perf_counter()
+            fn()
+            best[name] = min(best[name], time.perf_counter() - t0)
+    return {"stock_us": round(best["stock"] * 1e6, 1), "patched_us": round(best["patched"] * 1e6, 1),
+            "overhead_us": round((best["patched"] - best["stock"]) * 1e6, 1),
+            "bit_exact_vs_stock": exact, "threads": torch.get_num_threads(),
+            "note": "fp32 on the host CPU, [8,256,2048] k3 p1 groups=256, min of 15 alternating runs"}
 
 
 # ---------------------------------------------------------------------------
@@ -499,16 +597,30 @@ def bench_gn_detail(shape, G, eps, dtype, silu, dev):
         if k[0] == kind and (tuple(x.shape) in k):
             won = v
     won = won or "?"
+    nbytes = 2 * x.numel() * x.element_size()
     if won.startswith("native."):
         vi = nat.variants(nat.OP_GROUP_NORM).index(won[7:])
         out = torch.empty_like(x)
         ms = graph_time_ms(lambda: nat.group_norm(x, G, gm, bt, eps, silu=silu, variant=vi, out=out), 50)
+        cold_ms = cold_graph_time_ms(lambda xi, yi: nat.group_norm(xi, G, gm, bt, eps, silu=silu, variant=vi, out=yi),
+                                     x, nbytes)
     else:
         ms = event_time_ms(lambda: torch.group_norm(x, G, gm, bt, eps), 50)
-    nbytes = 2 * x.numel() * x.element_size()
+        cold_ms = None
+    if silu:
+        call = lambda: amd_tuned_torch.group_norm_silu(x, G, gm, bt, eps)  # noqa: E731
+    else:
+        call = lambda: F.group_norm(x, G, gm, bt, eps)  # noqa: E731
+    call_ms = event_time_ms(call, 100)
     gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"ms": round(ms, 4), "GB/s": round(gbs, 1), "roofline_frac": round(gbs / HBM_PEAK_GBS, 4),
-            "variant": won, "max_rel_err_vs_stock_fp32": float(f"{err:.3g}")}
+    res = {"ms": round(ms, 4), "GB/s": round(gbs, 1), "roofline_frac": round(gbs / HBM_PEAK_GBS, 4),
+           "variant": won, "max_rel_err_vs_stock_fp32": float(f"{err:.3g}"),
+           "patched_call_ms": round(call_ms, 4),
+           "patched_call_roofline_frac": round(nbytes / (call_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    if cold_ms is not None:
+        res.update({"cold_ms": round(cold_ms, 4),
+                    "cold_roofline_frac": round(nbytes / (cold_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+    return res
 
 
 # ---------------------------------------------------------------------------
@@ -541,9 +653,12 @@ def bench_conv_detail(xs, ws, pad, dtype, dev, iters=20):
     flops = 2.0 * xs[0] * ws[0] * osp * ws[1] * math.prod(ws[2:])
     tf = flops / (ms * 1e-3) / 1e12
     key = {torch.bfloat16: "bf16", torch.float16: "fp16", torch.float32: "fp32"}[dtype]
+    call_ms = event_time_ms(lambda: F.conv3d(x, w, b, 1, pad), iters)
     res = {"ms": round(ms, 4), "TFLOP/s": round(tf, 2),
            "roofline_frac": round(tf / MFMA_PEAK_TFLOPS[key], 4), "variant": won,
-           "max_rel_err_vs_stock_fp32": float(f"{err:.3g}")}
+           "max_rel_err_vs_stock_fp32": float(f"{err:.3g}"),
+           "patched_call_ms": round(call_ms, 4),
+           "patched_call_roofline_frac": round(flops / (call_ms * 1e-3) / 1e12 / MFMA_PEAK_TFLOPS[key], 4)}
     if dtype != torch.float32:
         # the same GEMM (M = output positions, N = Co, K = Ci*k^3) through torch.matmul
         # (hipBLASLt), operands already laid out: what a library GEMM does without the gather
@@ -620,11 +735,33 @@ def calibration(dev):
 # ---------------------------------------------------------------------------
 # CPU baseline: stock torch.nn.functional on the host (the reference's CPU path)
 # ---------------------------------------------------------------------------
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_share() -> "tuple[int, str]":
+    """Threads for the CPU baseline and why: the host cores this process may run on
+    (sched_getaffinity), capped by OMP_NUM_THREADS when the job sets it (the GPU box allots
+    16 host threads per GPU that way, whatever os.cpu_count() shows)."""
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and 0 < int(omp) < usable:
+        return int(omp), f"OMP_NUM_THREADS={omp} (the job's host-thread share) of {usable} usable cores"
+    return usable, f"all {usable} cores this process may run on"
+
+
 def cpu_baseline(rows_sample: int = 1):
     import torch
     import amd_tuned_torch
     conv1d = amd_tuned_torch.miopen_fallback._original_conv1d or torch.nn.functional.conv1d
-    threads = min(16, os.cpu_count() or 1)
+    threads, why = _cpu_share()
     torch.set_num_threads(threads)
     g = _gen(1002)
     C, L, K = 2048, 8192, 4
@@ -641,8 +778,9 @@ def cpu_baseline(rows_sample: int = 1):
         best = min(best, time.perf_counter() - t0)
         rounds += 1
     nbytes = 2 * x.numel() * 2  # the bf16 workload's algorithmic bytes for this sample
-    return {"value": round(nbytes / best / 1e9, 2), "unit": "GB/s", "cores": threads,
-            "kind": "reference",
+    return {"value": round(nbytes / best / 1e9, 2), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "reference", "threads_reason": why, "os_cpu_count": os.cpu_count(),
+            "cpu_model": _cpu_model(), "torch": torch.__version__,
             "sample": (f"stock torch.nn.functional.conv1d (fp32 upcast of the bf16 inputs) on "
                        f"{rows_sample} of the 16 batch rows ([{rows_sample},2048,8192], k=4, pad=3, "
                        f"[..., :L]), min of {rounds} runs; GB/s counts the bf16 workload's "
@@ -1054,6 +1192,9 @@ def main():
     details = {}
     if not args.no_details:
         plan = [
+            ("c1_gpu_fp32", lambda: bench_c1_gpu_detail(torch.float32, dev)),
+            ("c1_gpu_fp16", lambda: bench_c1_gpu_detail(torch.float16, dev)),
+            ("c1_cpu_dispatch_overhead", bench_c1_cpu_dispatch_overhead),
             ("c2_causal_fp16", lambda: bench_dw_detail(torch.float16, "causal", dev)),
             ("c2_sym_k3_bf16", lambda: bench_dw_detail(torch.bfloat16, "sym", dev)),
             ("c2_sym_k3_fp16", lambda: bench_dw_detail(torch.float16, "sym", dev)),

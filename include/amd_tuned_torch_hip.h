@@ -323,6 +323,39 @@ int atk_conv_fwd(const void* x, const void* w, const void* bias, void* y, int64_
                  atk_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * The same convolution in two steps, for weights that stay constant across calls (the
+ * reference's native conv re-derives its weight layout inside every `conv3d` /
+ * `conv2d` call, src/main_rocm.cpp:669-715,798-854; inference weights need it once):
+ *   atk_conv_pack_weights   w -> packed (atk_conv_packed_weight_bytes bytes, the fragment
+ *                           order MFMA variant `variant` reads; valid for that variant and
+ *                           geometry only, and only while w is unchanged);
+ *   atk_conv_fwd_prepacked  y from x and the packed weights; the workspace holds only the
+ *                           split-K partial sums (atk_conv_prepacked_workspace_bytes bytes,
+ *                           0 when the variant does not split this shape).
+ * Same geometry arguments, arithmetic and results as atk_conv_fwd.  Variant 0 (the direct
+ * kernel) has no packed form: ATK_UNSUPPORTED.  The size queries return 0 for shapes the
+ * variant declines.
+ * ------------------------------------------------------------------------- */
+size_t atk_conv_packed_weight_bytes(int64_t N, int64_t Ci, int64_t D, int64_t H, int64_t W,
+                                    int64_t Co, int KD, int KH, int KW, int sd, int sh, int sw,
+                                    int pd, int ph, int pw, int dd, int dh, int dw, int dtype,
+                                    int variant);
+size_t atk_conv_prepacked_workspace_bytes(int64_t N, int64_t Ci, int64_t D, int64_t H, int64_t W,
+                                          int64_t Co, int KD, int KH, int KW, int sd, int sh,
+                                          int sw, int pd, int ph, int pw, int dd, int dh, int dw,
+                                          int dtype, int variant);
+int atk_conv_pack_weights(const void* w, void* packed, size_t packed_bytes, int64_t N, int64_t Ci,
+                          int64_t D, int64_t H, int64_t W, int64_t Co, int KD, int KH, int KW,
+                          int sd, int sh, int sw, int pd, int ph, int pw, int dd, int dh, int dw,
+                          int dtype, int variant, atk_stream_t stream);
+int atk_conv_fwd_prepacked(const void* x, const void* packed, size_t packed_bytes,
+                           const void* bias, void* y, int64_t N, int64_t Ci, int64_t D,
+                           int64_t H, int64_t W, int64_t Co, int KD, int KH, int KW, int sd,
+                           int sh, int sw, int pd, int ph, int pw, int dd, int dh, int dw,
+                           int dtype, int variant, void* workspace, size_t workspace_bytes,
+                           atk_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Conv weight gradient (replaces the dweight part of `aten.convolution_backward` that the
  * reference's _Conv3dFn.backward calls, amd_tuned_torch/_dispatch.py:2064-2075), for
  * stride-1, dilation-1 convs with kernel (KD, 3, 3), KD in {1, 3}, and "same" padding

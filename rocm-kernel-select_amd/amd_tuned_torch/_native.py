@@ -18,6 +18,7 @@ from __future__ import annotations
 import ctypes
 import os
 import threading
+import weakref
 from typing import Optional, Sequence
 
 import torch
@@ -43,6 +44,8 @@ EXPORTED_SYMBOLS = (
     "atk_group_norm_bwd", "atk_conv_workspace_bytes",
     "atk_conv_fwd", "atk_conv_wgrad_workspace_bytes", "atk_conv_wgrad", "atk_transpose_last2",
     "atk_dwconv1d_bwd", "atk_group_norm_noalloc_scratch_bytes", "atk_group_norm_fwd_noalloc",
+    "atk_conv_packed_weight_bytes", "atk_conv_prepacked_workspace_bytes", "atk_conv_pack_weights",
+    "atk_conv_fwd_prepacked",
 )
 
 
@@ -106,6 +109,14 @@ def _declare(lib) -> None:
     lib.atk_conv_workspace_bytes.restype = sz
     lib.atk_conv_fwd.argtypes = [vp, vp, vp, vp] + conv_geom + [i32, i32, vp, sz, vp]
     lib.atk_conv_fwd.restype = i32
+    lib.atk_conv_packed_weight_bytes.argtypes = conv_geom + [i32, i32]
+    lib.atk_conv_packed_weight_bytes.restype = sz
+    lib.atk_conv_prepacked_workspace_bytes.argtypes = conv_geom + [i32, i32]
+    lib.atk_conv_prepacked_workspace_bytes.restype = sz
+    lib.atk_conv_pack_weights.argtypes = [vp, vp, sz] + conv_geom + [i32, i32, vp]
+    lib.atk_conv_pack_weights.restype = i32
+    lib.atk_conv_fwd_prepacked.argtypes = [vp, vp, sz, vp, vp] + conv_geom + [i32, i32, vp, sz, vp]
+    lib.atk_conv_fwd_prepacked.restype = i32
     lib.atk_conv_wgrad_workspace_bytes.argtypes = [i64, i64, i64, i64, i64, i64, i32]
     lib.atk_conv_wgrad_workspace_bytes.restype = sz
     lib.atk_conv_wgrad.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, i64, i32, i32, vp, sz, vp]
@@ -827,6 +838,55 @@ def conv_out_size(inp: int, k: int, s: int, p: int, d: int) -> int:
     return (inp + 2 * p - d * (k - 1) - 1) // s + 1
 
 
+# ---------------------------------------------------------------------------
+# Packed conv weights, kept across calls.  The MFMA tiles read the weights in a fragment order
+# made by a packing kernel; for weights that do not change between calls (inference, or the
+# several convs of one training step) packing once is enough.  An entry is valid for one
+# weight tensor object at one version of its contents (torch bumps `_version` on every
+# in-place write through the tensor or a view of it), one geometry, variant and stream.  An
+# entry dies with its weight tensor.  Writes through `.data` bypass the version counter:
+# callers that modify weights that way call clear_packed_weight_cache() afterwards, or set
+# AMD_TUNED_TORCH_CONV_WEIGHT_CACHE=0.
+# ---------------------------------------------------------------------------
+_PACK_CACHE_ON = os.environ.get("AMD_TUNED_TORCH_CONV_WEIGHT_CACHE", "1") != "0"
+_PACK_CACHE_MAX = 64
+_pack_lock = threading.Lock()
+_packed: "dict[tuple, tuple]" = {}  # key -> (weakref to weight, packed uint8 tensor)
+
+
+def clear_packed_weight_cache() -> None:
+    """Drop every cached packed conv weight."""
+    with _pack_lock:
+        _packed.clear()
+
+
+def packed_weight_cache_size() -> int:
+    with _pack_lock:
+        return len(_packed)
+
+
+def _packed_conv_weights(weight: torch.Tensor, geom: tuple, dt: int, variant: int, nbytes: int,
+                         stream: int) -> torch.Tensor:
+    """The packed form of `weight` for (geometry, variant) on `stream`: cached, or packed now."""
+    key = (id(weight), weight.data_ptr(), weight._version, geom, dt, variant, stream)
+    with _pack_lock:
+        hit = _packed.get(key)
+        if hit is not None and hit[0]() is weight:
+            return hit[1]
+    packed = torch.empty(nbytes, dtype=torch.uint8, device=weight.device)
+    rc = lib().atk_conv_pack_weights(_ptr(weight), _ptr(packed), nbytes, *geom, dt, variant, stream)
+    _check(rc, "conv weight packing")
+    if _PACK_CACHE_ON:
+        def forget(_ref, key=key):
+            with _pack_lock:
+                _packed.pop(key, None)
+        with _pack_lock:
+            while len(_packed) >= _PACK_CACHE_MAX:
+                _packed.pop(next(iter(_packed)))  # oldest first
+            _packed[key] = (weakref.ref(weight, forget), packed)
+    return packed
+
+
 def _conv(input, weight, bias, stride, padding, dilation, nd: int, variant: int,
           out: Optional[torch.Tensor] = None) -> torch.Tensor:
     _require_cuda(input, weight, bias)
@@ -865,6 +925,18 @@ def _conv(input, weight, bias, stride, padding, dilation, nd: int, variant: int,
     L = lib()
     dt = _DTYPE_CODE[input.dtype]
     geom = (N, Ci, D, H, W, Co, KD, KH, KW, *s, *p, *d)
+    packed_bytes = L.atk_conv_packed_weight_bytes(*geom, dt, int(variant)) if variant > 0 else 0
+    if packed_bytes:
+        # an MFMA variant that takes the shape: packed weights from the cache, the workspace
+        # only for split-K partials
+        stream = _stream(input)
+        packed = _packed_conv_weights(weight, geom, dt, int(variant), packed_bytes, stream)
+        nws = L.atk_conv_prepacked_workspace_bytes(*geom, dt, int(variant))
+        ws = workspace(input.device, "conv", nws) if nws else None
+        rc = L.atk_conv_fwd_prepacked(_ptr(input), _ptr(packed), packed_bytes, _ptr(bias), _ptr(y), *geom, dt,
+                                      int(variant), _ptr(ws), ws.numel() if ws is not None else 0, stream)
+        _check(rc, f"conv{nd}d")
+        return y
     nbytes = L.atk_conv_workspace_bytes(*geom, dt, int(variant))
     ws_ptr, ws_len = None, 0
     if nbytes:

@@ -150,3 +150,50 @@ extern "C" int atk_conv_fwd(const void* x, const void* w, const void* bias, void
     default: return launch_direct<__bf16>(p, x, w, bias, y, s);
   }
 }
+
+// ---- packed-weight entry points (MFMA variants only) ------------------------------------
+#define ATK_CONV_GEOM_ARGS                                                                          \
+  int64_t N, int64_t Ci, int64_t D, int64_t H, int64_t W, int64_t Co, int KD, int KH, int KW, int sd, \
+      int sh, int sw, int pd, int ph, int pw, int dd, int dh, int dw, int dtype
+#define ATK_CONV_GEOM N, Ci, D, H, W, Co, KD, KH, KW, sd, sh, sw, pd, ph, pw, dd, dh, dw, dtype
+
+extern "C" size_t atk_conv_packed_weight_bytes(ATK_CONV_GEOM_ARGS, int variant) {
+  using namespace atk;
+  ConvShape p;
+  if (conv_shape(ATK_CONV_GEOM, p) || variant <= 0 || variant >= conv_num_variants()) return 0;
+  return conv_igemm_packed_bytes(p, variant - 1);
+}
+
+extern "C" size_t atk_conv_prepacked_workspace_bytes(ATK_CONV_GEOM_ARGS, int variant) {
+  using namespace atk;
+  ConvShape p;
+  if (conv_shape(ATK_CONV_GEOM, p) || variant <= 0 || variant >= conv_num_variants()) return 0;
+  return conv_igemm_prepacked_workspace_bytes(p, variant - 1);
+}
+
+extern "C" int atk_conv_pack_weights(const void* w, void* packed, size_t packed_bytes, ATK_CONV_GEOM_ARGS,
+                                     int variant, atk_stream_t stream) {
+  using namespace atk;
+  ConvShape p;
+  int rc = conv_shape(ATK_CONV_GEOM, p);
+  if (rc) return rc;
+  if (variant <= 0 || variant >= conv_num_variants())
+    return fail(variant == 0 ? ATK_UNSUPPORTED : ATK_EINVAL, "conv: variant %d has no packed weights", variant);
+  if (!w) return fail(ATK_EINVAL, "conv: null weight pointer");
+  return conv_igemm_pack(p, w, packed, packed_bytes, variant - 1, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int atk_conv_fwd_prepacked(const void* x, const void* packed, size_t packed_bytes, const void* bias,
+                                      void* y, ATK_CONV_GEOM_ARGS, int variant, void* workspace,
+                                      size_t workspace_bytes, atk_stream_t stream) {
+  using namespace atk;
+  ConvShape p;
+  int rc = conv_shape(ATK_CONV_GEOM, p);
+  if (rc) return rc;
+  if (variant <= 0 || variant >= conv_num_variants())
+    return fail(variant == 0 ? ATK_UNSUPPORTED : ATK_EINVAL, "conv: variant %d has no packed weights", variant);
+  if (N == 0) return ATK_OK;
+  if (!x || !y) return fail(ATK_EINVAL, "conv: null pointer");
+  return conv_igemm_run_prepacked(p, x, packed, packed_bytes, bias, y, variant - 1, workspace, workspace_bytes,
+                                  reinterpret_cast<hipStream_t>(stream));
+}

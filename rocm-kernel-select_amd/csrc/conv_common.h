@@ -19,5 +19,11 @@ const char* conv_igemm_variant_name(int v);
 size_t conv_igemm_workspace_bytes(const ConvShape& p, int v);
 int conv_igemm_launch(const ConvShape& p, const void* x, const void* w, const void* bias, void* y,
                       int v, void* ws, size_t ws_bytes, hipStream_t s);
+// The same in two steps: pack the weights once, then run on the packed weights.
+size_t conv_igemm_packed_bytes(const ConvShape& p, int v);
+size_t conv_igemm_prepacked_workspace_bytes(const ConvShape& p, int v);
+int conv_igemm_pack(const ConvShape& p, const void* w, void* packed, size_t packed_bytes, int v, hipStream_t s);
+int conv_igemm_run_prepacked(const ConvShape& p, const void* x, const void* packed, size_t packed_bytes,
+                             const void* bias, void* y, int v, void* ws, size_t ws_bytes, hipStream_t s);
 
 }  // namespace atk

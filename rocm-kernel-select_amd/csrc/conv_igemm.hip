@@ -594,25 +594,31 @@ struct IgVariant {
   int dtype_class;  // 0 = 16-bit, 1 = fp32
   int wco, wsp, fco, fsp, cb;
   int xc;           // patch-loader capacity multiplier (PatchLoader XC)
+  int max_splits;   // split-K limit (1: never split, so a call is one launch)
 };
 
 const IgVariant kIg[] = {
-    {"h_w22_f22_cb32", 0, 2, 2, 2, 2, 32, 1},
-    {"h_w22_f24_cb32", 0, 2, 2, 2, 4, 32, 1},
-    {"h_w14_f22_cb32", 0, 1, 4, 2, 2, 32, 1},
-    {"h_w22_f22_cb16", 0, 2, 2, 2, 2, 16, 1},
-    {"h_w41_f22_cb32", 0, 4, 1, 2, 2, 32, 1},
-    {"h_w21_f24_cb32", 0, 2, 1, 2, 4, 32, 1},
-    {"h_w22_f12_cb32", 0, 2, 2, 1, 2, 32, 1},
-    {"h_w21_f14_cb32", 0, 2, 1, 1, 4, 32, 1},
-    {"h_w22_f24_cb16", 0, 2, 2, 2, 4, 16, 1},
-    {"f32_w22_f22_cb16", 1, 2, 2, 2, 2, 16, 1},
-    {"f32_w14_f22_cb16", 1, 1, 4, 2, 2, 16, 1},
-    {"f32_w22_f12_cb16", 1, 2, 2, 1, 2, 16, 1},
-    {"f32_w21_f14_cb16", 1, 2, 1, 1, 4, 16, 1},
+    {"h_w22_f22_cb32", 0, 2, 2, 2, 2, 32, 1, 16},
+    {"h_w22_f24_cb32", 0, 2, 2, 2, 4, 32, 1, 16},
+    {"h_w14_f22_cb32", 0, 1, 4, 2, 2, 32, 1, 16},
+    {"h_w22_f22_cb16", 0, 2, 2, 2, 2, 16, 1, 16},
+    {"h_w41_f22_cb32", 0, 4, 1, 2, 2, 32, 1, 16},
+    {"h_w21_f24_cb32", 0, 2, 1, 2, 4, 32, 1, 16},
+    {"h_w22_f12_cb32", 0, 2, 2, 1, 2, 32, 1, 16},
+    {"h_w21_f14_cb32", 0, 2, 1, 1, 4, 32, 1, 16},
+    {"h_w22_f24_cb16", 0, 2, 2, 2, 4, 16, 1, 16},
+    {"f32_w22_f22_cb16", 1, 2, 2, 2, 2, 16, 1, 16},
+    {"f32_w14_f22_cb16", 1, 1, 4, 2, 2, 16, 1, 16},
+    {"f32_w22_f12_cb16", 1, 2, 2, 1, 2, 16, 1, 16},
+    {"f32_w21_f14_cb16", 1, 2, 1, 1, 4, 16, 1, 16},
     // 64 output channels with a 7x7 plane: the 32x32-position tile's 14-row patch needs twice
     // the default loader capacity
-    {"h_w14_f22_cb16x2", 0, 1, 4, 2, 2, 16, 2},
+    {"h_w14_f22_cb16x2", 0, 1, 4, 2, 2, 16, 2, 16},
+    // small tiles that never split K: for shapes too small to fill the chip (config 4's
+    // 64-channel conv), one launch with no partial sums to write and add up
+    {"h_w12_f21_cb32_ns", 0, 1, 2, 2, 1, 32, 1, 1},
+    {"h_w22_f11_cb32_ns", 0, 2, 2, 1, 1, 32, 1, 1},
+    {"h_w21_f12_cb32_ns", 0, 2, 1, 1, 2, 32, 1, 1},
 };
 constexpr int kNumIg = sizeof(kIg) / sizeof(kIg[0]);
 
@@ -682,7 +688,7 @@ int plan_ig(const ConvShape& p, int v, IgPlan& pl) {
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
   const int64_t wgs = pl.tiles * co_tiles;
   int splits = 1;
-  while (wgs * splits < 2 * cus && splits * 2 <= a.n_stages && splits < 16) splits *= 2;
+  while (wgs * splits < 2 * cus && splits * 2 <= a.n_stages && splits * 2 <= vr.max_splits) splits *= 2;
   a.stages_per_split = (a.n_stages + splits - 1) / splits;
   splits = (a.n_stages + a.stages_per_split - 1) / a.stages_per_split;
   pl.splits = splits;
@@ -732,28 +738,30 @@ int launch_ig_t(const IgPlan& pl, hipStream_t s) {
   }
 }
 
+// Pack w[Co][Ci][taps] into the fragment order variant v reads (plan_ig's layout) at wp.
 template <typename T>
-int launch_ig(const ConvShape& p, const void* x, const void* w, const void* bias, void* y, int v,
-              void* ws, size_t ws_bytes, hipStream_t s) {
-  IgPlan pl;
-  int rc = plan_ig(p, v, pl);
-  if (rc) return rc;
-  const size_t need = align256(pl.wp_bytes) + pl.part_bytes;
-  if (!ws || ws_bytes < need) return fail(ATK_EINVAL, "conv: workspace of %zu bytes needed", need);
+int pack_ig(const ConvShape& p, const IgPlan& pl, const void* w, void* wp, hipStream_t s) {
+  const int taps = p.KD * p.KH * p.KW;
+  const uint32_t chunks = (uint32_t)(pl.wp_bytes / 16);  // wp_bytes: a multiple of 32 rows x KB elements
+  hipLaunchKernelGGL((pack_weights_kernel<T>), dim3((chunks + 255) / 256), dim3(256), 0, s,
+                     static_cast<const T*>(w), static_cast<T*>(wp), p.Co, p.Ci, taps, pl.a.n_kb, pl.a.co_blocks,
+                     chunks);
+  return check_launch("pack_weights_kernel");
+}
+
+// The implicit GEMM on weights already packed at wp; `part` holds the split-K partials (or is
+// null when the plan does not split).
+template <typename T>
+int run_ig(const ConvShape& p, IgPlan& pl, const void* x, const void* wp, const void* bias, void* y, int v,
+           float* part, hipStream_t s) {
+  int rc = ATK_OK;
   IgArgs& a = pl.a;
   a.x = x; a.bias = bias; a.y = y;
   a.vec_rows = (p.W % (16 / (int)sizeof(T)) == 0) && aligned16(x);
   a.x_sample_bytes = (uint32_t)((int64_t)p.Ci * p.D * p.H * p.W * sizeof(T));
   a.wp_bytes = (uint32_t)pl.wp_bytes;
-  a.wp = ws;
-  a.part = pl.splits > 1 ? reinterpret_cast<float*>(static_cast<char*>(ws) + align256(pl.wp_bytes)) : nullptr;
-  // pack the weights
-  const int taps = p.KD * p.KH * p.KW;
-  const uint32_t chunks = (uint32_t)(pl.wp_bytes / 16);  // wp_bytes: a multiple of 32 rows x KB elements
-  hipLaunchKernelGGL((pack_weights_kernel<T>), dim3((chunks + 255) / 256), dim3(256), 0, s,
-                     static_cast<const T*>(w), static_cast<T*>(ws), p.Co, p.Ci, taps, a.n_kb, a.co_blocks, chunks);
-  rc = check_launch("pack_weights_kernel");
-  if (rc) return rc;
+  a.wp = wp;
+  a.part = pl.splits > 1 ? part : nullptr;
   // instantiate only the variants of this element type's class
   if constexpr (sizeof(T) == 2) {
     switch (v) {
@@ -767,6 +775,9 @@ int launch_ig(const ConvShape& p, const void* x, const void* w, const void* bias
       case 7: rc = launch_ig_t<T, 2, 1, 1, 4, 32>(pl, s); break;
       case 8: rc = launch_ig_t<T, 2, 2, 2, 4, 16>(pl, s); break;
       case 13: rc = launch_ig_t<T, 1, 4, 2, 2, 16, 2>(pl, s); break;
+      case 14: rc = launch_ig_t<T, 1, 2, 2, 1, 32>(pl, s); break;
+      case 15: rc = launch_ig_t<T, 2, 2, 1, 1, 32>(pl, s); break;
+      case 16: rc = launch_ig_t<T, 2, 1, 1, 2, 32>(pl, s); break;
       default: return fail(ATK_EINVAL, "conv: bad variant");
     }
   } else {
@@ -786,6 +797,21 @@ int launch_ig(const ConvShape& p, const void* x, const void* w, const void* bias
   return check_launch("splitk_finalize_kernel");
 }
 
+// Pack, then run: the packed weights at the front of the workspace, the partials after them.
+template <typename T>
+int launch_ig(const ConvShape& p, const void* x, const void* w, const void* bias, void* y, int v,
+              void* ws, size_t ws_bytes, hipStream_t s) {
+  IgPlan pl;
+  int rc = plan_ig(p, v, pl);
+  if (rc) return rc;
+  const size_t need = align256(pl.wp_bytes) + pl.part_bytes;
+  if (!ws || ws_bytes < need) return fail(ATK_EINVAL, "conv: workspace of %zu bytes needed", need);
+  rc = pack_ig<T>(p, pl, w, ws, s);
+  if (rc) return rc;
+  return run_ig<T>(p, pl, x, ws, bias, y, v,
+                   reinterpret_cast<float*>(static_cast<char*>(ws) + align256(pl.wp_bytes)), s);
+}
+
 }  // namespace
 
 int conv_igemm_num_variants() { return kNumIg; }
@@ -796,6 +822,54 @@ size_t conv_igemm_workspace_bytes(const ConvShape& p, int v) {
   IgPlan pl;
   if (plan_ig(p, v, pl)) return 0;
   return align256(pl.wp_bytes) + pl.part_bytes;
+}
+
+size_t conv_igemm_packed_bytes(const ConvShape& p, int v) {
+  if (v < 0 || v >= kNumIg) return 0;
+  IgPlan pl;
+  if (plan_ig(p, v, pl)) return 0;
+  return align256(pl.wp_bytes);
+}
+
+size_t conv_igemm_prepacked_workspace_bytes(const ConvShape& p, int v) {
+  if (v < 0 || v >= kNumIg) return 0;
+  IgPlan pl;
+  if (plan_ig(p, v, pl)) return 0;
+  return pl.part_bytes;
+}
+
+int conv_igemm_pack(const ConvShape& p, const void* w, void* packed, size_t packed_bytes, int v, hipStream_t s) {
+  if (v < 0 || v >= kNumIg) return fail(ATK_EINVAL, "conv: variant out of range");
+  IgPlan pl;
+  int rc = plan_ig(p, v, pl);
+  if (rc) return rc;
+  if (!packed || packed_bytes < align256(pl.wp_bytes))
+    return fail(ATK_EINVAL, "conv: packed weights need %zu bytes", align256(pl.wp_bytes));
+  switch (p.dtype) {
+    case ATK_F32: return pack_ig<float>(p, pl, w, packed, s);
+    case ATK_F16: return pack_ig<_Float16>(p, pl, w, packed, s);
+    default: return pack_ig<__bf16>(p, pl, w, packed, s);
+  }
+}
+
+int conv_igemm_run_prepacked(const ConvShape& p, const void* x, const void* packed, size_t packed_bytes,
+                             const void* bias, void* y, int v, void* ws, size_t ws_bytes, hipStream_t s) {
+  if (v < 0 || v >= kNumIg) return fail(ATK_EINVAL, "conv: variant out of range");
+  const int64_t ysz = (int64_t)p.N * p.Co * p.Do * p.Ho * p.Wo;
+  if (ysz >= (1ll << 31)) return fail(ATK_UNSUPPORTED, "conv: output too large for the split-K finalize");
+  IgPlan pl;
+  int rc = plan_ig(p, v, pl);
+  if (rc) return rc;
+  if (!packed || packed_bytes < align256(pl.wp_bytes))
+    return fail(ATK_EINVAL, "conv: packed weights of %zu bytes expected", align256(pl.wp_bytes));
+  if (pl.part_bytes && (!ws || ws_bytes < pl.part_bytes))
+    return fail(ATK_EINVAL, "conv: workspace of %zu bytes needed", pl.part_bytes);
+  float* part = static_cast<float*>(ws);
+  switch (p.dtype) {
+    case ATK_F32: return run_ig<float>(p, pl, x, packed, bias, y, v, part, s);
+    case ATK_F16: return run_ig<_Float16>(p, pl, x, packed, bias, y, v, part, s);
+    default: return run_ig<__bf16>(p, pl, x, packed, bias, y, v, part, s);
+  }
 }
 
 int conv_igemm_launch(const ConvShape& p, const void* x, const void* w, const void* bias, void* y, int v,

@@ -397,3 +397,74 @@ def test_conv_autograd_native_wgrad(nd, channels_last):
     assert O.max_rel_err(wg.grad.float(), wr.grad) <= 1e-2
     assert O.max_rel_err(bg.grad.float(), br.grad) <= 1e-2
     assert O.max_rel_err(xg.grad.float(), xr.grad) <= 1e-2
+
+
+# ---------------------------------------------------------------------------
+# packed weights kept across calls (atk_conv_pack_weights / atk_conv_fwd_prepacked)
+# ---------------------------------------------------------------------------
+def _raw_conv3d(nat, x, w, b, s, p, d, vi):
+    """atk_conv_fwd (packing inside the call) with no cache in between."""
+    import ctypes
+    L = nat.lib()
+    dt = nat._DTYPE_CODE[x.dtype]
+    N, Ci, D, H, W = x.shape
+    Co, _, KD, KH, KW = w.shape
+    geom = (N, Ci, D, H, W, Co, KD, KH, KW, *([s] * 3), *([p] * 3), *([d] * 3))
+    y = torch.empty(N, Co, *[(e + 2 * p - d * (k - 1) - 1) // s + 1 for e, k in zip((D, H, W), (KD, KH, KW))],
+                    dtype=x.dtype, device=x.device)
+    nbytes = L.atk_conv_workspace_bytes(*geom, dt, vi)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=x.device)
+    rc = L.atk_conv_fwd(x.data_ptr(), w.data_ptr(), None if b is None else b.data_ptr(), y.data_ptr(), *geom, dt,
+                        vi, ws.data_ptr(), ctypes.c_size_t(ws.numel()), torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, nat.last_error()
+    return y
+
+
+@pytest.mark.parametrize("xs,ws", [((1, 32, 8, 16, 16), (64, 32, 3, 3, 3)),      # split-K tiles
+                                   ((1, 64, 16, 32, 32), (64, 64, 3, 3, 3)),      # config 4, small
+                                   ((2, 5, 5, 6, 7), (3, 5, 3, 3, 3))])           # off the tiles
+def test_prepacked_conv_equals_single_call(dev, xs, ws):
+    """For every 16-bit MFMA variant that takes the shape, the cached-packed-weight path gives
+    exactly the bytes of the pack-in-the-call path."""
+    nat = _native()
+    x, w, b = _inputs(xs, ws, torch.bfloat16, seed=3)
+    xd, wd, bd = x.to(dev), w.to(dev), b.to(dev)
+    ran = 0
+    for vi, name in _variants_for(torch.bfloat16):
+        if name == "direct":
+            continue
+        try:
+            want = _raw_conv3d(nat, xd, wd, bd, 1, 1, 1, vi)
+        except AssertionError:
+            continue  # the variant declines the shape
+        got = nat.conv3d(xd, wd, bd, 1, 1, 1, variant=vi)
+        again = nat.conv3d(xd, wd, bd, 1, 1, 1, variant=vi)  # from the cache
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), name
+        assert torch.equal(again.view(torch.int16), want.view(torch.int16)), name
+        ran += 1
+    assert ran >= 3
+
+
+def test_packed_weight_cache_follows_the_weight(dev):
+    """A cached entry serves the same weight object while its contents are unchanged; an
+    in-place update (version bump) is packed again; the entry dies with the weight."""
+    import gc
+    nat = _native()
+    nat.clear_packed_weight_cache()
+    x, w, b = _inputs((1, 32, 8, 16, 16), (64, 32, 3, 3, 3), torch.float16, seed=4)
+    xd, wd = x.to(dev), w.to(dev)
+    vi = [i for i, n in _variants_for(torch.float16) if n == "h_w22_f22_cb32"][0]
+    y1 = nat.conv3d(xd, wd, None, 1, 1, 1, variant=vi)
+    assert nat.packed_weight_cache_size() == 1
+    nat.conv3d(xd, wd, None, 1, 1, 1, variant=vi)
+    assert nat.packed_weight_cache_size() == 1                 # hit, nothing new
+    wd.mul_(2.0)                                               # in place: new version
+    y2 = nat.conv3d(xd, wd, None, 1, 1, 1, variant=vi)
+    torch.cuda.synchronize()
+    assert torch.equal(y2.cpu(), (2.0 * y1.float()).to(torch.float16).cpu()) or \
+        O.max_rel_err(y2.cpu(), O.conv3d(x, 2.0 * w.float(), None, 1, 1, 1)) <= 1e-2
+    assert O.max_rel_err(y2.cpu(), O.conv3d(x, (2.0 * w.float()).to(torch.float16), None, 1, 1, 1)) <= 1e-2
+    del wd
+    gc.collect()
+    assert nat.packed_weight_cache_size() == 0                 # entries die with the weight
