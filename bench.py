@@ -438,13 +438,43 @@ def bench_vae_block_detail(dev):
         y = model(x)
         ref = stock(x.float(), True)
         ms = graph_time_ms(lambda: model(x), 10)
+        conv_ms = graph_time_ms(lambda: F.conv3d(x, m.conv.weight, m.conv.bias, 1, 1), 10)
         stock_ms = event_time_ms(stock, 3)
     err = max_rel_err(y, ref)
+    won = [v for k, v in amd_tuned_torch.kernel_select.debug_winners().items() if k[0] == "conv_group_norm"]
     flops = 2.0 * C * 8 * 64 * 64 * C * 27
     tf = flops / (ms * 1e-3) / 1e12
-    return {"ms": round(ms, 4), "conv_TFLOP/s_over_block": round(tf, 1),
+    return {"ms": round(ms, 4), "conv_alone_ms": round(conv_ms, 4),
+            "block_minus_conv_us": round((ms - conv_ms) * 1e3, 2), "conv_TFLOP/s_over_block": round(tf, 1),
             "roofline_frac": round(tf / MFMA_PEAK_TFLOPS["bf16"], 4), "stock_block_ms": round(stock_ms, 3),
-            "variant": type(m).__name__, "max_rel_err_vs_stock_fp32": float(f"{err:.3g}")}
+            "variant": type(m).__name__ + " (" + (won[0] if won else "?") + ": conv epilogue statistics + "
+                       "GroupNorm+SiLU apply)",
+            "max_rel_err_vs_stock_fp32": float(f"{err:.3g}")}
+
+
+def bench_conv_residual_detail(dev):
+    """Config 5's conv (C5a, bf16) with a residual added in the MFMA epilogue
+    (conv_fusion_ops.conv_residual), against the conv alone and stock conv + add."""
+    import torch
+    import torch.nn.functional as F
+    import amd_tuned_torch
+    from amd_tuned_torch import conv_fusion_ops
+    g = _gen(1013)
+    C = 256
+    x = torch.randn(1, C, 8, 64, 64, generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn(C, C, 3, 3, 3, generator=g) * math.sqrt(2.0 / (C * 27))).to(torch.bfloat16).to(dev)
+    b = (0.1 * torch.randn(C, generator=g)).to(torch.bfloat16).to(dev)
+    r = torch.randn(1, C, 8, 64, 64, generator=g).to(torch.bfloat16).to(dev)
+    conv3d = amd_tuned_torch._ORIGINALS[(F, "conv3d")]
+    with torch.no_grad():
+        y = conv_fusion_ops.conv_residual(x, w, b, r, 1, 1, 1)
+        ref = conv3d(x.float(), w.float(), b.float(), 1, 1) + r.float()
+        ms = graph_time_ms(lambda: conv_fusion_ops.conv_residual(x, w, b, r, 1, 1, 1), 10)
+        conv_ms = graph_time_ms(lambda: F.conv3d(x, w, b, 1, 1), 10)
+        unfused_ms = graph_time_ms(lambda: F.conv3d(x, w, b, 1, 1) + r, 10)
+    won = [v for k, v in amd_tuned_torch.kernel_select.debug_winners().items() if k[0] == "conv_residual"]
+    return {"ms": round(ms, 4), "conv_alone_ms": round(conv_ms, 4), "conv_then_add_ms": round(unfused_ms, 4),
+            "variant": won[0] if won else "?", "max_rel_err_vs_stock_fp32": float(f"{max_rel_err(y, ref):.3g}")}
 
 
 def bench_causal_silu_backward_detail(dev):
@@ -1226,6 +1256,7 @@ def main():
             ("c5_conv3d_bf16", lambda: bench_conv_detail((1, 256, 8, 64, 64), (256, 256, 3, 3, 3), 1, torch.bfloat16, dev, 10)),
             ("c5_conv3d_k7_fp16", lambda: bench_conv_detail((1, 64, 16, 32, 32), (64, 64, 7, 7, 7), 3, torch.float16, dev, 10)),
             ("c5_vae_block_bf16", lambda: bench_vae_block_detail(dev)),
+            ("c5_conv3d_residual_bf16", lambda: bench_conv_residual_detail(dev)),
             ("c5_conv3d_wgrad_bf16", lambda: bench_conv_wgrad_detail((1, 256, 8, 64, 64), 256, dev)),
             ("c4_conv3d_scaled_wgrad_bf16", lambda: bench_conv_wgrad_detail((2, 128, 16, 64, 64), 128, dev)),
             ("c5_conv3d_ndhwc_bf16", lambda: bench_conv_cl_detail(dev)),

@@ -356,6 +356,38 @@ int atk_conv_fwd_prepacked(const void* x, const void* packed, size_t packed_byte
                            atk_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Conv epilogue fusion (the reference fuses GroupNorm+SiLU before a conv and names
+ * "Conv -> +residual" as the epilogue to fuse, amd_tuned_torch/conv_fusion_ops.py:1-40,
+ * 355-439): atk_conv_fwd_prepacked with, on an unsplit launch,
+ *   residual   y = conv + bias + residual (residual: y's shape and layout, dtype), or NULL;
+ *   gn_stats   GroupNorm statistics of the stored y for `gn_groups` groups: records
+ *              (count, mean, M2, 0) as 4 floats, atk_conv_gn_records(...) per (n, g),
+ *              laid out [N * gn_groups][records]; atk_conv_gn_stats_bytes(...) bytes (0
+ *              when the variant splits this shape or Co/groups is not 4, 8, 16, 32 or a
+ *              multiple of 32 -- then the call returns ATK_UNSUPPORTED), or NULL.
+ * atk_group_norm_apply then normalises y with those records (no statistics pass over y):
+ *   y_out = act((x - mean) * rsqrt(var + eps) * gamma + beta), x and y_out may be the same
+ *   buffer; `variant` is a split GroupNorm variant (-1: split_nt256_v8).
+ * ------------------------------------------------------------------------- */
+size_t atk_conv_gn_stats_bytes(int64_t N, int64_t Ci, int64_t D, int64_t H, int64_t W, int64_t Co,
+                               int KD, int KH, int KW, int sd, int sh, int sw, int pd, int ph, int pw,
+                               int dd, int dh, int dw, int dtype, int variant, int gn_groups);
+int atk_conv_gn_records(int64_t N, int64_t Ci, int64_t D, int64_t H, int64_t W, int64_t Co, int KD,
+                        int KH, int KW, int sd, int sh, int sw, int pd, int ph, int pw, int dd, int dh,
+                        int dw, int dtype, int variant, int gn_groups);
+int atk_conv_fwd_prepacked_ex(const void* x, const void* packed, size_t packed_bytes,
+                              const void* bias, const void* residual, void* y, int64_t N,
+                              int64_t Ci, int64_t D, int64_t H, int64_t W, int64_t Co, int KD,
+                              int KH, int KW, int sd, int sh, int sw, int pd, int ph, int pw,
+                              int dd, int dh, int dw, int dtype, int variant, int gn_groups,
+                              void* gn_stats, size_t gn_stats_bytes, void* workspace,
+                              size_t workspace_bytes, atk_stream_t stream);
+int atk_group_norm_apply(const void* x, const void* gamma, const void* beta, void* y, int64_t N,
+                         int64_t C, int64_t S, int G, float eps, int fuse_silu, int dtype,
+                         int param_dtype, const void* stats, int64_t records_per_group,
+                         int variant, atk_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Conv weight gradient (replaces the dweight part of `aten.convolution_backward` that the
  * reference's _Conv3dFn.backward calls, amd_tuned_torch/_dispatch.py:2064-2075), for
  * stride-1, dilation-1 convs with kernel (KD, 3, 3), KD in {1, 3}, and "same" padding

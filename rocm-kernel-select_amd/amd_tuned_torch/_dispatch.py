@@ -814,8 +814,7 @@ def _patched_sequential_forward(self, input):
                 and isinstance(conv, (torch.nn.Conv2d, torch.nn.Conv3d))):
             if _DEBUG:
                 _debug("sequential", "conv_fusion", "conv then GroupNorm+SiLU fused", input=input)
-            return conv_fusion_ops.group_norm_silu(conv(input), norm.num_groups, norm.weight, norm.bias,
-                                                   norm.eps)
+            return conv_fusion_ops.FusedConvGroupNormSiLU.forward_parts(conv, norm, input)
     return _SEQ_FORWARD_ORIG(self, input)
 
 

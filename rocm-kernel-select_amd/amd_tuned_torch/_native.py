@@ -45,7 +45,8 @@ EXPORTED_SYMBOLS = (
     "atk_conv_fwd", "atk_conv_wgrad_workspace_bytes", "atk_conv_wgrad", "atk_transpose_last2",
     "atk_dwconv1d_bwd", "atk_group_norm_noalloc_scratch_bytes", "atk_group_norm_fwd_noalloc",
     "atk_conv_packed_weight_bytes", "atk_conv_prepacked_workspace_bytes", "atk_conv_pack_weights",
-    "atk_conv_fwd_prepacked",
+    "atk_conv_fwd_prepacked", "atk_conv_gn_stats_bytes", "atk_conv_gn_records", "atk_conv_fwd_prepacked_ex",
+    "atk_group_norm_apply",
 )
 
 
@@ -117,6 +118,16 @@ def _declare(lib) -> None:
     lib.atk_conv_pack_weights.restype = i32
     lib.atk_conv_fwd_prepacked.argtypes = [vp, vp, sz, vp, vp] + conv_geom + [i32, i32, vp, sz, vp]
     lib.atk_conv_fwd_prepacked.restype = i32
+    lib.atk_conv_gn_stats_bytes.argtypes = conv_geom + [i32, i32, i32]
+    lib.atk_conv_gn_stats_bytes.restype = sz
+    lib.atk_conv_gn_records.argtypes = conv_geom + [i32, i32, i32]
+    lib.atk_conv_gn_records.restype = i32
+    lib.atk_conv_fwd_prepacked_ex.argtypes = [vp, vp, sz, vp, vp, vp] + conv_geom + [i32, i32, i32, vp, sz, vp, sz,
+                                                                                     vp]
+    lib.atk_conv_fwd_prepacked_ex.restype = i32
+    lib.atk_group_norm_apply.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, c.c_float, i32, i32, i32, vp, i64,
+                                         i32, vp]
+    lib.atk_group_norm_apply.restype = i32
     lib.atk_conv_wgrad_workspace_bytes.argtypes = [i64, i64, i64, i64, i64, i64, i32]
     lib.atk_conv_wgrad_workspace_bytes.restype = sz
     lib.atk_conv_wgrad.argtypes = [vp, vp, vp, i64, i64, i64, i64, i64, i64, i32, i32, vp, sz, vp]
@@ -888,8 +899,11 @@ def _packed_conv_weights(weight: torch.Tensor, geom: tuple, dt: int, variant: in
 
 
 def _conv(input, weight, bias, stride, padding, dilation, nd: int, variant: int,
-          out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    _require_cuda(input, weight, bias)
+          out: Optional[torch.Tensor] = None, residual: Optional[torch.Tensor] = None, gn_groups: int = 0):
+    """y = conv(input, weight) + bias (+ residual).  With gn_groups > 0 the MFMA epilogue also
+    writes the GroupNorm records of y and (y, records, records_per_group) comes back.  The
+    epilogue extras need an MFMA variant that does not split this shape (else Unsupported)."""
+    _require_cuda(input, weight, bias, residual)
     if not (input.is_contiguous() and weight.is_contiguous()):
         raise RuntimeError("Input/weight must be contiguous")
     if input.dim() != nd + 2 or weight.dim() != nd + 2:
@@ -920,12 +934,18 @@ def _conv(input, weight, bias, stride, padding, dilation, nd: int, variant: int,
         raise RuntimeError("Conv output size must be positive")
     shape = (N, Co, *osz) if nd == 3 else (N, Co, osz[1], osz[2])
     y = out if out is not None else torch.empty(shape, dtype=input.dtype, device=input.device)
-    if y.numel() == 0:
+    extras = residual is not None or gn_groups > 0
+    if residual is not None and (tuple(residual.shape) != tuple(shape) or residual.dtype != input.dtype
+                                 or not residual.is_contiguous()):
+        raise RuntimeError("conv residual must be a contiguous tensor of the output's shape and dtype")
+    if y.numel() == 0 and not extras:
         return y
     L = lib()
     dt = _DTYPE_CODE[input.dtype]
     geom = (N, Ci, D, H, W, Co, KD, KH, KW, *s, *p, *d)
     packed_bytes = L.atk_conv_packed_weight_bytes(*geom, dt, int(variant)) if variant > 0 else 0
+    if extras and not packed_bytes:
+        raise Unsupported(f"conv{nd}d: the residual / GroupNorm epilogue needs an MFMA variant that takes the shape")
     if packed_bytes:
         # an MFMA variant that takes the shape: packed weights from the cache, the workspace
         # only for split-K partials
@@ -933,10 +953,24 @@ def _conv(input, weight, bias, stride, padding, dilation, nd: int, variant: int,
         packed = _packed_conv_weights(weight, geom, dt, int(variant), packed_bytes, stream)
         nws = L.atk_conv_prepacked_workspace_bytes(*geom, dt, int(variant))
         ws = workspace(input.device, "conv", nws) if nws else None
-        rc = L.atk_conv_fwd_prepacked(_ptr(input), _ptr(packed), packed_bytes, _ptr(bias), _ptr(y), *geom, dt,
-                                      int(variant), _ptr(ws), ws.numel() if ws is not None else 0, stream)
+        if not extras:
+            rc = L.atk_conv_fwd_prepacked(_ptr(input), _ptr(packed), packed_bytes, _ptr(bias), _ptr(y), *geom, dt,
+                                          int(variant), _ptr(ws), ws.numel() if ws is not None else 0, stream)
+            _check(rc, f"conv{nd}d")
+            return y
+        stats, nrec = None, 0
+        if gn_groups > 0:
+            nbytes = L.atk_conv_gn_stats_bytes(*geom, dt, int(variant), int(gn_groups))
+            nrec = L.atk_conv_gn_records(*geom, dt, int(variant), int(gn_groups))
+            if not nbytes or not nrec:
+                raise Unsupported(f"conv{nd}d: this variant cannot write GroupNorm statistics for the shape")
+            stats = torch.empty(nbytes // 4, dtype=torch.float32, device=input.device)
+        rc = L.atk_conv_fwd_prepacked_ex(_ptr(input), _ptr(packed), packed_bytes, _ptr(bias), _ptr(residual), _ptr(y),
+                                         *geom, dt, int(variant), int(gn_groups), _ptr(stats),
+                                         stats.numel() * 4 if stats is not None else 0, _ptr(ws),
+                                         ws.numel() if ws is not None else 0, stream)
         _check(rc, f"conv{nd}d")
-        return y
+        return (y, stats, nrec) if gn_groups > 0 else y
     nbytes = L.atk_conv_workspace_bytes(*geom, dt, int(variant))
     ws_ptr, ws_len = None, 0
     if nbytes:
@@ -949,17 +983,55 @@ def _conv(input, weight, bias, stride, padding, dilation, nd: int, variant: int,
 
 
 def conv2d(input, weight, bias=None, stride: Sequence[int] = (1, 1), padding=(0, 0),
-           dilation=(1, 1), *, variant: int = -1, out=None) -> torch.Tensor:
+           dilation=(1, 1), *, variant: int = -1, out=None, residual=None) -> torch.Tensor:
     """Reference signature `conv2d(input, weight, bias?, stride, padding, dilation)`
-    (src/main_rocm.cpp:669-715), groups = 1, NCHW."""
-    return _conv(input, weight, bias, stride, padding, dilation, 2, variant, out)
+    (src/main_rocm.cpp:669-715), groups = 1, NCHW; `residual` is added in the epilogue."""
+    return _conv(input, weight, bias, stride, padding, dilation, 2, variant, out, residual)
 
 
 def conv3d(input, weight, bias=None, stride: Sequence[int] = (1, 1, 1), padding=(0, 0, 0),
-           dilation=(1, 1, 1), *, variant: int = -1, out=None) -> torch.Tensor:
+           dilation=(1, 1, 1), *, variant: int = -1, out=None, residual=None) -> torch.Tensor:
     """Reference signature `conv3d(input, weight, bias?, stride, padding, dilation)`
-    (src/main_rocm.cpp:798-854), groups = 1, NCDHW."""
-    return _conv(input, weight, bias, stride, padding, dilation, 3, variant, out)
+    (src/main_rocm.cpp:798-854), groups = 1, NCDHW; `residual` is added in the epilogue."""
+    return _conv(input, weight, bias, stride, padding, dilation, 3, variant, out, residual)
+
+
+def conv_gn_stats(input, weight, bias, stride, padding, dilation, nd: int, groups: int, *, variant: int,
+                  residual=None, out=None):
+    """The conv (+ residual) of an unsplit MFMA variant with the GroupNorm records of its
+    output for `groups` groups written by the epilogue: (y, records, records_per_group)."""
+    return _conv(input, weight, bias, stride, padding, dilation, nd, variant, out, residual, gn_groups=groups)
+
+
+def group_norm_apply(x: torch.Tensor, num_groups: int, weight: Optional[torch.Tensor], bias: Optional[torch.Tensor],
+                     eps: float, records: torch.Tensor, records_per_group: int, *, silu: bool = False,
+                     out: Optional[torch.Tensor] = None, variant: int = -1) -> torch.Tensor:
+    """GroupNorm (+ SiLU) of x from precomputed statistics records (count, mean, M2, -) per
+    (n, g), e.g. the conv epilogue's: one read and one write of x.  `out` may be x itself."""
+    _require_cuda(x, weight, bias, records, out)
+    if not x.is_contiguous() or x.dim() < 2 or x.dtype not in _DTYPE_CODE:
+        raise RuntimeError("group_norm_apply: contiguous (N, C, ...) input of a float dtype")
+    N, C = x.shape[0], x.shape[1]
+    S = x.numel() // max(1, N * C)
+    G = int(num_groups)
+    if G <= 0 or C % G:
+        raise RuntimeError("group_norm_apply: channels must be divisible by groups")
+    if records.dtype != torch.float32 or records.numel() < N * G * records_per_group * 4:
+        raise RuntimeError("group_norm_apply: records must be float32 [N * G * records_per_group * 4]")
+    if weight is not None and bias is not None and weight.dtype != bias.dtype:
+        bias = bias.to(weight.dtype)
+    pdt = _DTYPE_CODE[(weight if weight is not None else bias).dtype] if (weight is not None or bias is not None) \
+        else ATK_F32
+    weight = weight.contiguous() if weight is not None else None
+    bias = bias.contiguous() if bias is not None else None
+    y = out if out is not None else torch.empty_like(x)
+    if x.numel() == 0:
+        return y
+    rc = lib().atk_group_norm_apply(_ptr(x), _ptr(weight), _ptr(bias), _ptr(y), N, C, S, G, float(eps),
+                                    int(bool(silu)), _DTYPE_CODE[x.dtype], pdt, _ptr(records), int(records_per_group),
+                                    int(variant), _stream(x))
+    _check(rc, "group_norm_apply")
+    return y
 
 
 def conv_wgrad(x: torch.Tensor, dy: torch.Tensor, kd: int) -> torch.Tensor:

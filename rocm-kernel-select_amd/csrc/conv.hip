@@ -197,3 +197,36 @@ extern "C" int atk_conv_fwd_prepacked(const void* x, const void* packed, size_t 
   return conv_igemm_run_prepacked(p, x, packed, packed_bytes, bias, y, variant - 1, workspace, workspace_bytes,
                                   reinterpret_cast<hipStream_t>(stream));
 }
+
+extern "C" size_t atk_conv_gn_stats_bytes(ATK_CONV_GEOM_ARGS, int variant, int groups) {
+  using namespace atk;
+  ConvShape p;
+  if (conv_shape(ATK_CONV_GEOM, p) || variant <= 0 || variant >= conv_num_variants()) return 0;
+  return conv_igemm_gn_stats_bytes(p, variant - 1, groups);
+}
+
+extern "C" int atk_conv_gn_records(ATK_CONV_GEOM_ARGS, int variant, int groups) {
+  using namespace atk;
+  ConvShape p;
+  if (conv_shape(ATK_CONV_GEOM, p) || variant <= 0 || variant >= conv_num_variants()) return 0;
+  return conv_igemm_gn_records(p, variant - 1, groups);
+}
+
+extern "C" int atk_conv_fwd_prepacked_ex(const void* x, const void* packed, size_t packed_bytes, const void* bias,
+                                         const void* residual, void* y, ATK_CONV_GEOM_ARGS, int variant,
+                                         int gn_groups, void* gn_stats, size_t gn_stats_bytes, void* workspace,
+                                         size_t workspace_bytes, atk_stream_t stream) {
+  using namespace atk;
+  ConvShape p;
+  int rc = conv_shape(ATK_CONV_GEOM, p);
+  if (rc) return rc;
+  if (variant <= 0 || variant >= conv_num_variants())
+    return fail(variant == 0 ? ATK_UNSUPPORTED : ATK_EINVAL, "conv: variant %d has no packed weights", variant);
+  if (gn_stats && (gn_groups <= 0 || Co % gn_groups))
+    return fail(ATK_EINVAL, "conv: %d GroupNorm groups do not divide %lld channels", gn_groups, (long long)Co);
+  if (N == 0) return ATK_OK;
+  if (!x || !y) return fail(ATK_EINVAL, "conv: null pointer");
+  return conv_igemm_run_prepacked(p, x, packed, packed_bytes, bias, y, variant - 1, workspace, workspace_bytes,
+                                  reinterpret_cast<hipStream_t>(stream), residual, gn_stats, gn_stats_bytes,
+                                  gn_stats ? gn_groups : 0);
+}

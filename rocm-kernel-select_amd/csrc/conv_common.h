@@ -23,7 +23,14 @@ int conv_igemm_launch(const ConvShape& p, const void* x, const void* w, const vo
 size_t conv_igemm_packed_bytes(const ConvShape& p, int v);
 size_t conv_igemm_prepacked_workspace_bytes(const ConvShape& p, int v);
 int conv_igemm_pack(const ConvShape& p, const void* w, void* packed, size_t packed_bytes, int v, hipStream_t s);
+// resid: y += resid (same layout), or null.  gn_stats: GroupNorm records of y for gn_G groups
+// (conv_igemm_gn_stats_bytes bytes, conv_igemm_gn_records per (n, g)), or null.  Both need an
+// unsplit launch.
 int conv_igemm_run_prepacked(const ConvShape& p, const void* x, const void* packed, size_t packed_bytes,
-                             const void* bias, void* y, int v, void* ws, size_t ws_bytes, hipStream_t s);
+                             const void* bias, void* y, int v, void* ws, size_t ws_bytes, hipStream_t s,
+                             const void* resid = nullptr, void* gn_stats = nullptr, size_t gn_stats_bytes = 0,
+                             int gn_G = 0);
+size_t conv_igemm_gn_stats_bytes(const ConvShape& p, int v, int G);
+int conv_igemm_gn_records(const ConvShape& p, int v, int G);
 
 }  // namespace atk

@@ -52,6 +52,12 @@ struct IgArgs {
   int stages_per_split;
   int n_kb;           // ci k-blocks in the packed weights = n_cc * CB / KB
   int co_blocks;      // 32-row co blocks in the packed weights (multiple of BN / 32)
+  // epilogue extras (unsplit launches only)
+  const void* resid;  // y += resid (same shape and layout as y), or null
+  float4* gn_parts;   // GroupNorm partial records [N * G][gn_np] (count, mean, M2, -), or null
+  int gn_cpg;         // channels per GroupNorm group: 4, 8, 16, 32 or a multiple of 32
+  int gn_G;           // groups (Co = gn_G * gn_cpg)
+  int gn_np;          // records per (n, g)
 };
 
 template <typename T> struct MfmaTraits;
@@ -244,13 +250,130 @@ __device__ __forceinline__ void stage_bias(const IgArgs& a, int co_tile, float* 
   }
 }
 
-// Epilogue: accumulator rows = output channels, columns = positions.  Writes y (bias added,
-// converted) or, under split-K, this split's fp32 partial sums.
-template <typename T, int FCO, int FSP, int BN>
-__device__ __forceinline__ void store_tile(const IgArgs& a, const f32x16 (&acc)[FCO][FSP], const float* s_bias,
+// GroupNorm statistics of the values a wave stores (an unsplit launch): one (count, mean, M2)
+// record per (wave tile, group) -- per 32-channel block and group for groups of up to 32
+// channels, per block for wider groups -- so the merge in the apply kernel is exact.  A lane
+// holds, for block i and position column j, the channels (r >> 2) * 8 + half * 4 + (r & 3),
+// r = 0..15: its 4 channels of octet q = r >> 2 always lie in one group (cpg >= 8) or are the
+// group (cpg == 4).  While the values are stored, each lane keeps per (block, octet) the sums
+// of d = v - K and d^2 about K = its first value of that octet (n <= 16 values, so the shifted
+// one-pass M2 = sum d^2 - (sum d)^2 / n is exact to rounding); nothing else stays live, so
+// the epilogue adds little register pressure to the kernel.  The lanes are then merged per
+// group: mean = sum n_l mean_l / n, M2 = sum (M2_l + n_l (mean_l - mean)^2).
+template <int FCO>
+struct GnLaneStats {
+  float K[FCO][4], s1[FCO][4], s2[FCO][4];
+};
+
+template <int FCO, int FSP, int BN>
+__device__ __forceinline__ void tile_gn_records(const IgArgs& a, const GnLaneStats<FCO>& st, float nl, int n,
+                                                int co_tile, int sp_rec, int wco, int half) {
+  const int cpg = a.gn_cpg;
+  const int lane = threadIdx.x & 63;
+  // values this wave stored: lanes 0-31 cover the columns once, nl of them each
+  const float npos = wave_sum(lane < 32 ? nl : 0.f);
+  const int per_blk = cpg >= 32 ? 1 : 32 / cpg;  // records (groups) per 32-channel block
+  const int oct = cpg >= 32 ? 4 : (cpg >= 8 ? cpg / 8 : 1);
+  const float cnt = npos * (float)(cpg >= 32 ? 32 : cpg);
+  const float nq = 4.f * nl;  // values per (lane, octet)
+  // sum over a group's lanes: 64 lanes, or one half (cpg == 4; xor offsets below 32 stay
+  // within a half)
+  auto group_sum = [&](float x) {
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) x += __shfl_xor(x, off, 64);
+    if (cpg != 4) x += __shfl_xor(x, 32, 64);
+    return x;
+  };
+#pragma unroll
+  for (int i = 0; i < FCO; ++i) {
+    const int cblk = co_tile * BN + (wco * FCO + i) * 32;  // first channel of the block
+    if (cblk >= a.gn_G * cpg) continue;
+    float mq[4], m2q[4];  // the lane's mean and M2 per octet
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float t = nq > 0.f ? st.s1[i][q] / nq : 0.f;
+      mq[q] = st.K[i][q] + t;
+      m2q[q] = fmaxf(fmaf(-st.s1[i][q], t, st.s2[i][q]), 0.f);
+    }
+    for (int k = 0; k < per_blk && k < 8; ++k) {  // group k of the block (cpg == 4: k = 2q + half)
+      const int q0 = cpg == 4 ? k >> 1 : k * oct;
+      const bool mine = cpg != 4 || (k & 1) == half;
+      float sm = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) sm += (mine && q >= q0 && q < q0 + oct) ? nq * mq[q] : 0.f;
+      const float mean = cnt > 0.f ? group_sum(sm) / cnt : 0.f;
+      float m2 = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float d = mq[q] - mean;
+        m2 += (mine && q >= q0 && q < q0 + oct) ? m2q[q] + nq * d * d : 0.f;
+      }
+      m2 = group_sum(m2);
+      const int g = (cblk + k * (cpg >= 32 ? 0 : cpg)) / cpg;
+      const bool writer = cpg == 4 ? lane == ((k & 1) ? 32 : 0) : lane == 0;
+      if (writer && g < a.gn_G) {
+        const int part = cpg > 32 ? (cblk % cpg) / 32 : 0;
+        const int rec = sp_rec * (cpg > 32 ? cpg / 32 : 1) + part;
+        // every record the layout reserves is written -- a wave whose tile lies past the
+        // output's edge writes a zero-count record, which the merge weighs by its count 0
+        a.gn_parts[((int64_t)n * a.gn_G + g) * a.gn_np + rec] = make_float4(cnt, mean, m2, 0.f);
+      }
+    }
+  }
+}
+
+// Epilogue: accumulator rows = output channels, columns = positions.  Writes y (bias and the
+// optional residual added, converted) or, under split-K, this split's fp32 partial sums; on an
+// unsplit launch with gn_parts set it also writes the GroupNorm records of the stored values.
+template <typename T, int FCO, int FSP, int BN, bool EPI>
+__device__ __forceinline__ void store_tile(const IgArgs& a, f32x16 (&acc)[FCO][FSP], const float* s_bias,
                                            int n, int co_tile, int split, int oz, int oy0, int ox0, int wco,
-                                           int wsp, int half, int col) {
+                                           int wsp, int half, int col, int sp_rec) {
   const int64_t spo = (int64_t)a.Do * a.Ho * a.Wo;
+  if constexpr (EPI) {
+    // opaque copies of the lane coordinates: the address math below then cannot be hoisted
+    // above the main loop, where its results would stay live (and cost registers) throughout
+    int colx = col, halfx = half;
+    asm volatile("" : "+v"(colx), "+v"(halfx));
+    GnLaneStats<FCO> st;
+    float nl = 0.f;  // positions this lane stores (per channel)
+#pragma unroll
+    for (int j = 0; j < FSP; ++j) {
+      const int m = (wsp * FSP + j) * 32 + colx;
+      const int ty = m / a.TX, tx = m - (m / a.TX) * a.TX;
+      const int oy = oy0 + ty, ox = ox0 + tx;
+      const bool okj = oy < a.Ho && ox < a.Wo;
+      nl += okj ? 1.f : 0.f;
+      const int64_t sp = okj ? ((int64_t)oz * a.Ho + oy) * a.Wo + ox : 0;
+#pragma unroll
+      for (int i = 0; i < FCO; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int cl = (wco * FCO + i) * 32 + (r >> 2) * 8 + halfx * 4 + (r & 3);
+          const int co = co_tile * BN + cl;
+          const bool in = okj && co < a.Co;
+          const int64_t o = ((int64_t)n * a.Co + (in ? co : 0)) * spo + sp;
+          float v = acc[i][j][r] + s_bias[cl];
+          if (a.resid && in) v += to_f32(static_cast<const T*>(a.resid)[o]);
+          const T t = from_f32<T>(v);
+          if (in) static_cast<T*>(a.y)[o] = t;
+          // running shifted sums of the stored value (shift: the octet's value at j = 0, r = 4q)
+          const int q = r >> 2;
+          const float sv = okj ? to_f32(t) : 0.f;
+          if (j == 0 && (r & 3) == 0) {
+            st.K[i][q] = sv;
+            st.s1[i][q] = 0.f;
+            st.s2[i][q] = 0.f;
+          }
+          const float d = okj ? sv - st.K[i][q] : 0.f;
+          st.s1[i][q] += d;
+          st.s2[i][q] = fmaf(d, d, st.s2[i][q]);
+        }
+      }
+    }
+    if (a.gn_parts) tile_gn_records<FCO, FSP, BN>(a, st, nl, n, co_tile, sp_rec, wco, halfx);
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < FSP; ++j) {
     const int m = (wsp * FSP + j) * 32 + col;
@@ -278,7 +401,7 @@ __device__ __forceinline__ void store_tile(const IgArgs& a, const f32x16 (&acc)[
 
 // Tiles of 8 accumulator blocks (128 AGPRs) are asked to fit 2 waves per SIMD: with their
 // LDS footprint two workgroups share a CU, and one wave per SIMD leaves no latency cover.
-template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, int XC, bool VR, int KHT, int KWT>
+template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, int XC, bool VR, int KHT, int KWT, bool EPI>
 __global__ __launch_bounds__(64 * WCO * WSP)
 __attribute__((amdgpu_waves_per_eu((FCO * FSP >= 8 && CB == 16) || XC > 1 ? 2 : 1))) void conv_igemm_kernel(IgArgs a) {
   constexpr int NT = 64 * WCO * WSP;
@@ -538,7 +661,9 @@ __attribute__((amdgpu_waves_per_eu((FCO * FSP >= 8 && CB == 16) || XC > 1 ? 2 : 
     kd = kd1;
   }
 
-  store_tile<T, FCO, FSP, BN>(a, acc, s_bias, n, co_tile, split, oz, oy0, ox0, wco, wsp, half, col);
+  // GroupNorm record index of this wave's spatial tile: (z, tile row, tile column), then wave
+  const int sp_rec = ((oz * a.tiles_y + ty_t) * a.tiles_x + tx_t) * WSP + wsp;
+  store_tile<T, FCO, FSP, BN, EPI>(a, acc, s_bias, n, co_tile, split, oz, oy0, ox0, wco, wsp, half, col, sp_rec);
 }
 
 // Packed weights Wp[tap][kb][co_block][32][KB] from w[Co][Ci][taps]; zero beyond Co / Ci.
@@ -704,22 +829,34 @@ int plan_ig(const ConvShape& p, int v, IgPlan& pl) {
 
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, int XC, bool VR, int KHT, int KWT>
-int launch_ig_vr(const IgPlan& pl, hipStream_t s) {
-  auto kern = conv_igemm_kernel<T, WCO, WSP, FCO, FSP, CB, XC, VR, KHT, KWT>;
+// One kernel instantiation: the LDS opt-in is a per-kernel attribute, set once per kernel.
+template <void (*Kern)(IgArgs)>
+int launch_ig_kern(const IgPlan& pl, int nthreads, hipStream_t s) {
   if (pl.lds > 64 * 1024) {
-    // opt in to more than 64 KB of dynamic LDS (gfx950 has 160 KB per CU); once per kernel
+    // opt in to more than 64 KB of dynamic LDS (gfx950 has 160 KB per CU)
     static bool raised = false;
     if (!raised) {
-      if (hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+      if (hipFuncSetAttribute(reinterpret_cast<const void*>(Kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                               150 * 1024) != hipSuccess)
         return fail(ATK_UNSUPPORTED, "conv: cannot raise the LDS limit");
       raised = true;
     }
   }
   dim3 grid((unsigned)pl.tiles, (unsigned)((pl.a.Co + pl.bn - 1) / pl.bn), (unsigned)pl.splits);
-  hipLaunchKernelGGL(kern, grid, dim3(64 * WCO * WSP), pl.lds, s, pl.a);
+  hipLaunchKernelGGL(Kern, grid, dim3(nthreads), pl.lds, s, pl.a);
   return check_launch("conv_igemm_kernel");
+}
+
+template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, int XC, bool VR, int KHT, int KWT>
+int launch_ig_vr(const IgPlan& pl, hipStream_t s) {
+  // the residual / GroupNorm epilogue is its own instantiation, so the plain kernel is unchanged
+  if (pl.a.resid || pl.a.gn_parts) {
+    if constexpr (VR)
+      return launch_ig_kern<conv_igemm_kernel<T, WCO, WSP, FCO, FSP, CB, XC, VR, KHT, KWT, true>>(pl, 64 * WCO * WSP, s);
+    else
+      return fail(ATK_UNSUPPORTED, "conv: the residual / GroupNorm epilogue needs 16-byte aligned input rows");
+  }
+  return launch_ig_kern<conv_igemm_kernel<T, WCO, WSP, FCO, FSP, CB, XC, VR, KHT, KWT, false>>(pl, 64 * WCO * WSP, s);
 }
 
 template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, int XC = 1>
@@ -751,12 +888,30 @@ int pack_ig(const ConvShape& p, const IgPlan& pl, const void* w, void* wp, hipSt
 
 // The implicit GEMM on weights already packed at wp; `part` holds the split-K partials (or is
 // null when the plan does not split).
+// GroupNorm records per (n, g) that an unsplit launch of variant v writes (0: it cannot).
+int gn_records(const ConvShape& p, const IgPlan& pl, int v, int G) {
+  if (G <= 0 || p.Co % G || pl.splits != 1) return 0;
+  const int cpg = p.Co / G;
+  if (!((cpg % 4 == 0 && 32 % cpg == 0) || cpg % 32 == 0)) return 0;
+  const int64_t np = (int64_t)p.Do * pl.a.tiles_y * pl.a.tiles_x * kIg[v].wsp * (cpg > 32 ? cpg / 32 : 1);
+  return np < (1 << 30) ? (int)np : 0;
+}
+
 template <typename T>
 int run_ig(const ConvShape& p, IgPlan& pl, const void* x, const void* wp, const void* bias, void* y, int v,
-           float* part, hipStream_t s) {
+           float* part, hipStream_t s, const void* resid = nullptr, float4* gn_parts = nullptr, int gn_G = 0) {
   int rc = ATK_OK;
   IgArgs& a = pl.a;
   a.x = x; a.bias = bias; a.y = y;
+  a.resid = resid;
+  a.gn_parts = gn_parts;
+  a.gn_G = gn_G;
+  a.gn_cpg = gn_G > 0 ? p.Co / gn_G : 0;
+  a.gn_np = gn_parts ? gn_records(p, pl, v, gn_G) : 0;
+  if ((resid || gn_parts) && pl.splits != 1)
+    return fail(ATK_UNSUPPORTED, "conv: the residual / GroupNorm epilogue needs an unsplit launch");
+  if (gn_parts && a.gn_np == 0)
+    return fail(ATK_UNSUPPORTED, "conv: GroupNorm statistics need Co/G in {4, 8, 16, 32} or a multiple of 32");
   a.vec_rows = (p.W % (16 / (int)sizeof(T)) == 0) && aligned16(x);
   a.x_sample_bytes = (uint32_t)((int64_t)p.Ci * p.D * p.H * p.W * sizeof(T));
   a.wp_bytes = (uint32_t)pl.wp_bytes;
@@ -852,8 +1007,24 @@ int conv_igemm_pack(const ConvShape& p, const void* w, void* packed, size_t pack
   }
 }
 
+size_t conv_igemm_gn_stats_bytes(const ConvShape& p, int v, int G) {
+  if (v < 0 || v >= kNumIg) return 0;
+  IgPlan pl;
+  if (plan_ig(p, v, pl)) return 0;
+  const int np = gn_records(p, pl, v, G);
+  return np ? (size_t)p.N * G * np * sizeof(float4) : 0;
+}
+
+int conv_igemm_gn_records(const ConvShape& p, int v, int G) {
+  if (v < 0 || v >= kNumIg) return 0;
+  IgPlan pl;
+  if (plan_ig(p, v, pl)) return 0;
+  return gn_records(p, pl, v, G);
+}
+
 int conv_igemm_run_prepacked(const ConvShape& p, const void* x, const void* packed, size_t packed_bytes,
-                             const void* bias, void* y, int v, void* ws, size_t ws_bytes, hipStream_t s) {
+                             const void* bias, void* y, int v, void* ws, size_t ws_bytes, hipStream_t s,
+                             const void* resid, void* gn_stats, size_t gn_stats_bytes, int gn_G) {
   if (v < 0 || v >= kNumIg) return fail(ATK_EINVAL, "conv: variant out of range");
   const int64_t ysz = (int64_t)p.N * p.Co * p.Do * p.Ho * p.Wo;
   if (ysz >= (1ll << 31)) return fail(ATK_UNSUPPORTED, "conv: output too large for the split-K finalize");
@@ -865,10 +1036,18 @@ int conv_igemm_run_prepacked(const ConvShape& p, const void* x, const void* pack
   if (pl.part_bytes && (!ws || ws_bytes < pl.part_bytes))
     return fail(ATK_EINVAL, "conv: workspace of %zu bytes needed", pl.part_bytes);
   float* part = static_cast<float*>(ws);
+  float4* gp = nullptr;
+  if (gn_stats) {
+    const int np = gn_records(p, pl, v, gn_G);
+    if (!np) return fail(ATK_UNSUPPORTED, "conv: this variant cannot write GroupNorm statistics for the shape");
+    const size_t need = (size_t)p.N * gn_G * np * sizeof(float4);
+    if (gn_stats_bytes < need) return fail(ATK_EINVAL, "conv: GroupNorm statistics need %zu bytes", need);
+    gp = static_cast<float4*>(gn_stats);
+  }
   switch (p.dtype) {
-    case ATK_F32: return run_ig<float>(p, pl, x, packed, bias, y, v, part, s);
-    case ATK_F16: return run_ig<_Float16>(p, pl, x, packed, bias, y, v, part, s);
-    default: return run_ig<__bf16>(p, pl, x, packed, bias, y, v, part, s);
+    case ATK_F32: return run_ig<float>(p, pl, x, packed, bias, y, v, part, s, resid, gp, gn_G);
+    case ATK_F16: return run_ig<_Float16>(p, pl, x, packed, bias, y, v, part, s, resid, gp, gn_G);
+    default: return run_ig<__bf16>(p, pl, x, packed, bias, y, v, part, s, resid, gp, gn_G);
   }
 }
 

@@ -86,6 +86,8 @@ struct GnArgs {
   uint32_t* done;     // workspace: [ngroups] workgroups that finished reading the slots
   GnSlot* slots;      // workspace: [ngroups][NS] (register-resident)
   float* partials;    // workspace: [ngroups][NS][2] (mean, M2) (two-pass)
+  float4* parts;      // split kernels: [ngroups][NP] records (count, mean, M2, -)
+  int NP;             // records per group
 };
 
 __device__ __forceinline__ int64_t slice_len(int i, int64_t slice, int64_t E) {
@@ -432,6 +434,158 @@ void gn_resident_kernel(GnArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------
+// Split GroupNorm: a statistics kernel and an apply kernel.  For groups too large for one
+// workgroup's registers, the register-resident kernel exchanges slice statistics between
+// workgroups inside one launch; here the launch boundary is the exchange.  The statistics
+// kernel loads its slice with every 16-byte load in flight (cached: the apply kernel reads
+// x again, from L2 / the Infinity Cache) and writes one record (count, mean, M2) per slice;
+// the apply kernel issues its loads, merges the group's records on one wave meanwhile, and
+// normalises from registers.  The records have explicit counts, so the apply kernel also
+// takes statistics written by other producers (the conv epilogue).
+// ---------------------------------------------------------------------------------------
+// Merge NP (count, mean, M2) records on one wave (all 64 lanes of wave 0), in a fixed order:
+//   n = sum n_i,  mean = sum n_i mean_i / n,  M2 = sum (M2_i + n_i (mean_i - mean)^2).
+// Lane l takes records l, l+64, ...; up to 64 * RC of them are read once and kept in registers
+// for the second sum.  The xor-butterfly sums give every lane (and every workgroup merging the
+// same records) bit-identical statistics.
+template <typename GetRec>
+__device__ __forceinline__ void wave_merge_counted(int NP, GetRec rec, float& mean, float& var) {
+  constexpr int RC = 8;
+  const int lane = threadIdx.x & 63;
+  float4 r[RC];
+#pragma unroll
+  for (int k = 0; k < RC; ++k) r[k] = lane + 64 * k < NP ? rec(lane + 64 * k) : make_float4(0.f, 0.f, 0.f, 0.f);
+  float sn = 0.f, sm = 0.f;
+#pragma unroll
+  for (int k = 0; k < RC; ++k) {
+    sn += r[k].x;
+    sm = fmaf(r[k].x, r[k].y, sm);
+  }
+  for (int i = lane + 64 * RC; i < NP; i += 64) {
+    const float4 x = rec(i);
+    sn += x.x;
+    sm = fmaf(x.x, x.y, sm);
+  }
+  const float n = wave_sum(sn);
+  mean = wave_sum(sm) / n;
+  float m2 = 0.f;
+#pragma unroll
+  for (int k = 0; k < RC; ++k) {
+    const float d = r[k].y - mean;
+    m2 += r[k].z + r[k].x * d * d;
+  }
+  for (int i = lane + 64 * RC; i < NP; i += 64) {
+    const float4 x = rec(i);
+    const float d = x.y - mean;
+    m2 += x.z + x.x * d * d;
+  }
+  var = wave_sum(m2) / n;
+}
+
+template <typename T, int NT, int EPV>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(EPV <= 16 ? 4 : 1)))
+void gn_split_stats_kernel(GnArgs a) {
+  constexpr int VEC = 16 / sizeof(T);
+  __shared__ float red[NT / 64];
+  const int tid = threadIdx.x;
+  const int64_t gi = blockIdx.x / a.NS;
+  const int s = (int)(blockIdx.x - gi * a.NS);
+  const int64_t E = a.E;
+  const int64_t s0 = (int64_t)s * a.slice;
+  const T* __restrict__ xg = static_cast<const T*>(a.x) + gi * E;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(xg, (uint32_t)(E * (int64_t)sizeof(T)));
+  const uint32_t lane_off = (uint32_t)tid * 16u;
+  const uint32_t n_vec = (uint32_t)((E - s0 + VEC - 1) / VEC);
+  Vec16<T> buf[EPV];
+#pragma unroll
+  for (int i = 0; i < EPV; ++i)
+    buf[i].raw = bload16(rx, (uint32_t)(i * NT + tid) < n_vec ? lane_off : kOOB,
+                         (uint32_t)((s0 + (int64_t)i * NT * VEC) * (int64_t)sizeof(T)));
+  float mean_l, m2;
+  slice_stats<T, NT, EPV, true>(buf, xg, s0, E, a.slice, red, mean_l, m2);
+  if (tid == 0) {
+    const float n_l = (float)((E - s0) < a.slice ? (E - s0) : a.slice);
+    a.parts[gi * a.NP + s] = make_float4(n_l, mean_l, m2, 0.f);
+  }
+}
+
+template <typename T, int NT, int EPV, bool SILU>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(EPV <= 16 ? 4 : 1)))
+void gn_split_apply_kernel(GnArgs a) {
+  constexpr int VEC = 16 / sizeof(T);
+  __shared__ float s_stat[2];
+  __shared__ float aff[2 * GN_MAX_AFF];
+  const int tid = threadIdx.x;
+  const int64_t gi = blockIdx.x / a.NS;
+  const int s = (int)(blockIdx.x - gi * a.NS);
+  const int64_t E = a.E;
+  const int64_t s0 = (int64_t)s * a.slice;
+  const T* __restrict__ xg = static_cast<const T*>(a.x) + gi * E;
+  T* __restrict__ yg = static_cast<T*>(a.y) + gi * E;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(xg, (uint32_t)(E * (int64_t)sizeof(T)));
+  const uint32_t lane_off = (uint32_t)tid * 16u;
+  const uint32_t n_vec = (uint32_t)((E - s0 + VEC - 1) / VEC);
+  Vec16<T> buf[EPV];
+#pragma unroll
+  for (int i = 0; i < EPV; ++i)  // last read of x: nontemporal
+    buf[i].raw = bload16<2>(rx, (uint32_t)(i * NT + tid) < n_vec ? lane_off : kOOB,
+                            (uint32_t)((s0 + (int64_t)i * NT * VEC) * (int64_t)sizeof(T)));
+  // the slice's channels and their gamma / beta words (unconditional buffer loads that
+  // nothing waits for until the merge is done)
+  const int64_t last = (s0 + a.slice < E ? s0 + a.slice : E) - 1;
+  const uint32_t c_lo = fdiv((uint32_t)s0, a.div_s);
+  const uint32_t c_hi = fdiv((uint32_t)last, a.div_s) + 1;
+  const int nch = (int)(c_hi - c_lo);
+  const int64_t cabs0 = (int64_t)(gi % a.G) * a.cpg + c_lo;
+  const bool staged = nch <= GN_MAX_AFF;
+  const int64_t nchan = (int64_t)a.G * a.cpg;
+  const int64_t cme = cabs0 + (tid < nch ? tid : 0);
+  uint32_t gsel, bsel;
+  const uint32_t gword = param_word(a.gamma, a.pdt, cme, nchan, gsel);
+  const uint32_t bword = param_word(a.beta, a.pdt, cme, nchan, bsel);
+  if (tid < 64) {
+    const float4* rp = a.parts + gi * a.NP;
+    float mean, var;
+    wave_merge_counted(a.NP, [&](int i) { return rp[i]; }, mean, var);
+    if (tid == 0) {
+      s_stat[0] = mean;
+      s_stat[1] = 1.0f / sqrtf(var + a.eps);
+    }
+  }
+  __syncthreads();
+  const float mean = s_stat[0], rstd = s_stat[1];
+  if (staged) {
+    if (tid < nch) {
+      const float sc = rstd * (a.gamma ? param_decode(gword, gsel, a.pdt) : 1.f);
+      aff[tid] = sc;
+      aff[GN_MAX_AFF + tid] = (a.beta ? param_decode(bword, bsel, a.pdt) : 0.f) - mean * sc;
+    }
+    for (int i = tid + NT; i < nch; i += NT) {
+      float sc, sh;
+      channel_affine(a, cabs0 + i, mean, rstd, sc, sh);
+      aff[i] = sc;
+      aff[GN_MAX_AFF + i] = sh;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < EPV; ++i) {
+    reg_fence<T, 1>(&buf[i]);
+    const bool ok = (uint32_t)(i * NT + tid) < n_vec;
+    const int64_t e = ok ? s0 + ((int64_t)i * NT + tid) * VEC : s0;
+    const int cl = (int)(fdiv((uint32_t)e, a.div_s) - c_lo);
+    float sc, sh;
+    if (staged) {
+      sc = aff[cl];
+      sh = aff[GN_MAX_AFF + cl];
+    } else {
+      channel_affine(a, cabs0 + cl, mean, rstd, sc, sh);
+    }
+    if (ok) st16<true>(yg + e, normalize_vec<T, SILU>(buf[i], sc, sh));
+  }
+}
+
+// ---------------------------------------------------------------------------------------
 // Two-pass streaming fallback.  VECOK: S % VEC == 0 and 16B-aligned pointers.
 // ---------------------------------------------------------------------------------------
 template <typename T, bool VECOK>
@@ -532,24 +686,31 @@ __global__ __launch_bounds__(GN_TP_NT) void gn_apply_kernel(GnArgs a) {
   }
 }
 
+enum GnKind { GN_RESIDENT = 0, GN_TWOPASS = 1, GN_SPLIT = 2 };
+
 struct GnVariant {
   const char* name;
-  int nt, epv;  // epv == 0: two-pass
+  int nt, epv;  // threads per workgroup, 16-byte vectors per thread (two-pass: unused)
+  int kind;
 };
 
 const GnVariant kGnVariants[] = {
-    {"res_nt1024_v8", 1024, 8},
-    {"res_nt1024_v16", 1024, 16},
-    {"res_nt1024_v4", 1024, 4},
-    {"res_nt512_v8", 512, 8},
-    {"res_nt256_v8", 256, 8},
-    {"res_nt256_v16", 256, 16},
-    {"twopass", GN_TP_NT, 0},
-    {"res_nt256_v4", 256, 4},
-    {"res_nt512_v4", 512, 4},
-    {"res_nt512_v16", 512, 16},
-    {"res_nt512_v32", 512, 32},
-    {"res_nt256_v32", 256, 32},
+    {"res_nt1024_v8", 1024, 8, GN_RESIDENT},
+    {"res_nt1024_v16", 1024, 16, GN_RESIDENT},
+    {"res_nt1024_v4", 1024, 4, GN_RESIDENT},
+    {"res_nt512_v8", 512, 8, GN_RESIDENT},
+    {"res_nt256_v8", 256, 8, GN_RESIDENT},
+    {"res_nt256_v16", 256, 16, GN_RESIDENT},
+    {"twopass", GN_TP_NT, 0, GN_TWOPASS},
+    {"res_nt256_v4", 256, 4, GN_RESIDENT},
+    {"res_nt512_v4", 512, 4, GN_RESIDENT},
+    {"res_nt512_v16", 512, 16, GN_RESIDENT},
+    {"res_nt512_v32", 512, 32, GN_RESIDENT},
+    {"res_nt256_v32", 256, 32, GN_RESIDENT},
+    {"split_nt256_v8", 256, 8, GN_SPLIT},
+    {"split_nt512_v8", 512, 8, GN_SPLIT},
+    {"split_nt256_v4", 256, 4, GN_SPLIT},
+    {"split_nt1024_v4", 1024, 4, GN_SPLIT},
 };
 constexpr int kNumGn = sizeof(kGnVariants) / sizeof(kGnVariants[0]);
 
@@ -579,10 +740,10 @@ bool plan_gn(int64_t N, int64_t C, int64_t S, int G, int dtype, int variant, GnP
   const int64_t ngroups = N * G;
   const int vec = (int)(16 / dtype_size(dtype));
   const GnVariant& v = kGnVariants[variant];
-  if (v.epv > 0) {
+  if (v.kind != GN_TWOPASS) {
     p.slice = (int64_t)v.nt * v.epv * vec;
     p.NS = (int)((E + p.slice - 1) / p.slice);
-    if (p.NS > GN_RES_MAX_NS) return false;
+    if (v.kind == GN_RESIDENT && p.NS > GN_RES_MAX_NS) return false;
     if (E * (int64_t)dtype_size(dtype) >= (int64_t)kOOB) return false;  // 32-bit buffer offsets
   } else {
     // aim for >= ~2048 workgroups, slices of at least 4K elements
@@ -598,7 +759,8 @@ bool plan_gn(int64_t N, int64_t C, int64_t S, int G, int dtype, int variant, GnP
   }
   if (p.NS > GN_MAX_NS) return false;
   p.zero_bytes = GN_ZERO_BYTES;
-  p.ws_bytes = GN_PARTIALS_OFF + (v.epv > 0 ? 0 : round256((size_t)ngroups * p.NS * 8));
+  const size_t rec = v.kind == GN_TWOPASS ? 8 : v.kind == GN_SPLIT ? 16 : 0;
+  p.ws_bytes = GN_PARTIALS_OFF + round256((size_t)ngroups * p.NS * rec);
   return true;
 }
 
@@ -646,10 +808,33 @@ int launch_twopass(const GnArgs& a, int64_t nblk, hipStream_t s) {
   return check_launch("gn_apply_kernel");
 }
 
+template <typename T, int NT, int EPV>
+int launch_split(GnArgs a, int64_t ngroups, hipStream_t s) {
+  const int64_t nblk = ngroups * a.NS;
+  if (nblk > 0x7fffffff) return fail(ATK_UNSUPPORTED, "group_norm: grid too large");
+  a.NP = a.NS;
+  hipLaunchKernelGGL((gn_split_stats_kernel<T, NT, EPV>), dim3((unsigned)nblk), dim3(NT), 0, s, a);
+  const int rc = check_launch("gn_split_stats_kernel");
+  if (rc) return rc;
+  if (a.silu) hipLaunchKernelGGL((gn_split_apply_kernel<T, NT, EPV, true>), dim3((unsigned)nblk), dim3(NT), 0, s, a);
+  else hipLaunchKernelGGL((gn_split_apply_kernel<T, NT, EPV, false>), dim3((unsigned)nblk), dim3(NT), 0, s, a);
+  return check_launch("gn_split_apply_kernel");
+}
+
 template <typename T>
 int launch_gn(GnArgs a, int64_t ngroups, int variant, bool vec_ok, hipStream_t s) {
   const GnVariant& v = kGnVariants[variant];
-  if (v.epv > 0) {
+  if (v.kind == GN_SPLIT) {
+    if (!vec_ok) return fail(ATK_UNSUPPORTED, "group_norm: %s needs S %% 16B == 0 and aligned pointers", v.name);
+    switch (variant) {
+      case 12: return launch_split<T, 256, 8>(a, ngroups, s);
+      case 13: return launch_split<T, 512, 8>(a, ngroups, s);
+      case 14: return launch_split<T, 256, 4>(a, ngroups, s);
+      case 15: return launch_split<T, 1024, 4>(a, ngroups, s);
+      default: return fail(ATK_EINVAL, "group_norm: bad variant");
+    }
+  }
+  if (v.kind == GN_RESIDENT) {
     if (!vec_ok) return fail(ATK_UNSUPPORTED, "group_norm: %s needs S %% 16B == 0 and aligned pointers", v.name);
     switch (variant) {
       case 0: return launch_resident<T, 1024, 8>(a, ngroups, s);
@@ -1199,6 +1384,8 @@ int gn_fwd(const void* x, const void* gamma, const void* beta, void* y, int64_t 
   a.done = reinterpret_cast<uint32_t*>(ws + 256);
   a.slots = reinterpret_cast<GnSlot*>(ws + GN_SLOTS_OFF);
   a.partials = reinterpret_cast<float*>(ws + GN_PARTIALS_OFF);
+  a.parts = reinterpret_cast<float4*>(ws + GN_PARTIALS_OFF);
+  a.NP = p.NS;
   const int khz = device_wall_clock_khz();
   // ATK_GN_WAIT_US overrides the wait (tests set 0 to exercise the stand-in path)
   const char* wenv = getenv("ATK_GN_WAIT_US");
@@ -1289,6 +1476,66 @@ extern "C" int atk_group_norm_fwd_noalloc(const void* x, const void* gamma, cons
   if (rc) return rc;
   return gn_fwd(x, gamma, beta, y, N, C, S, G, eps, fuse_silu, dtype, param_dtype, variant, ws, GN_NOALLOC_BYTES,
                 reinterpret_cast<hipStream_t>(stream), nullptr);
+}
+
+extern "C" int atk_group_norm_apply(const void* x, const void* gamma, const void* beta, void* y, int64_t N,
+                                    int64_t C, int64_t S, int G, float eps, int fuse_silu, int dtype,
+                                    int param_dtype, const void* stats, int64_t records_per_group, int variant,
+                                    atk_stream_t stream) {
+  using namespace atk;
+  if (variant < 0) variant = 12;  // split_nt256_v8
+  int rc = validate_gn(N, C, S, G, dtype, variant);
+  if (rc) return rc;
+  if (kGnVariants[variant].kind != GN_SPLIT)
+    return fail(ATK_EINVAL, "group_norm apply: %s is not a split variant", kGnVariants[variant].name);
+  if ((gamma || beta) && !dtype_ok(param_dtype))
+    return fail(ATK_EINVAL, "group_norm apply: unknown param dtype code %d", param_dtype);
+  if (N == 0) return ATK_OK;
+  if (!x || !y || !stats || records_per_group <= 0 || records_per_group >= (1ll << 30))
+    return fail(ATK_EINVAL, "group_norm apply: null pointer or bad record count");
+  const int vec = (int)(16 / dtype_size(dtype));
+  if (S % vec || !aligned16(x) || !aligned16(y) || !aligned16(stats))
+    return fail(ATK_UNSUPPORTED, "group_norm apply: needs S %% %d == 0 and 16-byte aligned tensors", vec);
+  GnPlan p;
+  if (!plan_gn(N, C, S, G, dtype, variant, p)) return fail(ATK_UNSUPPORTED, "group_norm apply: shape too large");
+  GnArgs a = {};
+  a.x = x; a.gamma = gamma; a.beta = beta; a.y = y;
+  a.E = (C / G) * S;
+  a.S = (uint32_t)S;
+  a.cpg = (uint32_t)(C / G);
+  a.G = (uint32_t)G;
+  a.NS = p.NS;
+  a.slice = p.slice;
+  a.eps = eps;
+  a.silu = fuse_silu ? 1 : 0;
+  a.pdt = param_dtype;
+  a.div_s = make_fastdiv((uint32_t)S);
+  a.parts = static_cast<float4*>(const_cast<void*>(stats));
+  a.NP = (int)records_per_group;
+  const int64_t nblk = N * G * p.NS;
+  if (nblk > 0x7fffffff) return fail(ATK_UNSUPPORTED, "group_norm apply: grid too large");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const GnVariant& v = kGnVariants[variant];
+  auto go = [&](auto kern) {
+    hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(v.nt), 0, s, a);
+    return check_launch("gn_split_apply_kernel");
+  };
+#define ATK_GN_APPLY(T, NT_, EPV_)                                                                      \
+  return a.silu ? go(gn_split_apply_kernel<T, NT_, EPV_, true>) : go(gn_split_apply_kernel<T, NT_, EPV_, false>)
+#define ATK_GN_APPLY_T(T)                                        \
+  switch (variant) {                                             \
+    case 12: ATK_GN_APPLY(T, 256, 8);                            \
+    case 13: ATK_GN_APPLY(T, 512, 8);                            \
+    case 14: ATK_GN_APPLY(T, 256, 4);                            \
+    default: ATK_GN_APPLY(T, 1024, 4);                           \
+  }
+  switch (dtype) {
+    case ATK_F32: ATK_GN_APPLY_T(float);
+    case ATK_F16: ATK_GN_APPLY_T(_Float16);
+    default: ATK_GN_APPLY_T(__bf16);
+  }
+#undef ATK_GN_APPLY_T
+#undef ATK_GN_APPLY
 }
 
 extern "C" size_t atk_group_norm_bwd_workspace_bytes(int64_t N, int64_t C) {

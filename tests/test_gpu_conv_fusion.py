@@ -1,0 +1,205 @@
+"""GPU parity of the conv epilogue fusion: residual add and GroupNorm statistics written by the
+MFMA conv's epilogue (atk_conv_fwd_prepacked_ex), and the GroupNorm apply pass that consumes
+them (atk_group_norm_apply), against the float64 oracle.  Bars: fp32 <= 1e-5 (conv),
+fp16/bf16 <= 1e-2 max-abs-rel; GroupNorm of the stored conv output <= 1e-2 (16-bit) /
+1e-4 (fp32)."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+BAR = {torch.float32: 1e-5, torch.float16: 1e-2, torch.bfloat16: 1e-2}
+GN_BAR = {torch.float32: 1e-4, torch.float16: 1e-2, torch.bfloat16: 1e-2}
+
+
+def _native():
+    from amd_tuned_torch import _native
+    return _native
+
+
+def _inputs(xs, ws, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(*xs, generator=g)
+    w = torch.randn(*ws, generator=g) * math.sqrt(2.0 / math.prod(ws[1:]))
+    b = 0.3 * torch.randn(ws[0], generator=g)
+    return x.to(dtype), w.to(dtype), b.to(dtype)
+
+
+def _mfma(nat, dtype):
+    pre = "f32_" if dtype == torch.float32 else "h_"
+    return [(i, n) for i, n in enumerate(nat.variants(nat.OP_CONV)) if n.startswith(pre)]
+
+
+def _merge(records: np.ndarray):
+    """(mean, var) per (n, g) from [N*G][P][4] records (count, mean, M2, -), float64."""
+    n, m, m2 = records[..., 0], records[..., 1], records[..., 2]
+    cnt = n.sum(-1)
+    mean = (n * m).sum(-1) / cnt
+    var = (m2 + n * (m - mean[:, None]) ** 2).sum(-1) / cnt
+    return cnt, mean, var
+
+
+CASES = [
+    # xshape, wshape, pad, groups (channels per group = Co / groups)
+    ((1, 32, 8, 16, 16), (64, 32, 3, 3, 3), 1, 8),     # cpg 8
+    ((2, 16, 5, 9, 16), (32, 16, 3, 3, 3), 1, 8),      # cpg 4, edge tiles (H = 9, D = 5), N = 2
+    ((1, 32, 4, 12, 24), (64, 32, 3, 3, 3), 1, 4),     # cpg 16
+    ((1, 32, 4, 8, 8), (64, 32, 3, 3, 3), 1, 2),       # cpg 32
+    ((1, 16, 4, 8, 8), (128, 16, 3, 3, 3), 1, 2),      # cpg 64: a group spans two 32-blocks
+    ((1, 16, 16, 64, 64), (32, 16, 3, 3, 3), 1, 4),    # large enough that fp32 tiles do not split
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32], ids=["bf16", "fp16", "fp32"])
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(map(str, c[0])) + "_g%d" % c[3])
+def test_conv_epilogue_group_norm_records(dev, case, dtype):
+    """Every unsplit MFMA variant: y is the plain conv's output byte for byte, the records merge
+    to the statistics of the stored y (float64), and the apply pass is GroupNorm(+SiLU) of y."""
+    xs, ws, pad, G = case
+    nat = _native()
+    x, w, b = _inputs(xs, ws, dtype, seed=sum(xs) + G)
+    xd, wd, bd = x.to(dev), w.to(dev), b.to(dev)
+    gc = torch.Generator().manual_seed(5)
+    gm = (1 + 0.1 * torch.randn(ws[0], generator=gc)).to(dtype)
+    bt = (0.1 * torch.randn(ws[0], generator=gc)).to(dtype)
+    ran = 0
+    for vi, name in _mfma(nat, dtype):
+        try:
+            y, rec, nrec = nat.conv_gn_stats(xd, wd, bd, 1, pad, 1, 3, G, variant=vi)
+        except nat.Unsupported:
+            continue  # declines the shape, or splits it
+        plain = nat.conv3d(xd, wd, bd, 1, pad, 1, variant=vi)
+        torch.cuda.synchronize()
+        assert torch.equal(y, plain), name
+        assert O.max_rel_err(y.cpu(), O.conv3d(x, w, b, 1, pad, 1)) <= BAR[dtype], name
+        yc = y.cpu().double().reshape(xs[0] * G, -1)
+        r = rec.cpu().double().numpy().reshape(xs[0] * G, nrec, 4)
+        cnt, mean, var = _merge(r)
+        assert np.array_equal(cnt, np.full(xs[0] * G, yc.shape[1], dtype=np.float64)), name
+        ref_mean = yc.mean(-1).numpy()
+        ref_var = yc.var(-1, unbiased=False).numpy()
+        scale = max(1.0, float(np.abs(ref_mean).max()))
+        assert np.abs(mean - ref_mean).max() <= 1e-5 * scale + 1e-6, name
+        assert np.abs(var - ref_var).max() <= 1e-4 * ref_var.max() + 1e-7, name
+        if (y.numel() // (y.shape[0] * y.shape[1])) % (16 // y.element_size()):
+            # the apply pass reads 16-byte vectors: a spatial size off that grid is declined
+            # (the fused block then runs stock)
+            with pytest.raises(nat.Unsupported):
+                nat.group_norm_apply(y, G, gm.to(dev), bt.to(dev), 1e-5, rec, nrec)
+            ran += 1
+            continue
+        for silu in (False, True):
+            out = nat.group_norm_apply(y, G, gm.to(dev), bt.to(dev), 1e-5, rec, nrec, silu=silu)
+            torch.cuda.synchronize()
+            ref = O.group_norm(y.cpu(), G, gm, bt, 1e-5, silu=silu)
+            assert O.max_rel_err(out.cpu(), ref) <= GN_BAR[dtype], (name, silu)
+        ran += 1
+    # the fp32 tiles split K on the small shapes (too few output tiles), which rules the
+    # epilogue out there; the last case is large enough for them
+    assert ran >= 1 or (dtype == torch.float32 and xs[2] * xs[3] * xs[4] < 32768)
+
+
+def test_conv_epilogue_needs_aligned_rows(dev):
+    """The epilogue instantiations read input rows as 16-byte vectors: a width off that grid
+    (W = 11 for bf16) is declined with ATK_UNSUPPORTED, and the plain conv still serves it."""
+    nat = _native()
+    x, w, b = _inputs((2, 16, 5, 9, 11), (32, 16, 3, 3, 3), torch.bfloat16, seed=3)
+    xd, wd, bd = x.to(dev), w.to(dev), b.to(dev)
+    for vi, name in _mfma(nat, torch.bfloat16):
+        try:
+            nat.conv3d(xd, wd, bd, 1, 1, 1, variant=vi)
+        except nat.Unsupported:
+            continue
+        with pytest.raises(nat.Unsupported):
+            nat.conv_gn_stats(xd, wd, bd, 1, 1, 1, 3, 8, variant=vi)
+        with pytest.raises(nat.Unsupported):
+            nat.conv3d(xd, wd, bd, 1, 1, 1, variant=vi, residual=torch.zeros(2, 32, 5, 9, 11, device=dev,
+                                                                            dtype=torch.bfloat16))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+def test_conv_epilogue_residual(dev, dtype):
+    """y = conv + bias + residual in the epilogue, for every MFMA variant that takes the shape
+    unsplit, against the float64 oracle; conv2d too."""
+    nat = _native()
+    x, w, b = _inputs((2, 16, 8, 64, 64), (48, 16, 3, 3, 3), dtype, seed=8)  # unsplit for fp32 tiles too
+    r = torch.randn(2, 48, 8, 64, 64, generator=torch.Generator().manual_seed(9)).to(dtype)
+    ref = O.conv3d(x, w, b, 1, 1, 1) + O.f64(r)
+    xd, wd, bd, rd = x.to(dev), w.to(dev), b.to(dev), r.to(dev)
+    ran = 0
+    for vi, name in _mfma(nat, dtype):
+        try:
+            y = nat.conv3d(xd, wd, bd, 1, 1, 1, variant=vi, residual=rd)
+        except nat.Unsupported:
+            continue
+        torch.cuda.synchronize()
+        assert O.max_rel_err(y.cpu(), ref) <= max(BAR[dtype], 2e-5), name
+        ran += 1
+    assert ran >= 1
+    x2, w2, b2 = _inputs((4, 16, 96, 128), (32, 16, 3, 3), dtype, seed=10)
+    r2 = torch.randn(4, 32, 96, 128, generator=torch.Generator().manual_seed(11)).to(dtype)
+    ref2 = O.conv2d(x2, w2, b2, 1, 1, 1) + O.f64(r2)
+    for vi, name in _mfma(nat, dtype):
+        try:
+            y2 = nat.conv2d(x2.to(dev), w2.to(dev), b2.to(dev), 1, 1, 1, variant=vi, residual=r2.to(dev))
+        except nat.Unsupported:
+            continue
+        torch.cuda.synchronize()
+        assert O.max_rel_err(y2.cpu(), ref2) <= max(BAR[dtype], 2e-5), name
+
+
+def test_conv_residual_api(dev):
+    """conv_fusion_ops.conv_residual through its contest (cached winner on the second call)
+    equals the stock conv plus the residual within the bf16 bar."""
+    from amd_tuned_torch import conv_fusion_ops
+    x, w, b = _inputs((1, 64, 8, 32, 32), (64, 64, 3, 3, 3), torch.bfloat16, seed=12)
+    r = torch.randn(1, 64, 8, 32, 32, generator=torch.Generator().manual_seed(13)).to(torch.bfloat16)
+    ref = O.conv3d(x, w, b, 1, 1, 1) + O.f64(r)
+    xd, wd, bd, rd = x.to(dev), w.to(dev), b.to(dev), r.to(dev)
+    with torch.no_grad():
+        for _ in range(2):
+            y = conv_fusion_ops.conv_residual(xd, wd, bd, rd, 1, 1, 1)
+            torch.cuda.synchronize()
+            assert O.max_rel_err(y.cpu(), ref) <= 1e-2
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "fp32"])
+def test_fused_conv_group_norm_silu_block(dev, dtype):
+    """The config-5 block order (Conv3d -> GroupNorm -> SiLU) through FusedConvGroupNormSiLU and
+    through the patched nn.Sequential at inference: the conv epilogue's statistics path, against
+    the float64 CPU block."""
+    import amd_tuned_torch  # noqa: F401
+    from amd_tuned_torch import conv_fusion_ops
+    torch.manual_seed(14)
+    conv = torch.nn.Conv3d(64, 64, 3, padding=1)
+    norm = torch.nn.GroupNorm(32, 64, eps=1e-6)
+    with torch.no_grad():
+        norm.weight.normal_(1.0, 0.1)
+        norm.bias.normal_(0.0, 0.1)
+    x = torch.randn(1, 64, 4, 32, 32)
+    seq64 = torch.nn.Sequential(conv, norm, torch.nn.SiLU()).double()
+    with torch.no_grad():
+        ref = conv_fusion_ops._dispatch_stock_gn()(
+            amd_tuned_torch._dispatch._STOCK_F["conv3d"](x.double(), seq64[0].weight, seq64[0].bias, 1, 1),
+            32, seq64[1].weight, seq64[1].bias, 1e-6)
+        ref = F.silu(ref)
+    seq = torch.nn.Sequential(conv, norm, torch.nn.SiLU()).to(dev, dtype)
+    fused = conv_fusion_ops.FusedConvGroupNormSiLU(seq[0], seq[1])
+    xd = x.to(dev, dtype)
+    bar = 2e-2 if dtype != torch.float32 else 1e-4
+    with torch.no_grad():
+        for _ in range(2):   # contest, then the cached winner
+            y = fused(xd)
+            torch.cuda.synchronize()
+            assert O.max_rel_err(y.cpu(), ref) <= bar
+        y2 = seq(xd)
+        torch.cuda.synchronize()
+        assert O.max_rel_err(y2.cpu(), ref) <= bar
