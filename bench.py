@@ -858,7 +858,7 @@ def traffic_probe(variants: str, iters: int = 10):
 
 # conv tiles profiled by --conv-probe: (label, x shape, w shape, padding, dtype name, variant)
 CONV_PROBE = [
-    ("C4s fp16", (1, 64, 16, 32, 32), (64, 64, 3, 3, 3), 1, "float16", "h_w14_f22_cb32"),
+    ("C4s fp16", (1, 64, 16, 32, 32), (64, 64, 3, 3, 3), 1, "float16", "h_w22_f11_cb32_ns"),
     ("C4b bf16", (2, 128, 16, 64, 64), (128, 128, 3, 3, 3), 1, "bfloat16", "h_w22_f24_cb16"),
     ("C5a bf16", (1, 256, 8, 64, 64), (256, 256, 3, 3, 3), 1, "bfloat16", "h_w41_f22_cb32"),
     ("C5b fp16", (1, 64, 16, 32, 32), (64, 64, 7, 7, 7), 3, "float16", "h_w14_f22_cb16x2"),
@@ -1015,6 +1015,75 @@ def summarize_mfma(run_dir: str, out_path: str, command: str, iters: int = 10):
     print("\n".join(lines))
 
 
+def summarize_conv_pmc(run_dirs: "list[str]", out_path: str, command: str, iters: int = 10):
+    """Stall and unit-busy counters of the CONV_PROBE conv kernels from one or more rocprofv3
+    --pmc passes (each pass its own run directory over `bench.py --conv-probe`).  Dispatches
+    are attributed by order (iters + 1 per probe entry).  Ratios: TA busy = TA_BUSY_avr
+    cycles / (duration x engine clock) (one TA per CU); MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES /
+    (SIMDs x duration x clock); the SQ_WAIT_* / SQ_ACTIVE_INST_* counters as fractions of
+    SQ_WAVE_CYCLES (summed over waves); LDS bank-conflict cycles per LDS-active cycle."""
+    import csv
+    import glob
+    simds, clk_mhz = 1024, 2400.0
+    merged: "dict[int, dict]" = {}  # probe index -> counter -> list of per-dispatch values
+    durations: "dict[int, list]" = {}
+    n = iters + 1
+    for run_dir in run_dirs:
+        for f in glob.glob(os.path.join(run_dir, "**", "*agent_info.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                if r.get("Agent_Type") == "GPU":
+                    simds = int(r["Simd_Count"]) or simds
+                    clk_mhz = float(r["Max_Engine_Clk_Fcompute"]) or clk_mhz
+        per: "dict[int, dict]" = {}
+        for f in glob.glob(os.path.join(run_dir, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                if "conv_igemm_kernel" not in r["Kernel_Name"]:
+                    continue
+                d = per.setdefault(int(r["Dispatch_Id"]),
+                                   {"ns": float(r["End_Timestamp"]) - float(r["Start_Timestamp"])})
+                d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        order = [per[k] for k in sorted(per)]
+        if len(order) != n * len(CONV_PROBE):
+            continue
+        for j in range(len(CONV_PROBE)):
+            for d in order[j * n:(j + 1) * n]:
+                durations.setdefault(j, []).append(d["ns"])
+                for k, v in d.items():
+                    if k != "ns":
+                        merged.setdefault(j, {}).setdefault(k, []).append(v)
+    lines = ["# Unit-busy and stall counters of the conv implicit-GEMM kernels (rocprofv3 --pmc passes)",
+             f"# command: {command}",
+             f"# {simds} SIMDs at {clk_mhz:.0f} MHz; per-dispatch averages over {n} launches per tile"]
+    mean = lambda xs: sum(xs) / max(1, len(xs))  # noqa: E731
+    for j, (label, xs, ws, pad, dt, vn) in enumerate(CONV_PROBE):
+        if j not in merged:
+            lines.append(f"  {label} {vn}: no complete pass")
+            continue
+        c = {k: mean(v) for k, v in merged[j].items()}
+        ns = mean(durations[j])
+        cyc = ns * 1e-9 * clk_mhz * 1e6
+        wave_cyc = c.get("SQ_WAVE_CYCLES", 0.0)
+        parts = [f"{label} {vn}: {ns / 1e3:.2f} us"]
+        if "TA_BUSY_avr" in c:
+            parts.append(f"TA busy {100 * c['TA_BUSY_avr'] / cyc:.1f}%")
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in c:
+            parts.append(f"MFMA busy {100 * c['SQ_VALU_MFMA_BUSY_CYCLES'] / (simds * cyc):.1f}%")
+        for k in ("SQ_WAIT_ANY", "SQ_WAIT_INST_ANY", "SQ_WAIT_INST_LDS", "SQ_ACTIVE_INST_LDS",
+                  "SQ_ACTIVE_INST_VMEM", "SQ_ACTIVE_INST_VALU", "SQ_ACTIVE_INST_ANY", "SQ_INST_CYCLES_VMEM_RD"):
+            if k in c and wave_cyc:
+                parts.append(f"{k[3:]} {100 * c[k] / wave_cyc:.1f}% of wave cycles")
+        if "SQ_LDS_BANK_CONFLICT" in c and c.get("SQ_ACTIVE_INST_LDS"):
+            parts.append(f"LDS bank conflict {c['SQ_LDS_BANK_CONFLICT'] / c['SQ_ACTIVE_INST_LDS']:.2f} per LDS-active cycle")
+        for k in ("TA_ADDR_STALLED_BY_TC_CYCLES", "TA_DATA_STALLED_BY_TC_CYCLES", "TA_ADDR_STALLED_BY_TD_CYCLES"):
+            if k in c:
+                parts.append(f"{k} {100 * c[k] / cyc:.1f}% of kernel cycles")
+        lines.append("  " + "; ".join(parts))
+        lines.append("      raw: " + ", ".join(f"{k}={v:.4g}" for k, v in sorted(c.items())))
+    with open(out_path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def _counter_means(run_dir: str, counter: str) -> "dict[str, float]":
     """Mean per-dispatch value of `counter` for each kernel name in a rocprofv3 --pmc run."""
     import csv
@@ -1130,6 +1199,8 @@ def main():
     ap.add_argument("--command", default="", help="command line recorded by --summarize-traffic")
     ap.add_argument("--conv-probe", action="store_true",
                     help="run only the workload of the MFMA counter pass (CONV_PROBE conv tiles)")
+    ap.add_argument("--summarize-conv-pmc", nargs="+", metavar="DIR_OR_OUT",
+                    help="PMC_DIR [PMC_DIR ...] OUT: unit-busy / stall summary of --conv-probe passes")
     ap.add_argument("--summarize-mfma", nargs=2, metavar=("PMC_DIR", "OUT"),
                     help="write the MFMA utilisation summary from a rocprofv3 --pmc output folder")
     ap.add_argument("--gn-probe", action="store_true",
@@ -1145,6 +1216,9 @@ def main():
         return
     if args.summarize_mfma:
         summarize_mfma(*args.summarize_mfma, args.command)
+        return
+    if args.summarize_conv_pmc:
+        summarize_conv_pmc(args.summarize_conv_pmc[:-1], args.summarize_conv_pmc[-1], args.command)
         return
     if args.summarize_gn_traffic:
         summarize_gn_traffic(*args.summarize_gn_traffic, args.command)
