@@ -531,6 +531,15 @@ __attribute__((amdgpu_waves_per_eu((FCO * FSP >= 8 && CB == 16) || XC > 1 ? 2 : 
 #pragma unroll
       for (int p = 0; p < PF; ++p) load_w(wb[p], wbase(cc, kd) + p * tap_bytes);
     }
+    // im2col fragments are read from LDS one k-step ahead of the MFMAs that use them (two
+    // register sets), so inside a stage a wave's MFMAs do not wait on its own LDS reads
+    constexpr int NSTEP = NT2 * NKB;
+    auto rd_b = [&](uint4 (&pf)[FSP], uint32_t pbuf, int step) {
+      const int t2 = step / NKB, kb = step % NKB;
+      const uint32_t toffb = (uint32_t)(t2 / KWT) * kh_step + (uint32_t)(t2 % KWT) * kw_step + kb * KB * ES;
+#pragma unroll
+      for (int j = 0; j < FSP; ++j) pf[j] = *reinterpret_cast<const uint4*>(lds_bytes + pbuf + pb[j] + toffb);
+    };
     for (int s = s_begin; s < s_end; ++s) {
       const int iz = iz_base + kd * a.dd;
       const bool zin = (unsigned)iz < (unsigned)a.D;
@@ -546,6 +555,8 @@ __attribute__((amdgpu_waves_per_eu((FCO * FSP >= 8 && CB == 16) || XC > 1 ? 2 : 
       const int lim1 = __builtin_amdgcn_readfirstlane(ld.stage_lim(a, cc1, iz1, has_next));
       const uint32_t wb_cur = wbase(cc, kd);
       const uint32_t wb_nxt = has_next ? wbase(cc1, kd1) : wb_cur;  // last stage: harmless reload
+      uint4 pfb[2][FSP];
+      if (zin) rd_b(pfb[0], pbuf, 0);
 #pragma unroll
       for (int t2 = 0; t2 < NT2; ++t2) {
         const int tp = t2 + PF;
@@ -556,18 +567,15 @@ __attribute__((amdgpu_waves_per_eu((FCO * FSP >= 8 && CB == 16) || XC > 1 ? 2 : 
             if (t2 * LPT + l < MAXC) ld.load_fast(rx, t2 * LPT + l, so1, lim1);
         }
         if (zin) {
-          const uint32_t toffb = (uint32_t)(t2 / KWT) * kh_step + (uint32_t)(t2 % KWT) * kw_step;
 #pragma unroll
           for (int kb = 0; kb < NKB; ++kb) {
-            uint4 pf[FSP];
-#pragma unroll
-            for (int j = 0; j < FSP; ++j)
-              pf[j] = *reinterpret_cast<const uint4*>(lds_bytes + pbuf + pb[j] + toffb + kb * KB * ES);
+            const int step = t2 * NKB + kb;
+            if (step + 1 < NSTEP) rd_b(pfb[(step + 1) & 1], pbuf, step + 1);
 #pragma unroll
             for (int i = 0; i < FCO; ++i)
 #pragma unroll
               for (int j = 0; j < FSP; ++j)
-                mfma_block(acc[i][j], wb[t2 % NB][kb][i], pf[j], static_cast<T*>(nullptr));
+                mfma_block(acc[i][j], wb[t2 % NB][kb][i], pfb[step & 1][j], static_cast<T*>(nullptr));
           }
         }
         // the idle buffer was released by every wave at the previous stage's barrier
