@@ -81,7 +81,9 @@ const char* atk_variant_name(int op, int variant);
  *     F.conv1d shape) or L_out = L (the truncated shape
  *     `causal_conv1d_fwd(x, w, bias, ..., silu)` returns,
  *     src/causal-conv1d-amd/csrc/causal_conv1d.cpp:131-238).
- * x: [N, C, L], w: [C, K], bias: [C] or NULL, y: [N, C, L_out]; all of `dtype`.
+ * x: [N, C, L], y: [N, C, L_out] of `dtype`; w: [C, K] and bias: [C] (or NULL) of
+ * w_dtype, which is `dtype` or fp32 (the causal interface keeps fp32 weights with
+ * 16-bit activations, causal_conv1d.cpp:139-141; they are used unrounded).
  * Accumulation is fp32 for every dtype.  fuse_silu != 0 applies y*sigmoid(y)
  * before the store (the causal kernel's `silu_activation` flag).
  * K in [1, 64]; pad_left in [0, 64].  variant < 0 takes the first of xlane,
@@ -89,7 +91,7 @@ const char* atk_variant_name(int op, int variant);
  * ------------------------------------------------------------------------- */
 int atk_dwconv1d_fwd(const void* x, const void* w, const void* bias, void* y,
                      int64_t N, int64_t C, int64_t L, int K, int pad_left, int64_t L_out,
-                     int dtype, int fuse_silu, int variant, atk_stream_t stream);
+                     int dtype, int w_dtype, int fuse_silu, int variant, atk_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Causal conv1d decode step (replaces `causal_conv1d_update(x, conv_state, weight,
@@ -97,11 +99,13 @@ int atk_dwconv1d_fwd(const void* x, const void* w, const void* bias, void* y,
  * causal_conv1d_update.cu:27-66):
  *   conv_state[b,d,:] <- (conv_state[b,d,1:], x[b,d]),
  *   y[b,d] = bias[d] + sum_j w[d,j] * conv_state[b,d,j]   (+ SiLU if fuse_silu).
- * x, y: [B, D]; conv_state: [B, D, W] (updated in place); w: [D, W]; bias: [D] or
- * NULL; all of `dtype`.  W in [1, 64] (the reference: [2, 4]).
+ * x, y: [B, D] and conv_state: [B, D, W] (updated in place) of `dtype`; w: [D, W] and
+ * bias: [D] (or NULL) of w_dtype, `dtype` or fp32 (causal_conv1d.cpp:437 dispatches the
+ * weight type separately).  W in [1, 64] (the reference: [2, 4]).
  * ------------------------------------------------------------------------- */
 int atk_causal_conv1d_update(const void* x, void* conv_state, const void* w, const void* bias, void* y,
-                             int64_t B, int64_t D, int W, int dtype, int fuse_silu, atk_stream_t stream);
+                             int64_t B, int64_t D, int W, int dtype, int w_dtype, int fuse_silu,
+                             atk_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Depthwise / causal conv1d backward, weight and bias gradients (replaces the

@@ -67,9 +67,9 @@ def _declare(lib) -> None:
     lib.atk_num_variants.restype = i32
     lib.atk_variant_name.argtypes = [i32, i32]
     lib.atk_variant_name.restype = c.c_char_p
-    lib.atk_dwconv1d_fwd.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, i32, i64, i32, i32, i32, vp]
+    lib.atk_dwconv1d_fwd.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, i32, i64, i32, i32, i32, i32, vp]
     lib.atk_dwconv1d_fwd.restype = i32
-    lib.atk_causal_conv1d_update.argtypes = [vp, vp, vp, vp, vp, i64, i64, i32, i32, i32, vp]
+    lib.atk_causal_conv1d_update.argtypes = [vp, vp, vp, vp, vp, i64, i64, i32, i32, i32, i32, vp]
     lib.atk_causal_conv1d_update.restype = i32
     lib.atk_dwconv1d_bwd_weight_workspace_bytes.argtypes = [i64, i64, i32]
     lib.atk_dwconv1d_bwd_weight_workspace_bytes.restype = sz
@@ -291,7 +291,8 @@ def dwconv1d(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]
              l_out: int, *, silu: bool = False, variant: int = -1,
              out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """y[n,c,t] = bias[c] + sum_j weight[c,j] * x[n,c,t-pad_left+j], t < l_out (x = 0
-    outside [0, L)).  x [N,C,L] contiguous, weight [C,K] (squeezed depthwise kernel)."""
+    outside [0, L)).  x [N,C,L] contiguous, weight [C,K] (squeezed depthwise kernel); weight
+    and bias in x's dtype or, both, in fp32 (used unrounded)."""
     _require_cuda(x, weight, bias)
     if x.dim() != 3 or weight.dim() != 2:
         raise RuntimeError("dwconv1d expects x [N, C, L] and weight [C, K]")
@@ -300,8 +301,8 @@ def dwconv1d(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]
         raise RuntimeError("dwconv1d: weight.shape[0] must equal channels")
     if x.dtype not in _DTYPE_CODE:
         raise RuntimeError("dwconv1d: x must be float16, bfloat16 or float32")
-    if weight.dtype != x.dtype or (bias is not None and bias.dtype != x.dtype):
-        raise RuntimeError("dwconv1d: x, weight and bias must have the same dtype")
+    if weight.dtype not in (x.dtype, torch.float32) or (bias is not None and bias.dtype != weight.dtype):
+        raise RuntimeError("dwconv1d: weight and bias must share x's dtype or be fp32")
     if bias is not None and (bias.dim() != 1 or bias.shape[0] != C):
         raise RuntimeError("dwconv1d: bias must be [C]")
     if not x.is_contiguous():
@@ -311,7 +312,8 @@ def dwconv1d(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]
     K = weight.shape[1]
     y = out if out is not None else torch.empty((N, C, l_out), dtype=x.dtype, device=x.device)
     rc = lib().atk_dwconv1d_fwd(_ptr(x), _ptr(weight), _ptr(bias), _ptr(y), N, C, L, K, pad_left,
-                                l_out, _DTYPE_CODE[x.dtype], int(bool(silu)), variant, _stream(x))
+                                l_out, _DTYPE_CODE[x.dtype], _DTYPE_CODE[weight.dtype], int(bool(silu)), variant,
+                                _stream(x))
     _check(rc, "dwconv1d")
     return y
 
@@ -319,8 +321,9 @@ def dwconv1d(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]
 def causal_conv1d_update(x: torch.Tensor, conv_state: torch.Tensor, weight: torch.Tensor,
                          bias: Optional[torch.Tensor] = None, *, silu: bool = False) -> torch.Tensor:
     """Decode step: conv_state [B, D, W] <- (conv_state[..., 1:], x); returns
-    y [B, D] = bias + sum_j weight[:, j] * conv_state[..., j] (+ SiLU).  x [B, D],
-    weight [D, W], bias [D] or None, all one dtype; conv_state contiguous (updated in place)."""
+    y [B, D] = bias + sum_j weight[:, j] * conv_state[..., j] (+ SiLU).  x [B, D] and
+    conv_state (contiguous, updated in place) of one dtype; weight [D, W] and bias [D] or None
+    in that dtype or, both, fp32."""
     _require_cuda(x, conv_state, weight, bias)
     if x.dim() != 2 or conv_state.dim() != 3 or weight.dim() != 2:
         raise RuntimeError("causal_conv1d_update expects x [B, D], conv_state [B, D, W], weight [D, W]")
@@ -328,9 +331,10 @@ def causal_conv1d_update(x: torch.Tensor, conv_state: torch.Tensor, weight: torc
     W = weight.shape[1]
     if tuple(conv_state.shape) != (B, D, W) or weight.shape[0] != D:
         raise RuntimeError("causal_conv1d_update: conv_state must be [B, D, W] and weight [D, W]")
-    if x.dtype not in _DTYPE_CODE or conv_state.dtype != x.dtype or weight.dtype != x.dtype or \
-            (bias is not None and bias.dtype != x.dtype):
-        raise RuntimeError("causal_conv1d_update: x, conv_state, weight and bias must share a dtype")
+    if x.dtype not in _DTYPE_CODE or conv_state.dtype != x.dtype or weight.dtype not in (x.dtype, torch.float32) \
+            or (bias is not None and bias.dtype != weight.dtype):
+        raise RuntimeError("causal_conv1d_update: x and conv_state must share a dtype; weight and bias that "
+                           "dtype or fp32")
     if not conv_state.is_contiguous():
         raise RuntimeError("causal_conv1d_update: conv_state must be contiguous (it is updated in place)")
     x = x.contiguous()
@@ -338,7 +342,8 @@ def causal_conv1d_update(x: torch.Tensor, conv_state: torch.Tensor, weight: torc
     bias = bias.contiguous() if bias is not None else None
     y = torch.empty_like(x)
     rc = lib().atk_causal_conv1d_update(_ptr(x), _ptr(conv_state), _ptr(weight), _ptr(bias), _ptr(y), B, D, W,
-                                        _DTYPE_CODE[x.dtype], int(bool(silu)), _stream(x))
+                                        _DTYPE_CODE[x.dtype], _DTYPE_CODE[weight.dtype], int(bool(silu)),
+                                        _stream(x))
     _check(rc, "causal_conv1d_update")
     return y
 

@@ -12,8 +12,9 @@ out[b,c,t] = act(bias[c] + sum_j weight[c,j] * x[b,c,t-(width-1)+j]), x < 0 take
 (causal_conv1d.cpp:155-222) the layout decides the kernel: x.stride(1) == 1 with
 x.stride(2) > 1 is channel-last and runs the channels-last kernel, which also serves seq_idx
 (taps across a sequence boundary dropped) and initial / final states; any other x runs the
-(B, C, L) kernel and rejects those three.  Weights are used as fp32 when given in fp32 on the
-channel-last path; the (B, C, L) kernel takes them in x's dtype.  The backward (the
+(B, C, L) kernel and rejects those three.  Weights given in fp32 are used unrounded by both
+layouts and by the decode step, as the reference dispatches the weight type separately
+(causal_conv1d.cpp:139-141,229,437); weights of another type are used in x's dtype.  The backward (the
 reference's causal_conv1d_bwd) is one fused channels-last kernel (dx, dweight, dbias, with the
 SiLU derivative from the recomputed fp32 pre-activation); the (B, C, L) layout composes the
 forward kernel on the flipped weights with the weight-gradient kernel.  The decode step
@@ -33,7 +34,8 @@ def _channel_last(x: torch.Tensor) -> bool:
     return x.stride(1) == 1 and x.stride(2) > 1
 
 
-def _cl_weight(weight: torch.Tensor, x: torch.Tensor, bias):
+def _kernel_weight(weight: torch.Tensor, x: torch.Tensor, bias):
+    """The weights (and bias) as the kernels take them: fp32, or x's dtype."""
     w = weight if weight.dtype in (torch.float32, x.dtype) else weight.float()
     return w, (bias.to(w.dtype) if bias is not None else None)
 
@@ -42,7 +44,7 @@ def _forward(x, weight, bias, seq_idx, initial_states, final_states_out, silu: b
     B, D, L = x.shape
     K = weight.shape[1]
     if _channel_last(x):
-        w, b = _cl_weight(weight, x, bias)
+        w, b = _kernel_weight(weight, x, bias)
         out = torch.empty_like(x)
         _native.dwconv1d_cl(
             x.transpose(1, 2), w, b, K - 1, L, silu=silu, seq_idx=seq_idx,
@@ -57,9 +59,8 @@ def _forward(x, weight, bias, seq_idx, initial_states, final_states_out, silu: b
         raise RuntimeError("initial_states is only supported for channel last layout")
     if final_states_out is not None:
         raise RuntimeError("final_states is only supported for channel last layout")
-    w = weight.to(x.dtype)
-    b = bias.to(x.dtype) if bias is not None else None
-    return _native.dwconv1d(x.contiguous(), w, b, K - 1, L, silu=silu)
+    w, b = _kernel_weight(weight, x, bias)
+    return _native.dwconv1d(x.contiguous(), w.contiguous(), b, K - 1, L, silu=silu)
 
 
 def _dsilu(z: torch.Tensor) -> torch.Tensor:
@@ -75,19 +76,20 @@ def _backward(x, weight, bias, dout, seq_idx, initial_states, dfinal, silu: bool
     if _channel_last(x):
         if dout.stride(1) != 1:
             dout = dout.transpose(-1, -2).contiguous().transpose(-1, -2)
-        w, b = _cl_weight(weight, x, bias)
+        w, b = _kernel_weight(weight, x, bias)
         dx = torch.empty_like(x)
         _, dw, db = _native.causal_conv1d_cl_bwd(
             x.transpose(1, 2), dout.transpose(1, 2), w, b, silu=silu, seq_idx=seq_idx,
             initial_states=None if initial_states is None else initial_states.transpose(1, 2),
             dx=dx.transpose(1, 2))
     else:
-        # the forward used the weights and bias in x's dtype: differentiate that function
+        # differentiate the function the forward computed: weights and bias as the kernel took them
         xc, g = x.contiguous(), dout.contiguous()
-        wq = weight.to(x.dtype)
+        wq, bq = _kernel_weight(weight, x, bias)
+        wq = wq.contiguous()
         fused = None
         try:
-            fused = _native.causal_conv1d_bwd(xc, g, wq, bias.to(x.dtype) if bias is not None else None, silu=silu)
+            fused = _native.causal_conv1d_bwd(xc, g, wq, bq, silu=silu)
         except _native.Unsupported:
             fused = None
         if fused is not None:
@@ -95,12 +97,12 @@ def _backward(x, weight, bias, dout, seq_idx, initial_states, dfinal, silu: bool
         elif silu:
             # the SiLU derivative needs the fp32 pre-activation: run both kernels in fp32
             xf, wf = xc.float(), wq.float()
-            z = _native.dwconv1d(xf, wf, bias.to(x.dtype).float() if bias is not None else None, K - 1, L)
+            z = _native.dwconv1d(xf, wf, bq.float() if bq is not None else None, K - 1, L)
             gf = g.float() * _dsilu(z)
-            dx = _native.dwconv1d(gf, wf.flip(-1), None, 0, L).to(x.dtype)
+            dx = _native.dwconv1d(gf, wf.flip(-1).contiguous(), None, 0, L).to(x.dtype)
             dw, db = _native.dwconv1d_bwd_weight(xf, gf, K, K - 1)
         else:
-            dx = _native.dwconv1d(g, wq.flip(-1), None, 0, L)
+            dx = _native.dwconv1d(g, wq.flip(-1).contiguous(), None, 0, L)
             dw, db = _native.dwconv1d_bwd_weight(xc, g, K, K - 1)
     dinit = None
     if initial_states is not None and want_dinit:
@@ -231,10 +233,7 @@ def causal_conv1d_update(x, conv_state, weight, bias=None, activation=None):
     width = weight.shape[-1]
     if not 2 <= width <= 4:
         raise RuntimeError("causal_conv1d only supports width between 2 and 4")
-    if weight.dtype != x.dtype:
-        weight = weight.to(x.dtype)
-    if bias is not None and bias.dtype != x.dtype:
-        bias = bias.to(x.dtype)
+    weight, bias = _kernel_weight(weight, x, bias)
     return _native.causal_conv1d_update(x, conv_state, weight, bias, silu=activation is not None)
 
 

@@ -46,9 +46,35 @@ struct DwArgs {
   int K, pad;
   int x_off, y_off;        // misalignment of the x / y base pointers, in elements
   int silu;
+  int w32;                 // w and b are fp32 (else the activations' type)
   FastDiv div_lout, div_c;
   int win_cap;             // LDS window capacity, elements
 };
+
+// Weight / bias element i, stored in the activations' type T or (w32) in fp32 -- the causal
+// interface takes fp32 weights with 16-bit activations and computes with them unrounded
+// (src/causal-conv1d-amd/csrc/causal_conv1d.cpp:139-141).  The dword holding the element is
+// loaded either way (it lies inside the array's allocation) and decoded by the flag, so the
+// load is issued before the value is needed with no branch around it.
+template <typename T>
+__device__ __forceinline__ uint32_t dw_pword(const void* p, bool w32, int64_t i) {
+  const uintptr_t ad = reinterpret_cast<uintptr_t>(p) + (uintptr_t)i * ((sizeof(T) == 4 || w32) ? 4u : 2u);
+  return *reinterpret_cast<const uint32_t*>(ad & ~(uintptr_t)3);
+}
+template <typename T>
+__device__ __forceinline__ float dw_pdecode(uint32_t d, const void* p, bool w32, int64_t i) {
+  if constexpr (sizeof(T) == 4) {
+    return __uint_as_float(d);
+  } else {
+    if (w32) return __uint_as_float(d);
+    const uintptr_t ad = reinterpret_cast<uintptr_t>(p) + (uintptr_t)i * 2u;
+    return to_f32(__builtin_bit_cast(T, (unsigned short)((ad & 2u) ? (d >> 16) : (d & 0xffffu))));
+  }
+}
+template <typename T>
+__device__ __forceinline__ float dw_param(const void* p, bool w32, int64_t i) {
+  return dw_pdecode<T>(dw_pword<T>(p, w32, i), p, w32, i);
+}
 
 template <typename T, int KT, int OPT, bool NTH, bool SILU>
 __global__ __launch_bounds__(DW_NT) void dwconv1d_lds_kernel(DwArgs a) {
@@ -134,8 +160,8 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_lds_kernel(DwArgs a) {
       const uint32_t c = fdiv((uint32_t)(ra + rr), a.div_c);
       const uint32_t ch = (uint32_t)(ra + rr) - c * a.C;
       float v;
-      if (j < K) v = to_f32(w[(int64_t)ch * K + j]);
-      else v = bias ? to_f32(bias[ch]) : 0.f;
+      if (j < K) v = dw_param<T>(w, a.w32, (int64_t)ch * K + j);
+      else v = bias ? dw_param<T>(bias, a.w32, ch) : 0.f;
       wl[i] = v;
     }
   }
@@ -186,7 +212,7 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_lds_kernel(DwArgs a) {
       float wk[KT > 0 ? KT : 1];
       float bv;
       const float* wrow = nullptr;
-      const T* wg = nullptr;
+      int64_t wg = 0;  // element index of the row's first weight
       uint32_t ch = 0;
       if (rows_in_lds) {
         wrow = wl + r_rel * per;
@@ -194,8 +220,8 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_lds_kernel(DwArgs a) {
       } else {
         const uint32_t c = fdiv((uint32_t)r, a.div_c);
         ch = (uint32_t)r - c * a.C;
-        wg = w + (int64_t)ch * K;
-        bv = bias ? to_f32(bias[ch]) : 0.f;
+        wg = (int64_t)ch * K;
+        bv = bias ? dw_param<T>(bias, a.w32, ch) : 0.f;
       }
       if (KT > 0) {
         if (rows_in_lds) {
@@ -203,7 +229,7 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_lds_kernel(DwArgs a) {
           for (int j = 0; j < (KT > 0 ? KT : 1); ++j) wk[j] = wrow[j];
         } else {
 #pragma unroll
-          for (int j = 0; j < (KT > 0 ? KT : 1); ++j) wk[j] = to_f32(wg[j]);
+          for (int j = 0; j < (KT > 0 ? KT : 1); ++j) wk[j] = dw_param<T>(w, a.w32, wg + j);
         }
       }
       const int s = (int)t - pad;  // input position of window element 0
@@ -233,7 +259,7 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_lds_kernel(DwArgs a) {
         for (int j = 0; j < K; ++j) {
           float wj;
           if (rows_in_lds) wj = wrow[j];
-          else wj = to_f32(wg[j]);
+          else wj = dw_param<T>(w, a.w32, wg + j);
 #pragma unroll
           for (int e = 0; e < VEC; ++e) {
             const int pos = s + e + j;
@@ -261,13 +287,13 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_lds_kernel(DwArgs a) {
         const uint32_t c = fdiv((uint32_t)r, a.div_c);
         const uint32_t ch = (uint32_t)r - c * a.C;
         if (rows_in_lds) acc = wl[rr * per + K];
-        else acc = bias ? to_f32(bias[ch]) : 0.f;
+        else acc = bias ? dw_param<T>(bias, a.w32, ch) : 0.f;
         const int s = (int)te - pad;
         const int p0 = (int)(r * (int64_t)L + s - I_base);
         for (int j = 0; j < K; ++j) {
           const int pos = s + j;
           if ((unsigned)pos >= L) continue;
-          wj = rows_in_lds ? wl[rr * per + j] : to_f32(w[(int64_t)ch * K + j]);
+          wj = rows_in_lds ? wl[rr * per + j] : dw_param<T>(w, a.w32, (int64_t)ch * K + j);
           acc = fmaf(wj, to_f32(win[p0 + j]), acc);
         }
         if constexpr (SILU) acc = silu_f32(acc);
@@ -289,12 +315,12 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_direct_kernel(DwArgs a) {
   const int64_t r = f / a.Lout;
   const int64_t t = f - r * a.Lout;
   const int64_t ch = r % a.C;
-  float acc = bias ? to_f32(bias[ch]) : 0.f;
+  float acc = bias ? dw_param<T>(bias, a.w32, ch) : 0.f;
   const int64_t s = t - a.pad;
   for (int j = 0; j < a.K; ++j) {
     const int64_t pos = s + j;
     if (pos < 0 || pos >= (int64_t)a.L) continue;
-    acc = fmaf(to_f32(w[ch * a.K + j]), to_f32(x[r * (int64_t)a.L + pos]), acc);
+    acc = fmaf(dw_param<T>(w, a.w32, ch * a.K + j), to_f32(x[r * (int64_t)a.L + pos]), acc);
   }
   if constexpr (SILU) acc = silu_f32(acc);
   y[f] = from_f32<T>(acc);
@@ -394,17 +420,18 @@ __device__ __forceinline__ void reg_vector(const DwArgs& a, int64_t f) {
     int mA;
     Win::fetch(rx, (int)(r * L + t) - pad + a.x_off, true, DA, mA);
     const uint32_t c = r - fdiv(r, a.div_c) * a.C;
-    const T* bsrc = bias ? bias : w;  // w has >= C elements
+    const void* bsrc = bias ? static_cast<const void*>(bias) : a.w;  // w has >= C elements
     const float bscale = bias ? 1.f : 0.f;
-    T wr[KT];
+    const bool w32 = a.w32;
+    uint32_t wr[KT];
 #pragma unroll
-    for (int j = 0; j < KT; ++j) wr[j] = w[c * KT + j];
-    const T br = bsrc[c];
+    for (int j = 0; j < KT; ++j) wr[j] = dw_pword<T>(w, w32, (int64_t)c * KT + j);
+    const uint32_t br = dw_pword<T>(bsrc, w32, c);
     float xv[WN], xw[WN], wk[KT], wk2[KT];
     Win::extract(DA, mA, (int)t - pad, L, xv);
 #pragma unroll
-    for (int j = 0; j < KT; ++j) wk[j] = to_f32(wr[j]);
-    const float bv = to_f32(br) * bscale;
+    for (int j = 0; j < KT; ++j) wk[j] = dw_pdecode<T>(wr[j], w, w32, (int64_t)c * KT + j);
+    const float bv = dw_pdecode<T>(br, bsrc, w32, c) * bscale;
     float bv2 = bv;
     // a vector crossing into row r + 1 (once per row for unaligned rows): its second window
     // and the next channel's weights are fetched here, off the common path
@@ -415,8 +442,8 @@ __device__ __forceinline__ void reg_vector(const DwArgs& a, int64_t f) {
       Win::fetch(rx, (int)((r + 1) * L) - (int)eb - pad + a.x_off, true, DB, mB);
       const uint32_t c2 = c + 1 == a.C ? 0u : c + 1;
 #pragma unroll
-      for (int j = 0; j < KT; ++j) wk2[j] = to_f32(w[c2 * KT + j]);
-      bv2 = to_f32(bsrc[c2]) * bscale;
+      for (int j = 0; j < KT; ++j) wk2[j] = dw_param<T>(w, w32, (int64_t)c2 * KT + j);
+      bv2 = dw_param<T>(bsrc, w32, c2) * bscale;
       Win::extract(DB, mB, -(int)eb - pad, L, xw);
     }
     Vec16<T> o;
@@ -445,11 +472,11 @@ __device__ __forceinline__ void reg_vector(const DwArgs& a, int64_t f) {
       const uint32_t re = fdiv((uint32_t)fe, a.div_lout);
       const uint32_t te = (uint32_t)fe - re * Lout;
       const uint32_t ce = re - fdiv(re, a.div_c) * a.C;
-      float acc = bias ? to_f32(bias[ce]) : 0.f;
+      float acc = bias ? dw_param<T>(bias, a.w32, ce) : 0.f;
       const int se = (int)te - pad;
       for (int j = 0; j < KT; ++j) {
         const int pos = se + j;
-        if ((unsigned)pos < L) acc = fmaf(to_f32(w[ce * KT + j]), to_f32(x[(int64_t)re * L + pos]), acc);
+        if ((unsigned)pos < L) acc = fmaf(dw_param<T>(w, a.w32, (int64_t)ce * KT + j), to_f32(x[(int64_t)re * L + pos]), acc);
       }
       if constexpr (SILU) acc = silu_f32(acc);
       y[fe] = from_f32<T>(acc);
@@ -468,13 +495,18 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_reg_kernel(DwArgs a) {
 // that holds an element of the array (w and b are element-aligned).
 template <typename T, int KT>
 __device__ __forceinline__ void uniform_params(const void* wp, const void* bp, uint32_t c, float* wk,
-                                               float& bv) {
+                                               float& bv, bool w32) {
   typedef const __attribute__((address_space(4))) uint32_t* cptr;
-  if constexpr (sizeof(T) == 4) {
+  auto fp32_params = [&]() {
     const cptr q = (cptr)((uintptr_t)wp + (uintptr_t)c * KT * 4u);
 #pragma unroll
     for (int j = 0; j < KT; ++j) wk[j] = __uint_as_float(q[j]);
     bv = bp ? __uint_as_float(((cptr)((uintptr_t)bp + (uintptr_t)c * 4u))[0]) : 0.f;
+  };
+  if constexpr (sizeof(T) == 4) {
+    fp32_params();
+  } else if (w32) {
+    fp32_params();
   } else {
     auto half = [](uint32_t d, uint32_t byte) {
       return to_f32(__builtin_bit_cast(T, (unsigned short)((byte & 2u) ? (d >> 16) : (d & 0xffffu))));
@@ -615,7 +647,7 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_xlane_kernel(DwArgs a) {
   const uint4 E = bload16<NTH ? 2 : 0>(rx, be >= 0 ? (uint32_t)be * 16u : kOOB, 0);
   const uint4 X = bload16(rx, lane < 2 && bx >= 0 ? (uint32_t)bx * 16u : kOOB, 0);
   float wk[KT], bv;
-  uniform_params<T, KT>(a.w, a.b, r0 - fdiv(r0, a.div_c) * a.C, wk, bv);
+  uniform_params<T, KT>(a.w, a.b, r0 - fdiv(r0, a.div_c) * a.C, wk, bv, a.w32);
   // lanes whose window reaches past a row edge need the zero-padding mask (uniform test)
   const bool edge = (int)t0 - a.pad < 0 || (int)(t0 + VEC * 63) - a.pad + WN > (int)a.L;
   xlane_dispatch<T, KT, NTH, SILU>(m, E, X, lane, edge, (int)t - a.pad, a.L, wk, bv, static_cast<T*>(a.y) + f);
@@ -958,35 +990,34 @@ int launch_dw_bwd_w(const DwBwdArgs& a, int64_t rows, int K, hipStream_t s) {
 // element is read before it is overwritten.  Latency-bound: B*D*(W+2) elements per step.
 template <typename T, bool SILU>
 __global__ __launch_bounds__(256) void causal_conv1d_update_kernel(const T* __restrict__ x, T* __restrict__ state,
-                                                                   const T* __restrict__ w,
-                                                                   const T* __restrict__ bias, T* __restrict__ y,
-                                                                   int64_t rows, uint32_t D, int W) {
+                                                                   const void* __restrict__ w,
+                                                                   const void* __restrict__ bias, T* __restrict__ y,
+                                                                   int64_t rows, uint32_t D, int W, bool w32) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // b * D + d
   if (i >= rows) return;
   const uint32_t d = (uint32_t)(i % D);
   T* st = state + i * W;
-  const T* wd = w + (int64_t)d * W;
-  float acc = bias ? to_f32(bias[d]) : 0.f;
+  const int64_t wd = (int64_t)d * W;
+  float acc = bias ? dw_param<T>(bias, w32, d) : 0.f;
   for (int j = 0; j + 1 < W; ++j) {
     const T v = st[j + 1];
     st[j] = v;
-    acc = fmaf(to_f32(wd[j]), to_f32(v), acc);
+    acc = fmaf(dw_param<T>(w, w32, wd + j), to_f32(v), acc);
   }
   const T v = x[i];
   st[W - 1] = v;
-  acc = fmaf(to_f32(wd[W - 1]), to_f32(v), acc);
+  acc = fmaf(dw_param<T>(w, w32, wd + W - 1), to_f32(v), acc);
   if constexpr (SILU) acc = silu_f32(acc);
   y[i] = from_f32<T>(acc);
 }
 
 template <typename T>
 int launch_update(const void* x, void* state, const void* w, const void* bias, void* y, int64_t rows, int64_t D,
-                  int W, int silu, hipStream_t s) {
+                  int W, int silu, bool w32, hipStream_t s) {
   const dim3 grid((unsigned)((rows + 255) / 256)), block(256);
   auto args = [&](auto kern) {
-    hipLaunchKernelGGL(kern, grid, block, 0, s, static_cast<const T*>(x), static_cast<T*>(state),
-                       static_cast<const T*>(w), static_cast<const T*>(bias), static_cast<T*>(y), rows,
-                       (uint32_t)D, W);
+    hipLaunchKernelGGL(kern, grid, block, 0, s, static_cast<const T*>(x), static_cast<T*>(state), w, bias,
+                       static_cast<T*>(y), rows, (uint32_t)D, W, w32);
   };
   if (silu) args(causal_conv1d_update_kernel<T, true>);
   else args(causal_conv1d_update_kernel<T, false>);
@@ -1127,10 +1158,14 @@ const char* dwconv1d_variant_name(int v) {
 
 extern "C" int atk_dwconv1d_fwd(const void* x, const void* w, const void* bias, void* y,
                                 int64_t N, int64_t C, int64_t L, int K, int pad_left,
-                                int64_t L_out, int dtype, int fuse_silu, int variant,
+                                int64_t L_out, int dtype, int w_dtype, int fuse_silu, int variant,
                                 atk_stream_t stream) {
   using namespace atk;
   if (!dtype_ok(dtype)) return fail(ATK_EINVAL, "dwconv1d: unknown dtype code %d", dtype);
+  if (w_dtype != dtype && w_dtype != ATK_F32)
+    return fail(ATK_EINVAL, "dwconv1d: weights must be in the input's dtype or fp32 (code %d)", w_dtype);
+  if (w_dtype == ATK_F32 && ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(bias)) & 3u))
+    return fail(ATK_EINVAL, "dwconv1d: misaligned fp32 weight or bias pointer");
   if (N < 0 || C <= 0 || L < 0 || L_out < 0) return fail(ATK_EINVAL, "dwconv1d: bad sizes");
   if (K < 1 || K > DW_KMAX) return fail(ATK_UNSUPPORTED, "dwconv1d: kernel width %d outside [1, %d]", K, DW_KMAX);
   if (pad_left < 0 || pad_left > DW_PADMAX) return fail(ATK_UNSUPPORTED, "dwconv1d: padding %d outside [0, %d]", pad_left, DW_PADMAX);
@@ -1153,6 +1188,7 @@ extern "C" int atk_dwconv1d_fwd(const void* x, const void* w, const void* bias, 
   a.x_off = (int)((xa & 15u) / es);
   a.y_off = (int)((ya & 15u) / es);
   a.silu = fuse_silu ? 1 : 0;
+  a.w32 = w_dtype == ATK_F32 && dtype != ATK_F32;
   a.div_lout = make_fastdiv((uint32_t)L_out);
   a.div_c = make_fastdiv((uint32_t)C);
   a.win_cap = 0;
@@ -1279,10 +1315,15 @@ extern "C" int atk_dwconv1d_bwd(const void* x, const void* dy, const void* w, vo
 }
 
 extern "C" int atk_causal_conv1d_update(const void* x, void* conv_state, const void* w, const void* bias, void* y,
-                                        int64_t B, int64_t D, int W, int dtype, int fuse_silu,
+                                        int64_t B, int64_t D, int W, int dtype, int w_dtype, int fuse_silu,
                                         atk_stream_t stream) {
   using namespace atk;
   if (!dtype_ok(dtype)) return fail(ATK_EINVAL, "causal_conv1d_update: unknown dtype code %d", dtype);
+  if (w_dtype != dtype && w_dtype != ATK_F32)
+    return fail(ATK_EINVAL, "causal_conv1d_update: weights must be in the input's dtype or fp32 (code %d)", w_dtype);
+  if (w_dtype == ATK_F32 && ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(bias)) & 3u))
+    return fail(ATK_EINVAL, "causal_conv1d_update: misaligned fp32 weight or bias pointer");
+  const bool w32 = w_dtype == ATK_F32 && dtype != ATK_F32;
   if (B < 0 || D <= 0) return fail(ATK_EINVAL, "causal_conv1d_update: bad sizes");
   if (W < 1 || W > DW_KMAX) return fail(ATK_UNSUPPORTED, "causal_conv1d_update: width %d outside [1, %d]", W, DW_KMAX);
   const int64_t rows = B * D;
@@ -1291,9 +1332,9 @@ extern "C" int atk_causal_conv1d_update(const void* x, void* conv_state, const v
   if (rows >= (1ll << 31) * 256ll) return fail(ATK_UNSUPPORTED, "causal_conv1d_update: too many rows");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (dtype) {
-    case ATK_F32: return launch_update<float>(x, conv_state, w, bias, y, rows, D, W, fuse_silu, s);
-    case ATK_F16: return launch_update<_Float16>(x, conv_state, w, bias, y, rows, D, W, fuse_silu, s);
-    default: return launch_update<__bf16>(x, conv_state, w, bias, y, rows, D, W, fuse_silu, s);
+    case ATK_F32: return launch_update<float>(x, conv_state, w, bias, y, rows, D, W, fuse_silu, w32, s);
+    case ATK_F16: return launch_update<_Float16>(x, conv_state, w, bias, y, rows, D, W, fuse_silu, w32, s);
+    default: return launch_update<__bf16>(x, conv_state, w, bias, y, rows, D, W, fuse_silu, w32, s);
   }
 }
 

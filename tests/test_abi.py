@@ -70,17 +70,23 @@ def test_variant_tables(nat):
 def test_argument_validation_codes(nat):
     lib = nat.lib()
     # dwconv1d
-    assert lib.atk_dwconv1d_fwd(None, None, None, None, 1, 1, 1, 3, 1, 1, 7, 0, 0, None) == nat.ATK_EINVAL
-    assert lib.atk_dwconv1d_fwd(None, None, None, None, 1, 4, 16, 65, 1, 16, 0, 0, 0, None) == nat.ATK_UNSUPPORTED
-    assert lib.atk_dwconv1d_fwd(None, None, None, None, 1, 4, 16, 3, 65, 16, 0, 0, 0, None) == nat.ATK_UNSUPPORTED
-    assert lib.atk_dwconv1d_fwd(None, None, None, None, 1, 4, 16, 3, 1, 16, 0, 0, 99, None) == nat.ATK_EINVAL
-    assert lib.atk_dwconv1d_fwd(None, None, None, None, 1, 4, 16, 3, 1, 16, 0, 0, 0, None) == nat.ATK_EINVAL
+    assert lib.atk_dwconv1d_fwd(None, None, None, None, 1, 1, 1, 3, 1, 1, 7, 7, 0, 0, None) == nat.ATK_EINVAL
+    assert lib.atk_dwconv1d_fwd(None, None, None, None, 1, 4, 16, 65, 1, 16, 0, 0, 0, 0, None) == nat.ATK_UNSUPPORTED
+    assert lib.atk_dwconv1d_fwd(None, None, None, None, 1, 4, 16, 3, 65, 16, 0, 0, 0, 0, None) == nat.ATK_UNSUPPORTED
+    assert lib.atk_dwconv1d_fwd(None, None, None, None, 1, 4, 16, 3, 1, 16, 0, 0, 0, 99, None) == nat.ATK_EINVAL
+    assert lib.atk_dwconv1d_fwd(None, None, None, None, 1, 4, 16, 3, 1, 16, 0, 0, 0, 0, None) == nat.ATK_EINVAL
     assert "null" in nat.last_error()
-    assert lib.atk_dwconv1d_fwd(None, None, None, None, 0, 4, 16, 3, 1, 16, 0, 0, 0, None) == nat.ATK_OK
+    assert lib.atk_dwconv1d_fwd(None, None, None, None, 0, 4, 16, 3, 1, 16, 0, 0, 0, 0, None) == nat.ATK_OK
+    # weights in neither the input's dtype nor fp32 (fp16 input, bf16 weights)
+    assert lib.atk_dwconv1d_fwd(None, None, None, None, 1, 4, 16, 3, 1, 16, nat.ATK_F16, nat.ATK_BF16, 0, 0,
+                                None) == nat.ATK_EINVAL
+    assert "fp32" in nat.last_error()
     # decode step
-    assert lib.atk_causal_conv1d_update(None, None, None, None, None, 2, 4, 4, 2, 0, None) == nat.ATK_EINVAL
-    assert lib.atk_causal_conv1d_update(None, None, None, None, None, 2, 4, 65, 2, 0, None) == nat.ATK_UNSUPPORTED
-    assert lib.atk_causal_conv1d_update(None, None, None, None, None, 0, 4, 4, 2, 0, None) == nat.ATK_OK
+    assert lib.atk_causal_conv1d_update(None, None, None, None, None, 2, 4, 4, 2, 2, 0, None) == nat.ATK_EINVAL
+    assert lib.atk_causal_conv1d_update(None, None, None, None, None, 2, 4, 65, 2, 2, 0, None) == nat.ATK_UNSUPPORTED
+    assert lib.atk_causal_conv1d_update(None, None, None, None, None, 0, 4, 4, 2, 2, 0, None) == nat.ATK_OK
+    assert lib.atk_causal_conv1d_update(None, None, None, None, None, 2, 4, 4, nat.ATK_BF16, nat.ATK_F16, 0,
+                                        None) == nat.ATK_EINVAL
     # dwconv1d backward (weight / bias gradients)
     assert lib.atk_dwconv1d_bwd_weight_workspace_bytes(2, 3, 4) == 2 * 3 * 5 * 4
     assert lib.atk_dwconv1d_bwd_weight_workspace_bytes(0, 3, 4) == 0

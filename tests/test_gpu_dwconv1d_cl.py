@@ -204,8 +204,9 @@ def test_causal_bcl_autograd(dtype, silu, L, K):
     y = causal_conv1d_fn(x, w, b, activation="silu" if silu else None)
     dy = torch.randn(y.shape, generator=g).to(dtype).cuda()
     y.backward(dy)
-    # the (B, C, L) kernel takes the weights and bias in x's dtype: the oracle gets the same
-    wq, bq = w.detach().to(dtype), b.detach().to(dtype)
+    # fp32 weights and bias are used unrounded (the reference dispatches the weight type
+    # separately): the oracle gets them as given
+    wq, bq = w.detach(), b.detach()
     ry, _ = O.causal_conv1d_states(x.detach(), wq, bq, silu=silu)
     _close(y, ry, dtype, "bcl out")
     dx, dw, db, _ = O.causal_conv1d_states_bwd(x.detach(), wq, bq, dy, silu=silu)
@@ -292,3 +293,52 @@ def test_causal_bcl_fused_backward_full_size():
     assert O.max_rel_err(dw, dw_ref) <= 1e-4 and O.max_rel_err(db, db_ref) <= 1e-4
     del x, dy, dx, dx_ref
     torch.cuda.empty_cache()
+
+
+# The (B, C, L) causal path and the decode step use fp32 weights unrounded, as the
+# reference does (causal_conv1d.cpp:139-141, 437).  A cancellation makes rounding visible:
+# with w = (1 + 2^-12, -1) on all-ones input, y = 2^-12 exactly (representable in fp16 and
+# bf16), while weights rounded to fp16 / bf16 (1 + 2^-12 -> 1) would give 0.
+EPS_W = 2.0 ** -12
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+@pytest.mark.parametrize("L", [64, 300])
+def test_causal_bcl_fp32_weights_are_not_rounded(dtype, L):
+    from amd_tuned_torch.causal_conv1d import causal_conv1d_fn
+    B, D, K = 2, 8, 2
+    x = torch.ones(B, D, L, dtype=dtype, device="cuda", requires_grad=True)
+    w = torch.tensor([1.0 + EPS_W, -1.0], dtype=torch.float32).repeat(D, 1).cuda().requires_grad_()
+    y = causal_conv1d_fn(x, w)
+    ry, _ = O.causal_conv1d_states(x.detach(), w.detach())
+    assert ry[0, 0, 1] == EPS_W and ry[0, 0, 0] == -1.0
+    assert torch.equal(y.detach().double().cpu(), torch.from_numpy(ry)), "forward used rounded weights"
+    # backward: dx of the same cancellation (L = 300 takes the composed fallback)
+    dy = torch.ones(B, D, L, dtype=dtype, device="cuda")
+    y.backward(dy)
+    rdx, rdw, _, _ = O.causal_conv1d_states_bwd(x.detach(), w.detach(), None, dy)
+    assert torch.equal(x.grad.double().cpu(), torch.from_numpy(rdx)), "backward used rounded weights"
+    _grad_close(w.grad, rdw, "dweight")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+def test_causal_conv1d_update_fp32_weights_are_not_rounded(dtype):
+    from amd_tuned_torch import causal_conv1d as cc
+    B, D, W = 3, 16, 2
+    x = torch.ones(B, D, dtype=dtype, device="cuda")
+    st = torch.ones(B, D, W, dtype=dtype, device="cuda")
+    w = torch.tensor([1.0 + EPS_W, -1.0], dtype=torch.float32).repeat(D, 1).cuda()
+    b = torch.zeros(D, dtype=torch.float32, device="cuda")
+    y = cc.causal_conv1d_update(x, st, w, b)
+    assert torch.all(y.double().cpu() == EPS_W), "decode step used rounded weights"
+    # and on random data it matches the float64 oracle with the fp32 weights as given
+    g = torch.Generator().manual_seed(99)
+    x2 = torch.randn(B, D, generator=g).to(dtype)
+    st2 = torch.randn(B, D, 4, generator=g).to(dtype)
+    w2 = torch.randn(D, 4, generator=g) * 0.5
+    b2 = 0.1 * torch.randn(D, generator=g)
+    sd = st2.cuda()
+    y2 = cc.causal_conv1d_update(x2.cuda(), sd, w2.cuda(), b2.cuda(), activation="silu")
+    ry, rs = O.causal_conv1d_update(x2, st2, w2, b2, True)
+    assert O.max_rel_err(y2.cpu(), ry) <= BAR[dtype]
+    assert torch.equal(sd.cpu().double(), torch.from_numpy(rs))
