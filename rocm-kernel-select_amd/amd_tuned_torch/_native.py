@@ -217,6 +217,24 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
+# Size queries (packed-weight bytes, workspace bytes) depend only on the shape, dtype,
+# variant and device (the split-K plan reads the device's CU count), so each is asked of the
+# library once: a ctypes call with twenty integer arguments costs a few microseconds of host
+# time, about as long as a small kernel.
+_size_cache: dict = {}
+
+
+def _cached_size(fn, *args, device: int = -1) -> int:
+    key = (fn.__name__, device, args)
+    hit = _size_cache.get(key)
+    if hit is None:
+        hit = int(fn(*args))
+        if len(_size_cache) > 4096:
+            _size_cache.clear()
+        _size_cache[key] = hit
+    return hit
+
+
 def _require_cuda(*tensors) -> None:
     for t in tensors:
         if t is not None and not t.is_cuda:
@@ -241,11 +259,13 @@ def _device_index(device: torch.device) -> int:
     return device.index if device.index is not None else torch.cuda.current_device()
 
 
-def workspace(device: torch.device, purpose: str, nbytes: int) -> torch.Tensor:
+def workspace(device: torch.device, purpose: str, nbytes: int, stream=None) -> torch.Tensor:
     """A zero-initialised uint8 buffer of at least `nbytes` for `purpose`, private to the
-    current stream of `device`.  The zeroing (torch's fill kernel, ordered on that stream)
-    happens only when a buffer is created; kernels that need zeroed scratch leave it zero."""
-    stream = torch.cuda.current_stream(device)
+    current stream of `device` (or to `stream`, which must be that stream).  The zeroing
+    (torch's fill kernel, ordered on that stream) happens only when a buffer is created;
+    kernels that need zeroed scratch leave it zero."""
+    if stream is None:
+        stream = torch.cuda.current_stream(device)
     key = (_device_index(device), stream.cuda_stream, purpose)
     with _ws_lock:
         buf = _ws_live.get(key)
@@ -681,13 +701,16 @@ def group_norm(input: torch.Tensor, num_groups: int, weight: Optional[torch.Tens
     L = lib()
     dt = _DTYPE_CODE[input.dtype]
     v = int(variant)
-    nbytes = L.atk_group_norm_workspace_bytes(N, C, S, G, dt, v)
+    nbytes = _cached_size(L.atk_group_norm_workspace_bytes, N, C, S, G, dt, v)
     if nbytes == 0:
+        _size_cache.pop(("atk_group_norm_workspace_bytes", -1, (N, C, S, G, dt, v)), None)
+        L.atk_group_norm_workspace_bytes(N, C, S, G, dt, v)  # sets the reason
         raise RuntimeError(f"group_norm: {last_error()}")
-    ws = workspace(input.device, "group_norm", nbytes)
+    stream = torch.cuda.current_stream(input.device)
+    ws = workspace(input.device, "group_norm", nbytes, stream)
     rc = L.atk_group_norm_fwd(_ptr(input), _ptr(weight), _ptr(bias), _ptr(y), N, C, S, G,
                               float(eps), int(bool(silu)), dt, pdt, v, ws.data_ptr(), ws.numel(),
-                              _stream(input))
+                              stream.cuda_stream)
     _check(rc, "group_norm")
     return y
 
@@ -948,16 +971,19 @@ def _conv(input, weight, bias, stride, padding, dilation, nd: int, variant: int,
     L = lib()
     dt = _DTYPE_CODE[input.dtype]
     geom = (N, Ci, D, H, W, Co, KD, KH, KW, *s, *p, *d)
-    packed_bytes = L.atk_conv_packed_weight_bytes(*geom, dt, int(variant)) if variant > 0 else 0
+    dev = _device_index(input.device)
+    packed_bytes = _cached_size(L.atk_conv_packed_weight_bytes, *geom, dt, int(variant), device=dev) \
+        if variant > 0 else 0
     if extras and not packed_bytes:
         raise Unsupported(f"conv{nd}d: the residual / GroupNorm epilogue needs an MFMA variant that takes the shape")
     if packed_bytes:
         # an MFMA variant that takes the shape: packed weights from the cache, the workspace
         # only for split-K partials
-        stream = _stream(input)
+        stream_obj = torch.cuda.current_stream(input.device)
+        stream = stream_obj.cuda_stream
         packed = _packed_conv_weights(weight, geom, dt, int(variant), packed_bytes, stream)
-        nws = L.atk_conv_prepacked_workspace_bytes(*geom, dt, int(variant))
-        ws = workspace(input.device, "conv", nws) if nws else None
+        nws = _cached_size(L.atk_conv_prepacked_workspace_bytes, *geom, dt, int(variant), device=dev)
+        ws = workspace(input.device, "conv", nws, stream_obj) if nws else None
         if not extras:
             rc = L.atk_conv_fwd_prepacked(_ptr(input), _ptr(packed), packed_bytes, _ptr(bias), _ptr(y), *geom, dt,
                                           int(variant), _ptr(ws), ws.numel() if ws is not None else 0, stream)
@@ -976,7 +1002,7 @@ def _conv(input, weight, bias, stride, padding, dilation, nd: int, variant: int,
                                          ws.numel() if ws is not None else 0, stream)
         _check(rc, f"conv{nd}d")
         return (y, stats, nrec) if gn_groups > 0 else y
-    nbytes = L.atk_conv_workspace_bytes(*geom, dt, int(variant))
+    nbytes = _cached_size(L.atk_conv_workspace_bytes, *geom, dt, int(variant), device=dev)
     ws_ptr, ws_len = None, 0
     if nbytes:
         ws = workspace(input.device, "conv", nbytes)
