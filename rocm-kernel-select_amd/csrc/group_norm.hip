@@ -448,13 +448,24 @@ void gn_resident_kernel(GnArgs a) {
 // Lane l takes records l, l+64, ...; up to 64 * RC of them are read once and kept in registers
 // for the second sum.  The xor-butterfly sums give every lane (and every workgroup merging the
 // same records) bit-identical statistics.
+constexpr int GN_MERGE_RC = 8;  // records per lane held in registers by wave_merge_counted
+
+// The first 64 * GN_MERGE_RC records of a group, lane l holding l, l+64, ...: loaded by the
+// caller before anything else it waits for less urgently (vector-memory loads complete in
+// issue order, so records loaded after x would wait for x).
 template <typename GetRec>
-__device__ __forceinline__ void wave_merge_counted(int NP, GetRec rec, float& mean, float& var) {
-  constexpr int RC = 8;
+__device__ __forceinline__ void load_records(int NP, GetRec rec, float4 (&r)[GN_MERGE_RC]) {
   const int lane = threadIdx.x & 63;
-  float4 r[RC];
 #pragma unroll
-  for (int k = 0; k < RC; ++k) r[k] = lane + 64 * k < NP ? rec(lane + 64 * k) : make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int k = 0; k < GN_MERGE_RC; ++k)
+    r[k] = lane + 64 * k < NP ? rec(lane + 64 * k) : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+template <typename GetRec>
+__device__ __forceinline__ void wave_merge_counted(int NP, GetRec rec, const float4 (&r)[GN_MERGE_RC], float& mean,
+                                                   float& var) {
+  constexpr int RC = GN_MERGE_RC;
+  const int lane = threadIdx.x & 63;
   float sn = 0.f, sm = 0.f;
 #pragma unroll
   for (int k = 0; k < RC; ++k) {
@@ -525,6 +536,10 @@ void gn_split_apply_kernel(GnArgs a) {
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(xg, (uint32_t)(E * (int64_t)sizeof(T)));
   const uint32_t lane_off = (uint32_t)tid * 16u;
   const uint32_t n_vec = (uint32_t)((E - s0 + VEC - 1) / VEC);
+  // the group's records first: merged while x is still arriving
+  const float4* rp = a.parts + gi * a.NP;
+  float4 rec[GN_MERGE_RC];
+  if (tid < 64) load_records(a.NP, [&](int i) { return rp[i]; }, rec);
   Vec16<T> buf[EPV];
 #pragma unroll
   for (int i = 0; i < EPV; ++i)  // last read of x: nontemporal
@@ -544,9 +559,8 @@ void gn_split_apply_kernel(GnArgs a) {
   const uint32_t gword = param_word(a.gamma, a.pdt, cme, nchan, gsel);
   const uint32_t bword = param_word(a.beta, a.pdt, cme, nchan, bsel);
   if (tid < 64) {
-    const float4* rp = a.parts + gi * a.NP;
     float mean, var;
-    wave_merge_counted(a.NP, [&](int i) { return rp[i]; }, mean, var);
+    wave_merge_counted(a.NP, [&](int i) { return rp[i]; }, rec, mean, var);
     if (tid == 0) {
       s_stat[0] = mean;
       s_stat[1] = 1.0f / sqrtf(var + a.eps);
