@@ -1161,7 +1161,7 @@ def summarize_stats(stats_dir: str, out_path: str, command: str, top: int = 25, 
     for r in rows[:top]:
         lines.append(f"  {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:10.2f} "
                      f"{float(r['MinNs']) / 1e3:10.2f} {float(r['MaxNs']) / 1e3:10.2f} "
-                     f"{float(r['Percentage']):6.2f}  {r['Name'][:150]}")
+                     f"{float(r['Percentage']):6.2f}  {r['Name'].replace('_ZN3atk12_GLOBAL__N_1', '')[:110]}")
     with open(out_path, "w") as f:
         f.write("\n".join(lines) + "\n")
     print("\n".join(lines))
