@@ -15,8 +15,12 @@
 //  * A workgroup = 4 waves = 128 output channels x 32 input channels x one kz; each wave
 //    holds 3x3 accumulator tiles (144 fp32 registers) for its 32 output channels.
 //  * The position range is split into chunks of (n, z) output planes across workgroups;
-//    each writes fp32 partials in the final weight layout, summed in a fixed order by a
-//    reduce kernel (deterministic).
+//    each writes its fp32 partials in the accumulator layout of its waves (one 1 KB run per
+//    store instruction), summed in a fixed order by a reduce kernel (deterministic) that
+//    turns them into the weight layout through LDS.  Partials written straight in the
+//    weight layout cost more than all the MFMAs: each 128-byte line of that layout holds
+//    the taps of all kz, so three workgroups (often on different XCDs, with separate L2s)
+//    each write a few 4-byte pieces of it.
 // The next stage's input rows are loaded into registers while the current stage computes.
 #include <algorithm>
 
@@ -39,14 +43,16 @@ constexpr int WG_PAD = 8;    // zero elements left / right of each staged row
 constexpr int WG_MAXW = 64;  // staging map: 32 ci x 6 rows x W / 8 chunks over 256 threads x 6 loads
 constexpr int WG_LD = 6;     // 16-byte staging loads per thread
 constexpr int WG_PF = 4;     // dy fragments in flight per lane
+constexpr int WG_UNIT = 9 * 16 * 64;  // partial floats of one wave: 9 taps x 16 registers x 64 lanes
+constexpr int WG_RNT = 288;  // reduce workgroup: 9 taps x 32 input channels
 
 struct WgArgs {
   const void* x;
   const void* dy;
-  float* part;                 // [chunks][Co][Ci][KD*9]
+  float* part;                 // [chunks][kz][Co/128][Ci/32][wave][tap 9][reg quad 4][lane 64][4]
   float* dw;                   // [Co][Ci][KD*9]
   int N, Ci, Co, D, H, W, KD, pd;
-  int planes_per_chunk, chunks;
+  int stages_per_chunk, chunks;  // a chunk is a run of (n, z, 4-row) stages
   int pitch;                   // staged row pitch in elements (W + 2*PAD)
   int slab;                    // elements per input channel in LDS (R * pitch, bank padded)
   int chunks16;                // 16-byte chunks per staged stage = WG_CI * R * W / 8
@@ -70,10 +76,16 @@ __global__ __launch_bounds__(WG_NT, 2) void conv_wgrad_kernel(WgArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 31, half = lane >> 5;
   const int n_ci = a.Ci / WG_CI;
-  const int ci_base = (blockIdx.x % n_ci) * WG_CI;
-  const int co_base = (blockIdx.x / n_ci) * WG_CO + wave * 32;
-  const int kz = blockIdx.y;
-  const int chunk = blockIdx.z;
+  // Consecutive workgroup ids are dispatched to the 8 XCDs in turn.  Each XCD gets a
+  // contiguous run of logical tiles instead, so the input-channel blocks that read the same
+  // dy rows (and the output-channel blocks that read the same input rows) share one L2.
+  const int gx = gridDim.x, gy = gridDim.y;
+  const int nwg = gx * gy * gridDim.z;
+  int lid = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+  if ((nwg & 7) == 0) lid = (lid & 7) * (nwg >> 3) + (lid >> 3);
+  const int bx = lid % gx, kz = (lid / gx) % gy, chunk = lid / (gx * gy);
+  const int ci_base = (bx % n_ci) * WG_CI;
+  const int co_base = (bx / n_ci) * WG_CO + wave * 32;
   const int HW = a.H * a.W;
   const int64_t plane_x = (int64_t)a.D * HW;  // elements per (n, channel) volume
 
@@ -120,17 +132,14 @@ __global__ __launch_bounds__(WG_NT, 2) void conv_wgrad_kernel(WgArgs a) {
     }
   };
 
-  const int total_planes = a.N * a.D;
-  const int p_begin = chunk * a.planes_per_chunk;
-  const int p_end = min(p_begin + a.planes_per_chunk, total_planes);
   const int n_ystages = (a.H + WG_TY - 1) / WG_TY;
   const int ksteps_row = a.W >> 4;
   // LDS read base of this lane: input channel `col`, first 8 output positions of its half
   const T* s_lane = s_x + col * a.slab + half * 8;
 
   uint4 buf[WG_LD];
-  int st = p_begin * n_ystages;
-  const int st_end = p_end * n_ystages;
+  int st = chunk * a.stages_per_chunk;
+  const int st_end = min(st + a.stages_per_chunk, a.N * a.D * n_ystages);
   if (st < st_end) {
     const int pl = st / n_ystages, ys = st - (st / n_ystages) * n_ystages;
     stage_load(pl / a.D, pl % a.D + kz - a.pd, ys * WG_TY, buf);
@@ -142,21 +151,24 @@ __global__ __launch_bounds__(WG_NT, 2) void conv_wgrad_kernel(WgArgs a) {
     __syncthreads();  // previous stage's reads done
     stage_store(buf);
     __syncthreads();
-    if (st + 1 < st_end) {
-      const int pl2 = (st + 1) / n_ystages, ys2 = (st + 1) - pl2 * n_ystages;
-      stage_load(pl2 / a.D, pl2 % a.D + kz - a.pd, ys2 * WG_TY, buf);
-    }
     const int zi = z + kz - a.pd;
-    if (zi < 0 || zi >= a.D) continue;  // this kz tap reads only zero padding here (uniform)
+    const bool live = zi >= 0 && zi < a.D;  // else this kz tap reads only zero padding (uniform)
     // a stage covers whole output rows, so k-step ks (16 positions) starts at position
     // y0*W + ks*16 of the plane: the dy offset is linear in ks
     const uint32_t g0 = (uint32_t)((((int64_t)n * a.Co + co_base + col) * plane_x + (int64_t)z * HW +
                                     (int64_t)y0 * a.W + half * 8) * (int64_t)sizeof(T));
     const int rows = min(WG_TY, a.H - y0);
-    const int nk = rows * ksteps_row;
+    const int nk = live ? rows * ksteps_row : 0;
     uint4 ar[WG_PF];  // dy fragments stream through a ring, WG_PF k-steps ahead
 #pragma unroll
     for (int u = 0; u < WG_PF; ++u) ar[u] = bload16(rg, u < nk ? g0 + (uint32_t)u * 32u : kOOB, 0);
+    // the next stage's input rows are requested after this stage's first dy fragments: load
+    // counters complete in issue order, so the first MFMAs do not wait for the input rows
+    if (st + 1 < st_end) {
+      const int pl2 = (st + 1) / n_ystages, ys2 = (st + 1) - pl2 * n_ystages;
+      stage_load(pl2 / a.D, pl2 % a.D + kz - a.pd, ys2 * WG_TY, buf);
+    }
+    if (!live) continue;
     int xs = 0;                   // 16-position column block of the current k-step
     const T* prow = s_lane + WG_PAD;  // staged row ty (+ ky below) of the current k-step
     for (int ks0 = 0; ks0 < nk; ks0 += WG_PF) {
@@ -198,32 +210,68 @@ __global__ __launch_bounds__(WG_NT, 2) void conv_wgrad_kernel(WgArgs a) {
     }
   }
 
-  // partials in the weight layout: part[chunk][co][ci][kz*9 + ky*3 + kx]
-  const int taps = a.KD * 9;
+  // partials in the accumulator layout: one float4 (4 consecutive accumulator registers)
+  // per lane, so a store instruction writes 1 KB contiguous
+  const int n_ci_blk = a.Ci / WG_CI;
+  const int64_t unit = ((int64_t)kz * (a.Co / WG_CO) + bx / n_ci_blk) * n_ci_blk + bx % n_ci_blk;
+  float* dst = a.part + (int64_t)chunk * a.Co * a.Ci * a.KD * 9 + (unit * 4 + wave) * WG_UNIT + lane * 4;
 #pragma unroll
   for (int ky = 0; ky < 3; ++ky)
 #pragma unroll
     for (int kx = 0; kx < 3; ++kx)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int co = co_base + (r >> 2) * 8 + half * 4 + (r & 3);
-        const int ci = ci_base + col;
-        a.part[(((int64_t)chunk * a.Co + co) * a.Ci + ci) * taps + kz * 9 + ky * 3 + kx] = acc[ky][kx][r];
-      }
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<float4*>(dst + ((ky * 3 + kx) * 4 + q) * 256) =
+            make_float4(acc[ky][kx][4 * q], acc[ky][kx][4 * q + 1], acc[ky][kx][4 * q + 2], acc[ky][kx][4 * q + 3]);
 }
 
-__global__ __launch_bounds__(256) void conv_wgrad_reduce_kernel(WgArgs a) {
-  const int64_t total = (int64_t)a.Co * a.Ci * a.KD * 9;
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= total) return;
-  float s0 = 0.f, s1 = 0.f;
-  int c = 0;
-  for (; c + 2 <= a.chunks; c += 2) {
-    s0 += a.part[(int64_t)c * total + i];
-    s1 += a.part[(int64_t)(c + 1) * total + i];
+// Sums the chunks' partials in a fixed order and writes dW.  In a wave's accumulator,
+// register r = 4 q + e of lane (half, col) holds output channel 8 q + 4 half + e and input
+// channel col, so a (wave, q, half) slice is 4 consecutive output channels x 32 input
+// channels: a workgroup takes one such slice over every kz and tap, sums it into LDS as
+// [co 4][ci 32][kz][tap] -- 4 contiguous runs of dW -- and writes those with float4 stores.
+template <int KD>
+__global__ __launch_bounds__(WG_RNT) void conv_wgrad_reduce_kernel(WgArgs a) {
+  __shared__ __align__(16) float s_w[4 * WG_CI * KD * 9];
+  constexpr int ROW = WG_CI * KD * 9;  // floats of one output channel's run in dW
+  const int t = threadIdx.x;
+  const int n_ci_blk = a.Ci / WG_CI, n_co_blk = a.Co / WG_CO;
+  const int half = blockIdx.x & 1, q = (blockIdx.x >> 1) & 3, wave = (blockIdx.x >> 3) & 3;
+  const int tile = blockIdx.x >> 5;
+  const int co_blk = tile / n_ci_blk, ci_blk = tile - co_blk * n_ci_blk;
+  const int64_t total = (int64_t)a.Co * a.Ci * KD * 9;
+  const int tap = t >> 5, col = t & 31;
+  const int64_t lane_off = (((int64_t)tap * 4 + q) * 64 + half * 32 + col) * 4;
+#pragma unroll
+  for (int kz = 0; kz < KD; ++kz) {
+    const int64_t unit = ((int64_t)kz * n_co_blk + co_blk) * n_ci_blk + ci_blk;
+    const float* src = a.part + (unit * 4 + wave) * WG_UNIT + lane_off;
+    float4 s0 = make_float4(0.f, 0.f, 0.f, 0.f), s1 = s0;
+    int c = 0;
+    for (; c + 2 <= a.chunks; c += 2) {
+      const float4 v0 = *reinterpret_cast<const float4*>(src + c * total);
+      const float4 v1 = *reinterpret_cast<const float4*>(src + (c + 1) * total);
+      s0.x += v0.x; s0.y += v0.y; s0.z += v0.z; s0.w += v0.w;
+      s1.x += v1.x; s1.y += v1.y; s1.z += v1.z; s1.w += v1.w;
+    }
+    if (c < a.chunks) {
+      const float4 v0 = *reinterpret_cast<const float4*>(src + c * total);
+      s0.x += v0.x; s0.y += v0.y; s0.z += v0.z; s0.w += v0.w;
+    }
+    float* d = s_w + col * (KD * 9) + kz * 9 + tap;
+    d[0] = s0.x + s1.x;
+    d[ROW] = s0.y + s1.y;
+    d[2 * ROW] = s0.z + s1.z;
+    d[3 * ROW] = s0.w + s1.w;
   }
-  if (c < a.chunks) s0 += a.part[(int64_t)c * total + i];
-  a.dw[i] = s0 + s1;
+  __syncthreads();
+  float* out = a.dw + ((int64_t)(co_blk * WG_CO + wave * 32 + q * 8 + half * 4) * a.Ci + ci_blk * WG_CI) * (KD * 9);
+#pragma unroll
+  for (int i = t; i < ROW; i += WG_RNT) {  // 4 rows of ROW / 4 float4s
+    const int row = i / (ROW / 4), v = i - row * (ROW / 4);
+    *reinterpret_cast<float4*>(out + (int64_t)row * a.Ci * (KD * 9) + v * 4) =
+        *reinterpret_cast<const float4*>(s_w + row * ROW + v * 4);
+  }
 }
 
 int wgrad_plan(int64_t N, int64_t Ci, int64_t Co, int64_t D, int64_t H, int64_t W, int KD, WgArgs* a) {
@@ -235,12 +283,14 @@ int wgrad_plan(int64_t N, int64_t Ci, int64_t Co, int64_t D, int64_t H, int64_t 
   a->slab = slab;
   a->chunks16 = (int)(WG_CI * WG_R * (W / 8));
   const int64_t groups = std::max<int64_t>(1, (Ci / WG_CI) * (Co / WG_CO) * KD);
-  const int64_t planes = N * D;
-  int64_t chunks = (512 + groups - 1) / groups;
-  if (chunks > planes) chunks = planes;
-  if (chunks < 1) chunks = 1;
-  a->planes_per_chunk = (int)((planes + chunks - 1) / chunks);
-  a->chunks = (int)((planes + a->planes_per_chunk - 1) / a->planes_per_chunk);
+  // as many chunks as keep the grid within one round of 512 resident workgroups (2 per CU):
+  // a grid just over a multiple of 512 leaves most CUs idle for its last round.  A chunk
+  // spans at least 4 stages, so a workgroup's partials (128 x 32 x 9 floats, 147 KB) stay
+  // below half of what it reads (88 KB of input and dy rows per stage at W = 64).
+  const int64_t stages = N * D * ((H + WG_TY - 1) / WG_TY);
+  int64_t chunks = std::max<int64_t>(1, std::min<int64_t>(512 / groups, stages / 4));
+  a->stages_per_chunk = (int)((stages + chunks - 1) / chunks);
+  a->chunks = (int)((stages + a->stages_per_chunk - 1) / a->stages_per_chunk);
   return ATK_OK;
 }
 
@@ -267,7 +317,7 @@ extern "C" int atk_conv_wgrad(const void* x, const void* dy, float* dw, int64_t 
   if (KD != 1 && KD != 3) return fail(ATK_UNSUPPORTED, "conv_wgrad: kernel depth 1 or 3");
   if (Ci % WG_CI || Co % WG_CO || W % 16 || W > WG_MAXW)
     return fail(ATK_UNSUPPORTED, "conv_wgrad: needs Ci %% 32, Co %% 128, W %% 16 == 0 and W <= 64");
-  if (!aligned16(x) || !aligned16(dy)) return fail(ATK_UNSUPPORTED, "conv_wgrad: 16-byte aligned tensors");
+  if (!aligned16(x) || !aligned16(dy) || !aligned16(dw)) return fail(ATK_UNSUPPORTED, "conv_wgrad: 16-byte aligned tensors");
   const int64_t xe = N * Ci * D * H * W, ge = N * Co * D * H * W;
   if (xe * 2 >= ((int64_t)1 << 31) || ge * 2 >= ((int64_t)1 << 31))
     return fail(ATK_UNSUPPORTED, "conv_wgrad: tensors over 2 GiB");
@@ -289,7 +339,8 @@ extern "C" int atk_conv_wgrad(const void* x, const void* dy, float* dw, int64_t 
   else hipLaunchKernelGGL((conv_wgrad_kernel<_Float16>), grid, dim3(WG_NT), lds, s, a);
   int rc = check_launch("conv_wgrad_kernel");
   if (rc != ATK_OK) return rc;
-  const int64_t total = Co * Ci * KD * 9;
-  hipLaunchKernelGGL(conv_wgrad_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a);
+  const dim3 rgrid((unsigned)((Co / WG_CO) * (Ci / WG_CI) * 32));
+  if (KD == 3) hipLaunchKernelGGL(conv_wgrad_reduce_kernel<3>, rgrid, dim3(WG_RNT), 0, s, a);
+  else hipLaunchKernelGGL(conv_wgrad_reduce_kernel<1>, rgrid, dim3(WG_RNT), 0, s, a);
   return check_launch("conv_wgrad_reduce_kernel");
 }

@@ -319,6 +319,8 @@ WGRAD_CASES = [
     (2, 64, 128, 3, 5, 32, 3),     # H not a multiple of the 4-row stage
     (1, 32, 256, 1, 8, 64, 1),     # conv2d form
     (2, 32, 128, 2, 4, 48, 3),
+    (2, 64, 256, 8, 20, 16, 3),    # 240 workgroups (XCD remap), chunks of 4 stages crossing planes
+    (16, 32, 128, 1, 16, 64, 1),   # conv2d form, 16 chunks of 4 stages (XCD remap)
 ]
 
 
