@@ -885,13 +885,15 @@ int validate_gn(int64_t N, int64_t C, int64_t S, int G, int dtype, int variant) 
 //   g = gamma_c * dy,  x_hat = (x - mu) * rstd,
 //   dx = rstd * (g - mean_group(g) - x_hat * mean_group(g * x_hat)),
 //   dgamma_c = sum_{n,s} dy * x_hat,  dbeta_c = sum_{n,s} dy.
-// Three kernels, 5 tensor-passes of HBM traffic (x and dy read twice, dx written once):
+// Two kernels, 5 tensor-passes of HBM traffic (x and dy read twice, dx written once):
 //   rows:     one workgroup per (n, c) row: x's mean / M2 about a row-wide shift K (the
 //             row's first element), A = sum dy, B = sum dy * (x - K);
 //   apply:    one workgroup per row: one wave merges the group's rows (Chan, fixed order, so
-//             every row of a group derives the same statistics), then dx; also the row's
-//             dgamma term rstd * sum dy * (x - mu) = rstd * (B + (K - mu) * A);
-//   finalize: dgamma / dbeta summed over n in order.
+//             every row of a group derives the same statistics), then dx.  The workgroups
+//             of n = 0 then also sum channel c's parameter gradients over n in a fixed
+//             order, from the rows alone: dgamma_c = sum_n rstd_n * (B + (K - mu_n) * A),
+//             dbeta_c = sum_n A.  They are dispatched first, so this tail hides behind
+//             the later rows' work (a separate kernel cost a launch gap).
 // Requires S % VEC == 0 and 16-byte aligned x / dy / dx (host check).
 struct GnBwdArgs {
   const void* x;
@@ -899,7 +901,6 @@ struct GnBwdArgs {
   const void* gamma;
   void* dx;           // may be null (parameter gradients only)
   float* rows;        // [N*C][5]: mean, M2, A, B, K
-  float* dg_part;     // [N*C]
   float* dgamma;      // [C] or null
   float* dbeta;       // [C] or null
   int64_t S;
@@ -978,6 +979,22 @@ __global__ __launch_bounds__(GN_TP_NT) void gn_bwd_rows_kernel(GnBwdArgs a) {
   }
 }
 
+// mean and rstd of group (rows rg[0 .. cpg)) from its rows' (mean, M2): call with all 64
+// lanes of a wave; every lane gets the same values (fixed-order butterfly sums)
+__device__ __forceinline__ void gn_bwd_group_stats(const GnBwdArgs& a, const float* rg, int lane, float& mu,
+                                                   float& rstd) {
+  float sm = 0.f;
+  for (uint32_t j = lane; j < a.cpg; j += 64) sm += rg[j * 5];
+  mu = wave_sum(sm) / (float)a.cpg;  // equal row sizes
+  float m2 = 0.f;
+  for (uint32_t j = lane; j < a.cpg; j += 64) {
+    const float dm = rg[j * 5] - mu;
+    m2 += rg[j * 5 + 1] + (float)a.S * dm * dm;
+  }
+  m2 = wave_sum(m2);
+  rstd = 1.0f / sqrtf(m2 / (float)((int64_t)a.cpg * a.S) + a.eps);
+}
+
 template <typename T, int U>
 __global__ __launch_bounds__(GN_TP_NT) void gn_bwd_apply_kernel(GnBwdArgs a) {
   constexpr int VEC = 16 / sizeof(T);
@@ -1009,63 +1026,72 @@ __global__ __launch_bounds__(GN_TP_NT) void gn_bwd_apply_kernel(GnBwdArgs a) {
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
     const float* rows = a.rows + r0 * 5;
-    float sm = 0.f;
-    for (uint32_t j = lane; j < a.cpg; j += 64) sm += rows[j * 5];
-    const float mu = wave_sum(sm) / (float)a.cpg;  // equal row sizes
-    float m2 = 0.f, sg = 0.f, sgx = 0.f;
+    float mu, rstd;
+    gn_bwd_group_stats(a, rows, lane, mu, rstd);
+    float sg = 0.f, sgx = 0.f;
     for (uint32_t j = lane; j < a.cpg; j += 64) {
       const float* o = rows + j * 5;
-      const float dm = o[0] - mu;
-      m2 += o[1] + (float)a.S * dm * dm;
       const float gam = a.gamma ? load_param(a.gamma, a.pdt, g0 + j) : 1.f;
       sg = fmaf(gam, o[2], sg);
       sgx = fmaf(gam, o[3] + (o[4] - mu) * o[2], sgx);
     }
-    m2 = wave_sum(m2);
     sg = wave_sum(sg);
     sgx = wave_sum(sgx);
     if (lane == 0) {
-      const float rstd = 1.0f / sqrtf(m2 / E + a.eps);
-      const float* o = a.rows + r * 5;
       st[0] = mu;
       st[1] = rstd;
       st[2] = sg / E;
       st[3] = rstd * sgx / E;
       st[4] = a.gamma ? load_param(a.gamma, a.pdt, c) : 1.f;
-      a.dg_part[r] = rstd * (o[3] + (o[4] - mu) * o[2]);
     }
   }
   __syncthreads();
-  if (!a.dx) return;
-  const float mu = st[0], rstd = st[1], c1 = st[2], c2 = st[3], gam = st[4];
-  T* __restrict__ dxr = static_cast<T*>(a.dx) + r * a.S;
-  for (int64_t e0 = e_first; e0 < a.S; e0 += (int64_t)GN_TP_NT * VEC * U) {
-    if (e0 != e_first) issue(e0);
+  if (a.dx) {
+    const float mu = st[0], rstd = st[1], c1 = st[2], c2 = st[3], gam = st[4];
+    T* __restrict__ dxr = static_cast<T*>(a.dx) + r * a.S;
+    for (int64_t e0 = e_first; e0 < a.S; e0 += (int64_t)GN_TP_NT * VEC * U) {
+      if (e0 != e_first) issue(e0);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t e = e0 + (int64_t)u * GN_TP_NT * VEC;
-      float o[VEC];
+      for (int u = 0; u < U; ++u) {
+        const int64_t e = e0 + (int64_t)u * GN_TP_NT * VEC;
+        float o[VEC];
 #pragma unroll
-      for (int k = 0; k < VEC; ++k) {
-        const float xh = (to_f32(xv[u].e[k]) - mu) * rstd;
-        o[k] = rstd * (fmaf(gam, to_f32(gv[u].e[k]), -c1) - xh * c2);
+        for (int k = 0; k < VEC; ++k) {
+          const float xh = (to_f32(xv[u].e[k]) - mu) * rstd;
+          o[k] = rstd * (fmaf(gam, to_f32(gv[u].e[k]), -c1) - xh * c2);
+        }
+        if (e < a.S) st16<true>(dxr + e, pack16<T>(o));
       }
-      if (e < a.S) st16<true>(dxr + e, pack16<T>(o));
     }
   }
-}
-
-__global__ __launch_bounds__(256) void gn_bwd_finalize_kernel(GnBwdArgs a) {
-  const uint32_t c = blockIdx.x * 256 + threadIdx.x;
-  if (c >= a.C) return;
+  if (n != 0 || (!a.dgamma && !a.dbeta)) return;
+  // parameter gradients of channel c: wave w takes samples w, w + 4, ... in order; the four
+  // wave totals are added in wave order (deterministic)
+  __shared__ float fin[2 * (GN_TP_NT / 64)];
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   float sgm = 0.f, sbt = 0.f;
-  for (int n = 0; n < a.N; ++n) {
-    const int64_t r = (int64_t)n * a.C + c;
-    sgm += a.dg_part[r];
-    sbt += a.rows[r * 5 + 2];
+  for (int m = w; m < a.N; m += GN_TP_NT / 64) {
+    float mu, rstd;
+    gn_bwd_group_stats(a, a.rows + ((int64_t)m * a.C + g0) * 5, lane, mu, rstd);
+    const float* o = a.rows + ((int64_t)m * a.C + c) * 5;
+    sgm += rstd * (o[3] + (o[4] - mu) * o[2]);
+    sbt += o[2];
   }
-  if (a.dgamma) a.dgamma[c] = sgm;
-  if (a.dbeta) a.dbeta[c] = sbt;
+  if (lane == 0) {
+    fin[w] = sgm;
+    fin[GN_TP_NT / 64 + w] = sbt;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    sgm = sbt = 0.f;
+#pragma unroll
+    for (int v = 0; v < GN_TP_NT / 64; ++v) {
+      sgm += fin[v];
+      sbt += fin[GN_TP_NT / 64 + v];
+    }
+    if (a.dgamma) a.dgamma[c] = sgm;
+    if (a.dbeta) a.dbeta[c] = sbt;
+  }
 }
 
 template <typename T, int U>
@@ -1083,11 +1109,7 @@ int launch_gn_bwd(const GnBwdArgs& a, int64_t rows, hipStream_t s) {
   if (vpt <= 1) launch_gn_bwd_u<T, 1>(a, rows, s);
   else if (vpt <= 2) launch_gn_bwd_u<T, 2>(a, rows, s);
   else launch_gn_bwd_u<T, GN_BWD_U>(a, rows, s);
-  const int rc = check_launch("gn_bwd_rows_kernel / gn_bwd_apply_kernel");
-  if (rc) return rc;
-  if (!a.dgamma && !a.dbeta) return ATK_OK;
-  hipLaunchKernelGGL(gn_bwd_finalize_kernel, dim3((a.C + 255) / 256), dim3(256), 0, s, a);
-  return check_launch("gn_bwd_finalize_kernel");
+  return check_launch("gn_bwd_rows_kernel / gn_bwd_apply_kernel");
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1554,7 +1576,7 @@ extern "C" int atk_group_norm_apply(const void* x, const void* gamma, const void
 
 extern "C" size_t atk_group_norm_bwd_workspace_bytes(int64_t N, int64_t C) {
   if (N <= 0 || C <= 0) return 0;
-  return (size_t)N * (size_t)C * 6 * sizeof(float);
+  return (size_t)N * (size_t)C * 5 * sizeof(float);  // per (n, c) row: mean, M2, A, B, K
 }
 
 extern "C" int atk_group_norm_bwd(const void* x, const void* dy, const void* gamma, void* dx, float* dgamma,
@@ -1580,7 +1602,6 @@ extern "C" int atk_group_norm_bwd(const void* x, const void* dy, const void* gam
   GnBwdArgs a;
   a.x = x; a.dy = dy; a.gamma = gamma; a.dx = dx;
   a.rows = static_cast<float*>(workspace);
-  a.dg_part = a.rows + rows * 5;
   a.dgamma = dgamma; a.dbeta = dbeta;
   a.S = S; a.C = (uint32_t)C; a.cpg = (uint32_t)(C / G); a.N = (int)N;
   a.eps = eps; a.pdt = param_dtype;
