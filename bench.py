@@ -563,15 +563,15 @@ def bench_gn_backward_detail(shape, G, dev):
     nbytes = 3 * x.numel() * x.element_size()
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"ms": round(ms, 4), "GB/s": round(gbs, 1), "roofline_frac": round(gbs / HBM_PEAK_GBS, 4),
-            "variant": "native gn_bwd_rows/apply/finalize", "torch_op_backward_ms": round(torch_ms, 4),
+            "variant": "native gn_bwd_rows/apply", "torch_op_backward_ms": round(torch_ms, 4),
             "max_rel_err_vs_fp32_torch_ops": float(f"{err:.3g}")}
 
 
 def bench_gn_cl_backward_detail(shape, G, dev):
     """GroupNorm backward on channels-last (NHWC / NDHWC) bf16 tensors, as _GroupNormFn's
-    backward runs it: x and dy to NC[S] through the native transpose, the native backward
-    kernels, dx back to channels-last.  Against the torch-op backward on the same tensors
-    (the path channels-last input took before).  Bytes as for the NC[S] backward."""
+    backward runs it: the channels-last backward kernels straight on x and dy.  Beside it,
+    the earlier route (x and dy to NC[S] through the native transpose, the NC[S] kernels, dx
+    back) and the torch-op backward.  Bytes as for the NC[S] backward."""
     import torch
     from amd_tuned_torch import _native as nat
     from amd_tuned_torch import _dispatch
@@ -583,6 +583,9 @@ def bench_gn_cl_backward_detail(shape, G, dev):
     gm = (1 + 0.1 * torch.randn(C, generator=g)).to(torch.bfloat16).to(dev)
 
     def native():
+        return nat.group_norm_cl_backward(dy, x, G, gm, 1e-5, (True, True, True))
+
+    def via_transpose():
         dx, dg, db = nat.group_norm_backward(nat.channels_last_to_contiguous(dy), nat.channels_last_to_contiguous(x),
                                              G, gm, 1e-5, (True, True, True))
         return nat.contiguous_to_channels_last(dx), dg, db
@@ -592,11 +595,13 @@ def bench_gn_cl_backward_detail(shape, G, dev):
     assert dx.is_contiguous(memory_format=fmt)
     del dx, dg, db, rx, rg, rb
     ms = graph_time_ms(native, 20)
+    tp_ms = graph_time_ms(via_transpose, 20)
     torch_ms = event_time_ms(lambda: _dispatch._group_norm_backward(dy, x, G, gm, 1e-5, (True, True, True)), 10)
     nbytes = 3 * x.numel() * x.element_size()
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"ms": round(ms, 4), "GB/s": round(gbs, 1), "roofline_frac": round(gbs / HBM_PEAK_GBS, 4),
-            "variant": "transpose_tile x3 + native gn_bwd_rows/apply/finalize",
+            "variant": "native gn_cl_bwd_stats/merge/apply (channels-last)",
+            "via_transposes_ms": round(tp_ms, 4),
             "torch_op_backward_ms": round(torch_ms, 4), "max_rel_err_vs_fp32_torch_ops": float(f"{err:.3g}")}
 
 
@@ -1321,6 +1326,7 @@ def main():
         plan.append(("c3_nchw_backward_bf16", lambda: bench_gn_backward_detail((8, 512, 64, 64), 32, dev)))
         plan.append(("c3_ncdhw_backward_bf16", lambda: bench_gn_backward_detail((1, 512, 16, 64, 64), 32, dev)))
         plan.append(("c3_nhwc_backward_bf16", lambda: bench_gn_cl_backward_detail((8, 512, 64, 64), 32, dev)))
+        plan.append(("c3_ndhwc_backward_bf16", lambda: bench_gn_cl_backward_detail((1, 512, 16, 64, 64), 32, dev)))
         plan.append(("c5_gn_silu_bf16", lambda: bench_gn_detail((1, 256, 8, 64, 64), 32, 1e-6,
                                                                 torch.bfloat16, True, dev)))
         plan += [

@@ -302,6 +302,22 @@ int atk_group_norm_bwd(const void* x, const void* dy, const void* gamma, void* d
                        int param_dtype, void* workspace, size_t ws_bytes, atk_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * GroupNorm backward, channels-last layout (x, dy, dx: [N][S][C], NHWC / NDHWC
+ * memory).  Replaces the same torch-op backward (amd_tuned_torch/_dispatch.py:
+ * 2212-2302) for the channels-last input the reference's CK forward serves
+ * (amd_tuned_torch/ck_norm_ops.py:9-27, 93-103).  Same math and arguments as
+ * atk_group_norm_bwd.  Needs (C/G) * sizeof(dtype) a multiple of 16,
+ * C / (16 / sizeof(dtype)) dividing 256 (C <= 2048 for 16-bit types), 16-byte
+ * aligned x / dy / dx and one sample under 2 GiB (else ATK_UNSUPPORTED).  The
+ * workspace (atk_group_norm_cl_bwd_workspace_bytes, 16-byte aligned) needs no
+ * initialisation.  All sums are taken in a fixed order (deterministic).
+ * ------------------------------------------------------------------------- */
+size_t atk_group_norm_cl_bwd_workspace_bytes(int64_t N, int64_t C, int64_t S, int G);
+int atk_group_norm_cl_bwd(const void* x, const void* dy, const void* gamma, void* dx, float* dgamma,
+                          float* dbeta, int64_t N, int64_t C, int64_t S, int G, float eps, int dtype,
+                          int param_dtype, void* workspace, size_t ws_bytes, atk_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Dense convolution forward, groups = 1, NCDHW layout, as an implicit GEMM on
  * MFMA (replaces `conv3d(input, weight, bias?, stride, padding, dilation)`,
  * src/main_rocm.cpp:798-854, and `conv2d(...)`, src/main_rocm.cpp:669-715):

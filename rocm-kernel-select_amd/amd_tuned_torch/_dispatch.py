@@ -724,11 +724,19 @@ def _group_norm_backward(grad_output, input, num_groups, weight, eps, needs, bia
 
 def _group_norm_grads(grad_output, input, num_groups, weight, eps, needs):
     """(dx, dgamma, dbeta) of GroupNorm for `needs` = (dx, dgamma, dbeta) wanted: the native
-    backward kernels for contiguous or channels-last GPU input (channels-last x and dy go to
-    NC[S] through the native transpose, dx comes back in the input's layout; dgamma / dbeta
-    in fp32), the textbook torch-op backward otherwise (dgamma / dbeta in the parameter
-    dtypes).  Entries not asked for are None."""
+    backward kernels for contiguous or channels-last GPU input (channels-last first on the
+    channels-last kernels, else through NC[S] copies made by the native transpose, dx coming
+    back in the input's layout; dgamma / dbeta in fp32), the textbook torch-op backward
+    otherwise (dgamma / dbeta in the parameter dtypes).  Entries not asked for are None."""
     cl = _channels_last(input)
+    if input.is_cuda and cl and _native.available():
+        try:  # straight on the channels-last layout
+            fmt = torch.channels_last if input.dim() == 4 else torch.channels_last_3d
+            dy = grad_output if _channels_last(grad_output) else grad_output.contiguous(memory_format=fmt)
+            return _native.group_norm_cl_backward(dy, input.detach(), num_groups,
+                                                  None if weight is None else weight.detach(), eps, needs)
+        except _native.Unsupported:
+            pass
     if input.is_cuda and (input.is_contiguous() or cl) and _native.available():
         try:
             x = _native.channels_last_to_contiguous(input.detach()) if cl else input.detach()

@@ -46,7 +46,7 @@ EXPORTED_SYMBOLS = (
     "atk_dwconv1d_bwd", "atk_group_norm_noalloc_scratch_bytes", "atk_group_norm_fwd_noalloc",
     "atk_conv_packed_weight_bytes", "atk_conv_prepacked_workspace_bytes", "atk_conv_pack_weights",
     "atk_conv_fwd_prepacked", "atk_conv_gn_stats_bytes", "atk_conv_gn_records", "atk_conv_fwd_prepacked_ex",
-    "atk_group_norm_apply",
+    "atk_group_norm_apply", "atk_group_norm_cl_bwd_workspace_bytes", "atk_group_norm_cl_bwd",
 )
 
 
@@ -98,6 +98,10 @@ def _declare(lib) -> None:
     lib.atk_group_norm_bwd_workspace_bytes.restype = sz
     lib.atk_group_norm_bwd.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i32, c.c_float, i32, i32, vp, sz, vp]
     lib.atk_group_norm_bwd.restype = i32
+    lib.atk_group_norm_cl_bwd_workspace_bytes.argtypes = [i64, i64, i64, i32]
+    lib.atk_group_norm_cl_bwd_workspace_bytes.restype = sz
+    lib.atk_group_norm_cl_bwd.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i32, c.c_float, i32, i32, vp, sz, vp]
+    lib.atk_group_norm_cl_bwd.restype = i32
     lib.atk_group_norm_workspace_bytes.argtypes = [i64, i64, i64, i32, i32, i32]
     lib.atk_group_norm_workspace_bytes.restype = sz
     lib.atk_group_norm_workspace_zero_bytes.argtypes = [i64, i64, i64, i32, i32, i32]
@@ -855,6 +859,41 @@ def group_norm_backward(dy: torch.Tensor, x: torch.Tensor, num_groups: int,
                                _DTYPE_CODE[weight.dtype] if weight is not None else 0, _ptr(ws), ws.numel(),
                                _stream(x))
     _check(rc, "group_norm_backward")
+    return dx, dg, db
+
+
+def group_norm_cl_backward(dy: torch.Tensor, x: torch.Tensor, num_groups: int,
+                           weight: Optional[torch.Tensor], eps: float, needs=(True, True, True)):
+    """group_norm_backward for channels-last x and dy (NHWC / NDHWC memory, both in the same
+    format): dx comes back in that format, dgamma / dbeta in fp32.  Raises Unsupported for
+    shapes the kernels do not take (C/G not a multiple of 16 bytes, C above 2048 16-bit
+    channels, C/(16 bytes) not dividing 256, misaligned data)."""
+    _require_cuda(x, dy, weight)
+    if not (is_channels_last(x) and is_channels_last(dy)) or dy.shape != x.shape:
+        raise RuntimeError("group_norm_cl_backward: x and dy must be channels-last tensors of one shape")
+    if x.dtype not in _DTYPE_CODE or dy.dtype != x.dtype:
+        raise RuntimeError("group_norm_cl_backward: x and dy must share a float16/bfloat16/float32 dtype")
+    if weight is not None and weight.dtype not in _DTYPE_CODE:
+        raise RuntimeError("group_norm_cl_backward: weight must be float16, bfloat16 or float32")
+    N, C = x.shape[0], x.shape[1]
+    S = x.numel() // max(1, N * C)
+    if N == 0 or S == 0:
+        raise Unsupported("group_norm_cl_backward: empty input")
+    G = int(num_groups)
+    if G <= 0 or C % G:
+        raise RuntimeError("group_norm_cl_backward: channels must be divisible by num_groups")
+    weight = weight.contiguous() if weight is not None else None
+    dx = torch.empty_like(x) if needs[0] else None  # same memory format
+    dg = torch.empty(C, dtype=torch.float32, device=x.device) if needs[1] else None
+    db = torch.empty(C, dtype=torch.float32, device=x.device) if needs[2] else None
+    L_ = lib()
+    nbytes = L_.atk_group_norm_cl_bwd_workspace_bytes(N, C, S, G)
+    ws = workspace(x.device, "group_norm_cl_bwd", nbytes)
+    rc = L_.atk_group_norm_cl_bwd(_ptr(x), _ptr(dy), _ptr(weight), _ptr(dx), _ptr(dg), _ptr(db), N, C, S, G,
+                                  float(eps), _DTYPE_CODE[x.dtype],
+                                  _DTYPE_CODE[weight.dtype] if weight is not None else 0, _ptr(ws), ws.numel(),
+                                  _stream(x))
+    _check(rc, "group_norm_cl_backward")
     return dx, dg, db
 
 

@@ -1351,6 +1351,301 @@ int launch_gn_cl(const GnClArgs& a, int N, int silu, hipStream_t s) {
   return check_launch("gn_cl_apply_kernel");
 }
 
+// ---------------------------------------------------------------------------------------
+// Channels-last GroupNorm backward (x, dy, dx: [n][s][c]); the math of the NC[S] backward
+// above, without the layout conversions.  Three kernels, 5 tensor passes (x and dy read
+// twice, the second time mostly from the Infinity Cache; dx written once):
+//   stats: a workgroup per (n, spatial chunk); thread t owns one channel vector on rows
+//          t / CV, t / CV + R, ... and accumulates per channel x's sums about a shift K (its
+//          first x of that channel), sum dy and sum dy * (x - K); the workgroup then merges
+//          its rows per channel, in row order, into the chunk's record
+//          (mean, M2, A = sum dy, B = sum dy * (x - mean));
+//   merge: a workgroup per (n, g) merges the group's (chunk, channel) records into the
+//          group's mean and rstd, c1 = sum gamma*dy / E and c2 = rstd * sum gamma*dy*(x - mean) / E,
+//          and writes each channel's dx coefficients and its dgamma / dbeta term of sample n;
+//   apply: a workgroup per (n, chunk) forms dx = rstd*gamma_c*dy - rstd*c1 - rstd^2*c2*(x - mean),
+//          each thread loading its channels' coefficients next to its first rows of x and dy;
+//          workgroup (0, 0) also sums the parameter-gradient terms over n, in order
+//          (deterministic).
+struct GnClBwdArgs {
+  const void* x;
+  const void* dy;
+  const void* gamma;
+  void* dx;           // may be null
+  float* dgamma;      // [C] or null
+  float* dbeta;       // [C] or null
+  float4* part;       // [N][NCH][C] chunk records (mean, M2, A, B)
+  float4* coef;       // [N][C] dx coefficients (rstd * gamma_c, mean, -rstd^2 * c2, -rstd * c1)
+  float2* dpar;       // [N][C] (dgamma term, dbeta term)
+  int64_t S, SC;      // spatial positions, positions per chunk
+  uint32_t sample_bytes;
+  uint32_t C, G, cpg;
+  int N, NCH;
+  float eps;
+  int pdt;
+};
+
+// (count, mean, M2, A = sum dy, B = sum dy * (x - mean)) of a set of positions
+struct GnBwdRec {
+  float n, mean, m2, a, b;
+};
+
+__device__ __forceinline__ void bwd_rec_merge(GnBwdRec& r, const GnBwdRec& o) {
+  if (o.n == 0.f) return;
+  if (r.n == 0.f) {
+    r = o;
+    return;
+  }
+  const float n = r.n + o.n, d = o.mean - r.mean;
+  const float mean = r.mean + d * (o.n / n);
+  r.m2 = r.m2 + o.m2 + d * d * (r.n * o.n / n);
+  r.b = (r.b + (r.mean - mean) * r.a) + (o.b + (o.mean - mean) * o.a);
+  r.a = r.a + o.a;
+  r.mean = mean;
+  r.n = n;
+}
+
+constexpr int GN_CL_BWD_U = 4;  // rows of x and of dy in flight per thread
+
+template <typename T>
+__global__ __launch_bounds__(GN_CL_NT) void gn_cl_bwd_stats_kernel(GnClBwdArgs a) {
+  constexpr int VEC = 16 / sizeof(T);
+  __shared__ float4 rec[GN_CL_NT * VEC];  // [row phase rr][channel]
+  __shared__ float cnt_s[GN_CL_NT];
+  const int n = blockIdx.y, ch = blockIdx.x;
+  const int CV = (int)(a.C / VEC), R = GN_CL_NT / CV;
+  const int v = threadIdx.x % CV, rr = threadIdx.x / CV;
+  const int64_t s0 = (int64_t)ch * a.SC, s1 = min(a.S, s0 + a.SC);
+  const int64_t base = (int64_t)n * a.S * a.C;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(static_cast<const T*>(a.x) + base, a.sample_bytes);
+  const __amdgpu_buffer_rsrc_t rg = make_rsrc(static_cast<const T*>(a.dy) + base, a.sample_bytes);
+  const uint32_t vb = (uint32_t)(v * VEC * sizeof(T)), rowb = (uint32_t)(a.C * sizeof(T));
+  float K[VEC], t1[VEC], t2[VEC], sa[VEC], sb[VEC];
+  float cnt = 0.f;
+  {
+    Vec16<T> k0;
+    k0.raw = bload16(rx, s0 + rr < s1 ? (uint32_t)(s0 + rr) * rowb + vb : kOOB, 0);
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+      K[k] = to_f32(k0.e[k]);
+      t1[k] = t2[k] = sa[k] = sb[k] = 0.f;
+    }
+  }
+  for (int64_t s = s0 + rr; s < s1; s += (int64_t)R * GN_CL_BWD_U) {
+    Vec16<T> xv[GN_CL_BWD_U], gv[GN_CL_BWD_U];
+#pragma unroll
+    for (int u = 0; u < GN_CL_BWD_U; ++u) {
+      const int64_t sp = s + (int64_t)u * R;
+      const uint32_t off = sp < s1 ? (uint32_t)sp * rowb + vb : kOOB;
+      xv[u].raw = bload16(rx, off, 0);  // cached: the apply kernel reads x and dy again
+      gv[u].raw = bload16(rg, off, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < GN_CL_BWD_U; ++u) {
+      const float m = (s + (int64_t)u * R < s1) ? 1.f : 0.f;
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) {
+        const float d = (to_f32(xv[u].e[k]) - K[k]) * m;
+        const float g = to_f32(gv[u].e[k]);  // 0 past the chunk (out-of-range loads)
+        t1[k] += d;
+        t2[k] = fmaf(d, d, t2[k]);
+        sa[k] += g;
+        sb[k] = fmaf(g, d, sb[k]);
+      }
+      cnt += m;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) {
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (cnt > 0.f) {
+      const float q = t1[k] / cnt;
+      o = make_float4(K[k] + q, fmaxf(fmaf(-t1[k], q, t2[k]), 0.f), sa[k], fmaf(-q, sa[k], sb[k]));
+    }
+    rec[rr * a.C + v * VEC + k] = o;
+  }
+  if (v == 0) cnt_s[rr] = cnt;
+  __syncthreads();
+  float4* out = a.part + ((int64_t)n * a.NCH + ch) * a.C;
+  for (uint32_t c = threadIdx.x; c < a.C; c += GN_CL_NT) {
+    GnBwdRec r{0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int r2 = 0; r2 < R; ++r2) {
+      const float4 e = rec[r2 * a.C + c];
+      bwd_rec_merge(r, GnBwdRec{cnt_s[r2], e.x, e.y, e.z, e.w});
+    }
+    out[c] = make_float4(r.mean, r.m2, r.a, r.b);
+  }
+}
+
+// Two flat passes over the group's (chunk, channel) records, no per-record division:
+//   1. mean  = sum len * mean_r / E;
+//   2. M2    = sum (M2_r + len * (mean_r - mean)^2), and per channel A_c = sum A_r and
+//      B_c   = sum (B_r + (mean_r - mean) * A_r), i.e. sum dy * (x - mean) about the group mean.
+// Thread t = p * cblk + j takes channel j's chunks p, p + tpc, ... (lanes run along the
+// channels, so a wave's loads are contiguous runs of a chunk's records); a channel's tpc
+// partial sums are added in p order, the group totals in thread order (deterministic).
+constexpr int GN_CL_BWD_MNT = 1024;
+__global__ __launch_bounds__(GN_CL_BWD_MNT) void gn_cl_bwd_merge_kernel(GnClBwdArgs a) {
+  __shared__ float red[GN_CL_BWD_MNT / 64];
+  __shared__ float2 part_s[GN_CL_BWD_MNT];
+  __shared__ float s_stat[2];
+  const int64_t ng = blockIdx.x;  // n * G + g
+  const int n = (int)(ng / a.G);
+  const uint32_t g = (uint32_t)(ng - (int64_t)n * a.G);
+  const int tid = threadIdx.x;
+  const int cblk = (int)min(a.cpg, (uint32_t)GN_CL_BWD_MNT);  // channels taken at once
+  const int tpc = GN_CL_BWD_MNT / cblk;                       // threads per channel
+  const int jt = tid % cblk, p = tid / cblk;
+  const float4* pn = a.part + (int64_t)n * a.NCH * a.C + (int64_t)g * a.cpg;
+  const float E = (float)((int64_t)a.cpg * a.S);
+  auto len_of = [&](int q) { return (float)(min(a.S, (int64_t)(q + 1) * a.SC) - (int64_t)q * a.SC); };
+  // pass 1: the group mean
+  float sm = 0.f;
+  for (int j0 = 0; j0 < (int)a.cpg; j0 += cblk) {
+    const int j = j0 + jt;
+    if (p < tpc && j < (int)a.cpg) {
+#pragma unroll 4
+      for (int q = p; q < a.NCH; q += tpc) sm = fmaf(len_of(q), pn[(int64_t)q * a.C + j].x, sm);
+    }
+  }
+  const float mu = block_sum<GN_CL_BWD_MNT>(sm, red) / E;
+  // pass 2: M2 and the per-channel sums about mu
+  float m2 = 0.f, sg = 0.f, sgx = 0.f;
+  for (int j0 = 0; j0 < (int)a.cpg; j0 += cblk) {
+    const int j = j0 + jt;
+    float ca = 0.f, cb = 0.f;
+    if (p < tpc && j < (int)a.cpg) {
+#pragma unroll 4
+      for (int q = p; q < a.NCH; q += tpc) {
+        const float4 e = pn[(int64_t)q * a.C + j];
+        const float dm = e.x - mu;
+        m2 += e.y + len_of(q) * dm * dm;
+        ca += e.z;
+        cb += e.w + dm * e.z;
+      }
+    }
+    part_s[tid] = make_float2(ca, cb);
+    __syncthreads();
+    if (tid < cblk && j0 + tid < (int)a.cpg) {
+      float A = 0.f, B = 0.f;
+      for (int q = 0; q < tpc; ++q) {
+        A += part_s[q * cblk + tid].x;
+        B += part_s[q * cblk + tid].y;
+      }
+      const uint32_t c = g * a.cpg + j0 + tid;
+      const float gam = a.gamma ? load_param(a.gamma, a.pdt, c) : 1.f;
+      sg = fmaf(gam, A, sg);
+      sgx = fmaf(gam, B, sgx);
+      a.dpar[(int64_t)n * a.C + c] = make_float2(B, A);  // B scaled by rstd below
+    }
+    __syncthreads();
+  }
+  m2 = block_sum<GN_CL_BWD_MNT>(m2, red);
+  sg = block_sum<GN_CL_BWD_MNT>(sg, red);
+  sgx = block_sum<GN_CL_BWD_MNT>(sgx, red);
+  const float rstd = 1.0f / sqrtf(m2 / E + a.eps);
+  const float c1 = sg / E, c2 = rstd * sgx / E;
+  // per channel: the dx coefficients, and the dgamma term rstd * sum dy * (x - mean) (this
+  // thread wrote the dpar entries it scales: same thread, program order)
+  for (uint32_t j = tid; j < a.cpg; j += GN_CL_BWD_MNT) {
+    const uint32_t c = g * a.cpg + j;
+    const float gam = a.gamma ? load_param(a.gamma, a.pdt, c) : 1.f;
+    a.coef[(int64_t)n * a.C + c] = make_float4(rstd * gam, mu, -rstd * rstd * c2, -rstd * c1);
+  }
+  for (int j0 = 0; j0 < (int)a.cpg; j0 += cblk)
+    if (tid < cblk && j0 + tid < (int)a.cpg) {
+      float2* d = a.dpar + (int64_t)n * a.C + g * a.cpg + j0 + tid;
+      d->x *= rstd;
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(GN_CL_NT) void gn_cl_bwd_apply_kernel(GnClBwdArgs a) {
+  constexpr int VEC = 16 / sizeof(T);
+  const int n = blockIdx.y, ch = blockIdx.x;
+  const int CV = (int)(a.C / VEC), R = GN_CL_NT / CV;
+  const int v = threadIdx.x % CV, rr = threadIdx.x / CV;
+  const int64_t s0 = (int64_t)ch * a.SC, s1 = min(a.S, s0 + a.SC);
+  const int64_t base = (int64_t)n * a.S * a.C;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(static_cast<const T*>(a.x) + base, a.sample_bytes);
+  const __amdgpu_buffer_rsrc_t rg = make_rsrc(static_cast<const T*>(a.dy) + base, a.sample_bytes);
+  const uint32_t vb = (uint32_t)(v * VEC * sizeof(T)), rowb = (uint32_t)(a.C * sizeof(T));
+  if (a.dx) {
+    Vec16<T> xv[GN_CL_BWD_U], gv[GN_CL_BWD_U];
+    auto issue = [&](int64_t s) {
+#pragma unroll
+      for (int u = 0; u < GN_CL_BWD_U; ++u) {
+        const int64_t sp = s + (int64_t)u * R;
+        const uint32_t off = sp < s1 ? (uint32_t)sp * rowb + vb : kOOB;
+        xv[u].raw = bload16<2>(rx, off, 0);  // last reads of x and dy
+        gv[u].raw = bload16<2>(rg, off, 0);
+      }
+    };
+    // the first rows and this thread's channel coefficients are requested together
+    const int64_t s_first = s0 + rr;
+    issue(s_first);
+    const float4* cf = a.coef + (int64_t)n * a.C + v * VEC;
+    float P[VEC], M[VEC], Q[VEC], Rc[VEC];
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+      const float4 e = cf[k];
+      P[k] = e.x;
+      M[k] = e.y;
+      Q[k] = e.z;
+      Rc[k] = e.w;
+    }
+    T* __restrict__ dxn = static_cast<T*>(a.dx) + base + v * VEC;
+    for (int64_t s = s_first; s < s1; s += (int64_t)R * GN_CL_BWD_U) {
+      if (s != s_first) issue(s);
+#pragma unroll
+      for (int u = 0; u < GN_CL_BWD_U; ++u) {
+        const int64_t sp = s + (int64_t)u * R;
+        float o[VEC];
+#pragma unroll
+        for (int k = 0; k < VEC; ++k)
+          o[k] = fmaf(P[k], to_f32(gv[u].e[k]), fmaf(Q[k], to_f32(xv[u].e[k]) - M[k], Rc[k]));
+        if (sp < s1) st16<true>(dxn + sp * a.C, pack16<T>(o));
+      }
+    }
+  }
+  if (n != 0 || ch != 0 || (!a.dgamma && !a.dbeta)) return;
+  for (uint32_t c = threadIdx.x; c < a.C; c += GN_CL_NT) {
+    float sgm = 0.f, sbt = 0.f;
+    for (int m = 0; m < a.N; ++m) {
+      const float2 d = a.dpar[(int64_t)m * a.C + c];
+      sgm += d.x;
+      sbt += d.y;
+    }
+    if (a.dgamma) a.dgamma[c] = sgm;
+    if (a.dbeta) a.dbeta[c] = sbt;
+  }
+}
+
+// About 512 workgroups (two per CU; each keeps 32 KB of x and dy in flight), at least 64
+// positions per chunk: fewer, larger chunks than the forward's, since every chunk leaves a
+// 16-byte record per channel that the merge reads twice.
+inline GnClPlan plan_gn_cl_bwd(int64_t N, int64_t S) {
+  int64_t nch = (512 + N - 1) / N;
+  nch = std::max<int64_t>(1, std::min<int64_t>(nch, (S + 63) / 64));
+  GnClPlan p;
+  p.SC = (S + nch - 1) / nch;
+  p.NCH = (int)((S + p.SC - 1) / p.SC);
+  return p;
+}
+
+template <typename T>
+int launch_gn_cl_bwd(const GnClBwdArgs& a, hipStream_t s) {
+  const dim3 grid((unsigned)a.NCH, (unsigned)a.N), block(GN_CL_NT);
+  hipLaunchKernelGGL((gn_cl_bwd_stats_kernel<T>), grid, block, 0, s, a);
+  int rc = check_launch("gn_cl_bwd_stats_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(gn_cl_bwd_merge_kernel, dim3((unsigned)((int64_t)a.N * a.G)), dim3(GN_CL_BWD_MNT), 0, s, a);
+  rc = check_launch("gn_cl_bwd_merge_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL((gn_cl_bwd_apply_kernel<T>), grid, block, 0, s, a);
+  return check_launch("gn_cl_bwd_apply_kernel");
+}
+
 }  // namespace
 
 int group_norm_num_variants() { return kNumGn; }
@@ -1655,5 +1950,52 @@ extern "C" int atk_group_norm_cl_fwd(const void* x, const void* gamma, const voi
     case ATK_F32: return launch_gn_cl<float>(a, (int)N, fuse_silu, s);
     case ATK_F16: return launch_gn_cl<_Float16>(a, (int)N, fuse_silu, s);
     default: return launch_gn_cl<__bf16>(a, (int)N, fuse_silu, s);
+  }
+}
+
+extern "C" size_t atk_group_norm_cl_bwd_workspace_bytes(int64_t N, int64_t C, int64_t S, int G) {
+  if (N <= 0 || C <= 0 || S <= 0 || G <= 0) return 0;
+  const atk::GnClPlan p = atk::plan_gn_cl_bwd(N, S);
+  return (size_t)N * (size_t)C * ((size_t)p.NCH * 16 + 16 + 8);  // records, dx coefficients, dpar
+}
+
+extern "C" int atk_group_norm_cl_bwd(const void* x, const void* dy, const void* gamma, void* dx, float* dgamma,
+                                     float* dbeta, int64_t N, int64_t C, int64_t S, int G, float eps, int dtype,
+                                     int param_dtype, void* workspace, size_t ws_bytes, atk_stream_t stream) {
+  using namespace atk;
+  if (!dtype_ok(dtype) || (gamma && !dtype_ok(param_dtype)))
+    return fail(ATK_EINVAL, "group_norm backward (channels-last): unknown dtype code");
+  if (N <= 0 || C <= 0 || S <= 0 || G <= 0) return fail(ATK_EINVAL, "group_norm backward (channels-last): bad sizes");
+  if (C % G)
+    return fail(ATK_EINVAL, "group_norm backward (channels-last): channels (%lld) not divisible by groups (%d)",
+                (long long)C, G);
+  if (!x || !dy) return fail(ATK_EINVAL, "group_norm backward (channels-last): null pointer");
+  const int64_t es = (int64_t)dtype_size(dtype), vec = 16 / es;
+  const int64_t cpg = C / G;
+  if (cpg % vec || C > GN_CL_MAXC || GN_CL_NT % (C / vec) || !aligned16(x) || !aligned16(dy) || (dx && !aligned16(dx)))
+    return fail(ATK_UNSUPPORTED, "group_norm backward (channels-last): needs C/G %% %lld == 0, C/%lld dividing %d "
+                "and 16-byte aligned tensors", (long long)vec, (long long)vec, GN_CL_NT);
+  if (N >= 65536) return fail(ATK_UNSUPPORTED, "group_norm backward (channels-last): batch too large");
+  if (S * C * es >= ((int64_t)1 << 31))
+    return fail(ATK_UNSUPPORTED, "group_norm backward (channels-last): one sample over 2 GiB (32-bit buffer offsets)");
+  const size_t need = atk_group_norm_cl_bwd_workspace_bytes(N, C, S, G);
+  if (!workspace || ws_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 15u))
+    return fail(ATK_EINVAL, "group_norm backward (channels-last): workspace of %zu bytes (16-byte aligned) needed",
+                need);
+  const GnClPlan p = plan_gn_cl_bwd(N, S);
+  GnClBwdArgs a;
+  a.x = x; a.dy = dy; a.gamma = gamma; a.dx = dx; a.dgamma = dgamma; a.dbeta = dbeta;
+  a.part = static_cast<float4*>(workspace);
+  a.coef = a.part + (size_t)N * p.NCH * C;
+  a.dpar = reinterpret_cast<float2*>(a.coef + (size_t)N * C);
+  a.S = S; a.SC = p.SC; a.NCH = p.NCH; a.N = (int)N;
+  a.sample_bytes = (uint32_t)(S * C * es);
+  a.C = (uint32_t)C; a.G = (uint32_t)G; a.cpg = (uint32_t)cpg;
+  a.eps = eps; a.pdt = param_dtype;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case ATK_F32: return launch_gn_cl_bwd<float>(a, s);
+    case ATK_F16: return launch_gn_cl_bwd<_Float16>(a, s);
+    default: return launch_gn_cl_bwd<__bf16>(a, s);
   }
 }

@@ -281,8 +281,8 @@ def test_group_norm_autograd_through_patched_group_norm(dev, dtype):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
 def test_group_norm_autograd_channels_last(dev, dtype):
     """Channels-last (NHWC / NDHWC) input through the patched F.group_norm with gradients:
-    x and dy reach the native backward through the native layout conversion, dx comes back
-    channels-last; every gradient matches the oracle."""
+    x and dy reach the native channels-last backward, dx comes back channels-last; every
+    gradient matches the oracle."""
     import torch.nn.functional as F
     import amd_tuned_torch  # noqa: F401
     for shape, G, fmt in (((2, 64, 8, 8), 8, torch.channels_last),
@@ -323,6 +323,53 @@ CL_SHAPES = [
     ((1, 256, 4, 16, 16), 32),      # C5-like channels, NDHWC
     ((3, 32, 7, 5), 4),             # odd spatial sizes
 ]
+
+
+CL_BWD_SHAPES = CL_SHAPES + [
+    ((1, 64, 1, 2048), 4),          # one long row: 32 chunks of 64 positions
+    ((2, 128, 3, 40, 40), 16),      # NDHWC, chunk boundaries inside rows
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("shape_g", CL_BWD_SHAPES, ids=lambda s: "x".join(map(str, s[0])) + f"_g{s[1]}")
+def test_group_norm_channels_last_backward(dev, shape_g, dtype):
+    """atk_group_norm_cl_bwd on channels-last x and dy against the float64 oracle (which
+    reads the same values in NC[S] order): dx in the input's memory format, dgamma, dbeta;
+    also without affine weights and with only the parameter gradients asked for."""
+    shape, G = shape_g
+    nat = _native()
+    x, gm, _ = _inputs(shape, dtype, seed=len(shape) + G + 300)
+    dy = torch.randn(*shape, generator=torch.Generator().manual_seed(G + 7)).to(dtype)
+    fmt = torch.channels_last if len(shape) == 4 else torch.channels_last_3d
+    xd, dyd = x.to(dev).contiguous(memory_format=fmt), dy.to(dev).contiguous(memory_format=fmt)
+    for weight in (gm, None):
+        dx, dg, db = nat.group_norm_cl_backward(dyd, xd, G, None if weight is None else weight.to(dev), 1e-5)
+        torch.cuda.synchronize()
+        assert dx.is_contiguous(memory_format=fmt) and dx.dtype == dtype
+        rdx, rdg, rdb = O.group_norm_bwd(x, G, weight, dy, 1e-5)
+        assert O.max_rel_err(dx.cpu().contiguous(), rdx) <= BAR[dtype], O.max_rel_err(dx.cpu().contiguous(), rdx)
+        assert O.max_rel_err(dg.cpu(), rdg) <= BWD_BAR_P[dtype], O.max_rel_err(dg.cpu(), rdg)
+        assert O.max_rel_err(db.cpu(), rdb) <= BWD_BAR_P[dtype], O.max_rel_err(db.cpu(), rdb)
+    dx2, dg2, db2 = nat.group_norm_cl_backward(dyd, xd, G, gm.to(dev), 1e-5, (False, True, True))
+    assert dx2 is None and torch.equal(dg2.cpu(), nat.group_norm_cl_backward(dyd, xd, G, gm.to(dev), 1e-5)[1].cpu())
+
+
+def test_group_norm_channels_last_backward_c3_full_size(dev):
+    """C3's NDHWC shape at full size, bf16, through the channels-last backward kernels:
+    every gradient element against the oracle."""
+    nat = _native()
+    shape, G = (1, 512, 16, 64, 64), 32
+    x, gm, _ = _inputs(shape, torch.bfloat16, seed=3103)
+    dy = torch.randn(*shape, generator=torch.Generator().manual_seed(3104)).to(torch.bfloat16)
+    fmt = torch.channels_last_3d
+    dx, dg, db = nat.group_norm_cl_backward(dy.to(dev).contiguous(memory_format=fmt),
+                                            x.to(dev).contiguous(memory_format=fmt), G, gm.to(dev), 1e-5)
+    torch.cuda.synchronize()
+    rdx, rdg, rdb = O.group_norm_bwd(x, G, gm, dy, 1e-5)
+    assert O.max_rel_err(dx.cpu().contiguous(), rdx) <= BAR[torch.bfloat16]
+    assert O.max_rel_err(dg.cpu(), rdg) <= BWD_BAR_P[torch.bfloat16]
+    assert O.max_rel_err(db.cpu(), rdb) <= BWD_BAR_P[torch.bfloat16]
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
