@@ -200,21 +200,46 @@ def _check(rc: int, what: str) -> None:
     raise RuntimeError(msg)
 
 
+# The variant tables are compiled into the library, so they are read once per op: the
+# patched calls look a cached winner's index up on every call, and one ctypes call per
+# variant name would cost more host time than a small kernel takes.
+_variant_names: dict = {}
+_variant_pos: dict = {}
+
+
 def variants(op: int) -> list:
     """Names of the library's variants of `op` (OP_DWCONV1D / OP_GROUP_NORM / OP_CONV)."""
-    L = lib()
-    return [L.atk_variant_name(op, i).decode() for i in range(L.atk_num_variants(op))]
+    names = _variant_names.get(op)
+    if names is None:
+        L = lib()
+        names = [L.atk_variant_name(op, i).decode() for i in range(L.atk_num_variants(op))]
+        _variant_names[op] = names
+        _variant_pos[op] = {n: i for i, n in enumerate(names)}
+    return list(names)
 
 
 def variant_index(op: int, name: str) -> int:
+    """Index of variant `name` of `op`; RuntimeError if the library has no such variant."""
+    pos = _variant_pos.get(op)
+    if pos is None:
+        variants(op)
+        pos = _variant_pos[op]
     try:
-        return variants(op).index(name)
-    except ValueError:
+        return pos[name]
+    except KeyError:
         raise RuntimeError(f"unknown variant {name!r} for op {op}") from None
 
 
+def _raw_stream(device: torch.device) -> int:
+    """Handle of `device`'s current HIP stream.  torch's raw-stream query: building a
+    torch.cuda.Stream object (torch.cuda.current_stream) costs several microseconds of host
+    time per call, as long as a small kernel."""
+    idx = device.index
+    return torch._C._cuda_getCurrentRawStream(idx if idx is not None else torch.cuda.current_device())
+
+
 def _stream(t: torch.Tensor) -> int:
-    return torch.cuda.current_stream(t.device).cuda_stream
+    return _raw_stream(t.device)
 
 
 def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
@@ -265,12 +290,12 @@ def _device_index(device: torch.device) -> int:
 
 def workspace(device: torch.device, purpose: str, nbytes: int, stream=None) -> torch.Tensor:
     """A zero-initialised uint8 buffer of at least `nbytes` for `purpose`, private to the
-    current stream of `device` (or to `stream`, which must be that stream).  The zeroing
-    (torch's fill kernel, ordered on that stream) happens only when a buffer is created;
-    kernels that need zeroed scratch leave it zero."""
+    current stream of `device` (or to `stream`, a raw handle or torch.cuda.Stream, which must
+    be that stream).  The zeroing (torch's fill kernel, ordered on that stream) happens only
+    when a buffer is created; kernels that need zeroed scratch leave it zero."""
     if stream is None:
-        stream = torch.cuda.current_stream(device)
-    key = (_device_index(device), stream.cuda_stream, purpose)
+        stream = _raw_stream(device)
+    key = (_device_index(device), getattr(stream, "cuda_stream", stream), purpose)
     with _ws_lock:
         buf = _ws_live.get(key)
         if buf is not None and buf.numel() >= nbytes:
@@ -707,14 +732,17 @@ def group_norm(input: torch.Tensor, num_groups: int, weight: Optional[torch.Tens
     v = int(variant)
     nbytes = _cached_size(L.atk_group_norm_workspace_bytes, N, C, S, G, dt, v)
     if nbytes == 0:
+        # the size query declined: the forward entry point, which validates and plans before
+        # it looks at the workspace, returns the code and reason (nothing is launched)
         _size_cache.pop(("atk_group_norm_workspace_bytes", -1, (N, C, S, G, dt, v)), None)
-        L.atk_group_norm_workspace_bytes(N, C, S, G, dt, v)  # sets the reason
-        raise RuntimeError(f"group_norm: {last_error()}")
-    stream = torch.cuda.current_stream(input.device)
+        rc = L.atk_group_norm_fwd(_ptr(input), _ptr(weight), _ptr(bias), _ptr(y), N, C, S, G, float(eps),
+                                  int(bool(silu)), dt, pdt, v, None, 0, _stream(input))
+        _check(rc if rc != ATK_OK else ATK_EINVAL, "group_norm")
+    stream = _raw_stream(input.device)
     ws = workspace(input.device, "group_norm", nbytes, stream)
     rc = L.atk_group_norm_fwd(_ptr(input), _ptr(weight), _ptr(bias), _ptr(y), N, C, S, G,
                               float(eps), int(bool(silu)), dt, pdt, v, ws.data_ptr(), ws.numel(),
-                              stream.cuda_stream)
+                              stream)
     _check(rc, "group_norm")
     return y
 
@@ -1018,11 +1046,10 @@ def _conv(input, weight, bias, stride, padding, dilation, nd: int, variant: int,
     if packed_bytes:
         # an MFMA variant that takes the shape: packed weights from the cache, the workspace
         # only for split-K partials
-        stream_obj = torch.cuda.current_stream(input.device)
-        stream = stream_obj.cuda_stream
+        stream = _raw_stream(input.device)
         packed = _packed_conv_weights(weight, geom, dt, int(variant), packed_bytes, stream)
         nws = _cached_size(L.atk_conv_prepacked_workspace_bytes, *geom, dt, int(variant), device=dev)
-        ws = workspace(input.device, "conv", nws, stream_obj) if nws else None
+        ws = workspace(input.device, "conv", nws, stream) if nws else None
         if not extras:
             rc = L.atk_conv_fwd_prepacked(_ptr(input), _ptr(packed), packed_bytes, _ptr(bias), _ptr(y), *geom, dt,
                                           int(variant), _ptr(ws), ws.numel() if ws is not None else 0, stream)

@@ -1691,7 +1691,8 @@ int gn_fwd(const void* x, const void* gamma, const void* beta, void* y, int64_t 
   if (!x || !y) return fail(ATK_EINVAL, "group_norm: null pointer");
   GnPlan p;
   if (!plan_gn(N, C, S, G, dtype, variant, p))
-    return fail(ATK_UNSUPPORTED, "group_norm: too many slices per group for %s", kGnVariants[variant].name);
+    return fail(ATK_UNSUPPORTED, "group_norm: %s does not take this shape (slices per group)",
+                kGnVariants[variant].name);
   if (need_out) *need_out = p.ws_bytes;
   if (!workspace || workspace_bytes < p.ws_bytes)
     return fail(ATK_EINVAL, "group_norm: workspace of %zu bytes needed", p.ws_bytes);
@@ -1797,7 +1798,8 @@ extern "C" int atk_group_norm_fwd_noalloc(const void* x, const void* gamma, cons
   if (N == 0) return ATK_OK;
   GnPlan p;
   if (!plan_gn(N, C, S, G, dtype, variant, p))
-    return fail(ATK_UNSUPPORTED, "group_norm: too many slices per group for %s", kGnVariants[variant].name);
+    return fail(ATK_UNSUPPORTED, "group_norm: %s does not take this shape (slices per group)",
+                kGnVariants[variant].name);
   if (p.ws_bytes > GN_NOALLOC_BYTES)
     return fail(ATK_EINVAL, "group_norm (no-alloc): this shape and variant need %zu bytes of scratch; the "
                 "static scratch holds %zu (use atk_group_norm_fwd with a workspace)", p.ws_bytes,

@@ -535,11 +535,8 @@ def test_causal_truncate_mode_gate(monkeypatch):
 def test_workspaces_are_private_per_stream_and_retired_on_growth(monkeypatch):
     """Scratch is pooled per (device, stream, purpose); a grown buffer replaces the old one,
     which stays alive (a captured graph may still point at it)."""
-    class FakeStream:
-        def __init__(self, h):
-            self.cuda_stream = h
-    current = [FakeStream(11)]
-    monkeypatch.setattr(torch.cuda, "current_stream", lambda device=None: current[0])
+    current = [11]
+    monkeypatch.setattr(_native, "_raw_stream", lambda device: current[0])
     real_zeros = torch.zeros
     monkeypatch.setattr(torch, "zeros", lambda n, dtype=None, device=None: real_zeros(n, dtype=dtype))
     monkeypatch.setattr(_native, "_ws_live", {})
@@ -547,10 +544,10 @@ def test_workspaces_are_private_per_stream_and_retired_on_growth(monkeypatch):
     dev = torch.device("cuda", 0)
     a = _native.workspace(dev, "conv", 100)
     assert _native.workspace(dev, "conv", 50) is a            # same stream, fits: reused
-    current[0] = FakeStream(22)
+    current[0] = 22
     b = _native.workspace(dev, "conv", 100)
     assert b is not a                                         # another stream: its own buffer
-    current[0] = FakeStream(11)
+    current[0] = 11
     grown = _native.workspace(dev, "conv", 1 << 20)
     assert grown.numel() >= 1 << 20 and grown is not a
     assert any(r is a for r in _native._ws_retired)           # retired, not freed
