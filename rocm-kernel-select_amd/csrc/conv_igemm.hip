@@ -23,6 +23,8 @@
 //    global load, L2-resident across the workgroups that share the output-channel tile.
 //  * Split-K over stages for shapes with too few output tiles to fill 256 CUs, with
 //    per-split fp32 partials summed in a deterministic finalize kernel.
+#include <algorithm>
+
 #include "conv_common.h"
 
 namespace atk {
@@ -401,10 +403,22 @@ __device__ __forceinline__ void store_tile(const IgArgs& a, f32x16 (&acc)[FCO][F
 
 // Tiles of 8 accumulator blocks (128 AGPRs) are asked to fit 2 waves per SIMD: with their
 // LDS footprint two workgroups share a CU, and one wave per SIMD leaves no latency cover.
-template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, int XC, bool VR, int KHT, int KWT, bool EPI>
-__global__ __launch_bounds__(64 * WCO * WSP)
-__attribute__((amdgpu_waves_per_eu((FCO * FSP >= 8 && CB == 16) || XC > 1 ? 2 : 1))) void conv_igemm_kernel(IgArgs a) {
-  constexpr int NT = 64 * WCO * WSP;
+//
+// KS > 1 splits K inside the workgroup: KS groups of WCO x WSP waves each take a contiguous
+// share of the stages, with patch buffers of their own, and run in lockstep (same iteration
+// count, shared barriers).  At the end groups 1..KS-1 hand their accumulators to group 0
+// through LDS, which adds them in group order (deterministic) and stores the tile.  Shapes
+// too small to fill the chip with one wave per SIMD (a few stages, one accumulator block per
+// wave) then get KS waves per SIMD and a KS-times shorter chain of stage latencies, in one
+// launch and with no partial sums in memory.
+template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, int XC, bool VR, int KHT, int KWT, bool EPI,
+          int KS = 1>
+__global__ __launch_bounds__(64 * WCO * WSP * KS)
+__attribute__((amdgpu_waves_per_eu(KS > 1 ? KS : ((FCO * FSP >= 8 && CB == 16) || XC > 1 ? 2 : 1))))
+void conv_igemm_kernel(IgArgs a) {
+  static_assert(KS == 1 || KHT > 0, "the in-workgroup K split runs on the static tap schedule");
+  constexpr int NWG = WCO * WSP;          // waves per K group
+  constexpr int NT = 64 * NWG;            // threads per K group (the tile's loaders)
   constexpr int KB = MfmaTraits<T>::KB, VEC = MfmaTraits<T>::VEC;
   constexpr int ES = sizeof(T);
   constexpr int CBS = CB + VEC;           // padded channel stride of a patch position
@@ -413,11 +427,15 @@ __attribute__((amdgpu_waves_per_eu((FCO * FSP >= 8 && CB == 16) || XC > 1 ? 2 : 
   constexpr uint32_t FRAG = 32 * KB * ES; // bytes of one packed weight fragment
   static_assert(CB % KB == 0, "chunk must hold whole k-blocks");
   extern __shared__ uint4 lds_raw[];
-  char* lds_bytes = reinterpret_cast<char*>(lds_raw);
+  char* lds_base = reinterpret_cast<char*>(lds_raw);
 
-  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int lane = threadIdx.x & 63;
+  const int kg = (threadIdx.x >> 6) / NWG;          // K group
+  const int tid = threadIdx.x - kg * NT, wv = tid >> 6;
   const int wco = wv % WCO, wsp = wv / WCO;
   const int half = lane >> 5, col = lane & 31;
+  // this K group's patch buffers
+  char* lds_bytes = lds_base + (size_t)kg * 2 * (size_t)a.patch_elems * sizeof(T);
 
   // ---- tile coordinates ---------------------------------------------------------------
   int t = blockIdx.x;
@@ -428,9 +446,13 @@ __attribute__((amdgpu_waves_per_eu((FCO * FSP >= 8 && CB == 16) || XC > 1 ? 2 : 
   const int co_tile = blockIdx.y;
   const int split = blockIdx.z;
   __shared__ float s_bias[BN];
-  stage_bias<T, BN, NT>(a, co_tile, s_bias);  // visible after the prologue's barrier
-  const int s_begin = split * a.stages_per_split;
-  const int s_end = min(a.n_stages, s_begin + a.stages_per_split);
+  if (kg == 0) stage_bias<T, BN, NT>(a, co_tile, s_bias);  // visible after the prologue's barrier
+  // stages of this split, then this K group's share of them; every group runs n_it iterations
+  const int sp_begin = split * a.stages_per_split;
+  const int sp_end = min(a.n_stages, sp_begin + a.stages_per_split);
+  const int n_it = KS == 1 ? sp_end - sp_begin : (sp_end - sp_begin + KS - 1) / KS;
+  const int s_begin = sp_begin + kg * n_it;
+  const int s_end = min(sp_end, s_begin + n_it);
   const int oy0 = ty_t * a.TY, ox0 = tx_t * a.TX;
   const int iy0 = oy0 * a.sh - a.ph, ix0 = ox0 * a.sw - a.pw;
   const int gx0 = (ix0 >= 0 ? ix0 / VEC : -((-ix0 + VEC - 1) / VEC)) * VEC;  // aligned-down start
@@ -508,9 +530,13 @@ __attribute__((amdgpu_waves_per_eu((FCO * FSP >= 8 && CB == 16) || XC > 1 ? 2 : 
     // so every wait is an exact vmcnt/lgkmcnt count.
     constexpr int NT2 = KHT * KWT;
     // NB rotating weight buffers (a divisor of NT2, so the rotation repeats every stage),
-    // prefetching PF taps ahead; only PF + 1 of them are live at once
-    constexpr int NB = NT2 % 3 == 0 ? 3 : NT2 % 5 == 0 ? 5 : 7;
-    constexpr int PF = NB - 1 < 3 ? NB - 1 : 3;
+    // prefetching PF taps ahead; only PF + 1 of them are live at once.  Tiles of one or two
+    // accumulator blocks (one output-channel block) run a tap's MFMAs in 32-64 cycles, far
+    // less than an L2 round trip, so they keep a whole 3x3 stage of weights in registers and
+    // prefetch 6 taps ahead.
+    constexpr bool DEEPW = FCO == 1 && FSP <= 2 && NT2 == 9;
+    constexpr int NB = DEEPW ? 9 : NT2 % 3 == 0 ? 3 : NT2 % 5 == 0 ? 5 : 7;
+    constexpr int PF = DEEPW ? 6 : NB - 1 < 3 ? NB - 1 : 3;
     constexpr int MAXC = PatchLoader<T, CB, VR, NT, XC>::MAXC;
     constexpr int NQ = PatchLoader<T, CB, VR, NT, XC>::NQ;
     static_assert(NT2 % NB == 0, "buffer rotation must repeat every stage");
@@ -519,7 +545,9 @@ __attribute__((amdgpu_waves_per_eu((FCO * FSP >= 8 && CB == 16) || XC > 1 ? 2 : 
     // chunks issued by tap 1), quads [QH, NQ) at tap QS1 (chunks issued by tap 3)
     constexpr int LPT = MAXC <= 8 ? 2 : MAXC / 4;
     constexpr int QH = (NQ + 1) / 2;
-    constexpr int QS0 = 5, QS1 = 8;
+    // (deep-prefetch tiles write the quads as late as the stage allows: their loads then
+    // have the longest time to arrive)
+    constexpr int QS0 = DEEPW ? 7 : 5, QS1 = 8;
     uint4 wb[NB][NKB][FCO];
     auto load_w = [&](uint4 (&w)[NKB][FCO], uint32_t so) {
 #pragma unroll
@@ -540,9 +568,10 @@ __attribute__((amdgpu_waves_per_eu((FCO * FSP >= 8 && CB == 16) || XC > 1 ? 2 : 
 #pragma unroll
       for (int j = 0; j < FSP; ++j) pf[j] = *reinterpret_cast<const uint4*>(lds_bytes + pbuf + pb[j] + toffb);
     };
-    for (int s = s_begin; s < s_end; ++s) {
+    for (int s = s_begin; s < s_begin + n_it; ++s) {
+      // (s >= s_end: a K group with fewer stages than n_it keeps the shared barriers)
       const int iz = iz_base + kd * a.dd;
-      const bool zin = (unsigned)iz < (unsigned)a.D;
+      const bool zin = s < s_end && (unsigned)iz < (unsigned)a.D;
       const uint32_t pbuf = ((s - s_begin) & 1) ? patch_bytes : 0u;
       const bool has_next = s + 1 < s_end;
       int cc1 = cc, kd1 = kd + 1;
@@ -669,6 +698,31 @@ __attribute__((amdgpu_waves_per_eu((FCO * FSP >= 8 && CB == 16) || XC > 1 ? 2 : 
     kd = kd1;
   }
 
+  if constexpr (KS > 1) {
+    // groups 1..KS-1 park their accumulators in LDS (the patch buffers are free: the last
+    // iteration ended with a barrier); group 0 adds them in group order
+    float* red = reinterpret_cast<float*>(lds_base);
+    auto slot = [&](int g, int i, int j, int r) {
+      return ((((g - 1) * NWG + wv) * FCO + i) * FSP + j) * 16 * 64 + r * 64 + lane;
+    };
+    if (kg > 0) {
+#pragma unroll
+      for (int i = 0; i < FCO; ++i)
+#pragma unroll
+        for (int j = 0; j < FSP; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) red[slot(kg, i, j, r)] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (kg > 0) return;
+    for (int g = 1; g < KS; ++g)
+#pragma unroll
+      for (int i = 0; i < FCO; ++i)
+#pragma unroll
+        for (int j = 0; j < FSP; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][j][r] += red[slot(g, i, j, r)];
+  }
   // GroupNorm record index of this wave's spatial tile: (z, tile row, tile column), then wave
   const int sp_rec = ((oz * a.tiles_y + ty_t) * a.tiles_x + tx_t) * WSP + wsp;
   store_tile<T, FCO, FSP, BN, EPI>(a, acc, s_bias, n, co_tile, split, oz, oy0, ox0, wco, wsp, half, col, sp_rec);
@@ -728,6 +782,7 @@ struct IgVariant {
   int wco, wsp, fco, fsp, cb;
   int xc;           // patch-loader capacity multiplier (PatchLoader XC)
   int max_splits;   // split-K limit (1: never split, so a call is one launch)
+  int ks = 1;       // K groups inside the workgroup (conv_igemm_kernel KS)
 };
 
 const IgVariant kIg[] = {
@@ -752,6 +807,14 @@ const IgVariant kIg[] = {
     {"h_w12_f21_cb32_ns", 0, 1, 2, 2, 1, 32, 1, 1},
     {"h_w22_f11_cb32_ns", 0, 2, 2, 1, 1, 32, 1, 1},
     {"h_w21_f12_cb32_ns", 0, 2, 1, 1, 2, 32, 1, 1},
+    // the same small tiles with K split inside the workgroup (2-4 waves per SIMD on shapes
+    // that give each SIMD one output tile)
+    {"h_w22_f11_cb32_k2", 0, 2, 2, 1, 1, 32, 1, 1, 2},
+    {"h_w22_f11_cb32_k3", 0, 2, 2, 1, 1, 32, 1, 1, 3},
+    {"h_w22_f11_cb16_k4", 0, 2, 2, 1, 1, 16, 1, 1, 4},
+    {"h_w12_f21_cb32_k2", 0, 1, 2, 2, 1, 32, 1, 1, 2},
+    {"f32_w22_f11_cb16_k2", 1, 2, 2, 1, 1, 16, 1, 1, 2},
+    {"f32_w22_f11_cb16_k3", 1, 2, 2, 1, 1, 16, 1, 1, 3},
 };
 constexpr int kNumIg = sizeof(kIg) / sizeof(kIg[0]);
 
@@ -770,7 +833,8 @@ int plan_ig(const ConvShape& p, int v, IgPlan& pl) {
   const int KB = f32 ? 8 : 16, VEC = f32 ? 4 : 8;
   pl.bn = vr.wco * vr.fco * 32;
   pl.bm = vr.wsp * vr.fsp * 32;
-  pl.nthreads = 64 * vr.wco * vr.wsp;
+  const int ntg = 64 * vr.wco * vr.wsp;  // threads of one K group (the patch loaders)
+  pl.nthreads = ntg * vr.ks;
   IgArgs& a = pl.a;
   a.N = p.N; a.Ci = p.Ci; a.D = p.D; a.H = p.H; a.W = p.W; a.Co = p.Co;
   a.KD = p.KD; a.KH = p.KH; a.KW = p.KW; a.sd = p.sd; a.sh = p.sh; a.sw = p.sw;
@@ -807,10 +871,13 @@ int plan_ig(const ConvShape& p, int v, IgPlan& pl) {
     a.PXS = a.NCX * VEC + (kLdsCu / padded == kLdsCu / plain ? row_pad : 0);
   }
   a.patch_elems = a.PY * a.PXS * (vr.cb + VEC);
-  pl.lds = (size_t)2 * a.patch_elems * es;
+  // two patch buffers per K group; with K groups, the accumulator hand-over reuses them
+  pl.lds = (size_t)2 * a.patch_elems * es * vr.ks;
+  if (vr.ks > 1)
+    pl.lds = std::max(pl.lds, (size_t)(vr.ks - 1) * vr.wco * vr.wsp * vr.fco * vr.fsp * 16 * 64 * 4);
   {
-    const int maxc = (f32 ? vr.cb / 2 : vr.cb / 4) * (256 / pl.nthreads) * vr.xc;  // PatchLoader::MAXC
-    if (pl.lds > 150 * 1024 || vr.cb * a.PY * a.NCX > maxc * pl.nthreads)
+    const int maxc = (f32 ? vr.cb / 2 : vr.cb / 4) * (256 / ntg) * vr.xc;  // PatchLoader::MAXC
+    if (pl.lds > 150 * 1024 || vr.cb * a.PY * a.NCX > maxc * ntg)
       return fail(ATK_UNSUPPORTED, "conv %s: stage of %zu LDS bytes does not fit the variant", vr.name, pl.lds);
   }
   a.n_stages = n_cc * p.KD;
@@ -855,25 +922,28 @@ int launch_ig_kern(const IgPlan& pl, int nthreads, hipStream_t s) {
   return check_launch("conv_igemm_kernel");
 }
 
-template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, int XC, bool VR, int KHT, int KWT>
+template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, int XC, bool VR, int KHT, int KWT, int KS = 1>
 int launch_ig_vr(const IgPlan& pl, hipStream_t s) {
+  constexpr int nt = 64 * WCO * WSP * KS;
   // the residual / GroupNorm epilogue is its own instantiation, so the plain kernel is unchanged
   if (pl.a.resid || pl.a.gn_parts) {
     if constexpr (VR)
-      return launch_ig_kern<conv_igemm_kernel<T, WCO, WSP, FCO, FSP, CB, XC, VR, KHT, KWT, true>>(pl, 64 * WCO * WSP, s);
+      return launch_ig_kern<conv_igemm_kernel<T, WCO, WSP, FCO, FSP, CB, XC, VR, KHT, KWT, true, KS>>(pl, nt, s);
     else
       return fail(ATK_UNSUPPORTED, "conv: the residual / GroupNorm epilogue needs 16-byte aligned input rows");
   }
-  return launch_ig_kern<conv_igemm_kernel<T, WCO, WSP, FCO, FSP, CB, XC, VR, KHT, KWT, false>>(pl, 64 * WCO * WSP, s);
+  return launch_ig_kern<conv_igemm_kernel<T, WCO, WSP, FCO, FSP, CB, XC, VR, KHT, KWT, false, KS>>(pl, nt, s);
 }
 
-template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, int XC = 1>
+template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, int XC = 1, int KS = 1>
 int launch_ig_t(const IgPlan& pl, hipStream_t s) {
   if (pl.a.KH == 3 && pl.a.KW == 3 && pl.a.vec_rows)
-    return launch_ig_vr<T, WCO, WSP, FCO, FSP, CB, XC, true, 3, 3>(pl, s);
+    return launch_ig_vr<T, WCO, WSP, FCO, FSP, CB, XC, true, 3, 3, KS>(pl, s);
   if (pl.a.KH == 7 && pl.a.KW == 7 && pl.a.vec_rows)
-    return launch_ig_vr<T, WCO, WSP, FCO, FSP, CB, XC, true, 7, 7>(pl, s);
-  if constexpr (XC > 1) {
+    return launch_ig_vr<T, WCO, WSP, FCO, FSP, CB, XC, true, 7, 7, KS>(pl, s);
+  if constexpr (KS > 1) {
+    return fail(ATK_UNSUPPORTED, "conv: the in-workgroup K split needs a 3x3 or 7x7 plane and 16-byte aligned rows");
+  } else if constexpr (XC > 1) {
     // the element-wise loader of unaligned rows spills at this capacity
     if (!pl.a.vec_rows) return fail(ATK_UNSUPPORTED, "conv: this tile needs 16-byte aligned input rows");
     return launch_ig_vr<T, WCO, WSP, FCO, FSP, CB, XC, true, 0, 0>(pl, s);
@@ -941,6 +1011,10 @@ int run_ig(const ConvShape& p, IgPlan& pl, const void* x, const void* wp, const 
       case 14: rc = launch_ig_t<T, 1, 2, 2, 1, 32>(pl, s); break;
       case 15: rc = launch_ig_t<T, 2, 2, 1, 1, 32>(pl, s); break;
       case 16: rc = launch_ig_t<T, 2, 1, 1, 2, 32>(pl, s); break;
+      case 17: rc = launch_ig_t<T, 2, 2, 1, 1, 32, 1, 2>(pl, s); break;
+      case 18: rc = launch_ig_t<T, 2, 2, 1, 1, 32, 1, 3>(pl, s); break;
+      case 19: rc = launch_ig_t<T, 2, 2, 1, 1, 16, 1, 4>(pl, s); break;
+      case 20: rc = launch_ig_t<T, 1, 2, 2, 1, 32, 1, 2>(pl, s); break;
       default: return fail(ATK_EINVAL, "conv: bad variant");
     }
   } else {
@@ -949,6 +1023,8 @@ int run_ig(const ConvShape& p, IgPlan& pl, const void* x, const void* wp, const 
       case 10: rc = launch_ig_t<T, 1, 4, 2, 2, 16>(pl, s); break;
       case 11: rc = launch_ig_t<T, 2, 2, 1, 2, 16>(pl, s); break;
       case 12: rc = launch_ig_t<T, 2, 1, 1, 4, 16>(pl, s); break;
+      case 21: rc = launch_ig_t<T, 2, 2, 1, 1, 16, 1, 2>(pl, s); break;
+      case 22: rc = launch_ig_t<T, 2, 2, 1, 1, 16, 1, 3>(pl, s); break;
       default: return fail(ATK_EINVAL, "conv: bad variant");
     }
   }

@@ -51,6 +51,9 @@ CONV3D = [
     ((1, 4, 7, 8, 9), (6, 4, 3, 2, 3), (2, 1, 1), (1, 0, 2), (1, 2, 1)),
     ((1, 32, 8, 16, 16), (64, 32, 3, 3, 3), 1, 1, 1),
     ((1, 8, 9, 9, 9), (8, 8, 5, 5, 5), 1, 2, 1),
+    # stage counts that the in-workgroup K split divides unevenly (some K groups idle)
+    ((1, 40, 5, 12, 16), (32, 40, 3, 3, 3), 1, 1, 1),
+    ((1, 16, 6, 16, 16), (16, 16, 7, 7, 7), 1, 3, 1),
 ]
 
 
