@@ -815,6 +815,8 @@ const IgVariant kIg[] = {
     {"h_w12_f21_cb32_k2", 0, 1, 2, 2, 1, 32, 1, 1, 2},
     {"f32_w22_f11_cb16_k2", 1, 2, 2, 1, 1, 16, 1, 1, 2},
     {"f32_w22_f11_cb16_k3", 1, 2, 2, 1, 1, 16, 1, 1, 3},
+    // the 7x7-plane tile with two K groups: half the split-K partials in memory
+    {"h_w14_f22_cb16x2_k2", 0, 1, 4, 2, 2, 16, 2, 16, 2},
 };
 constexpr int kNumIg = sizeof(kIg) / sizeof(kIg[0]);
 
@@ -884,11 +886,12 @@ int plan_ig(const ConvShape& p, int v, IgPlan& pl) {
   pl.tiles = (int64_t)p.N * p.Do * a.tiles_y * a.tiles_x;
   const int co_tiles = (p.Co + pl.bn - 1) / pl.bn;
   if (pl.tiles > 0x7fffffff || co_tiles > 65535) return fail(ATK_UNSUPPORTED, "conv %s: grid too large", vr.name);
-  // split K (stages) until the grid covers the chip about twice
+  // split K (stages) until the grid covers the chip about twice (a workgroup with K groups
+  // counts as that many workgroups)
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
-  const int64_t wgs = pl.tiles * co_tiles;
+  const int64_t wgs = pl.tiles * co_tiles * vr.ks;
   int splits = 1;
-  while (wgs * splits < 2 * cus && splits * 2 <= a.n_stages && splits * 2 <= vr.max_splits) splits *= 2;
+  while (wgs * splits < 2 * cus && splits * 2 * vr.ks <= a.n_stages && splits * 2 <= vr.max_splits) splits *= 2;
   a.stages_per_split = (a.n_stages + splits - 1) / splits;
   splits = (a.n_stages + a.stages_per_split - 1) / a.stages_per_split;
   pl.splits = splits;
@@ -1015,6 +1018,7 @@ int run_ig(const ConvShape& p, IgPlan& pl, const void* x, const void* wp, const 
       case 18: rc = launch_ig_t<T, 2, 2, 1, 1, 32, 1, 3>(pl, s); break;
       case 19: rc = launch_ig_t<T, 2, 2, 1, 1, 16, 1, 4>(pl, s); break;
       case 20: rc = launch_ig_t<T, 1, 2, 2, 1, 32, 1, 2>(pl, s); break;
+      case 23: rc = launch_ig_t<T, 1, 4, 2, 2, 16, 2, 2>(pl, s); break;
       default: return fail(ATK_EINVAL, "conv: bad variant");
     }
   } else {
