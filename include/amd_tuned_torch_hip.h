@@ -293,8 +293,12 @@ int atk_group_norm_cl_fwd(const void* x, const void* gamma, const void* beta, vo
  * dgamma / dbeta: [C] fp32.  Any of dx / dgamma / dbeta may be NULL.  The group
  * statistics are recomputed from x with the forward's eps.  Needs S * sizeof(dtype)
  * to be a multiple of 16 and 16-byte aligned x / dy / dx (else ATK_UNSUPPORTED).
- * The workspace (atk_group_norm_bwd_workspace_bytes) needs no initialisation.
- * Sums over n are taken in a fixed order (deterministic).
+ * The first 16 KiB of the workspace (atk_group_norm_bwd_workspace_bytes) must be zero
+ * before the first call that uses it; every call leaves them zero (per-group counters).
+ * Sums over n are taken in a fixed order (deterministic).  Groups of up to 8192 16-byte
+ * vectors whose spatial size is a multiple of 64 vectors run register-resident (x and dy
+ * read once) when a group has at most 512 channels; other shapes take two kernels that
+ * read x and dy twice.
  * ------------------------------------------------------------------------- */
 size_t atk_group_norm_bwd_workspace_bytes(int64_t N, int64_t C);
 int atk_group_norm_bwd(const void* x, const void* dy, const void* gamma, void* dx, float* dgamma,

@@ -1100,6 +1100,216 @@ void launch_gn_bwd_u(const GnBwdArgs& a, int64_t rows, hipStream_t s) {
   hipLaunchKernelGGL((gn_bwd_apply_kernel<T, U>), dim3((unsigned)rows), dim3(GN_TP_NT), 0, s, a);
 }
 
+// ---------------------------------------------------------------------------------------
+// Register-resident backward: one workgroup per group (n, g) holds the group's x and dy in
+// registers (up to NT * EPV 16-byte vectors of each), so x and dy are read once and dx
+// written once -- 3 tensor passes instead of the rows / apply pair's 5.  In one pass over
+// the registers after the statistics (mu, rstd of x, as the forward computes them):
+//   A = sum gamma_c dy,  B = sum gamma_c dy (x - mu)   -> c1 = A / E,  c2 = B rstd / E,
+//   dx = rstd (gamma_c dy - c1 - (x - mu) rstd c2).
+// Parameter gradients: each wave's segment of 64 vectors lies in one channel (host check:
+// S a multiple of 64 vectors), so per-channel sums of dy (x - mu) rstd and dy are wave sums,
+// added per channel in (vector, wave) order into a row per (n, c), stored with agent-scope
+// atomic stores by wave 0, which then counts the workgroup in on a per-group counter while
+// the other waves write dx.  The last of the group's N workgroups adds the N rows of its
+// channels in n order (deterministic) and resets the counter: no workgroup waits for
+// another, and every launch leaves the counters zero (HIP-graph replay safe).  A second
+// kernel for the sums over n cost more (a dependent launch's gap).
+constexpr int GN_BWD_MAXG = 4096;                        // groups per launch (counters)
+constexpr size_t GN_BWD_CNT_BYTES = 4 * (size_t)GN_BWD_MAXG;
+constexpr int GN_BWD_RES_NT = 1024;
+
+struct GnBwdResArgs {
+  const void* x;
+  const void* dy;
+  const void* gamma;
+  void* dx;            // may be null
+  float* dgamma;       // [C] or null
+  float* dbeta;        // [C] or null
+  uint32_t* counter;   // [G], zero on entry and on exit
+  float* part;         // [N][C][2]: sum dy (x - mu) rstd, sum dy of (n, c)
+  int64_t E;           // cpg * S
+  uint32_t S, cpg, C, G;
+  int N;
+  float eps;
+  int pdt;
+  FastDiv div_s;
+};
+
+template <typename T, int NT, int EPV>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(4)))
+void gn_bwd_resident_kernel(GnBwdResArgs a) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int NW = NT / 64;
+  __shared__ float red[NW];
+  __shared__ float s_gam[GN_MAX_AFF];
+  __shared__ float2 s_part[EPV][NW];
+  __shared__ float2 s_rows[NT];
+  __shared__ uint32_t s_prev;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int64_t gi = blockIdx.x;
+  const int n = (int)(gi / a.G), g = (int)(gi - (int64_t)n * a.G);
+  const int cpg = (int)a.cpg;
+  const int64_t E = a.E;
+  const int64_t c0 = (int64_t)g * cpg;  // the group's first channel
+
+  // gamma word first (loads complete in issue order: issued after x / dy it would wait for them)
+  uint32_t gsel;
+  const uint32_t gword = param_word(a.gamma, a.pdt, c0 + (tid < cpg ? tid : 0), (int64_t)a.C, gsel);
+  const uint32_t bytes = (uint32_t)(E * (int64_t)sizeof(T));
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(static_cast<const T*>(a.x) + gi * E, bytes);
+  const __amdgpu_buffer_rsrc_t rd = make_rsrc(static_cast<const T*>(a.dy) + gi * E, bytes);
+  const uint32_t lane_off = (uint32_t)tid * 16u;
+  const uint32_t n_vec = (uint32_t)(E / VEC);
+  auto voff = [&](int i) { return (uint32_t)(i * NT + tid) < n_vec ? lane_off : kOOB; };
+  auto soff = [&](int i) { return (uint32_t)i * NT * 16u; };
+  Vec16<T> xb[EPV], db[EPV];
+#pragma unroll
+  for (int i = 0; i < EPV; ++i) xb[i].raw = bload16<2>(rx, voff(i), soff(i));
+#pragma unroll
+  for (int i = 0; i < EPV; ++i) db[i].raw = bload16<2>(rd, voff(i), soff(i));
+  if (tid < cpg) s_gam[tid] = a.gamma ? param_decode(gword, gsel, a.pdt) : 1.f;
+
+  // statistics of x, bit-identical to the forward's single-slice arithmetic (the barriers
+  // inside also publish s_gam)
+  float mean, m2;
+  slice_stats<T, NT, EPV, true>(xb, nullptr, 0, E, E, red, mean, m2);
+  const float rstd = 1.0f / sqrtf(m2 / (float)E + a.eps);
+
+  // per thread: A, B and, per vector, sum dy (x - mu) and sum dy.  Each vector pair is
+  // fenced together with the running sums, so it is unpacked only after the previous one is
+  // accumulated (left free, the compiler unpacks every vector up front and spills).
+  float A = 0.f, B = 0.f;
+  const bool params = a.dgamma || a.dbeta;
+#pragma unroll
+  for (int i = 0; i < EPV; ++i) {
+    asm volatile("" : "+v"(xb[i].raw.x), "+v"(xb[i].raw.y), "+v"(xb[i].raw.z), "+v"(xb[i].raw.w),
+                 "+v"(db[i].raw.x), "+v"(db[i].raw.y), "+v"(db[i].raw.z), "+v"(db[i].raw.w), "+v"(A), "+v"(B));
+    const bool ok = (uint32_t)(i * NT + tid) < n_vec;
+    const uint32_t e = ok ? (uint32_t)((i * NT + tid) * VEC) : 0u;
+    const float gm = s_gam[fdiv(e, a.div_s)];
+    float sg = 0.f, sb = 0.f;
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+      const float d = to_f32(db[i].e[k]);
+      const float xc = to_f32(xb[i].e[k]) - mean;
+      sb += d;
+      sg = fmaf(d, xc, sg);
+    }
+    // out-of-range vectors read zeros: d = 0 adds nothing
+    A = fmaf(gm, sb, A);
+    B = fmaf(gm, sg, B);
+    if (params) {  // the wave's segment sums, right away (nothing stays live for later)
+      const float wg = wave_sum(sg), wb = wave_sum(sb);
+      if (lane == 0) s_part[i][wv] = make_float2(wg, wb);
+    }
+  }
+  reg_fence<T, EPV>(xb);
+  reg_fence<T, EPV>(db);
+  const float c1 = block_sum<NT>(A, red) / (float)E;
+  const float c2 = block_sum<NT>(B, red) * rstd / (float)E;
+
+  uint32_t prev = 0;  // thread 0: the group counter before this workgroup's count
+  if (params && wv == 0) {
+    // Wave 0 alone (lane l for channels l, l + 64, ...) writes the rows and counts the
+    // workgroup in, so the wait for the row stores is the wave's own and the other waves go
+    // on to write dx meanwhile.  s_part is complete: the block sums above contain barriers.
+    // Segment q = i * NW + w covers elements [q, q + 1) * 64 * VEC, so channel c owns
+    // segments [c, c + 1) * spc.
+    const int spc = (int)(a.S / (64 * VEC));
+    const float2* seg = &s_part[0][0];
+    for (int c = lane; c < cpg; c += 64) {
+      float sg = 0.f, sb = 0.f;
+      for (int q = c * spc; q < (c + 1) * spc; ++q) {  // in order
+        sg += seg[q].x;
+        sb += seg[q].y;
+      }
+      uint32_t* row = reinterpret_cast<uint32_t*>(a.part + ((int64_t)n * a.C + c0 + c) * 2);
+      __hip_atomic_store(row, __float_as_uint(sg * rstd), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(row + 1, __float_as_uint(sb), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // the wave's rows are complete before it counts the workgroup done (issued before this
+    // wave's dx stores, so this waits for the row stores only)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    if (tid == 0) prev = __hip_atomic_fetch_add(a.counter + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  if (a.dx) {
+    T* __restrict__ dxg = static_cast<T*>(a.dx) + gi * E;
+#pragma unroll
+    for (int i = 0; i < EPV; ++i) {
+      // vector i is unpacked only after store i-1 has issued
+      reg_fence<T, 1>(&xb[i]);
+      reg_fence<T, 1>(&db[i]);
+      const bool ok = (uint32_t)(i * NT + tid) < n_vec;
+      const uint32_t e = ok ? (uint32_t)((i * NT + tid) * VEC) : 0u;
+      const float gm = s_gam[fdiv(e, a.div_s)];
+      float v[VEC];
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) {
+        const float xh = (to_f32(xb[i].e[k]) - mean) * rstd;
+        v[k] = rstd * (gm * to_f32(db[i].e[k]) - c1 - xh * c2);
+      }
+      if (ok) st16<true>(dxg + e, pack16<T>(v));
+    }
+  }
+
+  if (params) {
+    if (tid == 0) s_prev = prev;
+    __syncthreads();
+    if (s_prev == (uint32_t)a.N - 1) {
+      // last of the group's N workgroups: every row of the group is written.  The N x cpg
+      // rows are fetched NT at a time, one per thread with all loads in flight, staged in
+      // LDS and added per channel in n order.
+      const int per = NT / cpg;  // samples per round (cpg <= NT)
+      float sg = 0.f, sb = 0.f;
+      for (int m0 = 0; m0 < a.N; m0 += per) {
+        const int m = m0 + tid / cpg, c = tid - (tid / cpg) * cpg;
+        if (tid < per * cpg && m < a.N) {
+          const uint32_t* row = reinterpret_cast<const uint32_t*>(a.part + ((int64_t)m * a.C + c0 + c) * 2);
+          s_rows[tid] = make_float2(
+              __uint_as_float(__hip_atomic_load(row, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)),
+              __uint_as_float(__hip_atomic_load(row + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)));
+        }
+        __syncthreads();
+        if (tid < cpg) {
+          const int mn = min(per, a.N - m0);
+          for (int k = 0; k < mn; ++k) {
+            sg += s_rows[k * cpg + tid].x;
+            sb += s_rows[k * cpg + tid].y;
+          }
+        }
+        __syncthreads();
+      }
+      if (tid < cpg) {
+        if (a.dgamma) a.dgamma[c0 + tid] = sg;
+        if (a.dbeta) a.dbeta[c0 + tid] = sb;
+      }
+      if (tid == 0) __hip_atomic_store(a.counter + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// vectors per thread the resident backward needs for (cpg, S), or 0 when it does not apply
+inline int gn_bwd_resident_epv(int64_t N, int64_t C, int64_t S, int G, int dtype) {
+  const int64_t vec = 16 / (int64_t)dtype_size(dtype);
+  const int64_t cpg = C / G, E = cpg * S;
+  if (S % (64 * vec) || cpg > GN_MAX_AFF || G > GN_BWD_MAXG || N * G >= (1ll << 31) || N * C >= (1ll << 30))
+    return 0;
+  const int64_t per = (int64_t)GN_BWD_RES_NT * vec;
+  if (E > 8 * per) return 0;
+  return E <= 2 * per ? 2 : E <= 4 * per ? 4 : 8;
+}
+
+template <typename T>
+int launch_gn_bwd_resident(const GnBwdResArgs& a, int epv, hipStream_t s) {
+  const dim3 grid((unsigned)((int64_t)a.N * a.G)), block(GN_BWD_RES_NT);
+  if (epv == 2) hipLaunchKernelGGL((gn_bwd_resident_kernel<T, GN_BWD_RES_NT, 2>), grid, block, 0, s, a);
+  else if (epv == 4) hipLaunchKernelGGL((gn_bwd_resident_kernel<T, GN_BWD_RES_NT, 4>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((gn_bwd_resident_kernel<T, GN_BWD_RES_NT, 8>), grid, block, 0, s, a);
+  return check_launch("gn_bwd_resident_kernel");
+}
+
 template <typename T>
 int launch_gn_bwd(const GnBwdArgs& a, int64_t rows, hipStream_t s) {
   // vectors per thread and batch: no more than a row holds (C3a's 4096-element rows are two
@@ -1873,7 +2083,9 @@ extern "C" int atk_group_norm_apply(const void* x, const void* gamma, const void
 
 extern "C" size_t atk_group_norm_bwd_workspace_bytes(int64_t N, int64_t C) {
   if (N <= 0 || C <= 0) return 0;
-  return (size_t)N * (size_t)C * 5 * sizeof(float);  // per (n, c) row: mean, M2, A, B, K
+  // per-group counters of the resident kernel (zero between launches), then per (n, c) row:
+  // mean, M2, A, B, K (the rows / apply pair) or the resident kernel's two sums
+  return atk::GN_BWD_CNT_BYTES + (size_t)N * (size_t)C * 5 * sizeof(float);
 }
 
 extern "C" int atk_group_norm_bwd(const void* x, const void* dy, const void* gamma, void* dx, float* dgamma,
@@ -1896,13 +2108,30 @@ extern "C" int atk_group_norm_bwd(const void* x, const void* dy, const void* gam
   if (rows >= (1ll << 31) || C >= (1ll << 31) || N >= (1ll << 31))
     return fail(ATK_UNSUPPORTED, "group_norm backward: too many rows");
   if (S * es >= (1ll << 31)) return fail(ATK_UNSUPPORTED, "group_norm backward: rows over 2 GiB (32-bit buffer offsets)");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int epv = gn_bwd_resident_epv(N, C, S, G, dtype);
+  if (epv) {
+    GnBwdResArgs r;
+    r.x = x; r.dy = dy; r.gamma = gamma; r.dx = dx;
+    r.dgamma = dgamma; r.dbeta = dbeta;
+    r.counter = static_cast<uint32_t*>(workspace);
+    r.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + GN_BWD_CNT_BYTES);
+    r.E = (C / G) * S;
+    r.S = (uint32_t)S; r.cpg = (uint32_t)(C / G); r.C = (uint32_t)C; r.G = (uint32_t)G;
+    r.N = (int)N; r.eps = eps; r.pdt = param_dtype;
+    r.div_s = make_fastdiv((uint32_t)S);
+    switch (dtype) {
+      case ATK_F32: return launch_gn_bwd_resident<float>(r, epv, s);
+      case ATK_F16: return launch_gn_bwd_resident<_Float16>(r, epv, s);
+      default: return launch_gn_bwd_resident<__bf16>(r, epv, s);
+    }
+  }
   GnBwdArgs a;
   a.x = x; a.dy = dy; a.gamma = gamma; a.dx = dx;
-  a.rows = static_cast<float*>(workspace);
+  a.rows = reinterpret_cast<float*>(static_cast<char*>(workspace) + GN_BWD_CNT_BYTES);
   a.dgamma = dgamma; a.dbeta = dbeta;
   a.S = S; a.C = (uint32_t)C; a.cpg = (uint32_t)(C / G); a.N = (int)N;
   a.eps = eps; a.pdt = param_dtype;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (dtype) {
     case ATK_F32: return launch_gn_bwd<float>(a, rows, s);
     case ATK_F16: return launch_gn_bwd<_Float16>(a, rows, s);

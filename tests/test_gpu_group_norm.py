@@ -238,6 +238,10 @@ BWD_SHAPES = [
     ((2, 12, 4, 6, 8), 3, False),     # 3-D spatial, no affine
     ((3, 10, 24), 5, True),           # 1-D spatial
     ((8, 512, 16, 16), 32, True),     # C3-like channel count
+    # register-resident backward (spatial size a multiple of 64 vectors, group <= 8192 vectors)
+    ((4, 64, 32, 32), 8, True),
+    ((3, 96, 16, 32), 6, False),      # three samples per group counter, no affine
+    ((1, 32, 8, 64, 64), 4, True),    # one sample, groups of the largest resident size (16-bit)
 ]
 
 
@@ -298,6 +302,42 @@ def test_group_norm_autograd_channels_last(dev, dtype):
         assert O.max_rel_err(gx.cpu().contiguous(), rdx) <= BAR[dtype]
         assert O.max_rel_err(gg.cpu(), rdg) <= BAR[dtype]
         assert O.max_rel_err(gb.cpu(), rdb) <= BAR[dtype]
+
+
+@pytest.mark.parametrize("needs", [(True, False, False), (False, True, True), (True, True, False)],
+                         ids=["dx_only", "params_only", "dx_dgamma"])
+def test_group_norm_backward_resident_subsets(dev, needs):
+    """The register-resident backward with some gradients not asked for; two calls in a row
+    (the per-group counters must be left zero by the first)."""
+    nat = _native()
+    shape, G = (2, 64, 16, 64), 8
+    x, gm, _ = _inputs(shape, torch.bfloat16, seed=77)
+    dy = torch.randn(*shape, generator=torch.Generator().manual_seed(78)).to(torch.bfloat16)
+    rdx, rdg, rdb = O.group_norm_bwd(x, G, gm, dy, 1e-5)
+    for _ in range(2):
+        dx, dg, db = nat.group_norm_backward(dy.to(dev), x.to(dev), G, gm.to(dev), 1e-5, needs)
+        torch.cuda.synchronize()
+        for got, ref, want, bar in ((dx, rdx, needs[0], BAR[torch.bfloat16]),
+                                    (dg, rdg, needs[1], BWD_BAR_P[torch.bfloat16]),
+                                    (db, rdb, needs[2], BWD_BAR_P[torch.bfloat16])):
+            assert (got is not None) == want
+            if want:
+                assert O.max_rel_err(got.cpu(), ref) <= bar
+
+
+def test_group_norm_backward_c3a_full_size(dev):
+    """C3's NCHW shape at full size, bf16 (the register-resident backward): every gradient
+    element against the oracle."""
+    nat = _native()
+    shape, G = (8, 512, 64, 64), 32
+    x, gm, _ = _inputs(shape, torch.bfloat16, seed=3005)
+    dy = torch.randn(*shape, generator=torch.Generator().manual_seed(3006)).to(torch.bfloat16)
+    dx, dg, db = nat.group_norm_backward(dy.to(dev), x.to(dev), G, gm.to(dev), 1e-5, (True, True, True))
+    torch.cuda.synchronize()
+    rdx, rdg, rdb = O.group_norm_bwd(x, G, gm, dy, 1e-5)
+    assert O.max_rel_err(dx.cpu(), rdx) <= BAR[torch.bfloat16]
+    assert O.max_rel_err(dg.cpu(), rdg) <= BWD_BAR_P[torch.bfloat16]
+    assert O.max_rel_err(db.cpu(), rdb) <= BWD_BAR_P[torch.bfloat16]
 
 
 def test_group_norm_backward_c3_full_size(dev):
