@@ -545,7 +545,8 @@ def bench_gn_cl_detail(shape, G, silu, dev):
 def bench_gn_backward_detail(shape, G, dev):
     """GroupNorm backward (dx, dgamma, dbeta), bf16: native kernels against the torch-op
     backward that the reference uses.  Algorithmic bytes: read x and dy, write dx (the
-    kernels make 5 tensor-passes: x and dy are read twice)."""
+    register-resident kernel makes exactly these 3 tensor-passes; the rows / apply pair, for
+    groups too large for one workgroup, makes 5: x and dy are read twice)."""
     import torch
     from amd_tuned_torch import _native as nat
     from amd_tuned_torch import _dispatch
@@ -562,8 +563,13 @@ def bench_gn_backward_detail(shape, G, dev):
     torch_ms = event_time_ms(lambda: _dispatch._group_norm_backward(dy, x, G, gm, 1e-5, (True, True, True)), 10)
     nbytes = 3 * x.numel() * x.element_size()
     gbs = nbytes / (ms * 1e-3) / 1e9
+    # the library's rule for the register-resident kernel (atk_group_norm_bwd): spatial size a
+    # multiple of 64 16-byte vectors, at most 512 channels and 8192 vectors per group
+    S, vec, cpg = x.numel() // (shape[0] * C), 16 // x.element_size(), C // G
+    resident = S % (64 * vec) == 0 and cpg <= 512 and cpg * S <= 8192 * vec
     return {"ms": round(ms, 4), "GB/s": round(gbs, 1), "roofline_frac": round(gbs / HBM_PEAK_GBS, 4),
-            "variant": "native gn_bwd_rows/apply", "torch_op_backward_ms": round(torch_ms, 4),
+            "variant": "native gn_bwd_resident_kernel" if resident else "native gn_bwd_rows/apply",
+            "torch_op_backward_ms": round(torch_ms, 4),
             "max_rel_err_vs_fp32_torch_ops": float(f"{err:.3g}")}
 
 
