@@ -380,6 +380,22 @@ int atk_conv_fwd_prepacked(const void* x, const void* packed, size_t packed_byte
                            atk_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * atk_conv_fwd_prepacked on channels-last tensors: x [N, D, H, W, Ci] and y [N, Do, Ho, Wo,
+ * Co] in memory (NDHWC; conv2d NHWC with D = KD = 1), the same packed weights, geometry
+ * arguments (logical sizes), arithmetic and workspace.  The reference serves channels-last
+ * convs with CK or stock (amd_tuned_torch/_dispatch.py:1813,1947, contest key with the memory
+ * format kernel_select.py:438-445); here the MFMA tiles stage channels-last patches straight
+ * into LDS, with no layout conversion.  16-bit dtypes, a 3x3 or 7x7 (kh, kw) plane, Ci and Co
+ * multiples of 8 and 16-byte aligned x and y; otherwise ATK_UNSUPPORTED.
+ * ------------------------------------------------------------------------- */
+int atk_conv_fwd_prepacked_cl(const void* x, const void* packed, size_t packed_bytes,
+                              const void* bias, void* y, int64_t N, int64_t Ci, int64_t D,
+                              int64_t H, int64_t W, int64_t Co, int KD, int KH, int KW, int sd,
+                              int sh, int sw, int pd, int ph, int pw, int dd, int dh, int dw,
+                              int dtype, int variant, void* workspace, size_t workspace_bytes,
+                              atk_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Conv epilogue fusion (the reference fuses GroupNorm+SiLU before a conv and names
  * "Conv -> +residual" as the epilogue to fuse, amd_tuned_torch/conv_fusion_ops.py:1-40,
  * 355-439): atk_conv_fwd_prepacked with, on an unsplit launch,

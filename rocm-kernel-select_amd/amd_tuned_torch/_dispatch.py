@@ -361,9 +361,16 @@ def _to_ncdhw(t: torch.Tensor) -> torch.Tensor:
 
 def _in_ncdhw(fn: Callable, cl_out: bool, nd: int) -> Callable:
     """`fn` on contiguous (NC(D)HW) copies of input and weight; the output converted to
-    channels-last when `cl_out`.  The conversions run on the native transpose kernel."""
+    channels-last when `cl_out`.  The conversions run on the native transpose kernel.  A
+    channels-last input first goes to the MFMA tiles that stage channels-last patches
+    directly (no conversions); shapes they decline take the conversions."""
 
     def run(i, w, b, s, p, d, variant: int = -1):
+        if cl_out:
+            try:
+                return _native.conv_channels_last(i, w, b, s, p, d, nd, variant=variant)
+            except _native.Unsupported:
+                pass
         y = fn(_to_ncdhw(i), _to_ncdhw(w), b, s, p, d, variant=variant)
         return _native.contiguous_to_channels_last(y) if cl_out else y
     return run

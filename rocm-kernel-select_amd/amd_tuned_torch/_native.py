@@ -45,7 +45,8 @@ EXPORTED_SYMBOLS = (
     "atk_conv_fwd", "atk_conv_wgrad_workspace_bytes", "atk_conv_wgrad", "atk_transpose_last2",
     "atk_dwconv1d_bwd", "atk_group_norm_noalloc_scratch_bytes", "atk_group_norm_fwd_noalloc",
     "atk_conv_packed_weight_bytes", "atk_conv_prepacked_workspace_bytes", "atk_conv_pack_weights",
-    "atk_conv_fwd_prepacked", "atk_conv_gn_stats_bytes", "atk_conv_gn_records", "atk_conv_fwd_prepacked_ex",
+    "atk_conv_fwd_prepacked", "atk_conv_fwd_prepacked_cl", "atk_conv_gn_stats_bytes", "atk_conv_gn_records",
+    "atk_conv_fwd_prepacked_ex",
     "atk_group_norm_apply", "atk_group_norm_cl_bwd_workspace_bytes", "atk_group_norm_cl_bwd",
 )
 
@@ -122,6 +123,8 @@ def _declare(lib) -> None:
     lib.atk_conv_pack_weights.restype = i32
     lib.atk_conv_fwd_prepacked.argtypes = [vp, vp, sz, vp, vp] + conv_geom + [i32, i32, vp, sz, vp]
     lib.atk_conv_fwd_prepacked.restype = i32
+    lib.atk_conv_fwd_prepacked_cl.argtypes = [vp, vp, sz, vp, vp] + conv_geom + [i32, i32, vp, sz, vp]
+    lib.atk_conv_fwd_prepacked_cl.restype = i32
     lib.atk_conv_gn_stats_bytes.argtypes = conv_geom + [i32, i32, i32]
     lib.atk_conv_gn_stats_bytes.restype = sz
     lib.atk_conv_gn_records.argtypes = conv_geom + [i32, i32, i32]
@@ -973,14 +976,17 @@ def packed_weight_cache_size() -> int:
 
 def _packed_conv_weights(weight: torch.Tensor, geom: tuple, dt: int, variant: int, nbytes: int,
                          stream: int) -> torch.Tensor:
-    """The packed form of `weight` for (geometry, variant) on `stream`: cached, or packed now."""
+    """The packed form of `weight` for (geometry, variant) on `stream`: cached, or packed now.
+    A weight in another memory layout (channels-last) is keyed as itself and read through a
+    contiguous copy only when it has to be packed."""
     key = (id(weight), weight.data_ptr(), weight._version, geom, dt, variant, stream)
     with _pack_lock:
         hit = _packed.get(key)
         if hit is not None and hit[0]() is weight:
             return hit[1]
     packed = torch.empty(nbytes, dtype=torch.uint8, device=weight.device)
-    rc = lib().atk_conv_pack_weights(_ptr(weight), _ptr(packed), nbytes, *geom, dt, variant, stream)
+    src = weight if weight.is_contiguous() else weight.contiguous()
+    rc = lib().atk_conv_pack_weights(_ptr(src), _ptr(packed), nbytes, *geom, dt, variant, stream)
     _check(rc, "conv weight packing")
     if _PACK_CACHE_ON:
         def forget(_ref, key=key):
@@ -1076,6 +1082,61 @@ def _conv(input, weight, bias, stride, padding, dilation, nd: int, variant: int,
     rc = L.atk_conv_fwd(_ptr(input), _ptr(weight), _ptr(bias), _ptr(y), *geom, dt, int(variant),
                         ws_ptr, ws_len, _stream(input))
     _check(rc, f"conv{nd}d")
+    return y
+
+
+def conv_channels_last(input, weight, bias, stride, padding, dilation, nd: int, *, variant: int):
+    """conv2d / conv3d on a channels-last input (NHWC / NDHWC memory) with the MFMA tiles
+    staging channels-last patches directly (atk_conv_fwd_prepacked_cl): the output comes back
+    channels-last, as stock returns it.  The weight may be in either layout.  Raises
+    Unsupported where the channels-last tiles do not apply (fp32, planes other than 3x3 /
+    7x7, channel counts that are not multiples of 8, misaligned tensors)."""
+    fmt = torch.channels_last_3d if nd == 3 else torch.channels_last
+    if input.dim() != nd + 2 or weight.dim() != nd + 2 or not input.is_contiguous(memory_format=fmt):
+        raise Unsupported(f"conv{nd}d (channels-last): input must be a channels-last {nd + 2}D tensor")
+    if input.dtype not in (torch.float16, torch.bfloat16) or weight.dtype != input.dtype:
+        raise Unsupported("conv (channels-last): float16 / bfloat16 input and weight")
+    _require_cuda(input, weight, bias)
+    if weight.shape[1] != input.shape[1]:
+        raise RuntimeError("weight.size(1) must equal input channels (groups=1 only)")
+    if bias is not None:
+        if bias.numel() != weight.shape[0] or bias.dtype != input.dtype:
+            raise RuntimeError("Bias shape/dtype mismatch")
+        bias = bias.contiguous()
+    if variant <= 0:
+        raise Unsupported("conv (channels-last): an MFMA variant is needed")
+    s, p, d = _ntuple(stride, nd), _ntuple(padding, nd), _ntuple(dilation, nd)
+    N, Ci = input.shape[:2]
+    Co = weight.shape[0]
+    if nd == 2:
+        D, (H, W) = 1, input.shape[2:]
+        KD, (KH, KW) = 1, weight.shape[2:]
+        s, p, d = (1,) + s, (0,) + p, (1,) + d
+    else:
+        D, H, W = input.shape[2:]
+        KD, KH, KW = weight.shape[2:]
+    osz = [conv_out_size(i, k, ss, pp, dd)
+           for i, k, ss, pp, dd in zip((D, H, W), (KD, KH, KW), s, p, d)]
+    if min(osz) <= 0:
+        raise RuntimeError("Conv output size must be positive")
+    shape = (N, Co, *osz) if nd == 3 else (N, Co, osz[1], osz[2])
+    y = torch.empty(shape, dtype=input.dtype, device=input.device, memory_format=fmt)
+    if y.numel() == 0:
+        return y
+    L = lib()
+    dt = _DTYPE_CODE[input.dtype]
+    geom = (N, Ci, D, H, W, Co, KD, KH, KW, *s, *p, *d)
+    dev = _device_index(input.device)
+    packed_bytes = _cached_size(L.atk_conv_packed_weight_bytes, *geom, dt, int(variant), device=dev)
+    if not packed_bytes:
+        raise Unsupported(f"conv{nd}d (channels-last): variant {variant} does not take the shape")
+    stream = _raw_stream(input.device)
+    packed = _packed_conv_weights(weight, geom, dt, int(variant), packed_bytes, stream)
+    nws = _cached_size(L.atk_conv_prepacked_workspace_bytes, *geom, dt, int(variant), device=dev)
+    ws = workspace(input.device, "conv", nws, stream) if nws else None
+    rc = L.atk_conv_fwd_prepacked_cl(_ptr(input), _ptr(packed), packed_bytes, _ptr(bias), _ptr(y), *geom, dt,
+                                     int(variant), _ptr(ws), ws.numel() if ws is not None else 0, stream)
+    _check(rc, f"conv{nd}d (channels-last)")
     return y
 
 

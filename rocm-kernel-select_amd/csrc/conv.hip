@@ -198,6 +198,21 @@ extern "C" int atk_conv_fwd_prepacked(const void* x, const void* packed, size_t 
                                   reinterpret_cast<hipStream_t>(stream));
 }
 
+extern "C" int atk_conv_fwd_prepacked_cl(const void* x, const void* packed, size_t packed_bytes, const void* bias,
+                                         void* y, ATK_CONV_GEOM_ARGS, int variant, void* workspace,
+                                         size_t workspace_bytes, atk_stream_t stream) {
+  using namespace atk;
+  ConvShape p;
+  int rc = conv_shape(ATK_CONV_GEOM, p);
+  if (rc) return rc;
+  if (variant <= 0 || variant >= conv_num_variants())
+    return fail(variant == 0 ? ATK_UNSUPPORTED : ATK_EINVAL, "conv: variant %d has no packed weights", variant);
+  if (N == 0) return ATK_OK;
+  if (!x || !y) return fail(ATK_EINVAL, "conv: null pointer");
+  return conv_igemm_run_prepacked(p, x, packed, packed_bytes, bias, y, variant - 1, workspace, workspace_bytes,
+                                  reinterpret_cast<hipStream_t>(stream), nullptr, nullptr, 0, 0, true);
+}
+
 extern "C" size_t atk_conv_gn_stats_bytes(ATK_CONV_GEOM_ARGS, int variant, int groups) {
   using namespace atk;
   ConvShape p;

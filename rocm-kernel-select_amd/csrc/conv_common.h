@@ -29,7 +29,7 @@ int conv_igemm_pack(const ConvShape& p, const void* w, void* packed, size_t pack
 int conv_igemm_run_prepacked(const ConvShape& p, const void* x, const void* packed, size_t packed_bytes,
                              const void* bias, void* y, int v, void* ws, size_t ws_bytes, hipStream_t s,
                              const void* resid = nullptr, void* gn_stats = nullptr, size_t gn_stats_bytes = 0,
-                             int gn_G = 0);
+                             int gn_G = 0, bool channels_last = false);
 size_t conv_igemm_gn_stats_bytes(const ConvShape& p, int v, int G);
 int conv_igemm_gn_records(const ConvShape& p, int v, int G);
 

@@ -240,6 +240,69 @@ struct PatchLoader {
   }
 };
 
+// Patch staging from a channels-last input (x[n][z][y][x][ci], NDHWC / NHWC).  A 16-byte
+// chunk of memory is 8 consecutive channels of one position, which is exactly the patch's
+// LDS layout (patch[(py * PXS + px) * CBS + cl]), so each chunk goes to LDS as one 16-byte
+// store with no transposition.  Chunk c of a stage is (position p = c / (CB/8), channel
+// octet c % (CB/8)), positions row-major over PY x PX from (iy0, ix0); chunks outside the
+// input (padding) read zero.  Same interface as PatchLoader (MAXC chunks per thread, NQ
+// groups of four written together), so the tap schedules drive either.  Needs Ci % 8 == 0
+// and 16-byte aligned x (host check).  16-bit types only.
+template <typename T, int CB, int NTH = 256, int XC = 1>
+struct PatchLoaderCL {
+  static_assert(sizeof(T) == 2, "channels-last staging is for 16-bit types");
+  static constexpr int MAXC = CB / 4 * (256 / NTH) * XC;
+  static constexpr int NQ = MAXC / 4;
+  static constexpr int CO8 = CB / 8;  // chunks per position
+  uint4 buf[MAXC];
+  uint32_t goff[MAXC];  // element offset in the sample without the stage term
+  int clim[MAXC];       // the chunk's first channel inside the CB block, or a huge value
+  uint32_t loff[MAXC];  // LDS element offset
+  int total;            // chunks of a stage
+
+  __device__ __forceinline__ void init(const IgArgs& a, int iy0, int ix0, int /*total_quads*/, int tid, int nt) {
+    constexpr int CBS = CB + 8;
+    const int PX = a.PX;
+    total = a.PY * PX * CO8;
+#pragma unroll
+    for (int u = 0; u < MAXC; ++u) {
+      const int c = tid + u * nt;
+      const int p = c / CO8, o8 = c - (c / CO8) * CO8;
+      const int py = p / PX, px = p - (p / PX) * PX;
+      const int iy = iy0 + py, ix = ix0 + px;
+      const bool ok = c < total && (unsigned)iy < (unsigned)a.H && (unsigned)ix < (unsigned)a.W;
+      goff[u] = ok ? (uint32_t)(((iy * a.W + ix) * a.Ci) + o8 * 8) : 0u;
+      clim[u] = ok ? o8 * 8 : (1 << 30);
+      loff[u] = (uint32_t)((py * a.PXS + px) * CBS + o8 * 8);
+    }
+  }
+  __device__ __forceinline__ static uint32_t stage_off(const IgArgs& a, int cc, int iz) {
+    return (uint32_t)(iz * a.H * a.W * a.Ci + cc * CB);
+  }
+  __device__ __forceinline__ static int stage_lim(const IgArgs& a, int cc, int iz, bool valid) {
+    return (valid && (unsigned)iz < (unsigned)a.D) ? a.Ci - cc * CB : 0;
+  }
+  __device__ __forceinline__ void load_fast(__amdgpu_buffer_rsrc_t rx, int u, uint32_t soff_el, int lim) {
+    buf[u] = bload16(rx, clim[u] < lim ? (goff[u] + soff_el) * (uint32_t)sizeof(T) : kOOB, 0);
+  }
+  __device__ __forceinline__ void store_quad(T* patch, int g, int /*total_quads*/, int tid, int nt) const {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int u = 4 * g + k;
+      if (tid + u * nt < total) *reinterpret_cast<uint4*>(patch + loff[u]) = buf[u];
+    }
+  }
+};
+
+template <typename T, int CB, bool VR, int NTH, int XC, bool CL>
+struct LoaderSel {
+  using type = PatchLoader<T, CB, VR, NTH, XC>;
+};
+template <typename T, int CB, bool VR, int NTH, int XC>
+struct LoaderSel<T, CB, VR, NTH, XC, true> {
+  using type = PatchLoaderCL<T, CB, NTH, XC>;
+};
+
 // Bias of the workgroup's BN output channels as fp32 in LDS (zero without bias or when
 // writing split-K partials), staged before the main loop: read per element in the epilogue
 // from global memory, every element would wait for its own load.
@@ -327,11 +390,43 @@ __device__ __forceinline__ void tile_gn_records(const IgArgs& a, const GnLaneSta
 // Epilogue: accumulator rows = output channels, columns = positions.  Writes y (bias and the
 // optional residual added, converted) or, under split-K, this split's fp32 partial sums; on an
 // unsplit launch with gn_parts set it also writes the GroupNorm records of the stored values.
-template <typename T, int FCO, int FSP, int BN, bool EPI>
+template <typename T, int FCO, int FSP, int BN, bool EPI, bool CL = false>
 __device__ __forceinline__ void store_tile(const IgArgs& a, f32x16 (&acc)[FCO][FSP], const float* s_bias,
                                            int n, int co_tile, int split, int oz, int oy0, int ox0, int wco,
                                            int wsp, int half, int col, int sp_rec) {
   const int64_t spo = (int64_t)a.Do * a.Ho * a.Wo;
+  if constexpr (CL) {
+    // channels-last output y[n][sp][co]: a lane's 4 consecutive channels (r & 3) of one
+    // position go out as one 8-byte store (fp32 partials: one 16-byte store); Co % 8 == 0
+#pragma unroll
+    for (int j = 0; j < FSP; ++j) {
+      const int m = (wsp * FSP + j) * 32 + col;
+      const int ty = m / a.TX, tx = m - (m / a.TX) * a.TX;
+      const int oy = oy0 + ty, ox = ox0 + tx;
+      if (oy >= a.Ho || ox >= a.Wo) continue;
+      const int64_t base = ((int64_t)n * spo + ((int64_t)oz * a.Ho + oy) * a.Wo + ox) * a.Co;
+#pragma unroll
+      for (int i = 0; i < FCO; ++i) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int cl = (wco * FCO + i) * 32 + q * 8 + half * 4;
+          const int co = co_tile * BN + cl;
+          if (co >= a.Co) continue;
+          if (a.part) {
+            *reinterpret_cast<float4*>(a.part + (int64_t)split * a.N * a.Co * spo + base + co) =
+                make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+          } else {
+            float v[8] = {acc[i][j][4 * q] + s_bias[cl], acc[i][j][4 * q + 1] + s_bias[cl + 1],
+                          acc[i][j][4 * q + 2] + s_bias[cl + 2], acc[i][j][4 * q + 3] + s_bias[cl + 3],
+                          0.f, 0.f, 0.f, 0.f};
+            const uint4 pk = pack16<T>(v);
+            *reinterpret_cast<uint2*>(static_cast<T*>(a.y) + base + co) = make_uint2(pk.x, pk.y);
+          }
+        }
+      }
+    }
+    return;
+  }
   if constexpr (EPI) {
     // opaque copies of the lane coordinates: the address math below then cannot be hoisted
     // above the main loop, where its results would stay live (and cost registers) throughout
@@ -412,11 +507,13 @@ __device__ __forceinline__ void store_tile(const IgArgs& a, f32x16 (&acc)[FCO][F
 // wave) then get KS waves per SIMD and a KS-times shorter chain of stage latencies, in one
 // launch and with no partial sums in memory.
 template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, int XC, bool VR, int KHT, int KWT, bool EPI,
-          int KS = 1>
+          int KS = 1, bool CL = false>
 __global__ __launch_bounds__(64 * WCO * WSP * KS)
 __attribute__((amdgpu_waves_per_eu(KS > 1 ? KS : ((FCO * FSP >= 8 && CB == 16) || XC > 1 ? 2 : 1))))
 void conv_igemm_kernel(IgArgs a) {
   static_assert(KS == 1 || KHT > 0, "the in-workgroup K split runs on the static tap schedule");
+  static_assert(!CL || (KHT > 0 && VR && !EPI), "channels-last staging runs on the static tap schedule");
+  using Loader = typename LoaderSel<T, CB, VR, 64 * WCO * WSP, XC, CL>::type;
   constexpr int NWG = WCO * WSP;          // waves per K group
   constexpr int NT = 64 * NWG;            // threads per K group (the tile's loaders)
   constexpr int KB = MfmaTraits<T>::KB, VEC = MfmaTraits<T>::VEC;
@@ -455,7 +552,8 @@ void conv_igemm_kernel(IgArgs a) {
   const int s_end = min(sp_end, s_begin + n_it);
   const int oy0 = ty_t * a.TY, ox0 = tx_t * a.TX;
   const int iy0 = oy0 * a.sh - a.ph, ix0 = ox0 * a.sw - a.pw;
-  const int gx0 = (ix0 >= 0 ? ix0 / VEC : -((-ix0 + VEC - 1) / VEC)) * VEC;  // aligned-down start
+  // aligned-down start of the patch rows (channels-last rows need no alignment along x)
+  const int gx0 = CL ? ix0 : (ix0 >= 0 ? ix0 / VEC : -((-ix0 + VEC - 1) / VEC)) * VEC;
   const int mis = ix0 - gx0;
   const int total_chunks = CB * a.PY * a.NCX;
 
@@ -487,7 +585,7 @@ void conv_igemm_kernel(IgArgs a) {
   const int ntaps2d = a.KH * a.KW;
   const int co_blk0 = co_tile * (BN / 32) + wco * FCO;
 
-  PatchLoader<T, CB, VR, NT, XC> ld;
+  Loader ld;
   const int total_quads = total_chunks / 4;
   if constexpr (VR) ld.init(a, iy0, gx0, total_quads, tid, NT);
   // stage s = (channel chunk cc, kernel plane kd), walked incrementally
@@ -499,9 +597,9 @@ void conv_igemm_kernel(IgArgs a) {
       const uint32_t so = ld.stage_off(a, cc, iz);
       const int lim = ld.stage_lim(a, cc, iz, true);
 #pragma unroll
-      for (int u = 0; u < PatchLoader<T, CB, VR, NT, XC>::MAXC; ++u) ld.load_fast(rx, u, so, lim);
+      for (int u = 0; u < Loader::MAXC; ++u) ld.load_fast(rx, u, so, lim);
 #pragma unroll
-      for (int g = 0; g < PatchLoader<T, CB, VR, NT, XC>::NQ; ++g)
+      for (int g = 0; g < Loader::NQ; ++g)
         ld.store_quad(reinterpret_cast<T*>(lds_bytes), g, total_quads, tid, NT);
     } else {
       ld.load(a, rx, cc, iz_base + kd * a.dd, iy0, gx0, total_chunks, tid, NT);
@@ -537,8 +635,8 @@ void conv_igemm_kernel(IgArgs a) {
     constexpr bool DEEPW = FCO == 1 && FSP <= 2 && NT2 == 9;
     constexpr int NB = DEEPW ? 9 : NT2 % 3 == 0 ? 3 : NT2 % 5 == 0 ? 5 : 7;
     constexpr int PF = DEEPW ? 6 : NB - 1 < 3 ? NB - 1 : 3;
-    constexpr int MAXC = PatchLoader<T, CB, VR, NT, XC>::MAXC;
-    constexpr int NQ = PatchLoader<T, CB, VR, NT, XC>::NQ;
+    constexpr int MAXC = Loader::MAXC;
+    constexpr int NQ = Loader::NQ;
     static_assert(NT2 % NB == 0, "buffer rotation must repeat every stage");
     static_assert(NQ >= 1 && NQ <= 4 && NT2 >= 9, "schedule below assumes <= 4 quads, 9+ taps");
     // chunks are issued LPT per tap over taps 0-3; quads [0, QH) are written at tap QS0 (their
@@ -634,7 +732,7 @@ void conv_igemm_kernel(IgArgs a) {
       const uint32_t so1 = __builtin_amdgcn_readfirstlane(ld.stage_off(a, cc1, iz1));
       const int lim1 = __builtin_amdgcn_readfirstlane(ld.stage_lim(a, cc1, iz1, has_next));
 #pragma unroll
-      for (int u = 0; u < PatchLoader<T, CB, VR, NT, XC>::MAXC; ++u) ld.load_fast(rx, u, so1, lim1);
+      for (int u = 0; u < Loader::MAXC; ++u) ld.load_fast(rx, u, so1, lim1);
     } else {
       ld.load(a, rx, cc1, iz_base + kd1 * a.dd, iy0, gx0, total_chunks, tid, NT, has_next);
     }
@@ -687,7 +785,7 @@ void conv_igemm_kernel(IgArgs a) {
     if (has_next) {
       if constexpr (VR) {
 #pragma unroll
-        for (int g = 0; g < PatchLoader<T, CB, VR, NT, XC>::NQ; ++g)
+        for (int g = 0; g < Loader::NQ; ++g)
           ld.store_quad(reinterpret_cast<T*>(lds_bytes + (pbuf ^ patch_bytes)), g, total_quads, tid, NT);
       } else {
         ld.store(a, reinterpret_cast<T*>(lds_bytes + (pbuf ^ patch_bytes)), total_chunks, tid, NT);
@@ -725,7 +823,7 @@ void conv_igemm_kernel(IgArgs a) {
   }
   // GroupNorm record index of this wave's spatial tile: (z, tile row, tile column), then wave
   const int sp_rec = ((oz * a.tiles_y + ty_t) * a.tiles_x + tx_t) * WSP + wsp;
-  store_tile<T, FCO, FSP, BN, EPI>(a, acc, s_bias, n, co_tile, split, oz, oy0, ox0, wco, wsp, half, col, sp_rec);
+  store_tile<T, FCO, FSP, BN, EPI, CL>(a, acc, s_bias, n, co_tile, split, oz, oy0, ox0, wco, wsp, half, col, sp_rec);
 }
 
 // Packed weights Wp[tap][kb][co_block][32][KB] from w[Co][Ci][taps]; zero beyond Co / Ci.
@@ -764,15 +862,16 @@ __global__ __launch_bounds__(256) void pack_weights_kernel(const T* __restrict__
 }
 
 // y = sum over splits of the fp32 partials + bias
+// (cl: y and the partials channels-last, so element i is channel i % Co)
 template <typename T>
 __global__ __launch_bounds__(256) void splitk_finalize_kernel(const float* __restrict__ part, const T* __restrict__ bias,
                                                               T* __restrict__ y, int splits, int Co, int64_t spo,
-                                                              int64_t total) {
+                                                              int64_t total, int cl) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= total) return;
   float v = 0.f;
   for (int s = 0; s < splits; ++s) v += part[(int64_t)s * total + i];
-  if (bias) v += to_f32(bias[(i / spo) % Co]);
+  if (bias) v += to_f32(bias[cl ? i % Co : (i / spo) % Co]);
   y[i] = from_f32<T>(v);
 }
 
@@ -822,6 +921,7 @@ constexpr int kNumIg = sizeof(kIg) / sizeof(kIg[0]);
 
 struct IgPlan {
   IgArgs a;
+  bool cl = false;  // channels-last x and y (NDHWC / NHWC)
   int bn, bm, splits, nthreads;
   size_t lds, wp_bytes, part_bytes;
   int64_t tiles;
@@ -928,6 +1028,12 @@ int launch_ig_kern(const IgPlan& pl, int nthreads, hipStream_t s) {
 template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, int XC, bool VR, int KHT, int KWT, int KS = 1>
 int launch_ig_vr(const IgPlan& pl, hipStream_t s) {
   constexpr int nt = 64 * WCO * WSP * KS;
+  if (pl.cl) {
+    if constexpr (sizeof(T) == 2 && VR && KHT > 0)
+      return launch_ig_kern<conv_igemm_kernel<T, WCO, WSP, FCO, FSP, CB, XC, VR, KHT, KWT, false, KS, true>>(pl, nt, s);
+    else
+      return fail(ATK_UNSUPPORTED, "conv (channels-last): 16-bit types with a 3x3 or 7x7 plane only");
+  }
   // the residual / GroupNorm epilogue is its own instantiation, so the plain kernel is unchanged
   if (pl.a.resid || pl.a.gn_parts) {
     if constexpr (VR)
@@ -944,6 +1050,8 @@ int launch_ig_t(const IgPlan& pl, hipStream_t s) {
     return launch_ig_vr<T, WCO, WSP, FCO, FSP, CB, XC, true, 3, 3, KS>(pl, s);
   if (pl.a.KH == 7 && pl.a.KW == 7 && pl.a.vec_rows)
     return launch_ig_vr<T, WCO, WSP, FCO, FSP, CB, XC, true, 7, 7, KS>(pl, s);
+  if (pl.cl)
+    return fail(ATK_UNSUPPORTED, "conv (channels-last): needs a 3x3 or 7x7 plane, Ci %% 8 == 0 and aligned tensors");
   if constexpr (KS > 1) {
     return fail(ATK_UNSUPPORTED, "conv: the in-workgroup K split needs a 3x3 or 7x7 plane and 16-byte aligned rows");
   } else if constexpr (XC > 1) {
@@ -980,9 +1088,13 @@ int gn_records(const ConvShape& p, const IgPlan& pl, int v, int G) {
 
 template <typename T>
 int run_ig(const ConvShape& p, IgPlan& pl, const void* x, const void* wp, const void* bias, void* y, int v,
-           float* part, hipStream_t s, const void* resid = nullptr, float4* gn_parts = nullptr, int gn_G = 0) {
+           float* part, hipStream_t s, const void* resid = nullptr, float4* gn_parts = nullptr, int gn_G = 0,
+           bool cl = false) {
   int rc = ATK_OK;
   IgArgs& a = pl.a;
+  pl.cl = cl;
+  if (cl && (sizeof(T) != 2 || resid || gn_parts || p.Ci % 8 || p.Co % 8))
+    return fail(ATK_UNSUPPORTED, "conv (channels-last): 16-bit types, Ci and Co multiples of 8, no epilogue extras");
   a.x = x; a.bias = bias; a.y = y;
   a.resid = resid;
   a.gn_parts = gn_parts;
@@ -993,7 +1105,8 @@ int run_ig(const ConvShape& p, IgPlan& pl, const void* x, const void* wp, const 
     return fail(ATK_UNSUPPORTED, "conv: the residual / GroupNorm epilogue needs an unsplit launch");
   if (gn_parts && a.gn_np == 0)
     return fail(ATK_UNSUPPORTED, "conv: GroupNorm statistics need Co/G in {4, 8, 16, 32} or a multiple of 32");
-  a.vec_rows = (p.W % (16 / (int)sizeof(T)) == 0) && aligned16(x);
+  // 16-byte patch chunks: along x rows (NCDHW) or along channels (channels-last)
+  a.vec_rows = cl ? (aligned16(x) && aligned16(y)) : (p.W % (16 / (int)sizeof(T)) == 0) && aligned16(x);
   a.x_sample_bytes = (uint32_t)((int64_t)p.Ci * p.D * p.H * p.W * sizeof(T));
   a.wp_bytes = (uint32_t)pl.wp_bytes;
   a.wp = wp;
@@ -1036,7 +1149,7 @@ int run_ig(const ConvShape& p, IgPlan& pl, const void* x, const void* wp, const 
   const int64_t ysz = (int64_t)p.N * p.Co * p.Do * p.Ho * p.Wo;
   const int64_t spo = (int64_t)p.Do * p.Ho * p.Wo;
   hipLaunchKernelGGL((splitk_finalize_kernel<T>), dim3((unsigned)((ysz + 255) / 256)), dim3(256), 0, s,
-                     a.part, static_cast<const T*>(bias), static_cast<T*>(y), pl.splits, p.Co, spo, ysz);
+                     a.part, static_cast<const T*>(bias), static_cast<T*>(y), pl.splits, p.Co, spo, ysz, cl ? 1 : 0);
   return check_launch("splitk_finalize_kernel");
 }
 
@@ -1112,7 +1225,7 @@ int conv_igemm_gn_records(const ConvShape& p, int v, int G) {
 
 int conv_igemm_run_prepacked(const ConvShape& p, const void* x, const void* packed, size_t packed_bytes,
                              const void* bias, void* y, int v, void* ws, size_t ws_bytes, hipStream_t s,
-                             const void* resid, void* gn_stats, size_t gn_stats_bytes, int gn_G) {
+                             const void* resid, void* gn_stats, size_t gn_stats_bytes, int gn_G, bool cl) {
   if (v < 0 || v >= kNumIg) return fail(ATK_EINVAL, "conv: variant out of range");
   const int64_t ysz = (int64_t)p.N * p.Co * p.Do * p.Ho * p.Wo;
   if (ysz >= (1ll << 31)) return fail(ATK_UNSUPPORTED, "conv: output too large for the split-K finalize");
@@ -1133,9 +1246,9 @@ int conv_igemm_run_prepacked(const ConvShape& p, const void* x, const void* pack
     gp = static_cast<float4*>(gn_stats);
   }
   switch (p.dtype) {
-    case ATK_F32: return run_ig<float>(p, pl, x, packed, bias, y, v, part, s, resid, gp, gn_G);
-    case ATK_F16: return run_ig<_Float16>(p, pl, x, packed, bias, y, v, part, s, resid, gp, gn_G);
-    default: return run_ig<__bf16>(p, pl, x, packed, bias, y, v, part, s, resid, gp, gn_G);
+    case ATK_F32: return run_ig<float>(p, pl, x, packed, bias, y, v, part, s, resid, gp, gn_G, cl);
+    case ATK_F16: return run_ig<_Float16>(p, pl, x, packed, bias, y, v, part, s, resid, gp, gn_G, cl);
+    default: return run_ig<__bf16>(p, pl, x, packed, bias, y, v, part, s, resid, gp, gn_G, cl);
   }
 }
 

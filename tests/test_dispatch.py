@@ -228,6 +228,31 @@ def test_conv_channels_last_contests_native_on_nchw_copies(monkeypatch, contest)
     assert kernel_select.cached("conv2d", x.contiguous(), w, 1, 1, 1) is None  # layout in the key
 
 
+def test_conv_channels_last_16bit_takes_the_channels_last_tiles(monkeypatch, contest):
+    """A 16-bit channels-last input goes to the tiles that stage channels-last patches
+    (no layout conversions); where they decline, the NC(D)HW copies are used."""
+    fake = FakeNative(monkeypatch, ["h_a", "h_b"], ["res"])
+    cl_calls = []
+
+    def conv_cl(input, weight, bias, stride, padding, dilation, nd, *, variant):
+        cl_calls.append(variant)
+        if variant == 2:
+            raise _native.Unsupported("declined")
+        ref = _dispatch._ORIGINALS[(F, "conv%dd" % nd)](input.float(), weight.float(),
+                                                       None if bias is None else bias.float(),
+                                                       stride, padding, dilation)
+        return ref.to(input.dtype).contiguous(memory_format=torch.channels_last)
+    monkeypatch.setattr(_native, "conv_channels_last", conv_cl)
+    contest.update({"native.h_a": 0.5, "native.h_b": 0.4, "stock": 2.0})
+    x = torch.randn(1, 8, 6, 6).to(torch.bfloat16).to(memory_format=torch.channels_last)
+    w = torch.randn(8, 8, 3, 3).to(torch.bfloat16)
+    y = F.conv2d(x, w, None, 1, 1)
+    assert set(cl_calls) == {1, 2}                           # both candidates tried the tiles
+    assert ("conv2d", "h_a") not in fake.calls               # h_a ran channels-last, no copy
+    assert ("conv2d", "h_b") in fake.calls                   # h_b declined: NCHW copies
+    assert y.is_contiguous(memory_format=torch.channels_last)
+
+
 def test_group_norm_contest_and_key(monkeypatch, contest):
     fake = FakeNative(monkeypatch, ["f32_a"], ["res_a", "twopass"])
     monkeypatch.setattr(_dispatch, "_group_norm_candidates",

@@ -266,6 +266,73 @@ def test_channels_last_conv_through_patched_functional(nd, dtype):
     assert y2.is_contiguous(memory_format=fmt) and O.max_rel_err(y2.float().contiguous(), ref) <= bar
 
 
+CL_NATIVE_CASES = [
+    # xshape (logical NC[D]HW), wshape, padding: 3x3(x3) and 7x7x7 planes, edges, odd sizes
+    ((1, 32, 6, 20, 20), (48, 32, 3, 3, 3), 1),
+    ((2, 64, 4, 9, 13), (32, 64, 3, 3, 3), 1),
+    ((1, 16, 5, 12, 12), (16, 16, 7, 7, 7), 3),
+    ((2, 40, 17, 11), (24, 40, 3, 3), 1),
+    ((1, 256, 2, 16, 16), (64, 256, 1, 3, 3), (0, 1, 1)),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("case", CL_NATIVE_CASES, ids=lambda c: "x".join(map(str, c[0])) + "_w" + "x".join(map(str, c[1])))
+def test_conv_channels_last_native_tiles(dev, case, dtype):
+    """The MFMA tiles on channels-last input (atk_conv_fwd_prepacked_cl) against the same
+    variant on the NC(D)HW copy: bit-identical (same patch values, same MFMA order), the
+    output channels-last; one variant also against the float64 oracle.  Channels-last and
+    contiguous weights give the same packed weights."""
+    nat = _native()
+    xs, ws, pad = case
+    nd = len(xs) - 2
+    x, w, b = _inputs(xs, ws, dtype, seed=sum(xs))
+    fmt = torch.channels_last_3d if nd == 3 else torch.channels_last
+    xd, wd, bd = x.to(dev), w.to(dev), b.to(dev)
+    xcl = xd.contiguous(memory_format=fmt)
+    plain = nat.conv3d if nd == 3 else nat.conv2d
+    ran = 0
+    for vi, name in _variants_for(dtype):
+        if name == "direct":
+            continue
+        try:
+            ycl = nat.conv_channels_last(xcl, wd, bd, 1, pad, 1, nd, variant=vi)
+        except nat.Unsupported:
+            continue
+        assert ycl.is_contiguous(memory_format=fmt)
+        try:
+            y = plain(xd, wd, bd, 1, pad, 1, variant=vi)
+        except nat.Unsupported:  # the NC(D)HW tile needs 16-byte rows along x: check values only
+            y = None
+        torch.cuda.synchronize()
+        if y is not None:
+            assert ycl.shape == y.shape and torch.equal(ycl.contiguous(), y), name
+        if ran == 0 or y is None:
+            ref = (O.conv3d if nd == 3 else O.conv2d)(x, w, b, 1, pad, 1)
+            assert O.max_rel_err(ycl.float().contiguous().cpu(), ref) <= BAR[dtype], name
+        if ran == 0:
+            ycw = nat.conv_channels_last(xcl, wd.contiguous(memory_format=fmt), bd, 1, pad, 1, nd, variant=vi)
+            assert torch.equal(ycw, ycl), name
+        ran += 1
+    assert ran >= 3
+
+
+def test_conv_channels_last_native_declines():
+    """fp32, planes other than 3x3 / 7x7 and channel counts off multiples of 8 are declined
+    (the dispatch then converts layouts for the NC(D)HW tiles)."""
+    nat = _native()
+    names = nat.variants(nat.OP_CONV)
+    vi = names.index("h_w22_f22_cb32")
+    for xs, ws, dt in [((1, 16, 4, 8, 8), (16, 16, 3, 3, 3), torch.float32),
+                       ((1, 16, 4, 8, 8), (16, 16, 5, 5, 5), torch.bfloat16),
+                       ((1, 12, 4, 8, 8), (16, 12, 3, 3, 3), torch.bfloat16)]:
+        x = torch.randn(*xs, device="cuda", dtype=dt).contiguous(memory_format=torch.channels_last_3d)
+        w = torch.randn(*ws, device="cuda", dtype=dt)
+        vv = names.index("f32_w22_f22_cb16") if dt == torch.float32 else vi
+        with pytest.raises(nat.Unsupported):
+            nat.conv_channels_last(x, w, None, 1, 1, 1, 3, variant=vv)
+
+
 TRANSPOSE_CASES = [
     # (B, R, C): vector path, odd rows / columns (element path), partial tiles, one row
     (2, 4096, 256), (1, 64, 64), (3, 100, 40), (2, 67, 13), (1, 1, 520), (5, 33, 1),
