@@ -750,7 +750,9 @@ def bench_conv_dgrad_detail(xs, ws, pad, dtype, dev, iters=10):
 
 def calibration(dev):
     """Achievable ceilings on this box: a large bf16 GEMM through torch.matmul (hipBLASLt),
-    and torch's device copy at the tensor sizes the HBM-bound configs move."""
+    and torch's device copy at the tensor sizes the HBM-bound configs move, replayed on one
+    buffer pair (cache-warm, as the GroupNorm `ms` figures) and over rotating buffers larger
+    than the Infinity Cache (cold, as the GroupNorm `cold_ms` figures)."""
     import torch
     out = {}
     n = 8192
@@ -767,6 +769,10 @@ def calibration(dev):
         ms = graph_time_ms(lambda: dst.copy_(src), 20)
         copies[label] = {"us": round(ms * 1e3, 2),
                          "GB/s": round(2 * numel * 2 / (ms * 1e-3) / 1e9, 1)}
+        if numel * 2 < (256 << 20):
+            cold = cold_graph_time_ms(lambda xi, yi: yi.copy_(xi), src, 2 * numel * 2)
+            copies[label].update({"cold_us": round(cold * 1e3, 2),
+                                  "cold_roofline_frac": round(2 * numel * 2 / (cold * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
         del src, dst
     out["torch_copy_bf16"] = copies
     torch.cuda.empty_cache()
