@@ -1562,6 +1562,485 @@ int launch_gn_cl(const GnClArgs& a, int N, int silu, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------------------
+// Channels-last GroupNorm forward, register-resident single pass (same semantics as the
+// kernels above; one read and one write of the tensor, one launch).  A workgroup owns a
+// chunk of SC consecutive positions of sample n, all C channels: NT threads x EPV 16-byte
+// vectors, vector i of thread t being element (i * NT + t) * VEC of the chunk, i.e. column
+// v = t % CV (channels v*VEC .. v*VEC+VEC-1, inside one group) at position i * R + t / CV
+// (CV = C / VEC, R = NT / CV).  It loads its chunk once, computes every group's (mean, M2)
+// over the chunk, publishes them in slots, obtains every group's statistics over the sample
+// and normalises from its registers.  Two ways to obtain them:
+//   direct     every workgroup merges all G x NCH chunk records of its sample (G x NCH small);
+//   two-level  workgroup g < G of a sample merges group g's NCH records and publishes the
+//              group's (mean, var) in a second slot; every workgroup then reads the G results.
+// Slots are tagged with an epoch held in the workspace header.  Every workgroup reads it at
+// its start; the last workgroup of the launch to finish reading slots (counted per block of
+// 64 workgroups, then per block) advances it and resets the counters.  A slot written by any
+// earlier launch -- including an earlier replay of the same HIP graph -- never carries the
+// current tag, so no slot ever needs clearing.  Every wait is bounded by wall-clock time: a chunk record that
+// has not appeared is computed by the waiting workgroup from x with the owner's arithmetic
+// (bit-identical), so the result never depends on which workgroups are resident; the host
+// only launches grids that fit at once, since stand-ins are slow.
+// ---------------------------------------------------------------------------------------
+constexpr int GN_CLR_MAXNCH = 1024;              // chunks per sample
+constexpr int GN_CLR_DIRECT = 1024;              // records merged by every workgroup (direct)
+constexpr int64_t GN_CLR_MAX_SLOTS = 65536;      // N x G x NCH chunk records
+constexpr int64_t GN_CLR_MAX_FINALS = 16384;     // N x G group results (two-level)
+// workspace: diagnostics word [0], epoch [64], launch counter [128], block counters (one
+// per 64 workgroups, 128 bytes apart) from [256]; slots; group results
+constexpr int GN_CLR_BLOCK = 64;                 // workgroups per block counter
+constexpr int GN_CLR_MAXBLK = 64;                // block counters: at most 4096 workgroups
+constexpr size_t GN_CLR_SLOTS_OFF = 256 + 128 * (size_t)GN_CLR_MAXBLK;
+constexpr size_t GN_CLR_FINALS_OFF = GN_CLR_SLOTS_OFF + 16 * (size_t)GN_CLR_MAX_SLOTS;
+constexpr size_t GN_CLR_BYTES = GN_CLR_FINALS_OFF + 16 * (size_t)GN_CLR_MAX_FINALS;
+
+struct GnClResArgs {
+  const void* x;
+  const void* gamma;
+  const void* beta;
+  void* y;
+  uint32_t* hdr;        // workspace header (zero at allocation)
+  GnSlot* slots;        // [N][G][NCH]
+  GnSlot* finals;       // [N][G]
+  int64_t S;            // positions per sample
+  int SC, NCH;          // positions per chunk (EPV * R), chunks per sample
+  int C, G, cpg;
+  int two_level;
+  int pdt;
+  float eps;
+  uint64_t wait_ticks;  // longest a workgroup waits, in total, for other workgroups' slots
+};
+
+__device__ __forceinline__ int cl_chunk_positions(const GnClResArgs& a, int c) {
+  const int64_t left = a.S - (int64_t)c * a.SC;
+  return left < a.SC ? (int)left : a.SC;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t cl_chunk_rsrc(const GnClResArgs& a, int n, int c, int es) {
+  const char* base = static_cast<const char*>(a.x) + (((int64_t)n * a.S + (int64_t)c * a.SC) * a.C) * es;
+  return make_rsrc(base, (uint32_t)((int64_t)cl_chunk_positions(a, c) * a.C * es));
+}
+
+// Sum of v over the M consecutive threads of this thread's segment (M a power of two, segments
+// aligned to M): an xor butterfly inside the wave, then, for segments spanning several waves,
+// the waves' totals in order.  Every thread of a segment gets the same bits.  M is uniform
+// over the workgroup (the barriers are reached by every thread or by none).
+template <int NT>
+__device__ __forceinline__ float seg_sum(float v, int M, float* red) {
+  const int lim = M < 64 ? M : 64;
+  for (int off = lim >> 1; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  if (M <= 64) return v;
+  const int w = threadIdx.x >> 6, wpg = M >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < wpg; ++i) t += red[(w / wpg) * wpg + i];
+  return t;
+}
+
+// Per-group (mean, M2) of chunk `ch` into rm[g], rq[g] (g < G).  Thread t accumulates shifted
+// sums over its vectors (about K = its first element; vectors past the chunk read zero and
+// are shifted by zero, so they add nothing), leaves (n_t, mean_t, M2_t) in LDS, and thread g
+// merges group g's threads in a fixed order -- rows, then the group's columns:
+//   mean = sum n_e mean_e / n,  M2 = sum (M2_e + n_e (mean_e - mean)^2).
+// The owner runs it on its registers (FROM_REG), a workgroup standing in for a late owner
+// on memory, with the same operations in the same order: the results are bit-identical.
+// Ends with the records visible to the whole workgroup.
+template <typename T, int NT, int EPV, bool FROM_REG>
+__device__ __forceinline__ void cl_chunk_stats(Vec16<T>* buf, __amdgpu_buffer_rsrc_t rx, int P, const GnClResArgs& a,
+                                               float* en, float* em, float* eq, float* red, float* rm, float* rq) {
+  constexpr int VEC = 16 / sizeof(T);
+  const int tid = threadIdx.x;
+  const int CV = a.C / VEC;
+  const int nv = P * CV;  // vectors of the chunk
+  auto get = [&](int i) -> Vec16<T> {
+    if constexpr (FROM_REG) {
+      return buf[i];
+    } else {
+      Vec16<T> v;
+      v.raw = bload16(rx, (uint32_t)tid * 16u, (uint32_t)(i * NT * 16));
+      return v;
+    }
+  };
+  const float K = to_f32(get(0).e[0]);
+  float s1 = 0.f, s2 = 0.f;
+  int nvt = 0;
+  auto acc = [&](int i) {
+    const bool ok = i * NT + tid < nv;
+    const float Ki = ok ? K : 0.f;
+    if constexpr (FROM_REG)
+      asm volatile("" : "+v"(buf[i].raw.x), "+v"(buf[i].raw.y), "+v"(buf[i].raw.z), "+v"(buf[i].raw.w),
+                   "+v"(s1), "+v"(s2));
+    const Vec16<T> v = get(i);
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+      const float d = to_f32(v.e[k]) - Ki;
+      s1 += d;
+      s2 = fmaf(d, d, s2);
+    }
+    nvt += ok ? 1 : 0;
+  };
+  if constexpr (FROM_REG) {
+#pragma unroll
+    for (int i = 0; i < EPV; ++i) acc(i);
+  } else {
+#pragma unroll 1
+    for (int i = 0; i < EPV; ++i) acc(i);
+  }
+  const float nt = (float)(nvt * VEC);
+  float mean_t = 0.f, m2_t = 0.f;
+  if (nvt > 0) {
+    const float q = s1 / nt;
+    mean_t = K + q;
+    m2_t = fmaxf(fmaf(-s1, q, s2), 0.f);
+  }
+  en[tid] = nt;
+  em[tid] = mean_t;
+  eq[tid] = m2_t;
+  __syncthreads();
+  // Thread t takes entry j = t % M of group g = t / M (M = NT / G: G divides CV = C / VEC,
+  // a power of two dividing NT), entry j being row j / cpv, column g * cpv + j % cpv.
+  const int cpv = a.cpg / VEC, M = NT / a.G;
+  const int g = tid / M, j = tid - (tid / M) * M;
+  const int e = (j / cpv) * CV + g * cpv + (j - (j / cpv) * cpv);
+  const float ne = en[e], me = em[e], qe = eq[e];
+  const float n = seg_sum<NT>(ne, M, red);
+  const float mean = seg_sum<NT>(ne * me, M, red) / n;
+  const float d = me - mean;
+  const float m2 = seg_sum<NT>(fmaf(ne * d, d, qe), M, red);
+  if (j == 0) {
+    rm[g] = mean;
+    rq[g] = m2;
+  }
+  __syncthreads();
+}
+
+// (mean, var) of a group from its NCH chunk records tm[c], tq[c] (chunk c holding
+// positions(c) * cpg elements), on one wave: lanes over chunks, then the xor butterfly, so
+// every lane -- and every workgroup merging the same records -- gets the same bits.
+__device__ __forceinline__ void cl_merge_group(const GnClResArgs& a, const float* tm, const float* tq, float& mean,
+                                               float& var) {
+  const int lane = threadIdx.x & 63;
+  const float E = (float)(a.S * a.cpg);
+  float sm = 0.f;
+  for (int c = lane; c < a.NCH; c += 64) sm = fmaf((float)(cl_chunk_positions(a, c) * a.cpg), tm[c], sm);
+  mean = wave_sum(sm) / E;
+  float m2 = 0.f;
+  for (int c = lane; c < a.NCH; c += 64) {
+    const float d = tm[c] - mean;
+    m2 += tq[c];
+    m2 = fmaf((float)(cl_chunk_positions(a, c) * a.cpg) * d, d, m2);
+  }
+  var = wave_sum(m2) / E;
+}
+
+// Reads slot w (two tagged words) once; true with the values if both carry `tag`.
+__device__ __forceinline__ bool read_slot(const GnSlot* sl, uint32_t tag, float& m, float& q) {
+  const unsigned long long w0 = __hip_atomic_load(&sl->w[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const unsigned long long w1 = __hip_atomic_load(&sl->w[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  m = __uint_as_float((uint32_t)w0);
+  q = __uint_as_float((uint32_t)w1);
+  return (uint32_t)(w0 >> 32) == tag && (uint32_t)(w1 >> 32) == tag;
+}
+
+__device__ __forceinline__ void write_slot(GnSlot* sl, uint32_t tag, float m, float q) {
+  const unsigned long long hi = (unsigned long long)tag << 32;
+  __hip_atomic_store(&sl->w[0], hi | __float_as_uint(m), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(&sl->w[1], hi | __float_as_uint(q), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Workgroup-wide: chunk records r < nrec into tm[r], tq[r], record r being group gr(r) of
+// chunk cr(r); this workgroup's own chunk comes from rm / rq.  Thread t polls records
+// t, t + NT, ... (up to RPT), all outstanding loads issued together, until they carry the
+// tag or the workgroup's deadline passes; a chunk with a record still missing is then
+// computed from x by the whole workgroup (cl_chunk_stats on memory) and its records filled in.
+template <typename T, int NT, int EPV, int RPT, typename GR, typename CR>
+__device__ __forceinline__ void cl_collect(const GnClResArgs& a, int n, int ch, uint32_t tag, uint64_t deadline, int nrec,
+                                           GR gr, CR cr, float* tm, float* tq, const float* rm, const float* rq,
+                                           float* en, float* em, float* eq, float* red, float* xm, float* xq, int* s_flag,
+                                           int* s_list, int* s_cnt) {
+  const int tid = threadIdx.x;
+  bool need[RPT];
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    const int r = tid + k * NT;
+    need[k] = false;
+    if (r < nrec) {
+      if (cr(r) == ch) {
+        tm[r] = rm[gr(r)];
+        tq[r] = rq[gr(r)];
+      } else {
+        need[k] = true;
+      }
+    }
+  }
+  for (;;) {
+    float m[RPT], q[RPT];
+    bool ok[RPT];
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      ok[k] = false;
+      if (need[k]) {
+        const int r = tid + k * NT;
+        ok[k] = read_slot(&a.slots[((int64_t)n * a.G + gr(r)) * a.NCH + cr(r)], tag, m[k], q[k]);
+      }
+    }
+    bool left = false;
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      if (need[k] && ok[k]) {
+        tm[tid + k * NT] = m[k];
+        tq[tid + k * NT] = q[k];
+        need[k] = false;
+      }
+      left = left || need[k];
+    }
+    if (!left || wall_clock64() > deadline) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+#pragma unroll
+  for (int k = 0; k < RPT; ++k)
+    if (need[k]) {
+      const int c = cr(tid + k * NT);
+      if (atomicExch(&s_flag[c], 1) == 0) s_list[atomicAdd(s_cnt, 1)] = c;
+    }
+  __syncthreads();
+  const int nmiss = *s_cnt;
+  if (nmiss > 0) {
+    if (tid == 0) __hip_atomic_store(a.hdr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int m = 0; m < nmiss; ++m) {
+      const int c = s_list[m];
+      cl_chunk_stats<T, NT, EPV, false>(nullptr, cl_chunk_rsrc(a, n, c, (int)sizeof(T)), cl_chunk_positions(a, c), a,
+                                        en, em, eq, red, xm, xq);
+      for (int r = tid; r < nrec; r += NT)
+        if (cr(r) == c) {
+          tm[r] = xm[gr(r)];
+          tq[r] = xq[gr(r)];
+        }
+      __syncthreads();
+    }
+    for (int m = tid; m < nmiss; m += NT) s_flag[s_list[m]] = 0;
+    __syncthreads();
+    if (tid == 0) *s_cnt = 0;
+    __syncthreads();
+  }
+}
+
+template <typename T, int NT, int EPV, bool SILU>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(EPV <= 16 ? 4 : 1)))
+void gn_cl_resident_kernel(GnClResArgs a) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int NW = NT / 64;
+  constexpr int RPT = GN_CLR_DIRECT / NT;  // records per thread (direct: G x NCH; one group: NCH)
+  static_assert(GN_CLR_MAXNCH <= GN_CLR_DIRECT, "one group's records fit the record table");
+  __shared__ float en[NT], em[NT], eq[NT];
+  __shared__ float s_red[NT / 64];
+  __shared__ float rm[GN_CL_MAXG], rq[GN_CL_MAXG];  // this chunk's records
+  __shared__ float xm[GN_CL_MAXG], xq[GN_CL_MAXG];  // a stand-in chunk's records
+  __shared__ float gm[GN_CL_MAXG], gv[GN_CL_MAXG];  // the sample's group statistics
+  __shared__ float gam[GN_CL_MAXC], bet[GN_CL_MAXC];
+  __shared__ float big[2 * GN_CL_MAXC];             // records tm / tq, then scale / shift
+  static_assert(GN_CLR_DIRECT <= GN_CL_MAXC, "the record table fits the scale / shift arrays");
+  __shared__ int s_flag[GN_CLR_MAXNCH], s_list[GN_CLR_MAXNCH];
+  __shared__ int s_cnt, s_gcnt;
+  __shared__ int s_glist[GN_CL_MAXG + 1];
+  float* tm = big;
+  float* tq = big + GN_CLR_DIRECT;
+
+  const int tid = threadIdx.x;
+  const int n = blockIdx.x / a.NCH, ch = blockIdx.x - (blockIdx.x / a.NCH) * a.NCH;
+  const int CV = a.C / VEC;
+  const int P = cl_chunk_positions(a, ch);
+  const int nv = P * CV;
+
+  // The epoch and gamma / beta first, then every x load of the chunk, branch-free.  Vector
+  // loads complete in issue order, so staging gamma / beta in LDS waits for them alone.
+  const uint32_t epoch = __hip_atomic_load(a.hdr + 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int c = tid; c < a.C; c += NT) {
+    gam[c] = a.gamma ? load_param(a.gamma, a.pdt, c) : 1.f;
+    bet[c] = a.beta ? load_param(a.beta, a.pdt, c) : 0.f;
+  }
+  const __amdgpu_buffer_rsrc_t rx = cl_chunk_rsrc(a, n, ch, (int)sizeof(T));
+  Vec16<T> buf[EPV];
+#pragma unroll
+  for (int i = 0; i < EPV; ++i) buf[i].raw = bload16<2>(rx, (uint32_t)tid * 16u, (uint32_t)(i * NT * 16));
+  if (tid == 0) {
+    s_cnt = 0;
+    // the record sets this workgroup merges: all groups (-1, direct) or its own group
+    // (two-level, workgroup g < G); groups whose published result does not appear in time
+    // are appended later
+    s_gcnt = a.two_level ? (ch < a.G ? 1 : 0) : 1;
+    s_glist[0] = a.two_level ? ch : -1;
+  }
+  for (int c = tid; c < GN_CLR_MAXNCH; c += NT) s_flag[c] = 0;
+
+  cl_chunk_stats<T, NT, EPV, true>(buf, rx, P, a, en, em, eq, s_red, rm, rq);
+  reg_fence<T, EPV>(buf);
+  const uint32_t tag = (epoch << 1) | 1u;
+  for (int g = tid; g < a.G; g += NT) write_slot(&a.slots[((int64_t)n * a.G + g) * a.NCH + ch], tag, rm[g], rq[g]);
+  const uint64_t deadline = wall_clock64() + a.wait_ticks;
+
+  GnSlot* fin = a.finals + (int64_t)n * a.G;
+  const int NCH = a.NCH;
+  bool polled = !a.two_level;
+  for (int k = 0;;) {
+    if (k < s_gcnt) {  // uniform: LDS read after a barrier
+      const int gf = s_glist[k++];
+      cl_collect<T, NT, EPV, RPT>(a, n, ch, tag, deadline, gf < 0 ? a.G * NCH : NCH,
+                                  [&](int r) { return gf < 0 ? r / NCH : gf; },
+                                  [&](int r) { return gf < 0 ? r - (r / NCH) * NCH : r; }, tm, tq, rm, rq, en, em,
+                                  eq, s_red, xm, xq, s_flag, s_list, &s_cnt);
+      __syncthreads();
+      const int w = tid >> 6;
+      for (int g = gf < 0 ? w : (w == 0 ? gf : a.G); g < (gf < 0 ? a.G : gf + 1); g += NW) {
+        float mean, var;
+        cl_merge_group(a, gf < 0 ? tm + g * NCH : tm, gf < 0 ? tq + g * NCH : tq, mean, var);
+        if ((tid & 63) == 0) {
+          gm[g] = mean;
+          gv[g] = var;
+          if (gf == ch && a.two_level) write_slot(&fin[gf], tag, mean, var);
+        }
+      }
+      __syncthreads();
+      continue;
+    }
+    if (polled) break;
+    polled = true;
+    // two-level: the other groups' results, one thread per group
+    for (int g = tid; g < a.G; g += NT) {
+      if (g == ch) continue;
+      float m, q;
+      bool ok;
+      for (;;) {
+        ok = read_slot(&fin[g], tag, m, q);
+        if (ok || wall_clock64() > deadline) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      if (ok) {
+        gm[g] = m;
+        gv[g] = q;
+      } else {
+        s_glist[atomicAdd(&s_gcnt, 1)] = g;
+      }
+    }
+    __syncthreads();
+  }
+  // per-channel scale / shift (over the record table, no longer needed)
+  float* scs = big;
+  float* shs = big + GN_CL_MAXC;
+  for (int c = tid; c < a.C; c += NT) {
+    const int g = c / a.cpg;
+    const float rstd = 1.0f / sqrtf(gv[g] + a.eps);
+    const float sc = rstd * gam[c];
+    scs[c] = sc;
+    shs[c] = bet[c] - gm[g] * sc;
+  }
+  __syncthreads();
+  const int v = tid % CV;
+  float sc[VEC], sh[VEC];
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) {
+    sc[k] = scs[v * VEC + k];
+    sh[k] = shs[v * VEC + k];
+  }
+  T* __restrict__ yc = static_cast<T*>(a.y) + ((int64_t)n * a.S + (int64_t)ch * a.SC) * a.C;
+#pragma unroll
+  for (int i = 0; i < EPV; ++i) {
+    reg_fence<T, 1>(&buf[i]);
+    const int e = i * NT + tid;
+    if (e < nv) {
+      float o[VEC];
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) {
+        o[k] = fmaf(to_f32(buf[i].e[k]), sc[k], sh[k]);
+        if constexpr (SILU) o[k] = silu_f32(o[k]);
+      }
+      st16<true>(yc + (int64_t)e * VEC, pack16<T>(o));
+    }
+  }
+  // Done with the slots (every read above has returned): count this workgroup in its block
+  // of GN_CLR_BLOCK; the block's last counts the block in the launch, and the launch's last
+  // advances the epoch.  Each counter is reset by the workgroup that completes it.  Counting
+  // after the stores keeps the atomics' round trips off the store phase, and the blocks keep
+  // all workgroups from queueing on one address.
+  if (tid == 0) {
+    const uint32_t b = blockIdx.x / GN_CLR_BLOCK, nb = (gridDim.x + GN_CLR_BLOCK - 1) / GN_CLR_BLOCK;
+    const uint32_t in_b = min((uint32_t)GN_CLR_BLOCK, gridDim.x - b * GN_CLR_BLOCK);
+    uint32_t* bc = a.hdr + 64 + 32 * b;
+    if (__hip_atomic_fetch_add(bc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == in_b - 1) {
+      __hip_atomic_store(bc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__hip_atomic_fetch_add(a.hdr + 32, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nb - 1) {
+        __hip_atomic_store(a.hdr + 32, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.hdr + 16, (epoch + 1u) & 0x7fffffffu, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+}
+
+struct GnClResPlan {
+  int nt, epv, NCH, SC, two_level;
+};
+
+// The register-resident configuration for a channels-last shape, or false.  Left to itself
+// the library takes 16 vectors per thread (128 KB chunks in 16-bit types) when that grid
+// covers every CU and fits at once: the exchange of statistics costs about 5 us (two rounds
+// of agent-coherent stores and polls), which a 128 KB chunk per workgroup amortises against
+// the three-kernel path's second read of x and two extra launches, and 64 KB chunks do not.
+// `force_epv` (8 or 16) takes that configuration wherever it fits.  Two-level whenever there
+// are at least as many chunks as groups (measured faster than every workgroup polling all
+// G x NCH records), else direct if G x NCH <= GN_CLR_DIRECT.
+template <typename T>
+bool plan_gn_cl_res(int64_t N, int64_t C, int64_t S, int G, int force_epv, GnClResPlan& out);
+
+template <typename T, int NT, int EPV>
+int64_t gn_cl_res_capacity() {
+  static int per_cu[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (per_cu[dev] == 0 &&
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &per_cu[dev], reinterpret_cast<const void*>(gn_cl_resident_kernel<T, NT, EPV, true>), NT, 0) != hipSuccess)
+    return 0;
+  return (int64_t)per_cu[dev] * device_cu_count();
+}
+
+template <typename T>
+bool plan_gn_cl_res(int64_t N, int64_t C, int64_t S, int G, int force_epv, GnClResPlan& out) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int NT = 512;
+  const int64_t CV = C / VEC;
+  if (C % VEC || (C / G) % VEC || C > GN_CL_MAXC || G > GN_CL_MAXG || NT % CV) return false;
+  const int epv = force_epv ? force_epv : 16;
+  const int64_t sc = (int64_t)epv * (NT / CV);
+  const int64_t nch = (S + sc - 1) / sc;
+  if (nch > GN_CLR_MAXNCH || N * G * nch > GN_CLR_MAX_SLOTS || N * G > GN_CLR_MAX_FINALS) return false;
+  GnClResPlan p{NT, epv, (int)nch, (int)sc, 0};
+  if (nch >= G) p.two_level = 1;
+  else if (G * nch <= GN_CLR_DIRECT) p.two_level = 0;
+  else return false;
+  const int64_t nblk = N * nch;
+  const int64_t cap = epv == 16 ? gn_cl_res_capacity<T, NT, 16>() : gn_cl_res_capacity<T, NT, 8>();
+  if (nblk > cap || nblk > (int64_t)GN_CLR_BLOCK * GN_CLR_MAXBLK) return false;
+  if (!force_epv && nblk < device_cu_count()) return false;
+  out = p;
+  return true;
+}
+
+template <typename T>
+int launch_gn_cl_res(const GnClResArgs& a, const GnClResPlan& p, int64_t N, int silu, hipStream_t s) {
+  const dim3 grid((unsigned)(N * p.NCH)), block(p.nt);
+  if (p.epv == 16) {
+    if (silu) hipLaunchKernelGGL((gn_cl_resident_kernel<T, 512, 16, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((gn_cl_resident_kernel<T, 512, 16, false>), grid, block, 0, s, a);
+  } else {
+    if (silu) hipLaunchKernelGGL((gn_cl_resident_kernel<T, 512, 8, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((gn_cl_resident_kernel<T, 512, 8, false>), grid, block, 0, s, a);
+  }
+  return check_launch("gn_cl_resident_kernel");
+}
+
+// ---------------------------------------------------------------------------------------
 // Channels-last GroupNorm backward (x, dy, dx: [n][s][c]); the math of the NC[S] backward
 // above, without the layout conversions.  Three kernels, 5 tensor passes (x and dy read
 // twice, the second time mostly from the Infinity Cache; dx written once):
@@ -2141,8 +2620,10 @@ extern "C" int atk_group_norm_bwd(const void* x, const void* dy, const void* gam
 
 extern "C" size_t atk_group_norm_cl_workspace_bytes(int64_t N, int64_t C, int64_t S, int G) {
   if (N <= 0 || C <= 0 || S <= 0 || G <= 0) return 0;
+  // the register-resident kernel's header and slots (fixed layout), then the three-kernel
+  // path's chunk partials and group statistics
   const atk::GnClPlan p = atk::plan_gn_cl(N, S);
-  return ((size_t)N * (size_t)p.NCH + (size_t)N) * (size_t)G * 2 * sizeof(float);
+  return atk::GN_CLR_BYTES + ((size_t)N * (size_t)p.NCH + (size_t)N) * (size_t)G * 2 * sizeof(float);
 }
 
 extern "C" int atk_group_norm_cl_fwd(const void* x, const void* gamma, const void* beta, void* y, int64_t N,
@@ -2165,18 +2646,52 @@ extern "C" int atk_group_norm_cl_fwd(const void* x, const void* gamma, const voi
   if (S * C * es >= ((int64_t)1 << 31))
     return fail(ATK_UNSUPPORTED, "group_norm (channels-last): one sample over 2 GiB (32-bit buffer offsets)");
   const GnClPlan p = plan_gn_cl(N, S);
-  const size_t need = ((size_t)N * (size_t)p.NCH + (size_t)N) * (size_t)G * 2 * sizeof(float);
+  const size_t need = atk_group_norm_cl_workspace_bytes(N, C, S, G);
   if (!workspace || ws_bytes < need)
     return fail(ATK_EINVAL, "group_norm (channels-last): workspace of %zu bytes needed", need);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // Register-resident single pass where the library's rule takes it (plan_gn_cl_res);
+  // ATK_GN_CL_RESIDENT=0 turns it off, =8 / =16 takes that many vectors per thread wherever
+  // that configuration fits.
+  const char* renv = getenv("ATK_GN_CL_RESIDENT");
+  const int rmode = renv ? atoi(renv) : 1;
+  if (rmode != 0) {
+    const int force = (rmode == 8 || rmode == 16) ? rmode : 0;
+    GnClResPlan rp;
+    const bool fits = dtype == ATK_F32   ? plan_gn_cl_res<float>(N, C, S, G, force, rp)
+                      : dtype == ATK_F16 ? plan_gn_cl_res<_Float16>(N, C, S, G, force, rp)
+                                         : plan_gn_cl_res<__bf16>(N, C, S, G, force, rp);
+    if (fits) {
+      GnClResArgs r;
+      r.x = x; r.gamma = gamma; r.beta = beta; r.y = y;
+      char* ws = static_cast<char*>(workspace);
+      r.hdr = reinterpret_cast<uint32_t*>(ws);
+      r.slots = reinterpret_cast<GnSlot*>(ws + GN_CLR_SLOTS_OFF);
+      r.finals = reinterpret_cast<GnSlot*>(ws + GN_CLR_FINALS_OFF);
+      r.S = S; r.SC = rp.SC; r.NCH = rp.NCH;
+      r.C = (int)C; r.G = G; r.cpg = (int)cpg;
+      r.two_level = rp.two_level;
+      r.pdt = param_dtype;
+      r.eps = eps;
+      const int khz = device_wall_clock_khz();
+      const char* wenv = getenv("ATK_GN_WAIT_US");
+      const uint64_t wait_us = wenv ? strtoull(wenv, nullptr, 10) : GN_WAIT_US;
+      r.wait_ticks = (uint64_t)(khz > 0 ? khz : 100000) * wait_us / 1000;
+      switch (dtype) {
+        case ATK_F32: return launch_gn_cl_res<float>(r, rp, N, fuse_silu, s);
+        case ATK_F16: return launch_gn_cl_res<_Float16>(r, rp, N, fuse_silu, s);
+        default: return launch_gn_cl_res<__bf16>(r, rp, N, fuse_silu, s);
+      }
+    }
+  }
   GnClArgs a;
   a.x = x; a.gamma = gamma; a.beta = beta; a.y = y;
-  a.part = static_cast<float*>(workspace);
+  a.part = reinterpret_cast<float*>(static_cast<char*>(workspace) + GN_CLR_BYTES);
   a.stat = a.part + (size_t)N * p.NCH * G * 2;
   a.S = S; a.SC = p.SC; a.NCH = p.NCH;
   a.sample_bytes = (uint32_t)(S * C * es);
   a.C = (uint32_t)C; a.G = (uint32_t)G; a.cpg = (uint32_t)cpg;
   a.eps = eps; a.pdt = param_dtype;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (dtype) {
     case ATK_F32: return launch_gn_cl<float>(a, (int)N, fuse_silu, s);
     case ATK_F16: return launch_gn_cl<_Float16>(a, (int)N, fuse_silu, s);

@@ -427,6 +427,107 @@ def test_group_norm_channels_last(dev, shape_g, dtype):
         _check(y.cpu().contiguous(), x, G, gm, bt, 1e-5, silu=silu, what=f"cl silu={silu}")
 
 
+# (shape, G, ATK_GN_CL_RESIDENT): which register-resident configuration the channels-last
+# forward takes ("0" = the three-kernel path).  With at least as many chunks per sample as
+# groups, one workgroup per group merges that group's chunk records (two-level); with fewer,
+# every workgroup merges all G x NCH records (direct, at most 1024).  (2,256,100,130) bf16 has
+# 102 chunks of 128 positions per sample at 8 vectors per thread and 51 of 256 at 16 (both
+# two-level, a partial last chunk); (1,256,31,256) at 16 has 31 chunks of 32 groups (direct,
+# 992 records); (8,512,16,16) and (1,64,3,1000) are direct.
+CL_RES_CASES = [
+    ((2, 256, 100, 130), 32, "8"),
+    ((2, 256, 100, 130), 32, "16"),
+    ((2, 256, 100, 130), 32, "0"),
+    ((1, 512, 4, 32, 64), 32, "16"),    # C3-like channels, NDHWC (fp32: two-level)
+    ((1, 256, 31, 256), 32, "16"),      # 31 x 32 records: direct (16-bit)
+    ((8, 512, 16, 16), 32, "8"),
+    ((1, 64, 3, 1000), 4, "16"),         # one sample, 1 chunk per 1024 positions
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("case", CL_RES_CASES, ids=lambda c: "x".join(map(str, c[0])) + f"_g{c[1]}_r{c[2]}")
+def test_group_norm_channels_last_resident(dev, case, dtype, monkeypatch):
+    """The channels-last forward in each register-resident configuration (and the
+    three-kernel path) against the oracle, with and without SiLU and affine parameters;
+    repeated calls are bit-identical (the slot epoch advances between them) and no launch
+    fell back to computing another workgroup's statistics."""
+    shape, G, mode = case
+    nat = _native()
+    monkeypatch.setenv("ATK_GN_CL_RESIDENT", mode)
+    fmt = torch.channels_last if len(shape) == 4 else torch.channels_last_3d
+    for affine in (True, False):
+        x, gm, bt = _inputs(shape, dtype, seed=len(shape) + G + int(mode) + 500, affine=affine)
+        xd = x.to(dev).contiguous(memory_format=fmt)
+        gd = gm.to(dev) if gm is not None else None
+        bd = bt.to(dev) if bt is not None else None
+        for silu in (False, True):
+            y = nat.group_norm_cl(xd, G, gd, bd, 1e-5, silu=silu)
+            y2 = nat.group_norm_cl(xd, G, gd, bd, 1e-5, silu=silu)
+            torch.cuda.synchronize()
+            assert y.is_contiguous(memory_format=fmt)
+            assert torch.equal(y, y2), f"repeat differs (mode {mode}, silu={silu})"
+            _check(y.cpu().contiguous(), x, G, gm, bt, 1e-5, silu=silu,
+                   what=f"cl resident={mode} silu={silu} affine={affine}")
+    assert not nat.group_norm_barrier_error(dev)
+
+
+@pytest.mark.parametrize("shape,mode", [((1, 256, 65, 128), "8"), ((1, 256, 31, 256), "16")],
+                         ids=["two_level", "direct"])
+def test_group_norm_channels_last_standin_bit_identical(dev, shape, mode, monkeypatch):
+    """With a zero wait, workgroups compute every chunk record (and, two-level, every group
+    result) that is not yet published themselves; the outputs must equal the normal path's
+    byte for byte.  65 chunks x 32 groups at 8 vectors per thread (two-level); 31 x 32 at 16
+    (direct)."""
+    nat = _native()
+    G = 32
+    monkeypatch.setenv("ATK_GN_CL_RESIDENT", mode)
+    x, gm, bt = _inputs(shape, torch.bfloat16, seed=611)
+    xd = x.to(dev).contiguous(memory_format=torch.channels_last)
+    gd, bd = gm.to(dev), bt.to(dev)
+    y0 = nat.group_norm_cl(xd, G, gd, bd, 1e-5, silu=True)
+    torch.cuda.synchronize()
+    assert not nat.group_norm_barrier_error(dev)
+    monkeypatch.setenv("ATK_GN_WAIT_US", "0")
+    for _ in range(3):
+        y1 = nat.group_norm_cl(xd, G, gd, bd, 1e-5, silu=True)
+        torch.cuda.synchronize()
+        assert torch.equal(y0.view(torch.int16), y1.view(torch.int16))
+    monkeypatch.delenv("ATK_GN_WAIT_US")
+    nat.group_norm_clear_diag(dev)
+    _check(y1.cpu().contiguous(), x, G, gm, bt, 1e-5, silu=True, what="cl stand-in")
+
+
+@pytest.mark.parametrize("mode", ["8", "16"])
+def test_group_norm_channels_last_graph_replay(dev, mode, monkeypatch):
+    """The resident channels-last forward captured in a HIP graph and replayed with new
+    inputs copied in between (eager work and synchronisation between replays): every replay
+    matches the eager result bit for bit -- the slot epoch lives in device memory, so a
+    replay never accepts a slot written by the previous one."""
+    nat = _native()
+    shape, G = (2, 256, 100, 130), 32
+    monkeypatch.setenv("ATK_GN_CL_RESIDENT", mode)
+    data = [_inputs(shape, torch.bfloat16, seed=70 + i) for i in range(3)]
+    gd, bd = data[0][1].to(dev), data[0][2].to(dev)
+    xs = data[0][0].to(dev).contiguous(memory_format=torch.channels_last)
+    out = torch.empty_like(xs)
+    nat.group_norm_cl(xs, G, gd, bd, 1e-5, out=out)   # workspace allocated before capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        nat.group_norm_cl(xs, G, gd, bd, 1e-5, out=out)
+    for rep in range(6):
+        x = data[rep % 3][0]
+        xs.copy_(x.to(dev).contiguous(memory_format=torch.channels_last))
+        g.replay()
+        torch.cuda.synchronize()
+        eager = nat.group_norm_cl(xs, G, gd, bd, 1e-5)
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {rep}"
+    _check(out.cpu().contiguous(), data[5 % 3][0], G, data[0][1], data[0][2], 1e-5, what="cl graph replay")
+    assert not nat.group_norm_barrier_error(dev)
+
+
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
 def test_group_norm_channels_last_through_patched_api(dev, dtype):
     """F.group_norm and conv_fusion_ops.group_norm_silu on channels-last tensors take the
