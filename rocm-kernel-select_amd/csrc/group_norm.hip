@@ -316,6 +316,10 @@ void gn_resident_kernel(GnArgs a) {
                          __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(&slots[s].w[1], hi | __float_as_uint(m2), __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
+      // the publish completes before this workgroup counts itself done (below, after its
+      // stores), so the last workgroup's clear can never be overtaken by a late publish, which
+      // would leave a filled slot behind (the barrier that follows waits for it anyway)
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       s_missing[0] = 0;
     }
     __syncthreads();
@@ -369,25 +373,6 @@ void gn_resident_kernel(GnArgs a) {
         s_stat[0] = mean;
         s_stat[1] = var;
       }
-      // This workgroup is done with the slots (its lanes' reads returned before this point).
-      // The last of the group's NS workgroups -- every one has published by then -- empties
-      // them for the next launch and resets the counter.  Thread 0 published this
-      // workgroup's slot; it waits for those stores to complete before counting itself
-      // done, so the last workgroup's clear can never be overtaken by a late publish (which
-      // would leave a filled slot behind).  One wait per workgroup, none per poll.
-      uint32_t prev = 0;
-      if (tid == 0) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        prev = __hip_atomic_fetch_add(a.done + gi, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-      prev = __shfl(prev, 0, 64);
-      if (prev == (uint32_t)a.NS - 1) {
-        for (int j = tid; j < a.NS; j += 64) {
-          __hip_atomic_store(&slots[j].w[0], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(&slots[j].w[1], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        if (tid == 0) __hip_atomic_store(a.done + gi, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
     }
     __syncthreads();
     mean = s_stat[0];
@@ -429,6 +414,24 @@ void gn_resident_kernel(GnArgs a) {
         channel_affine(a, cabs0 + cl, mean, rstd, sc, sh);
         st16<true>(yg + e, normalize_vec<T, SILU>(buf[i], sc, sh));
       }
+    }
+  }
+  if (a.NS > 1 && tid < 64) {
+    // This workgroup is done with the slots (every read of them returned before the barrier
+    // above) and its publish completed: count it, after its stores are issued, so that the
+    // atomic's round trip overlaps them rather than delaying them.  The last of the group's NS
+    // workgroups to count itself -- every one has published and finished reading by then --
+    // empties the slots for the next launch and resets the counter.
+    GnSlot* slots = a.slots + gi * (int64_t)a.NS;
+    uint32_t prev = 0;
+    if (tid == 0) prev = __hip_atomic_fetch_add(a.done + gi, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    prev = __shfl(prev, 0, 64);
+    if (prev == (uint32_t)a.NS - 1) {
+      for (int j = tid; j < a.NS; j += 64) {
+        __hip_atomic_store(&slots[j].w[0], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&slots[j].w[1], 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      if (tid == 0) __hip_atomic_store(a.done + gi, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
