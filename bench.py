@@ -538,8 +538,19 @@ def bench_gn_cl_detail(shape, G, silu, dev):
     stock_ms = event_time_ms(stock, 10)
     nbytes = 2 * x.numel() * x.element_size()
     gbs = nbytes / (ms * 1e-3) / 1e9
+    # the library's rule (plan_gn_cl_res): one register-resident launch when 128 KB chunks (512
+    # threads x 16 vectors) cover every CU and fit at once, else stats / merge / apply kernels
+    N, S = shape[0], x.numel() // (shape[0] * C)
+    vec = 16 // x.element_size()
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    nch = -(-S // (16 * (512 // (C // vec))))
+    resident = (C % vec == 0 and (C // G) % vec == 0 and 512 % (C // vec) == 0 and nch <= 1024
+                and (nch >= G or G * nch <= 1024) and cus <= N * nch <= 2 * cus)
+    cold = cold_graph_time_ms(lambda a, b: nat.group_norm_cl(a, G, gm, bt, 1e-5, silu=silu, out=b), x, nbytes)
     return {"ms": round(ms, 4), "GB/s": round(gbs, 1), "roofline_frac": round(gbs / HBM_PEAK_GBS, 4),
-            "variant": "native.cl", "stock_ms": round(stock_ms, 4), "max_rel_err_vs_stock_fp32": float(f"{err:.3g}")}
+            "cold_ms": round(cold, 4), "cold_roofline_frac": round(nbytes / (cold * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "variant": "native gn_cl_resident_kernel" if resident else "native gn_cl stats/merge/apply",
+            "stock_ms": round(stock_ms, 4), "max_rel_err_vs_stock_fp32": float(f"{err:.3g}")}
 
 
 def bench_gn_backward_detail(shape, G, dev):

@@ -203,6 +203,28 @@ int atk_causal_conv1d_cl_bwd(const void* x, const void* dout, const void* w, con
                              int w_dtype, int silu, void* workspace, size_t ws_bytes, atk_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Channels-last depthwise conv1d backward in one pass (replaces `conv1d_backward(dout, u,
+ * weight, bias, padding, is_bhl=false)`, amd_tuned_torch/_vendor/flashfftconv_depthwise_conv1d/
+ * conv1d_bwd_hip_blh.hip:21-127, behind amd_tuned_torch/depthwise_conv1d_ops.py's backward):
+ * for y = atk_dwconv1d_cl_fwd(x, w, NULL, pad_left, L_out),
+ *   dx[b,q,c] = sum_k w[c,k] * dy[b, q+pad_left-k, c]   (dy = 0 outside [0, L_out)),
+ *   dw[c,k]   = sum_{b,t} dy[b,t,c] * x[b, t-pad_left+k, c],   db[c] = sum_{b,t} dy[b,t,c].
+ * x, dx (B, L, D) and dy (B, L_out, D) views with channel stride 1 (layouts as in
+ * atk_dwconv1d_cl_fwd); w read at (w_stride_c, w_stride_k) in w_dtype; dw [D, K], db [D]
+ * fp32 (db may be NULL).  x and dy are each read once; the two-pass route (the forward
+ * kernel on dy for dx, atk_dwconv1d_cl_bwd_weight for dw / db) reads dy twice.  K in [2, 4],
+ * any pad_left >= 0 and L_out >= 1.  The workspace holds per-span partials (deterministic
+ * fixed-order sum); it needs no initialisation.
+ * ------------------------------------------------------------------------- */
+size_t atk_dwconv1d_cl_bwd_workspace_bytes(int64_t B, int64_t D, int64_t L, int K, int pad_left, int64_t L_out,
+                                           int dtype);
+int atk_dwconv1d_cl_bwd(const void* x, const void* dy, const void* w, void* dx, float* dw, float* db, int64_t B,
+                        int64_t D, int64_t L, int K, int pad_left, int64_t L_out, int64_t x_stride_b,
+                        int64_t x_stride_l, int64_t dy_stride_b, int64_t dy_stride_l, int64_t dx_stride_b,
+                        int64_t dx_stride_l, int64_t w_stride_c, int64_t w_stride_k, int dtype, int w_dtype,
+                        void* workspace, size_t ws_bytes, atk_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Depthwise conv1d backward in one pass (replaces `conv1d_backward(dout, u, weight, bias,
  * padding, is_bhl=True)`, _vendor/flashfftconv_depthwise_conv1d/conv1d_bwd_hip_bhl.hip:39-116,
  * behind amd_tuned_torch/depthwise_conv1d_ops.py's backward, and the (B, C, L) backward of a

@@ -38,6 +38,7 @@ EXPORTED_SYMBOLS = (
     "atk_dwconv1d_fwd", "atk_causal_conv1d_update", "atk_dwconv1d_bwd_weight_workspace_bytes",
     "atk_dwconv1d_bwd_weight", "atk_causal_conv1d_bwd", "atk_dwconv1d_cl_fwd", "atk_dwconv1d_cl_bwd_weight_workspace_bytes",
     "atk_dwconv1d_cl_bwd_weight", "atk_causal_conv1d_cl_bwd_workspace_bytes", "atk_causal_conv1d_cl_bwd",
+    "atk_dwconv1d_cl_bwd_workspace_bytes", "atk_dwconv1d_cl_bwd",
     "atk_group_norm_workspace_bytes",
     "atk_group_norm_workspace_zero_bytes", "atk_group_norm_fwd", "atk_group_norm_cl_workspace_bytes",
     "atk_group_norm_cl_fwd", "atk_group_norm_bwd_workspace_bytes",
@@ -91,6 +92,10 @@ def _declare(lib) -> None:
     lib.atk_causal_conv1d_cl_bwd_workspace_bytes.restype = sz
     lib.atk_causal_conv1d_cl_bwd.argtypes = [vp] * 9 + [i64, i64, i64, i32] + [i64] * 10 + [i32, i32, i32, vp, sz, vp]
     lib.atk_causal_conv1d_cl_bwd.restype = i32
+    lib.atk_dwconv1d_cl_bwd_workspace_bytes.argtypes = [i64, i64, i64, i32, i32, i64, i32]
+    lib.atk_dwconv1d_cl_bwd_workspace_bytes.restype = sz
+    lib.atk_dwconv1d_cl_bwd.argtypes = [vp] * 6 + [i64, i64, i64, i32, i32, i64] + [i64] * 8 + [i32, i32, vp, sz, vp]
+    lib.atk_dwconv1d_cl_bwd.restype = i32
     lib.atk_group_norm_cl_workspace_bytes.argtypes = [i64, i64, i64, i32]
     lib.atk_group_norm_cl_workspace_bytes.restype = sz
     lib.atk_group_norm_cl_fwd.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, c.c_float, i32, i32, i32, vp, sz, vp]
@@ -527,6 +532,39 @@ def dwconv1d_cl_bwd_weight(x: torch.Tensor, dy: torch.Tensor, K: int, pad_left: 
         1 if seq_idx is not None else 0, _ptr(ws), ws.numel(), _stream(x))
     _check(rc, "dwconv1d_cl_bwd_weight")
     return dw, db
+
+
+def dwconv1d_cl_bwd(x: torch.Tensor, dy: torch.Tensor, weight_dk: torch.Tensor, pad_left: int, *,
+                    with_bias: bool = True):
+    """One-pass backward of dwconv1d_cl (x (B, L, D), dy (B, L_out, D) views with unit channel
+    stride, one dtype; weight_dk (D, K) float32 or x's dtype, K in 2..4): (dx (B, L, D)
+    contiguous in x's dtype, dw (D, K) fp32, db (D,) fp32 or None).  Raises Unsupported for
+    shapes the fused kernel does not take."""
+    _require_cuda(x, dy, weight_dk)
+    _bld_view(x, "dwconv1d_cl_bwd: x")
+    _bld_view(dy, "dwconv1d_cl_bwd: dy")
+    if x.dtype not in _DTYPE_CODE or dy.dtype != x.dtype or dy.shape[0] != x.shape[0] or dy.shape[2] != x.shape[2]:
+        raise RuntimeError("dwconv1d_cl_bwd: x (B, L, D) and dy (B, L_out, D) of one dtype")
+    if weight_dk.dim() != 2 or weight_dk.shape[0] != x.shape[2] or weight_dk.dtype not in (torch.float32, x.dtype):
+        raise RuntimeError("dwconv1d_cl_bwd: weight (D, K), float32 or x's dtype")
+    B, L, D = x.shape
+    K, l_out = weight_dk.shape[1], dy.shape[1]
+    if B == 0 or L == 0 or l_out == 0:
+        raise Unsupported("dwconv1d_cl_bwd: empty input")
+    dx = torch.empty((B, L, D), dtype=x.dtype, device=x.device)
+    dw = torch.empty((D, K), dtype=torch.float32, device=x.device)
+    db = torch.empty((D,), dtype=torch.float32, device=x.device) if with_bias else None
+    L_ = lib()
+    nbytes = L_.atk_dwconv1d_cl_bwd_workspace_bytes(B, D, L, K, int(pad_left), l_out, _DTYPE_CODE[x.dtype])
+    if nbytes == 0:
+        raise Unsupported("dwconv1d_cl_bwd: shape not taken")
+    ws = workspace(x.device, "dwconv1d_cl_bwd", nbytes)
+    rc = L_.atk_dwconv1d_cl_bwd(
+        _ptr(x), _ptr(dy), _ptr(weight_dk), _ptr(dx), _ptr(dw), _ptr(db), B, D, L, K, int(pad_left), l_out,
+        *_bld_strides(x), *_bld_strides(dy), *_bld_strides(dx), weight_dk.stride(0), weight_dk.stride(1),
+        _DTYPE_CODE[x.dtype], _DTYPE_CODE[weight_dk.dtype], _ptr(ws), ws.numel(), _stream(x))
+    _check(rc, "dwconv1d_cl_bwd")
+    return dx, dw, db
 
 
 def causal_conv1d_bwd(x: torch.Tensor, dout: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor],

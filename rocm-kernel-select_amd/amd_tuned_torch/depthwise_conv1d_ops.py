@@ -85,10 +85,18 @@ def _backward(dout, input_, weight, bias, padding: int, is_bhl: bool):
     serves it, the rest stock."""
     du = dw = db = None
     if not is_bhl and input_.is_cuda and _native.available():
-        # (B, L, C) layout, weight [K, C]: du through the channels-last forward kernel on dout
-        # with the taps reversed; dweight / dbias through its channels-last reduction
+        # (B, L, C) layout, weight [K, C]: du, dweight and dbias in one pass over x and dout
+        # where the fused kernel takes the shape (K 2..4); else du through the channels-last
+        # forward kernel on dout with the taps reversed and dweight / dbias through its
+        # channels-last reduction
         K = weight.shape[0]
         wf = weight if weight.dtype in (torch.float32, input_.dtype) else weight.float()
+        if dout.stride(-1) == 1 and input_.stride(-1) == 1:
+            try:
+                du, dw32, db32 = _native.dwconv1d_cl_bwd(input_, dout, wf.t(), padding)
+                return du, dw32.t().contiguous().to(weight.dtype), db32.to(dout.dtype)
+            except _native.Unsupported:
+                pass
         try:
             if padding <= K - 1:
                 du = _native.dwconv1d_cl(dout, wf.t().flip(-1), None, K - 1 - padding, input_.shape[1])

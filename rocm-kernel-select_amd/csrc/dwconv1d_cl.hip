@@ -377,11 +377,18 @@ __global__ __launch_bounds__(CLF_COLS * CLF_SPLIT) void dwconv1d_cl_bwd_finalize
 }
 
 // ---------------------------------------------------------------------------
-// Causal backward, fused (src/causal-conv1d-amd/csrc/causal_conv1d_bwd.cu channel-last path):
-// with H = K-1 and z[t] the pre-activation of the forward (recomputed here in fp32),
+// Backward, fused (src/causal-conv1d-amd/csrc/causal_conv1d_bwd.cu channel-last path, and
+// the (B, L, C) depthwise conv1d backward of conv1d_bwd_hip_bhl.hip): with H = K-1 and z[t]
+// the pre-activation of the forward (recomputed here in fp32; causal form only),
 //   g[t]  = dout[t] * silu'(z[t])   (or dout[t] without the activation),
 //   dx[q] = sum_j w[j] * g[q + H - j] * [seq(q) == seq(q + H - j)],
 //   dw[j] = sum_t g[t] * x[t - H + j] * [seq(t - H + j) == seq(t)],  db = sum_t g[t].
+// Any left padding P and output length L_out reduce to that form by a shift sh = H - P: the
+// kernel walks u over the union of [0, L_out) (dout rows) and [-sh, L - sh) (dx rows), reads
+// x at u + sh (x~[u] = x[u + sh]) and stores dx[u + sh]; with x~ the sums above read
+//   dx[u + sh] = sum_j w[j] g[u + H - j],   dw[j] = sum_t g[t] x~[t - H + j] = sum_t g[t] x[t - P + j],
+// i.e. dx[q] = sum_j w[j] g[q + P - j], the depthwise conv's input gradient.  dout rows outside
+// [0, L_out) read zero and so add nothing.  The causal form is sh = 0, L_out = L.
 // A thread owns VEC channels and a span of positions, walked in steps of CLB_STEP rows.
 // Each step loads the CLB_STEP new dout / x rows at positions [p + H, p + H + STEP) and keeps
 // the 2H x rows and H gradient rows that the next step shares as carried registers, so dout
@@ -403,6 +410,9 @@ struct DwClCbArgs {
   int64_t ib, il;
   int64_t xb, xl, gb, gl, ob, ol;  // element strides of x, dout, dx
   uint32_t B, D, L;
+  uint32_t Lout;                   // dout rows (L in the causal form)
+  int sh, u0;                      // x / dx shift H - P; first loop position min(0, -sh)
+  int u1;                          // loop end max(L_out, L - sh)
   uint32_t x_bytes, g_bytes, seq_bytes;
   uint32_t ncv, nspan, span;       // span: positions per thread, a multiple of CLB_STEP
   FastDiv div_ncv, div_nspan;
@@ -428,8 +438,8 @@ __global__ __launch_bounds__(CL_NT) void dwconv1d_cl_causal_bwd_kernel(DwClCbArg
   const uint32_t sp = rest - b * a.nspan;
   if (b >= a.B) return;
   const uint32_t c0 = cv * VEC;
-  const int p_start = (int)(sp * a.span);
-  const int p_end = min(p_start + (int)a.span, (int)a.L);
+  const int p_start = a.u0 + (int)(sp * a.span);
+  const int p_end = min(p_start + (int)a.span, a.u1);
 
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(a.x, a.x_bytes);
   const __amdgpu_buffer_rsrc_t rg = make_rsrc(a.dy, a.g_bytes);
@@ -437,9 +447,12 @@ __global__ __launch_bounds__(CL_NT) void dwconv1d_cl_causal_bwd_kernel(DwClCbArg
   const uint32_t gbase = (uint32_t)(b * a.gb + c0) * (uint32_t)sizeof(T);
   const uint32_t xrow = (uint32_t)a.xl * (uint32_t)sizeof(T);
   const uint32_t grow = (uint32_t)a.gl * (uint32_t)sizeof(T);
-  const int L = (int)a.L;
-  auto xld = [&](int p) { return bload16(rx, (p >= 0 && p < L) ? xbase + (uint32_t)p * xrow : kOOB, 0); };
-  auto gld = [&](int t) { return bload16(rg, (t >= 0 && t < L) ? gbase + (uint32_t)t * grow : kOOB, 0); };
+  const int L = (int)a.L, Lout = (int)a.Lout, sh = a.sh;
+  auto xld = [&](int p) {
+    const int q = p + sh;
+    return bload16(rx, (q >= 0 && q < L) ? xbase + (uint32_t)q * xrow : kOOB, 0);
+  };
+  auto gld = [&](int t) { return bload16(rg, (t >= 0 && t < Lout) ? gbase + (uint32_t)t * grow : kOOB, 0); };
   __amdgpu_buffer_rsrc_t rq;
   if constexpr (SEQ) rq = make_rsrc(a.seq, a.seq_bytes);
   auto seq_at = [&](int p) {
@@ -551,8 +564,9 @@ __global__ __launch_bounds__(CL_NT) void dwconv1d_cl_causal_bwd_kernel(DwClCbArg
 #pragma unroll
         for (int v = 0; v < VEC; ++v) d[v] = __builtin_fmaf(wv[j][v], m ? GAT(i + H - j, v) : 0.f, d[v]);
       }
-      if (p + i < L) st16<false>(op + (int64_t)(p + i) * a.ol, pack16<T>(d));
-      // dw / db for t = p + i (rows past L carry a zero gradient)
+      const int q = p + i + sh;
+      if (q >= 0 && q < L) st16<false>(op + (int64_t)q * a.ol, pack16<T>(d));
+      // dw / db for t = p + i (rows outside [0, L_out) carry a zero gradient)
 #pragma unroll
       for (int v = 0; v < VEC; ++v) accb[v] += GAT(i, v);
 #pragma unroll
@@ -845,8 +859,104 @@ extern "C" int atk_dwconv1d_cl_bwd_weight(const void* x, const void* dy, const i
   return check_launch("dwconv1d_cl_bwd_weight");
 }
 
+namespace atk {
+namespace {
+
+// Loop span of the fused backward: positions u in [min(0, -sh), max(L_out, L - sh)), cut
+// into per-thread runs of `run` positions (a multiple of CLB_STEP, at least 64) so that
+// about CLB_THREADS threads are in flight -- two waves per SIMD on 256 CUs; with a quarter of
+// that the kernel reached 0.50 of HBM instead of 0.63.  Each run leaves (K + 1) x VEC fp32
+// partials per thread, summed by the finalize kernel.
+constexpr int64_t CLB_THREADS = 131072;
+struct ClbSpan {
+  int sh, u0, u1;
+  uint32_t run, nrun;
+};
+ClbSpan clb_span(int64_t B, int64_t D, int64_t L, int K, int pad_left, int64_t L_out, int vec) {
+  ClbSpan r;
+  r.sh = (K - 1) - pad_left;
+  r.u0 = std::min(0, -r.sh);
+  r.u1 = (int)std::max<int64_t>(L_out, L - r.sh);
+  const int64_t len = (int64_t)r.u1 - r.u0, lanes = B * (D / vec);
+  int64_t run = (len * lanes + CLB_THREADS - 1) / CLB_THREADS;
+  run = std::max<int64_t>(64, (run + CLB_STEP - 1) / CLB_STEP * CLB_STEP);
+  r.run = (uint32_t)run;
+  r.nrun = (uint32_t)((len + run - 1) / run);
+  return r;
+}
+size_t clb_workspace_bytes(int64_t B, int64_t D, int K, const ClbSpan& sp) {
+  return (size_t)B * sp.nrun * (size_t)(K + 1) * (size_t)D * sizeof(float);
+}
+
+// The fused backward behind atk_causal_conv1d_cl_bwd (pad K-1, L_out = L, SiLU / seq_idx /
+// initial states) and atk_dwconv1d_cl_bwd (any left padding and output length, none of those).
+int cl_bwd_fused(const char* what, const void* x, const void* dout, const void* w, const void* bias,
+                 const int* seq_idx, const void* initial_states, void* dx, float* dw, float* db, int64_t B,
+                 int64_t D, int64_t L, int K, int pad_left, int64_t L_out, int64_t x_stride_b, int64_t x_stride_l,
+                 int64_t dout_stride_b, int64_t dout_stride_l, int64_t dx_stride_b, int64_t dx_stride_l,
+                 int64_t w_stride_c, int64_t w_stride_k, int64_t is_stride_b, int64_t is_stride_l, int dtype,
+                 int w_dtype, int silu, void* workspace, size_t ws_bytes, hipStream_t s) {
+  const int vec = cl_check(x, B, D, L, K, dtype, x_stride_b, x_stride_l);
+  if (vec < 0) return fail(-vec, "%s: unsupported shape/layout", what);
+  if (K < 2 || K > 4) return fail(ATK_UNSUPPORTED, "%s: width 2..4", what);
+  if (pad_left < 0 || L_out <= 0 || L_out > (1 << 30) || pad_left > (1 << 20))
+    return fail(ATK_EINVAL, "%s: bad padding / output length", what);
+  if (!dout || !dx || !w || !dw || !dtype_ok(w_dtype)) return fail(ATK_EINVAL, "%s: null pointer / dtype", what);
+  for (const auto& st : {std::pair<int64_t, int64_t>{dout_stride_b, dout_stride_l}, {dx_stride_b, dx_stride_l}})
+    if (st.first % vec || st.second % vec || st.second < D) return fail(ATK_UNSUPPORTED, "%s: dout / dx layout", what);
+  if (!aligned16(dout) || !aligned16(dx)) return fail(ATK_UNSUPPORTED, "%s: dout / dx alignment", what);
+  if (initial_states && (is_stride_b % vec || is_stride_l % vec || !aligned16(initial_states)))
+    return fail(ATK_UNSUPPORTED, "%s: initial_states layout", what);
+  if (seq_idx && (uint64_t)B * (uint64_t)L * 4u >= (1ull << 31))
+    return fail(ATK_UNSUPPORTED, "%s: seq_idx larger than 2 GiB", what);
+  const ClbSpan sp = clb_span(B, D, L, K, pad_left, L_out, vec);
+  const size_t need = clb_workspace_bytes(B, D, K, sp);
+  if (!workspace || ws_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 15u))
+    return fail(ATK_EINVAL, "%s: workspace too small or misaligned", what);
+  const size_t es = dtype_size(dtype);
+  const int64_t xspan = (L - 1) * x_stride_l + D, gspan = (L_out - 1) * dout_stride_l + D;
+  if ((B - 1) * x_stride_b * (int64_t)es + xspan * (int64_t)es >= ((int64_t)1 << 31) ||
+      (B - 1) * dout_stride_b * (int64_t)es + gspan * (int64_t)es >= ((int64_t)1 << 31))
+    return fail(ATK_UNSUPPORTED, "%s: tensors over 2 GiB", what);
+  DwClCbArgs a{};
+  a.x = x; a.dy = dout; a.dx = dx; a.w = w; a.b = bias; a.wdt = w_dtype; a.wc = w_stride_c; a.wk = w_stride_k;
+  cl_param_modes(w, bias, w_dtype, K, w_stride_c, w_stride_k, vec, &a.wmode, &a.bvec);
+  a.seq = seq_idx; a.init = initial_states; a.ib = is_stride_b; a.il = is_stride_l;
+  a.xb = x_stride_b; a.xl = x_stride_l; a.gb = dout_stride_b; a.gl = dout_stride_l;
+  a.ob = dx_stride_b; a.ol = dx_stride_l;
+  a.B = (uint32_t)B; a.D = (uint32_t)D; a.L = (uint32_t)L; a.Lout = (uint32_t)L_out;
+  a.sh = sp.sh; a.u0 = sp.u0; a.u1 = sp.u1;
+  a.x_bytes = (uint32_t)(((B - 1) * x_stride_b + xspan) * (int64_t)es);
+  a.g_bytes = (uint32_t)(((B - 1) * dout_stride_b + gspan) * (int64_t)es);
+  a.seq_bytes = (uint32_t)(B * L * 4);
+  a.ncv = (uint32_t)(D / vec);
+  a.span = sp.run;
+  a.nspan = sp.nrun;
+  a.div_ncv = make_fastdiv(a.ncv);
+  a.div_nspan = make_fastdiv(a.nspan);
+  a.part = static_cast<float*>(workspace);
+  const uint64_t threads = (uint64_t)B * a.nspan * a.ncv;
+  if (threads + CL_NT >= (1ull << 31)) return fail(ATK_UNSUPPORTED, "%s: too many threads", what);
+  const uint32_t blocks = (uint32_t)((threads + CL_NT - 1) / CL_NT);
+  int rc;
+  if (dtype == ATK_F32) rc = launch_clb<float>(a, K, blocks, silu, seq_idx != nullptr, s);
+  else if (dtype == ATK_F16) rc = launch_clb<_Float16>(a, K, blocks, silu, seq_idx != nullptr, s);
+  else rc = launch_clb<__bf16>(a, K, blocks, silu, seq_idx != nullptr, s);
+  if (rc != ATK_OK) return fail(rc, "%s: kernel width not served", what);
+  DwClBwArgs f{};
+  f.D = (uint32_t)D; f.part = a.part; f.dw = dw; f.db = db; f.P = (uint32_t)(B * a.nspan);
+  const uint32_t fblocks = (uint32_t)(((K + 1) * D + CLF_COLS - 1) / CLF_COLS);
+  hipLaunchKernelGGL(dwconv1d_cl_bwd_finalize_kernel, dim3(fblocks), dim3(CLF_COLS * CLF_SPLIT), 0, s, f, K);
+  return check_launch(what);
+}
+
+}  // namespace
+}  // namespace atk
+
 extern "C" size_t atk_causal_conv1d_cl_bwd_workspace_bytes(int64_t B, int64_t D, int64_t L, int K, int dtype) {
-  return atk_dwconv1d_cl_bwd_weight_workspace_bytes(B, D, L, K, dtype);
+  if (B <= 0 || D <= 0 || L <= 0 || K < 1 || !atk::dtype_ok(dtype)) return 0;
+  const int vec = 16 / (int)atk::dtype_size(dtype);
+  return atk::clb_workspace_bytes(B, D, K, atk::clb_span(B, D, L, K, K - 1, L, vec));
 }
 
 extern "C" int atk_causal_conv1d_cl_bwd(const void* x, const void* dout, const void* w, const void* bias,
@@ -857,54 +967,28 @@ extern "C" int atk_causal_conv1d_cl_bwd(const void* x, const void* dout, const v
                                         int64_t w_stride_k, int64_t is_stride_b, int64_t is_stride_l, int dtype,
                                         int w_dtype, int silu, void* workspace, size_t ws_bytes,
                                         atk_stream_t stream) {
-  using namespace atk;
-  const int vec = cl_check(x, B, D, L, K, dtype, x_stride_b, x_stride_l);
-  if (vec < 0) return fail(-vec, "causal_conv1d_cl_bwd: unsupported shape/layout");
-  if (K < 2 || K > 4) return fail(ATK_UNSUPPORTED, "causal_conv1d_cl_bwd: width 2..4");
-  if (!dout || !dx || !w || !dw || !dtype_ok(w_dtype)) return fail(ATK_EINVAL, "causal_conv1d_cl_bwd: null pointer / dtype");
-  for (const auto& st : {std::pair<int64_t, int64_t>{dout_stride_b, dout_stride_l}, {dx_stride_b, dx_stride_l}})
-    if (st.first % vec || st.second % vec || st.second < D) return fail(ATK_UNSUPPORTED, "causal_conv1d_cl_bwd: dout / dx layout");
-  if (!aligned16(dout) || !aligned16(dx)) return fail(ATK_UNSUPPORTED, "causal_conv1d_cl_bwd: dout / dx alignment");
-  if (initial_states && (is_stride_b % vec || is_stride_l % vec || !aligned16(initial_states)))
-    return fail(ATK_UNSUPPORTED, "causal_conv1d_cl_bwd: initial_states layout");
-  if (seq_idx && (uint64_t)B * (uint64_t)L * 4u >= (1ull << 31))
-    return fail(ATK_UNSUPPORTED, "causal_conv1d_cl_bwd: seq_idx larger than 2 GiB");
-  const size_t need = atk_dwconv1d_cl_bwd_weight_workspace_bytes(B, D, L, K, dtype);
-  if (!workspace || ws_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 15u))
-    return fail(ATK_EINVAL, "causal_conv1d_cl_bwd: workspace too small or misaligned");
-  const size_t es = dtype_size(dtype);
-  const int64_t xspan = (L - 1) * x_stride_l + D, gspan = (L - 1) * dout_stride_l + D;
-  if ((B - 1) * x_stride_b * (int64_t)es + xspan * (int64_t)es >= ((int64_t)1 << 31) ||
-      (B - 1) * dout_stride_b * (int64_t)es + gspan * (int64_t)es >= ((int64_t)1 << 31))
-    return fail(ATK_UNSUPPORTED, "causal_conv1d_cl_bwd: tensors over 2 GiB");
-  DwClCbArgs a{};
-  a.x = x; a.dy = dout; a.dx = dx; a.w = w; a.b = bias; a.wdt = w_dtype; a.wc = w_stride_c; a.wk = w_stride_k;
-  cl_param_modes(w, bias, w_dtype, K, w_stride_c, w_stride_k, vec, &a.wmode, &a.bvec);
-  a.seq = seq_idx; a.init = initial_states; a.ib = is_stride_b; a.il = is_stride_l;
-  a.xb = x_stride_b; a.xl = x_stride_l; a.gb = dout_stride_b; a.gl = dout_stride_l;
-  a.ob = dx_stride_b; a.ol = dx_stride_l;
-  a.B = (uint32_t)B; a.D = (uint32_t)D; a.L = (uint32_t)L;
-  a.x_bytes = (uint32_t)(((B - 1) * x_stride_b + xspan) * (int64_t)es);
-  a.g_bytes = (uint32_t)(((B - 1) * dout_stride_b + gspan) * (int64_t)es);
-  a.seq_bytes = (uint32_t)(B * L * 4);
-  a.ncv = (uint32_t)(D / vec);
-  a.span = clw_run(B, D, L, vec);  // a multiple of CLW_STEP, hence of CLB_STEP
-  a.nspan = (uint32_t)((L + a.span - 1) / a.span);
-  a.div_ncv = make_fastdiv(a.ncv);
-  a.div_nspan = make_fastdiv(a.nspan);
-  a.part = static_cast<float*>(workspace);
-  const uint64_t threads = (uint64_t)B * a.nspan * a.ncv;
-  if (threads + CL_NT >= (1ull << 31)) return fail(ATK_UNSUPPORTED, "causal_conv1d_cl_bwd: too many threads");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  const uint32_t blocks = (uint32_t)((threads + CL_NT - 1) / CL_NT);
-  int rc;
-  if (dtype == ATK_F32) rc = launch_clb<float>(a, K, blocks, silu, seq_idx != nullptr, s);
-  else if (dtype == ATK_F16) rc = launch_clb<_Float16>(a, K, blocks, silu, seq_idx != nullptr, s);
-  else rc = launch_clb<__bf16>(a, K, blocks, silu, seq_idx != nullptr, s);
-  if (rc != ATK_OK) return fail(rc, "causal_conv1d_cl_bwd: kernel width not served");
-  DwClBwArgs f{};
-  f.D = (uint32_t)D; f.part = a.part; f.dw = dw; f.db = db; f.P = (uint32_t)(B * a.nspan);
-  const uint32_t fblocks = (uint32_t)(((K + 1) * D + CLF_COLS - 1) / CLF_COLS);
-  hipLaunchKernelGGL(dwconv1d_cl_bwd_finalize_kernel, dim3(fblocks), dim3(CLF_COLS * CLF_SPLIT), 0, s, f, K);
-  return check_launch("causal_conv1d_cl_bwd");
+  return atk::cl_bwd_fused("causal_conv1d_cl_bwd", x, dout, w, bias, seq_idx, initial_states, dx, dw, db, B, D, L,
+                           K, K - 1, L, x_stride_b, x_stride_l, dout_stride_b, dout_stride_l, dx_stride_b,
+                           dx_stride_l, w_stride_c, w_stride_k, is_stride_b, is_stride_l, dtype, w_dtype, silu,
+                           workspace, ws_bytes, static_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t atk_dwconv1d_cl_bwd_workspace_bytes(int64_t B, int64_t D, int64_t L, int K, int pad_left,
+                                                      int64_t L_out, int dtype) {
+  if (B <= 0 || D <= 0 || L <= 0 || K < 1 || pad_left < 0 || L_out <= 0 || pad_left > (1 << 20) ||
+      !atk::dtype_ok(dtype))
+    return 0;
+  const int vec = 16 / (int)atk::dtype_size(dtype);
+  return atk::clb_workspace_bytes(B, D, K, atk::clb_span(B, D, L, K, pad_left, L_out, vec));
+}
+
+extern "C" int atk_dwconv1d_cl_bwd(const void* x, const void* dy, const void* w, void* dx, float* dw, float* db,
+                                   int64_t B, int64_t D, int64_t L, int K, int pad_left, int64_t L_out,
+                                   int64_t x_stride_b, int64_t x_stride_l, int64_t dy_stride_b, int64_t dy_stride_l,
+                                   int64_t dx_stride_b, int64_t dx_stride_l, int64_t w_stride_c, int64_t w_stride_k,
+                                   int dtype, int w_dtype, void* workspace, size_t ws_bytes, atk_stream_t stream) {
+  return atk::cl_bwd_fused("dwconv1d_cl_bwd", x, dy, w, nullptr, nullptr, nullptr, dx, dw, db, B, D, L, K, pad_left,
+                           L_out, x_stride_b, x_stride_l, dy_stride_b, dy_stride_l, dx_stride_b, dx_stride_l,
+                           w_stride_c, w_stride_k, 0, 0, dtype, w_dtype, 0, workspace, ws_bytes,
+                           static_cast<hipStream_t>(stream));
 }

@@ -93,6 +93,41 @@ def test_blh_backward_matches_oracle(case, dtype):
     _grad_close(b.grad, db, "blh dbias", 1e-5 if dtype == torch.float32 else 1e-2)
 
 
+# (B, L, D, K, pad_left, L_out): symmetric, 'valid', pad beyond K-1, one-sided, L = 1, and a
+# long row spanning several per-thread runs
+CL_BWD_FUSED = [
+    (2, 37, 64, 3, 1, 37),
+    (2, 50, 64, 3, 0, 48),
+    (3, 41, 128, 4, 3, 41),      # the causal form
+    (2, 29, 64, 2, 2, 31),       # pad_left = K: output longer than the input
+    (2, 33, 64, 3, 1, 32),       # one-sided: pad_left 1, pad_right 0
+    (1, 1, 64, 3, 1, 1),
+    (2, 2500, 256, 3, 1, 2500),
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("case", CL_BWD_FUSED, ids=lambda c: "_".join(map(str, c)))
+def test_blh_fused_backward_matches_oracle(case, dtype):
+    """atk_dwconv1d_cl_bwd (dx, dw, db in one pass) against the float64 oracle, on views: x a
+    channel slice of a wider tensor, dy dense; weight (D, K) as the transposed [K, D] view."""
+    from amd_tuned_torch import _native as nat
+    B, L, D, K, pad, l_out = case
+    g = torch.Generator().manual_seed(B * L + D + K + pad)
+    big = torch.randn(B, L, D + 64, generator=g).to(dtype)
+    x = big.cuda()[:, :, 32:32 + D]
+    w = (torch.randn(K, D, generator=g) / K ** 0.5).to(dtype)
+    dy = torch.randn(B, l_out, D, generator=g).to(dtype)
+    dx, dw, db = nat.dwconv1d_cl_bwd(x, dy.cuda(), w.cuda().t(), pad)
+    torch.cuda.synchronize()
+    rdx, rdw, rdb = O.dwconv1d_bwd(x.cpu().transpose(1, 2), w.t(), dy.transpose(1, 2), pad)
+    _close(dx, rdx.transpose(0, 2, 1), dtype, "fused dx")
+    _grad_close(dw, rdw, "fused dw", 1e-5 if dtype == torch.float32 else 1e-2)
+    _grad_close(db, rdb, "fused db", 1e-5 if dtype == torch.float32 else 1e-2)
+    dx2, dw2, db2 = nat.dwconv1d_cl_bwd(x, dy.cuda(), w.cuda().t(), pad)
+    assert torch.equal(dx, dx2) and torch.equal(dw, dw2) and torch.equal(db, db2), "not deterministic"
+
+
 # ---------------------------------------------------------------------------
 # causal_conv1d_fn, channel-last
 # ---------------------------------------------------------------------------
