@@ -616,8 +616,16 @@ def bench_gn_cl_backward_detail(shape, G, dev):
     torch_ms = event_time_ms(lambda: _dispatch._group_norm_backward(dy, x, G, gm, 1e-5, (True, True, True)), 10)
     nbytes = 3 * x.numel() * x.element_size()
     gbs = nbytes / (ms * 1e-3) / 1e9
+    # the library's rule (plan_gn_cl_bwd_res): one register-resident launch (+ a finalize for
+    # dgamma / dbeta) when 512 threads x 16 vectors of x and dy give exactly one workgroup per CU
+    C, N = shape[1], shape[0]
+    S, vec = x.numel() // (N * C), 16 // x.element_size()
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    nch = -(-S // (16 * (512 // (C // vec)))) if 512 % (C // vec) == 0 else 0
+    resident = nch and (nch >= G or G * nch <= 1024) and N * nch == cus
     return {"ms": round(ms, 4), "GB/s": round(gbs, 1), "roofline_frac": round(gbs / HBM_PEAK_GBS, 4),
-            "variant": "native gn_cl_bwd_stats/merge/apply (channels-last)",
+            "variant": ("native gn_cl_bwd_resident_kernel + rows finalize (channels-last)" if resident
+                        else "native gn_cl_bwd_stats/merge/apply (channels-last)"),
             "via_transposes_ms": round(tp_ms, 4),
             "torch_op_backward_ms": round(torch_ms, 4), "max_rel_err_vs_fp32_torch_ops": float(f"{err:.3g}")}
 

@@ -325,7 +325,8 @@ def workspace_keys() -> list:
 def _group_norm_buffers(device: Optional[torch.device]) -> list:
     idx = _device_index(device or torch.device("cuda", torch.cuda.current_device()))
     with _ws_lock:
-        return [b for (d, _, p), b in _ws_live.items() if d == idx and p in ("group_norm", "group_norm_cl")]
+        return [b for (d, _, p), b in _ws_live.items()
+                if d == idx and p in ("group_norm", "group_norm_cl", "group_norm_cl_bwd")]
 
 
 def group_norm_clear_diag(device: Optional[torch.device] = None) -> None:

@@ -2338,6 +2338,522 @@ int launch_gn_cl_bwd(const GnClBwdArgs& a, hipStream_t s) {
   return check_launch("gn_cl_bwd_apply_kernel");
 }
 
+// ---------------------------------------------------------------------------------------
+// Channels-last GroupNorm backward, register-resident: one read of x and dy, one write of
+// dx, in one launch plus a small finalize for the parameter gradients.  The chunking,
+// slots, epoch tags, stand-ins and the direct / two-level merge are the forward's
+// (gn_cl_resident_kernel); a chunk here holds EPV vectors of x and EPV of dy per thread.
+// Per (chunk, group) the record is (mean, M2) of x and, with gamma_c per channel,
+//   A = sum gamma_c dy,   B = sum gamma_c dy (x - mean_chunk),
+// merged over chunks as  A = sum A_i,  B = sum (B_i + (mean_i - mu) A_i).  Then, as in the
+// NC[S] backward, c1 = A / E, c2 = B rstd / E and  dx = rstd (gamma_c dy - c1 - (x - mu) rstd c2).
+// Each workgroup also writes a row of per-channel sums over its chunk, (rstd sum dy (x - mu),
+// sum dy); the finalize kernel adds the rows of every workgroup in a fixed order into
+// dgamma / dbeta.  Records travel as two slots (mean, M2) and (A, B), results as (mu, var),
+// (A, B).
+// ---------------------------------------------------------------------------------------
+struct GnClBwdResArgs {
+  const void* x;
+  const void* dy;
+  const void* gamma;
+  void* dx;             // may be null
+  float* dgamma;        // [C] or null
+  float* dbeta;         // [C] or null
+  uint32_t* hdr;        // workspace header (zero at allocation)
+  GnSlot* slots;        // [N][G][NCH][2]
+  GnSlot* finals;       // [N][G][2]
+  float2* rows;         // [N * NCH][C] (dgamma term, dbeta term) of each workgroup
+  int64_t S;
+  int SC, NCH;
+  int C, G, cpg, N;
+  int two_level;
+  int pdt;
+  float eps;
+  uint64_t wait_ticks;
+};
+
+template <typename A>
+__device__ __forceinline__ int clb_positions(const A& a, int c) {
+  const int64_t left = a.S - (int64_t)c * a.SC;
+  return left < a.SC ? (int)left : a.SC;
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t clb_rsrc(const void* t, const GnClBwdResArgs& a, int n, int c,
+                                                           int es) {
+  const char* base = static_cast<const char*>(t) + (((int64_t)n * a.S + (int64_t)c * a.SC) * a.C) * es;
+  return make_rsrc(base, (uint32_t)((int64_t)clb_positions(a, c) * a.C * es));
+}
+
+// Per-group records of chunk `ch` into r4[0..3][g] (mean, M2, A, B).  Thread t accumulates,
+// about K = its first x element, sum (x - K), sum (x - K)^2, A_t = sum gamma dy and
+// sum gamma dy (x - K); its (n, mean, M2, A, B about its own mean) go to LDS, and each group's
+// threads are merged by segmented butterflies.  FROM_REG: the owner, on its registers, which
+// also leaves per channel pdy[k] = sum dy and pdx[k] = sum dy (x - K) for the parameter
+// gradients; otherwise a stand-in, on memory, with the same arithmetic for the records.
+template <typename T, int NT, int EPV, bool FROM_REG>
+__device__ __forceinline__ void clb_chunk_stats(Vec16<T>* xb, Vec16<T>* db, __amdgpu_buffer_rsrc_t rx,
+                                                __amdgpu_buffer_rsrc_t rd, int P, const GnClBwdResArgs& a,
+                                                const float* gam, float* e5, float* red, float* r4, float& Kout,
+                                                float* pdy, float* pdx) {
+  constexpr int VEC = 16 / sizeof(T);
+  const int tid = threadIdx.x;
+  const int CV = a.C / VEC;
+  const int nv = P * CV;
+  const int v = tid % CV;
+  float gm[VEC];
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) gm[k] = gam[v * VEC + k];
+  auto getx = [&](int i) -> Vec16<T> {
+    if constexpr (FROM_REG) {
+      return xb[i];
+    } else {
+      Vec16<T> r;
+      r.raw = bload16(rx, (uint32_t)tid * 16u, (uint32_t)(i * NT * 16));
+      return r;
+    }
+  };
+  auto getd = [&](int i) -> Vec16<T> {
+    if constexpr (FROM_REG) {
+      return db[i];
+    } else {
+      Vec16<T> r;
+      r.raw = bload16(rd, (uint32_t)tid * 16u, (uint32_t)(i * NT * 16));
+      return r;
+    }
+  };
+  const float K = to_f32(getx(0).e[0]);
+  float s1 = 0.f, s2 = 0.f, sa = 0.f, sb = 0.f;
+  int nvt = 0;
+  auto acc = [&](int i) {
+    const bool ok = i * NT + tid < nv;
+    const float Ki = ok ? K : 0.f;
+    if constexpr (FROM_REG)
+      asm volatile("" : "+v"(xb[i].raw.x), "+v"(xb[i].raw.y), "+v"(xb[i].raw.z), "+v"(xb[i].raw.w),
+                   "+v"(db[i].raw.x), "+v"(db[i].raw.y), "+v"(db[i].raw.z), "+v"(db[i].raw.w), "+v"(s1), "+v"(s2),
+                   "+v"(sa), "+v"(sb));
+    const Vec16<T> xv = getx(i), dv = getd(i);
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+      const float d = to_f32(xv.e[k]) - Ki;  // vectors past the chunk read zero: d = 0, dy = 0
+      const float g = to_f32(dv.e[k]);
+      s1 += d;
+      s2 = fmaf(d, d, s2);
+      const float gg = gm[k] * g;
+      sa += gg;
+      sb = fmaf(gg, d, sb);
+      if constexpr (FROM_REG) {
+        pdy[k] += g;
+        pdx[k] = fmaf(g, d, pdx[k]);
+      }
+    }
+    // the per-channel sums are needed only at the end: left free, the compiler defers them
+    // there and keeps every vector's converted x and dy alive (and spills them)
+    if constexpr (FROM_REG) {
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) asm volatile("" : "+v"(pdy[k]), "+v"(pdx[k]));
+    }
+    nvt += ok ? 1 : 0;
+  };
+  if constexpr (FROM_REG) {
+#pragma unroll
+    for (int i = 0; i < EPV; ++i) acc(i);
+  } else {
+#pragma unroll 1
+    for (int i = 0; i < EPV; ++i) acc(i);
+  }
+  const float nt = (float)(nvt * VEC);
+  float mean_t = 0.f, m2_t = 0.f, b_t = 0.f;
+  if (nvt > 0) {
+    const float q = s1 / nt;
+    mean_t = K + q;
+    m2_t = fmaxf(fmaf(-s1, q, s2), 0.f);
+    b_t = fmaf(-q, sa, sb);  // sum gamma dy (x - mean_t) = sum gamma dy (x - K) - (mean_t - K) A_t
+  }
+  Kout = K;
+  e5[tid] = nt;
+  e5[NT + tid] = mean_t;
+  e5[2 * NT + tid] = m2_t;
+  e5[3 * NT + tid] = sa;
+  e5[4 * NT + tid] = b_t;
+  __syncthreads();
+  const int cpv = a.cpg / VEC, M = NT / a.G;
+  const int g = tid / M, j = tid - (tid / M) * M;
+  const int e = (j / cpv) * CV + g * cpv + (j - (j / cpv) * cpv);
+  const float ne = e5[e], me = e5[NT + e], qe = e5[2 * NT + e], ae = e5[3 * NT + e], be = e5[4 * NT + e];
+  const float n = seg_sum<NT>(ne, M, red);
+  const float mean = seg_sum<NT>(ne * me, M, red) / n;
+  const float d = me - mean;
+  const float m2 = seg_sum<NT>(fmaf(ne * d, d, qe), M, red);
+  const float A = seg_sum<NT>(ae, M, red);
+  const float B = seg_sum<NT>(fmaf(d, ae, be), M, red);
+  if (j == 0) {
+    r4[g] = mean;
+    r4[GN_CL_MAXG + g] = m2;
+    r4[2 * GN_CL_MAXG + g] = A;
+    r4[3 * GN_CL_MAXG + g] = B;
+  }
+  __syncthreads();
+}
+
+// (mu, var, A, B) of a group from its NCH chunk records t4[0..3][c], on one wave (lanes over
+// chunks, then the xor butterfly: every lane and every workgroup gets the same bits).
+__device__ __forceinline__ void clb_merge_group(const GnClBwdResArgs& a, const float* t4, int stride, float out[4]) {
+  const int lane = threadIdx.x & 63;
+  const float E = (float)(a.S * a.cpg);
+  float sm = 0.f, sa = 0.f;
+  for (int c = lane; c < a.NCH; c += 64) {
+    sm = fmaf((float)(clb_positions(a, c) * a.cpg), t4[c], sm);
+    sa += t4[2 * stride + c];
+  }
+  const float mu = wave_sum(sm) / E;
+  float m2 = 0.f, b = 0.f;
+  for (int c = lane; c < a.NCH; c += 64) {
+    const float d = t4[c] - mu;
+    m2 += t4[stride + c];
+    m2 = fmaf((float)(clb_positions(a, c) * a.cpg) * d, d, m2);
+    b = fmaf(d, t4[2 * stride + c], b + t4[3 * stride + c]);
+  }
+  out[0] = mu;
+  out[1] = wave_sum(m2) / E;
+  out[2] = wave_sum(sa);
+  out[3] = wave_sum(b);
+}
+
+// Workgroup-wide: records r < nrec (group gr(r) of chunk cr(r)) into t4[0..3][r] (stride
+// GN_CLR_DIRECT); this workgroup's own chunk from r4.  Polls as the forward's cl_collect;
+// chunks still missing at the deadline are computed from x and dy by the whole workgroup.
+template <typename T, int NT, int EPV, int RPT, typename GR, typename CR>
+__device__ __forceinline__ void clb_collect(const GnClBwdResArgs& a, int n, int ch, uint32_t tag, uint64_t deadline,
+                                            int nrec, GR gr, CR cr, float* t4, const float* r4, const float* gam,
+                                            float* e5, float* red, float* x4, int* s_flag, int* s_list, int* s_cnt) {
+  constexpr int ST = GN_CLR_DIRECT;
+  const int tid = threadIdx.x;
+  bool need[RPT];
+#pragma unroll
+  for (int k = 0; k < RPT; ++k) {
+    const int r = tid + k * NT;
+    need[k] = false;
+    if (r < nrec) {
+      if (cr(r) == ch) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) t4[q * ST + r] = r4[q * GN_CL_MAXG + gr(r)];
+      } else {
+        need[k] = true;
+      }
+    }
+  }
+  for (;;) {
+    float v[RPT][4];
+    bool ok[RPT];
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      ok[k] = false;
+      if (need[k]) {
+        const int r = tid + k * NT;
+        const GnSlot* sl = &a.slots[(((int64_t)n * a.G + gr(r)) * a.NCH + cr(r)) * 2];
+        const bool o0 = read_slot(sl, tag, v[k][0], v[k][1]);
+        const bool o1 = read_slot(sl + 1, tag, v[k][2], v[k][3]);
+        ok[k] = o0 && o1;
+      }
+    }
+    bool left = false;
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+      if (need[k] && ok[k]) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) t4[q * ST + tid + k * NT] = v[k][q];
+        need[k] = false;
+      }
+      left = left || need[k];
+    }
+    if (!left || wall_clock64() > deadline) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+#pragma unroll
+  for (int k = 0; k < RPT; ++k)
+    if (need[k]) {
+      const int c = cr(tid + k * NT);
+      if (atomicExch(&s_flag[c], 1) == 0) s_list[atomicAdd(s_cnt, 1)] = c;
+    }
+  __syncthreads();
+  const int nmiss = *s_cnt;
+  if (nmiss > 0) {
+    if (tid == 0) __hip_atomic_store(a.hdr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int m = 0; m < nmiss; ++m) {
+      const int c = s_list[m];
+      float Kd;
+      clb_chunk_stats<T, NT, EPV, false>(nullptr, nullptr, clb_rsrc(a.x, a, n, c, (int)sizeof(T)),
+                                         clb_rsrc(a.dy, a, n, c, (int)sizeof(T)), clb_positions(a, c), a, gam, e5,
+                                         red, x4, Kd, nullptr, nullptr);
+      for (int r = tid; r < nrec; r += NT)
+        if (cr(r) == c) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) t4[q * ST + r] = x4[q * GN_CL_MAXG + gr(r)];
+        }
+      __syncthreads();
+    }
+    for (int m = tid; m < nmiss; m += NT) s_flag[s_list[m]] = 0;
+    __syncthreads();
+    if (tid == 0) *s_cnt = 0;
+    __syncthreads();
+  }
+}
+
+// 512 threads x 16 vectors of x and of dy: 128 registers of data per thread, so two waves per
+// SIMD (256 VGPRs) and one workgroup per CU; at 8 vectors and four waves per SIMD the
+// per-channel sums and gamma spilled.
+template <typename T, int NT, int EPV>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2)))
+void gn_cl_bwd_resident_kernel(GnClBwdResArgs a) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int NW = NT / 64;
+  constexpr int RPT = GN_CLR_DIRECT / NT;
+  constexpr int ST = GN_CLR_DIRECT;
+  __shared__ float e5[5 * NT];
+  __shared__ float s_red[NW];
+  __shared__ float r4[4 * GN_CL_MAXG], x4[4 * GN_CL_MAXG];  // own chunk's / a stand-in's records
+  __shared__ float g4[4 * GN_CL_MAXG];                      // the sample's (mu, var, A, B) per group
+  __shared__ float gam[GN_CL_MAXC];
+  __shared__ float big[2 * NT * 8];                          // record table, then per-channel sums
+  __shared__ int s_flag[GN_CLR_MAXNCH], s_list[GN_CLR_MAXNCH];
+  __shared__ int s_cnt, s_gcnt;
+  __shared__ int s_glist[GN_CL_MAXG + 1];
+  static_assert(4 * GN_CLR_DIRECT <= 2 * NT * 8, "the record table fits");
+
+  const int tid = threadIdx.x;
+  const int n = blockIdx.x / a.NCH, ch = blockIdx.x - (blockIdx.x / a.NCH) * a.NCH;
+  const int CV = a.C / VEC;
+  const int P = clb_positions(a, ch);
+  const int nv = P * CV;
+  const int v = tid % CV, row = tid / CV, R = NT / CV;
+
+  const uint32_t epoch = __hip_atomic_load(a.hdr + 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int c = tid; c < a.C; c += NT) gam[c] = a.gamma ? load_param(a.gamma, a.pdt, c) : 1.f;
+  const __amdgpu_buffer_rsrc_t rx = clb_rsrc(a.x, a, n, ch, (int)sizeof(T));
+  const __amdgpu_buffer_rsrc_t rd = clb_rsrc(a.dy, a, n, ch, (int)sizeof(T));
+  Vec16<T> xb[EPV], db[EPV];
+#pragma unroll
+  for (int i = 0; i < EPV; ++i) xb[i].raw = bload16<2>(rx, (uint32_t)tid * 16u, (uint32_t)(i * NT * 16));
+#pragma unroll
+  for (int i = 0; i < EPV; ++i) db[i].raw = bload16<2>(rd, (uint32_t)tid * 16u, (uint32_t)(i * NT * 16));
+  if (tid == 0) {
+    s_cnt = 0;
+    s_gcnt = a.two_level ? (ch < a.G ? 1 : 0) : 1;
+    s_glist[0] = a.two_level ? ch : -1;
+  }
+  for (int c = tid; c < GN_CLR_MAXNCH; c += NT) s_flag[c] = 0;
+  __syncthreads();  // gam
+
+  float pdy[VEC], pdx[VEC], K;
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) pdy[k] = pdx[k] = 0.f;
+  clb_chunk_stats<T, NT, EPV, true>(xb, db, rx, rd, P, a, gam, e5, s_red, r4, K, pdy, pdx);
+  reg_fence<T, EPV>(xb);
+  reg_fence<T, EPV>(db);
+  const uint32_t tag = (epoch << 1) | 1u;
+  for (int g = tid; g < a.G; g += NT) {
+    GnSlot* sl = &a.slots[(((int64_t)n * a.G + g) * a.NCH + ch) * 2];
+    write_slot(sl, tag, r4[g], r4[GN_CL_MAXG + g]);
+    write_slot(sl + 1, tag, r4[2 * GN_CL_MAXG + g], r4[3 * GN_CL_MAXG + g]);
+  }
+  const uint64_t deadline = wall_clock64() + a.wait_ticks;
+
+  GnSlot* fin = a.finals + (int64_t)n * a.G * 2;
+  const int NCH = a.NCH;
+  bool polled = !a.two_level;
+  for (int k = 0;;) {
+    if (k < s_gcnt) {
+      const int gf = s_glist[k++];
+      clb_collect<T, NT, EPV, RPT>(a, n, ch, tag, deadline, gf < 0 ? a.G * NCH : NCH,
+                                   [&](int r) { return gf < 0 ? r / NCH : gf; },
+                                   [&](int r) { return gf < 0 ? r - (r / NCH) * NCH : r; }, big, r4, gam, e5, s_red,
+                                   x4, s_flag, s_list, &s_cnt);
+      __syncthreads();
+      const int w = tid >> 6;
+      for (int g = gf < 0 ? w : (w == 0 ? gf : a.G); g < (gf < 0 ? a.G : gf + 1); g += NW) {
+        float o[4];
+        clb_merge_group(a, gf < 0 ? big + g * NCH : big, ST, o);
+        if ((tid & 63) == 0) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) g4[q * GN_CL_MAXG + g] = o[q];
+          if (gf == ch && a.two_level) {
+            write_slot(&fin[2 * gf], tag, o[0], o[1]);
+            write_slot(&fin[2 * gf + 1], tag, o[2], o[3]);
+          }
+        }
+      }
+      __syncthreads();
+      continue;
+    }
+    if (polled) break;
+    polled = true;
+    for (int g = tid; g < a.G; g += NT) {
+      if (g == ch) continue;
+      float o[4];
+      bool ok;
+      for (;;) {
+        ok = read_slot(&fin[2 * g], tag, o[0], o[1]) && read_slot(&fin[2 * g + 1], tag, o[2], o[3]);
+        if (ok || wall_clock64() > deadline) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      if (ok) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) g4[q * GN_CL_MAXG + g] = o[q];
+      } else {
+        s_glist[atomicAdd(&s_gcnt, 1)] = g;
+      }
+    }
+    __syncthreads();
+  }
+
+  // this thread's channels lie in one group
+  const int g = (v * VEC) / a.cpg;
+  const float mu = g4[g], rstd = 1.0f / sqrtf(g4[GN_CL_MAXG + g] + a.eps);
+  const float E = (float)(a.S * a.cpg);
+  const float c1 = g4[2 * GN_CL_MAXG + g] / E;
+  const float c2 = g4[3 * GN_CL_MAXG + g] * rstd / E;
+  float gm[VEC];
+#pragma unroll
+  for (int k = 0; k < VEC; ++k) gm[k] = gam[v * VEC + k];
+  if (a.dx) {
+    T* __restrict__ dxc = static_cast<T*>(a.dx) + ((int64_t)n * a.S + (int64_t)ch * a.SC) * a.C;
+#pragma unroll
+    for (int i = 0; i < EPV; ++i) {
+      reg_fence<T, 1>(&xb[i]);
+      reg_fence<T, 1>(&db[i]);
+      const int e = i * NT + tid;
+      float o[VEC];
+#pragma unroll
+      for (int k = 0; k < VEC; ++k) {
+        const float xh = (to_f32(xb[i].e[k]) - mu) * rstd;
+        o[k] = rstd * (gm[k] * to_f32(db[i].e[k]) - c1 - xh * c2);
+      }
+      if (e < nv) st16<true>(dxc + (int64_t)e * VEC, pack16<T>(o));
+    }
+  }
+  if (a.dgamma || a.dbeta) {
+    // per channel over the chunk: rstd sum dy (x - mu) = rstd (pdx + (K - mu) pdy), sum dy;
+    // the R threads of a column are added in row order (threads past the chunk hold zeros)
+    float* cs = big;  // [R][C][2]
+    const float sh = K - mu;
+#pragma unroll
+    for (int k = 0; k < VEC; ++k) {
+      cs[((int64_t)row * a.C + v * VEC + k) * 2] = rstd * fmaf(sh, pdy[k], pdx[k]);
+      cs[((int64_t)row * a.C + v * VEC + k) * 2 + 1] = pdy[k];
+    }
+    __syncthreads();
+    float2* out = a.rows + (int64_t)blockIdx.x * a.C;
+    for (int c = tid; c < a.C; c += NT) {
+      float sg = 0.f, sb = 0.f;
+      for (int r = 0; r < R; ++r) {
+        sg += cs[((int64_t)r * a.C + c) * 2];
+        sb += cs[((int64_t)r * a.C + c) * 2 + 1];
+      }
+      out[c] = make_float2(sg, sb);
+    }
+  }
+  // done with the slots: count in blocks of GN_CLR_BLOCK; the last advances the epoch
+  if (tid == 0) {
+    const uint32_t b = blockIdx.x / GN_CLR_BLOCK, nb = (gridDim.x + GN_CLR_BLOCK - 1) / GN_CLR_BLOCK;
+    const uint32_t in_b = min((uint32_t)GN_CLR_BLOCK, gridDim.x - b * GN_CLR_BLOCK);
+    uint32_t* bc = a.hdr + 64 + 32 * b;
+    if (__hip_atomic_fetch_add(bc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == in_b - 1) {
+      __hip_atomic_store(bc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__hip_atomic_fetch_add(a.hdr + 32, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nb - 1) {
+        __hip_atomic_store(a.hdr + 32, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.hdr + 16, (epoch + 1u) & 0x7fffffffu, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+}
+
+// dgamma / dbeta: column c of the rows [nrows][C] summed in row order.  Each column's rows
+// are split over CLBF_SPLIT threads (contiguous ranges, loaded CLBF_U at a time so the loads
+// overlap), whose partials are then added in order: deterministic.
+constexpr int CLBF_COLS = 16, CLBF_SPLIT = 32, CLBF_U = 8;
+__global__ __launch_bounds__(CLBF_COLS * CLBF_SPLIT) void gn_cl_bwd_rows_finalize_kernel(const float2* rows, int nrows,
+                                                                                         int C, float* dgamma,
+                                                                                         float* dbeta) {
+  __shared__ float2 part[CLBF_SPLIT][CLBF_COLS];
+  const int cl = threadIdx.x % CLBF_COLS, sp = threadIdx.x / CLBF_COLS;
+  const int c = blockIdx.x * CLBF_COLS + cl;
+  const int per = (nrows + CLBF_SPLIT - 1) / CLBF_SPLIT;
+  const int r0 = sp * per, r1 = min(nrows, r0 + per);
+  float sg = 0.f, sb = 0.f;
+  if (c < C)
+    for (int r = r0; r < r1; r += CLBF_U) {
+      float2 q[CLBF_U];
+#pragma unroll
+      for (int u = 0; u < CLBF_U; ++u)
+        q[u] = r + u < r1 ? rows[(int64_t)(r + u) * C + c] : make_float2(0.f, 0.f);
+#pragma unroll
+      for (int u = 0; u < CLBF_U; ++u) {
+        sg += q[u].x;
+        sb += q[u].y;
+      }
+    }
+  part[sp][cl] = make_float2(sg, sb);
+  __syncthreads();
+  if (sp == 0 && c < C) {
+    float tg = 0.f, tb = 0.f;
+    for (int k = 0; k < CLBF_SPLIT; ++k) {
+      tg += part[k][cl].x;
+      tb += part[k][cl].y;
+    }
+    if (dgamma) dgamma[c] = tg;
+    if (dbeta) dbeta[c] = tb;
+  }
+}
+
+struct GnClBwdResPlan {
+  int NCH, SC, two_level;
+};
+
+template <typename T>
+int64_t gn_cl_bwd_res_capacity() {
+  static int per_cu[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (per_cu[dev] == 0 &&
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &per_cu[dev], reinterpret_cast<const void*>(gn_cl_bwd_resident_kernel<T, 512, 16>), 512, 0) != hipSuccess)
+    return 0;
+  return (int64_t)per_cu[dev] * device_cu_count();
+}
+
+// Register-resident configuration (512 threads x 16 vectors of x and of dy) for a shape, or
+// false.  Taken when the grid covers every CU and fits at once (`force` takes it wherever
+// it fits); merge forms as the forward's.
+template <typename T>
+bool plan_gn_cl_bwd_res(int64_t N, int64_t C, int64_t S, int G, bool force, GnClBwdResPlan& out) {
+  constexpr int VEC = 16 / sizeof(T);
+  constexpr int NT = 512, EPV = 16;
+  const int64_t CV = C / VEC;
+  if (C % VEC || (C / G) % VEC || C > GN_CL_MAXC || G > GN_CL_MAXG || NT % CV) return false;
+  const int64_t sc = (int64_t)EPV * (NT / CV);
+  const int64_t nch = (S + sc - 1) / sc;
+  if (nch > GN_CLR_MAXNCH || 2 * N * G * nch > GN_CLR_MAX_SLOTS || 2 * N * G > GN_CLR_MAX_FINALS) return false;
+  GnClBwdResPlan p{(int)nch, (int)sc, 0};
+  if (nch >= G) p.two_level = 1;
+  else if (G * nch <= GN_CLR_DIRECT) p.two_level = 0;
+  else return false;
+  const int64_t nblk = N * nch;
+  if (nblk > gn_cl_bwd_res_capacity<T>() || nblk > (int64_t)GN_CLR_BLOCK * GN_CLR_MAXBLK) return false;
+  if (!force && nblk < device_cu_count()) return false;
+  out = p;
+  return true;
+}
+
+template <typename T>
+int launch_gn_cl_bwd_res(const GnClBwdResArgs& a, int64_t N, hipStream_t s) {
+  hipLaunchKernelGGL((gn_cl_bwd_resident_kernel<T, 512, 16>), dim3((unsigned)(N * a.NCH)), dim3(512), 0, s, a);
+  int rc = check_launch("gn_cl_bwd_resident_kernel");
+  if (rc || !(a.dgamma || a.dbeta)) return rc;
+  hipLaunchKernelGGL(gn_cl_bwd_rows_finalize_kernel, dim3((unsigned)((a.C + CLBF_COLS - 1) / CLBF_COLS)),
+                     dim3(CLBF_COLS * CLBF_SPLIT), 0, s, a.rows, (int)(N * a.NCH), a.C, a.dgamma, a.dbeta);
+  return check_launch("gn_cl_bwd_rows_finalize_kernel");
+}
+
 }  // namespace
 
 int group_norm_num_variants() { return kNumGn; }
@@ -2704,8 +3220,14 @@ extern "C" int atk_group_norm_cl_fwd(const void* x, const void* gamma, const voi
 
 extern "C" size_t atk_group_norm_cl_bwd_workspace_bytes(int64_t N, int64_t C, int64_t S, int G) {
   if (N <= 0 || C <= 0 || S <= 0 || G <= 0) return 0;
+  // the register-resident kernel's header, slots and results (fixed layout), then either the
+  // three-kernel path's records / dx coefficients / dpar or the resident kernel's per-workgroup
+  // rows (chunks as small as fp32 makes them)
   const atk::GnClPlan p = atk::plan_gn_cl_bwd(N, S);
-  return (size_t)N * (size_t)C * ((size_t)p.NCH * 16 + 16 + 8);  // records, dx coefficients, dpar
+  const size_t three = (size_t)N * (size_t)C * ((size_t)p.NCH * 16 + 16 + 8);
+  const int64_t sc32 = std::max<int64_t>(1, 16 * (512 / std::max<int64_t>(1, C / 4)));
+  const size_t rows = (size_t)N * (size_t)((S + sc32 - 1) / sc32) * (size_t)C * 8;
+  return atk::GN_CLR_BYTES + std::max(three, rows);
 }
 
 extern "C" int atk_group_norm_cl_bwd(const void* x, const void* dy, const void* gamma, void* dx, float* dgamma,
@@ -2731,17 +3253,51 @@ extern "C" int atk_group_norm_cl_bwd(const void* x, const void* dy, const void* 
   if (!workspace || ws_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 15u))
     return fail(ATK_EINVAL, "group_norm backward (channels-last): workspace of %zu bytes (16-byte aligned) needed",
                 need);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // Register-resident single pass where the rule takes it (plan_gn_cl_bwd_res);
+  // ATK_GN_CL_RESIDENT=0 turns it off, =8 / =16 takes it wherever it fits.
+  const char* renv = getenv("ATK_GN_CL_RESIDENT");
+  const int rmode = renv ? atoi(renv) : 1;
+  if (rmode != 0) {
+    const bool force = rmode == 8 || rmode == 16;
+    GnClBwdResPlan rp;
+    const bool fits = dtype == ATK_F32   ? plan_gn_cl_bwd_res<float>(N, C, S, G, force, rp)
+                      : dtype == ATK_F16 ? plan_gn_cl_bwd_res<_Float16>(N, C, S, G, force, rp)
+                                         : plan_gn_cl_bwd_res<__bf16>(N, C, S, G, force, rp);
+    if (fits && GN_CLR_BYTES + (size_t)N * rp.NCH * (size_t)C * 8 <= ws_bytes) {
+      GnClBwdResArgs r;
+      r.x = x; r.dy = dy; r.gamma = gamma; r.dx = dx; r.dgamma = dgamma; r.dbeta = dbeta;
+      char* ws = static_cast<char*>(workspace);
+      r.hdr = reinterpret_cast<uint32_t*>(ws);
+      r.slots = reinterpret_cast<GnSlot*>(ws + GN_CLR_SLOTS_OFF);
+      r.finals = reinterpret_cast<GnSlot*>(ws + GN_CLR_FINALS_OFF);
+      r.rows = reinterpret_cast<float2*>(ws + GN_CLR_BYTES);
+      r.S = S; r.SC = rp.SC; r.NCH = rp.NCH;
+      r.C = (int)C; r.G = G; r.cpg = (int)cpg; r.N = (int)N;
+      r.two_level = rp.two_level;
+      r.pdt = param_dtype;
+      r.eps = eps;
+      const int khz = device_wall_clock_khz();
+      const char* wenv = getenv("ATK_GN_WAIT_US");
+      const uint64_t wait_us = wenv ? strtoull(wenv, nullptr, 10) : GN_WAIT_US;
+      r.wait_ticks = (uint64_t)(khz > 0 ? khz : 100000) * wait_us / 1000;
+      switch (dtype) {
+        case ATK_F32: return launch_gn_cl_bwd_res<float>(r, N, s);
+        case ATK_F16: return launch_gn_cl_bwd_res<_Float16>(r, N, s);
+        default: return launch_gn_cl_bwd_res<__bf16>(r, N, s);
+      }
+    }
+  }
   const GnClPlan p = plan_gn_cl_bwd(N, S);
   GnClBwdArgs a;
   a.x = x; a.dy = dy; a.gamma = gamma; a.dx = dx; a.dgamma = dgamma; a.dbeta = dbeta;
-  a.part = static_cast<float4*>(workspace);
+  a.part = reinterpret_cast<float4*>(static_cast<char*>(workspace) + GN_CLR_BYTES);
   a.coef = a.part + (size_t)N * p.NCH * C;
   a.dpar = reinterpret_cast<float2*>(a.coef + (size_t)N * C);
   a.S = S; a.SC = p.SC; a.NCH = p.NCH; a.N = (int)N;
   a.sample_bytes = (uint32_t)(S * C * es);
   a.C = (uint32_t)C; a.G = (uint32_t)G; a.cpg = (uint32_t)cpg;
   a.eps = eps; a.pdt = param_dtype;
-  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   switch (dtype) {
     case ATK_F32: return launch_gn_cl_bwd<float>(a, s);
     case ATK_F16: return launch_gn_cl_bwd<_Float16>(a, s);

@@ -395,6 +395,82 @@ def test_group_norm_channels_last_backward(dev, shape_g, dtype):
     assert dx2 is None and torch.equal(dg2.cpu(), nat.group_norm_cl_backward(dyd, xd, G, gm.to(dev), 1e-5)[1].cpu())
 
 
+@pytest.mark.parametrize("mode", ["16", "0"])
+@pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
+@pytest.mark.parametrize("shape_g", CL_BWD_SHAPES + [((2, 256, 100, 130), 32), ((1, 256, 31, 256), 32)],
+                         ids=lambda s: "x".join(map(str, s[0])) + f"_g{s[1]}")
+def test_group_norm_channels_last_backward_resident(dev, shape_g, dtype, mode, monkeypatch):
+    """The channels-last backward forced onto the register-resident kernel (and, "0", onto
+    the three kernels) wherever it fits: dx, dgamma, dbeta against the float64 oracle, with
+    and without affine weights; repeats are bit-identical and no record was computed by a
+    stand-in.  (2,256,100,130) has 51 chunks per sample (two-level), (1,256,31,256) 31 of 32
+    groups (direct)."""
+    shape, G = shape_g
+    nat = _native()
+    monkeypatch.setenv("ATK_GN_CL_RESIDENT", mode)
+    x, gm, _ = _inputs(shape, dtype, seed=len(shape) + G + 900)
+    dy = torch.randn(*shape, generator=torch.Generator().manual_seed(G + 17)).to(dtype)
+    fmt = torch.channels_last if len(shape) == 4 else torch.channels_last_3d
+    xd, dyd = x.to(dev).contiguous(memory_format=fmt), dy.to(dev).contiguous(memory_format=fmt)
+    for weight in (gm, None):
+        wd = None if weight is None else weight.to(dev)
+        dx, dg, db = nat.group_norm_cl_backward(dyd, xd, G, wd, 1e-5)
+        dx2, dg2, db2 = nat.group_norm_cl_backward(dyd, xd, G, wd, 1e-5)
+        torch.cuda.synchronize()
+        assert torch.equal(dx, dx2) and torch.equal(dg, dg2) and torch.equal(db, db2), "repeat differs"
+        rdx, rdg, rdb = O.group_norm_bwd(x, G, weight, dy, 1e-5)
+        assert O.max_rel_err(dx.cpu().contiguous(), rdx) <= BAR[dtype], O.max_rel_err(dx.cpu().contiguous(), rdx)
+        assert O.max_rel_err(dg.cpu(), rdg) <= BWD_BAR_P[dtype], O.max_rel_err(dg.cpu(), rdg)
+        assert O.max_rel_err(db.cpu(), rdb) <= BWD_BAR_P[dtype], O.max_rel_err(db.cpu(), rdb)
+    dxn, dgn, dbn = nat.group_norm_cl_backward(dyd, xd, G, gm.to(dev), 1e-5, (False, True, True))
+    assert dxn is None and torch.equal(dgn, nat.group_norm_cl_backward(dyd, xd, G, gm.to(dev), 1e-5)[1])
+    assert not nat.group_norm_barrier_error(dev)
+
+
+@pytest.mark.parametrize("shape", [(1, 256, 65, 256), (1, 256, 31, 256)], ids=["two_level", "direct"])
+def test_group_norm_channels_last_backward_standin_and_replay(dev, shape, monkeypatch):
+    """Resident channels-last backward: with a zero wait (stand-ins for records not yet
+    published) the outputs equal the normal path's byte for byte; captured in a HIP graph and
+    replayed with new inputs copied in between, every replay equals an eager run."""
+    nat = _native()
+    G = 32
+    monkeypatch.setenv("ATK_GN_CL_RESIDENT", "16")
+    fmt = torch.channels_last
+    data = []
+    for i in range(3):
+        x, gm, _ = _inputs(shape, torch.bfloat16, seed=950 + i)
+        dy = torch.randn(*shape, generator=torch.Generator().manual_seed(960 + i)).to(torch.bfloat16)
+        data.append((x.to(dev).contiguous(memory_format=fmt), dy.to(dev).contiguous(memory_format=fmt)))
+    gd = _inputs(shape, torch.bfloat16, seed=950)[1].to(dev)
+    ref = nat.group_norm_cl_backward(data[0][1], data[0][0], G, gd, 1e-5)
+    torch.cuda.synchronize()
+    assert not nat.group_norm_barrier_error(dev)
+    monkeypatch.setenv("ATK_GN_WAIT_US", "0")
+    for _ in range(2):
+        got = nat.group_norm_cl_backward(data[0][1], data[0][0], G, gd, 1e-5)
+        torch.cuda.synchronize()
+        for a, b in zip(got, ref):
+            assert torch.equal(a, b)
+    monkeypatch.delenv("ATK_GN_WAIT_US")
+    nat.group_norm_clear_diag(dev)
+    xs, dys = data[0][0].clone(), data[0][1].clone()
+    nat.group_norm_cl_backward(dys, xs, G, gd, 1e-5)   # workspace allocated before capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = nat.group_norm_cl_backward(dys, xs, G, gd, 1e-5)
+    for rep in range(6):
+        xs.copy_(data[rep % 3][0])
+        dys.copy_(data[rep % 3][1])
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = nat.group_norm_cl_backward(dys, xs, G, gd, 1e-5)
+        torch.cuda.synchronize()
+        for a, b in zip(out, eager):
+            assert torch.equal(a, b), f"replay {rep}"
+    assert not nat.group_norm_barrier_error(dev)
+
+
 def test_group_norm_channels_last_backward_c3_full_size(dev):
     """C3's NDHWC shape at full size, bf16, through the channels-last backward kernels:
     every gradient element against the oracle."""
