@@ -875,6 +875,46 @@ __global__ __launch_bounds__(256) void splitk_finalize_kernel(const float* __res
   y[i] = from_f32<T>(v);
 }
 
+// The same sum, 4 consecutive outputs per thread (16-byte partial loads, one 8- or 16-byte
+// store): for 4-aligned y / partials with the 4 outputs in one channel (NC[D]HW, spo % 4 == 0)
+// or in 4 consecutive channels (channels-last, Co % 4 == 0).  Same order of additions as the
+// scalar kernel, so the same bits.
+template <typename T>
+__global__ __launch_bounds__(256) void splitk_finalize4_kernel(const float4* __restrict__ part,
+                                                               const T* __restrict__ bias, T* __restrict__ y,
+                                                               int splits, int Co, int64_t spo4, int64_t total4,
+                                                               int cl) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total4) return;
+  float v[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < splits; ++s) {
+    const float4 q = part[(int64_t)s * total4 + i];
+    v[0] += q.x;
+    v[1] += q.y;
+    v[2] += q.z;
+    v[3] += q.w;
+  }
+  if (bias) {
+    if (cl) {
+      const int c = (int)((i * 4) % Co);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[k] += to_f32(bias[c + k]);
+    } else {
+      const float b = to_f32(bias[(i / spo4) % Co]);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[k] += b;
+    }
+  }
+  if constexpr (sizeof(T) == 4) {
+    reinterpret_cast<float4*>(y)[i] = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    T o[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = from_f32<T>(v[k]);
+    reinterpret_cast<uint2*>(y)[i] = *reinterpret_cast<const uint2*>(o);
+  }
+}
+
 struct IgVariant {
   const char* name;
   int dtype_class;  // 0 = 16-bit, 1 = fp32
@@ -1148,6 +1188,15 @@ int run_ig(const ConvShape& p, IgPlan& pl, const void* x, const void* wp, const 
   if (rc || pl.splits == 1) return rc;
   const int64_t ysz = (int64_t)p.N * p.Co * p.Do * p.Ho * p.Wo;
   const int64_t spo = (int64_t)p.Do * p.Ho * p.Wo;
+  const bool by4 = (cl ? p.Co % 4 == 0 : spo % 4 == 0) && (reinterpret_cast<uintptr_t>(y) % (4 * sizeof(T))) == 0 &&
+                   (reinterpret_cast<uintptr_t>(a.part) % 16) == 0;
+  if (by4) {
+    const int64_t n4 = ysz / 4;
+    hipLaunchKernelGGL((splitk_finalize4_kernel<T>), dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s,
+                       reinterpret_cast<const float4*>(a.part), static_cast<const T*>(bias), static_cast<T*>(y),
+                       pl.splits, p.Co, spo / 4, n4, cl ? 1 : 0);
+    return check_launch("splitk_finalize4_kernel");
+  }
   hipLaunchKernelGGL((splitk_finalize_kernel<T>), dim3((unsigned)((ysz + 255) / 256)), dim3(256), 0, s,
                      a.part, static_cast<const T*>(bias), static_cast<T*>(y), pl.splits, p.Co, spo, ysz, cl ? 1 : 0);
   return check_launch("splitk_finalize_kernel");
