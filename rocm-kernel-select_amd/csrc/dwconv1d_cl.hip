@@ -863,11 +863,11 @@ namespace atk {
 namespace {
 
 // Loop span of the fused backward: positions u in [min(0, -sh), max(L_out, L - sh)), cut
-// into per-thread runs of `run` positions (a multiple of CLB_STEP, at least 64) so that
-// about CLB_THREADS threads are in flight -- two waves per SIMD on 256 CUs; with a quarter of
-// that the kernel reached 0.50 of HBM instead of 0.63.  Each run leaves (K + 1) x VEC fp32
-// partials per thread, summed by the finalize kernel.
-constexpr int64_t CLB_THREADS = 131072;
+// into per-thread runs (multiples of CLB_STEP, at least 64) such that the grid is about one
+// workgroup per CU.  The wide kernels hold one wave per SIMD, so a grid slightly larger than
+// the CUs runs its last workgroups in a second round: 272 workgroups took C2's K = 4 backward
+// from 320 to 480 us, and 144 left half the CUs idle (0.50 of HBM); 256 ran every (K, pad) at
+// 0.61-0.65.  Each run leaves (K + 1) x VEC fp32 partials per thread for the finalize kernel.
 struct ClbSpan {
   int sh, u0, u1;
   uint32_t run, nrun;
@@ -878,7 +878,10 @@ ClbSpan clb_span(int64_t B, int64_t D, int64_t L, int K, int pad_left, int64_t L
   r.u0 = std::min(0, -r.sh);
   r.u1 = (int)std::max<int64_t>(L_out, L - r.sh);
   const int64_t len = (int64_t)r.u1 - r.u0, lanes = B * (D / vec);
-  int64_t run = (len * lanes + CLB_THREADS - 1) / CLB_THREADS;
+  const int64_t wg_per_run = (lanes + CL_NT - 1) / CL_NT;
+  const int cus = device_cu_count();
+  const int64_t runs = std::max<int64_t>(1, (cus > 0 ? cus : 256) / wg_per_run);
+  int64_t run = (len + runs - 1) / runs;
   run = std::max<int64_t>(64, (run + CLB_STEP - 1) / CLB_STEP * CLB_STEP);
   r.run = (uint32_t)run;
   r.nrun = (uint32_t)((len + run - 1) / run);
