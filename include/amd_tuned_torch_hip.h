@@ -296,8 +296,14 @@ int atk_group_norm_fwd_noalloc(const void* x, const void* gamma, const void* bet
  * amd_tuned_torch/_dispatch.py:2140-2200); same arithmetic and parameters as
  * atk_group_norm_fwd.  Needs (C/G)*sizeof(dtype) % 16 == 0, C*sizeof(dtype)/16 dividing
  * 256 (C <= 2048 for 16-bit types), G <= 256 and 16-byte aligned x / y (else
- * ATK_UNSUPPORTED).  The workspace (atk_group_norm_cl_workspace_bytes) needs no
- * initialisation.  Deterministic.
+ * ATK_UNSUPPORTED).  Deterministic.
+ * Where 128 KB chunks cover every CU, one register-resident launch exchanges per-chunk
+ * statistics between workgroups through the workspace (atk_group_norm_cl_workspace_bytes),
+ * whose first bytes hold an epoch and counters that every launch leaves consistent: the
+ * workspace must be zero-filled once when it is allocated and then passed unchanged to
+ * later calls (its contents are the state), and calls sharing one workspace must be
+ * ordered (one stream).  ATK_GN_CL_RESIDENT=0 in the environment keeps the three-kernel
+ * path (8 or 16 forces the resident configuration with that many vectors per thread).
  * ------------------------------------------------------------------------- */
 size_t atk_group_norm_cl_workspace_bytes(int64_t N, int64_t C, int64_t S, int G);
 int atk_group_norm_cl_fwd(const void* x, const void* gamma, const void* beta, void* y,
@@ -334,9 +340,12 @@ int atk_group_norm_bwd(const void* x, const void* dy, const void* gamma, void* d
  * (amd_tuned_torch/ck_norm_ops.py:9-27, 93-103).  Same math and arguments as
  * atk_group_norm_bwd.  Needs (C/G) * sizeof(dtype) a multiple of 16,
  * C / (16 / sizeof(dtype)) dividing 256 (C <= 2048 for 16-bit types), 16-byte
- * aligned x / dy / dx and one sample under 2 GiB (else ATK_UNSUPPORTED).  The
- * workspace (atk_group_norm_cl_bwd_workspace_bytes, 16-byte aligned) needs no
- * initialisation.  All sums are taken in a fixed order (deterministic).
+ * aligned x / dy / dx and one sample under 2 GiB (else ATK_UNSUPPORTED).  All sums are
+ * taken in a fixed order (deterministic).  The workspace
+ * (atk_group_norm_cl_bwd_workspace_bytes, 16-byte aligned) follows the forward's rule: zero-
+ * filled once when allocated, then passed unchanged to later calls on one stream (a register-
+ * resident launch, taken where the grid is one workgroup per CU, keeps an epoch and counters
+ * in its first bytes).
  * ------------------------------------------------------------------------- */
 size_t atk_group_norm_cl_bwd_workspace_bytes(int64_t N, int64_t C, int64_t S, int G);
 int atk_group_norm_cl_bwd(const void* x, const void* dy, const void* gamma, void* dx, float* dgamma,
