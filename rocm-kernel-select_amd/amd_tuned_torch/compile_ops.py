@@ -66,6 +66,24 @@ def _placeholder(like: torch.Tensor) -> torch.Tensor:
     return like.new_empty((0,))
 
 
+def _conform(t: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
+    """`t` with the dtype and strides of `like`, which is what a fake built by
+    torch.empty_like(like) promised the compiled graph.  The eager bodies can return other
+    dtypes (a stock fallback keeps the parameter dtype, a float32 weight promotes the input
+    gradient) or layouts; a graph built on the fake would then read the buffer with the wrong
+    element size or stride."""
+    if t.dtype == like.dtype and t.shape == like.shape and t.stride() == like.stride():
+        return t
+    out = torch.empty_like(like)
+    out.copy_(t)
+    return out
+
+
+def _f32_vector(t: torch.Tensor) -> torch.Tensor:
+    """A 1-D float32 contiguous gradient (the GroupNorm backward fake's dgamma / dbeta)."""
+    return t.to(torch.float32).contiguous()
+
+
 # ---------------------------------------------------------------------------
 # Eager bodies: the dispatch the patched API runs, reached lazily (the dispatch modules
 # import this one).
@@ -118,9 +136,11 @@ if _HAS_CUSTOM_OP and not _registered("group_norm"):
                            weight: Optional[torch.Tensor], eps: float, mask: list[bool]
                            ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         gx, gw, gb = _gn_backward(grad, input_, num_groups, weight, eps, mask)
-        return (gx if gx is not None else _placeholder(input_),
-                gw if gw is not None else _placeholder(input_),
-                gb if gb is not None else _placeholder(input_))
+        # the native backward gives dgamma / dbeta in float32, the torch-op fallback (a shape
+        # the native kernels decline) in the parameter dtypes: the fake promises float32
+        return (_conform(gx, input_) if gx is not None else _placeholder(input_),
+                _f32_vector(gw) if gw is not None else _placeholder(input_),
+                _f32_vector(gb) if gb is not None else _placeholder(input_))
 
     @_group_norm_bwd_op.register_fake
     def _(grad, input_, num_groups, weight, eps, mask):
@@ -183,9 +203,9 @@ if _HAS_CUSTOM_OP and not _registered("group_norm"):
                      stride: list[int], padding: list[int], dilation: list[int], nd: int,
                      mask: list[bool]) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         gi, gw, gb = _conv_backward(grad, input_, weight, has_bias, stride, padding, dilation, nd, mask)
-        return (gi if gi is not None else _placeholder(input_),
-                gw if gw is not None else _placeholder(input_),
-                gb if gb is not None else _placeholder(input_))
+        return (_conform(gi, input_) if gi is not None else _placeholder(input_),
+                _conform(gw, weight) if gw is not None else _placeholder(input_),
+                gb.to(weight.dtype).contiguous() if gb is not None else _placeholder(input_))
 
     @_conv_bwd_op.register_fake
     def _(grad, input_, weight, has_bias, stride, padding, dilation, nd, mask):

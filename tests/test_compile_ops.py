@@ -170,3 +170,52 @@ def test_custom_op_autograd_formulas_on_cpu():
     xg2 = xg.detach().requires_grad_(True)
     (gx_only,) = torch.autograd.grad(ops.group_norm(xg2, 4, gm.detach(), bt.detach(), 1e-5).sum(), (xg2,))
     assert gx_only.shape == xg2.shape
+
+
+def _real_vs_fake(op, *args):
+    """(real outputs, fake outputs) of one custom op on the same arguments."""
+    real = op(*args)
+    with FakeTensorMode(allow_non_fake_inputs=True) as mode:
+        fargs = [mode.from_tensor(a) if isinstance(a, torch.Tensor) else a for a in args]
+        fake = op(*fargs)
+    return real, fake
+
+
+def test_group_norm_backward_op_outputs_match_its_fake():
+    """The backward op's real outputs carry the dtypes and strides its fake promises, also when
+    the eager body falls back to the torch-op backward (CPU here; on a GPU a shape the native
+    kernels decline), which computes dgamma / dbeta in the parameter dtypes: a compiled graph
+    built on the fake would otherwise read 2-byte gradients as float32."""
+    torch.manual_seed(0)
+    for dt, wdt, cl in ((torch.bfloat16, torch.bfloat16, False), (torch.float16, torch.float16, False),
+                        (torch.bfloat16, torch.float32, False), (torch.bfloat16, torch.bfloat16, True)):
+        x = torch.randn(2, 8, 14, 14).to(dt)
+        if cl:
+            x = x.contiguous(memory_format=torch.channels_last)
+        dy = torch.randn(2, 8, 14, 14).to(dt).contiguous(memory_format=torch.channels_last if cl
+                                                           else torch.contiguous_format)
+        w = (1 + 0.1 * torch.randn(8)).to(wdt)
+        real, fake = _real_vs_fake(ops.group_norm_backward, dy, x, 4, w, 1e-5, [True, True, True])
+        for r, f in zip(real, fake):
+            assert r.dtype == f.dtype and r.shape == f.shape and r.stride() == f.stride(), \
+                (dt, wdt, cl, r.dtype, f.dtype, r.stride(), f.stride())
+        # the conformed values are the fallback's own
+        ref = torch.ops.aten.native_group_norm_backward(
+            dy.float().contiguous(), x.float().contiguous(), *torch.ops.aten.native_group_norm(
+                x.float().contiguous(), w.float(), None, 2, 8, 196, 4, 1e-5)[1:], w.float(), 2, 8, 196, 4,
+            [True, True, True])
+        assert torch.allclose(real[1], ref[1], rtol=2e-2, atol=2e-2)
+        assert torch.allclose(real[2], ref[2], rtol=2e-2, atol=2e-2)
+
+
+def test_conv_backward_op_outputs_match_its_fake():
+    """Same check for the conv backward op (dx in the input's layout and dtype, dw in the
+    weight's, db in the weight dtype)."""
+    torch.manual_seed(0)
+    x = torch.randn(1, 4, 6, 6).to(torch.bfloat16)
+    w = (0.2 * torch.randn(6, 4, 3, 3)).to(torch.bfloat16)
+    dy = torch.randn(1, 6, 6, 6).to(torch.bfloat16)
+    real, fake = _real_vs_fake(ops.conv_backward, dy, x, w, True, [1, 1], [1, 1], [1, 1], 2,
+                               [True, True, True])
+    for r, f in zip(real, fake):
+        assert r.dtype == f.dtype and r.shape == f.shape and r.stride() == f.stride()
