@@ -24,6 +24,7 @@
 //  * Split-K over stages for shapes with too few output tiles to fill 256 CUs, with
 //    per-split fp32 partials summed in a deterministic finalize kernel.
 #include <algorithm>
+#include <cstdlib>
 
 #include "conv_common.h"
 
@@ -60,6 +61,8 @@ struct IgArgs {
   int gn_cpg;         // channels per GroupNorm group: 4, 8, 16, 32 or a multiple of 32
   int gn_G;           // groups (Co = gn_G * gn_cpg)
   int gn_np;          // records per (n, g)
+  int lds_epi;        // unsplit plain 16-bit NC[D]HW output through the LDS-staged epilogue
+  int epi_pitch;      // its staging row pitch in bytes (BM * 2 + 16)
 };
 
 template <typename T> struct MfmaTraits;
@@ -496,6 +499,55 @@ __device__ __forceinline__ void store_tile(const IgArgs& a, f32x16 (&acc)[FCO][F
   }
 }
 
+// Plain output (bias added, 16-bit, NC[D]HW, unsplit) through LDS.  Stored straight from the
+// accumulators, every value is its own 2-byte store (a lane holds one position of 16 channels
+// per block), so a wave issues FCO * FSP * 16 store instructions, each moving 128 bytes; at the
+// end of a launch whose workgroups all finish together those stores are what the chip waits
+// for.  Here the tile goes to LDS as [channel][position] rows (pitch a.epi_pitch = BM * 2 + 16:
+// the two lane halves' rows, 4 channels apart, fall on disjoint banks), then every thread of
+// the workgroup stores 16-byte runs of 8 positions of one channel.  Needs TX % 8 == 0,
+// Wo % 8 == 0 and a 16-byte aligned y (host check), so a run is whole inside or outside the
+// output and aligned.  The caller has passed a barrier after the last read of the stage
+// buffers; every thread of the workgroup calls this (the K groups of a split workgroup too:
+// `active` is false for the ones whose accumulators were already handed over).
+template <typename T, int FCO, int FSP, int BN, int BM>
+__device__ __forceinline__ void store_tile_lds(const IgArgs& a, f32x16 (&acc)[FCO][FSP], const float* s_bias,
+                                               char* stg, int n, int co_tile, int oz, int oy0, int ox0, int wco,
+                                               int wsp, bool active, int tid, int nthreads) {
+  static_assert(sizeof(T) == 2, "16-bit outputs");
+  int lane = threadIdx.x & 63;
+  asm volatile("" : "+v"(lane));  // keep the address math below the main loop
+  const int half = lane >> 5, col = lane & 31;
+  const int EP = a.epi_pitch;
+  if (active) {
+#pragma unroll
+    for (int i = 0; i < FCO; ++i)
+#pragma unroll
+      for (int j = 0; j < FSP; ++j) {
+        const int m = (wsp * FSP + j) * 32 + col;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int cl = (wco * FCO + i) * 32 + (r >> 2) * 8 + half * 4 + (r & 3);
+          *reinterpret_cast<T*>(stg + cl * EP + m * 2) = from_f32<T>(acc[i][j][r] + s_bias[cl]);
+        }
+      }
+  }
+  __syncthreads();
+  const int64_t spo = (int64_t)a.Do * a.Ho * a.Wo;
+  constexpr int RPR = BM / 8;  // 16-byte runs per channel row
+  for (int q = tid; q < BN * RPR; q += nthreads) {
+    const int cl = q / RPR, m = (q - (q / RPR) * RPR) * 8;
+    const int ty = m / a.TX, tx = m - (m / a.TX) * a.TX;
+    const int oy = oy0 + ty, ox = ox0 + tx;
+    const int co = co_tile * BN + cl;
+    if (oy < a.Ho && ox < a.Wo && co < a.Co) {
+      const uint4 v = *reinterpret_cast<const uint4*>(stg + cl * EP + m * 2);
+      *reinterpret_cast<uint4*>(static_cast<T*>(a.y) + ((int64_t)n * a.Co + co) * spo +
+                                ((int64_t)oz * a.Ho + oy) * a.Wo + ox) = v;
+    }
+  }
+}
+
 // Tiles of 8 accumulator blocks (128 AGPRs) are asked to fit 2 waves per SIMD: with their
 // LDS footprint two workgroups share a CU, and one wave per SIMD leaves no latency cover.
 //
@@ -796,6 +848,9 @@ void conv_igemm_kernel(IgArgs a) {
     kd = kd1;
   }
 
+  // the LDS-staged plain epilogue (a runtime choice of the host: see store_tile_lds)
+  constexpr bool LDS_EPI_OK = sizeof(T) == 2 && !EPI && !CL;
+  const bool lds_epi = LDS_EPI_OK && a.lds_epi;
   if constexpr (KS > 1) {
     // groups 1..KS-1 park their accumulators in LDS (the patch buffers are free: the last
     // iteration ended with a barrier); group 0 adds them in group order
@@ -812,14 +867,25 @@ void conv_igemm_kernel(IgArgs a) {
           for (int r = 0; r < 16; ++r) red[slot(kg, i, j, r)] = acc[i][j][r];
     }
     __syncthreads();
-    if (kg > 0) return;
-    for (int g = 1; g < KS; ++g)
+    if (kg > 0 && !lds_epi) return;
+    if (kg == 0) {
+      for (int g = 1; g < KS; ++g)
 #pragma unroll
-      for (int i = 0; i < FCO; ++i)
+        for (int i = 0; i < FCO; ++i)
 #pragma unroll
-        for (int j = 0; j < FSP; ++j)
+          for (int j = 0; j < FSP; ++j)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) acc[i][j][r] += red[slot(g, i, j, r)];
+            for (int r = 0; r < 16; ++r) acc[i][j][r] += red[slot(g, i, j, r)];
+    }
+    if (lds_epi) __syncthreads();  // every group is done with the hand-over area
+  }
+  if constexpr (LDS_EPI_OK) {
+    if (lds_epi) {
+      // (KS == 1: the last stage ended with a barrier, so the patch buffers are free)
+      store_tile_lds<T, FCO, FSP, BN, WSP * FSP * 32>(a, acc, s_bias, lds_base, n, co_tile, oz, oy0, ox0, wco, wsp,
+                                                     kg == 0, threadIdx.x, 64 * NWG * KS);
+      return;
+    }
   }
   // GroupNorm record index of this wave's spatial tile: (z, tile row, tile column), then wave
   const int sp_rec = ((oz * a.tiles_y + ty_t) * a.tiles_x + tx_t) * WSP + wsp;
@@ -956,6 +1022,12 @@ const IgVariant kIg[] = {
     {"f32_w22_f11_cb16_k3", 1, 2, 2, 1, 1, 16, 1, 1, 3},
     // the 7x7-plane tile with two K groups: half the split-K partials in memory
     {"h_w14_f22_cb16x2_k2", 0, 1, 4, 2, 2, 16, 2, 16, 2},
+    // the large tiles with two K groups (two waves per SIMD from one workgroup per CU):
+    // shapes with about one output tile per CU (config 5's 256-channel conv) then need no
+    // split-K partials in memory and no finalize pass
+    {"h_w22_f24_cb16_k2", 0, 2, 2, 2, 4, 16, 1, 16, 2},
+    {"h_w41_f22_cb32_k2", 0, 4, 1, 2, 2, 32, 1, 16, 2},
+    {"h_w21_f24_cb32_k2", 0, 2, 1, 2, 4, 32, 1, 16, 2},
 };
 constexpr int kNumIg = sizeof(kIg) / sizeof(kIg[0]);
 
@@ -1151,6 +1223,22 @@ int run_ig(const ConvShape& p, IgPlan& pl, const void* x, const void* wp, const 
   a.wp_bytes = (uint32_t)pl.wp_bytes;
   a.wp = wp;
   a.part = pl.splits > 1 ? part : nullptr;
+  // LDS-staged epilogue for plain unsplit 16-bit NC[D]HW output (store_tile_lds), when its
+  // staging area fits without costing a resident workgroup per CU
+  a.lds_epi = 0;
+  a.epi_pitch = pl.bm * 2 + 16;
+  {
+    // ATK_CONV_LDS_EPI=0 keeps the per-value stores (read per call: tests compare the two)
+    const char* e = getenv("ATK_CONV_LDS_EPI");
+    const bool off = e && e[0] == '0';
+    const size_t stg = (size_t)pl.bn * a.epi_pitch;
+    constexpr size_t kLdsCu = 160 * 1024;
+    if (!off && sizeof(T) == 2 && !cl && !resid && !gn_parts && pl.splits == 1 && p.Wo % 8 == 0 &&
+        a.TX % 8 == 0 && aligned16(y) && stg <= 150 * 1024 && kLdsCu / std::max(pl.lds, stg) == kLdsCu / pl.lds) {
+      a.lds_epi = 1;
+      pl.lds = std::max(pl.lds, stg);
+    }
+  }
   // instantiate only the variants of this element type's class
   if constexpr (sizeof(T) == 2) {
     switch (v) {
@@ -1172,6 +1260,9 @@ int run_ig(const ConvShape& p, IgPlan& pl, const void* x, const void* wp, const 
       case 19: rc = launch_ig_t<T, 2, 2, 1, 1, 16, 1, 4>(pl, s); break;
       case 20: rc = launch_ig_t<T, 1, 2, 2, 1, 32, 1, 2>(pl, s); break;
       case 23: rc = launch_ig_t<T, 1, 4, 2, 2, 16, 2, 2>(pl, s); break;
+      case 24: rc = launch_ig_t<T, 2, 2, 2, 4, 16, 1, 2>(pl, s); break;
+      case 25: rc = launch_ig_t<T, 4, 1, 2, 2, 32, 1, 2>(pl, s); break;
+      case 26: rc = launch_ig_t<T, 2, 1, 2, 4, 32, 1, 2>(pl, s); break;
       default: return fail(ATK_EINVAL, "conv: bad variant");
     }
   } else {

@@ -540,3 +540,41 @@ def test_packed_weight_cache_follows_the_weight(dev):
     del wd
     gc.collect()
     assert nat.packed_weight_cache_size() == 0                 # entries die with the weight
+
+
+LDS_EPI_CASES = [
+    # one K stage (never split K): every 16-bit tile's plain epilogue runs; rows partly
+    # outside the output (H = 10), depth and 2-D shapes
+    ((1, 16, 4, 10, 64), (64, 16, 1, 3, 3)),
+    ((2, 16, 3, 16, 32), (96, 16, 1, 3, 3)),
+    ((2, 16, 12, 64), (32, 16, 3, 3)),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("case", LDS_EPI_CASES, ids=lambda c: "x".join(map(str, c[0])))
+def test_conv_lds_staged_epilogue_bit_exact(dev, case, dtype, monkeypatch):
+    """The LDS-staged epilogue (16-byte runs of 8 positions per channel) stores the same bits as
+    the per-value stores it replaces (ATK_CONV_LDS_EPI=0), for every 16-bit tile, and both
+    match the float64 oracle."""
+    xs, ws = case
+    nat = _native()
+    x, w, b = _inputs(xs, ws, dtype, seed=11)
+    conv = nat.conv3d if len(xs) == 5 else nat.conv2d
+    ref = (O.conv3d if len(xs) == 5 else O.conv2d)(x, w, b, 1, (0, 1, 1) if len(xs) == 5 else 1, 1)
+    pad = (0, 1, 1) if len(xs) == 5 else 1
+    xd, wd, bd = x.to(dev), w.to(dev), b.to(dev)
+    ran = 0
+    for vi, name in _variants_for(dtype):
+        try:
+            monkeypatch.setenv("ATK_CONV_LDS_EPI", "0")
+            want = conv(xd, wd, bd, 1, pad, 1, variant=vi)
+            monkeypatch.delenv("ATK_CONV_LDS_EPI")
+            got = conv(xd, wd, bd, 1, pad, 1, variant=vi)
+        except nat.Unsupported:
+            continue
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), name
+        assert O.max_rel_err(got.cpu(), ref) <= BAR[dtype], name
+        ran += 1
+    assert ran >= 5
