@@ -277,12 +277,16 @@ int atk_group_norm_fwd(const void* x, const void* gamma, const void* beta, void*
  * reference: it is for callers that cannot allocate device memory or hand over scratch --
  * code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.  Same
  * arguments (minus the workspace), kernels and results as atk_group_norm_fwd; the caller
- * still passes x and y.  The scratch is a static device array of
- * atk_group_norm_noalloc_scratch_bytes() bytes (about 2.1 MB) that each GPU the library
- * runs on holds until the process ends; shapes needing more (two-pass partials above 1 MiB)
- * are rejected with ATK_EINVAL.  Every call on one GPU shares that GPU's array, so calls that
- * overlap on one GPU (e.g. on two streams) race; calls ordered on one stream do not.  The
- * first call on a device resolves the array's address there (make it outside graph capture).
+ * still passes x and y.  The scratch is a static device array of 4 slices of
+ * atk_group_norm_noalloc_scratch_bytes() bytes (about 2.1 MB each, 8.5 MB in all) that each
+ * GPU the library runs on holds until the process ends; shapes needing more than a slice
+ * (two-pass partials above 1 MiB) are rejected with ATK_EINVAL.  The first call from a stream
+ * binds the next free slice of the current GPU to that stream handle for the rest of the
+ * process: calls on one stream are ordered and calls on different streams use different
+ * slices, so neither races.  A fifth stream on one GPU is refused with ATK_EINVAL.  A slice
+ * follows the handle value, so a stream destroyed with calls still in flight must not have
+ * its handle reused by a new stream before that work ends.  The first call on a device
+ * resolves the array's address there (make it outside graph capture).
  * ------------------------------------------------------------------------- */
 size_t atk_group_norm_noalloc_scratch_bytes(void);
 int atk_group_norm_fwd_noalloc(const void* x, const void* gamma, const void* beta, void* y,

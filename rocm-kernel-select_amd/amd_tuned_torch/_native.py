@@ -793,8 +793,9 @@ def group_norm_noalloc(input: torch.Tensor, num_groups: int, out: torch.Tensor,
                        weight: Optional[torch.Tensor] = None, bias: Optional[torch.Tensor] = None,
                        eps: float = 1e-5, *, silu: bool = False, variant: int = -1) -> torch.Tensor:
     """group_norm through atk_group_norm_fwd_noalloc: no workspace, the library's static
-    per-GPU scratch instead (calls overlapping on one GPU race on it).  `out` is the caller's
-    output tensor (input's shape and dtype, contiguous); nothing is allocated on the device."""
+    per-GPU scratch instead, one slice per stream (the current stream binds a slice on its
+    first call; a fifth stream on one GPU is refused).  `out` is the caller's output tensor
+    (input's shape and dtype, contiguous); nothing is allocated on the device."""
     _require_cuda(input, weight, bias, out)
     if not (input.is_contiguous() and out.is_contiguous()) or out.shape != input.shape or out.dtype != input.dtype:
         raise RuntimeError("group_norm_noalloc: contiguous input and an out of the same shape and dtype")

@@ -1821,6 +1821,11 @@ __device__ __forceinline__ void cl_collect(const GnClResArgs& a, int n, int ch, 
           tm[r] = xm[gr(r)];
           tq[r] = xq[gr(r)];
         }
+      // Publish every group's record of the stand-in chunk (the owner, when it runs, writes
+      // the same bits: same loads, same order of operations): a later collect for another
+      // group then finds them in the slots instead of reading the chunk from x again.
+      for (int g = tid; g < a.G; g += NT) write_slot(&a.slots[((int64_t)n * a.G + g) * a.NCH + c], tag, xm[g], xq[g]);
+      __threadfence();
       __syncthreads();
     }
     for (int m = tid; m < nmiss; m += NT) s_flag[s_list[m]] = 0;
@@ -1996,15 +2001,23 @@ struct GnClResPlan {
 template <typename T>
 bool plan_gn_cl_res(int64_t N, int64_t C, int64_t S, int G, int force_epv, GnClResPlan& out);
 
+// Workgroups of the resident kernel that fit the GPU at once: the smaller of its two builds
+// (with and without SiLU), since either may be launched on the plan this capacity admits.
 template <typename T, int NT, int EPV>
 int64_t gn_cl_res_capacity() {
   static int per_cu[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (per_cu[dev] == 0 &&
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(
-          &per_cu[dev], reinterpret_cast<const void*>(gn_cl_resident_kernel<T, NT, EPV, true>), NT, 0) != hipSuccess)
-    return 0;
+  if (per_cu[dev] == 0) {
+    int with_silu = 0, without = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &with_silu, reinterpret_cast<const void*>(gn_cl_resident_kernel<T, NT, EPV, true>), NT, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &without, reinterpret_cast<const void*>(gn_cl_resident_kernel<T, NT, EPV, false>), NT, 0) != hipSuccess)
+      return 0;
+    per_cu[dev] = std::min(with_silu, without);
+    if (per_cu[dev] == 0) return 0;
+  }
   return (int64_t)per_cu[dev] * device_cu_count();
 }
 
@@ -2590,6 +2603,13 @@ __device__ __forceinline__ void clb_collect(const GnClBwdResArgs& a, int n, int 
 #pragma unroll
           for (int q = 0; q < 4; ++q) t4[q * ST + r] = x4[q * GN_CL_MAXG + gr(r)];
         }
+      // publish all of the stand-in chunk's records (as the forward's cl_collect does)
+      for (int g = tid; g < a.G; g += NT) {
+        GnSlot* sl = &a.slots[(((int64_t)n * a.G + g) * a.NCH + c) * 2];
+        write_slot(sl, tag, x4[g], x4[GN_CL_MAXG + g]);
+        write_slot(sl + 1, tag, x4[2 * GN_CL_MAXG + g], x4[3 * GN_CL_MAXG + g]);
+      }
+      __threadfence();
       __syncthreads();
     }
     for (int m = tid; m < nmiss; m += NT) s_flag[s_list[m]] = 0;
@@ -2959,35 +2979,61 @@ extern "C" int atk_group_norm_fwd(const void* x, const void* gamma, const void* 
 // copy for the life of the process; its address is looked up once per device with
 // hipGetSymbolAddress, and that address -- never the array's name, which in host code is only
 // a stand-in -- is what the kernels get.
+//
+// The array holds GN_NOALLOC_SLICES slices of GN_NOALLOC_BYTES, one per stream: the first
+// call from a stream binds the next free slice of the current device to that stream handle,
+// and later calls from it reuse that slice.  Calls from one stream are ordered, so they never
+// overlap on a slice; calls on different streams use different slices, so they may overlap.
+// A further stream finds no slice and is refused (ATK_EINVAL) instead of sharing one.
 // ---------------------------------------------------------------------------------------
 namespace atk {
 namespace {
 
 constexpr size_t GN_NOALLOC_PARTIAL_BYTES = (size_t)1 << 20;  // 131072 (mean, M2) pairs
 constexpr size_t GN_NOALLOC_BYTES = GN_PARTIALS_OFF + GN_NOALLOC_PARTIAL_BYTES;
+constexpr int GN_NOALLOC_SLICES = 4;
 constexpr int GN_NOALLOC_MAX_DEVICES = 64;
+static_assert(GN_NOALLOC_BYTES % 256 == 0, "slices keep the array's 256-byte alignment");
 
-static __device__ __align__(256) unsigned char scratch[GN_NOALLOC_BYTES];
+static __device__ __align__(256) unsigned char scratch[GN_NOALLOC_SLICES * GN_NOALLOC_BYTES];
 
+struct NoallocDevice {
+  void* base = nullptr;                         // this device's copy of `scratch`
+  hipStream_t owner[GN_NOALLOC_SLICES] = {};    // stream bound to each slice
+  int used = 0;                                 // slices bound so far
+};
 std::mutex g_scratch_mu;
-void* g_scratch_ptr[GN_NOALLOC_MAX_DEVICES] = {};
+NoallocDevice g_noalloc[GN_NOALLOC_MAX_DEVICES];
 
-// The current device's copy of `scratch`, resolved on the first call on that device.
-int current_scratch(void** out) {
+// The slice of the current device's `scratch` bound to stream s (binding a free one on the
+// stream's first call), resolving the array's address on the device's first call.
+int current_scratch(hipStream_t s, void** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= GN_NOALLOC_MAX_DEVICES)
     return fail(ATK_ELAUNCH, "group_norm (no-alloc): no current device (or device index >= %d)",
                 GN_NOALLOC_MAX_DEVICES);
   std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (!g_scratch_ptr[dev]) {
+  NoallocDevice& d = g_noalloc[dev];
+  if (!d.base) {
     void* p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p)
       return fail(ATK_ELAUNCH, "group_norm (no-alloc): hipGetSymbolAddress failed on device %d: %s", dev,
                   hipGetErrorString(e));
-    g_scratch_ptr[dev] = p;
+    d.base = p;
   }
-  *out = g_scratch_ptr[dev];
+  int slice = -1;
+  for (int i = 0; i < d.used; ++i)
+    if (d.owner[i] == s) slice = i;
+  if (slice < 0) {
+    if (d.used == GN_NOALLOC_SLICES)
+      return fail(ATK_EINVAL, "group_norm (no-alloc): the static scratch of device %d has %d stream slices and "
+                  "all are bound to other streams; calls from a further stream would race on them (use "
+                  "atk_group_norm_fwd with a workspace)", dev, GN_NOALLOC_SLICES);
+    slice = d.used++;
+    d.owner[slice] = s;
+  }
+  *out = static_cast<char*>(d.base) + (size_t)slice * GN_NOALLOC_BYTES;
   return ATK_OK;
 }
 
@@ -3012,11 +3058,12 @@ extern "C" int atk_group_norm_fwd_noalloc(const void* x, const void* gamma, cons
     return fail(ATK_EINVAL, "group_norm (no-alloc): this shape and variant need %zu bytes of scratch; the "
                 "static scratch holds %zu (use atk_group_norm_fwd with a workspace)", p.ws_bytes,
                 GN_NOALLOC_BYTES);
+  const hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
   void* ws = nullptr;
-  rc = current_scratch(&ws);
+  rc = current_scratch(hs, &ws);
   if (rc) return rc;
   return gn_fwd(x, gamma, beta, y, N, C, S, G, eps, fuse_silu, dtype, param_dtype, variant, ws, GN_NOALLOC_BYTES,
-                reinterpret_cast<hipStream_t>(stream), nullptr);
+                hs, nullptr);
 }
 
 extern "C" int atk_group_norm_apply(const void* x, const void* gamma, const void* beta, void* y, int64_t N,

@@ -2,7 +2,9 @@
 scratch) against the workspace entry point (atk_group_norm_fwd) through the C ABI: the same
 kernels and arithmetic, so the outputs must be identical byte for byte -- over two calls in
 a row, the second on a smaller input, for a multi-slice register-resident variant (slot
-table in the scratch) and the two-pass variant (partials in the scratch)."""
+table in the scratch) and the two-pass variant (partials in the scratch); calls on two streams
+that may overlap (each stream has its own slice of the scratch); and the refusal of a stream
+beyond the slices."""
 from __future__ import annotations
 
 import pytest
@@ -60,3 +62,61 @@ def test_group_norm_noalloc_rejects_shapes_beyond_the_scratch(dev):
     with pytest.raises(RuntimeError, match="static scratch holds"):
         nat.group_norm_noalloc(x, 32, out, None, None, 1e-5, variant=vi)
     assert nat.lib().atk_group_norm_noalloc_scratch_bytes() > (1 << 20)
+
+
+def test_group_norm_noalloc_overlapping_streams_use_their_own_slices(dev):
+    """Calls on two streams, issued back to back so that they may overlap on the GPU, each use
+    the scratch slice bound to their stream: both results equal the workspace entry point's
+    bit for bit, over several rounds (multi-slice resident variant: slot table in the scratch;
+    two-pass: partials)."""
+    nat = _native()
+    s1, s2 = torch.cuda.Stream(dev), torch.cuda.Stream(dev)
+    for name in ("res_nt256_v8", "twopass"):
+        vi = nat.variants(nat.OP_GROUP_NORM).index(name)
+        ins = [_inputs((1, 64, 32, 32, 64), torch.bfloat16, 11), _inputs((1, 64, 32, 32, 64), torch.bfloat16, 12)]
+        dins = [tuple(t.to(dev) for t in xi) for xi in ins]
+        wants = [nat.group_norm(xd, 32, gd, bd, 1e-5, silu=True, variant=vi) for xd, gd, bd in dins]
+        outs = [torch.empty_like(xd) for xd, _, _ in dins]
+        torch.cuda.synchronize()
+        for _ in range(3):
+            for st, (xd, gd, bd), out in zip((s1, s2), dins, outs):
+                with torch.cuda.stream(st):
+                    nat.group_norm_noalloc(xd, 32, out, gd, bd, 1e-5, silu=True, variant=vi)
+            torch.cuda.synchronize()
+            for out, want in zip(outs, wants):
+                assert torch.equal(out.view(torch.int16), want.view(torch.int16)), name
+    for (x, gm, bt), out in zip(ins, outs):
+        assert O.max_rel_err(out.cpu(), O.group_norm(x, 32, gm, bt, 1e-5, silu=True)) <= 1e-2
+    assert not nat.group_norm_barrier_error(dev)
+
+
+def test_group_norm_noalloc_refuses_a_stream_beyond_its_slices(dev):
+    """Once every slice of the GPU's scratch is bound to a stream, a call from a further
+    stream is refused with a clear error (it would race on a bound slice); streams that hold
+    a slice keep working.  Runs last: it leaves every slice bound for the process."""
+    nat = _native()
+    vi = nat.variants(nat.OP_GROUP_NORM).index("res_nt256_v8")
+    x, gm, bt = (t.to(dev) for t in _inputs((2, 32, 16, 16), torch.bfloat16, 5))
+    want = nat.group_norm(x, 8, gm, bt, 1e-5, variant=vi)
+    torch.cuda.synchronize()  # the inputs and the reference are ready before other streams read them
+    streams, refused = [], None
+    for i in range(5):
+        st = torch.cuda.Stream(dev)
+        streams.append(st)
+        out = torch.empty_like(x)
+        with torch.cuda.stream(st):
+            try:
+                nat.group_norm_noalloc(x, 8, out, gm, bt, 1e-5, variant=vi)
+            except RuntimeError as exc:
+                assert "stream slices" in str(exc)
+                refused = i
+                break
+        st.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+    assert refused is not None, "a fifth stream was given a slice of a 4-slice scratch"
+    if refused > 0:
+        out = torch.empty_like(x)
+        with torch.cuda.stream(streams[0]):
+            nat.group_norm_noalloc(x, 8, out, gm, bt, 1e-5, variant=vi)
+        streams[0].synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16))
