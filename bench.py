@@ -939,10 +939,11 @@ def traffic_probe(variants: str, iters: int = 10):
 
 # conv tiles profiled by --conv-probe: (label, x shape, w shape, padding, dtype name, variant)
 CONV_PROBE = [
-    ("C4s fp16", (1, 64, 16, 32, 32), (64, 64, 3, 3, 3), 1, "float16", "h_w22_f11_cb32_ns"),
+    ("C4s fp16", (1, 64, 16, 32, 32), (64, 64, 3, 3, 3), 1, "float16", "h_w22_f11_cb32_k2"),
     ("C4b bf16", (2, 128, 16, 64, 64), (128, 128, 3, 3, 3), 1, "bfloat16", "h_w22_f24_cb16"),
-    ("C5a bf16", (1, 256, 8, 64, 64), (256, 256, 3, 3, 3), 1, "bfloat16", "h_w41_f22_cb32"),
-    ("C5b fp16", (1, 64, 16, 32, 32), (64, 64, 7, 7, 7), 3, "float16", "h_w14_f22_cb16x2"),
+    ("C4b bf16 K2", (2, 128, 16, 64, 64), (128, 128, 3, 3, 3), 1, "bfloat16", "h_w22_f24_cb16_k2"),
+    ("C5a bf16 K2", (1, 256, 8, 64, 64), (256, 256, 3, 3, 3), 1, "bfloat16", "h_w22_f24_cb16_k2"),
+    ("C5b fp16", (1, 64, 16, 32, 32), (64, 64, 7, 7, 7), 3, "float16", "h_w14_f22_cb16x2_k2"),
 ]
 
 

@@ -98,9 +98,9 @@ template <typename T, int CB, bool VR, int NTH = 256, int XC = 1>
 struct PatchLoader {
   static constexpr int VEC = 16 / sizeof(T);
   // chunks per thread held for the next stage: CB/4 for 16-bit types, CB/2 for fp32, at 256
-  // threads per workgroup (scaled up for smaller workgroups), times XC for tiles whose patch
+  // threads per workgroup (scaled by 256 / NTH for other workgroup sizes), times XC for tiles whose patch
   // has a wide halo (7x7 planes); the host plan rejects tiles whose patch needs more
-  static constexpr int MAXC = (sizeof(T) == 2 ? CB / 4 : CB / 2) * (256 / NTH) * XC;
+  static constexpr int MAXC = (sizeof(T) == 2 ? CB / 4 : CB / 2) * XC * 256 / NTH;
   uint4 buf[MAXC];
 
   // rsrc covers sample n of the input; iz may be out of range (a padding plane)
@@ -254,7 +254,7 @@ struct PatchLoader {
 template <typename T, int CB, int NTH = 256, int XC = 1>
 struct PatchLoaderCL {
   static_assert(sizeof(T) == 2, "channels-last staging is for 16-bit types");
-  static constexpr int MAXC = CB / 4 * (256 / NTH) * XC;
+  static constexpr int MAXC = CB / 4 * XC * 256 / NTH;
   static constexpr int NQ = MAXC / 4;
   static constexpr int CO8 = CB / 8;  // chunks per position
   uint4 buf[MAXC];
@@ -499,21 +499,30 @@ __device__ __forceinline__ void store_tile(const IgArgs& a, f32x16 (&acc)[FCO][F
   }
 }
 
-// Plain output (bias added, 16-bit, NC[D]HW, unsplit) through LDS.  Stored straight from the
+// Output (bias added, 16-bit, NC[D]HW, unsplit) through LDS.  Stored straight from the
 // accumulators, every value is its own 2-byte store (a lane holds one position of 16 channels
 // per block), so a wave issues FCO * FSP * 16 store instructions, each moving 128 bytes; at the
 // end of a launch whose workgroups all finish together those stores are what the chip waits
 // for.  Here the tile goes to LDS as [channel][position] rows (pitch a.epi_pitch = BM * 2 + 16:
 // the two lane halves' rows, 4 channels apart, fall on disjoint banks), then every thread of
 // the workgroup stores 16-byte runs of 8 positions of one channel.  Needs TX % 8 == 0,
-// Wo % 8 == 0 and a 16-byte aligned y (host check), so a run is whole inside or outside the
-// output and aligned.  The caller has passed a barrier after the last read of the stage
-// buffers; every thread of the workgroup calls this (the K groups of a split workgroup too:
-// `active` is false for the ones whose accumulators were already handed over).
-template <typename T, int FCO, int FSP, int BN, int BM>
+// Wo % 8 == 0 and 16-byte aligned y / residual (host check), so a run is whole inside or
+// outside the output and aligned.  The caller has passed a barrier after the last read of the
+// stage buffers; every thread of the workgroup calls this (the K groups of a split workgroup
+// too: `active` is false for the ones whose accumulators were already handed over).
+//
+// With EPI, the residual is added to each run before its store (the staged value is the
+// conv output rounded to T; residual added in fp32, rounded again -- the stock composition of
+// a conv followed by an add), and GroupNorm records of the stored values are written: per
+// 32-channel block and group (groups of up to 32 channels) or per block (wider groups), one
+// record per workgroup tile at the first of the WSP per-wave slots that gn_records() counts,
+// zero-count records at the others; each from a two-pass mean / M2 over the staged values of
+// the positions inside the output.
+template <typename T, int FCO, int FSP, int BN, int BM, int WSP, bool EPI, int NTHR>
 __device__ __forceinline__ void store_tile_lds(const IgArgs& a, f32x16 (&acc)[FCO][FSP], const float* s_bias,
                                                char* stg, int n, int co_tile, int oz, int oy0, int ox0, int wco,
-                                               int wsp, bool active, int tid, int nthreads) {
+                                               int wsp, bool active, int tid, int tile_rec) {
+  constexpr int nthreads = NTHR;
   static_assert(sizeof(T) == 2, "16-bit outputs");
   int lane = threadIdx.x & 63;
   asm volatile("" : "+v"(lane));  // keep the address math below the main loop
@@ -535,15 +544,115 @@ __device__ __forceinline__ void store_tile_lds(const IgArgs& a, f32x16 (&acc)[FC
   __syncthreads();
   const int64_t spo = (int64_t)a.Do * a.Ho * a.Wo;
   constexpr int RPR = BM / 8;  // 16-byte runs per channel row
-  for (int q = tid; q < BN * RPR; q += nthreads) {
-    const int cl = q / RPR, m = (q - (q / RPR) * RPR) * 8;
-    const int ty = m / a.TX, tx = m - (m / a.TX) * a.TX;
-    const int oy = oy0 + ty, ox = ox0 + tx;
-    const int co = co_tile * BN + cl;
-    if (oy < a.Ho && ox < a.Wo && co < a.Co) {
-      const uint4 v = *reinterpret_cast<const uint4*>(stg + cl * EP + m * 2);
-      *reinterpret_cast<uint4*>(static_cast<T*>(a.y) + ((int64_t)n * a.Co + co) * spo +
-                                ((int64_t)oz * a.Ho + oy) * a.Wo + ox) = v;
+  const bool resid = EPI && a.resid;
+  // runs of this thread: q = tid + k * NTHR, in batches of RB: every residual load of a batch
+  // is issued, then every value is formed, then every store is issued.  (On this ISA stores
+  // and loads share one counter: a store between two waited-for loads would make each wait
+  // cover the store too, serialising the batch on store latency.)
+  constexpr int NRUN = (BN * RPR + NTHR - 1) / NTHR, RB = NRUN < 8 ? NRUN : 8;
+#pragma unroll
+  for (int k0 = 0; k0 < NRUN; k0 += RB) {
+    int64_t off[RB];
+    bool ok[RB];
+    uint4 v[RB];
+#pragma unroll
+    for (int k = 0; k < RB; ++k) {
+      const int q = tid + (k0 + k) * NTHR;
+      const int cl = q / RPR, m = (q - (q / RPR) * RPR) * 8;
+      const int ty = m / a.TX, tx = m - (m / a.TX) * a.TX;
+      const int oy = oy0 + ty, ox = ox0 + tx;
+      const int co = co_tile * BN + cl;
+      ok[k] = k0 + k < NRUN && q < BN * RPR && oy < a.Ho && ox < a.Wo && co < a.Co;
+      off[k] = ((int64_t)n * a.Co + (ok[k] ? co : 0)) * spo + ((int64_t)oz * a.Ho + (ok[k] ? oy : 0)) * a.Wo +
+               (ok[k] ? ox : 0);
+      // (out-of-range runs load element 0 of their plane, which exists, and discard it)
+      if (resid) v[k] = *reinterpret_cast<const uint4*>(static_cast<const T*>(a.resid) + off[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < RB; ++k) {
+      const int q = tid + (k0 + k) * NTHR;
+      const int cl = ok[k] ? q / RPR : 0, m = ok[k] ? (q - (q / RPR) * RPR) * 8 : 0;
+      uint4* sp = reinterpret_cast<uint4*>(stg + cl * EP + m * 2);
+      const uint4 c = *sp;
+      if (resid) {
+        Vec16<T> cv, r;
+        cv.raw = c;
+        r.raw = v[k];
+        float f[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = to_f32(cv.e[e]) + to_f32(r.e[e]);
+        v[k] = pack16<T>(f);
+        if (a.gn_parts && ok[k]) *sp = v[k];  // the statistics below are of the stored values
+      } else {
+        v[k] = c;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < RB; ++k)
+      if (ok[k]) *reinterpret_cast<uint4*>(static_cast<T*>(a.y) + off[k]) = v[k];
+  }
+  if (!(EPI && a.gn_parts)) return;
+  if (resid) __syncthreads();
+  // GroupNorm records: unit u = (32-channel block, group inside it) of this tile, one wave per
+  // unit.  One pass over the staged values with sums shifted by the unit's first value K (the
+  // tile's first position always lies inside the output): mean = K + s1 / n, M2 = s2 - s1^2 / n,
+  // exact to rounding for values that spread over a few standard deviations.  A lane's runs
+  // are all read before any is used; the count follows from the tile's extent inside the
+  // output.  (TX is a power of two: positions split by shift and mask.)
+  const int cpg = a.gn_cpg;
+  const int upb = cpg >= 32 ? 1 : 32 / cpg;  // units per block
+  const int uch = cpg >= 32 ? 32 : cpg;      // channels per unit
+  const int nunits = (BN / 32) * upb;
+  constexpr int NW = NTHR / 64, MAXR = (32 * RPR + 63) / 64;  // runs per lane for a 32-channel unit
+  const int wave = tid >> 6;
+  const int txs = __builtin_ctz((unsigned)a.TX), txm = a.TX - 1;
+  const int vy = min(BM / a.TX, a.Ho - oy0), vx = min(a.TX, a.Wo - ox0);
+  const int nruns = uch * RPR, nri = (nruns + 63) / 64;  // runs of the unit, runs per lane
+  for (int u = wave; u < nunits; u += NW) {
+    const int c0 = (u / upb) * 32 + (u - (u / upb) * upb) * uch;  // first channel (tile-local)
+    const int co0 = co_tile * BN + c0;
+    const int nvch = min(uch, a.Co - co0);
+    if (nvch <= 0) continue;
+    const float cnt = (float)(vy * vx * nvch);
+    const float K = to_f32(*reinterpret_cast<const T*>(stg + c0 * EP));
+    Vec16<T> v[MAXR];
+#pragma unroll
+    for (int i = 0; i < MAXR; ++i) {
+      if (i < nri) {
+        const int r = lane + 64 * i;
+        const int rr = r < nruns ? r : 0;
+        v[i].raw = *reinterpret_cast<const uint4*>(stg + (c0 + rr / RPR) * EP + (rr % RPR) * 16);
+      }
+    }
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < MAXR; ++i) {
+      if (i < nri) {
+        const int r = lane + 64 * i;
+        const int m = (r % RPR) * 8;
+        const bool ok = r < nruns && ((m >> txs) < vy) && ((m & txm) < vx) && (r / RPR) < nvch;
+        if (ok) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float d = to_f32(v[i].e[e]) - K;
+            s1 += d;
+            s2 = fmaf(d, d, s2);
+          }
+        }
+      }
+    }
+    s1 = wave_sum(s1);
+    s2 = wave_sum(s2);
+    const float t = s1 / cnt;
+    const float mean = K + t, m2 = fmaxf(fmaf(-s1, t, s2), 0.f);
+    const int g = co0 / cpg;
+    if (lane == 0 && co0 < a.gn_G * cpg) {
+      const int parts = cpg > 32 ? cpg / 32 : 1;
+      const int part = cpg > 32 ? (co0 % cpg) / 32 : 0;
+      float4* recs = a.gn_parts + ((int64_t)n * a.gn_G + g) * a.gn_np;
+      // slot (tile, wave-column 0, part); the tile's other WSP - 1 slots hold count 0
+      recs[(tile_rec * WSP) * parts + part] = make_float4(cnt, mean, m2, 0.f);
+      for (int w = 1; w < WSP; ++w) recs[(tile_rec * WSP + w) * parts + part] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
   }
 }
@@ -559,7 +668,7 @@ __device__ __forceinline__ void store_tile_lds(const IgArgs& a, f32x16 (&acc)[FC
 // wave) then get KS waves per SIMD and a KS-times shorter chain of stage latencies, in one
 // launch and with no partial sums in memory.
 template <typename T, int WCO, int WSP, int FCO, int FSP, int CB, int XC, bool VR, int KHT, int KWT, bool EPI,
-          int KS = 1, bool CL = false>
+          int KS = 1, bool CL = false, bool LEPI = false>
 __global__ __launch_bounds__(64 * WCO * WSP * KS)
 __attribute__((amdgpu_waves_per_eu(KS > 1 ? KS : ((FCO * FSP >= 8 && CB == 16) || XC > 1 ? 2 : 1))))
 void conv_igemm_kernel(IgArgs a) {
@@ -848,8 +957,8 @@ void conv_igemm_kernel(IgArgs a) {
     kd = kd1;
   }
 
-  // the LDS-staged plain epilogue (a runtime choice of the host: see store_tile_lds)
-  constexpr bool LDS_EPI_OK = sizeof(T) == 2 && !EPI && !CL;
+  // the LDS-staged epilogue (a runtime choice of the host: see store_tile_lds)
+  constexpr bool LDS_EPI_OK = sizeof(T) == 2 && !CL;
   const bool lds_epi = LDS_EPI_OK && a.lds_epi;
   if constexpr (KS > 1) {
     // groups 1..KS-1 park their accumulators in LDS (the patch buffers are free: the last
@@ -882,14 +991,21 @@ void conv_igemm_kernel(IgArgs a) {
   if constexpr (LDS_EPI_OK) {
     if (lds_epi) {
       // (KS == 1: the last stage ended with a barrier, so the patch buffers are free)
-      store_tile_lds<T, FCO, FSP, BN, WSP * FSP * 32>(a, acc, s_bias, lds_base, n, co_tile, oz, oy0, ox0, wco, wsp,
-                                                     kg == 0, threadIdx.x, 64 * NWG * KS);
+      store_tile_lds<T, FCO, FSP, BN, WSP * FSP * 32, WSP, EPI, 64 * NWG * KS>(
+          a, acc, s_bias, lds_base, n, co_tile, oz, oy0, ox0, wco, wsp, kg == 0, threadIdx.x,
+          (oz * a.tiles_y + ty_t) * a.tiles_x + tx_t);
       return;
     }
   }
-  // GroupNorm record index of this wave's spatial tile: (z, tile row, tile column), then wave
-  const int sp_rec = ((oz * a.tiles_y + ty_t) * a.tiles_x + tx_t) * WSP + wsp;
-  store_tile<T, FCO, FSP, BN, EPI, CL>(a, acc, s_bias, n, co_tile, split, oz, oy0, ox0, wco, wsp, half, col, sp_rec);
+  // (LEPI: the instantiation that carries only the LDS-staged epilogue -- the host launches
+  // it only with a.lds_epi set; without the per-value epilogue extras beside it, the epilogue
+  // variant keeps the plain kernel's register budget)
+  if constexpr (!LEPI) {
+    // GroupNorm record index of this wave's spatial tile: (z, tile row, tile column), then wave
+    const int sp_rec = ((oz * a.tiles_y + ty_t) * a.tiles_x + tx_t) * WSP + wsp;
+    store_tile<T, FCO, FSP, BN, EPI, CL>(a, acc, s_bias, n, co_tile, split, oz, oy0, ox0, wco, wsp, half, col,
+                                         sp_rec);
+  }
 }
 
 // Packed weights Wp[tap][kb][co_block][32][KB] from w[Co][Ci][taps]; zero beyond Co / Ci.
@@ -1090,7 +1206,7 @@ int plan_ig(const ConvShape& p, int v, IgPlan& pl) {
   if (vr.ks > 1)
     pl.lds = std::max(pl.lds, (size_t)(vr.ks - 1) * vr.wco * vr.wsp * vr.fco * vr.fsp * 16 * 64 * 4);
   {
-    const int maxc = (f32 ? vr.cb / 2 : vr.cb / 4) * (256 / ntg) * vr.xc;  // PatchLoader::MAXC
+    const int maxc = (f32 ? vr.cb / 2 : vr.cb / 4) * vr.xc * 256 / ntg;  // PatchLoader::MAXC
     if (pl.lds > 150 * 1024 || vr.cb * a.PY * a.NCX > maxc * ntg)
       return fail(ATK_UNSUPPORTED, "conv %s: stage of %zu LDS bytes does not fit the variant", vr.name, pl.lds);
   }
@@ -1120,8 +1236,41 @@ int plan_ig(const ConvShape& p, int v, IgPlan& pl) {
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // One kernel instantiation: the LDS opt-in is a per-kernel attribute, set once per kernel.
+// Workgroups of kernel Kern resident per CU with `lds` bytes of dynamic LDS: the register /
+// wave limit (queried once per kernel and device) and the 160 KB of LDS, whichever is lower.
 template <void (*Kern)(IgArgs)>
-int launch_ig_kern(const IgPlan& pl, int nthreads, hipStream_t s) {
+int resident_per_cu(int nthreads, size_t lds) {
+  static int by_regs[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (by_regs[dev] == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, reinterpret_cast<const void*>(Kern), nthreads, 0) !=
+        hipSuccess)
+      return 0;
+    by_regs[dev] = n;
+  }
+  return std::min<int>(by_regs[dev], (int)((160 * 1024) / std::max<size_t>(lds, 1)));
+}
+
+// Launches Kern.  With `lds_only` (an instantiation carrying only the LDS-staged epilogue)
+// it returns kNeedPerValue instead of launching when that epilogue cannot be kept.
+constexpr int kNeedPerValue = -1;
+
+template <void (*Kern)(IgArgs)>
+int launch_ig_kern(const IgPlan& plan, int nthreads, hipStream_t s, bool lds_only = false) {
+  IgPlan pl = plan;
+  if (pl.a.lds_epi) {
+    // the staging area of the LDS-staged epilogue: keep it only where it costs no resident
+    // workgroup per CU
+    const size_t stg = (size_t)pl.bn * pl.a.epi_pitch;
+    if (stg > pl.lds) {
+      const int before = resident_per_cu<Kern>(nthreads, pl.lds);
+      if (before > 0 && resident_per_cu<Kern>(nthreads, stg) == before) pl.lds = stg;
+      else pl.a.lds_epi = 0;
+    }
+  }
+  if (lds_only && !pl.a.lds_epi) return kNeedPerValue;
   if (pl.lds > 64 * 1024) {
     // opt in to more than 64 KB of dynamic LDS (gfx950 has 160 KB per CU)
     static bool raised = false;
@@ -1146,12 +1295,23 @@ int launch_ig_vr(const IgPlan& pl, hipStream_t s) {
     else
       return fail(ATK_UNSUPPORTED, "conv (channels-last): 16-bit types with a 3x3 or 7x7 plane only");
   }
-  // the residual / GroupNorm epilogue is its own instantiation, so the plain kernel is unchanged
+  // the residual / GroupNorm epilogue is its own instantiation, so the plain kernel is unchanged;
+  // the LDS-staged form of it (16-bit types) another, tried first
   if (pl.a.resid || pl.a.gn_parts) {
-    if constexpr (VR)
-      return launch_ig_kern<conv_igemm_kernel<T, WCO, WSP, FCO, FSP, CB, XC, VR, KHT, KWT, true, KS>>(pl, nt, s);
-    else
+    if constexpr (VR) {
+      if constexpr (sizeof(T) == 2 && KHT > 0) {
+        if (pl.a.lds_epi) {
+          const int rc = launch_ig_kern<conv_igemm_kernel<T, WCO, WSP, FCO, FSP, CB, XC, VR, KHT, KWT, true, KS,
+                                                          false, true>>(pl, nt, s, true);
+          if (rc != kNeedPerValue) return rc;
+        }
+      }
+      IgPlan pv = pl;
+      pv.a.lds_epi = 0;
+      return launch_ig_kern<conv_igemm_kernel<T, WCO, WSP, FCO, FSP, CB, XC, VR, KHT, KWT, true, KS>>(pv, nt, s);
+    } else {
       return fail(ATK_UNSUPPORTED, "conv: the residual / GroupNorm epilogue needs 16-byte aligned input rows");
+    }
   }
   return launch_ig_kern<conv_igemm_kernel<T, WCO, WSP, FCO, FSP, CB, XC, VR, KHT, KWT, false, KS>>(pl, nt, s);
 }
@@ -1223,21 +1383,16 @@ int run_ig(const ConvShape& p, IgPlan& pl, const void* x, const void* wp, const 
   a.wp_bytes = (uint32_t)pl.wp_bytes;
   a.wp = wp;
   a.part = pl.splits > 1 ? part : nullptr;
-  // LDS-staged epilogue for plain unsplit 16-bit NC[D]HW output (store_tile_lds), when its
-  // staging area fits without costing a resident workgroup per CU
-  a.lds_epi = 0;
+  // LDS-staged epilogue for plain unsplit 16-bit NC[D]HW output (store_tile_lds) where the
+  // shape allows it; launch_ig_kern keeps it only if its staging area costs no resident
+  // workgroup per CU
   a.epi_pitch = pl.bm * 2 + 16;
   {
     // ATK_CONV_LDS_EPI=0 keeps the per-value stores (read per call: tests compare the two)
     const char* e = getenv("ATK_CONV_LDS_EPI");
     const bool off = e && e[0] == '0';
-    const size_t stg = (size_t)pl.bn * a.epi_pitch;
-    constexpr size_t kLdsCu = 160 * 1024;
-    if (!off && sizeof(T) == 2 && !cl && !resid && !gn_parts && pl.splits == 1 && p.Wo % 8 == 0 &&
-        a.TX % 8 == 0 && aligned16(y) && stg <= 150 * 1024 && kLdsCu / std::max(pl.lds, stg) == kLdsCu / pl.lds) {
-      a.lds_epi = 1;
-      pl.lds = std::max(pl.lds, stg);
-    }
+    a.lds_epi = (!off && sizeof(T) == 2 && !cl && pl.splits == 1 && p.Wo % 8 == 0 && a.TX % 8 == 0 &&
+                 aligned16(y) && (!resid || aligned16(resid)) && (size_t)pl.bn * a.epi_pitch <= 150 * 1024) ? 1 : 0;
   }
   // instantiate only the variants of this element type's class
   if constexpr (sizeof(T) == 2) {

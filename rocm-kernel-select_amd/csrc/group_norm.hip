@@ -3071,7 +3071,21 @@ extern "C" int atk_group_norm_apply(const void* x, const void* gamma, const void
                                     int param_dtype, const void* stats, int64_t records_per_group, int variant,
                                     atk_stream_t stream) {
   using namespace atk;
-  if (variant < 0) variant = 12;  // split_nt256_v8
+  if (variant < 0) {
+    // default: the split variant with the largest slices whose grid still covers every CU (one
+    // record merge per workgroup, so fewer, larger workgroups merge less), else the smallest
+    // slices; split_nt1024_v4, split_nt512_v8, split_nt256_v8, split_nt256_v4 in that order
+    static const int order[] = {15, 13, 12, 14};
+    variant = 14;
+    const int64_t cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    for (int v : order) {
+      GnPlan q;
+      if (validate_gn(N, C, S, G, dtype, v) == ATK_OK && plan_gn(N, C, S, G, dtype, v, q) && N * G * q.NS >= cus) {
+        variant = v;
+        break;
+      }
+    }
+  }
   int rc = validate_gn(N, C, S, G, dtype, variant);
   if (rc) return rc;
   if (kGnVariants[variant].kind != GN_SPLIT)

@@ -204,7 +204,7 @@ def test_vae_block_fused_forward_and_grads(dtype):
     assert conv_fusion_ops.replace_conv_blocks(model) == 1
     assert isinstance(model[0], conv_fusion_ops.FusedConvGroupNormSiLU)
     x = torch.randn(1, C, 4, 16, 16)
-    bar = 1e-2 if dtype == torch.bfloat16 else 1e-4
+    bar = 1e-2 if dtype == torch.bfloat16 else 1e-5
     with torch.no_grad():
         y = model(x.to("cuda", dtype))
         amd_tuned_torch.disable()

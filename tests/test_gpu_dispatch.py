@@ -192,7 +192,7 @@ def test_torch_compile_block_matches_oracle_without_graph_breaks(dev):
     h = F.group_norm(h, 4, gm.double(), bt.double(), 1e-5)
     ref_y = F.silu(F.group_norm(h, 4, gm.double(), bt.double(), 1e-5))
     ref_z = O.dwconv1d(x1, w1.squeeze(1), b1, 3, 512 + 3)
-    assert O.max_rel_err(y.cpu(), ref_y) <= 2e-2
+    assert O.max_rel_err(y.cpu(), ref_y) <= 1e-2
     assert O.max_rel_err(z.cpu(), ref_z) <= 1e-2
 
     # training: gradients of every input through the ops' autograd formulas
@@ -213,7 +213,7 @@ def test_torch_compile_block_matches_oracle_without_graph_breaks(dev):
     ref_grads = torch.autograd.grad((ry, rz), ref_leaves, (gy.double(), gz.double()))
     for i, (a, r) in enumerate(zip(grads, ref_grads)):
         err = O.max_rel_err(a.cpu(), r)
-        assert err <= 3e-2, f"grad {i}: {err:.3g}"
+        assert err <= 1e-2, f"grad {i}: {err:.3g}"
 
 
 def test_two_streams_do_not_share_scratch(dev):

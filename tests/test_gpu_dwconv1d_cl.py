@@ -250,6 +250,11 @@ def test_causal_bcl_autograd(dtype, silu, L, K):
     _grad_close(b.grad, db, "bcl dbias", 1e-5 if dtype == torch.float32 else 2e-3)
 
 
+# channels checked against the float64 oracle in the full-size tests: first, last, a power of
+# two and two odd ones, over all 16 batch rows
+_SAMPLED_CHANNELS = [0, 1, 511, 1024, 2047]
+
+
 def test_causal_channel_last_full_size_matches_bcl_kernel():
     """C2's shape (16, 2048, 8192) bf16 in the channel-last layout, K = 4, against the
     parity-tested (B, C, L) kernel on the same values, and its backward against the
@@ -278,6 +283,17 @@ def test_causal_channel_last_full_size_matches_bcl_kernel():
     assert O.max_rel_err(xr.grad.float(), dx_ref.float()) <= 1e-2
     assert O.max_rel_err(wr.grad, dw_ref) <= 1e-4
     assert O.max_rel_err(br.grad, db_ref) <= 1e-4
+    # and against the float64 oracle on sampled channels (channels are independent: a few
+    # whole channels over every batch row pin forward, dx, dw and db exactly)
+    cs = torch.tensor(_SAMPLED_CHANNELS, device="cuda")
+    xs = x_cl.index_select(1, cs).cpu()
+    dys = dy.index_select(1, cs).cpu()
+    ws, bs = wr.detach().index_select(0, cs).cpu(), br.detach().index_select(0, cs).cpu()
+    _close(y.index_select(1, cs), O.dwconv1d(xs, ws, bs, K - 1, L), torch.bfloat16, "full-size forward")
+    dxo, dwo, dbo = O.dwconv1d_bwd(xs, ws, dys, K - 1)
+    _close(xr.grad.index_select(1, cs), dxo, torch.bfloat16, "full-size dx")
+    _grad_close(wr.grad.index_select(0, cs), dwo, "full-size dweight", 1e-5)
+    _grad_close(br.grad.index_select(0, cs), dbo, "full-size dbias", 1e-5)
     del x_cl, y, y_ref, xr, out, dy, dyc, dx_ref
     torch.cuda.empty_cache()
 
@@ -326,6 +342,13 @@ def test_causal_bcl_fused_backward_full_size():
     assert O.max_rel_err(dx.float(), dx_ref.float()) <= 1e-2
     assert (dx == dx_ref).float().mean().item() > 0.99
     assert O.max_rel_err(dw, dw_ref) <= 1e-4 and O.max_rel_err(db, db_ref) <= 1e-4
+    # against the float64 oracle on sampled whole channels (every batch row)
+    cs = torch.tensor(_SAMPLED_CHANNELS, device="cuda")
+    dxo, dwo, dbo = O.dwconv1d_bwd(x.index_select(1, cs).cpu(), w.index_select(0, cs).cpu(),
+                                   dy.index_select(1, cs).cpu(), K - 1)
+    _close(dx.index_select(1, cs), dxo, torch.bfloat16, "full-size fused dx")
+    _grad_close(dw.index_select(0, cs), dwo, "full-size fused dweight", 1e-5)
+    _grad_close(db.index_select(0, cs), dbo, "full-size fused dbias", 1e-5)
     del x, dy, dx, dx_ref
     torch.cuda.empty_cache()
 
