@@ -138,6 +138,27 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Sum over the wave on the VALU: DPP swaps inside quads (xor 1, xor 2), then half-row and row
+// mirrors give every lane its 16-lane row's sum; the four row sums are read out by lane reads
+// and added in row order.  The result is wave-uniform and its order fixed.  Unlike wave_sum
+// (LDS-pipe permutes, each waited for in turn) independent calls interleave freely.  Every lane
+// of the wave must be active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum_rows(float v) {
+  v += dpp_mov<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_mov<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_mov<0x141>(v);  // row_half_mirror
+  v += dpp_mov<0x140>(v);  // row_mirror
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+  return ((r0 + r1) + r2) + r3;
+}
+
 // Sum over the block; every thread receives the total.  `red` must hold
 // blockDim/64 floats of shared memory.  Contains two __syncthreads().
 template <int NT>

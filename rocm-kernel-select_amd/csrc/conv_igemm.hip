@@ -514,15 +514,14 @@ __device__ __forceinline__ void store_tile(const IgArgs& a, f32x16 (&acc)[FCO][F
 // With EPI, the residual is added to each run before its store (the staged value is the
 // conv output rounded to T; residual added in fp32, rounded again -- the stock composition of
 // a conv followed by an add), and GroupNorm records of the stored values are written: per
-// 32-channel block and group (groups of up to 32 channels) or per block (wider groups), one
-// record per workgroup tile at the first of the WSP per-wave slots that gn_records() counts,
-// zero-count records at the others; each from a two-pass mean / M2 over the staged values of
-// the positions inside the output.
+// 32-channel block and group (groups of up to 32 channels) or per block (wider groups), in the
+// WSP per-tile slots that gn_records() counts (one record per wave holding a share of the
+// unit, count-0 records in the rest); each a shifted one-pass mean / M2 of the unit's values
+// inside the output, summed per lane as they are stored.
 template <typename T, int FCO, int FSP, int BN, int BM, int WSP, bool EPI, int NTHR>
 __device__ __forceinline__ void store_tile_lds(const IgArgs& a, f32x16 (&acc)[FCO][FSP], const float* s_bias,
                                                char* stg, int n, int co_tile, int oz, int oy0, int ox0, int wco,
                                                int wsp, bool active, int tid, int tile_rec) {
-  constexpr int nthreads = NTHR;
   static_assert(sizeof(T) == 2, "16-bit outputs");
   int lane = threadIdx.x & 63;
   asm volatile("" : "+v"(lane));  // keep the address math below the main loop
@@ -544,12 +543,40 @@ __device__ __forceinline__ void store_tile_lds(const IgArgs& a, f32x16 (&acc)[FC
   __syncthreads();
   const int64_t spo = (int64_t)a.Do * a.Ho * a.Wo;
   constexpr int RPR = BM / 8;  // 16-byte runs per channel row
-  const bool resid = EPI && a.resid;
-  // runs of this thread: q = tid + k * NTHR, in batches of RB: every residual load of a batch
-  // is issued, then every value is formed, then every store is issued.  (On this ISA stores
-  // and loads share one counter: a store between two waited-for loads would make each wait
-  // cover the store too, serialising the batch on store latency.)
+  // (EXACT: every thread stores the same number of runs; otherwise -- workgroups of 3 K groups
+  // -- run q of store k is tid + k * NTHR and the register statistics are off)
+  constexpr bool EXACT = (BN * RPR) % NTHR == 0;
   constexpr int NRUN = (BN * RPR + NTHR - 1) / NTHR, RB = NRUN < 8 ? NRUN : 8;
+  const bool resid = EPI && a.resid;
+  // Wave w stores runs [w, w + 1) * NRUN * 64, store k of a lane being run q0 + 64 k + lane
+  // (64 consecutive runs per instruction: whole channel rows or one part of a row), in batches
+  // of RB: every residual load of a batch is issued, then every value is formed, then every
+  // store is issued.  (On this ISA stores and loads share one counter: a store between two
+  // waited-for loads would make each wait cover the store too, serialising the batch on store
+  // latency.)
+  const int q0 = (tid >> 6) * NRUN * 64;
+  // GroupNorm records from registers.  A unit (a group inside a 32-channel block, or a
+  // 32-channel part of a wider group) is uch channels, urun = uch * RPR runs.  When urun is a
+  // multiple of 64 every store instruction lies inside one unit, so each lane keeps one pair of
+  // shifted sums per instruction, about a wave-uniform K (the first staged value of the unit's
+  // runs in this wave), and the wave reduces them per unit on the VALU.  A unit longer than a
+  // wave's runs spans S <= WSP waves, each writing one of the tile's WSP record slots.  Other
+  // layouts take the LDS pass at the end.
+  const int cpg = EPI ? a.gn_cpg : 0;
+  const int uch = cpg >= 32 ? 32 : cpg;
+  const int urun = uch * RPR;
+  const bool gn = EPI && a.gn_parts;
+  const bool gn_reg = EXACT && gn && urun % 64 == 0 && (urun <= NRUN * 64 || urun / (NRUN * 64) <= WSP);
+  const int ush = gn_reg ? __builtin_ctz((unsigned)urun) : 0;
+  float s1[NRUN], s2[NRUN], kk[NRUN];
+#pragma unroll
+  for (int k = 0; k < NRUN; ++k) {
+    s1[k] = s2[k] = kk[k] = 0.f;
+    if (gn_reg) {
+      const int ps = max(((q0 + 64 * k) >> ush) << ush, q0);  // first run of the unit in this wave
+      kk[k] = to_f32(*reinterpret_cast<const T*>(stg + (ps / RPR) * EP));
+    }
+  }
 #pragma unroll
   for (int k0 = 0; k0 < NRUN; k0 += RB) {
     int64_t off[RB];
@@ -557,7 +584,7 @@ __device__ __forceinline__ void store_tile_lds(const IgArgs& a, f32x16 (&acc)[FC
     uint4 v[RB];
 #pragma unroll
     for (int k = 0; k < RB; ++k) {
-      const int q = tid + (k0 + k) * NTHR;
+      const int q = EXACT ? q0 + 64 * (k0 + k) + lane : tid + (k0 + k) * NTHR;
       const int cl = q / RPR, m = (q - (q / RPR) * RPR) * 8;
       const int ty = m / a.TX, tx = m - (m / a.TX) * a.TX;
       const int oy = oy0 + ty, ox = ox0 + tx;
@@ -570,7 +597,7 @@ __device__ __forceinline__ void store_tile_lds(const IgArgs& a, f32x16 (&acc)[FC
     }
 #pragma unroll
     for (int k = 0; k < RB; ++k) {
-      const int q = tid + (k0 + k) * NTHR;
+      const int q = EXACT ? q0 + 64 * (k0 + k) + lane : tid + (k0 + k) * NTHR;
       const int cl = ok[k] ? q / RPR : 0, m = ok[k] ? (q - (q / RPR) * RPR) * 8 : 0;
       uint4* sp = reinterpret_cast<uint4*>(stg + cl * EP + m * 2);
       const uint4 c = *sp;
@@ -582,16 +609,65 @@ __device__ __forceinline__ void store_tile_lds(const IgArgs& a, f32x16 (&acc)[FC
 #pragma unroll
         for (int e = 0; e < 8; ++e) f[e] = to_f32(cv.e[e]) + to_f32(r.e[e]);
         v[k] = pack16<T>(f);
-        if (a.gn_parts && ok[k]) *sp = v[k];  // the statistics below are of the stored values
+        // (the LDS statistics pass reads the stored values back from the staging rows)
+        if (gn && !gn_reg && ok[k]) *sp = v[k];
       } else {
         v[k] = c;
+      }
+      if (gn_reg) {  // the statistics are of the stored values
+        Vec16<T> sv;
+        sv.raw = v[k];
+        float t1 = 0.f, t2 = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = to_f32(sv.e[e]) - kk[k0 + k];
+          t1 += d;
+          t2 = fmaf(d, d, t2);
+        }
+        s1[k0 + k] = ok[k] ? t1 : 0.f;
+        s2[k0 + k] = ok[k] ? t2 : 0.f;
       }
     }
 #pragma unroll
     for (int k = 0; k < RB; ++k)
       if (ok[k]) *reinterpret_cast<uint4*>(static_cast<T*>(a.y) + off[k]) = v[k];
   }
-  if (!(EPI && a.gn_parts)) return;
+  if (gn_reg) {
+    // stores k of one unit: KPU = min(urun / 64, NRUN) consecutive ones, from a multiple of
+    // KPU; pairwise sums in a fixed tree leave each unit's lane sums at its first store
+    const int kpu = min(urun >> 6, NRUN);
+#pragma unroll
+    for (int w = 1; w < NRUN; w *= 2)
+#pragma unroll
+      for (int k = 0; k + w < NRUN; k += 2 * w) {
+        const bool take = 2 * w <= kpu;
+        s1[k] = take ? s1[k] + s1[k + w] : s1[k];
+        s2[k] = take ? s2[k] + s2[k + w] : s2[k];
+      }
+    const int vy = min(BM / a.TX, a.Ho - oy0), vx = min(a.TX, a.Wo - ox0);
+    const int parts = cpg > 32 ? cpg / 32 : 1;
+    const int span = urun > NRUN * 64 ? urun / (NRUN * 64) : 1;  // waves per unit
+#pragma unroll
+    for (int k = 0; k < NRUN; ++k) {
+      if (k % kpu) continue;  // (wave-uniform)
+      const float w1 = wave_sum_rows(s1[k]), w2 = wave_sum_rows(s2[k]);
+      const int qk = q0 + 64 * k;
+      const int us = (qk >> ush) << ush, ps = max(us, q0);
+      const int co0 = co_tile * BN + ps / RPR;
+      const int nvch = min(min(urun, NRUN * 64) / RPR, a.Co - co0);
+      if (nvch <= 0 || lane != 0) continue;
+      const float cnt = (float)(vy * vx * nvch);
+      const float t = w1 / cnt;
+      const int g = co0 / cpg, part = cpg > 32 ? (co0 % cpg) / 32 : 0;
+      const int pw = (ps - us) / (NRUN * 64);  // this wave's share of the unit
+      float4* recs = a.gn_parts + ((int64_t)n * a.gn_G + g) * a.gn_np;
+      recs[(tile_rec * WSP + pw) * parts + part] = make_float4(cnt, kk[k] + t, fmaxf(fmaf(-w1, t, w2), 0.f), 0.f);
+      if (pw == 0)  // the slots no wave of this unit fills hold count 0
+        for (int w = span; w < WSP; ++w) recs[(tile_rec * WSP + w) * parts + part] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    return;
+  }
+  if (!gn) return;
   if (resid) __syncthreads();
   // GroupNorm records: unit u = (32-channel block, group inside it) of this tile, one wave per
   // unit.  One pass over the staged values with sums shifted by the unit's first value K (the
@@ -599,9 +675,7 @@ __device__ __forceinline__ void store_tile_lds(const IgArgs& a, f32x16 (&acc)[FC
   // exact to rounding for values that spread over a few standard deviations.  A lane's runs
   // are all read before any is used; the count follows from the tile's extent inside the
   // output.  (TX is a power of two: positions split by shift and mask.)
-  const int cpg = a.gn_cpg;
   const int upb = cpg >= 32 ? 1 : 32 / cpg;  // units per block
-  const int uch = cpg >= 32 ? 32 : cpg;      // channels per unit
   const int nunits = (BN / 32) * upb;
   constexpr int NW = NTHR / 64, MAXR = (32 * RPR + 63) / 64;  // runs per lane for a 32-channel unit
   const int wave = tid >> 6;
