@@ -463,6 +463,33 @@ int atk_group_norm_apply(const void* x, const void* gamma, const void* beta, voi
                          int variant, atk_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Conv -> GroupNorm -> (SiLU) in one launch: the block the reference's fused module runs
+ * (amd_tuned_torch/conv_fusion_ops.py:355-439, "Conv3d -> GroupNorm -> SiLU") as three
+ * kernels.  The MFMA tile keeps its output in registers while the epilogue's GroupNorm
+ * records are exchanged between workgroups (tagged slots in `workspace`), then stores
+ *   y = act((conv + bias - mean) * rsqrt(var + eps) * gamma + beta)
+ * once.  The statistics are of the conv output rounded to the dtype, as the three-kernel
+ * block computes them.  16-bit NC[D]HW, groups with Co/groups in {4, 8, 16, 32} or a multiple
+ * of 32, an unsplit variant whose records are summed in registers and a grid that is resident
+ * at once: it is a cooperative launch.  atk_conv_gn_onepass_workspace_bytes(...) gives the
+ * workspace (0: the variant cannot take the shape; the call then returns ATK_UNSUPPORTED); the
+ * workspace is zeroed before its first use, kept between calls and private to one stream.
+ * gamma / beta: C values of param_dtype, or NULL (1 / 0).  Word 0 of the workspace (int32) is
+ * set if a wait for another workgroup ran out, which a resident grid never does.
+ * ------------------------------------------------------------------------- */
+size_t atk_conv_gn_onepass_workspace_bytes(int64_t N, int64_t Ci, int64_t D, int64_t H, int64_t W,
+                                           int64_t Co, int KD, int KH, int KW, int sd, int sh, int sw,
+                                           int pd, int ph, int pw, int dd, int dh, int dw, int dtype,
+                                           int variant, int groups);
+int atk_conv_group_norm_fwd(const void* x, const void* packed, size_t packed_bytes, const void* bias,
+                            const void* gamma, const void* beta, void* y, int64_t N, int64_t Ci,
+                            int64_t D, int64_t H, int64_t W, int64_t Co, int KD, int KH, int KW,
+                            int sd, int sh, int sw, int pd, int ph, int pw, int dd, int dh, int dw,
+                            int dtype, int variant, int groups, float eps, int fuse_silu,
+                            int param_dtype, void* workspace, size_t workspace_bytes,
+                            atk_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Conv weight gradient (replaces the dweight part of `aten.convolution_backward` that the
  * reference's _Conv3dFn.backward calls, amd_tuned_torch/_dispatch.py:2064-2075), for
  * stride-1, dilation-1 convs with kernel (KD, 3, 3), KD in {1, 3}, and "same" padding

@@ -47,7 +47,7 @@ EXPORTED_SYMBOLS = (
     "atk_dwconv1d_bwd", "atk_group_norm_noalloc_scratch_bytes", "atk_group_norm_fwd_noalloc",
     "atk_conv_packed_weight_bytes", "atk_conv_prepacked_workspace_bytes", "atk_conv_pack_weights",
     "atk_conv_fwd_prepacked", "atk_conv_fwd_prepacked_cl", "atk_conv_gn_stats_bytes", "atk_conv_gn_records",
-    "atk_conv_fwd_prepacked_ex",
+    "atk_conv_fwd_prepacked_ex", "atk_conv_gn_onepass_workspace_bytes", "atk_conv_group_norm_fwd",
     "atk_group_norm_apply", "atk_group_norm_cl_bwd_workspace_bytes", "atk_group_norm_cl_bwd",
 )
 
@@ -137,6 +137,11 @@ def _declare(lib) -> None:
     lib.atk_conv_fwd_prepacked_ex.argtypes = [vp, vp, sz, vp, vp, vp] + conv_geom + [i32, i32, i32, vp, sz, vp, sz,
                                                                                      vp]
     lib.atk_conv_fwd_prepacked_ex.restype = i32
+    lib.atk_conv_gn_onepass_workspace_bytes.argtypes = conv_geom + [i32, i32, i32]
+    lib.atk_conv_gn_onepass_workspace_bytes.restype = sz
+    lib.atk_conv_group_norm_fwd.argtypes = [vp, vp, sz, vp, vp, vp, vp] + conv_geom + [i32, i32, i32, c.c_float, i32,
+                                                                                   i32, vp, sz, vp]
+    lib.atk_conv_group_norm_fwd.restype = i32
     lib.atk_group_norm_apply.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, c.c_float, i32, i32, i32, vp, i64,
                                          i32, vp]
     lib.atk_group_norm_apply.restype = i32
@@ -1199,6 +1204,79 @@ def conv_gn_stats(input, weight, bias, stride, padding, dilation, nd: int, group
     """The conv (+ residual) of an unsplit MFMA variant with the GroupNorm records of its
     output for `groups` groups written by the epilogue: (y, records, records_per_group)."""
     return _conv(input, weight, bias, stride, padding, dilation, nd, variant, out, residual, gn_groups=groups)
+
+
+def conv_group_norm(input, weight, bias, gamma, beta, stride, padding, dilation, nd: int, groups: int, eps: float,
+                    *, silu: bool = False, variant: int, out=None) -> torch.Tensor:
+    """act(GroupNorm(conv(input) + bias)) in one cooperative launch of an MFMA variant: the
+    tile stays in registers while the GroupNorm statistics are exchanged between workgroups,
+    and y is written once.  Unsupported where the variant splits the shape, cannot sum the
+    records in registers, or the grid is not resident at once."""
+    _require_cuda(input, weight, bias, gamma, beta)
+    if not (input.is_contiguous() and weight.is_contiguous()) or input.dim() != nd + 2 or weight.dim() != nd + 2:
+        raise RuntimeError("conv_group_norm: contiguous input / weight of matching rank")
+    if input.dtype != weight.dtype or input.dtype not in (torch.float16, torch.bfloat16):
+        raise Unsupported("conv_group_norm: 16-bit input and weight of one dtype")
+    if weight.shape[1] != input.shape[1]:
+        raise RuntimeError("weight.size(1) must equal input channels (groups=1 only)")
+    Co = weight.shape[0]
+    if bias is not None:
+        if bias.numel() != Co or bias.dtype != input.dtype:
+            raise RuntimeError("Bias shape/dtype mismatch")
+        bias = bias.contiguous()
+    if gamma is not None and beta is not None and gamma.dtype != beta.dtype:
+        beta = beta.to(gamma.dtype)
+    for t in (gamma, beta):
+        if t is not None and (t.numel() != Co or t.dtype not in _DTYPE_CODE):
+            raise RuntimeError("conv_group_norm: gamma / beta of Co floats")
+    pdt = _DTYPE_CODE[(gamma if gamma is not None else beta).dtype] if (gamma is not None or beta is not None) \
+        else ATK_F32
+    gamma = gamma.contiguous() if gamma is not None else None
+    beta = beta.contiguous() if beta is not None else None
+    s, p, d = _ntuple(stride, nd), _ntuple(padding, nd), _ntuple(dilation, nd)
+    N, Ci = input.shape[:2]
+    if nd == 2:
+        D, (H, W) = 1, input.shape[2:]
+        KD, (KH, KW) = 1, weight.shape[2:]
+        s, p, d = (1,) + s, (0,) + p, (1,) + d
+    else:
+        D, H, W = input.shape[2:]
+        KD, KH, KW = weight.shape[2:]
+    osz = [conv_out_size(i, k, ss, pp, dd) for i, k, ss, pp, dd in zip((D, H, W), (KD, KH, KW), s, p, d)]
+    if min(osz) <= 0:
+        raise RuntimeError("Conv output size must be positive")
+    shape = (N, Co, *osz) if nd == 3 else (N, Co, osz[1], osz[2])
+    y = out if out is not None else torch.empty(shape, dtype=input.dtype, device=input.device)
+    if y.numel() == 0:
+        return y
+    L = lib()
+    dt = _DTYPE_CODE[input.dtype]
+    geom = (N, Ci, D, H, W, Co, KD, KH, KW, *s, *p, *d)
+    dev = _device_index(input.device)
+    packed_bytes = _cached_size(L.atk_conv_packed_weight_bytes, *geom, dt, int(variant), device=dev) \
+        if variant > 0 else 0
+    nws = _cached_size(L.atk_conv_gn_onepass_workspace_bytes, *geom, dt, int(variant), int(groups), device=dev) \
+        if packed_bytes else 0
+    if not nws:
+        raise Unsupported("conv_group_norm: this variant cannot run the one-pass GroupNorm for the shape")
+    stream = _raw_stream(input.device)
+    packed = _packed_conv_weights(weight, geom, dt, int(variant), packed_bytes, stream)
+    ws = workspace(input.device, "conv_gn_onepass", nws, stream)
+    rc = L.atk_conv_group_norm_fwd(_ptr(input), _ptr(packed), packed_bytes, _ptr(bias), _ptr(gamma), _ptr(beta),
+                                   _ptr(y), *geom, dt, int(variant), int(groups), float(eps), int(bool(silu)), pdt,
+                                   _ptr(ws), ws.numel(), stream)
+    _check(rc, f"conv{nd}d + group_norm")
+    return y
+
+
+def conv_group_norm_wait_error(device: Optional[torch.device] = None) -> bool:
+    """True if a one-pass conv + GroupNorm launch on `device` (any stream) ever ran out of a
+    wait for another workgroup's statistics (its output was then invalid; a cooperative launch
+    keeps every workgroup resident, so this stays False)."""
+    idx = _device_index(device or torch.device("cuda", torch.cuda.current_device()))
+    with _ws_lock:
+        bufs = [b for (d, _, p), b in _ws_live.items() if d == idx and p == "conv_gn_onepass"]
+    return any(int(b[:4].view(torch.int32).item()) != 0 for b in bufs)
 
 
 def group_norm_apply(x: torch.Tensor, num_groups: int, weight: Optional[torch.Tensor], bias: Optional[torch.Tensor],

@@ -251,10 +251,13 @@ def conv_group_norm_silu(input: torch.Tensor, weight: torch.Tensor, bias: Option
                          padding, dilation, num_groups: int, gamma: Optional[torch.Tensor],
                          beta: Optional[torch.Tensor], eps: float, silu: bool = True) -> torch.Tensor:
     """act(GroupNorm(conv(input, weight, bias))) for a groups-1, zero-padded conv2d / conv3d
-    (act = SiLU or identity): the conv's epilogue writes the GroupNorm statistics of its
-    output, then one pass normalises it in place -- the config-5 block as two kernels.  Falls
-    back to the stock sequence (the reference of the contest) and, with a gradient live, to the
-    patched functional path."""
+    (act = SiLU or identity).  Candidates per MFMA variant: `native.<variant>` -- the conv's
+    epilogue writes the GroupNorm statistics of its output, then one pass normalises it in
+    place (two kernels) -- and `native.onepass.<variant>` -- one cooperative launch whose tiles
+    stay in registers while the statistics are exchanged, so y is written once, normalised;
+    plus the accelerated conv followed by the accelerated GroupNorm(+SiLU).  Falls back to the
+    stock sequence (the reference of the contest) and, with a gradient live, to the patched
+    functional path."""
     nd = input.dim() - 2 if isinstance(input, torch.Tensor) else 0
 
     def unfused_patched():
@@ -287,6 +290,15 @@ def conv_group_norm_silu(input: torch.Tensor, weight: torch.Tensor, bias: Option
                 return None
         return run
 
+    def onepass(vi):
+        def run():
+            try:
+                return _native.conv_group_norm(input, weight, bias, gamma, beta, stride, padding, dilation, nd,
+                                               num_groups, eps, silu=silu, variant=vi)
+            except _native.Unsupported:
+                return None
+        return run
+
     key = ("conv%dd" % nd, input.dtype, tuple(input.shape), tuple(weight.shape), _norm(stride, nd),
            _norm(padding, nd), _norm(dilation, nd), bias is not None, num_groups, silu,
            gamma is not None, beta is not None)
@@ -299,6 +311,8 @@ def conv_group_norm_silu(input: torch.Tensor, weight: torch.Tensor, bias: Option
     # GroupNorm(+SiLU) -- whichever is fastest for this block (the epilogue statistics cost
     # the conv a little; they pay only when they save more in the GroupNorm pass)
     cands = [("native." + n, fused(i)) for i, n in _mfma_variants(input.dtype)]
+    if input.dtype in (torch.float16, torch.bfloat16):
+        cands += [("native.onepass." + n, onepass(i)) for i, n in _mfma_variants(input.dtype)]
     cands.append(("native.unfused", unfused_patched))
     if won is not None:
         for name, run in cands:

@@ -227,6 +227,30 @@ extern "C" int atk_conv_gn_records(ATK_CONV_GEOM_ARGS, int variant, int groups) 
   return conv_igemm_gn_records(p, variant - 1, groups);
 }
 
+extern "C" size_t atk_conv_gn_onepass_workspace_bytes(ATK_CONV_GEOM_ARGS, int variant, int groups) {
+  using namespace atk;
+  ConvShape p;
+  if (conv_shape(ATK_CONV_GEOM, p) || variant <= 0 || variant >= conv_num_variants()) return 0;
+  return conv_igemm_gn_onepass_bytes(p, variant - 1, groups);
+}
+
+extern "C" int atk_conv_group_norm_fwd(const void* x, const void* packed, size_t packed_bytes, const void* bias,
+                                       const void* gamma, const void* beta, void* y, ATK_CONV_GEOM_ARGS,
+                                       int variant, int groups, float eps, int silu, int param_dtype,
+                                       void* workspace, size_t workspace_bytes, atk_stream_t stream) {
+  using namespace atk;
+  ConvShape p;
+  int rc = conv_shape(ATK_CONV_GEOM, p);
+  if (rc) return rc;
+  if (variant <= 0 || variant >= conv_num_variants())
+    return fail(variant == 0 ? ATK_UNSUPPORTED : ATK_EINVAL, "conv: variant %d has no packed weights", variant);
+  if (N == 0) return ATK_OK;
+  if (!x || !y) return fail(ATK_EINVAL, "conv: null pointer");
+  return conv_igemm_run_gn_onepass(p, x, packed, packed_bytes, bias, gamma, beta, param_dtype, eps, silu, y,
+                                   variant - 1, groups, workspace, workspace_bytes,
+                                   reinterpret_cast<hipStream_t>(stream));
+}
+
 extern "C" int atk_conv_fwd_prepacked_ex(const void* x, const void* packed, size_t packed_bytes, const void* bias,
                                          const void* residual, void* y, ATK_CONV_GEOM_ARGS, int variant,
                                          int gn_groups, void* gn_stats, size_t gn_stats_bytes, void* workspace,

@@ -32,5 +32,12 @@ int conv_igemm_run_prepacked(const ConvShape& p, const void* x, const void* pack
                              int gn_G = 0, bool channels_last = false);
 size_t conv_igemm_gn_stats_bytes(const ConvShape& p, int v, int G);
 int conv_igemm_gn_records(const ConvShape& p, int v, int G);
+// Conv + GroupNorm (+ SiLU) in one cooperative launch (16-bit NC[D]HW, unsplit, no residual):
+// y is written once, normalised.  ws: conv_igemm_gn_onepass_bytes bytes, zeroed before its
+// first use and private to one stream; 0 bytes = the variant cannot take the shape.
+size_t conv_igemm_gn_onepass_bytes(const ConvShape& p, int v, int G);
+int conv_igemm_run_gn_onepass(const ConvShape& p, const void* x, const void* packed, size_t packed_bytes,
+                              const void* bias, const void* gamma, const void* beta, int param_dtype, float eps,
+                              int silu, void* y, int v, int G, void* ws, size_t ws_bytes, hipStream_t s);
 
 }  // namespace atk

@@ -25,6 +25,7 @@
 //    per-split fp32 partials summed in a deterministic finalize kernel.
 #include <algorithm>
 #include <cstdlib>
+#include <type_traits>
 
 #include "conv_common.h"
 
@@ -63,6 +64,18 @@ struct IgArgs {
   int gn_np;          // records per (n, g)
   int lds_epi;        // unsplit plain 16-bit NC[D]HW output through the LDS-staged epilogue
   int epi_pitch;      // its staging row pitch in bytes (BM * 2 + 16)
+  // One-pass GroupNorm (+ SiLU) of the output inside the launch (cooperative launch: every
+  // workgroup is resident): the records go to tagged slots, one workgroup per (n, g) merges
+  // them and publishes (mean, rstd), and every tile is stored normalised from registers.
+  int gn_onepass;
+  int gn_silu;
+  int gn_pdt;                      // dtype code of gamma / beta
+  float gn_eps;
+  const void* gn_gamma;            // or null (1)
+  const void* gn_beta;             // or null (0)
+  unsigned long long* gn_slots;    // [N * G][gn_np][3] record words, then [N * G][2] result words
+  unsigned int* gn_hdr;            // diagnostics [0], epoch [16], launch counter [32], block counters [64 + 16 b]
+  unsigned long long gn_wait_ticks;  // bound of every wait (wall-clock ticks): a hang guard only
 };
 
 template <typename T> struct MfmaTraits;
@@ -499,6 +512,195 @@ __device__ __forceinline__ void store_tile(const IgArgs& a, f32x16 (&acc)[FCO][F
   }
 }
 
+// Tagged words of the one-pass GroupNorm exchange: the launch's tag in the high half, a
+// float's bits in the low half, each one 64-bit agent-scope store or load, so a word read with
+// the current tag is whole and current without a fence.
+__device__ __forceinline__ void gn_put(unsigned long long* p, uint32_t tag, float v) {
+  __hip_atomic_store(p, ((unsigned long long)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ bool gn_get(unsigned long long* p, uint32_t tag, float& v) {
+  const unsigned long long w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  v = __uint_as_float((uint32_t)w);
+  return (uint32_t)(w >> 32) == tag;
+}
+
+// One-pass GroupNorm (+SiLU), after this workgroup has published its records (every record
+// slot (n, g, tile, wave share < span, part) of the launch is written by exactly one wave):
+//  1. workgroup j (linear index) merges the records of (n, g) = j, j + nwg, ..., one group per
+//     wave: records read once into registers, counted merge in record order with DPP wave sums
+//     (mean = sum c_i m_i / n, M2 = sum (M2_i + c_i (m_i - mean)^2)), then (mean, rstd) published;
+//  2. every workgroup polls the results of the groups its channel tile touches into LDS;
+//  3. the runs, held in registers since the statistics were taken, are normalised (+SiLU) and
+//     stored -- y is written once, normalised;
+//  4. the last workgroup to finish advances the epoch in the header (a counter per 64
+//     workgroups, then a launch counter, each reset by the workgroup that completes it), so no
+//     slot is ever cleared and a replayed graph sees fresh tags.
+// The host launches this cooperatively (every workgroup resident), so every record arrives.
+// Each wait is still bounded by a.gn_wait_ticks -- a guard against a hang, not a fallback: a
+// wait that runs out sets the header's diagnostics word and the launch's output is invalid.
+template <typename T, int BN, int RPR, int NRUN, int NTHR, int WSP>
+__device__ __forceinline__ void gn_onepass_finish(const IgArgs& a, const uint4 (&keep)[NRUN], int n, int co_tile,
+                                                  int oz, int oy0, int ox0, int q0, int lane, int tid, int span,
+                                                  uint32_t tag) {
+  constexpr int NW = NTHR / 64, RC = 4;
+  __shared__ float2 s_mr[BN / 4];  // (mean, rstd) of the groups of this channel tile
+  const int cpg = a.gn_cpg, G = a.gn_G, np = a.gn_np;
+  const int parts = cpg > 32 ? cpg / 32 : 1;
+  const int64_t spo = (int64_t)a.Do * a.Ho * a.Wo;
+  const int txs = __builtin_ctz((unsigned)a.TX);
+  // this thread's runs and their affine parameters, loaded before any wait
+  float gm[NRUN], bt[NRUN];
+#pragma unroll
+  for (int k = 0; k < NRUN; ++k) {
+    const int co = min(co_tile * BN + (q0 + 64 * k + lane) / RPR, a.Co - 1);
+    gm[k] = a.gn_gamma ? load_param(a.gn_gamma, a.gn_pdt, co) : 1.f;
+    bt[k] = a.gn_beta ? load_param(a.gn_beta, a.gn_pdt, co) : 0.f;
+  }
+  const int nwg = gridDim.x * gridDim.y;  // (unsplit: gridDim.z == 1)
+  const int wg = blockIdx.x + gridDim.x * blockIdx.y;
+  const uint64_t deadline = wall_clock64() + a.gn_wait_ticks;
+  bool late = false;
+  unsigned long long* res = a.gn_slots + (int64_t)a.N * G * np * 3;  // result words
+  // 1. merges
+  for (int j = wg + nwg * (tid >> 6); j < a.N * G; j += nwg * NW) {
+    unsigned long long* rs = a.gn_slots + (int64_t)j * np * 3;
+    auto live = [&](int r) { return r < np && (r / parts) % WSP < span; };
+    float c[RC], mu[RC], q2[RC];
+    bool have[RC];
+#pragma unroll
+    for (int i = 0; i < RC; ++i) {
+      c[i] = mu[i] = q2[i] = 0.f;
+      have[i] = !live(lane + 64 * i);
+    }
+    while (true) {
+      bool all = true;
+#pragma unroll
+      for (int i = 0; i < RC; ++i) {
+        if (have[i]) continue;
+        unsigned long long* w = rs + (int64_t)(lane + 64 * i) * 3;
+        float x0, x1, x2;
+        const bool o0 = gn_get(w, tag, x0), o1 = gn_get(w + 1, tag, x1), o2 = gn_get(w + 2, tag, x2);
+        if (o0 && o1 && o2) {
+          have[i] = true;
+          c[i] = x0;
+          mu[i] = x1;
+          q2[i] = x2;
+        }
+        all = all && have[i];
+      }
+      if (all) break;
+      if (wall_clock64() > deadline) {
+        late = true;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    float sn = 0.f, sm = 0.f;
+#pragma unroll
+    for (int i = 0; i < RC; ++i) {
+      sn += c[i];
+      sm = fmaf(c[i], mu[i], sm);
+    }
+    // records past 64 * RC (large grids): polled one at a time, read again below
+    for (int r = lane + 64 * RC; r < np; r += 64) {
+      if (!live(r)) continue;
+      float x0 = 0.f, x1 = 0.f, x2;
+      while (!(gn_get(rs + (int64_t)r * 3, tag, x0) && gn_get(rs + (int64_t)r * 3 + 1, tag, x1) &&
+               gn_get(rs + (int64_t)r * 3 + 2, tag, x2))) {
+        if (wall_clock64() > deadline) {
+          late = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      sn += x0;
+      sm = fmaf(x0, x1, sm);
+    }
+    const float cnt = wave_sum_rows(sn);
+    const float mean = wave_sum_rows(sm) / cnt;
+    float m2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < RC; ++i) {
+      const float d = mu[i] - mean;
+      m2 += q2[i] + c[i] * d * d;
+    }
+    for (int r = lane + 64 * RC; r < np; r += 64) {
+      if (!live(r)) continue;
+      float x0, x1, x2;
+      gn_get(rs + (int64_t)r * 3, tag, x0);
+      gn_get(rs + (int64_t)r * 3 + 1, tag, x1);
+      gn_get(rs + (int64_t)r * 3 + 2, tag, x2);
+      const float d = x1 - mean;
+      m2 += x2 + x0 * d * d;
+    }
+    const float var = wave_sum_rows(m2) / cnt;
+    if (lane == 0) {
+      gn_put(res + 2 * (int64_t)j, tag, mean);
+      gn_put(res + 2 * (int64_t)j + 1, tag, 1.0f / sqrtf(var + a.gn_eps));
+    }
+  }
+  // 2. the results this tile needs
+  const int g0 = (co_tile * BN) / cpg;
+  const int ng = min(G, ((co_tile + 1) * BN + cpg - 1) / cpg) - g0;
+  for (int t = tid; t < ng; t += NTHR) {
+    unsigned long long* w = res + 2 * ((int64_t)n * G + g0 + t);
+    float mean = 0.f, rstd = 0.f;
+    while (true) {
+      const bool o0 = gn_get(w, tag, mean), o1 = gn_get(w + 1, tag, rstd);
+      if (o0 && o1) break;
+      if (wall_clock64() > deadline) {
+        late = true;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    s_mr[t] = make_float2(mean, rstd);
+  }
+  if (late) __hip_atomic_store(a.gn_hdr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  // 3. normalise and store
+  auto finish = [&](auto silu) {
+#pragma unroll
+    for (int k = 0; k < NRUN; ++k) {
+      const int q = q0 + 64 * k + lane;
+      const int cl = q / RPR, m = (q - (q / RPR) * RPR) * 8;
+      const int oy = oy0 + (m >> txs), ox = ox0 + (m & (a.TX - 1));
+      const int co = co_tile * BN + cl;
+      const bool ok = oy < a.Ho && ox < a.Wo && co < a.Co;
+      const float2 st = s_mr[ok ? co / cpg - g0 : 0];
+      const float sc = st.y * gm[k], sh = bt[k] - st.x * sc;
+      Vec16<T> iv;
+      iv.raw = keep[k];
+      float f[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        f[e] = fmaf(to_f32(iv.e[e]), sc, sh);
+        if constexpr (decltype(silu)::value) f[e] = silu_f32(f[e]);
+      }
+      if (ok)
+        *reinterpret_cast<uint4*>(static_cast<T*>(a.y) + ((int64_t)n * a.Co + co) * spo +
+                                  ((int64_t)oz * a.Ho + oy) * a.Wo + ox) = pack16<T>(f);
+    }
+  };
+  if (a.gn_silu) finish(std::true_type());
+  else finish(std::false_type());
+  // 4. epoch
+  if (tid == 0) {
+    const int nb = (nwg + 63) / 64, b = wg / 64, in_b = min(64, nwg - b * 64);
+    unsigned int* bc = a.gn_hdr + 64 + 16 * b;
+    if (__hip_atomic_fetch_add(bc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (unsigned)in_b - 1) {
+      __hip_atomic_store(bc, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (__hip_atomic_fetch_add(a.gn_hdr + 32, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+          (unsigned)nb - 1) {
+        __hip_atomic_store(a.gn_hdr + 32, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(a.gn_hdr + 16, ((tag >> 1) + 1u) & 0x7fffffffu, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+}
+
 // Output (bias added, 16-bit, NC[D]HW, unsplit) through LDS.  Stored straight from the
 // accumulators, every value is its own 2-byte store (a lane holds one position of 16 channels
 // per block), so a wave issues FCO * FSP * 16 store instructions, each moving 128 bytes; at the
@@ -521,7 +723,7 @@ __device__ __forceinline__ void store_tile(const IgArgs& a, f32x16 (&acc)[FCO][F
 template <typename T, int FCO, int FSP, int BN, int BM, int WSP, bool EPI, int NTHR>
 __device__ __forceinline__ void store_tile_lds(const IgArgs& a, f32x16 (&acc)[FCO][FSP], const float* s_bias,
                                                char* stg, int n, int co_tile, int oz, int oy0, int ox0, int wco,
-                                               int wsp, bool active, int tid, int tile_rec) {
+                                               int wsp, bool active, int tid, int tile_rec, uint32_t gn_tag) {
   static_assert(sizeof(T) == 2, "16-bit outputs");
   int lane = threadIdx.x & 63;
   asm volatile("" : "+v"(lane));  // keep the address math below the main loop
@@ -562,11 +764,16 @@ __device__ __forceinline__ void store_tile_lds(const IgArgs& a, f32x16 (&acc)[FC
   // runs in this wave), and the wave reduces them per unit on the VALU.  A unit longer than a
   // wave's runs spans S <= WSP waves, each writing one of the tile's WSP record slots.  Other
   // layouts take the LDS pass at the end.
-  const int cpg = EPI ? a.gn_cpg : 0;
+  // (With gn_onepass the values stay in registers until the group statistics are known, and
+  // the host has checked that the records come from registers.)
+  const int cpg = a.gn_cpg;
   const int uch = cpg >= 32 ? 32 : cpg;
   const int urun = uch * RPR;
-  const bool gn = EPI && a.gn_parts;
+  const bool onepass = EPI && a.gn_onepass;
+  const bool gn = EPI && (a.gn_parts || onepass);
   const bool gn_reg = EXACT && gn && urun % 64 == 0 && (urun <= NRUN * 64 || urun / (NRUN * 64) <= WSP);
+  const int txs = __builtin_ctz((unsigned)a.TX);  // (TX is a power of two)
+  uint4 keep[NRUN];
   const int ush = gn_reg ? __builtin_ctz((unsigned)urun) : 0;
   float s1[NRUN], s2[NRUN], kk[NRUN];
 #pragma unroll
@@ -586,8 +793,7 @@ __device__ __forceinline__ void store_tile_lds(const IgArgs& a, f32x16 (&acc)[FC
     for (int k = 0; k < RB; ++k) {
       const int q = EXACT ? q0 + 64 * (k0 + k) + lane : tid + (k0 + k) * NTHR;
       const int cl = q / RPR, m = (q - (q / RPR) * RPR) * 8;
-      const int ty = m / a.TX, tx = m - (m / a.TX) * a.TX;
-      const int oy = oy0 + ty, ox = ox0 + tx;
+      const int oy = oy0 + (m >> txs), ox = ox0 + (m & (a.TX - 1));
       const int co = co_tile * BN + cl;
       ok[k] = k0 + k < NRUN && q < BN * RPR && oy < a.Ho && ox < a.Wo && co < a.Co;
       off[k] = ((int64_t)n * a.Co + (ok[k] ? co : 0)) * spo + ((int64_t)oz * a.Ho + (ok[k] ? oy : 0)) * a.Wo +
@@ -627,10 +833,11 @@ __device__ __forceinline__ void store_tile_lds(const IgArgs& a, f32x16 (&acc)[FC
         s1[k0 + k] = ok[k] ? t1 : 0.f;
         s2[k0 + k] = ok[k] ? t2 : 0.f;
       }
+      keep[k0 + k] = v[k];
     }
 #pragma unroll
     for (int k = 0; k < RB; ++k)
-      if (ok[k]) *reinterpret_cast<uint4*>(static_cast<T*>(a.y) + off[k]) = v[k];
+      if (ok[k] && !onepass) *reinterpret_cast<uint4*>(static_cast<T*>(a.y) + off[k]) = v[k];
   }
   if (gn_reg) {
     // stores k of one unit: KPU = min(urun / 64, NRUN) consecutive ones, from a multiple of
@@ -660,11 +867,22 @@ __device__ __forceinline__ void store_tile_lds(const IgArgs& a, f32x16 (&acc)[FC
       const float t = w1 / cnt;
       const int g = co0 / cpg, part = cpg > 32 ? (co0 % cpg) / 32 : 0;
       const int pw = (ps - us) / (NRUN * 64);  // this wave's share of the unit
+      const int64_t rec = ((int64_t)n * a.gn_G + g) * a.gn_np + (tile_rec * WSP + pw) * parts + part;
+      const float mean = kk[k] + t, m2 = fmaxf(fmaf(-w1, t, w2), 0.f);
+      if (onepass) {
+        // (slots with pw >= span are never written and never read)
+        gn_put(a.gn_slots + rec * 3, gn_tag, cnt);
+        gn_put(a.gn_slots + rec * 3 + 1, gn_tag, mean);
+        gn_put(a.gn_slots + rec * 3 + 2, gn_tag, m2);
+        continue;
+      }
       float4* recs = a.gn_parts + ((int64_t)n * a.gn_G + g) * a.gn_np;
-      recs[(tile_rec * WSP + pw) * parts + part] = make_float4(cnt, kk[k] + t, fmaxf(fmaf(-w1, t, w2), 0.f), 0.f);
+      recs[(tile_rec * WSP + pw) * parts + part] = make_float4(cnt, mean, m2, 0.f);
       if (pw == 0)  // the slots no wave of this unit fills hold count 0
         for (int w = span; w < WSP; ++w) recs[(tile_rec * WSP + w) * parts + part] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
+    if (onepass)
+      gn_onepass_finish<T, BN, RPR, NRUN, NTHR, WSP>(a, keep, n, co_tile, oz, oy0, ox0, q0, lane, tid, span, gn_tag);
     return;
   }
   if (!gn) return;
@@ -679,7 +897,7 @@ __device__ __forceinline__ void store_tile_lds(const IgArgs& a, f32x16 (&acc)[FC
   const int nunits = (BN / 32) * upb;
   constexpr int NW = NTHR / 64, MAXR = (32 * RPR + 63) / 64;  // runs per lane for a 32-channel unit
   const int wave = tid >> 6;
-  const int txs = __builtin_ctz((unsigned)a.TX), txm = a.TX - 1;
+  const int txm = a.TX - 1;
   const int vy = min(BM / a.TX, a.Ho - oy0), vx = min(a.TX, a.Wo - ox0);
   const int nruns = uch * RPR, nri = (nruns + 63) / 64;  // runs of the unit, runs per lane
   for (int u = wave; u < nunits; u += NW) {
@@ -779,6 +997,12 @@ void conv_igemm_kernel(IgArgs a) {
   const int split = blockIdx.z;
   __shared__ float s_bias[BN];
   if (kg == 0) stage_bias<T, BN, NT>(a, co_tile, s_bias);  // visible after the prologue's barrier
+  // one-pass GroupNorm: this launch's slot tag, from the epoch every workgroup reads first
+  __shared__ uint32_t s_tag;
+  if constexpr (EPI && LEPI) {
+    if (a.gn_onepass && threadIdx.x == 0)
+      s_tag = (__hip_atomic_load(a.gn_hdr + 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) << 1) | 1u;
+  }
   // stages of this split, then this K group's share of them; every group runs n_it iterations
   const int sp_begin = split * a.stages_per_split;
   const int sp_end = min(a.n_stages, sp_begin + a.stages_per_split);
@@ -1067,7 +1291,7 @@ void conv_igemm_kernel(IgArgs a) {
       // (KS == 1: the last stage ended with a barrier, so the patch buffers are free)
       store_tile_lds<T, FCO, FSP, BN, WSP * FSP * 32, WSP, EPI, 64 * NWG * KS>(
           a, acc, s_bias, lds_base, n, co_tile, oz, oy0, ox0, wco, wsp, kg == 0, threadIdx.x,
-          (oz * a.tiles_y + ty_t) * a.tiles_x + tx_t);
+          (oz * a.tiles_y + ty_t) * a.tiles_x + tx_t, EPI && LEPI ? s_tag : 0u);
       return;
     }
   }
@@ -1229,7 +1453,7 @@ struct IgPlan {
   int64_t tiles;
 };
 
-int plan_ig(const ConvShape& p, int v, IgPlan& pl) {
+int plan_ig(const ConvShape& p, int v, IgPlan& pl, bool unsplit = false) {
   const IgVariant& vr = kIg[v];
   const bool f32 = p.dtype == ATK_F32;
   if ((vr.dtype_class == 1) != f32) return fail(ATK_UNSUPPORTED, "conv %s: dtype not served", vr.name);
@@ -1289,11 +1513,12 @@ int plan_ig(const ConvShape& p, int v, IgPlan& pl) {
   const int co_tiles = (p.Co + pl.bn - 1) / pl.bn;
   if (pl.tiles > 0x7fffffff || co_tiles > 65535) return fail(ATK_UNSUPPORTED, "conv %s: grid too large", vr.name);
   // split K (stages) until the grid covers the chip about twice (a workgroup with K groups
-  // counts as that many workgroups)
+  // counts as that many workgroups); `unsplit` (the one-pass GroupNorm) keeps one split
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
   const int64_t wgs = pl.tiles * co_tiles * vr.ks;
   int splits = 1;
-  while (wgs * splits < 2 * cus && splits * 2 * vr.ks <= a.n_stages && splits * 2 <= vr.max_splits) splits *= 2;
+  while (!unsplit && wgs * splits < 2 * cus && splits * 2 * vr.ks <= a.n_stages && splits * 2 <= vr.max_splits)
+    splits *= 2;
   a.stages_per_split = (a.n_stages + splits - 1) / splits;
   splits = (a.n_stages + a.stages_per_split - 1) / a.stages_per_split;
   pl.splits = splits;
@@ -1328,8 +1553,11 @@ int resident_per_cu(int nthreads, size_t lds) {
 }
 
 // Launches Kern.  With `lds_only` (an instantiation carrying only the LDS-staged epilogue)
-// it returns kNeedPerValue instead of launching when that epilogue cannot be kept.
+// it returns kNeedPerValue instead of launching when that epilogue cannot be kept.  The
+// one-pass GroupNorm launch is cooperative.
 constexpr int kNeedPerValue = -1;
+constexpr int kOnePassHdrBytes = 4096;  // diagnostics, epoch, launch counter, block counters
+constexpr int kOnePassMaxWg = (kOnePassHdrBytes - 256) / 64 * 64;  // one 64-byte counter per 64 workgroups
 
 template <void (*Kern)(IgArgs)>
 int launch_ig_kern(const IgPlan& plan, int nthreads, hipStream_t s, bool lds_only = false) {
@@ -1344,7 +1572,8 @@ int launch_ig_kern(const IgPlan& plan, int nthreads, hipStream_t s, bool lds_onl
       else pl.a.lds_epi = 0;
     }
   }
-  if (lds_only && !pl.a.lds_epi) return kNeedPerValue;
+  if (lds_only && !pl.a.lds_epi) return pl.a.gn_onepass ? fail(ATK_UNSUPPORTED, "conv: the one-pass GroupNorm "
+                                                                  "needs the LDS-staged epilogue") : kNeedPerValue;
   if (pl.lds > 64 * 1024) {
     // opt in to more than 64 KB of dynamic LDS (gfx950 has 160 KB per CU)
     static bool raised = false;
@@ -1356,6 +1585,23 @@ int launch_ig_kern(const IgPlan& plan, int nthreads, hipStream_t s, bool lds_onl
     }
   }
   dim3 grid((unsigned)pl.tiles, (unsigned)((pl.a.Co + pl.bn - 1) / pl.bn), (unsigned)pl.splits);
+  if (pl.a.gn_onepass) {
+    // every workgroup waits for records of others: the grid must be resident at once, which a
+    // cooperative launch guarantees (or refuses)
+    const int64_t nwg = (int64_t)grid.x * grid.y;
+    if (nwg > (int64_t)resident_per_cu<Kern>(nthreads, pl.lds) * device_cu_count() || nwg > kOnePassMaxWg)
+      return fail(ATK_UNSUPPORTED, "conv: the one-pass GroupNorm grid (%lld workgroups) is not resident at once",
+                  (long long)nwg);
+    void* args[] = {&pl.a};
+    const hipError_t e = hipLaunchCooperativeKernel(reinterpret_cast<const void*>(Kern), grid, dim3(nthreads), args,
+                                                    (unsigned)pl.lds, s);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();  // (not sticky: clear it for the next launch's check)
+      return fail(e == hipErrorCooperativeLaunchTooLarge ? ATK_UNSUPPORTED : ATK_ELAUNCH,
+                  "conv (one-pass GroupNorm): cooperative launch refused: %s", hipGetErrorString(e));
+    }
+    return ATK_OK;
+  }
   hipLaunchKernelGGL(Kern, grid, dim3(nthreads), pl.lds, s, pl.a);
   return check_launch("conv_igemm_kernel");
 }
@@ -1371,7 +1617,7 @@ int launch_ig_vr(const IgPlan& pl, hipStream_t s) {
   }
   // the residual / GroupNorm epilogue is its own instantiation, so the plain kernel is unchanged;
   // the LDS-staged form of it (16-bit types) another, tried first
-  if (pl.a.resid || pl.a.gn_parts) {
+  if (pl.a.resid || pl.a.gn_parts || pl.a.gn_onepass) {
     if constexpr (VR) {
       if constexpr (sizeof(T) == 2 && KHT > 0) {
         if (pl.a.lds_epi) {
@@ -1380,6 +1626,7 @@ int launch_ig_vr(const IgPlan& pl, hipStream_t s) {
           if (rc != kNeedPerValue) return rc;
         }
       }
+      if (pl.a.gn_onepass) return fail(ATK_UNSUPPORTED, "conv: the one-pass GroupNorm needs the LDS-staged epilogue");
       IgPlan pv = pl;
       pv.a.lds_epi = 0;
       return launch_ig_kern<conv_igemm_kernel<T, WCO, WSP, FCO, FSP, CB, XC, VR, KHT, KWT, true, KS>>(pv, nt, s);
@@ -1432,13 +1679,56 @@ int gn_records(const ConvShape& p, const IgPlan& pl, int v, int G) {
   return np < (1 << 30) ? (int)np : 0;
 }
 
+// Whether store_tile_lds sums a tile's GroupNorm records in registers for channels-per-group
+// cpg (its gn_reg condition): equal run counts per thread, every store instruction inside one
+// unit, and a unit spread over at most WSP waves.
+bool gn_reg_layout(const IgPlan& pl, int v, int cpg) {
+  const int rpr = pl.bm / 8, nthr = pl.nthreads;
+  if (cpg <= 0 || (pl.bn * rpr) % nthr) return false;
+  const int nrun = pl.bn * rpr / nthr;
+  const int urun = (cpg >= 32 ? 32 : cpg) * rpr;
+  return urun % 64 == 0 && (urun <= nrun * 64 || urun / (nrun * 64) <= kIg[v].wsp);
+}
+
+// The one-pass GroupNorm's parameters and its workspace (kOnePassHdrBytes of header, then
+// 24 bytes per record slot and 16 per (n, g) result)
+struct GnOnePass {
+  const void* gamma;
+  const void* beta;
+  int pdt;
+  float eps;
+  int silu;
+  void* ws;
+};
+
+size_t gn_onepass_bytes(const ConvShape& p, int np, int G) {
+  return (size_t)kOnePassHdrBytes + (size_t)p.N * G * np * 24 + (size_t)p.N * G * 16;
+}
+
 template <typename T>
 int run_ig(const ConvShape& p, IgPlan& pl, const void* x, const void* wp, const void* bias, void* y, int v,
            float* part, hipStream_t s, const void* resid = nullptr, float4* gn_parts = nullptr, int gn_G = 0,
-           bool cl = false) {
+           bool cl = false, const GnOnePass* op = nullptr) {
   int rc = ATK_OK;
   IgArgs& a = pl.a;
   pl.cl = cl;
+  a.gn_onepass = 0;
+  if (op) {
+    if (sizeof(T) != 2 || cl || resid || gn_parts || pl.splits != 1)
+      return fail(ATK_UNSUPPORTED, "conv: the one-pass GroupNorm takes unsplit 16-bit NC[D]HW convs without a residual");
+    if (!gn_reg_layout(pl, v, gn_G > 0 ? p.Co / gn_G : 0))
+      return fail(ATK_UNSUPPORTED, "conv: the one-pass GroupNorm needs this tile's records summed in registers");
+    a.gn_onepass = 1;
+    a.gn_silu = op->silu;
+    a.gn_pdt = op->pdt;
+    a.gn_eps = op->eps;
+    a.gn_gamma = op->gamma;
+    a.gn_beta = op->beta;
+    a.gn_hdr = static_cast<unsigned int*>(op->ws);
+    a.gn_slots = reinterpret_cast<unsigned long long*>(static_cast<char*>(op->ws) + kOnePassHdrBytes);
+    const int khz = device_wall_clock_khz();
+    a.gn_wait_ticks = (unsigned long long)(khz > 0 ? khz : 100000) * 200;  // 200 ms
+  }
   if (cl && (sizeof(T) != 2 || resid || gn_parts || p.Ci % 8 || p.Co % 8))
     return fail(ATK_UNSUPPORTED, "conv (channels-last): 16-bit types, Ci and Co multiples of 8, no epilogue extras");
   a.x = x; a.bias = bias; a.y = y;
@@ -1446,10 +1736,10 @@ int run_ig(const ConvShape& p, IgPlan& pl, const void* x, const void* wp, const 
   a.gn_parts = gn_parts;
   a.gn_G = gn_G;
   a.gn_cpg = gn_G > 0 ? p.Co / gn_G : 0;
-  a.gn_np = gn_parts ? gn_records(p, pl, v, gn_G) : 0;
+  a.gn_np = gn_parts || op ? gn_records(p, pl, v, gn_G) : 0;
   if ((resid || gn_parts) && pl.splits != 1)
     return fail(ATK_UNSUPPORTED, "conv: the residual / GroupNorm epilogue needs an unsplit launch");
-  if (gn_parts && a.gn_np == 0)
+  if ((gn_parts || op) && a.gn_np == 0)
     return fail(ATK_UNSUPPORTED, "conv: GroupNorm statistics need Co/G in {4, 8, 16, 32} or a multiple of 32");
   // 16-byte patch chunks: along x rows (NCDHW) or along channels (channels-last)
   a.vec_rows = cl ? (aligned16(x) && aligned16(y)) : (p.W % (16 / (int)sizeof(T)) == 0) && aligned16(x);
@@ -1590,6 +1880,37 @@ int conv_igemm_gn_records(const ConvShape& p, int v, int G) {
   IgPlan pl;
   if (plan_ig(p, v, pl)) return 0;
   return gn_records(p, pl, v, G);
+}
+
+size_t conv_igemm_gn_onepass_bytes(const ConvShape& p, int v, int G) {
+  if (v < 0 || v >= kNumIg || p.dtype == ATK_F32) return 0;
+  IgPlan pl;
+  if (plan_ig(p, v, pl, true) || !gn_reg_layout(pl, v, G > 0 && p.Co % G == 0 ? p.Co / G : 0)) return 0;
+  const int np = gn_records(p, pl, v, G);
+  return np ? gn_onepass_bytes(p, np, G) : 0;
+}
+
+int conv_igemm_run_gn_onepass(const ConvShape& p, const void* x, const void* packed, size_t packed_bytes,
+                              const void* bias, const void* gamma, const void* beta, int param_dtype, float eps,
+                              int silu, void* y, int v, int G, void* ws, size_t ws_bytes, hipStream_t s) {
+  if (v < 0 || v >= kNumIg) return fail(ATK_EINVAL, "conv: variant out of range");
+  if (p.dtype == ATK_F32) return fail(ATK_UNSUPPORTED, "conv: the one-pass GroupNorm takes 16-bit types");
+  if (G <= 0 || p.Co % G) return fail(ATK_EINVAL, "conv: %d GroupNorm groups do not divide %d channels", G, p.Co);
+  if (!dtype_ok(param_dtype)) return fail(ATK_EINVAL, "conv: unknown GroupNorm parameter dtype code %d", param_dtype);
+  IgPlan pl;
+  int rc = plan_ig(p, v, pl, true);
+  if (rc) return rc;
+  if (!packed || packed_bytes < align256(pl.wp_bytes))
+    return fail(ATK_EINVAL, "conv: packed weights of %zu bytes expected", align256(pl.wp_bytes));
+  if (pl.splits != 1) return fail(ATK_UNSUPPORTED, "conv: the one-pass GroupNorm needs an unsplit launch");
+  const int np = gn_records(p, pl, v, G);
+  if (!np) return fail(ATK_UNSUPPORTED, "conv: GroupNorm statistics need Co/G in {4, 8, 16, 32} or a multiple of 32");
+  const size_t need = gn_onepass_bytes(p, np, G);
+  if (!ws || ws_bytes < need || (reinterpret_cast<uintptr_t>(ws) & 255))
+    return fail(ATK_EINVAL, "conv: the one-pass GroupNorm needs a 256-byte aligned workspace of %zu bytes", need);
+  const GnOnePass op{gamma, beta, param_dtype, eps, silu ? 1 : 0, ws};
+  if (p.dtype == ATK_F16) return run_ig<_Float16>(p, pl, x, packed, bias, y, v, nullptr, s, nullptr, nullptr, G, false, &op);
+  return run_ig<__bf16>(p, pl, x, packed, bias, y, v, nullptr, s, nullptr, nullptr, G, false, &op);
 }
 
 int conv_igemm_run_prepacked(const ConvShape& p, const void* x, const void* packed, size_t packed_bytes,

@@ -244,3 +244,119 @@ def test_conv_gn_stats_and_apply_full_size_c5(dev):
         ran += 1
         del y, rec, out, yd
     assert ran >= 1
+
+
+ONEPASS_CASES = [
+    # xshape, wshape, pad, groups, silu, affine
+    ((1, 32, 8, 16, 16), (64, 32, 3, 3, 3), 1, 8, True, True),      # cpg 8
+    ((2, 16, 5, 9, 16), (32, 16, 3, 3, 3), 1, 8, False, True),     # cpg 4, edge tiles, N = 2
+    ((1, 32, 4, 12, 24), (64, 32, 3, 3, 3), 1, 4, True, False),    # cpg 16, no affine
+    ((1, 32, 4, 8, 8), (64, 32, 3, 3, 3), 1, 2, True, True),       # cpg 32
+    ((1, 16, 4, 8, 8), (128, 16, 3, 3, 3), 1, 2, False, True),     # cpg 64: two 32-channel parts
+    ((2, 64, 4, 32, 32), (128, 64, 3, 3, 3), 1, 32, True, True),   # cpg 4 over 128 channels, N = 2
+    ((1, 32, 2, 16, 16), (64, 32, 1, 7, 7), (0, 3, 3), 16, True, True),  # 7x7 plane
+]
+
+
+def _onepass_params(co, dtype, affine, seed):
+    if not affine:
+        return None, None
+    gc = torch.Generator().manual_seed(seed)
+    return (1 + 0.1 * torch.randn(co, generator=gc)).to(dtype), (0.1 * torch.randn(co, generator=gc)).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("case", ONEPASS_CASES, ids=lambda c: "x".join(map(str, c[0])) + "_g%d" % c[3])
+def test_conv_group_norm_one_pass(dev, case, dtype):
+    """Conv -> GroupNorm (-> SiLU) in one cooperative launch, for every 16-bit variant that
+    takes the shape: against the float64 oracle of GroupNorm(+SiLU) applied to the plain conv's
+    output of the same variant (the statistics are of that stored output), and against the
+    float64 oracle of the whole block; repeats are bit-identical and no wait ran out."""
+    xs, ws, pad, G, silu, affine = case
+    nat = _native()
+    x, w, b = _inputs(xs, ws, dtype, seed=sum(xs) + 7 * G)
+    gm, bt = _onepass_params(ws[0], dtype, affine, seed=G)
+    xd, wd, bd = x.to(dev), w.to(dev), b.to(dev)
+    gmd = gm.to(dev) if gm is not None else None
+    btd = bt.to(dev) if bt is not None else None
+    block_ref = O.group_norm(torch.from_numpy(O.conv3d(x, w, b, 1, pad, 1)).to(dtype), G, gm, bt, 1e-5, silu=silu)
+    ran = 0
+    for vi, name in _mfma(nat, dtype):
+        try:
+            out = nat.conv_group_norm(xd, wd, bd, gmd, btd, 1, pad, 1, 3, G, 1e-5, silu=silu, variant=vi)
+        except nat.Unsupported:
+            continue
+        plain = nat.conv3d(xd, wd, bd, 1, pad, 1, variant=vi)
+        again = nat.conv_group_norm(xd, wd, bd, gmd, btd, 1, pad, 1, 3, G, 1e-5, silu=silu, variant=vi)
+        torch.cuda.synchronize()
+        assert not nat.conv_group_norm_wait_error(dev), name
+        assert torch.equal(out.view(torch.int16), again.view(torch.int16)), name
+        ref = O.group_norm(plain.cpu(), G, gm, bt, 1e-5, silu=silu)
+        assert O.max_rel_err(out.cpu(), ref) <= GN_BAR[dtype], name
+        assert O.max_rel_err(out.cpu(), block_ref) <= 2e-2, name
+        ran += 1
+    assert ran >= 1
+
+
+def test_conv_group_norm_one_pass_graph_replay(dev):
+    """The one-pass launch captured in a HIP graph: six replays, each after the input changed
+    in place, against eager calls on the same inputs (the slot tags come from the epoch the
+    launch itself advances, so a replay never reads the previous replay's records)."""
+    nat = _native()
+    xs, ws, G = (1, 32, 8, 16, 16), (64, 32, 3, 3, 3), 8
+    x, w, b = _inputs(xs, ws, torch.bfloat16, seed=77)
+    gm, bt = _onepass_params(64, torch.bfloat16, True, seed=3)
+    xd, wd, bd, gmd, btd = x.to(dev), w.to(dev), b.to(dev), gm.to(dev), bt.to(dev)
+    out = torch.empty(1, 64, 8, 16, 16, dtype=torch.bfloat16, device=dev)
+    vi = None
+    for i, _ in _mfma(nat, torch.bfloat16):
+        try:  # (also the warm-up: packed weights and workspace exist before the capture)
+            nat.conv_group_norm(xd, wd, bd, gmd, btd, 1, 1, 1, 3, G, 1e-6, silu=True, variant=i, out=out)
+        except nat.Unsupported:
+            continue
+        vi = i
+        break
+    assert vi is not None
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            nat.conv_group_norm(xd, wd, bd, gmd, btd, 1, 1, 1, 3, G, 1e-6, silu=True, variant=vi, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.Generator().manual_seed(78)
+    for _ in range(6):
+        xd.copy_(torch.randn(*xs, generator=g).to(torch.bfloat16))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = nat.conv_group_norm(xd, wd, bd, gmd, btd, 1, 1, 1, 3, G, 1e-6, silu=True, variant=vi)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+    assert not nat.conv_group_norm_wait_error(dev)
+
+
+def test_conv_group_norm_one_pass_full_size_c5(dev):
+    """Config 5's block at full size ([1, 256, 8, 64, 64] bf16, 3x3x3, GroupNorm(32, eps 1e-6)
+    + SiLU) in one launch, for every variant that takes it: against the float64 oracle of
+    GroupNorm+SiLU on the same variant's plain conv output."""
+    nat = _native()
+    xs, ws, G, eps = (1, 256, 8, 64, 64), (256, 256, 3, 3, 3), 32, 1e-6
+    x, w, b = _inputs(xs, ws, torch.bfloat16, seed=1005)
+    gm, bt = _onepass_params(256, torch.bfloat16, True, seed=6)
+    xd, wd, bd, gmd, btd = x.to(dev), w.to(dev), b.to(dev), gm.to(dev), bt.to(dev)
+    ran = 0
+    for vi, name in _mfma(nat, torch.bfloat16):
+        try:
+            out = nat.conv_group_norm(xd, wd, bd, gmd, btd, 1, 1, 1, 3, G, eps, silu=True, variant=vi)
+        except nat.Unsupported:
+            continue
+        plain = nat.conv3d(xd, wd, bd, 1, 1, 1, variant=vi)
+        torch.cuda.synchronize()
+        assert not nat.conv_group_norm_wait_error(dev), name
+        ref = O.group_norm(plain.cpu(), G, gm, bt, eps, silu=True)
+        assert O.max_rel_err(out.cpu(), ref) <= 1e-2, name
+        ran += 1
+        del out, plain
+    assert ran >= 1
