@@ -62,8 +62,8 @@ struct IgArgs {
   int gn_cpg;         // channels per GroupNorm group: 4, 8, 16, 32 or a multiple of 32
   int gn_G;           // groups (Co = gn_G * gn_cpg)
   int gn_np;          // records per (n, g)
-  int lds_epi;        // unsplit plain 16-bit NC[D]HW output through the LDS-staged epilogue
-  int epi_pitch;      // its staging row pitch in bytes (BM * 2 + 16)
+  int lds_epi;        // unsplit 16-bit output through the LDS-staged epilogue
+  int epi_pitch;      // its staging row pitch in bytes (NC[D]HW: BM * 2 + 16; channels-last: BN * 2 + 8)
   // One-pass GroupNorm (+ SiLU) of the output inside the launch (cooperative launch: every
   // workgroup is resident): the records go to tagged slots, one workgroup per (n, g) merges
   // them and publishes (mean, rstd), and every tile is stored normalised from registers.
@@ -701,6 +701,73 @@ __device__ __forceinline__ void gn_onepass_finish(const IgArgs& a, const uint4 (
   }
 }
 
+// Channels-last output (y[n][position][co], bias added, 16-bit, unsplit) through LDS.  Stored
+// straight from the accumulators, a lane's 4 consecutive channels of one position are one 8-byte
+// store, and the 64 lanes of a store instruction hit 64 positions Co * 2 bytes apart: partial
+// lines everywhere.  Here the tile goes to LDS as [position][channel] rows (pitch
+// a.epi_pitch = BN * 2 + 8, so the 32 positions of a write land on distinct bank pairs), each
+// lane's 4 channels as one 8-byte write; then consecutive threads store consecutive 16-byte runs
+// of 8 channels of one position -- BN * 2 contiguous bytes per position.  Needs Co % 8 == 0 and a
+// 16-byte aligned y (host check).  Every thread of the workgroup calls this after a barrier that
+// ends the last read of the stage buffers (`active`: the K group holding the sums).
+template <typename T, int FCO, int FSP, int BN, int BM, int WSP, int NTHR>
+__device__ __forceinline__ void store_tile_lds_cl(const IgArgs& a, f32x16 (&acc)[FCO][FSP], const float* s_bias,
+                                                  char* stg, int n, int co_tile, int oz, int oy0, int ox0, int wco,
+                                                  int wsp, bool active, int tid) {
+  static_assert(sizeof(T) == 2, "16-bit outputs");
+  int lane = threadIdx.x & 63;
+  asm volatile("" : "+v"(lane));  // keep the address math below the main loop
+  const int half = lane >> 5, col = lane & 31;
+  const int EP = a.epi_pitch;
+  if (active) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef T t2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int i = 0; i < FCO; ++i)
+#pragma unroll
+      for (int j = 0; j < FSP; ++j) {
+        const int m = (wsp * FSP + j) * 32 + col;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int cl = (wco * FCO + i) * 32 + q * 8 + half * 4;
+          const f2 lo = {acc[i][j][4 * q] + s_bias[cl], acc[i][j][4 * q + 1] + s_bias[cl + 1]};
+          const f2 hi = {acc[i][j][4 * q + 2] + s_bias[cl + 2], acc[i][j][4 * q + 3] + s_bias[cl + 3]};
+          *reinterpret_cast<uint2*>(stg + m * EP + cl * 2) =
+              make_uint2(__builtin_bit_cast(uint32_t, __builtin_convertvector(lo, t2)),
+                         __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, t2)));
+        }
+      }
+  }
+  __syncthreads();
+  const int64_t spo = (int64_t)a.Do * a.Ho * a.Wo;
+  const int txs = __builtin_ctz((unsigned)a.TX);  // (TX is a power of two)
+  constexpr int RPP = BN / 8;  // 16-byte runs per position
+  constexpr int NRUN = (BM * RPP + NTHR - 1) / NTHR, RB = NRUN < 8 ? NRUN : 8;
+#pragma unroll
+  for (int k0 = 0; k0 < NRUN; k0 += RB) {
+    int64_t off[RB];
+    bool ok[RB];
+    uint4 v[RB];
+#pragma unroll
+    for (int k = 0; k < RB; ++k) {
+      const int q = tid + (k0 + k) * NTHR;
+      const int m = q / RPP, c8 = q - (q / RPP) * RPP;
+      const int oy = oy0 + (m >> txs), ox = ox0 + (m & (a.TX - 1));
+      const int co = co_tile * BN + c8 * 8;
+      ok[k] = k0 + k < NRUN && q < BM * RPP && oy < a.Ho && ox < a.Wo && co < a.Co;
+      off[k] = ((int64_t)n * spo + ((int64_t)oz * a.Ho + (ok[k] ? oy : 0)) * a.Wo + (ok[k] ? ox : 0)) * a.Co +
+               (ok[k] ? co : 0);
+      // (rows are 8-byte aligned: two 8-byte reads)
+      const char* sp = stg + (ok[k] ? m : 0) * EP + (ok[k] ? c8 : 0) * 16;
+      const uint2 lo = *reinterpret_cast<const uint2*>(sp), hi = *reinterpret_cast<const uint2*>(sp + 8);
+      v[k] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+    }
+#pragma unroll
+    for (int k = 0; k < RB; ++k)
+      if (ok[k]) *reinterpret_cast<uint4*>(static_cast<T*>(a.y) + off[k]) = v[k];
+  }
+}
+
 // Output (bias added, 16-bit, NC[D]HW, unsplit) through LDS.  Stored straight from the
 // accumulators, every value is its own 2-byte store (a lane holds one position of 16 channels
 // per block), so a wave issues FCO * FSP * 16 store instructions, each moving 128 bytes; at the
@@ -1256,7 +1323,7 @@ void conv_igemm_kernel(IgArgs a) {
   }
 
   // the LDS-staged epilogue (a runtime choice of the host: see store_tile_lds)
-  constexpr bool LDS_EPI_OK = sizeof(T) == 2 && !CL;
+  constexpr bool LDS_EPI_OK = sizeof(T) == 2;
   const bool lds_epi = LDS_EPI_OK && a.lds_epi;
   if constexpr (KS > 1) {
     // groups 1..KS-1 park their accumulators in LDS (the patch buffers are free: the last
@@ -1289,9 +1356,13 @@ void conv_igemm_kernel(IgArgs a) {
   if constexpr (LDS_EPI_OK) {
     if (lds_epi) {
       // (KS == 1: the last stage ended with a barrier, so the patch buffers are free)
-      store_tile_lds<T, FCO, FSP, BN, WSP * FSP * 32, WSP, EPI, 64 * NWG * KS>(
-          a, acc, s_bias, lds_base, n, co_tile, oz, oy0, ox0, wco, wsp, kg == 0, threadIdx.x,
-          (oz * a.tiles_y + ty_t) * a.tiles_x + tx_t, EPI && LEPI ? s_tag : 0u);
+      if constexpr (CL)
+        store_tile_lds_cl<T, FCO, FSP, BN, WSP * FSP * 32, WSP, 64 * NWG * KS>(
+            a, acc, s_bias, lds_base, n, co_tile, oz, oy0, ox0, wco, wsp, kg == 0, threadIdx.x);
+      else
+        store_tile_lds<T, FCO, FSP, BN, WSP * FSP * 32, WSP, EPI, 64 * NWG * KS>(
+            a, acc, s_bias, lds_base, n, co_tile, oz, oy0, ox0, wco, wsp, kg == 0, threadIdx.x,
+            (oz * a.tiles_y + ty_t) * a.tiles_x + tx_t, EPI && LEPI ? s_tag : 0u);
       return;
     }
   }
@@ -1565,7 +1636,7 @@ int launch_ig_kern(const IgPlan& plan, int nthreads, hipStream_t s, bool lds_onl
   if (pl.a.lds_epi) {
     // the staging area of the LDS-staged epilogue: keep it only where it costs no resident
     // workgroup per CU
-    const size_t stg = (size_t)pl.bn * pl.a.epi_pitch;
+    const size_t stg = (size_t)(pl.cl ? pl.bm : pl.bn) * pl.a.epi_pitch;
     if (stg > pl.lds) {
       const int before = resident_per_cu<Kern>(nthreads, pl.lds);
       if (before > 0 && resident_per_cu<Kern>(nthreads, stg) == before) pl.lds = stg;
@@ -1750,13 +1821,17 @@ int run_ig(const ConvShape& p, IgPlan& pl, const void* x, const void* wp, const 
   // LDS-staged epilogue for plain unsplit 16-bit NC[D]HW output (store_tile_lds) where the
   // shape allows it; launch_ig_kern keeps it only if its staging area costs no resident
   // workgroup per CU
-  a.epi_pitch = pl.bm * 2 + 16;
+  a.epi_pitch = cl ? pl.bn * 2 + 8 : pl.bm * 2 + 16;
   {
     // ATK_CONV_LDS_EPI=0 keeps the per-value stores (read per call: tests compare the two)
     const char* e = getenv("ATK_CONV_LDS_EPI");
     const bool off = e && e[0] == '0';
-    a.lds_epi = (!off && sizeof(T) == 2 && !cl && pl.splits == 1 && p.Wo % 8 == 0 && a.TX % 8 == 0 &&
-                 aligned16(y) && (!resid || aligned16(resid)) && (size_t)pl.bn * a.epi_pitch <= 150 * 1024) ? 1 : 0;
+    if (cl)
+      a.lds_epi = (!off && sizeof(T) == 2 && pl.splits == 1 && p.Co % 8 == 0 && aligned16(y) &&
+                   (size_t)pl.bm * a.epi_pitch <= 150 * 1024) ? 1 : 0;
+    else
+      a.lds_epi = (!off && sizeof(T) == 2 && pl.splits == 1 && p.Wo % 8 == 0 && a.TX % 8 == 0 && aligned16(y) &&
+                   (!resid || aligned16(resid)) && (size_t)pl.bn * a.epi_pitch <= 150 * 1024) ? 1 : 0;
   }
   // instantiate only the variants of this element type's class
   if constexpr (sizeof(T) == 2) {

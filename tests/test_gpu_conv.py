@@ -317,6 +317,35 @@ def test_conv_channels_last_native_tiles(dev, case, dtype):
     assert ran >= 3
 
 
+@pytest.mark.parametrize("case", CL_NATIVE_CASES, ids=lambda c: "x".join(map(str, c[0])) + "_w" + "x".join(map(str, c[1])))
+def test_conv_channels_last_lds_staged_epilogue_bit_exact(dev, case, monkeypatch):
+    """The channels-last LDS-staged epilogue (16-byte runs of 8 channels per position) stores the
+    same bits as the per-value 8-byte stores it replaces (ATK_CONV_LDS_EPI=0), for every tile."""
+    nat = _native()
+    xs, ws, pad = case
+    nd = len(xs) - 2
+    x, w, b = _inputs(xs, ws, torch.bfloat16, seed=sum(xs) + 1)
+    fmt = torch.channels_last_3d if nd == 3 else torch.channels_last
+    xcl = x.to(dev).contiguous(memory_format=fmt)
+    wd, bd = w.to(dev), b.to(dev)
+    ran = 0
+    for vi, name in _variants_for(torch.bfloat16):
+        if name == "direct":
+            continue
+        try:
+            monkeypatch.setenv("ATK_CONV_LDS_EPI", "0")
+            want = nat.conv_channels_last(xcl, wd, bd, 1, pad, 1, nd, variant=vi)
+            monkeypatch.delenv("ATK_CONV_LDS_EPI")
+            got = nat.conv_channels_last(xcl, wd, bd, 1, pad, 1, nd, variant=vi)
+        except nat.Unsupported:
+            continue
+        torch.cuda.synchronize()
+        assert got.is_contiguous(memory_format=fmt)
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), name
+        ran += 1
+    assert ran >= 3
+
+
 def test_conv_channels_last_native_declines():
     """fp32, planes other than 3x3 / 7x7 and channel counts off multiples of 8 are declined
     (the dispatch then converts layouts for the NC(D)HW tiles)."""
