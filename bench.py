@@ -1055,7 +1055,9 @@ def summarize_mfma(run_dir: str, out_path: str, command: str, iters: int = 10):
     durations of the same dispatches).  The probe launches each tile iters + 1 times in
     CONV_PROBE order, so the conv_igemm dispatches are attributed by order (the trace names
     some instantiations mangled and some not).  MFMA busy % = busy cycles summed over the
-    SIMDs / (SIMDs x duration x engine clock); counted MFMA FLOPs = MOPS x 512."""
+    SIMDs / (SIMDs x duration x engine clock); busy_at_clk% uses the cycles the chip actually
+    ran (GRBM_GUI_ACTIVE summed over the XCDs / XCDs: the clock under MFMA load is below the
+    nominal one); counted MFMA FLOPs = MOPS x 512."""
     import csv
     import glob
     per: "dict[int, dict]" = {}
@@ -1066,19 +1068,22 @@ def summarize_mfma(run_dir: str, out_path: str, command: str, iters: int = 10):
             d = per.setdefault(int(r["Dispatch_Id"]), {"name": r["Kernel_Name"],
                                                         "ns": float(r["End_Timestamp"]) - float(r["Start_Timestamp"])})
             d[r["Counter_Name"]] = float(r["Counter_Value"])
-    simds, clk_mhz = 1024, 2400.0
+    simds, clk_mhz, nxcc = 1024, 2400.0, 8
     for f in glob.glob(os.path.join(run_dir, "**", "*agent_info.csv"), recursive=True):
         for r in csv.DictReader(open(f)):
             if r.get("Agent_Type") == "GPU":
                 simds = int(r["Simd_Count"]) or simds
                 clk_mhz = float(r["Max_Engine_Clk_Fcompute"]) or clk_mhz
+                nxcc = int(r.get("Num_Xcc") or nxcc)
     order = [per[k] for k in sorted(per)]
     n = iters + 1
     lines = ["# MFMA utilisation of the conv implicit-GEMM kernels (rocprofv3 --pmc, one pass)",
              f"# command: {command}",
              f"# {simds} SIMDs at {clk_mhz:.0f} MHz; mfma_busy% = sum SQ_VALU_MFMA_BUSY_CYCLES / "
-             "(SIMDs x duration x clock); counted = (MOPS_F16 + MOPS_BF16) x 512 / algorithmic FLOPs",
-             f"# {'calls':>5} {'avg_us':>8} {'algo_TF/s':>9} {'of_peak':>7} {'mfma_busy%':>10} {'counted':>7}  config / kernel"]
+             "(SIMDs x duration x clock); busy_at_clk% = the same over (SIMDs x GRBM_GUI_ACTIVE / XCDs), "
+             "the cycles run at the clock held (clk_MHz); counted = (MOPS_F16 + MOPS_BF16) x 512 / algorithmic FLOPs",
+             f"# {'calls':>5} {'avg_us':>8} {'algo_TF/s':>9} {'of_peak':>7} {'mfma_busy%':>10} "
+             f"{'busy_at_clk%':>12} {'clk_MHz':>7} {'counted':>7}  config / kernel"]
     if len(order) != n * len(CONV_PROBE):
         lines.append(f"  ({len(order)} conv dispatches, expected {n * len(CONV_PROBE)}: not attributed)")
     else:
@@ -1088,10 +1093,13 @@ def summarize_mfma(run_dir: str, out_path: str, command: str, iters: int = 10):
             busy = sum(d.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) for d in chunk) / n
             mops = sum(d.get("SQ_INSTS_VALU_MFMA_MOPS_F16", 0.0) + d.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0)
                        for d in chunk) / n
+            gui = sum(d.get("GRBM_GUI_ACTIVE", 0.0) for d in chunk) / n / max(nxcc, 1)  # cycles per XCD
             algo = 2.0 * xs[0] * ws[0] * math.prod(xs[2:]) * math.prod(ws[1:])  # stride 1, 'same'
             tfs = algo / ns / 1e3
+            at_clk = 100.0 * busy / (simds * gui) if gui > 0 else float("nan")
             lines.append(f"  {n:5d} {ns / 1e3:8.2f} {tfs:9.1f} {tfs / MFMA_PEAK_TFLOPS['bf16']:7.3f} "
-                         f"{100.0 * busy / (simds * ns * 1e-9 * clk_mhz * 1e6):10.1f} {mops * 512 / algo:7.3f}"
+                         f"{100.0 * busy / (simds * ns * 1e-9 * clk_mhz * 1e6):10.1f} {at_clk:12.1f} "
+                         f"{gui / (ns * 1e-3):7.0f} {mops * 512 / algo:7.3f}"
                          f"  {label} {vn}: {chunk[0]['name'][:100]}")
     with open(out_path, "w") as f:
         f.write("\n".join(lines) + "\n")

@@ -1326,32 +1326,40 @@ void conv_igemm_kernel(IgArgs a) {
   constexpr bool LDS_EPI_OK = sizeof(T) == 2;
   const bool lds_epi = LDS_EPI_OK && a.lds_epi;
   if constexpr (KS > 1) {
-    // groups 1..KS-1 park their accumulators in LDS (the patch buffers are free: the last
-    // iteration ended with a barrier); group 0 adds them in group order
+    // pairwise rounds of stride st = 1, 2, ...: a group still holding a partial sum whose index
+    // is an odd multiple of st parks it in LDS, and the group st below adds it -- a fixed order
+    // ((g0 + g1) + (g2 + g3), ...) with at most KS / 2 groups parked at once (the patch
+    // buffers are free: the last iteration ended with a barrier)
     float* red = reinterpret_cast<float*>(lds_base);
-    auto slot = [&](int g, int i, int j, int r) {
-      return ((((g - 1) * NWG + wv) * FCO + i) * FSP + j) * 16 * 64 + r * 64 + lane;
+    auto slot = [&](int p, int i, int j, int r) {
+      return ((((p * NWG + wv) * FCO + i) * FSP + j) * 16 + r) * 64 + lane;
     };
-    if (kg > 0) {
 #pragma unroll
-      for (int i = 0; i < FCO; ++i)
-#pragma unroll
-        for (int j = 0; j < FSP; ++j)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) red[slot(kg, i, j, r)] = acc[i][j][r];
-    }
-    __syncthreads();
-    if (kg > 0 && !lds_epi) return;
-    if (kg == 0) {
-      for (int g = 1; g < KS; ++g)
+    for (int st = 1; st < KS; st *= 2) {
+      const bool parks = kg % (2 * st) == st;
+      const bool adds = kg % (2 * st) == 0 && kg + st < KS;
+      const int p = kg / (2 * st);
+      if (parks) {
 #pragma unroll
         for (int i = 0; i < FCO; ++i)
 #pragma unroll
           for (int j = 0; j < FSP; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] += red[slot(g, i, j, r)];
+            for (int r = 0; r < 16; ++r) red[slot(p, i, j, r)] = acc[i][j][r];
+      }
+      __syncthreads();
+      if (adds) {
+#pragma unroll
+        for (int i = 0; i < FCO; ++i)
+#pragma unroll
+          for (int j = 0; j < FSP; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] += red[slot(p, i, j, r)];
+      }
+      // (the next round, or the staged epilogue, reuses the area)
+      if (st * 2 < KS || lds_epi) __syncthreads();
     }
-    if (lds_epi) __syncthreads();  // every group is done with the hand-over area
+    if (kg > 0 && !lds_epi) return;
   }
   if constexpr (LDS_EPI_OK) {
     if (lds_epi) {
@@ -1512,7 +1520,9 @@ const IgVariant kIg[] = {
     // split-K partials in memory and no finalize pass
     {"h_w22_f24_cb16_k2", 0, 2, 2, 2, 4, 16, 1, 16, 2},
     {"h_w41_f22_cb32_k2", 0, 4, 1, 2, 2, 32, 1, 16, 2},
-    {"h_w21_f24_cb32_k2", 0, 2, 1, 2, 4, 32, 1, 16, 2},
+    // 64 output channels on large grids: 2x4 register tiles (half the weight loads per MFMA of
+    // the 2x2 ones) over a 512-position tile, two workgroups per CU
+    {"h_w14_f24_cb16x2", 0, 1, 4, 2, 4, 16, 2, 16},
 };
 constexpr int kNumIg = sizeof(kIg) / sizeof(kIg[0]);
 
@@ -1570,10 +1580,11 @@ int plan_ig(const ConvShape& p, int v, IgPlan& pl, bool unsplit = false) {
     a.PXS = a.NCX * VEC + (kLdsCu / padded == kLdsCu / plain ? row_pad : 0);
   }
   a.patch_elems = a.PY * a.PXS * (vr.cb + VEC);
-  // two patch buffers per K group; with K groups, the accumulator hand-over reuses them
+  // two patch buffers per K group; with K groups, the accumulator hand-over reuses them (at
+  // most KS / 2 groups park at once)
   pl.lds = (size_t)2 * a.patch_elems * es * vr.ks;
   if (vr.ks > 1)
-    pl.lds = std::max(pl.lds, (size_t)(vr.ks - 1) * vr.wco * vr.wsp * vr.fco * vr.fsp * 16 * 64 * 4);
+    pl.lds = std::max(pl.lds, (size_t)(vr.ks / 2) * vr.wco * vr.wsp * vr.fco * vr.fsp * 16 * 64 * 4);
   {
     const int maxc = (f32 ? vr.cb / 2 : vr.cb / 4) * vr.xc * 256 / ntg;  // PatchLoader::MAXC
     if (pl.lds > 150 * 1024 || vr.cb * a.PY * a.NCX > maxc * ntg)
@@ -1856,7 +1867,7 @@ int run_ig(const ConvShape& p, IgPlan& pl, const void* x, const void* wp, const 
       case 23: rc = launch_ig_t<T, 1, 4, 2, 2, 16, 2, 2>(pl, s); break;
       case 24: rc = launch_ig_t<T, 2, 2, 2, 4, 16, 1, 2>(pl, s); break;
       case 25: rc = launch_ig_t<T, 4, 1, 2, 2, 32, 1, 2>(pl, s); break;
-      case 26: rc = launch_ig_t<T, 2, 1, 2, 4, 32, 1, 2>(pl, s); break;
+      case 26: rc = launch_ig_t<T, 1, 4, 2, 4, 16, 2>(pl, s); break;
       default: return fail(ATK_EINVAL, "conv: bad variant");
     }
   } else {
