@@ -247,26 +247,39 @@ def bench_c1_gpu_detail(dtype, dev):
 
 def bench_c1_cpu_dispatch_overhead():
     """Config 1 exactly as the reference runs it: fp32 on the CPU, where the patched F.conv1d
-    declines every native path and calls stock.  Reports both per-call times (min over
-    alternating rounds), the wrapper's overhead and whether the outputs are bit-identical."""
+    declines every native path and calls stock.  Reports both per-call times on C1 (median of
+    alternating rounds: the host's CPU time varies by tens of percent between runs), the wrapper's
+    own overhead -- measured on a [1, 256, 32] input of the same kind, where the conv itself
+    costs a few microseconds, as the min over alternating calls -- and whether the outputs are
+    bit-identical."""
+    import statistics
     import torch
     import torch.nn.functional as F
     import amd_tuned_torch
     stock = amd_tuned_torch.miopen_fallback._original_conv1d
     x, w, b = c1_inputs(torch.float32)
-    patched = lambda: F.conv1d(x, w, b, padding=1, groups=256)  # noqa: E731
-    plain = lambda: stock(x, w, b, 1, 1, 1, 256)  # noqa: E731
-    exact = bool(torch.equal(patched(), plain()))
-    best = {"stock": float("inf"), "patched": float("inf")}
-    for _ in range(15):
-        for name, fn in (("stock", plain), ("patched", patched)):
-            t0 = time.perf_counter()
-            fn()
-            best[name] = min(best[name], time.perf_counter() - t0)
-    return {"stock_us": round(best["stock"] * 1e6, 1), "patched_us": round(best["patched"] * 1e6, 1),
-            "overhead_us": round((best["patched"] - best["stock"]) * 1e6, 1),
+    exact = bool(torch.equal(F.conv1d(x, w, b, padding=1, groups=256), stock(x, w, b, 1, 1, 1, 256)))
+
+    def alternate(xx, rounds):
+        times = {"stock": [], "patched": []}
+        fns = (("stock", lambda: stock(xx, w, b, 1, 1, 1, 256)),
+               ("patched", lambda: F.conv1d(xx, w, b, padding=1, groups=256)))
+        for _ in range(rounds):
+            for name, fn in fns:
+                t0 = time.perf_counter()
+                fn()
+                times[name].append(time.perf_counter() - t0)
+        return times
+
+    full = alternate(x, 15)
+    small = alternate(x[:1, :, :32].contiguous(), 300)
+    overhead = min(small["patched"]) - min(small["stock"])
+    return {"stock_us": round(statistics.median(full["stock"]) * 1e6, 1),
+            "patched_us": round(statistics.median(full["patched"]) * 1e6, 1),
+            "overhead_us": round(overhead * 1e6, 2),
             "bit_exact_vs_stock": exact, "threads": torch.get_num_threads(),
-            "note": "fp32 on the host CPU, [8,256,2048] k3 p1 groups=256, min of 15 alternating runs"}
+            "note": "fp32 on the host CPU, [8,256,2048] k3 p1 groups=256: medians of 15 alternating runs; "
+                    "overhead: min over 300 alternating calls on [1,256,32]"}
 
 
 # ---------------------------------------------------------------------------
