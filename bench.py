@@ -1016,6 +1016,161 @@ def gn_probe(iters: int = 10):
     log("gn probe done")
 
 
+# channels-last GroupNorm kernels profiled by --gn-cl-probe: (label, NC[D]HW shape, silu, pass);
+# bf16, G = 32, eps 1e-5; a backward call is two dispatches (resident kernel, rows finalize)
+GN_CL_PROBE = [
+    ("C3a NHWC bf16", (8, 512, 64, 64), False, "fwd"),
+    ("C3a NHWC bf16 +SiLU", (8, 512, 64, 64), True, "fwd"),
+    ("C3b NDHWC bf16", (1, 512, 16, 64, 64), False, "fwd"),
+    ("C3a NHWC bf16 backward", (8, 512, 64, 64), False, "bwd"),
+]
+
+
+def gn_cl_probe(iters: int = 10):
+    """Workload for the channels-last GroupNorm traffic passes: `iters` calls of each
+    GN_CL_PROBE entry in order (register-resident kernels where the shape allows them), then
+    `iters` launches of the torch.neg calibration copy."""
+    import torch
+    from amd_tuned_torch import _native as nat
+    dev = torch.device("cuda", 0)
+    for label, shape, silu, kind in GN_CL_PROBE:
+        g = _gen(1003)
+        fmt = torch.channels_last if len(shape) == 4 else torch.channels_last_3d
+        C = shape[1]
+        x = torch.randn(*shape, generator=g).to(torch.bfloat16).to(dev).contiguous(memory_format=fmt)
+        gm = (1 + 0.1 * torch.randn(C, generator=g)).to(torch.bfloat16).to(dev)
+        bt = (0.1 * torch.randn(C, generator=g)).to(torch.bfloat16).to(dev)
+        dy = torch.randn_like(x)
+        for _ in range(iters):
+            if kind == "fwd":
+                nat.group_norm_cl(x, 32, gm, bt, 1e-5, silu=silu)
+            else:
+                nat.group_norm_cl_backward(dy, x, 32, gm, 1e-5)
+        torch.cuda.synchronize()
+        log(f"gn cl probe {label} done")
+    src = torch.randn(CALIB_ELEMS, device=dev, dtype=torch.bfloat16)
+    dst = torch.empty_like(src)
+    for _ in range(iters):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    log("gn cl probe done")
+
+
+def summarize_gn_cl_traffic(fetch_dir: str, write_dir: str, out_path: str, command: str, iters: int = 10):
+    """HBM traffic per call of the GN_CL_PROBE entries from a FETCH_SIZE pass and a WRITE_SIZE
+    pass over `bench.py --gn-cl-probe`, scaled by the torch.neg copy of the same runs.  The
+    channels-last GroupNorm dispatches are attributed by order (a backward call is two)."""
+    per_call = [1 if kind == "fwd" else 2 for *_, kind in GN_CL_PROBE]
+    rows = {}
+    for tag, run_dir, counter in (("fetch", fetch_dir, "FETCH_SIZE"), ("write", write_dir, "WRITE_SIZE")):
+        gn = _dispatch_counter(run_dir, counter, "gn_cl_")
+        neg = [v for _, _, v in _dispatch_counter(run_dir, counter, "neg")]
+        if len(gn) != iters * sum(per_call) or not neg:
+            raise SystemExit(f"{counter}: {len(gn)} channels-last GroupNorm dispatches, {len(neg)} calibration ones")
+        rows[tag] = (gn, sum(neg) / len(neg))
+    calib_bytes = CALIB_ELEMS * 2
+    f_scale = rows["fetch"][1] * 1024.0 / calib_bytes
+    w_scale = rows["write"][1] * 1024.0 / calib_bytes
+    lines = ["# HBM traffic per call of the channels-last GroupNorm kernels (bf16, G = 32)",
+             f"# commands: {command}",
+             f"# FETCH_SIZE scale {f_scale:.4f}, WRITE_SIZE scale {w_scale:.4f} (counter KiB x 1024 per true "
+             f"byte, from torch.neg over {calib_bytes} B read + written in the same runs); algorithmic: "
+             "forward x read + y written, backward x and dy read + dx written",
+             f"# {'read_MB':>8} {'write_MB':>8} {'algo_rd':>8} {'algo_wr':>8} {'read/algo':>9} "
+             f"{'write/algo':>10}  config / kernels"]
+    at = 0
+    for (label, shape, silu, kind), n in zip(GN_CL_PROBE, per_call):
+        span = slice(at * iters, (at + n) * iters)
+        rd = sum(v for _, _, v in rows["fetch"][0][span]) / iters * 1024.0 / f_scale
+        wr = sum(v for _, _, v in rows["write"][0][span]) / iters * 1024.0 / w_scale
+        names = sorted({nm[nm.find("gn_cl_"):].split("(")[0].split("EEEv")[0] for _, nm, _ in rows["fetch"][0][span]})
+        t = math.prod(shape) * 2
+        ard, awr = (t, t) if kind == "fwd" else (2 * t, t)
+        lines.append(f"  {rd / 1e6:8.2f} {wr / 1e6:8.2f} {ard / 1e6:8.2f} {awr / 1e6:8.2f} {rd / ard:9.4f} "
+                     f"{wr / awr:10.4f}  {label}: {', '.join(names)}")
+        at += n
+    with open(out_path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
+def gn_phase_probe(out_path: str, command: str, iters: int = 20):
+    """Per-phase timeline of the register-resident GroupNorm kernels of GN_PROBE: with
+    `_native.group_norm_trace` registered, every workgroup stamps the wall clock at entry, when
+    its slice statistics are done (its loads have all arrived), when the group statistics are
+    known (after the exchange with the group's other workgroups) and when its stores are issued.
+    Per launch: the spread of the entry stamps, the per-workgroup phases (median and max over
+    workgroups), the time from the first entry to the last workgroup's stores issued, and the
+    launch's duration from HIP events; medians over `iters` launches.  A torch copy of the same
+    bytes is timed beside each for reference."""
+    import statistics
+    import torch
+    from amd_tuned_torch import _native as nat
+    dev = torch.device("cuda", 0)
+    names = nat.variants(nat.OP_GROUP_NORM)
+    words = torch.zeros(4 * 8192, dtype=torch.int64, device=dev)
+    khz = nat.group_norm_trace(words)
+    if khz <= 0:
+        raise RuntimeError("no wall-clock rate")
+    us = 1e3 / khz  # microseconds per tick
+    lines = ["# Phase timeline of the register-resident GroupNorm kernels (wall-clock stamps per workgroup)",
+             f"# command: {command}",
+             f"# wall clock {khz} kHz; per launch: entry spread = last - first workgroup entry; per-workgroup "
+             "phases load+stats (entry -> slice statistics done), exchange (-> group statistics known), "
+             "store issue (-> stores issued), each median / max over workgroups; issued = first entry -> "
+             "last workgroup's stores issued; launch = HIP-event duration (includes the stores draining); "
+             f"medians over {iters} launches; copy = torch copy of the same bytes (events)",
+             f"# {'config':18s} {'variant':15s} {'wgs':>4} {'spread':>7} {'load+stats':>12} {'exchange':>12} "
+             f"{'store issue':>12} {'issued':>7} {'launch':>7} {'copy':>6}   (us)"]
+    try:
+        for label, shape, eps, silu, vn in GN_PROBE:
+            g = _gen(1003)
+            C = shape[1]
+            x = torch.randn(*shape, generator=g).to(torch.bfloat16).to(dev)
+            gm = (1 + 0.1 * torch.randn(C, generator=g)).to(torch.bfloat16).to(dev)
+            bt = (0.1 * torch.randn(C, generator=g)).to(torch.bfloat16).to(dev)
+            out = torch.empty_like(x)
+            vi = names.index(vn)
+            nat.group_norm(x, 32, gm, bt, eps, silu=silu, variant=vi, out=out)
+            torch.cuda.synchronize()
+            rows = []
+            for _ in range(iters):
+                words.zero_()
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                nat.group_norm(x, 32, gm, bt, eps, silu=silu, variant=vi, out=out)
+                b.record()
+                torch.cuda.synchronize()
+                t = words.view(-1, 4).cpu()
+                t = t[t[:, 0] != 0].double()
+                if t.shape[0] == 0:
+                    raise RuntimeError(f"{label}: no stamps (the variant did not take the resident kernel)")
+                t0 = float(t[:, 0].min())
+                ph = [(t[:, 1] - t[:, 0]) * us, (t[:, 2] - t[:, 1]) * us, (t[:, 3] - t[:, 2]) * us]
+                rows.append((t.shape[0], (float(t[:, 0].max()) - t0) * us,
+                             [(float(p.median()), float(p.max())) for p in ph],
+                             (float(t[:, 3].max()) - t0) * us, a.elapsed_time(b) * 1e3))
+            med = lambda f: statistics.median(f(r) for r in rows)  # noqa: E731
+            copy_us = []
+            for _ in range(iters):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                out.copy_(x)
+                b.record()
+                torch.cuda.synchronize()
+                copy_us.append(a.elapsed_time(b) * 1e3)
+            phases = "".join(f" {med(lambda r, i=i: r[2][i][0]):5.2f} / {med(lambda r, i=i: r[2][i][1]):4.2f}"
+                             for i in range(3))
+            lines.append(f"  {label:18s} {vn:15s} {rows[0][0]:4d} {med(lambda r: r[1]):7.2f}{phases} "
+                         f"{med(lambda r: r[3]):7.2f} {med(lambda r: r[4]):7.2f} {statistics.median(copy_us):6.2f}")
+            log(lines[-1])
+    finally:
+        nat.group_norm_trace(None)
+    with open(out_path, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    print("\n".join(lines))
+
+
 def _dispatch_counter(run_dir: str, counter: str, needle: str) -> "list[tuple[int, str, float]]":
     """(dispatch id, kernel name, value) of `counter` for the dispatches whose kernel name
     contains `needle`, in dispatch order."""
@@ -1307,6 +1462,12 @@ def main():
                     help="PMC_DIR [PMC_DIR ...] OUT: unit-busy / stall summary of --conv-probe passes")
     ap.add_argument("--summarize-mfma", nargs=2, metavar=("PMC_DIR", "OUT"),
                     help="write the MFMA utilisation summary from a rocprofv3 --pmc output folder")
+    ap.add_argument("--gn-cl-probe", action="store_true",
+                    help="run only the workload of the channels-last GroupNorm traffic passes (GN_CL_PROBE)")
+    ap.add_argument("--summarize-gn-cl-traffic", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "OUT"),
+                    help="write the channels-last GroupNorm traffic summary from the two rocprofv3 --pmc folders")
+    ap.add_argument("--gn-phase-probe", metavar="OUT",
+                    help="write the per-phase timeline of the resident GroupNorm kernels (GN_PROBE) to OUT")
     ap.add_argument("--gn-probe", action="store_true",
                     help="run only the workload of the GroupNorm traffic passes (GN_PROBE kernels)")
     ap.add_argument("--summarize-gn-traffic", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "OUT"),
@@ -1326,6 +1487,9 @@ def main():
         return
     if args.summarize_gn_traffic:
         summarize_gn_traffic(*args.summarize_gn_traffic, args.command)
+        return
+    if args.summarize_gn_cl_traffic:
+        summarize_gn_cl_traffic(*args.summarize_gn_cl_traffic, args.command)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; the hot path has no multi-GPU component "
@@ -1347,6 +1511,12 @@ def main():
         return
     if args.gn_probe:
         gn_probe()
+        return
+    if args.gn_cl_probe:
+        gn_cl_probe()
+        return
+    if args.gn_phase_probe:
+        gn_phase_probe(args.gn_phase_probe, args.command)
         return
 
     # ---- headline: causal depthwise conv1d bf16 (config 2) --------------------------

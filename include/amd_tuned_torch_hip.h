@@ -271,6 +271,13 @@ int atk_group_norm_fwd(const void* x, const void* gamma, const void* beta, void*
                        int64_t N, int64_t C, int64_t S, int G, float eps, int fuse_silu,
                        int dtype, int param_dtype, int variant, void* workspace,
                        size_t workspace_bytes, atk_stream_t stream);
+/* Diagnostics, no counterpart in the reference (its group_norm.cu has no phase timing):
+ * register a device buffer of n_words 64-bit words (NULL / 0 drops it); every later
+ * register-resident launch (res_* variants) with at most n_words / 4 workgroups stores, per
+ * workgroup w, four wall-clock stamps at words 4w..4w+3: entry, slice statistics done (all its
+ * loads arrived), group statistics known (after the exchange between workgroups), stores issued.
+ * Returns the wall-clock rate in kHz (0 on error).  Process-wide; not for concurrent use. */
+int atk_group_norm_trace(void* device_words, int64_t n_words);
 
 /* ---------------------------------------------------------------------------
  * GroupNorm forward that allocates nothing and takes no workspace.  No counterpart in the

@@ -40,7 +40,8 @@ EXPORTED_SYMBOLS = (
     "atk_dwconv1d_cl_bwd_weight", "atk_causal_conv1d_cl_bwd_workspace_bytes", "atk_causal_conv1d_cl_bwd",
     "atk_dwconv1d_cl_bwd_workspace_bytes", "atk_dwconv1d_cl_bwd",
     "atk_group_norm_workspace_bytes",
-    "atk_group_norm_workspace_zero_bytes", "atk_group_norm_fwd", "atk_group_norm_cl_workspace_bytes",
+    "atk_group_norm_workspace_zero_bytes", "atk_group_norm_fwd", "atk_group_norm_trace",
+    "atk_group_norm_cl_workspace_bytes",
     "atk_group_norm_cl_fwd", "atk_group_norm_bwd_workspace_bytes",
     "atk_group_norm_bwd", "atk_conv_workspace_bytes",
     "atk_conv_fwd", "atk_conv_wgrad_workspace_bytes", "atk_conv_wgrad", "atk_transpose_last2",
@@ -153,6 +154,8 @@ def _declare(lib) -> None:
     lib.atk_transpose_last2.restype = i32
     lib.atk_dwconv1d_bwd.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i32, i32, i64, i32, vp, sz, vp]
     lib.atk_dwconv1d_bwd.restype = i32
+    lib.atk_group_norm_trace.argtypes = [vp, i64]
+    lib.atk_group_norm_trace.restype = i32
     lib.atk_group_norm_noalloc_scratch_bytes.argtypes = []
     lib.atk_group_norm_noalloc_scratch_bytes.restype = sz
     lib.atk_group_norm_fwd_noalloc.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, c.c_float, i32, i32, i32,
@@ -1277,6 +1280,17 @@ def conv_group_norm_wait_error(device: Optional[torch.device] = None) -> bool:
     with _ws_lock:
         bufs = [b for (d, _, p), b in _ws_live.items() if d == idx and p == "conv_gn_onepass"]
     return any(int(b[:4].view(torch.int32).item()) != 0 for b in bufs)
+
+
+def group_norm_trace(words: Optional[torch.Tensor]) -> int:
+    """Diagnostics: register an int64 device tensor that later register-resident GroupNorm
+    launches fill with four wall-clock stamps per workgroup (entry, slice statistics done, group
+    statistics known, stores issued); None drops it.  Returns the wall-clock rate in kHz."""
+    if words is None:
+        return int(lib().atk_group_norm_trace(None, 0))
+    if words.dtype != torch.int64 or not words.is_cuda or not words.is_contiguous():
+        raise RuntimeError("group_norm_trace: a contiguous int64 CUDA tensor")
+    return int(lib().atk_group_norm_trace(_ptr(words), words.numel()))
 
 
 def group_norm_apply(x: torch.Tensor, num_groups: int, weight: Optional[torch.Tensor], bias: Optional[torch.Tensor],

@@ -88,7 +88,18 @@ struct GnArgs {
   float* partials;    // workspace: [ngroups][NS][2] (mean, M2) (two-pass)
   float4* parts;      // split kernels: [ngroups][NP] records (count, mean, M2, -)
   int NP;             // records per group
+  uint64_t* trace;    // resident kernel, diagnostics: [workgroup][4] wall-clock stamps, or null
 };
+
+// Phase trace of the register-resident kernel (atk_group_norm_trace): thread 0 of every
+// workgroup stamps the wall clock at entry, when its slice statistics are done (all its loads
+// have arrived), when the group statistics are known (after the exchange) and when its stores
+// are issued.  A process-wide registration read at launch; null = off.
+uint64_t* g_gn_trace = nullptr;
+int64_t g_gn_trace_words = 0;
+__device__ __forceinline__ void gn_stamp(const GnArgs& a, int k) {
+  if (a.trace && threadIdx.x == 0) a.trace[(int64_t)blockIdx.x * 4 + k] = wall_clock64();
+}
 
 __device__ __forceinline__ int64_t slice_len(int i, int64_t slice, int64_t E) {
   return (int64_t)(i + 1) * slice <= E ? slice : E - (int64_t)i * slice;
@@ -262,6 +273,7 @@ void gn_resident_kernel(GnArgs a) {
   const int64_t s0 = (int64_t)s * a.slice;
   const T* __restrict__ xg = static_cast<const T*>(a.x) + gi * E;
   T* __restrict__ yg = static_cast<T*>(a.y) + gi * E;
+  gn_stamp(a, 0);
 
   // All EPV loads in flight at once, branch-free: one lane offset (tid*16 B) plus a
   // uniform SGPR offset per vector; lanes past the group take an out-of-range offset and
@@ -293,6 +305,7 @@ void gn_resident_kernel(GnArgs a) {
 
   float mean_l, m2;
   slice_stats<T, NT, EPV, true>(buf, xg, s0, E, a.slice, red, mean_l, m2);
+  gn_stamp(a, 1);
   if (staged) {
     if (tid < nch) {
       aff[tid] = a.gamma ? param_decode(gword, gsel, a.pdt) : 1.f;
@@ -379,6 +392,7 @@ void gn_resident_kernel(GnArgs a) {
     var = s_stat[1];
   }
   const float rstd = 1.0f / sqrtf(var + a.eps);
+  gn_stamp(a, 2);
 
   if (staged) {
     for (int i = tid; i < nch; i += NT) {  // the entries this thread fetched above
@@ -416,6 +430,7 @@ void gn_resident_kernel(GnArgs a) {
       }
     }
   }
+  gn_stamp(a, 3);
   if (a.NS > 1 && tid < 64) {
     // This workgroup is done with the slots (every read of them returned before the barrier
     // above) and its publish completed: count it, after its stores are issued, so that the
@@ -805,6 +820,7 @@ int launch_resident_s(GnArgs a, int64_t ngroups, hipStream_t s) {
       return fail(ATK_UNSUPPORTED, "group_norm: %lld workgroups exceed the %lld that can be resident",
                   (long long)nblk, (long long)cap);
   }
+  a.trace = g_gn_trace && nblk * 4 <= g_gn_trace_words ? g_gn_trace : nullptr;
   hipLaunchKernelGGL(kern, dim3((unsigned)nblk), dim3(NT), 0, s, a);
   return check_launch("gn_resident_kernel");
 }
@@ -1835,8 +1851,12 @@ __device__ __forceinline__ void cl_collect(const GnClResArgs& a, int n, int ch, 
   }
 }
 
-template <typename T, int NT, int EPV, bool SILU>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(EPV <= 16 ? 4 : 1)))
+// WPE: waves per SIMD the build is sized for.  At 4 (two workgroups per CU, for grids up to
+// twice the CU count) the 16-vector build fits 128 VGPRs only by spilling about ten of them to
+// scratch, which costs HBM traffic; grids of at most one workgroup per CU take the 2-wave build,
+// which holds everything in registers.
+template <typename T, int NT, int EPV, bool SILU, int WPE = 4>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE)))
 void gn_cl_resident_kernel(GnClResArgs a) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int NW = NT / 64;
@@ -1953,10 +1973,14 @@ void gn_cl_resident_kernel(GnClResArgs a) {
     sh[k] = shs[v * VEC + k];
   }
   T* __restrict__ yc = static_cast<T*>(a.y) + ((int64_t)n * a.S + (int64_t)ch * a.SC) * a.C;
+  // (indices from an opaque copy of tid: the statistics phase's `i * NT + tid` would otherwise
+  // be kept for the stores, and at four waves per SIMD those are the values that spill)
+  int tid_s = tid;
+  asm volatile("" : "+v"(tid_s));
 #pragma unroll
   for (int i = 0; i < EPV; ++i) {
     reg_fence<T, 1>(&buf[i]);
-    const int e = i * NT + tid;
+    const int e = i * NT + tid_s;
     if (e < nv) {
       float o[VEC];
 #pragma unroll
@@ -2046,7 +2070,10 @@ bool plan_gn_cl_res(int64_t N, int64_t C, int64_t S, int G, int force_epv, GnClR
 template <typename T>
 int launch_gn_cl_res(const GnClResArgs& a, const GnClResPlan& p, int64_t N, int silu, hipStream_t s) {
   const dim3 grid((unsigned)(N * p.NCH)), block(p.nt);
-  if (p.epv == 16) {
+  if (p.epv == 16 && (int64_t)grid.x <= device_cu_count()) {
+    if (silu) hipLaunchKernelGGL((gn_cl_resident_kernel<T, 512, 16, true, 2>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((gn_cl_resident_kernel<T, 512, 16, false, 2>), grid, block, 0, s, a);
+  } else if (p.epv == 16) {
     if (silu) hipLaunchKernelGGL((gn_cl_resident_kernel<T, 512, 16, true>), grid, block, 0, s, a);
     else hipLaunchKernelGGL((gn_cl_resident_kernel<T, 512, 16, false>), grid, block, 0, s, a);
   } else {
@@ -2928,6 +2955,7 @@ int gn_fwd(const void* x, const void* gamma, const void* beta, void* y, int64_t 
   const int vec = (int)(16 / es);
   const bool vec_ok = (S % vec == 0) && aligned16(x) && aligned16(y);
   GnArgs a;
+  a.trace = nullptr;
   a.x = x; a.gamma = gamma; a.beta = beta; a.y = y;
   a.E = (C / G) * S;
   a.S = (uint32_t)S;
@@ -2962,6 +2990,16 @@ int gn_fwd(const void* x, const void* gamma, const void* beta, void* y, int64_t 
 
 }  // namespace
 }  // namespace atk
+
+// Diagnostics: register (or, with NULL, drop) a device buffer of n_words 64-bit words that
+// later register-resident launches fill with per-workgroup phase stamps; returns the wall-clock
+// rate in kHz that converts them.
+extern "C" int atk_group_norm_trace(void* device_words, int64_t n_words) {
+  using namespace atk;
+  g_gn_trace = device_words && n_words > 0 ? static_cast<uint64_t*>(device_words) : nullptr;
+  g_gn_trace_words = g_gn_trace ? n_words : 0;
+  return device_wall_clock_khz();
+}
 
 extern "C" int atk_group_norm_fwd(const void* x, const void* gamma, const void* beta, void* y,
                                   int64_t N, int64_t C, int64_t S, int G, float eps, int fuse_silu,
