@@ -253,8 +253,8 @@ def _conv_candidates(fn, input, weight, bias, stride, padding, dilation) -> list
 def _run_named_native(name: str, fn: Callable, op: int, *args, **kwargs):
     """Run cached winner `name` ("native.<variant>"); None if it declines or is unknown."""
     try:
-        idx = _variants(op).index(name[len(_NATIVE_PREFIX):])
-    except ValueError:
+        idx = _native.variant_index(op, name[len(_NATIVE_PREFIX):])
+    except RuntimeError:
         return None
     try:
         return fn(*args, variant=idx, **kwargs)
@@ -651,7 +651,8 @@ def _group_norm_channels_last(input, num_groups, weight, bias, eps, orig):
 
 def _group_norm_accelerated_forward(input, num_groups, weight, bias, eps):
     orig = _STOCK_F["group_norm"]
-    if isinstance(input, torch.Tensor) and _channels_last(input):
+    channels_last = isinstance(input, torch.Tensor) and _channels_last(input)
+    if channels_last:
         return _group_norm_channels_last(input, num_groups, weight, bias, eps, orig)
     if not (isinstance(input, torch.Tensor) and input.dim() >= 2 and input.is_contiguous()
             and _usable(input, dtypes=_GROUPNORM_DTYPES)
@@ -661,7 +662,6 @@ def _group_norm_accelerated_forward(input, num_groups, weight, bias, eps):
         if _DEBUG:
             _debug("group_norm", "stock", "layout/dtype outside this tier", input=input)
         return orig(input, num_groups, weight, bias, eps)
-    channels_last = _channels_last(input)
     if kernel_select.enabled():
         key = (input.dtype, tuple(input.shape), int(num_groups), channels_last)
         won = kernel_select.cached_key("group_norm", key)

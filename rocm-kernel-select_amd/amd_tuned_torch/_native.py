@@ -50,7 +50,55 @@ EXPORTED_SYMBOLS = (
     "atk_conv_fwd_prepacked", "atk_conv_fwd_prepacked_cl", "atk_conv_gn_stats_bytes", "atk_conv_gn_records",
     "atk_conv_fwd_prepacked_ex", "atk_conv_gn_onepass_workspace_bytes", "atk_conv_group_norm_fwd",
     "atk_group_norm_apply", "atk_group_norm_cl_bwd_workspace_bytes", "atk_group_norm_cl_bwd",
+    "atk_dwconv1d_fwd_args", "atk_group_norm_fwd_args", "atk_conv_fwd_prepacked_args",
 )
+
+
+# Argument blocks of the *_args entry points (include/amd_tuned_torch_hip.h): the fields of
+# atk_dwconv1d_fwd, atk_group_norm_fwd and atk_conv_fwd_prepacked, in order.  ctypes converts
+# every argument of a call (about 0.1 us apiece); a block is filled once per shape and only its
+# pointer fields change between calls.  One block per thread (ctypes releases the GIL during
+# the call, so a block shared between threads could change under a running call).
+class _DwArgs(ctypes.Structure):
+    _fields_ = [("x", ctypes.c_void_p), ("w", ctypes.c_void_p), ("bias", ctypes.c_void_p), ("y", ctypes.c_void_p),
+                ("N", ctypes.c_int64), ("C", ctypes.c_int64), ("L", ctypes.c_int64), ("K", ctypes.c_int),
+                ("pad_left", ctypes.c_int), ("L_out", ctypes.c_int64), ("dtype", ctypes.c_int),
+                ("w_dtype", ctypes.c_int), ("fuse_silu", ctypes.c_int), ("variant", ctypes.c_int),
+                ("stream", ctypes.c_void_p)]
+
+
+class _GnArgs(ctypes.Structure):
+    _fields_ = [("x", ctypes.c_void_p), ("gamma", ctypes.c_void_p), ("beta", ctypes.c_void_p), ("y", ctypes.c_void_p),
+                ("N", ctypes.c_int64), ("C", ctypes.c_int64), ("S", ctypes.c_int64), ("G", ctypes.c_int),
+                ("eps", ctypes.c_float), ("fuse_silu", ctypes.c_int), ("dtype", ctypes.c_int),
+                ("param_dtype", ctypes.c_int), ("variant", ctypes.c_int), ("workspace", ctypes.c_void_p),
+                ("workspace_bytes", ctypes.c_size_t), ("stream", ctypes.c_void_p)]
+
+
+_CONV_GEOM_FIELDS = ("N", "Ci", "D", "H", "W", "Co", "KD", "KH", "KW", "sd", "sh", "sw", "pd", "ph", "pw",
+                     "dd", "dh", "dw")
+
+
+class _ConvArgs(ctypes.Structure):
+    _fields_ = ([("x", ctypes.c_void_p), ("packed", ctypes.c_void_p), ("packed_bytes", ctypes.c_size_t),
+                 ("bias", ctypes.c_void_p), ("y", ctypes.c_void_p)]
+                + [(f, ctypes.c_int64) for f in _CONV_GEOM_FIELDS[:6]]
+                + [(f, ctypes.c_int) for f in _CONV_GEOM_FIELDS[6:]]
+                + [("dtype", ctypes.c_int), ("variant", ctypes.c_int), ("workspace", ctypes.c_void_p),
+                   ("workspace_bytes", ctypes.c_size_t), ("stream", ctypes.c_void_p)])
+
+
+_tls = threading.local()
+
+
+def _block(kind: str, cls):
+    """This thread's argument block of `kind`: [struct, its address, the static fields' key]."""
+    blk = getattr(_tls, kind, None)
+    if blk is None:
+        st = cls()
+        blk = [st, ctypes.addressof(st), None]
+        setattr(_tls, kind, blk)
+    return blk
 
 
 class Unsupported(RuntimeError):
@@ -161,6 +209,9 @@ def _declare(lib) -> None:
     lib.atk_group_norm_fwd_noalloc.argtypes = [vp, vp, vp, vp, i64, i64, i64, i32, c.c_float, i32, i32, i32,
                                                i32, vp]
     lib.atk_group_norm_fwd_noalloc.restype = i32
+    for name in ("atk_dwconv1d_fwd_args", "atk_group_norm_fwd_args", "atk_conv_fwd_prepacked_args"):
+        getattr(lib, name).argtypes = [vp]
+        getattr(lib, name).restype = i32
 
 
 def load(path: str = LIB_PATH):
@@ -357,11 +408,12 @@ def dwconv1d(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]
              l_out: int, *, silu: bool = False, variant: int = -1,
              out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """y[n,c,t] = bias[c] + sum_j weight[c,j] * x[n,c,t-pad_left+j], t < l_out (x = 0
-    outside [0, L)).  x [N,C,L] contiguous, weight [C,K] (squeezed depthwise kernel); weight
-    and bias in x's dtype or, both, in fp32 (used unrounded)."""
+    outside [0, L)).  x [N,C,L] contiguous, weight [C,K] (squeezed depthwise kernel) or the
+    depthwise conv's own [C,1,K], which has the same memory; weight and bias in x's dtype or,
+    both, in fp32 (used unrounded)."""
     _require_cuda(x, weight, bias)
-    if x.dim() != 3 or weight.dim() != 2:
-        raise RuntimeError("dwconv1d expects x [N, C, L] and weight [C, K]")
+    if x.dim() != 3 or not (weight.dim() == 2 or (weight.dim() == 3 and weight.shape[1] == 1)):
+        raise RuntimeError("dwconv1d expects x [N, C, L] and weight [C, K] or [C, 1, K]")
     N, C, L = x.shape
     if weight.shape[0] != C:
         raise RuntimeError("dwconv1d: weight.shape[0] must equal channels")
@@ -375,12 +427,20 @@ def dwconv1d(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor]
         raise RuntimeError("dwconv1d: x must be contiguous")
     weight = weight.contiguous()
     bias = bias.contiguous() if bias is not None else None
-    K = weight.shape[1]
+    K = weight.shape[-1]
     y = out if out is not None else torch.empty((N, C, l_out), dtype=x.dtype, device=x.device)
-    rc = lib().atk_dwconv1d_fwd(_ptr(x), _ptr(weight), _ptr(bias), _ptr(y), N, C, L, K, pad_left,
-                                l_out, _DTYPE_CODE[x.dtype], _DTYPE_CODE[weight.dtype], int(bool(silu)), variant,
-                                _stream(x))
-    _check(rc, "dwconv1d")
+    L_ = lib()
+    blk = _block("dw", _DwArgs)
+    a = blk[0]
+    key = (N, C, L, K, pad_left, l_out, x.dtype, weight.dtype, bool(silu), variant)
+    if blk[2] != key:
+        a.N, a.C, a.L, a.K, a.pad_left, a.L_out = N, C, L, K, pad_left, l_out
+        a.dtype, a.w_dtype = _DTYPE_CODE[x.dtype], _DTYPE_CODE[weight.dtype]
+        a.fuse_silu, a.variant = int(bool(silu)), int(variant)
+        blk[2] = key
+    a.x, a.w, a.bias, a.y = x.data_ptr(), weight.data_ptr(), _ptr(bias), y.data_ptr()
+    a.stream = _stream(x)
+    _check(L_.atk_dwconv1d_fwd_args(blk[1]), "dwconv1d")
     return y
 
 
@@ -790,10 +850,16 @@ def group_norm(input: torch.Tensor, num_groups: int, weight: Optional[torch.Tens
         _check(rc if rc != ATK_OK else ATK_EINVAL, "group_norm")
     stream = _raw_stream(input.device)
     ws = workspace(input.device, "group_norm", nbytes, stream)
-    rc = L.atk_group_norm_fwd(_ptr(input), _ptr(weight), _ptr(bias), _ptr(y), N, C, S, G,
-                              float(eps), int(bool(silu)), dt, pdt, v, ws.data_ptr(), ws.numel(),
-                              stream)
-    _check(rc, "group_norm")
+    blk = _block("gn", _GnArgs)
+    a = blk[0]
+    key = (N, C, S, G, float(eps), bool(silu), dt, pdt, v)
+    if blk[2] != key:
+        a.N, a.C, a.S, a.G, a.eps = N, C, S, G, float(eps)
+        a.fuse_silu, a.dtype, a.param_dtype, a.variant = int(bool(silu)), dt, pdt, v
+        blk[2] = key
+    a.x, a.gamma, a.beta, a.y = input.data_ptr(), _ptr(weight), _ptr(bias), y.data_ptr()
+    a.workspace, a.workspace_bytes, a.stream = ws.data_ptr(), ws.numel(), stream
+    _check(L.atk_group_norm_fwd_args(blk[1]), "group_norm")
     return y
 
 
@@ -1047,6 +1113,49 @@ def _packed_conv_weights(weight: torch.Tensor, geom: tuple, dt: int, variant: in
     return packed
 
 
+# Per-shape conv plans: (output shape, geometry, dtype code, packed-weight bytes, split-K
+# workspace bytes) for (nd, input and weight shapes, dtype, stride, padding, dilation, variant,
+# device).  Derived from hashable arguments only; a call whose stride / padding / dilation is
+# unhashable (a list) is planned without the memo.
+_conv_plans: dict = {}
+_CONV_PLANS_MAX = 1024
+
+
+def _conv_plan(L, input, weight, stride, padding, dilation, nd: int, variant: int, dev: int) -> tuple:
+    try:
+        key = (nd, input.shape, weight.shape, input.dtype, stride, padding, dilation, variant, dev)
+        plan = _conv_plans.get(key)
+    except TypeError:
+        key, plan = None, None
+    if plan is not None:
+        return plan
+    s, p, d = _ntuple(stride, nd), _ntuple(padding, nd), _ntuple(dilation, nd)
+    N, Ci = input.shape[:2]
+    Co = weight.shape[0]
+    if nd == 2:
+        D, (H, W) = 1, input.shape[2:]
+        KD, (KH, KW) = 1, weight.shape[2:]
+        s, p, d = (1,) + s, (0,) + p, (1,) + d
+    else:
+        D, H, W = input.shape[2:]
+        KD, KH, KW = weight.shape[2:]
+    osz = [conv_out_size(i, k, ss, pp, dd)
+           for i, k, ss, pp, dd in zip((D, H, W), (KD, KH, KW), s, p, d)]
+    if min(osz) <= 0:
+        raise RuntimeError("Conv output size must be positive")
+    shape = (N, Co, *osz) if nd == 3 else (N, Co, osz[1], osz[2])
+    dt = _DTYPE_CODE[input.dtype]
+    geom = tuple(int(v) for v in (N, Ci, D, H, W, Co, KD, KH, KW, *s, *p, *d))
+    packed_bytes = int(L.atk_conv_packed_weight_bytes(*geom, dt, variant)) if variant > 0 else 0
+    nws = int(L.atk_conv_prepacked_workspace_bytes(*geom, dt, variant)) if packed_bytes else 0
+    plan = (shape, geom, dt, packed_bytes, nws)
+    if key is not None:
+        if len(_conv_plans) >= _CONV_PLANS_MAX:
+            _conv_plans.clear()
+        _conv_plans[key] = plan
+    return plan
+
+
 def _conv(input, weight, bias, stride, padding, dilation, nd: int, variant: int,
           out: Optional[torch.Tensor] = None, residual: Optional[torch.Tensor] = None, gn_groups: int = 0):
     """y = conv(input, weight) + bias (+ residual).  With gn_groups > 0 the MFMA epilogue also
@@ -1067,21 +1176,10 @@ def _conv(input, weight, bias, stride, padding, dilation, nd: int, variant: int,
         if bias.numel() != weight.shape[0] or bias.dtype != input.dtype:
             raise RuntimeError("Bias shape/dtype mismatch")
         bias = bias.contiguous()
-    s, p, d = _ntuple(stride, nd), _ntuple(padding, nd), _ntuple(dilation, nd)
-    N, Ci = input.shape[:2]
-    Co = weight.shape[0]
-    if nd == 2:
-        D, (H, W) = 1, input.shape[2:]
-        KD, (KH, KW) = 1, weight.shape[2:]
-        s, p, d = (1,) + s, (0,) + p, (1,) + d
-    else:
-        D, H, W = input.shape[2:]
-        KD, KH, KW = weight.shape[2:]
-    osz = [conv_out_size(i, k, ss, pp, dd)
-           for i, k, ss, pp, dd in zip((D, H, W), (KD, KH, KW), s, p, d)]
-    if min(osz) <= 0:
-        raise RuntimeError("Conv output size must be positive")
-    shape = (N, Co, *osz) if nd == 3 else (N, Co, osz[1], osz[2])
+    L = lib()
+    dev = _device_index(input.device)
+    shape, geom, dt, packed_bytes, nws = _conv_plan(L, input, weight, stride, padding, dilation, nd,
+                                                    int(variant), dev)
     y = out if out is not None else torch.empty(shape, dtype=input.dtype, device=input.device)
     extras = residual is not None or gn_groups > 0
     if residual is not None and (tuple(residual.shape) != tuple(shape) or residual.dtype != input.dtype
@@ -1089,12 +1187,6 @@ def _conv(input, weight, bias, stride, padding, dilation, nd: int, variant: int,
         raise RuntimeError("conv residual must be a contiguous tensor of the output's shape and dtype")
     if y.numel() == 0 and not extras:
         return y
-    L = lib()
-    dt = _DTYPE_CODE[input.dtype]
-    geom = (N, Ci, D, H, W, Co, KD, KH, KW, *s, *p, *d)
-    dev = _device_index(input.device)
-    packed_bytes = _cached_size(L.atk_conv_packed_weight_bytes, *geom, dt, int(variant), device=dev) \
-        if variant > 0 else 0
     if extras and not packed_bytes:
         raise Unsupported(f"conv{nd}d: the residual / GroupNorm epilogue needs an MFMA variant that takes the shape")
     if packed_bytes:
@@ -1102,12 +1194,19 @@ def _conv(input, weight, bias, stride, padding, dilation, nd: int, variant: int,
         # only for split-K partials
         stream = _raw_stream(input.device)
         packed = _packed_conv_weights(weight, geom, dt, int(variant), packed_bytes, stream)
-        nws = _cached_size(L.atk_conv_prepacked_workspace_bytes, *geom, dt, int(variant), device=dev)
         ws = workspace(input.device, "conv", nws, stream) if nws else None
         if not extras:
-            rc = L.atk_conv_fwd_prepacked(_ptr(input), _ptr(packed), packed_bytes, _ptr(bias), _ptr(y), *geom, dt,
-                                          int(variant), _ptr(ws), ws.numel() if ws is not None else 0, stream)
-            _check(rc, f"conv{nd}d")
+            blk = _block("conv", _ConvArgs)
+            a = blk[0]
+            if blk[2] is not geom:
+                for f, v in zip(_CONV_GEOM_FIELDS, geom):
+                    setattr(a, f, v)
+                a.packed_bytes, a.dtype, a.variant = packed_bytes, dt, int(variant)
+                blk[2] = geom
+            a.x, a.packed, a.bias, a.y = input.data_ptr(), packed.data_ptr(), _ptr(bias), y.data_ptr()
+            a.workspace, a.workspace_bytes = (ws.data_ptr(), ws.numel()) if ws is not None else (None, 0)
+            a.stream = stream
+            _check(L.atk_conv_fwd_prepacked_args(blk[1]), f"conv{nd}d")
             return y
         stats, nrec = None, 0
         if gn_groups > 0:

@@ -282,8 +282,9 @@ def _norm(v):
 
 def _key(kind, input, weight, stride, padding, dilation):
     # memory format is part of the identity (kernel_select.py:438-445)
-    channels_last = (input.is_contiguous(memory_format=torch.channels_last)
-                     or input.is_contiguous(memory_format=torch.channels_last_3d))
+    nd = input.dim()
+    channels_last = ((nd == 4 and input.is_contiguous(memory_format=torch.channels_last))
+                     or (nd == 5 and input.is_contiguous(memory_format=torch.channels_last_3d)))
     return (kind, input.dtype, tuple(input.shape), tuple(weight.shape), _norm(stride),
             _norm(padding), _norm(dilation), channels_last)
 

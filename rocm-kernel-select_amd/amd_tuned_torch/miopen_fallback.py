@@ -196,7 +196,8 @@ class _DwConv1dFn(torch.autograd.Function):
 
 def _dw_call(input, weight, bias, pad_left, l_out, variant):
     if _grad_safe(input, weight, bias):
-        return _native.dwconv1d(input, weight.squeeze(1), bias, pad_left, l_out, variant=variant)
+        # the [C, 1, K] weight as it is: the same memory as [C, K]
+        return _native.dwconv1d(input, weight, bias, pad_left, l_out, variant=variant)
     return _DwConv1dFn.apply(input, weight, bias, pad_left, l_out, variant)
 
 
@@ -240,10 +241,13 @@ def _try_depthwise_fastpath(input, weight, bias, stride, padding, dilation, grou
         if won == "stock":
             return orig_fn(input, weight, bias, stride, padding, dilation, groups)
         if won is not None and won.startswith("native."):
-            names = _native.variants(_native.OP_DWCONV1D)
-            if won[7:] in names:
+            try:
+                vi = _native.variant_index(_native.OP_DWCONV1D, won[7:])
+            except RuntimeError:
+                vi = None
+            if vi is not None:
                 try:
-                    return _dw_call(input, weight, bias, pad_left, l_out, names.index(won[7:]))
+                    return _dw_call(input, weight, bias, pad_left, l_out, vi)
                 except _native.Unsupported:
                     pass
         candidates = _dw_candidates(input, weight, bias, pad_left, l_out)

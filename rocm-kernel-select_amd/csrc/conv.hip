@@ -269,3 +269,10 @@ extern "C" int atk_conv_fwd_prepacked_ex(const void* x, const void* packed, size
                                   reinterpret_cast<hipStream_t>(stream), residual, gn_stats, gn_stats_bytes,
                                   gn_stats ? gn_groups : 0);
 }
+
+extern "C" int atk_conv_fwd_prepacked_args(const atk_conv_prepacked_args* a) {
+  if (!a) return atk::fail(ATK_EINVAL, "conv: null argument block");
+  return atk_conv_fwd_prepacked(a->x, a->packed, a->packed_bytes, a->bias, a->y, a->N, a->Ci, a->D, a->H, a->W, a->Co,
+                                a->KD, a->KH, a->KW, a->sd, a->sh, a->sw, a->pd, a->ph, a->pw, a->dd, a->dh, a->dw,
+                                a->dtype, a->variant, a->workspace, a->workspace_bytes, a->stream);
+}

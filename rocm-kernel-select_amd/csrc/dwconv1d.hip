@@ -1373,3 +1373,9 @@ extern "C" int atk_causal_conv1d_bwd(const void* x, const void* dout, const void
                      a.part, dw, db, (int)B, (int)D, K);
   return check_launch("dwconv1d_bwd_finalize_kernel");
 }
+
+extern "C" int atk_dwconv1d_fwd_args(const atk_dwconv1d_args* a) {
+  if (!a) return atk::fail(ATK_EINVAL, "dwconv1d: null argument block");
+  return atk_dwconv1d_fwd(a->x, a->w, a->bias, a->y, a->N, a->C, a->L, a->K, a->pad_left, a->L_out, a->dtype,
+                          a->w_dtype, a->fuse_silu, a->variant, a->stream);
+}

@@ -1852,9 +1852,9 @@ __device__ __forceinline__ void cl_collect(const GnClResArgs& a, int n, int ch, 
 }
 
 // WPE: waves per SIMD the build is sized for.  At 4 (two workgroups per CU, for grids up to
-// twice the CU count) the 16-vector build fits 128 VGPRs only by spilling about ten of them to
-// scratch, which costs HBM traffic; grids of at most one workgroup per CU take the 2-wave build,
-// which holds everything in registers.
+// twice the CU count) the 16-vector build fits 128 VGPRs only by spilling two dwords to scratch;
+// grids of at most one workgroup per CU take the 2-wave build, which holds everything in
+// registers (no scratch traffic).
 template <typename T, int NT, int EPV, bool SILU, int WPE = 4>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(WPE)))
 void gn_cl_resident_kernel(GnClResArgs a) {
@@ -2067,10 +2067,29 @@ bool plan_gn_cl_res(int64_t N, int64_t C, int64_t S, int G, int force_epv, GnClR
   return true;
 }
 
+// Whether both 2-wave builds fit one workgroup per CU (checked once per device): grids of at
+// most one workgroup per CU are then resident at once with either build.
+template <typename T>
+bool gn_cl_res_two_wave_ok() {
+  static int ok[64] = {0};  // 0 unknown, 1 yes, -1 no
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  if (ok[dev] == 0) {
+    int a = 0, b = 0;
+    const bool q =
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &a, reinterpret_cast<const void*>(gn_cl_resident_kernel<T, 512, 16, true, 2>), 512, 0) == hipSuccess &&
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &b, reinterpret_cast<const void*>(gn_cl_resident_kernel<T, 512, 16, false, 2>), 512, 0) == hipSuccess;
+    ok[dev] = (q && a >= 1 && b >= 1) ? 1 : -1;
+  }
+  return ok[dev] > 0;
+}
+
 template <typename T>
 int launch_gn_cl_res(const GnClResArgs& a, const GnClResPlan& p, int64_t N, int silu, hipStream_t s) {
   const dim3 grid((unsigned)(N * p.NCH)), block(p.nt);
-  if (p.epv == 16 && (int64_t)grid.x <= device_cu_count()) {
+  if (p.epv == 16 && (int64_t)grid.x <= device_cu_count() && gn_cl_res_two_wave_ok<T>()) {
     if (silu) hipLaunchKernelGGL((gn_cl_resident_kernel<T, 512, 16, true, 2>), grid, block, 0, s, a);
     else hipLaunchKernelGGL((gn_cl_resident_kernel<T, 512, 16, false, 2>), grid, block, 0, s, a);
   } else if (p.epv == 16) {
@@ -3402,4 +3421,10 @@ extern "C" int atk_group_norm_cl_bwd(const void* x, const void* dy, const void* 
     case ATK_F16: return launch_gn_cl_bwd<_Float16>(a, s);
     default: return launch_gn_cl_bwd<__bf16>(a, s);
   }
+}
+
+extern "C" int atk_group_norm_fwd_args(const atk_group_norm_args* a) {
+  if (!a) return atk::fail(ATK_EINVAL, "group_norm: null argument block");
+  return atk_group_norm_fwd(a->x, a->gamma, a->beta, a->y, a->N, a->C, a->S, a->G, a->eps, a->fuse_silu, a->dtype,
+                            a->param_dtype, a->variant, a->workspace, a->workspace_bytes, a->stream);
 }

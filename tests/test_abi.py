@@ -167,3 +167,53 @@ def test_conv_wgrad_workspace_query_declines_unserved_shapes(nat):
     assert L.atk_conv_wgrad_workspace_bytes(2, 16, 6, 16, 16, 128, 3) == 0    # Ci = 16
     assert L.atk_conv_wgrad_workspace_bytes(1, 32, 4, 8, 80, 128, 3) == 0     # W > 64
     assert L.atk_conv_wgrad_workspace_bytes(1, 256, 8, 64, 64, 256, 3) > 0
+
+
+def test_argument_block_layouts_match_the_header(nat, tmp_path):
+    """The ctypes mirrors of atk_dwconv1d_args / atk_group_norm_args / atk_conv_prepacked_args
+    have the C compiler's size and field offsets (a C program compiled against the header
+    prints them)."""
+    blocks = {"atk_dwconv1d_args": nat._DwArgs, "atk_group_norm_args": nat._GnArgs,
+              "atk_conv_prepacked_args": nat._ConvArgs}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void) {"]
+    for cname, cls in blocks.items():
+        lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
+        for f, _ in cls._fields_:
+            lines.append(f'  printf("{cname} {f} %zu\\n", offsetof({cname}, {f}));')
+    lines.append("  return 0;\n}")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-O0", str(src), "-o", str(exe)], check=True)
+    got = subprocess.run([str(exe)], check=True, stdout=subprocess.PIPE, text=True).stdout.split("\n")
+    want = []
+    for cname, cls in blocks.items():
+        want.append(f"{cname} size {ctypes.sizeof(cls)}")
+        want += [f"{cname} {f} {getattr(cls, f).offset}" for f, _ in cls._fields_]
+    assert [g for g in got if g] == want
+
+
+def test_argument_blocks_validate_like_their_entry_points(nat):
+    """The block forms run the same checks as the positional entry points (no GPU needed:
+    every case is rejected, or is empty, before anything is launched)."""
+    lib = nat.lib()
+    assert lib.atk_dwconv1d_fwd_args(None) == nat.ATK_EINVAL
+    assert lib.atk_group_norm_fwd_args(None) == nat.ATK_EINVAL
+    assert lib.atk_conv_fwd_prepacked_args(None) == nat.ATK_EINVAL
+    cases = [  # (N, C, L, K, pad_left, L_out, dtype, w_dtype, silu, variant)
+        (1, 1, 1, 3, 1, 1, 7, 7, 0, 0), (1, 4, 16, 65, 1, 16, 0, 0, 0, 0), (1, 4, 16, 3, 65, 16, 0, 0, 0, 0),
+        (1, 4, 16, 3, 1, 16, 0, 0, 0, 99), (1, 4, 16, 3, 1, 16, 0, 0, 0, 0), (0, 4, 16, 3, 1, 16, 0, 0, 0, 0)]
+    for N, C, L, K, pl, lo, dt, wdt, silu, v in cases:
+        a = nat._DwArgs(None, None, None, None, N, C, L, K, pl, lo, dt, wdt, silu, v, None)
+        assert lib.atk_dwconv1d_fwd_args(ctypes.addressof(a)) == \
+            lib.atk_dwconv1d_fwd(None, None, None, None, N, C, L, K, pl, lo, dt, wdt, silu, v, None)
+    for G, dt in ((3, 0), (4, 9), (0, 0)):
+        g = nat._GnArgs(None, None, None, None, 2, 8, 16, G, 1e-5, 0, dt, 0, -1, None, 0, None)
+        assert lib.atk_group_norm_fwd_args(ctypes.addressof(g)) == \
+            lib.atk_group_norm_fwd(None, None, None, None, 2, 8, 16, G, ctypes.c_float(1e-5), 0, dt, 0, -1,
+                                   None, 0, None)
+    geom = (1, 8, 4, 8, 8, 8, 3, 3, 3, 1, 1, 1, 1, 1, 1, 1, 1, 1)
+    for dt, v in ((9, 1), (0, 0), (0, 10 ** 6)):
+        c = nat._ConvArgs(None, None, 0, None, None, *geom, dt, v, None, 0, None)
+        assert lib.atk_conv_fwd_prepacked_args(ctypes.addressof(c)) == \
+            lib.atk_conv_fwd_prepacked(None, None, 0, None, None, *geom, dt, v, None, 0, None)
