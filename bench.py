@@ -1030,6 +1030,14 @@ def gn_probe(iters: int = 10):
 
 # channels-last GroupNorm kernels profiled by --gn-cl-probe: (label, NC[D]HW shape, silu, pass);
 # bf16, G = 32, eps 1e-5; a backward call is two dispatches (resident kernel, rows finalize)
+# channels-last single-pass kernel in both chunk shapes (phase probe)
+GN_CL_PHASE = [
+    ("C3a NHWC rows", (8, 512, 64, 64), False, "rows"),
+    ("C3a NHWC blocks", (8, 512, 64, 64), False, "blocks"),
+    ("C3b NDHWC rows", (1, 512, 16, 64, 64), False, "rows"),
+    ("C3b NDHWC blocks", (1, 512, 16, 64, 64), False, "blocks"),
+]
+
 GN_CL_PROBE = [
     ("C3a NHWC bf16", (8, 512, 64, 64), False, "fwd"),
     ("C3a NHWC bf16 +SiLU", (8, 512, 64, 64), True, "fwd"),
@@ -1134,23 +1142,34 @@ def gn_phase_probe(out_path: str, command: str, iters: int = 20):
              f"medians over {iters} launches; copy = torch copy of the same bytes (events)",
              f"# {'config':18s} {'variant':15s} {'wgs':>4} {'spread':>7} {'load+stats':>12} {'exchange':>12} "
              f"{'store issue':>12} {'issued':>7} {'launch':>7} {'copy':>6}   (us)"]
+    # NC[S] cases (variant named), then channels-last cases (chunk shape named: the
+    # single-pass kernel's `rows` or `blocks` layout)
+    cases = [(label, shape, eps, silu, vn, None) for label, shape, eps, silu, vn in GN_PROBE]
+    cases += [(label, shape, 1e-5, silu, layout, layout) for label, shape, silu, layout in GN_CL_PHASE]
     try:
-        for label, shape, eps, silu, vn in GN_PROBE:
+        for label, shape, eps, silu, vn, layout in cases:
             g = _gen(1003)
             C = shape[1]
             x = torch.randn(*shape, generator=g).to(torch.bfloat16).to(dev)
+            if layout is not None:
+                x = x.contiguous(memory_format=torch.channels_last if x.dim() == 4 else torch.channels_last_3d)
             gm = (1 + 0.1 * torch.randn(C, generator=g)).to(torch.bfloat16).to(dev)
             bt = (0.1 * torch.randn(C, generator=g)).to(torch.bfloat16).to(dev)
             out = torch.empty_like(x)
-            vi = names.index(vn)
-            nat.group_norm(x, 32, gm, bt, eps, silu=silu, variant=vi, out=out)
+            if layout is None:
+                vi = names.index(vn)
+                call = lambda: nat.group_norm(x, 32, gm, bt, eps, silu=silu, variant=vi, out=out)  # noqa: E731
+            else:
+                os.environ["ATK_GN_CL_LAYOUT"] = layout
+                call = lambda: nat.group_norm_cl(x, 32, gm, bt, eps, silu=silu, out=out)  # noqa: E731
+            call()
             torch.cuda.synchronize()
             rows = []
             for _ in range(iters):
                 words.zero_()
                 a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 a.record()
-                nat.group_norm(x, 32, gm, bt, eps, silu=silu, variant=vi, out=out)
+                call()
                 b.record()
                 torch.cuda.synchronize()
                 t = words.view(-1, 4).cpu()
@@ -1178,6 +1197,7 @@ def gn_phase_probe(out_path: str, command: str, iters: int = 20):
             log(lines[-1])
     finally:
         nat.group_norm_trace(None)
+        os.environ.pop("ATK_GN_CL_LAYOUT", None)
     with open(out_path, "w") as f:
         f.write("\n".join(lines) + "\n")
     print("\n".join(lines))

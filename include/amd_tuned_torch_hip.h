@@ -273,7 +273,8 @@ int atk_group_norm_fwd(const void* x, const void* gamma, const void* beta, void*
                        size_t workspace_bytes, atk_stream_t stream);
 /* Diagnostics, no counterpart in the reference (its group_norm.cu has no phase timing):
  * register a device buffer of n_words 64-bit words (NULL / 0 drops it); every later
- * register-resident launch (res_* variants) with at most n_words / 4 workgroups stores, per
+ * register-resident launch (res_* variants of atk_group_norm_fwd, and the single-pass kernel
+ * of atk_group_norm_cl_fwd) with at most n_words / 4 workgroups stores, per
  * workgroup w, four wall-clock stamps at words 4w..4w+3: entry, slice statistics done (all its
  * loads arrived), group statistics known (after the exchange between workgroups), stores issued.
  * Returns the wall-clock rate in kHz (0 on error).  Process-wide; not for concurrent use. */

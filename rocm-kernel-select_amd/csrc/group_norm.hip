@@ -1624,11 +1624,17 @@ struct GnClResArgs {
   int64_t S;            // positions per sample
   int SC, NCH;          // positions per chunk (EPV * R), chunks per sample
   int C, G, cpg;
+  int CW, NB, GW;       // 16-byte columns per workgroup, channel blocks (C / VEC / CW), groups per block
   int two_level;
   int pdt;
   float eps;
   uint64_t wait_ticks;  // longest a workgroup waits, in total, for other workgroups' slots
+  uint64_t* trace;      // diagnostics: [workgroup][4] wall-clock stamps, or null
 };
+
+__device__ __forceinline__ void gn_stamp(const GnClResArgs& a, int k) {
+  if (a.trace && threadIdx.x == 0) a.trace[(int64_t)blockIdx.x * 4 + k] = wall_clock64();
+}
 
 __device__ __forceinline__ int cl_chunk_positions(const GnClResArgs& a, int c) {
   const int64_t left = a.S - (int64_t)c * a.SC;
@@ -1638,6 +1644,13 @@ __device__ __forceinline__ int cl_chunk_positions(const GnClResArgs& a, int c) {
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t cl_chunk_rsrc(const GnClResArgs& a, int n, int c, int es) {
   const char* base = static_cast<const char*>(a.x) + (((int64_t)n * a.S + (int64_t)c * a.SC) * a.C) * es;
   return make_rsrc(base, (uint32_t)((int64_t)cl_chunk_positions(a, c) * a.C * es));
+}
+
+// Byte offset, inside its chunk, of this thread's first vector (row tid / CW, column tid % CW
+// of channel block b); vector i lies i * R rows further (R = NT / CW).
+__device__ __forceinline__ uint32_t cl_lane_off(const GnClResArgs& a, int tid, int b, int es) {
+  const int row = tid / a.CW, col = tid - row * a.CW;
+  return (uint32_t)(row * a.C * es + (b * a.CW + col) * 16);
 }
 
 // Sum of v over the M consecutive threads of this thread's segment (M a power of two, segments
@@ -1667,18 +1680,19 @@ __device__ __forceinline__ float seg_sum(float v, int M, float* red) {
 // on memory, with the same operations in the same order: the results are bit-identical.
 // Ends with the records visible to the whole workgroup.
 template <typename T, int NT, int EPV, bool FROM_REG>
-__device__ __forceinline__ void cl_chunk_stats(Vec16<T>* buf, __amdgpu_buffer_rsrc_t rx, int P, const GnClResArgs& a,
-                                               float* en, float* em, float* eq, float* red, float* rm, float* rq) {
+__device__ __forceinline__ void cl_chunk_stats(Vec16<T>* buf, __amdgpu_buffer_rsrc_t rx, int P, int b,
+                                               const GnClResArgs& a, float* en, float* em, float* eq, float* red,
+                                               float* rm, float* rq) {
   constexpr int VEC = 16 / sizeof(T);
   const int tid = threadIdx.x;
-  const int CV = a.C / VEC;
-  const int nv = P * CV;  // vectors of the chunk
+  const int CW = a.CW, R = NT / CW;
+  const int row = tid / CW;
   auto get = [&](int i) -> Vec16<T> {
     if constexpr (FROM_REG) {
       return buf[i];
     } else {
       Vec16<T> v;
-      v.raw = bload16(rx, (uint32_t)tid * 16u, (uint32_t)(i * NT * 16));
+      v.raw = bload16(rx, cl_lane_off(a, tid, b, (int)sizeof(T)), (uint32_t)(i * R * a.C * (int)sizeof(T)));
       return v;
     }
   };
@@ -1686,7 +1700,7 @@ __device__ __forceinline__ void cl_chunk_stats(Vec16<T>* buf, __amdgpu_buffer_rs
   float s1 = 0.f, s2 = 0.f;
   int nvt = 0;
   auto acc = [&](int i) {
-    const bool ok = i * NT + tid < nv;
+    const bool ok = i * R + row < P;
     const float Ki = ok ? K : 0.f;
     if constexpr (FROM_REG)
       asm volatile("" : "+v"(buf[i].raw.x), "+v"(buf[i].raw.y), "+v"(buf[i].raw.z), "+v"(buf[i].raw.w),
@@ -1718,11 +1732,12 @@ __device__ __forceinline__ void cl_chunk_stats(Vec16<T>* buf, __amdgpu_buffer_rs
   em[tid] = mean_t;
   eq[tid] = m2_t;
   __syncthreads();
-  // Thread t takes entry j = t % M of group g = t / M (M = NT / G: G divides CV = C / VEC,
-  // a power of two dividing NT), entry j being row j / cpv, column g * cpv + j % cpv.
-  const int cpv = a.cpg / VEC, M = NT / a.G;
+  // Thread t takes entry j = t % M of the workgroup's group g = t / M (M = NT / GW: GW groups
+  // of cpv columns tile the CW columns, a power of two dividing NT), entry j being row j / cpv,
+  // column g * cpv + j % cpv.
+  const int cpv = a.cpg / VEC, M = NT / a.GW;
   const int g = tid / M, j = tid - (tid / M) * M;
-  const int e = (j / cpv) * CV + g * cpv + (j - (j / cpv) * cpv);
+  const int e = (j / cpv) * CW + g * cpv + (j - (j / cpv) * cpv);
   const float ne = en[e], me = em[e], qe = eq[e];
   const float n = seg_sum<NT>(ne, M, red);
   const float mean = seg_sum<NT>(ne * me, M, red) / n;
@@ -1775,7 +1790,8 @@ __device__ __forceinline__ void write_slot(GnSlot* sl, uint32_t tag, float m, fl
 // tag or the workgroup's deadline passes; a chunk with a record still missing is then
 // computed from x by the whole workgroup (cl_chunk_stats on memory) and its records filled in.
 template <typename T, int NT, int EPV, int RPT, typename GR, typename CR>
-__device__ __forceinline__ void cl_collect(const GnClResArgs& a, int n, int ch, uint32_t tag, uint64_t deadline, int nrec,
+__device__ __forceinline__ void cl_collect(const GnClResArgs& a, int n, int b, int ch, uint32_t tag, uint64_t deadline,
+                                           int nrec,
                                            GR gr, CR cr, float* tm, float* tq, const float* rm, const float* rq,
                                            float* en, float* em, float* eq, float* red, float* xm, float* xq, int* s_flag,
                                            int* s_list, int* s_cnt) {
@@ -1787,8 +1803,8 @@ __device__ __forceinline__ void cl_collect(const GnClResArgs& a, int n, int ch, 
     need[k] = false;
     if (r < nrec) {
       if (cr(r) == ch) {
-        tm[r] = rm[gr(r)];
-        tq[r] = rq[gr(r)];
+        tm[r] = rm[gr(r) - b * a.GW];
+        tq[r] = rq[gr(r) - b * a.GW];
       } else {
         need[k] = true;
       }
@@ -1830,17 +1846,18 @@ __device__ __forceinline__ void cl_collect(const GnClResArgs& a, int n, int ch, 
     if (tid == 0) __hip_atomic_store(a.hdr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     for (int m = 0; m < nmiss; ++m) {
       const int c = s_list[m];
-      cl_chunk_stats<T, NT, EPV, false>(nullptr, cl_chunk_rsrc(a, n, c, (int)sizeof(T)), cl_chunk_positions(a, c), a,
-                                        en, em, eq, red, xm, xq);
+      cl_chunk_stats<T, NT, EPV, false>(nullptr, cl_chunk_rsrc(a, n, c, (int)sizeof(T)), cl_chunk_positions(a, c), b,
+                                        a, en, em, eq, red, xm, xq);
       for (int r = tid; r < nrec; r += NT)
         if (cr(r) == c) {
-          tm[r] = xm[gr(r)];
-          tq[r] = xq[gr(r)];
+          tm[r] = xm[gr(r) - b * a.GW];
+          tq[r] = xq[gr(r) - b * a.GW];
         }
       // Publish every group's record of the stand-in chunk (the owner, when it runs, writes
       // the same bits: same loads, same order of operations): a later collect for another
       // group then finds them in the slots instead of reading the chunk from x again.
-      for (int g = tid; g < a.G; g += NT) write_slot(&a.slots[((int64_t)n * a.G + g) * a.NCH + c], tag, xm[g], xq[g]);
+      for (int g = tid; g < a.GW; g += NT)
+        write_slot(&a.slots[((int64_t)n * a.G + b * a.GW + g) * a.NCH + c], tag, xm[g], xq[g]);
       __threadfence();
       __syncthreads();
     }
@@ -1877,22 +1894,39 @@ void gn_cl_resident_kernel(GnClResArgs a) {
   float* tq = big + GN_CLR_DIRECT;
 
   const int tid = threadIdx.x;
-  const int n = blockIdx.x / a.NCH, ch = blockIdx.x - (blockIdx.x / a.NCH) * a.NCH;
-  const int CV = a.C / VEC;
+  // workgroup -> (sample n, channel block b, chunk ch), chunks fastest
+  const int per_n = a.NB * a.NCH;
+  const int n = blockIdx.x / per_n, rem = blockIdx.x - (blockIdx.x / per_n) * per_n;
+  const int b = rem / a.NCH, ch = rem - (rem / a.NCH) * a.NCH;
+  const int CW = a.CW, R = NT / CW;
+  const int CB = CW * VEC;  // channels of the block, the first being c0
+  const int c0 = b * CB, g0 = b * a.GW;
   const int P = cl_chunk_positions(a, ch);
-  const int nv = P * CV;
+  gn_stamp(a, 0);
 
-  // The epoch and gamma / beta first, then every x load of the chunk, branch-free.  Vector
-  // loads complete in issue order, so staging gamma / beta in LDS waits for them alone.
-  const uint32_t epoch = __hip_atomic_load(a.hdr + 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  for (int c = tid; c < a.C; c += NT) {
-    gam[c] = a.gamma ? load_param(a.gamma, a.pdt, c) : 1.f;
-    bet[c] = a.beta ? load_param(a.beta, a.pdt, c) : 0.f;
-  }
+  // Every x load of the chunk first, branch-free; then the epoch and gamma / beta, with
+  // unconditional buffer loads that nothing waits for until the chunk's statistics are done
+  // (loads complete in issue order: waiting for a parameter load issued before x would hold
+  // back every x load behind its round trip).
   const __amdgpu_buffer_rsrc_t rx = cl_chunk_rsrc(a, n, ch, (int)sizeof(T));
+  const uint32_t lane_off = cl_lane_off(a, tid, b, (int)sizeof(T));
+  const uint32_t row_step = (uint32_t)(R * a.C * (int)sizeof(T));  // bytes between a thread's vectors
   Vec16<T> buf[EPV];
 #pragma unroll
-  for (int i = 0; i < EPV; ++i) buf[i].raw = bload16<2>(rx, (uint32_t)tid * 16u, (uint32_t)(i * NT * 16));
+  for (int i = 0; i < EPV; ++i) buf[i].raw = bload16<2>(rx, lane_off, (uint32_t)i * row_step);
+  const uint32_t epoch = __hip_atomic_load(a.hdr + 16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  constexpr int PPT = (GN_CL_MAXC + NT - 1) / NT;  // parameters per thread, at most
+  uint32_t gword[PPT], bword[PPT], gsel[PPT], bsel[PPT];
+#pragma unroll
+  for (int k = 0; k < PPT; ++k) {
+    gword[k] = bword[k] = gsel[k] = bsel[k] = 0;
+    if (k == 0 || CB > k * NT) {  // uniform
+      const int c = tid + k * NT;
+      const int64_t ci = c0 + (c < CB ? c : 0);
+      gword[k] = param_word(a.gamma, a.pdt, ci, a.C, gsel[k]);
+      bword[k] = param_word(a.beta, a.pdt, ci, a.C, bsel[k]);
+    }
+  }
   if (tid == 0) {
     s_cnt = 0;
     // the record sets this workgroup merges: all groups (-1, direct) or its own group
@@ -1903,10 +1937,21 @@ void gn_cl_resident_kernel(GnClResArgs a) {
   }
   for (int c = tid; c < GN_CLR_MAXNCH; c += NT) s_flag[c] = 0;
 
-  cl_chunk_stats<T, NT, EPV, true>(buf, rx, P, a, en, em, eq, s_red, rm, rq);
+  cl_chunk_stats<T, NT, EPV, true>(buf, rx, P, b, a, en, em, eq, s_red, rm, rq);
   reg_fence<T, EPV>(buf);
+  gn_stamp(a, 1);
+  // (gam / bet are read only after the exchange's barriers)
+#pragma unroll
+  for (int k = 0; k < PPT; ++k) {
+    const int c = tid + k * NT;
+    if (c < CB) {
+      gam[c] = a.gamma ? param_decode(gword[k], gsel[k], a.pdt) : 1.f;
+      bet[c] = a.beta ? param_decode(bword[k], bsel[k], a.pdt) : 0.f;
+    }
+  }
   const uint32_t tag = (epoch << 1) | 1u;
-  for (int g = tid; g < a.G; g += NT) write_slot(&a.slots[((int64_t)n * a.G + g) * a.NCH + ch], tag, rm[g], rq[g]);
+  for (int g = tid; g < a.GW; g += NT)
+    write_slot(&a.slots[((int64_t)n * a.G + g0 + g) * a.NCH + ch], tag, rm[g], rq[g]);
   const uint64_t deadline = wall_clock64() + a.wait_ticks;
 
   GnSlot* fin = a.finals + (int64_t)n * a.G;
@@ -1915,13 +1960,14 @@ void gn_cl_resident_kernel(GnClResArgs a) {
   for (int k = 0;;) {
     if (k < s_gcnt) {  // uniform: LDS read after a barrier
       const int gf = s_glist[k++];
-      cl_collect<T, NT, EPV, RPT>(a, n, ch, tag, deadline, gf < 0 ? a.G * NCH : NCH,
-                                  [&](int r) { return gf < 0 ? r / NCH : gf; },
+      cl_collect<T, NT, EPV, RPT>(a, n, b, ch, tag, deadline, gf < 0 ? a.GW * NCH : NCH,
+                                  [&](int r) { return gf < 0 ? g0 + r / NCH : gf; },
                                   [&](int r) { return gf < 0 ? r - (r / NCH) * NCH : r; }, tm, tq, rm, rq, en, em,
                                   eq, s_red, xm, xq, s_flag, s_list, &s_cnt);
       __syncthreads();
       const int w = tid >> 6;
-      for (int g = gf < 0 ? w : (w == 0 ? gf : a.G); g < (gf < 0 ? a.G : gf + 1); g += NW) {
+      // direct: the block's GW groups (local indices); two-level (one block, g0 = 0): group gf
+      for (int g = gf < 0 ? w : (w == 0 ? gf : a.GW); g < (gf < 0 ? a.GW : gf + 1); g += NW) {
         float mean, var;
         cl_merge_group(a, gf < 0 ? tm + g * NCH : tm, gf < 0 ? tq + g * NCH : tq, mean, var);
         if ((tid & 63) == 0) {
@@ -1954,10 +2000,11 @@ void gn_cl_resident_kernel(GnClResArgs a) {
     }
     __syncthreads();
   }
-  // per-channel scale / shift (over the record table, no longer needed)
+  gn_stamp(a, 2);
+  // per-channel scale / shift of the block (over the record table, no longer needed)
   float* scs = big;
   float* shs = big + GN_CL_MAXC;
-  for (int c = tid; c < a.C; c += NT) {
+  for (int c = tid; c < CB; c += NT) {
     const int g = c / a.cpg;
     const float rstd = 1.0f / sqrtf(gv[g] + a.eps);
     const float sc = rstd * gam[c];
@@ -1965,7 +2012,7 @@ void gn_cl_resident_kernel(GnClResArgs a) {
     shs[c] = bet[c] - gm[g] * sc;
   }
   __syncthreads();
-  const int v = tid % CV;
+  const int v = tid % CW;
   float sc[VEC], sh[VEC];
 #pragma unroll
   for (int k = 0; k < VEC; ++k) {
@@ -1973,24 +2020,26 @@ void gn_cl_resident_kernel(GnClResArgs a) {
     sh[k] = shs[v * VEC + k];
   }
   T* __restrict__ yc = static_cast<T*>(a.y) + ((int64_t)n * a.S + (int64_t)ch * a.SC) * a.C;
-  // (indices from an opaque copy of tid: the statistics phase's `i * NT + tid` would otherwise
-  // be kept for the stores, and at four waves per SIMD those are the values that spill)
+  // (indices from an opaque copy of tid: the statistics phase's per-vector offsets would
+  // otherwise be kept for the stores, and at four waves per SIMD those are the values that spill)
   int tid_s = tid;
   asm volatile("" : "+v"(tid_s));
+  const int row_s = tid_s / CW;
+  const int lane_e = row_s * a.C + c0 + (tid_s - row_s * CW) * VEC;  // element offset of vector 0
 #pragma unroll
   for (int i = 0; i < EPV; ++i) {
     reg_fence<T, 1>(&buf[i]);
-    const int e = i * NT + tid_s;
-    if (e < nv) {
+    if (i * R + row_s < P) {
       float o[VEC];
 #pragma unroll
       for (int k = 0; k < VEC; ++k) {
         o[k] = fmaf(to_f32(buf[i].e[k]), sc[k], sh[k]);
         if constexpr (SILU) o[k] = silu_f32(o[k]);
       }
-      st16<true>(yc + (int64_t)e * VEC, pack16<T>(o));
+      st16<true>(yc + lane_e + (int64_t)i * R * a.C, pack16<T>(o));
     }
   }
+  gn_stamp(a, 3);
   // Done with the slots (every read above has returned): count this workgroup in its block
   // of GN_CLR_BLOCK; the block's last counts the block in the launch, and the launch's last
   // advances the epoch.  Each counter is reset by the workgroup that completes it.  Counting
@@ -2012,6 +2061,7 @@ void gn_cl_resident_kernel(GnClResArgs a) {
 
 struct GnClResPlan {
   int nt, epv, NCH, SC, two_level;
+  int CW, NB;  // 16-byte columns per workgroup, channel blocks per sample
 };
 
 // The register-resident configuration for a channels-last shape, or false.  Left to itself
@@ -2022,8 +2072,20 @@ struct GnClResPlan {
 // `force_epv` (8 or 16) takes that configuration wherever it fits.  Two-level whenever there
 // are at least as many chunks as groups (measured faster than every workgroup polling all
 // G x NCH records), else direct if G x NCH <= GN_CLR_DIRECT.
+//
+// Chunk shape.  `rows`: a chunk is SC whole positions (all C channels), and its records cover
+// every group, so a sample's statistics need the records of all its chunks (two-level or
+// direct).  `blocks`: a chunk is 8 columns (128 bytes of each position, whole groups) of
+// EPV * NT / 8 positions, so a workgroup merges only its block's groups over the sample's
+// chunks of that block -- one exchange round instead of two, over a few records.  Blocks are
+// taken where the groups tile 8 columns, C spans more than 8 and the rows grid would need more
+// than one workgroup per CU (measured, bf16, graph replay: C3b NDHWC 31.4 -> 27.6 us, +SiLU
+// 32.0 -> 30.2 us; on C3a NHWC, one rows workgroup per CU, blocks lose 17.8 -> 18.0 us and
+// +SiLU 17.8 -> 19.1 us: their 128-byte runs 1 KB apart load slower than whole 128 KB chunks,
+// which eats the saved round).  `layout` 1 / 2 forces rows / blocks (blocks only where they
+// apply).
 template <typename T>
-bool plan_gn_cl_res(int64_t N, int64_t C, int64_t S, int G, int force_epv, GnClResPlan& out);
+bool plan_gn_cl_res(int64_t N, int64_t C, int64_t S, int G, int force_epv, int layout, GnClResPlan& out);
 
 // Workgroups of the resident kernel that fit the GPU at once: the smaller of its two builds
 // (with and without SiLU), since either may be launched on the plan this capacity admits.
@@ -2046,20 +2108,44 @@ int64_t gn_cl_res_capacity() {
 }
 
 template <typename T>
-bool plan_gn_cl_res(int64_t N, int64_t C, int64_t S, int G, int force_epv, GnClResPlan& out) {
+bool plan_gn_cl_res(int64_t N, int64_t C, int64_t S, int G, int force_epv, int layout, GnClResPlan& out) {
   constexpr int VEC = 16 / sizeof(T);
   constexpr int NT = 512;
+  constexpr int BCOLS = 8;  // columns of a block: 128 bytes of a position
   const int64_t CV = C / VEC;
   if (C % VEC || (C / G) % VEC || C > GN_CL_MAXC || G > GN_CL_MAXG || NT % CV) return false;
   const int epv = force_epv ? force_epv : 16;
-  const int64_t sc = (int64_t)epv * (NT / CV);
-  const int64_t nch = (S + sc - 1) / sc;
-  if (nch > GN_CLR_MAXNCH || N * G * nch > GN_CLR_MAX_SLOTS || N * G > GN_CLR_MAX_FINALS) return false;
-  GnClResPlan p{NT, epv, (int)nch, (int)sc, 0};
-  if (nch >= G) p.two_level = 1;
-  else if (G * nch <= GN_CLR_DIRECT) p.two_level = 0;
-  else return false;
-  const int64_t nblk = N * nch;
+  const int64_t cpv = (C / G) / VEC;
+  const int64_t rows_grid = N * ((S + (int64_t)epv * (NT / CV) - 1) / ((int64_t)epv * (NT / CV)));
+  const bool blocks_fit = CV > BCOLS && CV % BCOLS == 0 && BCOLS % cpv == 0 &&
+                          (layout == 2 || rows_grid > device_cu_count());
+  GnClResPlan p{NT, epv, 0, 0, 0, (int)CV, 1};
+  int64_t nch = 0;
+  bool ok = false;
+  if (blocks_fit && layout != 1) {
+    const int64_t sc = (int64_t)epv * (NT / BCOLS);
+    nch = (S + sc - 1) / sc;
+    const int64_t gw = G / (CV / BCOLS);
+    if (nch <= GN_CLR_MAXNCH && N * G * nch <= GN_CLR_MAX_SLOTS && gw * nch <= GN_CLR_DIRECT) {
+      p.CW = BCOLS;
+      p.NB = (int)(CV / BCOLS);
+      p.SC = (int)sc;
+      p.NCH = (int)nch;
+      p.two_level = 0;
+      ok = true;
+    }
+  }
+  if (!ok) {
+    const int64_t sc = (int64_t)epv * (NT / CV);
+    nch = (S + sc - 1) / sc;
+    if (nch > GN_CLR_MAXNCH || N * G * nch > GN_CLR_MAX_SLOTS || N * G > GN_CLR_MAX_FINALS) return false;
+    p.SC = (int)sc;
+    p.NCH = (int)nch;
+    if (nch >= G) p.two_level = 1;
+    else if (G * nch <= GN_CLR_DIRECT) p.two_level = 0;
+    else return false;
+  }
+  const int64_t nblk = N * p.NB * nch;
   const int64_t cap = epv == 16 ? gn_cl_res_capacity<T, NT, 16>() : gn_cl_res_capacity<T, NT, 8>();
   if (nblk > cap || nblk > (int64_t)GN_CLR_BLOCK * GN_CLR_MAXBLK) return false;
   if (!force_epv && nblk < device_cu_count()) return false;
@@ -2088,7 +2174,7 @@ bool gn_cl_res_two_wave_ok() {
 
 template <typename T>
 int launch_gn_cl_res(const GnClResArgs& a, const GnClResPlan& p, int64_t N, int silu, hipStream_t s) {
-  const dim3 grid((unsigned)(N * p.NCH)), block(p.nt);
+  const dim3 grid((unsigned)(N * p.NB * p.NCH)), block(p.nt);
   if (p.epv == 16 && (int64_t)grid.x <= device_cu_count() && gn_cl_res_two_wave_ok<T>()) {
     if (silu) hipLaunchKernelGGL((gn_cl_resident_kernel<T, 512, 16, true, 2>), grid, block, 0, s, a);
     else hipLaunchKernelGGL((gn_cl_resident_kernel<T, 512, 16, false, 2>), grid, block, 0, s, a);
@@ -2239,7 +2325,6 @@ constexpr int GN_CL_BWD_MNT = 1024;
 __global__ __launch_bounds__(GN_CL_BWD_MNT) void gn_cl_bwd_merge_kernel(GnClBwdArgs a) {
   __shared__ float red[GN_CL_BWD_MNT / 64];
   __shared__ float2 part_s[GN_CL_BWD_MNT];
-  __shared__ float s_stat[2];
   const int64_t ng = blockIdx.x;  // n * G + g
   const int n = (int)(ng / a.G);
   const uint32_t g = (uint32_t)(ng - (int64_t)n * a.G);
@@ -3289,15 +3374,17 @@ extern "C" int atk_group_norm_cl_fwd(const void* x, const void* gamma, const voi
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   // Register-resident single pass where the library's rule takes it (plan_gn_cl_res);
   // ATK_GN_CL_RESIDENT=0 turns it off, =8 / =16 takes that many vectors per thread wherever
-  // that configuration fits.
+  // that configuration fits; ATK_GN_CL_LAYOUT=rows / blocks forces the chunk shape.
   const char* renv = getenv("ATK_GN_CL_RESIDENT");
   const int rmode = renv ? atoi(renv) : 1;
   if (rmode != 0) {
     const int force = (rmode == 8 || rmode == 16) ? rmode : 0;
+    const char* lenv = getenv("ATK_GN_CL_LAYOUT");
+    const int layout = !lenv ? 0 : !strcmp(lenv, "rows") ? 1 : !strcmp(lenv, "blocks") ? 2 : 0;
     GnClResPlan rp;
-    const bool fits = dtype == ATK_F32   ? plan_gn_cl_res<float>(N, C, S, G, force, rp)
-                      : dtype == ATK_F16 ? plan_gn_cl_res<_Float16>(N, C, S, G, force, rp)
-                                         : plan_gn_cl_res<__bf16>(N, C, S, G, force, rp);
+    const bool fits = dtype == ATK_F32   ? plan_gn_cl_res<float>(N, C, S, G, force, layout, rp)
+                      : dtype == ATK_F16 ? plan_gn_cl_res<_Float16>(N, C, S, G, force, layout, rp)
+                                         : plan_gn_cl_res<__bf16>(N, C, S, G, force, layout, rp);
     if (fits) {
       GnClResArgs r;
       r.x = x; r.gamma = gamma; r.beta = beta; r.y = y;
@@ -3307,6 +3394,8 @@ extern "C" int atk_group_norm_cl_fwd(const void* x, const void* gamma, const voi
       r.finals = reinterpret_cast<GnSlot*>(ws + GN_CLR_FINALS_OFF);
       r.S = S; r.SC = rp.SC; r.NCH = rp.NCH;
       r.C = (int)C; r.G = G; r.cpg = (int)cpg;
+      r.CW = rp.CW; r.NB = rp.NB; r.GW = G / rp.NB;
+      r.trace = g_gn_trace && N * rp.NB * rp.NCH * 4 <= g_gn_trace_words ? g_gn_trace : nullptr;
       r.two_level = rp.two_level;
       r.pdt = param_dtype;
       r.eps = eps;

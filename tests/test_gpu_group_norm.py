@@ -509,7 +509,11 @@ def test_group_norm_channels_last(dev, shape_g, dtype):
 # every workgroup merges all G x NCH records (direct, at most 1024).  (2,256,100,130) bf16 has
 # 102 chunks of 128 positions per sample at 8 vectors per thread and 51 of 256 at 16 (both
 # two-level, a partial last chunk); (1,256,31,256) at 16 has 31 chunks of 32 groups (direct,
-# 992 records); (8,512,16,16) and (1,64,3,1000) are direct.
+# 992 records); (8,512,16,16) and (1,64,3,1000) are direct.  Those are the `rows` chunk shape
+# (all channels of SC positions); where the groups tile 8 columns (128 bytes of a position)
+# and C spans more, `blocks` chunks hold 8 columns of EPV * 64 positions and a workgroup
+# merges only its block's groups, in one round ((1,64,3,1000) in 16-bit types has only 8
+# columns and stays rows).
 CL_RES_CASES = [
     ((2, 256, 100, 130), 32, "8"),
     ((2, 256, 100, 130), 32, "16"),
@@ -521,16 +525,20 @@ CL_RES_CASES = [
 ]
 
 
+@pytest.mark.parametrize("layout", ["rows", "blocks"])
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
 @pytest.mark.parametrize("case", CL_RES_CASES, ids=lambda c: "x".join(map(str, c[0])) + f"_g{c[1]}_r{c[2]}")
-def test_group_norm_channels_last_resident(dev, case, dtype, monkeypatch):
-    """The channels-last forward in each register-resident configuration (and the
-    three-kernel path) against the oracle, with and without SiLU and affine parameters;
+def test_group_norm_channels_last_resident(dev, case, dtype, layout, monkeypatch):
+    """The channels-last forward in each register-resident configuration and chunk shape (and
+    the three-kernel path) against the oracle, with and without SiLU and affine parameters;
     repeated calls are bit-identical (the slot epoch advances between them) and no launch
     fell back to computing another workgroup's statistics."""
     shape, G, mode = case
+    if mode == "0" and layout == "blocks":
+        pytest.skip("the three-kernel path has no chunk shape")
     nat = _native()
     monkeypatch.setenv("ATK_GN_CL_RESIDENT", mode)
+    monkeypatch.setenv("ATK_GN_CL_LAYOUT", layout)
     fmt = torch.channels_last if len(shape) == 4 else torch.channels_last_3d
     for affine in (True, False):
         x, gm, bt = _inputs(shape, dtype, seed=len(shape) + G + int(mode) + 500, affine=affine)
@@ -548,16 +556,18 @@ def test_group_norm_channels_last_resident(dev, case, dtype, monkeypatch):
     assert not nat.group_norm_barrier_error(dev)
 
 
+@pytest.mark.parametrize("layout", ["rows", "blocks"])
 @pytest.mark.parametrize("shape,mode", [((1, 256, 65, 128), "8"), ((1, 256, 31, 256), "16")],
                          ids=["two_level", "direct"])
-def test_group_norm_channels_last_standin_bit_identical(dev, shape, mode, monkeypatch):
+def test_group_norm_channels_last_standin_bit_identical(dev, shape, mode, layout, monkeypatch):
     """With a zero wait, workgroups compute every chunk record (and, two-level, every group
     result) that is not yet published themselves; the outputs must equal the normal path's
-    byte for byte.  65 chunks x 32 groups at 8 vectors per thread (two-level); 31 x 32 at 16
-    (direct)."""
+    byte for byte.  Rows: 65 chunks x 32 groups at 8 vectors per thread (two-level); 31 x 32 at
+    16 (direct).  Blocks: 4 channel blocks of 8 groups, 17 / 8 chunks each."""
     nat = _native()
     G = 32
     monkeypatch.setenv("ATK_GN_CL_RESIDENT", mode)
+    monkeypatch.setenv("ATK_GN_CL_LAYOUT", layout)
     x, gm, bt = _inputs(shape, torch.bfloat16, seed=611)
     xd = x.to(dev).contiguous(memory_format=torch.channels_last)
     gd, bd = gm.to(dev), bt.to(dev)
@@ -574,8 +584,9 @@ def test_group_norm_channels_last_standin_bit_identical(dev, shape, mode, monkey
     _check(y1.cpu().contiguous(), x, G, gm, bt, 1e-5, silu=True, what="cl stand-in")
 
 
+@pytest.mark.parametrize("layout", ["rows", "blocks"])
 @pytest.mark.parametrize("mode", ["8", "16"])
-def test_group_norm_channels_last_graph_replay(dev, mode, monkeypatch):
+def test_group_norm_channels_last_graph_replay(dev, mode, layout, monkeypatch):
     """The resident channels-last forward captured in a HIP graph and replayed with new
     inputs copied in between (eager work and synchronisation between replays): every replay
     matches the eager result bit for bit -- the slot epoch lives in device memory, so a
@@ -583,6 +594,7 @@ def test_group_norm_channels_last_graph_replay(dev, mode, monkeypatch):
     nat = _native()
     shape, G = (2, 256, 100, 130), 32
     monkeypatch.setenv("ATK_GN_CL_RESIDENT", mode)
+    monkeypatch.setenv("ATK_GN_CL_LAYOUT", layout)
     data = [_inputs(shape, torch.bfloat16, seed=70 + i) for i in range(3)]
     gd, bd = data[0][1].to(dev), data[0][2].to(dev)
     xs = data[0][0].to(dev).contiguous(memory_format=torch.channels_last)
@@ -602,6 +614,25 @@ def test_group_norm_channels_last_graph_replay(dev, mode, monkeypatch):
         assert torch.equal(out, eager), f"replay {rep}"
     _check(out.cpu().contiguous(), data[5 % 3][0], G, data[0][1], data[0][2], 1e-5, what="cl graph replay")
     assert not nat.group_norm_barrier_error(dev)
+
+
+@pytest.mark.parametrize("silu", [False, True])
+@pytest.mark.parametrize("shape", [(8, 512, 64, 64), (1, 512, 16, 64, 64)], ids=["c3a_nhwc", "c3b_ndhwc"])
+def test_group_norm_channels_last_c3_full_size(dev, shape, silu):
+    """C3's shapes in channels-last memory at full size, bf16, on the library's own choice of
+    kernel and chunk shape: every element against the float64 oracle; a repeat is
+    bit-identical and no statistics were computed by a stand-in."""
+    nat = _native()
+    G = 32
+    x, gm, bt = _inputs(shape, torch.bfloat16, seed=3200 + len(shape))
+    fmt = torch.channels_last if len(shape) == 4 else torch.channels_last_3d
+    xd = x.to(dev).contiguous(memory_format=fmt)
+    y = nat.group_norm_cl(xd, G, gm.to(dev), bt.to(dev), 1e-5, silu=silu)
+    y2 = nat.group_norm_cl(xd, G, gm.to(dev), bt.to(dev), 1e-5, silu=silu)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2)
+    assert not nat.group_norm_barrier_error(dev)
+    _check(y.cpu().contiguous(), x, G, gm, bt, 1e-5, silu=silu, what=f"cl full size {shape}")
 
 
 @pytest.mark.parametrize("dtype", DTYPES, ids=lambda d: str(d).split(".")[-1])
