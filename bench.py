@@ -1485,7 +1485,7 @@ def main():
                     help="with --summarize-stats: keep only kernels whose names contain this")
     ap.add_argument("--summarize-stats", nargs=2, metavar=("STATS_DIR", "OUT"),
                     help="write a text summary of a rocprofv3 --kernel-trace --stats folder")
-    ap.add_argument("--variant", default="xlane,lds_opt32_nt",
+    ap.add_argument("--variant", default="xlane2_nt,lds_opt32_nt",
                     help="dwconv1d variants (comma-separated, one per kernel) for --traffic-probe")
     ap.add_argument("--command", default="", help="command line recorded by --summarize-traffic")
     ap.add_argument("--conv-probe", action="store_true",

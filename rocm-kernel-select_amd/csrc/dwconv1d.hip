@@ -545,14 +545,32 @@ __device__ __forceinline__ float win_elem(const uint32_t* D, int e) {
   }
 }
 
+// c + w.lo * x.lo + w.hi * x.hi for two packed 16-bit elements (v_dot2c_f32_{bf16,f16}): the
+// products of 16-bit values are exact in fp32.
+template <typename T>
+__device__ __forceinline__ float dot2_acc(uint32_t w, uint32_t x, float c) {
+  if constexpr (sizeof(T) == 2 && __is_same(T, __bf16)) {
+    typedef __bf16 p2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(p2, w), __builtin_bit_cast(p2, x), c, false);
+  } else {
+    typedef _Float16 p2 __attribute__((ext_vector_type(2)));
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(p2, w), __builtin_bit_cast(p2, x), c, false);
+  }
+}
+
 // Tail of the cross-lane kernel for a wave-uniform window offset M (the window's first
 // element is element M of block bA + lane).  Fixed per M: which neighbour blocks are
 // exchanged and which register holds each window element, so the window costs only its
 // conversions -- no per-lane selects or shifts.  The padding mask runs only in waves with
 // a lane at a row edge.
-template <typename T, int KT, bool NTH, bool SILU, int M>
+// DOT (16-bit x with weights of its own dtype): the window stays packed, two taps per
+// v_dot2c with the weight pair (w[j], w[j+1]) -- an element pair that starts at an odd
+// element is cut from two dwords with one v_alignbit -- and an odd last tap is an FMA on the
+// converted element: about half the VALU work of converting every element and four FMAs
+// per output.
+template <typename T, int KT, bool NTH, bool SILU, int M, bool DOT>
 __device__ __forceinline__ void xlane_tail(const uint4& E, const uint4& X, int lane, bool edge, int p0,
-                                           uint32_t L, const float* wk, float bv, T* dst) {
+                                           uint32_t L, const float* wk, const uint32_t* wp, float bv, T* dst) {
   using Win = DwWindow<T, KT>;
   constexpr int VEC = Win::VEC, WN = Win::WN;
   // lanes 0 and 1 stand in with the blocks past the wave, which lanes 62 and 63 need
@@ -574,21 +592,42 @@ __device__ __forceinline__ void xlane_tail(const uint4& E, const uint4& X, int l
   } else {
     D[8] = D[9] = D[10] = D[11] = 0u;
   }
-  float xv[WN];
-#pragma unroll
-  for (int i = 0; i < WN; ++i) xv[i] = win_elem<T>(D, M + i);
-  if (edge) {
-#pragma unroll
-    for (int i = 0; i < WN; ++i)
-      if ((unsigned)(p0 + i) >= L) xv[i] = 0.f;
-  }
   float acc[VEC];
+  if constexpr (DOT && sizeof(T) == 2) {
+    if (edge) {  // zero the halves that hold elements past a row edge
 #pragma unroll
-  for (int e = 0; e < VEC; ++e) {
-    acc[e] = bv;
+      for (int i = 0; i < WN; ++i)
+        if ((unsigned)(p0 + i) >= L) D[(M + i) >> 1] &= ((M + i) & 1) ? 0x0000ffffu : 0xffff0000u;
+    }
+    // elements s, s + 1 as one dword (s is a compile-time index here)
+    auto pair = [&](int s) -> uint32_t {
+      return (s & 1) ? __builtin_amdgcn_alignbit(D[(s >> 1) + 1], D[s >> 1], 16) : D[s >> 1];
+    };
 #pragma unroll
-    for (int j = 0; j < KT; ++j) acc[e] = fmaf(wk[j], xv[e + j], acc[e]);
-    if constexpr (SILU) acc[e] = silu_f32(acc[e]);
+    for (int e = 0; e < VEC; ++e) {
+      float c = bv;
+#pragma unroll
+      for (int j = 0; j + 1 < KT; j += 2) c = dot2_acc<T>(wp[j >> 1], pair(M + e + j), c);
+      if constexpr (KT & 1) c = fmaf(wk[KT - 1], win_elem<T>(D, M + e + KT - 1), c);
+      if constexpr (SILU) c = silu_f32(c);
+      acc[e] = c;
+    }
+  } else {
+    float xv[WN];
+#pragma unroll
+    for (int i = 0; i < WN; ++i) xv[i] = win_elem<T>(D, M + i);
+    if (edge) {
+#pragma unroll
+      for (int i = 0; i < WN; ++i)
+        if ((unsigned)(p0 + i) >= L) xv[i] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+      acc[e] = bv;
+#pragma unroll
+      for (int j = 0; j < KT; ++j) acc[e] = fmaf(wk[j], xv[e + j], acc[e]);
+      if constexpr (SILU) acc[e] = silu_f32(acc[e]);
+    }
   }
   // SiLU is a template parameter: as a runtime flag the compiler evaluates it for every
   // output (two quarter-rate transcendentals each) and selects
@@ -599,12 +638,13 @@ __device__ __forceinline__ void xlane_tail(const uint4& E, const uint4& X, int l
 }
 
 // Uniform dispatch of the window offset m to its xlane_tail (a scalar compare chain).
-template <typename T, int KT, bool NTH, bool SILU, int M = 0>
+template <typename T, int KT, bool NTH, bool SILU, bool DOT, int M = 0>
 __device__ __forceinline__ void xlane_dispatch(int m, const uint4& E, const uint4& X, int lane, bool edge,
-                                               int p0, uint32_t L, const float* wk, float bv, T* dst) {
+                                               int p0, uint32_t L, const float* wk, const uint32_t* wp, float bv,
+                                               T* dst) {
   if constexpr (M < (int)(16 / sizeof(T))) {
-    if (m == M) xlane_tail<T, KT, NTH, SILU, M>(E, X, lane, edge, p0, L, wk, bv, dst);
-    else xlane_dispatch<T, KT, NTH, SILU, M + 1>(m, E, X, lane, edge, p0, L, wk, bv, dst);
+    if (m == M) xlane_tail<T, KT, NTH, SILU, M, DOT>(E, X, lane, edge, p0, L, wk, wp, bv, dst);
+    else xlane_dispatch<T, KT, NTH, SILU, DOT, M + 1>(m, E, X, lane, edge, p0, L, wk, wp, bv, dst);
   }
 }
 
@@ -617,46 +657,83 @@ __device__ __forceinline__ void xlane_dispatch(int m, const uint4& E, const uint
 // and bias come through scalar loads.  Vector-memory instructions per output vector: about
 // 1 load and 1 store, the access pattern of a streaming copy.  Other waves take the
 // per-lane path of the register kernel.
-template <typename T, int KT, bool NTH, bool SILU>
+template <typename T, int KT, bool NTH, bool SILU, int NV>
 __global__ __launch_bounds__(DW_NT) void dwconv1d_xlane_kernel(DwArgs a) {
   using Win = DwWindow<T, KT>;
   constexpr int VEC = Win::VEC, WN = Win::WN;
+  constexpr int SPAN = 64 * VEC;  // outputs of one 64-vector part of a wave
   static_assert(Win::NBLK <= 3, "window spans at most three blocks");
   const int lane = threadIdx.x & 63;
-  const int64_t f = ((int64_t)blockIdx.x * DW_NT + threadIdx.x) * VEC - a.y_off;
+  // the wave's NV * 64 consecutive output vectors: part h holds vectors 64 h .. 64 h + 63
+  const int64_t vw = ((int64_t)blockIdx.x * (DW_NT / 64) + (threadIdx.x >> 6)) * 64 * NV;
+  const int64_t f = (vw + lane) * VEC - a.y_off;  // this lane's output in part 0
   uint32_t r = 0, t = 0;
-  bool inrow = f >= 0 && f + VEC <= a.total_out;
+  bool inrow = f >= 0 && f + (int64_t)SPAN * (NV - 1) + VEC <= a.total_out;
   if (inrow) {
     r = fdiv((uint32_t)f, a.div_lout);
     t = (uint32_t)f - r * a.Lout;
-    inrow = t + VEC <= a.Lout;
+    inrow = t + SPAN * (NV - 1) + VEC <= a.Lout;
   }
   const uint32_t r0 = __builtin_amdgcn_readfirstlane(r);
   if (__builtin_amdgcn_ballot_w64(inrow && r == r0) != ~0ull) {
-    reg_vector<T, KT, NTH, SILU>(a, f);
+#pragma unroll
+    for (int h = 0; h < NV; ++h) reg_vector<T, KT, NTH, SILU>(a, f + (int64_t)SPAN * h);
     return;
   }
-  // every lane: row r0, position t = t0 + VEC * lane
+  // every lane: row r0, position t = t0 + VEC * lane (+ SPAN * h in part h)
   const uint32_t t0 = __builtin_amdgcn_readfirstlane(t);
   const int g0 = (int)(r0 * a.L + t0) - a.pad + a.x_off;  // lane 0's window start, from x's aligned base
   const int bA = g0 >= 0 ? g0 / VEC : -((-g0 + VEC - 1) / VEC);
   const int m = g0 - bA * VEC;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(
       static_cast<const T*>(a.x) - a.x_off, (uint32_t)(((int64_t)a.total_in + a.x_off + VEC - 1) / VEC * 16));
-  const int be = bA + lane, bx = bA + 64 + lane;
-  const uint4 E = bload16<NTH ? 2 : 0>(rx, be >= 0 ? (uint32_t)be * 16u : kOOB, 0);
+  // part h's blocks; the two blocks past part h are part h + 1's first two (lanes 0 and 1
+  // hold them), and past the last part two more blocks are loaded
+  uint4 E[NV];
+#pragma unroll
+  for (int h = 0; h < NV; ++h) {
+    const int be = bA + 64 * h + lane;
+    E[h] = bload16<NTH ? 2 : 0>(rx, be >= 0 ? (uint32_t)be * 16u : kOOB, 0);
+  }
+  const int bx = bA + 64 * NV + lane;
   const uint4 X = bload16(rx, lane < 2 && bx >= 0 ? (uint32_t)bx * 16u : kOOB, 0);
   float wk[KT], bv;
   uniform_params<T, KT>(a.w, a.b, r0 - fdiv(r0, a.div_c) * a.C, wk, bv, a.w32);
-  // lanes whose window reaches past a row edge need the zero-padding mask (uniform test)
-  const bool edge = (int)t0 - a.pad < 0 || (int)(t0 + VEC * 63) - a.pad + WN > (int)a.L;
-  xlane_dispatch<T, KT, NTH, SILU>(m, E, X, lane, edge, (int)t - a.pad, a.L, wk, bv, static_cast<T*>(a.y) + f);
+  T* dst = static_cast<T*>(a.y) + f;
+  auto parts = [&](auto dot, const uint32_t* wp) {
+#pragma unroll
+    for (int h = 0; h < NV; ++h) {
+      const int th = (int)t0 + SPAN * h;
+      // lanes whose window reaches past a row edge need the zero-padding mask (uniform test)
+      const bool edge = th - a.pad < 0 || th + VEC * 63 - a.pad + WN > (int)a.L;
+      xlane_dispatch<T, KT, NTH, SILU, decltype(dot)::value>(m, E[h], h + 1 < NV ? E[h + 1 < NV ? h + 1 : h] : X, lane,
+                                                             edge, (int)t - a.pad + SPAN * h, a.L, wk, wp, bv,
+                                                             dst + SPAN * h);
+    }
+  };
+  if constexpr (sizeof(T) == 2 && KT >= 2) {
+    if (!a.w32) {
+      // weight pairs (w[j], w[j+1]) packed back into 16-bit halves (exact: they were 16-bit)
+      constexpr int NP = KT / 2;
+      uint32_t wp[NP];
+#pragma unroll
+      for (int j = 0; j < NP; ++j) {
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        typedef T t2 __attribute__((ext_vector_type(2)));
+        const f2 pr = {wk[2 * j], wk[2 * j + 1]};
+        wp[j] = __builtin_bit_cast(uint32_t, __builtin_convertvector(pr, t2));
+      }
+      parts(std::true_type(), wp);
+      return;
+    }
+  }
+  parts(std::false_type(), nullptr);
 }
 
 struct DwVariant {
   const char* name;
   int opt;  // outputs per thread; 0 = direct kernel, -1 = register kernel (one vector),
-            // -2 = cross-lane register kernel
+            // -2 / -3 = cross-lane register kernel (64 / 128 vectors per wave)
   bool nt;  // nontemporal loads/stores
 };
 
@@ -672,6 +749,7 @@ const DwVariant kDwVariants[] = {
     {"reg", -1, false},
     {"xlane_nt", -2, true},
     {"xlane", -2, false},
+    {"xlane2_nt", -3, true},
 };
 constexpr int kNumDw = sizeof(kDwVariants) / sizeof(kDwVariants[0]);
 
@@ -698,23 +776,25 @@ int launch_lds_k(const DwArgs& a, size_t shmem, hipStream_t s) {
   }
 }
 
-template <typename T, int KT, bool NTH, bool XL>
+template <typename T, int KT, bool NTH, int XL>
 void launch_reg_k(dim3 grid, dim3 block, hipStream_t s, const DwArgs& a) {
-  if constexpr (XL) {
-    if (a.silu) hipLaunchKernelGGL((dwconv1d_xlane_kernel<T, KT, NTH, true>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((dwconv1d_xlane_kernel<T, KT, NTH, false>), grid, block, 0, s, a);
+  if constexpr (XL > 0) {
+    if (a.silu) hipLaunchKernelGGL((dwconv1d_xlane_kernel<T, KT, NTH, true, XL>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((dwconv1d_xlane_kernel<T, KT, NTH, false, XL>), grid, block, 0, s, a);
   } else {
     if (a.silu) hipLaunchKernelGGL((dwconv1d_reg_kernel<T, KT, NTH, true>), grid, block, 0, s, a);
     else hipLaunchKernelGGL((dwconv1d_reg_kernel<T, KT, NTH, false>), grid, block, 0, s, a);
   }
 }
 
-template <typename T, bool NTH, bool XL>
+// XL: 0 = the one-vector register kernel, 1 / 2 = the cross-lane kernel with 1 / 2 vectors per lane
+template <typename T, bool NTH, int XL>
 int launch_reg(const DwArgs& a, hipStream_t s) {
   constexpr int VEC = 16 / sizeof(T);
-  if (a.total_out + a.y_off >= (1ll << 31) - VEC || a.total_in + a.x_off >= (1ll << 31) / (int64_t)sizeof(T) - VEC)
+  constexpr int64_t PER_WG = (int64_t)DW_NT * VEC * (XL > 1 ? XL : 1);
+  if (a.total_out + a.y_off >= (1ll << 31) - PER_WG || a.total_in + a.x_off >= (1ll << 31) / (int64_t)sizeof(T) - VEC)
     return fail(ATK_UNSUPPORTED, "dwconv1d: tensor too large for the register kernel");
-  const int64_t nblk = (a.total_out + a.y_off + (int64_t)DW_NT * VEC - 1) / ((int64_t)DW_NT * VEC);
+  const int64_t nblk = (a.total_out + a.y_off + PER_WG - 1) / PER_WG;
   const dim3 grid((unsigned)nblk), block(DW_NT);
   switch (a.K) {
     case 2: launch_reg_k<T, 2, NTH, XL>(grid, block, s, a); break;
@@ -723,15 +803,16 @@ int launch_reg(const DwArgs& a, hipStream_t s) {
     case 5: launch_reg_k<T, 5, NTH, XL>(grid, block, s, a); break;
     default: return fail(ATK_UNSUPPORTED, "dwconv1d: register kernels serve K in [2, 5]");
   }
-  return check_launch(XL ? "dwconv1d_xlane_kernel" : "dwconv1d_reg_kernel");
+  return check_launch(XL > 0 ? "dwconv1d_xlane_kernel" : "dwconv1d_reg_kernel");
 }
 
 template <typename T>
 int launch_dw(DwArgs a, int variant, hipStream_t s) {
   constexpr int VEC = 16 / sizeof(T);
   const int opt = kDwVariants[variant].opt;
-  if (opt == -1) return kDwVariants[variant].nt ? launch_reg<T, true, false>(a, s) : launch_reg<T, false, false>(a, s);
-  if (opt == -2) return kDwVariants[variant].nt ? launch_reg<T, true, true>(a, s) : launch_reg<T, false, true>(a, s);
+  if (opt == -1) return kDwVariants[variant].nt ? launch_reg<T, true, 0>(a, s) : launch_reg<T, false, 0>(a, s);
+  if (opt == -2) return kDwVariants[variant].nt ? launch_reg<T, true, 1>(a, s) : launch_reg<T, false, 1>(a, s);
+  if (opt == -3) return kDwVariants[variant].nt ? launch_reg<T, true, 2>(a, s) : launch_reg<T, false, 2>(a, s);
   if (opt == 0 || opt < VEC) {
     const int64_t nblk = (a.total_out + DW_NT - 1) / DW_NT;
     if (nblk > 0x7fffffff) return fail(ATK_UNSUPPORTED, "dwconv1d: grid too large");

@@ -271,7 +271,7 @@ def test_conv_group_norm_one_pass(dev, case, dtype):
     """Conv -> GroupNorm (-> SiLU) in one cooperative launch, for every 16-bit variant that
     takes the shape: against the float64 oracle of GroupNorm(+SiLU) applied to the plain conv's
     output of the same variant (the statistics are of that stored output), and against the
-    float64 oracle of the whole block; repeats are bit-identical and no wait ran out."""
+    float64 oracle of the whole block (bar 1e-2); repeats are bit-identical and no wait ran out."""
     xs, ws, pad, G, silu, affine = case
     nat = _native()
     x, w, b = _inputs(xs, ws, dtype, seed=sum(xs) + 7 * G)
@@ -293,7 +293,7 @@ def test_conv_group_norm_one_pass(dev, case, dtype):
         assert torch.equal(out.view(torch.int16), again.view(torch.int16)), name
         ref = O.group_norm(plain.cpu(), G, gm, bt, 1e-5, silu=silu)
         assert O.max_rel_err(out.cpu(), ref) <= GN_BAR[dtype], name
-        assert O.max_rel_err(out.cpu(), block_ref) <= 2e-2, name
+        assert O.max_rel_err(out.cpu(), block_ref) <= 1e-2, name
         ran += 1
     assert ran >= 1
 
