@@ -981,27 +981,39 @@ __global__ __launch_bounds__(DW_NT) void dwconv1d_bwd_fused_kernel(DwBwdFusedArg
   float acc[KT + 1];
 #pragma unroll
   for (int k = 0; k <= KT; ++k) acc[k] = 0.f;
-  for (int p0 = a.p_lo + (int)threadIdx.x * VEC; p0 < a.p_end; p0 += DW_NT * VEC) {
-    uint32_t DD[4 * Dyw::NBLK], DX[4 * Xw::NBLK];
-    int md, mx;
-    const int g = p0 + a.pad - (KT - 1);  // row position of the window's first dy element
-    Dyw::fetch(rd, (int)(r * a.Lout) + g + a.dy_off, true, DD, md);
-    Xw::fetch(rx, (int)(r * a.L) + p0 + a.x_off, true, DX, mx);
-    float dv[WN], xv[VEC];
-    Dyw::extract(DD, md, g, a.Lout, dv);  // zero outside [0, L_out)
-    Xw::extract(DX, mx, p0, a.L, xv);     // zero outside [0, L)
-    float o[VEC];
+  // two positions per trip, every load of both issued before either is used (a trip past
+  // p_end loads zeros, which add nothing, and stores nothing)
+  constexpr int STEP = DW_NT * VEC;
+  for (int p0 = a.p_lo + (int)threadIdx.x * VEC; p0 < a.p_end; p0 += 2 * STEP) {
+    uint32_t DD[2][4 * Dyw::NBLK], DX[2][4 * Xw::NBLK];
+    int md[2], mx[2];
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      float sx = 0.f;
-#pragma unroll
-      for (int j = 0; j < KT; ++j) sx = fmaf(wv[j], dv[e + KT - 1 - j], sx);
-      o[e] = sx;
-      acc[KT] += dv[e];
-#pragma unroll
-      for (int j = 0; j < KT; ++j) acc[j] = fmaf(xv[e], dv[e + KT - 1 - j], acc[j]);
+    for (int u = 0; u < 2; ++u) {
+      const int pu = p0 + u * STEP;
+      const int g = pu + a.pad - (KT - 1);  // row position of the window's first dy element
+      Dyw::fetch(rd, (int)(r * a.Lout) + g + a.dy_off, pu < a.p_end, DD[u], md[u]);
+      Xw::fetch(rx, (int)(r * a.L) + pu + a.x_off, pu < a.p_end, DX[u], mx[u]);
     }
-    if (p0 >= 0 && p0 < L) st16<false>(dxr + p0, pack16<T>(o));
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int pu = p0 + u * STEP;
+      const int g = pu + a.pad - (KT - 1);
+      float dv[WN], xv[VEC];
+      Dyw::extract(DD[u], md[u], g, a.Lout, dv);  // zero outside [0, L_out)
+      Xw::extract(DX[u], mx[u], pu, a.L, xv);     // zero outside [0, L)
+      float o[VEC];
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+        float sx = 0.f;
+#pragma unroll
+        for (int j = 0; j < KT; ++j) sx = fmaf(wv[j], dv[e + KT - 1 - j], sx);
+        o[e] = sx;
+        acc[KT] += dv[e];
+#pragma unroll
+        for (int j = 0; j < KT; ++j) acc[j] = fmaf(xv[e], dv[e + KT - 1 - j], acc[j]);
+      }
+      if (pu < a.p_end && pu >= 0 && pu < L) st16<false>(dxr + pu, pack16<T>(o));
+    }
   }
   if (!a.part) return;
   // thread 0 writes the row's K+1 partials: one LDS exchange
