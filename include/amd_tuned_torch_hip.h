@@ -315,7 +315,10 @@ int atk_group_norm_fwd_noalloc(const void* x, const void* gamma, const void* bet
  * workspace must be zero-filled once when it is allocated and then passed unchanged to
  * later calls (its contents are the state), and calls sharing one workspace must be
  * ordered (one stream).  ATK_GN_CL_RESIDENT=0 in the environment keeps the three-kernel
- * path (8 or 16 forces the resident configuration with that many vectors per thread).
+ * path (8 or 16 forces the resident configuration with that many vectors per thread), and
+ * ATK_GN_CL_LAYOUT=rows / blocks forces its chunk shape (whole positions, or 128-byte column
+ * blocks of a position; by default blocks where the rows grid would need more than one
+ * workgroup per CU).
  * ------------------------------------------------------------------------- */
 size_t atk_group_norm_cl_workspace_bytes(int64_t N, int64_t C, int64_t S, int G);
 int atk_group_norm_cl_fwd(const void* x, const void* gamma, const void* beta, void* y,
